@@ -1,0 +1,239 @@
+"""Drop-in ``Attention`` and ``KVCache`` running on the gfx950 HIP kernels.
+
+Mirrors ``kempnerforge/model/attention.py``: same constructor and forward
+signatures, attributes, submodule names (so state-dict keys
+``{q,k,v,o}_proj.weight`` and ``{q,k}_norm.weight`` are unchanged), capture
+flag and ``last_attention_weights`` on the CPU.  What changes is below the
+projections: RoPE, the GQA expansion, the attention itself, the cache update
+and the capture math run in the kernels of ``libkf_attn.so``.
+
+Paths (reference lines in ``kempnerforge/model/attention.py``):
+
+* training / no cache (``:228-231`` with ``is_causal=True``): ``kf::attn_fwd``,
+  differentiable through ``kf::attn_bwd``;
+* decode, one token with a cache (``:169-175,229-231``): ``kf_attn_decode``;
+* prefill with a cache (``:169-175,229-231``): ``kf_kv_cache_append`` then the
+  forward over the cache with the reference's top-left causal alignment;
+* capture (``:184-189,238-280``): ``kf_attn_capture``.
+
+The explicit-mask branch for ``doc_ids`` / ``key_padding_mask`` (``:190-227``)
+is not on this path and keeps the reference's PyTorch SDPA call.
+"""
+
+from __future__ import annotations
+
+import contextlib
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+from torch.nn.attention import SDPBackend, sdpa_kernel
+
+from kempnerforge_amd import ops
+from kempnerforge_amd.norm import RMSNorm
+
+_SDPA_BACKENDS = {
+    "flash": SDPBackend.FLASH_ATTENTION,
+    "efficient": SDPBackend.EFFICIENT_ATTENTION,
+    "cudnn": SDPBackend.CUDNN_ATTENTION,
+    "math": SDPBackend.MATH,
+}
+
+
+class KVCache:
+    """Pre-allocated KV cache ``[B, n_kv_heads, max_seq_len, head_dim]``.
+
+    Same storage and API as ``kempnerforge/model/attention.py:29-70``: keys are
+    stored after RoPE and before GQA expansion; ``seq_len`` is the batch's fill
+    level.  ``lens`` is the same fill level per sequence as an int32 device
+    tensor, which the decode kernel reads without a host synchronisation.
+    """
+
+    def __init__(
+        self,
+        batch_size: int,
+        max_seq_len: int,
+        n_kv_heads: int,
+        head_dim: int,
+        dtype: torch.dtype,
+        device: torch.device,
+    ) -> None:
+        self.k = torch.zeros(batch_size, n_kv_heads, max_seq_len, head_dim, dtype=dtype,
+                             device=device)
+        self.v = torch.zeros(batch_size, n_kv_heads, max_seq_len, head_dim, dtype=dtype,
+                             device=device)
+        self.seq_len = 0
+        self.lens = torch.zeros(batch_size, dtype=torch.int32, device=device)
+
+    @property
+    def max_seq_len(self) -> int:
+        return self.k.shape[2]
+
+    def update(self, k_new: torch.Tensor, v_new: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+        """Append already-rotated ``(B, n_kv_heads, new_len, head_dim)`` keys and
+        values; return the filled ``[:, :, :seq_len]`` views
+        (``kempnerforge/model/attention.py:54-70``)."""
+        new_len = k_new.shape[2]
+        end = self.seq_len + new_len
+        self.k[:, :, self.seq_len : end] = k_new
+        self.v[:, :, self.seq_len : end] = v_new
+        self._advance(new_len)
+        return self.k[:, :, :end], self.v[:, :, :end]
+
+    def _check_room(self, new_len: int) -> None:
+        if self.seq_len + new_len > self.max_seq_len:
+            raise ValueError(
+                f"KV cache overflow: {self.seq_len} cached + {new_len} new tokens exceeds "
+                f"max_seq_len {self.max_seq_len}"
+            )
+
+    def _advance(self, new_len: int) -> None:
+        self.seq_len += new_len
+        self.lens.add_(new_len)
+
+
+def _apply_rope_torch(x, cos, sin):
+    """The reference's ``apply_rope`` (``kempnerforge/model/position.py:43-71``),
+    used only by the explicit-mask branch, which is outside the kernel path."""
+    d = x.shape[-1] // 2
+    x1, x2 = x[..., :d], x[..., d:]
+    shape = [1] * (x.ndim - 2) + list(cos.shape)
+    c = cos.view(*shape).to(x.dtype)
+    s = sin.view(*shape).to(x.dtype)
+    return torch.cat([x1 * c - x2 * s, x2 * c + x1 * s], dim=-1)
+
+
+class Attention(nn.Module):
+    """Grouped-Query Attention with RoPE on gfx950 HIP kernels."""
+
+    def __init__(
+        self,
+        dim: int,
+        n_heads: int,
+        n_kv_heads: int,
+        head_dim: int | None = None,
+        qk_norm: bool = False,
+        sdpa_backend: str = "auto",
+    ) -> None:
+        super().__init__()
+        self.n_heads = n_heads
+        self.n_kv_heads = n_kv_heads
+        self.head_dim = head_dim or (dim // n_heads)
+        self.n_rep = n_heads // n_kv_heads
+        # Kept for configuration compatibility; the HIP path has one kernel per
+        # operation and does not dispatch on it.
+        self.sdpa_backend = sdpa_backend
+
+        self.q_proj = nn.Linear(dim, n_heads * self.head_dim, bias=False)
+        self.k_proj = nn.Linear(dim, n_kv_heads * self.head_dim, bias=False)
+        self.v_proj = nn.Linear(dim, n_kv_heads * self.head_dim, bias=False)
+        self.o_proj = nn.Linear(n_heads * self.head_dim, dim, bias=False)
+
+        self.q_norm = RMSNorm(self.head_dim) if qk_norm else None
+        self.k_norm = RMSNorm(self.head_dim) if qk_norm else None
+
+        self.capture_attention_weights = False
+        self.last_attention_weights: torch.Tensor | None = None
+
+    def _sdpa_context(self):
+        if self.sdpa_backend == "auto":
+            return contextlib.nullcontext()
+        return sdpa_kernel(_SDPA_BACKENDS[self.sdpa_backend])
+
+    def forward(
+        self,
+        x: torch.Tensor,
+        rope_cos: torch.Tensor,
+        rope_sin: torch.Tensor,
+        *,
+        kv_cache: KVCache | None = None,
+        doc_ids: torch.Tensor | None = None,
+        key_padding_mask: torch.Tensor | None = None,
+    ) -> torch.Tensor:
+        """x ``(B, S, dim)``, rope tables ``(S, head_dim // 2)`` for positions
+        ``start_pos .. start_pos + S - 1`` → ``(B, S, dim)``."""
+        batch, seq_len, _ = x.shape
+        # BSHD views; -1 heads so tensor-parallel shards work (reference :148-152)
+        q = self.q_proj(x).view(batch, seq_len, -1, self.head_dim)
+        k = self.k_proj(x).view(batch, seq_len, -1, self.head_dim)
+        v = self.v_proj(x).view(batch, seq_len, -1, self.head_dim)
+        if self.q_norm is not None:
+            q = self.q_norm(q)
+            k = self.k_norm(k)  # type: ignore[reportOptionalCall]
+
+        if doc_ids is not None or key_padding_mask is not None:
+            out = self._masked_attention(q, k, v, rope_cos, rope_sin, seq_len, doc_ids,
+                                         kv_cache, key_padding_mask)
+        elif self.capture_attention_weights:
+            out, probs = self._capture(q, k, v, rope_cos, rope_sin, kv_cache)
+            self.last_attention_weights = probs.to(q.dtype).detach().cpu()
+        elif kv_cache is None:
+            out = ops.attention(q, k, v, rope_cos, rope_sin, causal=True)
+        elif seq_len == 1:
+            kv_cache._check_room(1)
+            out = ops.decode_raw(q, k, v, kv_cache.k, kv_cache.v, kv_cache.lens, rope_cos,
+                                 rope_sin, rope_row_offset=kv_cache.seq_len,
+                                 max_len=kv_cache.seq_len + 1)
+            kv_cache._advance(1)
+        else:
+            kc, vc = self._append(k, v, rope_cos, rope_sin, kv_cache)
+            out, _ = ops.fwd_raw(q, kc, vc, rope_cos, rope_sin, causal=True, k_rotated=True,
+                                 k_layout="bhsd")
+
+        out = out.reshape(batch, seq_len, -1)
+        return self.o_proj(out)
+
+    @staticmethod
+    def _append(k, v, rope_cos, rope_sin, kv_cache: KVCache):
+        new_len = k.shape[1]
+        kv_cache._check_room(new_len)
+        start = kv_cache.seq_len
+        ops.cache_append_raw(k, v, rope_cos, rope_sin, kv_cache.k, kv_cache.v, start)
+        kv_cache._advance(new_len)
+        end = kv_cache.seq_len
+        return kv_cache.k[:, :, :end], kv_cache.v[:, :, :end]
+
+    def _capture(self, q, k, v, rope_cos, rope_sin, kv_cache):
+        """Manual-attention replacement (``kempnerforge/model/attention.py:238-280``)."""
+        if kv_cache is None:
+            out, probs, _ = ops.capture_raw(q, k, v, rope_cos, rope_sin, causal=True,
+                                            k_rotated=False)
+            return out, probs
+        seq_len = q.shape[1]
+        kc, vc = self._append(k, v, rope_cos, rope_sin, kv_cache)
+        out, probs, _ = ops.capture_raw(q, kc, vc, rope_cos, rope_sin, causal=seq_len > 1,
+                                        k_rotated=True, k_layout="bhsd")
+        return out, probs
+
+    def _masked_attention(self, q, k, v, rope_cos, rope_sin, seq_len, doc_ids, kv_cache,
+                          key_padding_mask):
+        """Explicit-mask branch, kept as the reference's PyTorch code
+        (``kempnerforge/model/attention.py:190-227``, manual variant ``:262-271``)."""
+        assert kv_cache is None, (
+            "doc_ids / key_padding_mask are not supported with kv_cache decode "
+            "(would build an incorrect causal mask)."
+        )
+        batch = q.shape[0]
+        q = _apply_rope_torch(q.transpose(1, 2), rope_cos, rope_sin)
+        k = _apply_rope_torch(k.transpose(1, 2), rope_cos, rope_sin)
+        v = v.transpose(1, 2)
+        if self.n_rep > 1:
+            k = k.repeat_interleave(self.n_rep, dim=1)
+            v = v.repeat_interleave(self.n_rep, dim=1)
+        seq_len_kv = k.shape[2]
+        mask = torch.ones(seq_len, seq_len_kv, dtype=torch.bool, device=q.device).tril()
+        mask = mask.unsqueeze(0).unsqueeze(0)
+        if doc_ids is not None:
+            mask = mask & (doc_ids.unsqueeze(2) == doc_ids.unsqueeze(1)).unsqueeze(1)
+        if key_padding_mask is not None:
+            mask = mask & key_padding_mask.view(batch, 1, 1, seq_len_kv)
+        mask = mask | ~mask.any(dim=-1, keepdim=True)
+        if self.capture_attention_weights:
+            attn = torch.matmul(q, k.transpose(-2, -1)) * self.head_dim**-0.5
+            attn = F.softmax(attn.masked_fill(~mask, float("-inf")), dim=-1)
+            self.last_attention_weights = attn.detach().cpu()
+            out = torch.matmul(attn, v)
+        else:
+            with self._sdpa_context():
+                out = F.scaled_dot_product_attention(q, k, v, attn_mask=mask)
+        return out.transpose(1, 2)

@@ -1,0 +1,220 @@
+// C ABI entry points (declared in include/kf_attn.h).  Host-side argument
+// checks happen here, before any launch, so that every kernel only ever sees
+// shapes its grid and indexing were written for.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "kf_common.h"
+#include "kf_internal.h"
+
+namespace kf {
+
+static thread_local char g_err[512] = "";
+
+void set_error(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+}
+
+static int check_common(int B, int Sq, int Sk, int Hq, int Hkv, int D, int dtype) {
+  KF_CHECK_ARG(B > 0 && Sq > 0 && Sk > 0, "B, Sq, Sk must be positive (got %d, %d, %d)", B, Sq,
+               Sk);
+  KF_CHECK_ARG(Hq > 0 && Hkv > 0 && Hq % Hkv == 0,
+               "n_heads (%d) must be a positive multiple of n_kv_heads (%d)", Hq, Hkv);
+  KF_CHECK_ARG(D > 0 && D % 2 == 0 && D <= 256, "head_dim must be even and <= 256 (got %d)", D);
+  KF_CHECK_ARG(dtype == F32 || dtype == BF16 || dtype == F16, "unsupported dtype code %d", dtype);
+  return KF_OK;
+}
+
+static FwdArgs make_fwd(const void* q, const void* k, const void* v, const float* cos,
+                        const float* sin, void* out, float* lse, int B, int Sq, int Sk, int Hq,
+                        int Hkv, int D, int64_t ksb, int64_t kss, int64_t ksh, int64_t vsb,
+                        int64_t vss, int64_t vsh, int k_rotated, int causal, int dtype,
+                        void* stream) {
+  FwdArgs a;
+  a.q = q; a.k = k; a.v = v; a.cos = cos; a.sin = sin; a.out = out; a.lse = lse;
+  a.B = B; a.Sq = Sq; a.Sk = Sk; a.Hq = Hq; a.Hkv = Hkv; a.D = D;
+  a.ksb = ksb; a.kss = kss; a.ksh = ksh; a.vsb = vsb; a.vss = vss; a.vsh = vsh;
+  a.k_rotated = k_rotated; a.causal = causal; a.dtype = dtype;
+  a.scale = 1.0f / sqrtf((float)D);
+  a.stream = (hipStream_t)stream;
+  return a;
+}
+
+static size_t fwd_ws(const FwdArgs& a) {
+  return fwd_mfma_supported(a) ? fwd_mfma_workspace(a.B, a.Sk, a.Hkv, a.D) : 0;
+}
+
+}  // namespace kf
+
+using namespace kf;
+
+extern "C" {
+
+int kf_version(void) { return 100; }
+
+const char* kf_last_error(void) { return g_err; }
+
+int kf_attn_fwd_workspace_size(int B, int Sq, int Sk, int Hq, int Hkv, int D, int dtype,
+                               size_t* bytes) {
+  int rc = check_common(B, Sq, Sk, Hq, Hkv, D, dtype);
+  if (rc) return rc;
+  KF_CHECK_ARG(bytes != nullptr, "bytes is null");
+  // Contiguous BSHD strides and aligned pointers are assumed for the estimate;
+  // a call that falls back to the generic kernels needs no workspace.
+  FwdArgs a = make_fwd((void*)16, (void*)16, (void*)16, (float*)16, (float*)16, (void*)16,
+                       nullptr, B, Sq, Sk, Hq, Hkv, D, (int64_t)Sk * Hkv * D, (int64_t)Hkv * D, D,
+                       (int64_t)Sk * Hkv * D, (int64_t)Hkv * D, D, 0, 1, dtype, nullptr);
+  *bytes = fwd_ws(a);
+  return KF_OK;
+}
+
+int kf_attn_fwd(const void* q, const void* k, const void* v, const float* rope_cos,
+                const float* rope_sin, void* out, float* lse, void* workspace,
+                size_t workspace_bytes, int B, int Sq, int Sk, int Hq, int Hkv, int D,
+                int64_t ksb, int64_t kss, int64_t ksh, int64_t vsb, int64_t vss, int64_t vsh,
+                int k_rotated, int causal, int dtype, void* stream) {
+  int rc = check_common(B, Sq, Sk, Hq, Hkv, D, dtype);
+  if (rc) return rc;
+  KF_CHECK_ARG(q && k && v && rope_cos && rope_sin && out, "null tensor pointer");
+  KF_CHECK_ARG(k_rotated || Sk == Sq, "un-rotated keys need Sk == Sq (got %d, %d)", Sk, Sq);
+  FwdArgs a = make_fwd(q, k, v, rope_cos, rope_sin, out, lse, B, Sq, Sk, Hq, Hkv, D, ksb, kss,
+                       ksh, vsb, vss, vsh, k_rotated, causal, dtype, stream);
+  if (fwd_mfma_supported(a)) {
+    const size_t need = fwd_mfma_workspace(B, Sk, Hkv, D);
+    if (workspace_bytes < need || (need && !workspace)) {
+      set_error("workspace too small: need %zu bytes, got %zu", need, workspace_bytes);
+      return KF_ERR_WORKSPACE;
+    }
+    return fwd_mfma(a, workspace);
+  }
+  return fwd_generic(a);
+}
+
+int kf_attn_bwd_workspace_size(int B, int S, int Hq, int Hkv, int D, int dtype, size_t* bytes) {
+  int rc = check_common(B, S, S, Hq, Hkv, D, dtype);
+  if (rc) return rc;
+  KF_CHECK_ARG(bytes != nullptr, "bytes is null");
+  BwdArgs a{};
+  a.B = B; a.S = S; a.Hq = Hq; a.Hkv = Hkv; a.D = D; a.dtype = dtype; a.causal = 1;
+  a.q = a.k = a.v = a.out = a.dout = (void*)16;
+  a.dq = a.dk = a.dv = (void*)16;
+  a.cos = a.sin = (float*)16;
+  *bytes = bwd_mfma_supported(a) ? bwd_mfma_workspace(B, S, Hq, Hkv, D)
+                                 : (size_t)B * Hq * S * sizeof(float);
+  return KF_OK;
+}
+
+int kf_attn_bwd(const void* q, const void* k, const void* v, const float* rope_cos,
+                const float* rope_sin, const void* out, const float* lse, const void* dout,
+                void* dq, void* dk, void* dv, void* workspace, size_t workspace_bytes, int B,
+                int S, int Hq, int Hkv, int D, int causal, int dtype, void* stream) {
+  int rc = check_common(B, S, S, Hq, Hkv, D, dtype);
+  if (rc) return rc;
+  KF_CHECK_ARG(q && k && v && rope_cos && rope_sin && out && lse && dout && dq && dk && dv,
+               "null tensor pointer");
+  BwdArgs a;
+  a.q = q; a.k = k; a.v = v; a.cos = rope_cos; a.sin = rope_sin; a.out = out; a.lse = lse;
+  a.dout = dout; a.dq = dq; a.dk = dk; a.dv = dv;
+  a.B = B; a.S = S; a.Hq = Hq; a.Hkv = Hkv; a.D = D; a.causal = causal; a.dtype = dtype;
+  a.scale = 1.0f / sqrtf((float)D);
+  a.stream = (hipStream_t)stream;
+  if (bwd_mfma_supported(a)) {
+    const size_t need = bwd_mfma_workspace(B, S, Hq, Hkv, D);
+    if (workspace_bytes < need || !workspace) {
+      set_error("workspace too small: need %zu bytes, got %zu", need, workspace_bytes);
+      return KF_ERR_WORKSPACE;
+    }
+    return bwd_mfma(a, workspace);
+  }
+  const size_t need = (size_t)B * Hq * S * sizeof(float);
+  if (workspace_bytes < need || !workspace) {
+    set_error("workspace too small: need %zu bytes, got %zu", need, workspace_bytes);
+    return KF_ERR_WORKSPACE;
+  }
+  return bwd_generic(a, (float*)workspace);
+}
+
+int kf_attn_decode_workspace_size(int B, int Hq, int Hkv, int D, int max_len, int dtype,
+                                  size_t* bytes) {
+  int rc = check_common(B, 1, max_len, Hq, Hkv, D, dtype);
+  if (rc) return rc;
+  KF_CHECK_ARG(bytes != nullptr, "bytes is null");
+  *bytes = decode_workspace(B, Hq, D, max_len);
+  return KF_OK;
+}
+
+int kf_attn_decode(const void* q_new, const void* k_new, const void* v_new, void* k_cache,
+                   void* v_cache, const int32_t* lens, const float* rope_cos,
+                   const float* rope_sin, int64_t rope_row_offset, int64_t rope_rows, void* out,
+                   void* workspace,
+                   size_t workspace_bytes, int B, int Smax, int Hq, int Hkv, int D, int max_len,
+                   int dtype, void* stream) {
+  int rc = check_common(B, 1, max_len, Hq, Hkv, D, dtype);
+  if (rc) return rc;
+  KF_CHECK_ARG(q_new && k_new && v_new && k_cache && v_cache && lens && rope_cos && rope_sin &&
+                   out,
+               "null tensor pointer");
+  KF_CHECK_ARG(max_len <= Smax, "max_len (%d) exceeds the cache length (%d)", max_len, Smax);
+  const size_t need = decode_workspace(B, Hq, D, max_len);
+  if (workspace_bytes < need || !workspace) {
+    set_error("workspace too small: need %zu bytes, got %zu", need, workspace_bytes);
+    return KF_ERR_WORKSPACE;
+  }
+  DecodeArgs a;
+  a.q_new = q_new; a.k_new = k_new; a.v_new = v_new; a.k_cache = k_cache; a.v_cache = v_cache;
+  KF_CHECK_ARG(rope_rows > 0, "rope tables must have at least one row");
+  a.lens = lens; a.cos = rope_cos; a.sin = rope_sin; a.rope_row_offset = rope_row_offset;
+  a.rope_rows = rope_rows;
+  a.out = out; a.B = B; a.Smax = Smax; a.Hq = Hq; a.Hkv = Hkv; a.D = D; a.max_len = max_len;
+  a.dtype = dtype; a.scale = 1.0f / sqrtf((float)D); a.stream = (hipStream_t)stream;
+  return decode(a, workspace);
+}
+
+int kf_kv_cache_append(const void* k_new, const void* v_new, const float* rope_cos,
+                       const float* rope_sin, void* k_cache, void* v_cache, int start, int B,
+                       int Snew, int Hkv, int Smax, int D, int dtype, void* stream) {
+  int rc = check_common(B, Snew, Smax, Hkv, Hkv, D, dtype);
+  if (rc) return rc;
+  KF_CHECK_ARG(k_new && v_new && rope_cos && rope_sin && k_cache && v_cache,
+               "null tensor pointer");
+  KF_CHECK_ARG(start >= 0 && start + Snew <= Smax,
+               "cache overflow: start %d + %d new tokens > capacity %d", start, Snew, Smax);
+  return cache_append(k_new, v_new, rope_cos, rope_sin, k_cache, v_cache, start, B, Snew, Hkv,
+                      Smax, D, dtype, (hipStream_t)stream);
+}
+
+int kf_attn_capture_workspace_size(int B, int Sq, int Sk, int Hq, int Hkv, int D, int dtype,
+                                   size_t* bytes) {
+  return kf_attn_fwd_workspace_size(B, Sq, Sk, Hq, Hkv, D, dtype, bytes);
+}
+
+int kf_attn_capture(const void* q, const void* k, const void* v, const float* rope_cos,
+                    const float* rope_sin, float* probs, void* out, float* lse, void* workspace,
+                    size_t workspace_bytes, int B, int Sq, int Sk, int Hq, int Hkv, int D,
+                    int64_t ksb, int64_t kss, int64_t ksh, int64_t vsb, int64_t vss,
+                    int64_t vsh, int k_rotated, int causal, int dtype, void* stream) {
+  int rc = check_common(B, Sq, Sk, Hq, Hkv, D, dtype);
+  if (rc) return rc;
+  KF_CHECK_ARG(q && k && v && rope_cos && rope_sin && out && probs && lse, "null tensor pointer");
+  KF_CHECK_ARG(k_rotated || Sk == Sq, "un-rotated keys need Sk == Sq (got %d, %d)", Sk, Sq);
+  FwdArgs a = make_fwd(q, k, v, rope_cos, rope_sin, out, lse, B, Sq, Sk, Hq, Hkv, D, ksb, kss,
+                       ksh, vsb, vss, vsh, k_rotated, causal, dtype, stream);
+  if (fwd_mfma_supported(a) && ((uintptr_t)probs & 15) == 0) {
+    const size_t need = fwd_mfma_workspace(B, Sk, Hkv, D);
+    if (workspace_bytes < need || !workspace) {
+      set_error("workspace too small: need %zu bytes, got %zu", need, workspace_bytes);
+      return KF_ERR_WORKSPACE;
+    }
+    rc = fwd_mfma(a, workspace);
+    if (rc) return rc;
+    return capture_probs_mfma(a, lse, probs, workspace);
+  }
+  rc = fwd_generic(a);
+  if (rc) return rc;
+  return capture_probs_generic(a, lse, probs);
+}
+
+}  // extern "C"

@@ -1,0 +1,125 @@
+// Shared device helpers for the gfx950 attention kernels.
+//
+// Numeric contract for RoPE: the rotation is evaluated exactly as PyTorch eager
+// evaluates kempnerforge/model/position.py:65-71 — the float32 tables are cast to
+// the input dtype, and every product and every sum is rounded to the input dtype
+// before the next op.  For bfloat16 this is "compute in fp32, round to bf16"
+// per op (bf16*bf16 products are exact in fp32, so only the explicit roundings
+// matter).  For float32 the ops are kept separate (no FMA contraction).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace kf {
+
+typedef __bf16 bf16;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+enum DType : int { F32 = 0, BF16 = 1, F16 = 2 };
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+__device__ __forceinline__ float to_f32(float x) { return x; }
+__device__ __forceinline__ float to_f32(bf16 x) { return (float)x; }
+__device__ __forceinline__ float to_f32(_Float16 x) { return (float)x; }
+
+template <typename T> __device__ __forceinline__ T from_f32(float x);
+template <> __device__ __forceinline__ float from_f32<float>(float x) { return x; }
+template <> __device__ __forceinline__ bf16 from_f32<bf16>(float x) { return (bf16)x; }
+template <> __device__ __forceinline__ _Float16 from_f32<_Float16>(float x) { return (_Float16)x; }
+
+// Round a float to the storage type and back (the value a T tensor would hold).
+template <typename T> __device__ __forceinline__ float round_to(float x) {
+  return to_f32(from_f32<T>(x));
+}
+
+// Half-split RoPE of one (x1, x2) pair with table values (c, s) given in fp32
+// (the reference's float32 tables); eager-op rounding in dtype T.
+//   r1 = x1*c - x2*s ; r2 = x2*c + x1*s      (kempnerforge/model/position.py:71)
+template <typename T>
+__device__ __forceinline__ void rope_pair(float x1, float x2, float cf, float sf,
+                                          float& r1, float& r2) {
+#pragma clang fp contract(off)
+  const float c = round_to<T>(cf);
+  const float s = round_to<T>(sf);
+  const float a = round_to<T>(x1 * c);
+  const float b = round_to<T>(x2 * s);
+  const float e = round_to<T>(x2 * c);
+  const float f = round_to<T>(x1 * s);
+  r1 = round_to<T>(a - b);
+  r2 = round_to<T>(e + f);
+}
+
+// RoPE backward for one pair (transposed rotation), fp32 in and out; the table
+// values are the dtype-cast ones the forward multiplied by.
+template <typename T>
+__device__ __forceinline__ void rope_pair_bwd(float g1, float g2, float cf, float sf,
+                                              float& d1, float& d2) {
+  const float c = round_to<T>(cf);
+  const float s = round_to<T>(sf);
+  d1 = g1 * c + g2 * s;
+  d2 = g2 * c - g1 * s;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Unpack 8 bf16 held in a 16-byte vector into floats.
+__device__ __forceinline__ void unpack8(const u32x4& u, float* f) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = __uint_as_float(u[i] << 16);
+    f[2 * i + 1] = __uint_as_float(u[i] & 0xffff0000u);
+  }
+}
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+  bf16 a = (bf16)lo, b = (bf16)hi;
+  return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+}
+__device__ __forceinline__ u32x4 pack8(const float* f) {
+  u32x4 u;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) u[i] = pack2(f[2 * i], f[2 * i + 1]);
+  return u;
+}
+
+}  // namespace kf
+
+// ---------------------------------------------------------------- host side
+namespace kf {
+void set_error(const char* fmt, ...);
+}  // namespace kf
+
+#define KF_CHECK_ARG(cond, ...)          \
+  do {                                   \
+    if (!(cond)) {                       \
+      kf::set_error(__VA_ARGS__);        \
+      return KF_ERR_INVALID_ARGUMENT;    \
+    }                                    \
+  } while (0)
+
+#define KF_CHECK_LAUNCH()                                              \
+  do {                                                                 \
+    hipError_t e_ = hipGetLastError();                                 \
+    if (e_ != hipSuccess) {                                            \
+      kf::set_error("kernel launch failed: %s", hipGetErrorString(e_)); \
+      return KF_ERR_HIP;                                               \
+    }                                                                  \
+  } while (0)

@@ -1,0 +1,477 @@
+// bf16 MFMA forward attention for gfx950 (head_dim 64 or 128).
+//
+// Two kernels:
+//  kv_prep   stages one KV head's keys and values in the layout the MFMA loop
+//            reads: K rotated by RoPE (eager bf16 rounding) as [bh][Skp][D], and
+//            V transposed as [bh][D][Skp] with a quad swizzle inside every 16
+//            keys (see vt_logical_key) so that each lane's B-operand slots of
+//            the P·V product are one 16-byte read.  Keys >= Sk are zero.
+//  fwd_mfma  flash forward.  One workgroup = 4 wavefronts = 128 "rows", where
+//            a row is (query head of the KV group, position): every K/V tile in
+//            LDS is shared by all n_rep query heads of the group.  Each wave
+//            owns 32 rows and computes S^T = K·Q^T with
+//            v_mfma_f32_32x32x16_bf16, so a lane holds one query's 32 scores of
+//            a 64-key tile: the online-softmax max/sum is lane-local plus one
+//            exchange with lane^32.  O^T = V^T·P^T accumulates in 16 fp32
+//            registers per 32-d tile.  RoPE of q happens at the Q load.
+//
+// MFMA 32x32x16 operand layout used (lane l, h = l/32, slot j = 0..7):
+//   A[m][k]: m = l%32, k = 8h + j     B[k][n]: n = l%32, k = 8h + j
+//   C[m][n]: n = l%32, register i holds m = 8*(i/4) + 4h + (i%4)
+// Only the A/B k-assignment has to agree between the two operands; both
+// operands are always built with the same (h, j) -> k map.
+#include "kf_common.h"
+#include "kf_internal.h"
+
+namespace kf {
+
+namespace {
+
+constexpr int BN = 64;   // keys per tile
+constexpr int ROWS = 128;
+
+// Physical slot p (0..15) inside a 16-key group of the transposed V holds this
+// logical key: lane half h = p/8, slot j = p%8 of the P^T B-operand carries key
+// (j<4 ? 4h+j : 8+4h+j-4) because of the 32x32 C layout of S^T.
+__device__ __forceinline__ int vt_logical_key(int p) {
+  const int h = (p & 15) >> 3, j = p & 7;
+  return (p & ~15) + (j < 4 ? 4 * h + j : 8 + 4 * h + (j - 4));
+}
+
+__device__ __forceinline__ bf16x8 as_bf16x8(const u32x4& u) { return __builtin_bit_cast(bf16x8, u); }
+
+template <int D>
+__global__ __launch_bounds__(256) void kv_prep_kernel(
+    const bf16* __restrict__ k, const bf16* __restrict__ v, const float* __restrict__ cos,
+    const float* __restrict__ sin, bf16* __restrict__ krot, bf16* __restrict__ vt, int Sk,
+    int Skp, int Hkv, int64_t ksb, int64_t kss, int64_t ksh, int64_t vsb, int64_t vss,
+    int64_t vsh, int k_rotated) {
+  constexpr int HALF = D / 2;
+  constexpr int CP = HALF / 8;
+  constexpr int VLD = D + 8;
+  __shared__ __attribute__((aligned(16))) bf16 sv[BN * VLD];
+  const int s0 = blockIdx.x * BN;
+  const int bh = blockIdx.y;
+  const int b = bh / Hkv, g = bh % Hkv;
+  const int tid = threadIdx.x;
+
+  for (int it = tid; it < BN * CP; it += 256) {
+    const int key = it / CP, c = it % CP;
+    const int s = s0 + key;
+    u32x4 o1 = {0u, 0u, 0u, 0u}, o2 = {0u, 0u, 0u, 0u};
+    if (s < Sk) {
+      const bf16* src = k + b * ksb + (int64_t)s * kss + g * ksh;
+      const u32x4 a = *(const u32x4*)(src + 8 * c);
+      const u32x4 bb = *(const u32x4*)(src + 8 * c + HALF);
+      if (k_rotated) {
+        o1 = a;
+        o2 = bb;
+      } else {
+        float x1[8], x2[8], r1[8], r2[8];
+        unpack8(a, x1);
+        unpack8(bb, x2);
+        const float* cr = cos + (int64_t)s * HALF + 8 * c;
+        const float* sr = sin + (int64_t)s * HALF + 8 * c;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) rope_pair<bf16>(x1[j], x2[j], cr[j], sr[j], r1[j], r2[j]);
+        o1 = pack8(r1);
+        o2 = pack8(r2);
+      }
+    }
+    bf16* dst = krot + ((int64_t)bh * Skp + s) * D;
+    *(u32x4*)(dst + 8 * c) = o1;
+    *(u32x4*)(dst + 8 * c + HALF) = o2;
+  }
+
+  for (int it = tid; it < BN * (D / 8); it += 256) {
+    const int key = it / (D / 8), c = it % (D / 8);
+    const int s = s0 + key;
+    u32x4 a = {0u, 0u, 0u, 0u};
+    if (s < Sk) a = *(const u32x4*)(v + b * vsb + (int64_t)s * vss + g * vsh + 8 * c);
+    *(u32x4*)(&sv[key * VLD + 8 * c]) = a;
+  }
+  __syncthreads();
+  for (int it = tid; it < D * (BN / 8); it += 256) {
+    const int d = it / (BN / 8), pc = it % (BN / 8);
+    float f[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) f[j] = (float)sv[vt_logical_key(8 * pc + j) * VLD + d];
+    *(u32x4*)(vt + ((int64_t)bh * D + d) * Skp + s0 + 8 * pc) = pack8(f);
+  }
+}
+
+// Block-id remap so that the workgroups one XCD runs are a contiguous range of
+// logical ids (the dispatcher deals ids round-robin over the 8 XCDs): blocks of
+// one KV head then share that XCD's L2.
+__device__ __forceinline__ int xcd_logical_id(int L, int nblk) {
+  const int per = nblk / 8, rem = nblk % 8;
+  const int xcd = L % 8, idx = L / 8;
+  return xcd * per + min(xcd, rem) + idx;
+}
+
+struct RowInfo {
+  int b, g, hq, pos, p0;
+  bool q_valid;
+};
+
+__device__ __forceinline__ RowInfo row_info(int logical, int nqb, int Hkv, int n_rep, int bm_pos,
+                                            int Sq, int r) {
+  RowInfo ri;
+  const int bh = logical / nqb;
+  const int qb = nqb - 1 - (logical % nqb);  // longest causal rows first
+  ri.b = bh / Hkv;
+  ri.g = bh % Hkv;
+  ri.p0 = qb * bm_pos;
+  const bool row_valid = r < n_rep * bm_pos;
+  const int hl = row_valid ? r / bm_pos : 0;
+  ri.pos = ri.p0 + (row_valid ? r % bm_pos : 0);
+  ri.q_valid = row_valid && ri.pos < Sq;
+  ri.hq = ri.g * n_rep + hl;
+  return ri;
+}
+
+// Load this lane's rotated Q fragment: slots ks cover d = 16ks + 8h + 0..7.
+template <int D>
+__device__ __forceinline__ void load_q_frag(const bf16* __restrict__ q,
+                                            const float* __restrict__ cos,
+                                            const float* __restrict__ sin, const RowInfo& ri,
+                                            int Sq, int Hq, int hh, bf16x8* qf) {
+  constexpr int KS = D / 16, HALF = D / 2;
+  if (!ri.q_valid) {
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) qf[ks] = as_bf16x8(u32x4{0u, 0u, 0u, 0u});
+    return;
+  }
+  const bf16* qrow = q + (((int64_t)ri.b * Sq + ri.pos) * Hq + ri.hq) * D;
+  const float* cr = cos + (int64_t)ri.pos * HALF;
+  const float* sr = sin + (int64_t)ri.pos * HALF;
+#pragma unroll
+  for (int ks = 0; ks < KS / 2; ++ks) {
+    const int d0 = 16 * ks + 8 * hh;
+    float x1[8], x2[8], r1[8], r2[8];
+    unpack8(*(const u32x4*)(qrow + d0), x1);
+    unpack8(*(const u32x4*)(qrow + d0 + HALF), x2);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) rope_pair<bf16>(x1[j], x2[j], cr[d0 + j], sr[d0 + j], r1[j], r2[j]);
+    qf[ks] = as_bf16x8(pack8(r1));
+    qf[ks + KS / 2] = as_bf16x8(pack8(r2));
+  }
+}
+
+template <int D>
+__global__ __launch_bounds__(256, 2) void fwd_mfma_kernel(
+    const bf16* __restrict__ q, const float* __restrict__ cos, const float* __restrict__ sin,
+    const bf16* __restrict__ krot, const bf16* __restrict__ vt, bf16* __restrict__ out,
+    float* __restrict__ lse, int Sq, int Sk, int Skp, int Hq, int Hkv, int n_rep, int bm_pos,
+    int nqb, float scale_log2, int causal) {
+  constexpr int KS = D / 16, DT = D / 32;
+  constexpr int KLD = D + 8, VLD = BN + 8;
+  constexpr int KCH = BN * D / 8 / 256, VCH = D * BN / 8 / 256;
+  __shared__ __attribute__((aligned(16))) bf16 sK[BN * KLD];
+  __shared__ __attribute__((aligned(16))) bf16 sV[D * VLD];
+
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, hh = lane >> 5, c32 = lane & 31;
+  const int logical = xcd_logical_id(blockIdx.x, gridDim.x);
+  const RowInfo ri = row_info(logical, nqb, Hkv, n_rep, bm_pos, Sq, w * 32 + c32);
+  const int bh = ri.b * Hkv + ri.g;
+
+  bf16x8 qf[KS];
+  load_q_frag<D>(q, cos, sin, ri, Sq, Hq, hh, qf);
+
+  const int kend = causal ? min(Sk, min(ri.p0 + bm_pos, Sq)) : Sk;
+  const int ntiles = (kend + BN - 1) / BN;
+  const bf16* kbase = krot + (int64_t)bh * Skp * D;
+  const bf16* vbase = vt + (int64_t)bh * D * Skp;
+
+  u32x4 rk[KCH], rv[VCH];
+  auto gload = [&](int t) {
+#pragma unroll
+    for (int i = 0; i < KCH; ++i) {
+      const int id = tid + 256 * i, row = id / (D / 8), col = id % (D / 8);
+      rk[i] = *(const u32x4*)(kbase + (int64_t)(t * BN + row) * D + 8 * col);
+    }
+#pragma unroll
+    for (int i = 0; i < VCH; ++i) {
+      const int id = tid + 256 * i, row = id / (BN / 8), col = id % (BN / 8);
+      rv[i] = *(const u32x4*)(vbase + (int64_t)row * Skp + t * BN + 8 * col);
+    }
+  };
+  auto lstore = [&]() {
+#pragma unroll
+    for (int i = 0; i < KCH; ++i) {
+      const int id = tid + 256 * i, row = id / (D / 8), col = id % (D / 8);
+      *(u32x4*)(&sK[row * KLD + 8 * col]) = rk[i];
+    }
+#pragma unroll
+    for (int i = 0; i < VCH; ++i) {
+      const int id = tid + 256 * i, row = id / (BN / 8), col = id % (BN / 8);
+      *(u32x4*)(&sV[row * VLD + 8 * col]) = rv[i];
+    }
+  };
+
+  float m = -INFINITY, lsum = 0.f;
+  f32x16 acc[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[dt][i] = 0.f;
+
+  if (ntiles > 0) gload(0);
+  for (int t = 0; t < ntiles; ++t) {
+    __syncthreads();
+    lstore();
+    __syncthreads();
+    if (t + 1 < ntiles) gload(t + 1);
+
+    f32x16 s[2];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) s[mt][i] = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) {
+        const bf16x8 a = *(const bf16x8*)(&sK[(32 * mt + c32) * KLD + 16 * ks + 8 * hh]);
+        s[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[ks], s[mt], 0, 0, 0);
+      }
+    }
+
+    const int k0 = t * BN;
+    const bool need_mask = (causal && k0 + BN - 1 > ri.p0) || (k0 + BN > Sk);
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        float x = s[mt][i] * scale_log2;
+        if (need_mask) {
+          const int key = k0 + 32 * mt + 8 * (i >> 2) + 4 * hh + (i & 3);
+          if ((causal && key > ri.pos) || key >= Sk) x = -INFINITY;
+        }
+        s[mt][i] = x;
+        tmax = fmaxf(tmax, x);
+      }
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+    const float mnew = fmaxf(m, tmax);
+    const float alpha = fast_exp2(m - mnew);
+    float psum = 0.f;
+    u32x4 pk[4];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int i = 0; i < 16; i += 2) {
+        const float p0 = fast_exp2(s[mt][i] - mnew);
+        const float p1 = fast_exp2(s[mt][i + 1] - mnew);
+        psum += p0 + p1;
+        pk[2 * mt + (i >> 3)][(i & 7) >> 1] = pack2(p0, p1);
+      }
+    lsum = lsum * alpha + psum;
+    m = mnew;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc[dt][i] *= alpha;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const bf16x8 pb = as_bf16x8(pk[c]);
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        const bf16x8 a = *(const bf16x8*)(&sV[(32 * dt + c32) * VLD + 16 * c + 8 * hh]);
+        acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb, acc[dt], 0, 0, 0);
+      }
+    }
+  }
+
+  const float ltot = lsum + __shfl_xor(lsum, 32, 64);
+  const float inv = 1.f / ltot;
+  if (ri.q_valid) {
+    bf16* orow = out + (((int64_t)ri.b * Sq + ri.pos) * Hq + ri.hq) * D;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int gi = 0; gi < 4; ++gi) {
+        const int d = 32 * dt + 8 * gi + 4 * hh;
+        u32x2 pk2;
+        pk2[0] = pack2(acc[dt][4 * gi] * inv, acc[dt][4 * gi + 1] * inv);
+        pk2[1] = pack2(acc[dt][4 * gi + 2] * inv, acc[dt][4 * gi + 3] * inv);
+        *(u32x2*)(orow + d) = pk2;
+      }
+    if (lse != nullptr && hh == 0)
+      lse[((int64_t)ri.b * Hq + ri.hq) * Sq + ri.pos] = (m + log2f(ltot)) * kLn2;
+  }
+}
+
+// Capture probabilities P = exp(s - lse) as float32 [B, Hq, Sq, Sk].
+// S = Q·K^T with Q the A operand (this lane's rotated Q fragment doubles as the
+// A operand: row = l%32, k = 8h + j) and K^T the B operand read from LDS, so a
+// C register i holds (query row 8*(i/4)+4h+(i%4), key l%32): for a fixed i the
+// 32 lanes of one half write 32 consecutive floats of one row.  Key tiles fully
+// above the diagonal are written as zeros without computing.
+template <int D>
+__global__ __launch_bounds__(256, 2) void capture_probs_mfma_kernel(
+    const bf16* __restrict__ q, const float* __restrict__ cos, const float* __restrict__ sin,
+    const bf16* __restrict__ krot, const float* __restrict__ lse, float* __restrict__ probs,
+    int Sq, int Sk, int Skp, int Hq, int Hkv, int n_rep, int bm_pos, int nqb, float scale_log2,
+    int causal) {
+  constexpr int KS = D / 16;
+  constexpr int KLD = D + 8;
+  constexpr int KCH = BN * D / 8 / 256;
+  __shared__ __attribute__((aligned(16))) bf16 sK[BN * KLD];
+  __shared__ float sL[ROWS];
+  __shared__ int sRowOff[ROWS];  // row offset of (hq, pos) in units of Sk floats, or -1
+
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, hh = lane >> 5, c32 = lane & 31;
+  const int logical = xcd_logical_id(blockIdx.x, gridDim.x);
+  const RowInfo ri = row_info(logical, nqb, Hkv, n_rep, bm_pos, Sq, w * 32 + c32);
+  const int bh = ri.b * Hkv + ri.g;
+
+  if (hh == 0) {
+    const int r = w * 32 + c32;
+    const int64_t ro = ((int64_t)ri.b * Hq + ri.hq) * Sq + ri.pos;
+    sL[r] = ri.q_valid ? lse[ro] * kLog2e : 0.f;
+    sRowOff[r] = ri.q_valid ? (int)(ri.hq - (int64_t)ri.g * n_rep) * Sq + (ri.pos - ri.p0) : -1;
+  }
+  bf16x8 qf[KS];
+  load_q_frag<D>(q, cos, sin, ri, Sq, Hq, hh, qf);
+  __syncthreads();
+
+  // per-lane rows this lane stores (register i -> row 8*(i/4)+4h+(i%4) of the wave)
+  const int qmax = min(ri.p0 + bm_pos, Sq) - 1;  // largest position in the block
+  const int ntiles_all = (Sk + BN - 1) / BN;
+  const int ntiles = causal ? min(ntiles_all, (qmax + BN) / BN) : ntiles_all;
+  const bf16* kbase = krot + (int64_t)bh * Skp * D;
+  float* pbase = probs + (((int64_t)ri.b * Hq + (int64_t)ri.g * n_rep) * Sq + ri.p0) * Sk;
+
+  for (int t = 0; t < ntiles; ++t) {
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < KCH; ++i) {
+      const int id = tid + 256 * i, row = id / (D / 8), col = id % (D / 8);
+      *(u32x4*)(&sK[row * KLD + 8 * col]) =
+          *(const u32x4*)(kbase + (int64_t)(t * BN + row) * D + 8 * col);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+      f32x16 s;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) s[i] = 0.f;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const bf16x8 bk = *(const bf16x8*)(&sK[(32 * nt + c32) * KLD + 16 * ks + 8 * hh]);
+        s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qf[ks], bk, s, 0, 0, 0);
+      }
+      const int key = t * BN + 32 * nt + c32;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int r = w * 32 + 8 * (i >> 2) + 4 * hh + (i & 3);
+        const int off = sRowOff[r];
+        if (off < 0 || key >= Sk) continue;
+        const int pos = ri.p0 + (r % bm_pos);
+        float p = fast_exp2(s[i] * scale_log2 - sL[r]);
+        if (causal && key > pos) p = 0.f;
+        __builtin_nontemporal_store(p, pbase + (int64_t)off * Sk + key);
+      }
+    }
+  }
+  // zero the tiles right of the causal frontier
+  if (causal) {
+    const int zstart = ntiles * BN;
+    if (zstart < Sk) {
+      for (int r = 0; r < ROWS; ++r) {
+        const int off = sRowOff[r];
+        if (off < 0) continue;
+        float* prow = pbase + (int64_t)off * Sk;
+        for (int key = zstart + tid * 4; key < Sk; key += 256 * 4) {
+          if (key + 3 < Sk && (Sk & 3) == 0) {
+            __builtin_nontemporal_store(f32x4{0.f, 0.f, 0.f, 0.f}, (f32x4*)(prow + key));
+          } else {
+            for (int e = key; e < min(key + 4, Sk); ++e) __builtin_nontemporal_store(0.f, prow + e);
+          }
+        }
+      }
+    }
+  }
+}
+
+int pick_bm_pos(int n_rep) { return n_rep <= ROWS ? ROWS / n_rep : 0; }
+
+}  // namespace
+
+bool fwd_mfma_supported(const FwdArgs& a) {
+  if (a.dtype != BF16 || (a.D != 64 && a.D != 128)) return false;
+  const int n_rep = a.Hq / a.Hkv;
+  if (n_rep < 1 || n_rep > ROWS) return false;
+  auto al16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
+  if (!al16(a.q) || !al16(a.k) || !al16(a.v) || !al16(a.out) || !al16(a.cos) || !al16(a.sin))
+    return false;
+  if ((a.ksb | a.kss | a.ksh | a.vsb | a.vss | a.vsh) & 7) return false;
+  return true;
+}
+
+size_t fwd_mfma_workspace(int B, int Sk, int Hkv, int D) {
+  const size_t Skp = (size_t)((Sk + BN - 1) / BN) * BN;
+  return 2 * (size_t)B * Hkv * Skp * D * sizeof(uint16_t);
+}
+
+static int launch_kv_prep(const FwdArgs& a, bf16* krot, bf16* vt, int Skp) {
+  dim3 grid(Skp / BN, a.B * a.Hkv);
+  if (a.D == 128)
+    hipLaunchKernelGGL(kv_prep_kernel<128>, grid, dim3(256), 0, a.stream, (const bf16*)a.k,
+                       (const bf16*)a.v, a.cos, a.sin, krot, vt, a.Sk, Skp, a.Hkv, a.ksb, a.kss,
+                       a.ksh, a.vsb, a.vss, a.vsh, a.k_rotated);
+  else
+    hipLaunchKernelGGL(kv_prep_kernel<64>, grid, dim3(256), 0, a.stream, (const bf16*)a.k,
+                       (const bf16*)a.v, a.cos, a.sin, krot, vt, a.Sk, Skp, a.Hkv, a.ksb, a.kss,
+                       a.ksh, a.vsb, a.vss, a.vsh, a.k_rotated);
+  KF_CHECK_LAUNCH();
+  return KF_OK;
+}
+
+int fwd_mfma(const FwdArgs& a, void* workspace) {
+  const int Skp = (a.Sk + BN - 1) / BN * BN;
+  bf16* krot = (bf16*)workspace;
+  bf16* vt = krot + (size_t)a.B * a.Hkv * Skp * a.D;
+  int rc = launch_kv_prep(a, krot, vt, Skp);
+  if (rc) return rc;
+  const int n_rep = a.Hq / a.Hkv;
+  const int bm_pos = pick_bm_pos(n_rep);
+  const int nqb = (a.Sq + bm_pos - 1) / bm_pos;
+  const int64_t nblk = (int64_t)nqb * a.B * a.Hkv;
+  KF_CHECK_ARG(nblk < (1LL << 31), "grid too large");
+  const float scale_log2 = a.scale * kLog2e;
+  if (a.D == 128)
+    hipLaunchKernelGGL(fwd_mfma_kernel<128>, dim3((unsigned)nblk), dim3(256), 0, a.stream,
+                       (const bf16*)a.q, a.cos, a.sin, krot, vt, (bf16*)a.out, a.lse, a.Sq, a.Sk,
+                       Skp, a.Hq, a.Hkv, n_rep, bm_pos, nqb, scale_log2, a.causal);
+  else
+    hipLaunchKernelGGL(fwd_mfma_kernel<64>, dim3((unsigned)nblk), dim3(256), 0, a.stream,
+                       (const bf16*)a.q, a.cos, a.sin, krot, vt, (bf16*)a.out, a.lse, a.Sq, a.Sk,
+                       Skp, a.Hq, a.Hkv, n_rep, bm_pos, nqb, scale_log2, a.causal);
+  KF_CHECK_LAUNCH();
+  return KF_OK;
+}
+
+// Requires fwd_mfma to have run with the same workspace (krot is reused).
+int capture_probs_mfma(const FwdArgs& a, const float* lse, float* probs, void* workspace) {
+  const int Skp = (a.Sk + BN - 1) / BN * BN;
+  const bf16* krot = (const bf16*)workspace;
+  const int n_rep = a.Hq / a.Hkv;
+  const int bm_pos = pick_bm_pos(n_rep);
+  const int nqb = (a.Sq + bm_pos - 1) / bm_pos;
+  const int64_t nblk = (int64_t)nqb * a.B * a.Hkv;
+  const float scale_log2 = a.scale * kLog2e;
+  if (a.D == 128)
+    hipLaunchKernelGGL(capture_probs_mfma_kernel<128>, dim3((unsigned)nblk), dim3(256), 0,
+                       a.stream, (const bf16*)a.q, a.cos, a.sin, krot, lse, probs, a.Sq, a.Sk,
+                       Skp, a.Hq, a.Hkv, n_rep, bm_pos, nqb, scale_log2, a.causal);
+  else
+    hipLaunchKernelGGL(capture_probs_mfma_kernel<64>, dim3((unsigned)nblk), dim3(256), 0,
+                       a.stream, (const bf16*)a.q, a.cos, a.sin, krot, lse, probs, a.Sq, a.Sk,
+                       Skp, a.Hq, a.Hkv, n_rep, bm_pos, nqb, scale_log2, a.causal);
+  KF_CHECK_LAUNCH();
+  return KF_OK;
+}
+
+}  // namespace kf

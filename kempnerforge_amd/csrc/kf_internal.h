@@ -1,0 +1,80 @@
+// Internal (non-exported) argument bundles and launcher declarations shared by
+// the kernel translation units and the C-ABI layer in kf_api.hip.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../../include/kf_attn.h"
+
+namespace kf {
+
+struct FwdArgs {
+  const void* q;      // [B, Sq, Hq, D] contiguous, pre-RoPE
+  const void* k;      // element (b, s, h, d) at b*ksb + s*kss + h*ksh + d
+  const void* v;      // element (b, s, h, d) at b*vsb + s*vss + h*vsh + d
+  const float* cos;   // [Sq, D/2] float32 rows for query (and key) positions
+  const float* sin;
+  void* out;          // [B, Sq, Hq, D] contiguous
+  float* lse;         // [B, Hq, Sq] float32 (may be null for the generic path)
+  int B, Sq, Sk, Hq, Hkv, D;
+  int64_t ksb, kss, ksh, vsb, vss, vsh;
+  int k_rotated;      // 1: k already holds post-RoPE keys (KV-cache contents)
+  int causal;         // 1: top-left causal mask (query i sees keys j <= i)
+  int dtype;
+  float scale;        // softmax scale, D^-1/2
+  hipStream_t stream;
+};
+
+struct BwdArgs {
+  const void *q, *k, *v;  // [B, S, H, D] contiguous, pre-RoPE
+  const float *cos, *sin; // [S, D/2]
+  const void* out;        // forward output [B, S, Hq, D]
+  const float* lse;       // [B, Hq, S]
+  const void* dout;       // [B, S, Hq, D]
+  void *dq, *dk, *dv;     // pre-RoPE gradients, same layouts as q, k, v
+  int B, S, Hq, Hkv, D;
+  int causal, dtype;
+  float scale;
+  hipStream_t stream;
+};
+
+// generic kernels (kf_generic.hip)
+int fwd_generic(const FwdArgs& a);
+int bwd_generic(const BwdArgs& a, float* delta);
+int capture_probs_generic(const FwdArgs& a, const float* lse, float* probs);
+
+// bf16 MFMA kernels (kf_fwd.hip, kf_bwd.hip, kf_capture.hip)
+bool fwd_mfma_supported(const FwdArgs& a);
+size_t fwd_mfma_workspace(int B, int Sk, int Hkv, int D);
+int fwd_mfma(const FwdArgs& a, void* workspace);
+int capture_probs_mfma(const FwdArgs& a, const float* lse, float* probs, void* workspace);
+
+bool bwd_mfma_supported(const BwdArgs& a);
+size_t bwd_mfma_workspace(int B, int S, int Hq, int Hkv, int D);
+int bwd_mfma(const BwdArgs& a, void* workspace);
+
+// decode (kf_decode.hip)
+struct DecodeArgs {
+  const void *q_new, *k_new, *v_new;  // [B,1,Hq,D], [B,1,Hkv,D], [B,1,Hkv,D] contiguous
+  void *k_cache, *v_cache;            // [B, Hkv, Smax, D] contiguous
+  const int32_t* lens;                // [B] cached tokens per sequence = new token position
+  const float *cos, *sin;             // table; row = lens[b] - rope_row_offset
+  int64_t rope_row_offset;
+  int64_t rope_rows;                  // rows in the tables
+  void* out;                          // [B, 1, Hq, D]
+  int B, Smax, Hq, Hkv, D, max_len;   // max_len >= lens[b] + 1 for every b
+  int dtype;
+  float scale;
+  hipStream_t stream;
+};
+size_t decode_workspace(int B, int Hq, int D, int max_len);
+int decode(const DecodeArgs& a, void* workspace);
+
+// cache append (kf_decode.hip)
+int cache_append(const void* k_new, const void* v_new, const float* cos, const float* sin,
+                 void* k_cache, void* v_cache, int start, int B, int Snew, int Hkv, int Smax,
+                 int D, int dtype, hipStream_t stream);
+
+}  // namespace kf

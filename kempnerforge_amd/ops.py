@@ -1,0 +1,256 @@
+"""PyTorch operators over the C ABI (``include/kf_attn.h``).
+
+``attention`` is a ``torch.library`` custom op with a fake (meta) kernel and an
+autograd formula, so it works under ``torch.compile`` (the reference compiles
+the model, ``kempnerforge/distributed/parallel.py:590-592``) and under
+non-reentrant activation checkpointing (``kempnerforge/distributed/parallel.py:104``):
+the forward saves q, k, v (pre-RoPE), out and lse and is deterministic, so a
+recomputed forward reproduces the saved tensors bit for bit.
+
+All ops launch on ``torch.cuda.current_stream()``, allocate outputs and
+workspace through PyTorch's caching allocator, and never synchronise.  They
+only accept GPU tensors: there is no CPU path.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from kempnerforge_amd import _lib
+
+_DTYPES = {torch.float32: _lib.DTYPE_F32, torch.bfloat16: _lib.DTYPE_BF16,
+           torch.float16: _lib.DTYPE_F16}
+
+
+def _dtype_code(t: torch.Tensor) -> int:
+    try:
+        return _DTYPES[t.dtype]
+    except KeyError:
+        raise TypeError(f"kempnerforge_amd attention: unsupported dtype {t.dtype}") from None
+
+
+def _require_gpu(*ts: torch.Tensor) -> None:
+    for t in ts:
+        if t.device.type != "cuda":
+            raise RuntimeError(
+                "kempnerforge_amd attention runs only on a ROCm GPU (gfx950); got a tensor on "
+                f"{t.device}. There is no CPU fallback."
+            )
+
+
+def _stream(t: torch.Tensor) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def _ptr(t: torch.Tensor | None) -> ctypes.c_void_p:
+    return ctypes.c_void_p(0 if t is None else t.data_ptr())
+
+
+def _workspace(nbytes: int, device) -> torch.Tensor:
+    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
+
+
+def _rope_table(t: torch.Tensor, rows: int, half: int, name: str) -> torch.Tensor:
+    if t.dtype != torch.float32:
+        t = t.float()
+    t = t.contiguous()
+    if t.dim() != 2 or t.shape[0] < rows or t.shape[1] != half:
+        raise ValueError(f"{name} must be [>= {rows}, {half}] (got {tuple(t.shape)})")
+    return t
+
+
+# --------------------------------------------------------------------------- raw calls
+def fwd_raw(q, k, v, cos, sin, *, causal: bool, k_rotated: bool, k_layout: str = "bshd"):
+    """out, lse = attention(q, k, v) with RoPE fused (``kf_attn_fwd``).
+
+    q ``[B,Sq,Hq,D]``; k/v ``[B,Sk,Hkv,D]`` (``k_layout="bshd"``) or
+    ``[B,Hkv,Sk,D]`` views into a KV cache (``k_layout="bhsd"``, keys already
+    rotated).  Returns out ``[B,Sq,Hq,D]`` and lse ``[B,Hq,Sq]`` float32.
+    """
+    _require_gpu(q, k, v)
+    lib = _lib.load()
+    q = q.contiguous()
+    B, Sq, Hq, D = q.shape
+    if k_layout == "bshd":
+        Sk, Hkv = k.shape[1], k.shape[2]
+        kstr = (k.stride(0), k.stride(1), k.stride(2))
+        vstr = (v.stride(0), v.stride(1), v.stride(2))
+    else:
+        Hkv, Sk = k.shape[1], k.shape[2]
+        kstr = (k.stride(0), k.stride(2), k.stride(1))
+        vstr = (v.stride(0), v.stride(2), v.stride(1))
+    if k.stride(-1) != 1 or v.stride(-1) != 1 or tuple(v.shape) != tuple(k.shape):
+        raise ValueError("k and v must have the same shape and a contiguous head dim")
+    if k.dtype != q.dtype or v.dtype != q.dtype:
+        raise TypeError("q, k, v must share a dtype")
+    cos = _rope_table(cos, Sq, D // 2, "rope_cos")
+    sin = _rope_table(sin, Sq, D // 2, "rope_sin")
+    dt = _dtype_code(q)
+    out = torch.empty_like(q)
+    lse = torch.empty(B, Hq, Sq, dtype=torch.float32, device=q.device)
+    nbytes = _lib.size_out()
+    _lib.check(lib.kf_attn_fwd_workspace_size(B, Sq, Sk, Hq, Hkv, D, dt, ctypes.byref(nbytes)),
+               "kf_attn_fwd_workspace_size")
+    ws = _workspace(nbytes.value, q.device)
+    _lib.check(lib.kf_attn_fwd(_ptr(q), _ptr(k), _ptr(v), _ptr(cos), _ptr(sin), _ptr(out),
+                               _ptr(lse), _ptr(ws), ws.numel(), B, Sq, Sk, Hq, Hkv, D, *kstr,
+                               *vstr, int(k_rotated), int(causal), dt, _stream(q)),
+               "kf_attn_fwd")
+    return out, lse
+
+
+def bwd_raw(q, k, v, cos, sin, out, lse, dout, *, causal: bool):
+    """dq, dk, dv for :func:`fwd_raw` with un-rotated BSHD k (``kf_attn_bwd``)."""
+    _require_gpu(q, k, v, out, lse, dout)
+    lib = _lib.load()
+    q, k, v, out, dout = (t.contiguous() for t in (q, k, v, out, dout))
+    lse = lse.contiguous()
+    B, S, Hq, D = q.shape
+    Hkv = k.shape[2]
+    cos = _rope_table(cos, S, D // 2, "rope_cos")
+    sin = _rope_table(sin, S, D // 2, "rope_sin")
+    dt = _dtype_code(q)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    nbytes = _lib.size_out()
+    _lib.check(lib.kf_attn_bwd_workspace_size(B, S, Hq, Hkv, D, dt, ctypes.byref(nbytes)),
+               "kf_attn_bwd_workspace_size")
+    ws = _workspace(nbytes.value, q.device)
+    _lib.check(lib.kf_attn_bwd(_ptr(q), _ptr(k), _ptr(v), _ptr(cos), _ptr(sin), _ptr(out),
+                               _ptr(lse), _ptr(dout), _ptr(dq), _ptr(dk), _ptr(dv), _ptr(ws),
+                               ws.numel(), B, S, Hq, Hkv, D, int(causal), dt, _stream(q)),
+               "kf_attn_bwd")
+    return dq, dk, dv
+
+
+def decode_raw(q_new, k_new, v_new, k_cache, v_cache, lens, cos, sin, *, rope_row_offset: int,
+               max_len: int):
+    """One decode step (``kf_attn_decode``); writes the rotated new k and v into
+    the caches at ``lens[b]`` and returns out ``[B,1,Hq,D]``."""
+    _require_gpu(q_new, k_new, v_new, k_cache, v_cache, lens)
+    lib = _lib.load()
+    q_new, k_new, v_new = (t.contiguous() for t in (q_new, k_new, v_new))
+    if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
+        raise ValueError("KV caches must be contiguous [B, n_kv_heads, max_seq_len, head_dim]")
+    if lens.dtype != torch.int32 or not lens.is_contiguous():
+        raise TypeError("lens must be a contiguous int32 tensor")
+    B, _, Hq, D = q_new.shape
+    Hkv, Smax = k_cache.shape[1], k_cache.shape[2]
+    cos = _rope_table(cos, 1, D // 2, "rope_cos")
+    sin = _rope_table(sin, 1, D // 2, "rope_sin")
+    dt = _dtype_code(q_new)
+    out = torch.empty_like(q_new)
+    nbytes = _lib.size_out()
+    _lib.check(lib.kf_attn_decode_workspace_size(B, Hq, Hkv, D, max_len, dt, ctypes.byref(nbytes)),
+               "kf_attn_decode_workspace_size")
+    ws = _workspace(nbytes.value, q_new.device)
+    _lib.check(lib.kf_attn_decode(_ptr(q_new), _ptr(k_new), _ptr(v_new), _ptr(k_cache),
+                                  _ptr(v_cache), _ptr(lens), _ptr(cos), _ptr(sin),
+                                  int(rope_row_offset), cos.shape[0], _ptr(out), _ptr(ws), ws.numel(), B, Smax,
+                                  Hq, Hkv, D, int(max_len), dt, _stream(q_new)),
+               "kf_attn_decode")
+    return out
+
+
+def cache_append_raw(k_new, v_new, cos, sin, k_cache, v_cache, start: int) -> None:
+    """Rotate ``k_new [B,S,Hkv,D]`` and write it and ``v_new`` into the caches at
+    positions ``start..start+S-1`` (``kf_kv_cache_append``)."""
+    _require_gpu(k_new, v_new, k_cache, v_cache)
+    lib = _lib.load()
+    k_new, v_new = k_new.contiguous(), v_new.contiguous()
+    B, Snew, Hkv, D = k_new.shape
+    Smax = k_cache.shape[2]
+    cos = _rope_table(cos, Snew, D // 2, "rope_cos")
+    sin = _rope_table(sin, Snew, D // 2, "rope_sin")
+    _lib.check(lib.kf_kv_cache_append(_ptr(k_new), _ptr(v_new), _ptr(cos), _ptr(sin),
+                                      _ptr(k_cache), _ptr(v_cache), int(start), B, Snew, Hkv,
+                                      Smax, D, _dtype_code(k_new), _stream(k_new)),
+               "kf_kv_cache_append")
+
+
+def capture_raw(q, k, v, cos, sin, *, causal: bool, k_rotated: bool, k_layout: str = "bshd"):
+    """out, probs, lse with probs the float32 softmax matrix ``[B,Hq,Sq,Sk]``
+    (``kf_attn_capture``)."""
+    _require_gpu(q, k, v)
+    lib = _lib.load()
+    q = q.contiguous()
+    B, Sq, Hq, D = q.shape
+    if k_layout == "bshd":
+        Sk, Hkv = k.shape[1], k.shape[2]
+        kstr = (k.stride(0), k.stride(1), k.stride(2))
+        vstr = (v.stride(0), v.stride(1), v.stride(2))
+    else:
+        Hkv, Sk = k.shape[1], k.shape[2]
+        kstr = (k.stride(0), k.stride(2), k.stride(1))
+        vstr = (v.stride(0), v.stride(2), v.stride(1))
+    if k.stride(-1) != 1 or v.stride(-1) != 1:
+        raise ValueError("k and v need a contiguous head dim")
+    cos = _rope_table(cos, Sq, D // 2, "rope_cos")
+    sin = _rope_table(sin, Sq, D // 2, "rope_sin")
+    dt = _dtype_code(q)
+    out = torch.empty_like(q)
+    lse = torch.empty(B, Hq, Sq, dtype=torch.float32, device=q.device)
+    probs = torch.empty(B, Hq, Sq, Sk, dtype=torch.float32, device=q.device)
+    nbytes = _lib.size_out()
+    _lib.check(lib.kf_attn_capture_workspace_size(B, Sq, Sk, Hq, Hkv, D, dt, ctypes.byref(nbytes)),
+               "kf_attn_capture_workspace_size")
+    ws = _workspace(nbytes.value, q.device)
+    _lib.check(lib.kf_attn_capture(_ptr(q), _ptr(k), _ptr(v), _ptr(cos), _ptr(sin), _ptr(probs),
+                                   _ptr(out), _ptr(lse), _ptr(ws), ws.numel(), B, Sq, Sk, Hq, Hkv,
+                                   D, *kstr, *vstr, int(k_rotated), int(causal), dt, _stream(q)),
+               "kf_attn_capture")
+    return out, probs, lse
+
+
+# --------------------------------------------------------------------------- custom ops
+@torch.library.custom_op("kf::attn_fwd", mutates_args=(), device_types="cuda")
+def attn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos: torch.Tensor,
+             sin: torch.Tensor, causal: bool) -> tuple[torch.Tensor, torch.Tensor]:
+    return fwd_raw(q, k, v, cos, sin, causal=causal, k_rotated=False)
+
+
+@attn_fwd.register_fake
+def _(q, k, v, cos, sin, causal):
+    B, S, Hq, _ = q.shape
+    return torch.empty_like(q), q.new_empty(B, Hq, S, dtype=torch.float32)
+
+
+@torch.library.custom_op("kf::attn_bwd", mutates_args=(), device_types="cuda")
+def attn_bwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos: torch.Tensor,
+             sin: torch.Tensor, out: torch.Tensor, lse: torch.Tensor, dout: torch.Tensor,
+             causal: bool) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    return bwd_raw(q, k, v, cos, sin, out, lse, dout, causal=causal)
+
+
+@attn_bwd.register_fake
+def _(q, k, v, cos, sin, out, lse, dout, causal):
+    return torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+
+
+def _setup_context(ctx, inputs, output):
+    q, k, v, cos, sin, causal = inputs
+    out, lse = output
+    ctx.save_for_backward(q, k, v, cos, sin, out, lse)
+    ctx.causal = causal
+
+
+def _backward(ctx, dout, dlse):
+    q, k, v, cos, sin, out, lse = ctx.saved_tensors
+    dq, dk, dv = attn_bwd(q, k, v, cos, sin, out, lse, dout.contiguous(), ctx.causal)
+    return dq, dk, dv, None, None, None
+
+
+attn_fwd.register_autograd(_backward, setup_context=_setup_context)
+
+
+def attention(q, k, v, rope_cos, rope_sin, *, causal: bool = True) -> torch.Tensor:
+    """Differentiable RoPE + GQA + (causal) attention on BSHD tensors.
+
+    Equivalent to the reference's ``apply_rope`` on q and k
+    (``kempnerforge/model/attention.py:165-166``), ``repeat_interleave``
+    (``:173-175``) and ``F.scaled_dot_product_attention(..., is_causal=causal)``
+    (``:231``), returning BSHD instead of BHSD.
+    """
+    out, _ = attn_fwd(q, k, v, rope_cos, rope_sin, causal)
+    return out

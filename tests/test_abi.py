@@ -1,0 +1,111 @@
+"""CPU checks of the boundary: the C-ABI library loads and exports every entry
+point include/kf_attn.h declares, and the drop-in module keeps the reference's
+contract (kempnerforge/model/attention.py:29-114) without touching a GPU."""
+
+from __future__ import annotations
+
+import ctypes
+import inspect
+import os
+import re
+
+import pytest
+import torch
+
+import kempnerforge_amd
+from kempnerforge_amd import _lib
+from kempnerforge_amd.attention import Attention, KVCache
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "kf_attn.h")
+
+
+def _declared_symbols():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^(?:int|const char\*)\s+(kf_\w+)\(", text, re.M)))
+
+
+def test_header_declares_the_entry_points():
+    assert set(_declared_symbols()) >= {
+        "kf_version", "kf_last_error", "kf_attn_fwd", "kf_attn_bwd", "kf_attn_decode",
+        "kf_kv_cache_append", "kf_attn_capture", "kf_attn_fwd_workspace_size",
+        "kf_attn_bwd_workspace_size", "kf_attn_decode_workspace_size",
+        "kf_attn_capture_workspace_size",
+    }
+
+
+def test_library_exports_every_declared_symbol():
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.skip("library not built")
+    lib = ctypes.CDLL(_lib.LIB_PATH)
+    for name in _declared_symbols():
+        assert hasattr(lib, name), name
+    assert set(_lib.SIGNATURES) == set(_declared_symbols())
+
+
+def test_host_only_calls():
+    """Entry points that never touch the device: version, workspace sizing and
+    argument validation (which rejects before any launch)."""
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.skip("library not built")
+    lib = _lib.load()
+    assert lib.kf_version() >= 100
+    n = _lib.size_out()
+    assert lib.kf_attn_fwd_workspace_size(4, 4096, 4096, 32, 8, 128, 1, ctypes.byref(n)) == 0
+    assert n.value == 2 * 4 * 8 * 4096 * 128 * 2
+    assert lib.kf_attn_fwd_workspace_size(1, 8, 8, 6, 4, 64, 1, ctypes.byref(n)) == 1
+    assert b"multiple" in lib.kf_last_error()
+    assert lib.kf_attn_fwd_workspace_size(1, 8, 8, 4, 4, 63, 1, ctypes.byref(n)) == 1
+    assert lib.kf_attn_decode_workspace_size(32, 32, 8, 128, 8193, 1, ctypes.byref(n)) == 0
+    assert n.value == 32 * 32 * 33 * 130 * 4
+    # kv-cache overflow is rejected on the host (reference generate.py:92-96 guard)
+    rc = lib.kf_kv_cache_append(ctypes.c_void_p(16), ctypes.c_void_p(16), ctypes.c_void_p(16),
+                                ctypes.c_void_p(16), ctypes.c_void_p(16), ctypes.c_void_p(16),
+                                10, 1, 8, 2, 16, 64, 1, None)
+    assert rc == 1 and b"overflow" in lib.kf_last_error()
+
+
+def test_attention_constructor_contract():
+    sig = inspect.signature(Attention.__init__)
+    assert list(sig.parameters) == ["self", "dim", "n_heads", "n_kv_heads", "head_dim",
+                                    "qk_norm", "sdpa_backend"]
+    fsig = inspect.signature(Attention.forward)
+    assert list(fsig.parameters) == ["self", "x", "rope_cos", "rope_sin", "kv_cache", "doc_ids",
+                                     "key_padding_mask"]
+    a = Attention(dim=256, n_heads=8, n_kv_heads=2, qk_norm=True, sdpa_backend="math")
+    assert (a.n_heads, a.n_kv_heads, a.head_dim, a.n_rep) == (8, 2, 32, 4)
+    assert a.sdpa_backend == "math" and a.capture_attention_weights is False
+    assert a.last_attention_weights is None
+    assert sorted(a.state_dict()) == ["k_norm.weight", "k_proj.weight", "o_proj.weight",
+                                      "q_norm.weight", "q_proj.weight", "v_proj.weight"]
+    assert a.q_proj.weight.shape == (256, 256) and a.k_proj.weight.shape == (64, 256)
+    assert Attention(dim=128, n_heads=4, n_kv_heads=4).q_norm is None
+
+
+def test_kvcache_contract_cpu():
+    # reference tests/unit/test_generate.py:33-89 (storage and update semantics)
+    c = KVCache(2, 16, 4, 8, torch.float32, torch.device("cpu"))
+    assert c.k.shape == (2, 4, 16, 8) and c.seq_len == 0 and (c.k == 0).all()
+    k1, v1 = torch.randn(2, 4, 3, 8), torch.randn(2, 4, 3, 8)
+    ka, va = c.update(k1, v1)
+    assert ka.shape == (2, 4, 3, 8) and torch.equal(ka, k1) and c.seq_len == 3
+    k2, v2 = torch.randn(2, 4, 1, 8), torch.randn(2, 4, 1, 8)
+    ka, va = c.update(k2, v2)
+    assert torch.equal(ka, torch.cat([k1, k2], 2)) and torch.equal(va, torch.cat([v1, v2], 2))
+    assert c.lens.tolist() == [4, 4]
+
+
+def test_cpu_tensors_are_rejected_loudly():
+    a = Attention(dim=64, n_heads=4, n_kv_heads=2)
+    cos, sin = kempnerforge_amd.precompute_rope_frequencies(16, 8)
+    with pytest.raises(RuntimeError):
+        a(torch.randn(1, 8, 64), cos, sin)
+
+
+def test_oracle_not_imported_by_product():
+    pkg = os.path.join(ROOT, "kempnerforge_amd")
+    for dirpath, _, files in os.walk(pkg):
+        for f in files:
+            if f.endswith(".py"):
+                src = open(os.path.join(dirpath, f)).read()
+                assert "oracle" not in src, f

@@ -1,0 +1,108 @@
+"""GPU parity of the forward (kf_attn_fwd) against the CPU oracle.
+
+Tolerances (north-star): float32 max-abs 1e-5; bfloat16 max-abs 2e-2 on the
+output and 1e-3 on the LSE, both against the float64 oracle evaluated from the
+same inputs with the reference's RoPE rounding.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+import make_fixtures as mf
+from gpu_util import DEV, announce, load_fixture, max_abs, seeded
+from kempnerforge_amd import ops
+from oracle import attention_ref as ref
+
+pytestmark = pytest.mark.gpu
+
+TOL = {torch.float32: 1e-5, torch.bfloat16: 2e-2, torch.float16: 2e-2}
+
+
+def _run(q, k, v, cos, sin, causal=True):
+    return ops.fwd_raw(q.to(DEV), k.to(DEV), v.to(DEV), cos.to(DEV), sin.to(DEV),
+                       causal=causal, k_rotated=False)
+
+
+@pytest.mark.parametrize("name", list(mf.ATTN_CASES))
+def test_fixture(name):
+    announce(f"fwd fixture {name}")
+    fx = load_fixture(name)
+    dtype = mf.ATTN_CASES[name][0]
+    q, k, v, _, cos, sin = mf.attn_inputs(*mf.ATTN_CASES[name])
+    out, lse = _run(q, k, v, cos, sin)
+    torch.cuda.synchronize()
+    assert max_abs(out, torch.from_numpy(fx["out"])) <= TOL[dtype]
+    assert max_abs(lse, torch.from_numpy(fx["lse"])) <= (1e-5 if dtype == torch.float32 else 1e-3)
+
+
+SHAPES = [
+    # dtype, B, S, Hq, Hkv, D, theta       (what it exercises)
+    (torch.bfloat16, 2, 200, 4, 4, 64, 1e4),     # MHA, D=64, ragged last tile
+    (torch.bfloat16, 1, 300, 8, 1, 128, 5e5),    # MQA (n_rep 8)
+    (torch.bfloat16, 1, 130, 6, 2, 128, 5e5),    # n_rep 3: 126 of 128 block rows used
+    (torch.bfloat16, 1, 1, 4, 2, 128, 5e5),      # single token
+    (torch.bfloat16, 1, 64, 32, 1, 128, 5e5),    # n_rep 32: 4 positions per block
+    (torch.bfloat16, 1, 77, 4, 2, 32, 1e4),      # generic kernel (D=32)
+    (torch.float16, 1, 90, 4, 2, 128, 1e4),      # generic kernel (fp16)
+    (torch.float32, 1, 150, 8, 2, 128, 5e5),     # generic kernel (fp32, D=128)
+]
+
+
+@pytest.mark.parametrize("cfg", SHAPES, ids=lambda c: "-".join(map(str, c)))
+@pytest.mark.parametrize("causal", [True, False])
+def test_shapes(cfg, causal):
+    dtype, B, S, Hq, Hkv, D, theta = cfg
+    announce(f"fwd shape {cfg} causal={causal}")
+    q = seeded((B, S, Hq, D), 0, dtype)
+    k = seeded((B, S, Hkv, D), 1, dtype)
+    v = seeded((B, S, Hkv, D), 2, dtype)
+    cos, sin = ref.rope_tables(D, S, theta)
+    out, lse = _run(q, k, v, cos, sin, causal)
+    o_ref, l_ref = ref.attention_fwd(q, k, v, cos, sin, causal=causal)
+    torch.cuda.synchronize()
+    assert max_abs(out, o_ref) <= TOL[dtype]
+    assert max_abs(lse, l_ref) <= (1e-5 if dtype == torch.float32 else 1e-3)
+
+
+def test_llama8b_shape_rows():
+    """C2: B=4, S=4096, Hq=32, Hkv=8, D=128, theta 5e5 — spot rows against the
+    oracle, plus size-independent properties over the whole output."""
+    B, S, Hq, Hkv, D = 4, 4096, 32, 8, 128
+    announce("fwd 8B shape")
+    q = seeded((B, S, Hq, D), 0, torch.bfloat16)
+    k = seeded((B, S, Hkv, D), 1, torch.bfloat16)
+    v = seeded((B, S, Hkv, D), 2, torch.bfloat16)
+    cos, sin = ref.rope_tables(D, S, 5e5)
+    out, lse = _run(q, k, v, cos, sin)
+    out2, lse2 = _run(q, k, v, cos, sin)
+    torch.cuda.synchronize()
+    # deterministic: a recompute (activation checkpointing) is bit-identical
+    assert torch.equal(out, out2) and torch.equal(lse, lse2)
+    # outputs are convex combinations of value rows
+    assert out.float().abs().max().item() <= v.float().abs().max().item() + 1e-2
+    assert torch.isfinite(lse).all()
+    rows = torch.tensor([0, 1, 63, 64, 127, 1000, 2047, 2048, 4000, 4095])
+    heads = torch.tensor([0, 3, 4, 17, 31])
+    o_ref, l_ref = ref.attention_fwd_rows(q, k, v, cos, sin, rows, heads=heads)
+    got_o = out.cpu()[:, rows][:, :, heads]
+    got_l = lse.cpu()[:, heads][:, :, rows]
+    assert max_abs(got_o, o_ref) <= 2e-2
+    assert max_abs(got_l, l_ref) <= 1e-3
+
+
+def test_nan_propagates():
+    announce("fwd NaN propagation")
+    B, S, Hq, Hkv, D = 1, 128, 4, 2, 128
+    q = seeded((B, S, Hq, D), 0, torch.bfloat16)
+    k = seeded((B, S, Hkv, D), 1, torch.bfloat16)
+    v = seeded((B, S, Hkv, D), 2, torch.bfloat16)
+    v[0, 5, 1, 7] = float("nan")
+    cos, sin = ref.rope_tables(D, S, 1e4)
+    out, _ = _run(q, k, v, cos, sin)
+    torch.cuda.synchronize()
+    o = out.cpu()
+    # rows >= 5 of the heads of KV group 1 see the NaN; earlier rows do not
+    assert torch.isnan(o[0, 5:, 2:4]).any() and not torch.isnan(o[0, :5]).any()
+    assert not torch.isnan(o[0, :, 0:2]).any()

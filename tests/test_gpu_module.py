@@ -1,0 +1,164 @@
+"""The drop-in Attention / KVCache on the GPU, checked the way the reference's
+own tests check the module (kempnerforge tests/unit/test_model.py:114-187,
+test_hooks.py:169-245, test_generate.py:33-273), plus autograd, activation
+checkpointing and torch.compile compatibility."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from gpu_util import DEV, announce, max_abs
+from kempnerforge_amd import Attention, KVCache, ops
+from kempnerforge_amd.position import precompute_rope_frequencies
+from oracle import attention_ref as ref
+
+pytestmark = pytest.mark.gpu
+
+
+def _reference_module_out(attn: Attention, x, cos, sin):
+    """Reference Attention.forward restated with the module's weights (CPU, fp64 math)."""
+    B, S, _ = x.shape
+    xc = x.detach().cpu()
+    W = {n: p.detach().cpu() for n, p in attn.named_parameters()}
+    q = (xc @ W["q_proj.weight"].T).view(B, S, -1, attn.head_dim)
+    k = (xc @ W["k_proj.weight"].T).view(B, S, -1, attn.head_dim)
+    v = (xc @ W["v_proj.weight"].T).view(B, S, -1, attn.head_dim)
+    o, _ = ref.attention_fwd(q, k, v, cos.cpu(), sin.cpu())
+    return o.reshape(B, S, -1).to(xc.dtype) @ W["o_proj.weight"].T
+
+
+@pytest.mark.parametrize("n_heads,n_kv", [(8, 8), (8, 2), (8, 1)])
+def test_forward_shapes_and_values(n_heads, n_kv):
+    announce(f"module fwd {n_heads}/{n_kv}")
+    torch.manual_seed(0)
+    attn = Attention(dim=256, n_heads=n_heads, n_kv_heads=n_kv).to(DEV)
+    cos, sin = precompute_rope_frequencies(32, 64)
+    x = torch.randn(2, 64, 256, device=DEV)
+    out = attn(x, cos.to(DEV), sin.to(DEV))
+    assert out.shape == (2, 64, 256)
+    want = _reference_module_out(attn, x, cos, sin)
+    assert max_abs(out, want) <= 1e-4
+
+
+def test_bf16_module_no_warnings():
+    import warnings
+
+    torch.manual_seed(0)
+    attn = Attention(dim=1024, n_heads=8, n_kv_heads=2).to(DEV).to(torch.bfloat16)
+    cos, sin = precompute_rope_frequencies(128, 128, 5e5)
+    x = torch.randn(1, 128, 1024, device=DEV, dtype=torch.bfloat16)
+    with warnings.catch_warnings():
+        warnings.filterwarnings("error")
+        with torch.no_grad():
+            out = attn(x, cos.to(DEV), sin.to(DEV))
+    assert out.dtype == torch.bfloat16
+    want = _reference_module_out(attn, x, cos, sin)
+    assert max_abs(out, want.float()) <= 5e-2
+
+
+def test_qk_norm_large_inputs_finite():
+    torch.manual_seed(0)
+    attn = Attention(dim=128, n_heads=4, n_kv_heads=4, qk_norm=True).to(DEV)
+    cos, sin = precompute_rope_frequencies(32, 16)
+    out = attn(torch.randn(1, 16, 128, device=DEV) * 100.0, cos.to(DEV), sin.to(DEV))
+    assert out.isfinite().all()
+
+
+def test_capture_matches_reference_hooks_tests():
+    announce("module capture")
+    torch.manual_seed(0)
+    attn = Attention(64, 4, 4).to(DEV).eval()
+    cos, sin = precompute_rope_frequencies(16, 32)
+    cos, sin = cos[:16].to(DEV), sin[:16].to(DEV)
+    x = torch.randn(2, 16, 64, device=DEV)
+    out_sdpa = attn(x, cos, sin)
+    assert attn.last_attention_weights is None
+    attn.capture_attention_weights = True
+    out_manual = attn(x, cos, sin)
+    w = attn.last_attention_weights
+    assert w.shape == (2, 4, 16, 16) and w.device == torch.device("cpu")
+    assert torch.allclose(w.float().sum(-1), torch.ones(2, 4, 16), atol=1e-5)
+    upper = torch.triu(torch.ones(16, 16), diagonal=1).bool()
+    assert torch.allclose(w[0, 0][upper], torch.zeros(int(upper.sum())), atol=1e-6)
+    assert torch.allclose(out_sdpa, out_manual, atol=1e-4)
+
+
+def test_backward_through_module_and_checkpoint():
+    announce("module backward + activation checkpointing")
+    torch.manual_seed(0)
+    attn = Attention(dim=512, n_heads=8, n_kv_heads=2).to(DEV).to(torch.bfloat16)
+    cos, sin = precompute_rope_frequencies(64, 256, 5e5)
+    cos, sin = cos.to(DEV), sin.to(DEV)
+    x = torch.randn(2, 256, 512, device=DEV, dtype=torch.bfloat16, requires_grad=True)
+    y = attn(x, cos, sin)
+    y.float().pow(2).mean().backward()
+    g1 = [p.grad.clone() for p in attn.parameters()] + [x.grad.clone()]
+    attn.zero_grad()
+    x.grad = None
+    from torch.utils.checkpoint import checkpoint
+
+    y2 = checkpoint(lambda t: attn(t, cos, sin), x, use_reentrant=False)
+    y2.float().pow(2).mean().backward()
+    g2 = [p.grad for p in attn.parameters()] + [x.grad]
+    for a, b in zip(g1, g2):
+        assert torch.equal(a, b)
+
+
+def test_torch_compile_fullgraph():
+    announce("torch.compile")
+    torch.manual_seed(0)
+    B, S, Hq, Hkv, D = 1, 128, 4, 2, 64
+    q = torch.randn(B, S, Hq, D, device=DEV, dtype=torch.bfloat16, requires_grad=True)
+    k = torch.randn(B, S, Hkv, D, device=DEV, dtype=torch.bfloat16, requires_grad=True)
+    v = torch.randn(B, S, Hkv, D, device=DEV, dtype=torch.bfloat16, requires_grad=True)
+    cos, sin = precompute_rope_frequencies(D, S)
+    cos, sin = cos.to(DEV), sin.to(DEV)
+
+    def f(q, k, v):
+        return ops.attention(q, k, v, cos, sin).float().sum()
+
+    eager = f(q, k, v)
+    compiled = torch.compile(f, fullgraph=True, backend="aot_eager")(q, k, v)
+    assert torch.equal(eager, compiled)
+    compiled.backward()
+    assert q.grad is not None and k.grad is not None and v.grad is not None
+
+
+def test_generate_style_decode_matches_full_forward():
+    """Prefill then single-token decode through KVCache equals one causal forward
+    over the whole sequence (reference generate.py:100-124 flow)."""
+    announce("module prefill + decode")
+    torch.manual_seed(0)
+    dim, H, Hkv, D = 512, 8, 2, 64
+    attn = Attention(dim, H, Hkv).to(DEV).to(torch.bfloat16).eval()
+    T, P = 40, 24
+    cos, sin = precompute_rope_frequencies(D, 64, 5e5)
+    cos, sin = cos.to(DEV), sin.to(DEV)
+    x = torch.randn(2, T, dim, device=DEV, dtype=torch.bfloat16)
+    with torch.no_grad():
+        full = attn(x, cos[:T], sin[:T])
+        cache = KVCache(2, T, Hkv, D, torch.bfloat16, DEV)
+        outs = [attn(x[:, :P], cos[:P], sin[:P], kv_cache=cache)]
+        for t in range(P, T):
+            outs.append(attn(x[:, t:t + 1], cos[t:t + 1], sin[t:t + 1], kv_cache=cache))
+    inc = torch.cat(outs, dim=1)
+    assert cache.seq_len == T and cache.lens.tolist() == [T, T]
+    assert (inc.float() - full.float()).abs().max().item() <= 3e-2
+    with pytest.raises(ValueError):
+        attn(x[:, :1], cos[:1], sin[:1], kv_cache=cache)
+
+
+def test_doc_ids_branch_kept():
+    # explicit-mask branch (reference :190-227); one document equals causal
+    # (reference tests/unit/test_packing.py:269-277)
+    torch.manual_seed(0)
+    attn = Attention(128, 4, 2).to(DEV)
+    cos, sin = precompute_rope_frequencies(32, 32)
+    cos, sin = cos.to(DEV), sin.to(DEV)
+    x = torch.randn(2, 32, 128, device=DEV)
+    a = attn(x, cos, sin)
+    b = attn(x, cos, sin, doc_ids=torch.zeros(2, 32, dtype=torch.long, device=DEV))
+    assert torch.allclose(a, b, atol=1e-4)
+    del F
