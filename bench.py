@@ -1,0 +1,199 @@
+"""Benchmark of the gfx950 attention path on one GPU; prints one JSON line.
+
+Step = one training-step attention pass of the Llama-3-8B shape (BASELINE
+config C3): causal GQA forward (RoPE fused) + backward, bf16, B=4, S=4096,
+32 query heads, 8 KV heads, head_dim 128, RoPE theta 5e5, seeded N(0,1)
+synthetic inputs resident in HBM.  Algorithmic work per step is 14*D*P flops
+with P = B*Hq*S*(S+1)/2 causal (query, key) pairs (forward 4*D*P, backward
+10*D*P; GQA not discounted).
+
+Also reported: per-kernel HIP-event timings (the library brackets each launch
+on its own stream), the roofline of the dominant kernel, the KV-cache decode
+configuration C4 in GB/s, and the reference's PyTorch path timed on the host
+CPU on a bounded sample of the same workload.
+
+    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "causal GQA attn TFLOP/s fwd+bwd (8B shape) + decode HBM GB/s, 1 MI355X"
+PEAK_BF16_TFLOPS = 2516.6  # 256 CU x 2.4 GHz x 4096 flop/clk, dense
+PEAK_HBM_GBPS = 8000.0
+
+C3 = dict(B=4, S=4096, Hq=32, Hkv=8, D=128, theta=500000.0)
+C4 = dict(B=32, Hq=32, Hkv=8, D=128, lo=1024, hi=8192, theta=500000.0)
+
+
+def pairs(B, Hq, S):
+    return B * Hq * S * (S + 1) // 2
+
+
+def seeded(shape, seed, dtype, dev):
+    import torch
+
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(*shape, generator=g).to(dtype).to(dev)
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the attention path "
+              "shards over (batch x KV-head group) with no exchange, so each GPU runs this "
+              "same single-GPU workload.", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from kempnerforge_amd import _lib, ops
+    from kempnerforge_amd.position import precompute_rope_frequencies
+
+    dev = torch.device("cuda:0")
+    bf16 = torch.bfloat16
+    B, S, Hq, Hkv, D = (C3[k] for k in ("B", "S", "Hq", "Hkv", "D"))
+    q = seeded((B, S, Hq, D), 0, bf16, dev).requires_grad_(True)
+    k = seeded((B, S, Hkv, D), 1, bf16, dev).requires_grad_(True)
+    v = seeded((B, S, Hkv, D), 2, bf16, dev).requires_grad_(True)
+    do = seeded((B, S, Hq, D), 3, bf16, dev)
+    cos, sin = precompute_rope_frequencies(D, S, C3["theta"])
+    cos, sin = cos.to(dev), sin.to(dev)
+    P = pairs(B, Hq, S)
+    flops_step = 14.0 * D * P
+
+    def step():
+        out = ops.attention(q, k, v, cos, sin, causal=True)
+        torch.autograd.grad(out, (q, k, v), do)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    secs = time.perf_counter() - t0
+    ms_step = secs / args.steps * 1e3
+    value = flops_step / (ms_step * 1e-3) / 1e12
+
+    # per-kernel timing over the same number of steps (separate pass: the event
+    # records would otherwise sit inside the timed region)
+    with _lib.KernelTimer() as kt:
+        for _ in range(args.steps):
+            step()
+        torch.cuda.synchronize()
+    kstats = {n: {"avg_us": t / c * 1e3, "launches": c} for n, (t, c) in kt.stats.items()}
+    # algorithmic flops per launch of each MFMA kernel (the backward's 10*D*P is
+    # 4*D*P of recomputed S and dP plus dV, dK -> dkdv kernel 8*D*P; dQ 2*D*P)
+    algo = {"fwd_mfma": 4.0 * D * P, "bwd_dkdv": 8.0 * D * P, "bwd_dq": 2.0 * D * P}
+    dom = max(kstats, key=lambda n: kstats[n]["avg_us"] * kstats[n]["launches"])
+    roof = None
+    if dom in algo:
+        ach = algo[dom] / (kstats[dom]["avg_us"] * 1e-6) / 1e12
+        roof = {"kernel": dom, "bound": "mfma", "achieved": round(ach, 1),
+                "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(ach / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                "avg_us": round(kstats[dom]["avg_us"], 1)}
+    fwd_us = kstats.get("fwd_mfma", {}).get("avg_us")
+
+    # decode (C4)
+    g = torch.Generator().manual_seed(4)
+    Bd, Hqd, Hkvd, Dd = C4["B"], C4["Hq"], C4["Hkv"], C4["D"]
+    lens = torch.randint(C4["lo"], C4["hi"] + 1, (Bd,), generator=g, dtype=torch.int32)
+    Smax = C4["hi"] + 1
+    qn = seeded((Bd, 1, Hqd, Dd), 0, bf16, dev)
+    kn = seeded((Bd, 1, Hkvd, Dd), 1, bf16, dev)
+    vn = seeded((Bd, 1, Hkvd, Dd), 2, bf16, dev)
+    kc = torch.randn(Bd, Hkvd, Smax, Dd, device=dev, dtype=bf16)
+    vc = torch.randn(Bd, Hkvd, Smax, Dd, device=dev, dtype=bf16)
+    dcos, dsin = precompute_rope_frequencies(Dd, Smax, C4["theta"])
+    dcos, dsin = dcos.to(dev), dsin.to(dev)
+    lens_d = lens.to(dev)
+    dec_bytes = sum(4 * (int(L) + 1) * Hkvd * Dd for L in lens) + 4 * Bd * Hqd * Dd \
+        + 4 * Bd * Hkvd * Dd
+
+    def dstep():
+        ops.decode_raw(qn, kn, vn, kc, vc, lens_d, dcos, dsin, rope_row_offset=0, max_len=Smax)
+
+    for _ in range(args.warmup):
+        dstep()
+    torch.cuda.synchronize()
+    n_dec = max(args.steps, 50)
+    t0 = time.perf_counter()
+    for _ in range(n_dec):
+        dstep()
+    torch.cuda.synchronize()
+    dec_us = (time.perf_counter() - t0) / n_dec * 1e6
+    with _lib.KernelTimer() as kt2:
+        for _ in range(n_dec):
+            dstep()
+        torch.cuda.synchronize()
+    dstats = {n: {"avg_us": t / c * 1e3, "launches": c} for n, (t, c) in kt2.stats.items()}
+    split_us = dstats.get("decode_split", {}).get("avg_us")
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        from oracle import cpu_baseline
+
+        sample = dict(B=1, S=C3["S"], Hq=8, Hkv=2, D=D)
+        secs_cpu, reps, used = cpu_baseline.time_fwd_bwd(
+            sample["B"], sample["S"], sample["Hq"], sample["Hkv"], sample["D"], C3["theta"],
+            bf16, min_seconds=args.cpu_seconds)
+        fl = 14.0 * D * pairs(sample["B"], sample["Hq"], sample["S"])
+        cpu = {"value": round(fl / secs_cpu / 1e12, 4), "unit": "TFLOP/s",
+               "cores": torch.get_num_threads(), "kind": "port",
+               "sample": (f"reference PyTorch path (apply_rope -> repeat_interleave -> SDPA "
+                          f"is_causal, autograd) fwd+bwd on CPU, {str(used).replace('torch.', '')},"
+                          f" B=1 S={sample['S']} Hq=8 Hkv=2 D={D} (1/16 of C3), median of {reps}")}
+
+    line = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) q/k/v/dO, resident in HBM)",
+        "config": {"workload": "llama3-8b causal GQA attention fwd+bwd (C3)", "batch": B,
+                   "seq_len": S, "n_heads": Hq, "n_kv_heads": Hkv, "head_dim": D,
+                   "rope_theta": C3["theta"], "parallelism": "single GPU"},
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "frac_of_peak_step": round(value / PEAK_BF16_TFLOPS, 4),
+        "kernels_us": {n: round(s["avg_us"], 1) for n, s in kstats.items()},
+        "fwd_tflops": round(4.0 * D * P / (fwd_us * 1e-6) / 1e12, 1) if fwd_us else None,
+        "decode": {"config": "C4 B=32 Hq=32 Hkv=8 D=128 L~U[1024,8192] seed 4",
+                   "bytes": dec_bytes, "us_per_step": round(dec_us, 1),
+                   "GB/s": round(dec_bytes / (dec_us * 1e-6) / 1e9, 1),
+                   "frac_of_hbm_peak": round(dec_bytes / (dec_us * 1e-6) / 1e9 / PEAK_HBM_GBPS, 4),
+                   "kernels_us": {n: round(s["avg_us"], 1) for n, s in dstats.items()},
+                   "split_kernel_GB/s": round(dec_bytes / (split_us * 1e-6) / 1e9, 1)
+                   if split_us else None},
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

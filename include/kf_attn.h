@@ -151,6 +151,19 @@ int kf_attn_capture(const void* q, const void* k, const void* v, const float* ro
                     int64_t ksb, int64_t kss, int64_t ksh, int64_t vsb, int64_t vss,
                     int64_t vsh, int k_rotated, int causal, int dtype, void* stream);
 
+/* ---- Measurement hooks.  No counterpart in the reference: they exist so a
+ * benchmark can time each kernel of the library on the stream it runs on. */
+
+/* on != 0: bracket every kernel launch of the library with two HIP events
+ * recorded on the launch stream (adds two event records per launch). */
+int kf_prof_enable(int on);
+
+/* Wait for the recorded events, aggregate by kernel name and clear the record.
+ * Writes up to cap entries: names[64*i] (NUL-terminated), total_ms[i],
+ * counts[i] (any of the arrays may be NULL).  Returns the number of distinct
+ * kernel names recorded. */
+int kf_prof_collect(char* names, float* total_ms, int* counts, int cap);
+
 #ifdef __cplusplus
 }
 #endif

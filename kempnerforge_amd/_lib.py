@@ -35,6 +35,9 @@ SIGNATURES = {
     "kf_attn_capture_workspace_size": ([_c_int] * 7 + [_szp], _c_int),
     "kf_attn_capture": ([_vp, _vp, _vp, _fp, _fp, _fp, _vp, _fp, _vp, _c_sz] + [_c_int] * 6
                         + [_c_i64] * 6 + [_c_int] * 3 + [_vp], _c_int),
+    "kf_prof_enable": ([_c_int], _c_int),
+    "kf_prof_collect": ([ctypes.c_char_p, ctypes.POINTER(ctypes.c_float),
+                         ctypes.POINTER(ctypes.c_int), _c_int], _c_int),
 }
 
 _lock = threading.Lock()
@@ -75,3 +78,32 @@ def check(rc: int, what: str) -> None:
 
 def size_out() -> ctypes.c_size_t:
     return ctypes.c_size_t(0)
+
+
+class KernelTimer:
+    """Per-kernel HIP-event timing of the library's launches.
+
+    ``with KernelTimer() as t: ...`` enables the library's event bracketing;
+    on exit ``t.stats`` maps kernel name -> (total_ms, launches).
+    """
+
+    CAP = 64
+
+    def __enter__(self):
+        lib = load()
+        lib.kf_prof_collect(None, None, None, 0)  # drop anything recorded before
+        lib.kf_prof_enable(1)
+        self.stats = {}
+        return self
+
+    def __exit__(self, *exc):
+        lib = load()
+        lib.kf_prof_enable(0)
+        names = ctypes.create_string_buffer(64 * self.CAP)
+        tot = (ctypes.c_float * self.CAP)()
+        cnt = (ctypes.c_int * self.CAP)()
+        n = lib.kf_prof_collect(names, tot, cnt, self.CAP)
+        for i in range(min(n, self.CAP)):
+            name = names.raw[64 * i: 64 * (i + 1)].split(b"\0", 1)[0].decode()
+            self.stats[name] = (float(tot[i]), int(cnt[i]))
+        return False

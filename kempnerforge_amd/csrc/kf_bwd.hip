@@ -1,14 +1,544 @@
 // bf16 MFMA backward attention for gfx950 (head_dim 64 or 128).
+//
+// Four launches, no atomics (bit-deterministic):
+//  kv_prep_bwd  per KV head: K rotated (eager bf16 RoPE) [bh][P][D], its
+//               transpose with the 16-key quad swizzle [bh][D][P], V [bh][P][D].
+//  q_prep_bwd   per query head: Q rotated [bhq][P][D] and swizzled transpose
+//               [bhq][D][P]; dO [bhq][P][D] and swizzled transpose; lse*log2(e)
+//               and Delta = rowsum(dO o O) [bhq][P].  P = S rounded up to 128;
+//               padded rows are zero with lse = +inf, so they contribute nothing.
+//  dkdv         workgroup = 128 keys of one KV head (4 wavefronts x 32 keys,
+//               K and V held in registers as MFMA B operands), looping over every
+//               query head of the group and every query tile of 64: the
+//               repeat_interleave backward (sum over the group) happens in the
+//               accumulators.  S = Q K^T and dP = dO V^T land in the 32x32 C
+//               layout with one key per lane; P and dS then feed dV^T += dO^T P
+//               and dK^T += Q^T dS as B operands directly.  RoPE backward and the
+//               softmax scale are applied at the dK store.
+//  dq           forward-shaped: 128 (head, position) rows per workgroup sharing
+//               each K/V tile; S^T = K Q^T, dP^T = V dO^T, dQ^T += K^T dS^T.
+//               RoPE backward is applied at the dQ store.
+// The algorithm is the standard flash-attention backward (recompute P from the
+// saved log-sum-exp; dS = P o (dP - Delta)).
 #include "kf_common.h"
 #include "kf_internal.h"
+#include "kf_mfma.h"
 
 namespace kf {
 
-bool bwd_mfma_supported(const BwdArgs&) { return false; }
-size_t bwd_mfma_workspace(int, int, int, int, int) { return 0; }
-int bwd_mfma(const BwdArgs&, void*) {
-  set_error("MFMA backward not available");
-  return KF_ERR_UNSUPPORTED;
+namespace {
+
+using namespace mfma;
+
+constexpr int BKV = 128;  // keys per dK/dV workgroup
+constexpr int BQ = 64;    // queries per dK/dV tile
+
+__host__ __device__ constexpr int pad_len(int S) { return (S + BKV - 1) / BKV * BKV; }
+
+template <int D>
+__global__ __launch_bounds__(256) void kv_prep_bwd_kernel(
+    const bf16* __restrict__ k, const bf16* __restrict__ v, const float* __restrict__ cos,
+    const float* __restrict__ sin, bf16* __restrict__ krot, bf16* __restrict__ kt,
+    bf16* __restrict__ vn, int S, int P, int Hkv) {
+  constexpr int HALF = D / 2, CP = HALF / 8, LD = D + 8;
+  __shared__ __attribute__((aligned(16))) bf16 sk[BN * LD];
+  const int s0 = blockIdx.x * BN, bh = blockIdx.y, b = bh / Hkv, g = bh % Hkv;
+  const int tid = threadIdx.x;
+  for (int it = tid; it < BN * CP; it += 256) {
+    const int row = it / CP, c = it % CP, s = s0 + row;
+    u32x4 o1 = {0u, 0u, 0u, 0u}, o2 = {0u, 0u, 0u, 0u};
+    if (s < S) {
+      const bf16* src = k + (((int64_t)b * S + s) * Hkv + g) * D;
+      float x1[8], x2[8], r1[8], r2[8];
+      unpack8(*(const u32x4*)(src + 8 * c), x1);
+      unpack8(*(const u32x4*)(src + 8 * c + HALF), x2);
+      const float* cr = cos + (int64_t)s * HALF + 8 * c;
+      const float* sr = sin + (int64_t)s * HALF + 8 * c;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) rope_pair<bf16>(x1[j], x2[j], cr[j], sr[j], r1[j], r2[j]);
+      o1 = pack8(r1);
+      o2 = pack8(r2);
+    }
+    bf16* dst = krot + ((int64_t)bh * P + s) * D;
+    *(u32x4*)(dst + 8 * c) = o1;
+    *(u32x4*)(dst + 8 * c + HALF) = o2;
+    *(u32x4*)(&sk[row * LD + 8 * c]) = o1;
+    *(u32x4*)(&sk[row * LD + 8 * c + HALF]) = o2;
+  }
+  for (int it = tid; it < BN * (D / 8); it += 256) {
+    const int row = it / (D / 8), c = it % (D / 8), s = s0 + row;
+    u32x4 a = {0u, 0u, 0u, 0u};
+    if (s < S) a = *(const u32x4*)(v + (((int64_t)b * S + s) * Hkv + g) * D + 8 * c);
+    *(u32x4*)(vn + ((int64_t)bh * P + s) * D + 8 * c) = a;
+  }
+  __syncthreads();
+  for (int it = tid; it < D * (BN / 8); it += 256) {
+    const int d = it / (BN / 8), pc = it % (BN / 8);
+    float f[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) f[j] = (float)sk[vt_logical_key(8 * pc + j) * LD + d];
+    *(u32x4*)(kt + ((int64_t)bh * D + d) * P + s0 + 8 * pc) = pack8(f);
+  }
+}
+
+template <int D>
+__global__ __launch_bounds__(256) void q_prep_bwd_kernel(
+    const bf16* __restrict__ q, const bf16* __restrict__ out, const bf16* __restrict__ dout,
+    const float* __restrict__ lse, const float* __restrict__ cos, const float* __restrict__ sin,
+    bf16* __restrict__ qrot, bf16* __restrict__ qt, bf16* __restrict__ don,
+    bf16* __restrict__ dot, float* __restrict__ lse2, float* __restrict__ delta, int S, int P,
+    int Hq) {
+  constexpr int HALF = D / 2, CP = HALF / 8, LD = D + 8, TPR = D / 8;
+  __shared__ __attribute__((aligned(16))) bf16 sq[BN * LD];
+  __shared__ __attribute__((aligned(16))) bf16 sd[BN * LD];
+  const int s0 = blockIdx.x * BN, bhq = blockIdx.y, b = bhq / Hq, h = bhq % Hq;
+  const int tid = threadIdx.x;
+  for (int it = tid; it < BN * CP; it += 256) {
+    const int row = it / CP, c = it % CP, s = s0 + row;
+    u32x4 o1 = {0u, 0u, 0u, 0u}, o2 = {0u, 0u, 0u, 0u};
+    if (s < S) {
+      const bf16* src = q + (((int64_t)b * S + s) * Hq + h) * D;
+      float x1[8], x2[8], r1[8], r2[8];
+      unpack8(*(const u32x4*)(src + 8 * c), x1);
+      unpack8(*(const u32x4*)(src + 8 * c + HALF), x2);
+      const float* cr = cos + (int64_t)s * HALF + 8 * c;
+      const float* sr = sin + (int64_t)s * HALF + 8 * c;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) rope_pair<bf16>(x1[j], x2[j], cr[j], sr[j], r1[j], r2[j]);
+      o1 = pack8(r1);
+      o2 = pack8(r2);
+    }
+    bf16* dst = qrot + ((int64_t)bhq * P + s) * D;
+    *(u32x4*)(dst + 8 * c) = o1;
+    *(u32x4*)(dst + 8 * c + HALF) = o2;
+    *(u32x4*)(&sq[row * LD + 8 * c]) = o1;
+    *(u32x4*)(&sq[row * LD + 8 * c + HALF]) = o2;
+  }
+  // dO copy + Delta (TPR consecutive lanes own one row)
+  for (int it = tid; it < BN * TPR; it += 256) {
+    const int row = it / TPR, c = it % TPR, s = s0 + row;
+    u32x4 a = {0u, 0u, 0u, 0u};
+    float part = 0.f;
+    if (s < S) {
+      const int64_t off = (((int64_t)b * S + s) * Hq + h) * D + 8 * c;
+      a = *(const u32x4*)(dout + off);
+      float fd[8], fo[8];
+      unpack8(a, fd);
+      unpack8(*(const u32x4*)(out + off), fo);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) part += fd[j] * fo[j];
+    }
+#pragma unroll
+    for (int o = 1; o < TPR; o <<= 1) part += __shfl_xor(part, o, 64);
+    *(u32x4*)(don + ((int64_t)bhq * P + s) * D + 8 * c) = a;
+    *(u32x4*)(&sd[row * LD + 8 * c]) = a;
+    if (c == 0) {
+      delta[(int64_t)bhq * P + s] = part;
+      lse2[(int64_t)bhq * P + s] = s < S ? lse[(int64_t)bhq * S + s] * kLog2e : INFINITY;
+    }
+  }
+  __syncthreads();
+  for (int it = tid; it < D * (BN / 8); it += 256) {
+    const int d = it / (BN / 8), pc = it % (BN / 8);
+    float fq[8], fd[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int r = vt_logical_key(8 * pc + j);
+      fq[j] = (float)sq[r * LD + d];
+      fd[j] = (float)sd[r * LD + d];
+    }
+    *(u32x4*)(qt + ((int64_t)bhq * D + d) * P + s0 + 8 * pc) = pack8(fq);
+    *(u32x4*)(dot + ((int64_t)bhq * D + d) * P + s0 + 8 * pc) = pack8(fd);
+  }
+}
+
+template <int D>
+__global__ __launch_bounds__(256, 1) void bwd_dkdv_kernel(
+    const bf16* __restrict__ krot, const bf16* __restrict__ vn, const bf16* __restrict__ qrot,
+    const bf16* __restrict__ qt, const bf16* __restrict__ don, const bf16* __restrict__ dot,
+    const float* __restrict__ lse2, const float* __restrict__ delta,
+    const float* __restrict__ cos, const float* __restrict__ sin, bf16* __restrict__ dk,
+    bf16* __restrict__ dv, int S, int P, int Hq, int Hkv, int n_rep, int nkb, float scale_log2,
+    float scale, int causal) {
+  constexpr int KS = D / 16, DT = D / 32, HALF = D / 2;
+  constexpr int KLD = D + 8, QLD = BQ + 8;
+  constexpr int RCH = BQ * D / 8 / 256;  // 16-byte chunks per thread per staged tile
+  __shared__ __attribute__((aligned(16))) bf16 sQ[BQ * KLD];
+  __shared__ __attribute__((aligned(16))) bf16 sDO[BQ * KLD];
+  __shared__ __attribute__((aligned(16))) bf16 sQT[D * QLD];
+  __shared__ __attribute__((aligned(16))) bf16 sDOT[D * QLD];
+  __shared__ float sL[BQ], sDl[BQ];
+
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, hh = lane >> 5, c32 = lane & 31;
+  const int logical = xcd_logical_id(blockIdx.x, gridDim.x);
+  const int bh = logical / nkb;
+  const int kb = logical % nkb;  // ascending: the longest causal key tiles first
+  const int b = bh / Hkv, g = bh % Hkv;
+  const int k0 = kb * BKV;
+  const int key = k0 + 32 * w + c32;
+
+  bf16x8 kf[KS], vf[KS];
+  {
+    const bf16* kr = krot + ((int64_t)bh * P + key) * D + 8 * hh;
+    const bf16* vr = vn + ((int64_t)bh * P + key) * D + 8 * hh;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      kf[ks] = as_bf16x8(*(const u32x4*)(kr + 16 * ks));
+      vf[ks] = as_bf16x8(*(const u32x4*)(vr + 16 * ks));
+    }
+  }
+  f32x16 adk[DT], adv[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      adk[dt][i] = 0.f;
+      adv[dt][i] = 0.f;
+    }
+
+  const int nqt = (S + BQ - 1) / BQ;
+  const int qt0 = causal ? k0 / BQ : 0;
+  const int per_head = nqt - qt0;
+  const int total = per_head > 0 ? per_head * n_rep : 0;
+
+  u32x4 rq[RCH], rd[RCH], rqt[RCH], rdt[RCH];
+  float rl = 0.f;
+  auto gload = [&](int it) {
+    const int hl = it / per_head, qtile = qt0 + it % per_head;
+    const int64_t bhq = (int64_t)b * Hq + g * n_rep + hl;
+    const int q0 = qtile * BQ;
+#pragma unroll
+    for (int i = 0; i < RCH; ++i) {
+      const int id = tid + 256 * i;
+      const int row = id / (D / 8), col = id % (D / 8);
+      rq[i] = *(const u32x4*)(qrot + (bhq * P + q0 + row) * D + 8 * col);
+      rd[i] = *(const u32x4*)(don + (bhq * P + q0 + row) * D + 8 * col);
+      const int trow = id / (BQ / 8), tcol = id % (BQ / 8);
+      rqt[i] = *(const u32x4*)(qt + (bhq * D + trow) * P + q0 + 8 * tcol);
+      rdt[i] = *(const u32x4*)(dot + (bhq * D + trow) * P + q0 + 8 * tcol);
+    }
+    if (tid < BQ) rl = lse2[bhq * P + q0 + tid];
+    else if (tid < 2 * BQ) rl = delta[bhq * P + q0 + tid - BQ];
+  };
+  auto lstore = [&]() {
+#pragma unroll
+    for (int i = 0; i < RCH; ++i) {
+      const int id = tid + 256 * i;
+      const int row = id / (D / 8), col = id % (D / 8);
+      *(u32x4*)(&sQ[row * KLD + 8 * col]) = rq[i];
+      *(u32x4*)(&sDO[row * KLD + 8 * col]) = rd[i];
+      const int trow = id / (BQ / 8), tcol = id % (BQ / 8);
+      *(u32x4*)(&sQT[trow * QLD + 8 * tcol]) = rqt[i];
+      *(u32x4*)(&sDOT[trow * QLD + 8 * tcol]) = rdt[i];
+    }
+    if (tid < BQ) sL[tid] = rl;
+    else if (tid < 2 * BQ) sDl[tid - BQ] = rl;
+  };
+
+  if (total > 0) gload(0);
+  for (int it = 0; it < total; ++it) {
+    const int q0 = (qt0 + it % per_head) * BQ;
+    __syncthreads();
+    lstore();
+    __syncthreads();
+    if (it + 1 < total) gload(it + 1);
+
+    f32x16 s[2], dp[2];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        s[mt][i] = 0.f;
+        dp[mt][i] = 0.f;
+      }
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const bf16x8 aq = *(const bf16x8*)(&sQ[(32 * mt + c32) * KLD + 16 * ks + 8 * hh]);
+        s[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(aq, kf[ks], s[mt], 0, 0, 0);
+        const bf16x8 ad = *(const bf16x8*)(&sDO[(32 * mt + c32) * KLD + 16 * ks + 8 * hh]);
+        dp[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ad, vf[ks], dp[mt], 0, 0, 0);
+      }
+    }
+    const bool need_mask = causal && q0 < k0 + BKV;
+    u32x4 pk[4], dsk[4];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int i = 0; i < 16; i += 2) {
+        float pv[2], dsv[2];
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          const int r = 32 * mt + 8 * ((i + e) >> 2) + 4 * hh + ((i + e) & 3);
+          float p = fast_exp2(s[mt][i + e] * scale_log2 - sL[r]);
+          if (need_mask && key > q0 + r) p = 0.f;
+          pv[e] = p;
+          dsv[e] = p * (dp[mt][i + e] - sDl[r]);
+        }
+        pk[2 * mt + (i >> 3)][(i & 7) >> 1] = pack2(pv[0], pv[1]);
+        dsk[2 * mt + (i >> 3)][(i & 7) >> 1] = pack2(dsv[0], dsv[1]);
+      }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const bf16x8 pb = as_bf16x8(pk[c]);
+      const bf16x8 db = as_bf16x8(dsk[c]);
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        const bf16x8 a1 = *(const bf16x8*)(&sDOT[(32 * dt + c32) * QLD + 16 * c + 8 * hh]);
+        adv[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, pb, adv[dt], 0, 0, 0);
+        const bf16x8 a2 = *(const bf16x8*)(&sQT[(32 * dt + c32) * QLD + 16 * c + 8 * hh]);
+        adk[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a2, db, adk[dt], 0, 0, 0);
+      }
+    }
+  }
+
+  if (key < S) {
+    bf16* dkr = dk + (((int64_t)b * S + key) * Hkv + g) * D;
+    bf16* dvr = dv + (((int64_t)b * S + key) * Hkv + g) * D;
+    const float* cr = cos + (int64_t)key * HALF;
+    const float* sr = sin + (int64_t)key * HALF;
+#pragma unroll
+    for (int dt = 0; dt < DT / 2; ++dt)
+#pragma unroll
+      for (int gi = 0; gi < 4; ++gi) {
+        const int d = 32 * dt + 8 * gi + 4 * hh;
+        float lo[4], hi[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          rope_pair_bwd<bf16>(adk[dt][4 * gi + e] * scale, adk[dt + DT / 2][4 * gi + e] * scale,
+                              cr[d + e], sr[d + e], lo[e], hi[e]);
+        *(u32x2*)(dkr + d) = u32x2{pack2(lo[0], lo[1]), pack2(lo[2], lo[3])};
+        *(u32x2*)(dkr + d + HALF) = u32x2{pack2(hi[0], hi[1]), pack2(hi[2], hi[3])};
+      }
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int gi = 0; gi < 4; ++gi) {
+        const int d = 32 * dt + 8 * gi + 4 * hh;
+        *(u32x2*)(dvr + d) = u32x2{pack2(adv[dt][4 * gi], adv[dt][4 * gi + 1]),
+                                   pack2(adv[dt][4 * gi + 2], adv[dt][4 * gi + 3])};
+      }
+  }
+}
+
+template <int D>
+__global__ __launch_bounds__(256, D == 128 ? 1 : 2) void bwd_dq_kernel(
+    const bf16* __restrict__ qrot, const bf16* __restrict__ don, const float* __restrict__ lse2,
+    const float* __restrict__ delta, const bf16* __restrict__ krot, const bf16* __restrict__ vn,
+    const bf16* __restrict__ kt, const float* __restrict__ cos, const float* __restrict__ sin,
+    bf16* __restrict__ dq, int S, int P, int Hq, int Hkv, int n_rep, int bm_pos, int nqb,
+    float scale_log2, float scale, int causal) {
+  constexpr int KS = D / 16, DT = D / 32, HALF = D / 2;
+  constexpr int KLD = D + 8, VLD = BN + 8;
+  constexpr int KCH = BN * D / 8 / 256;
+  __shared__ __attribute__((aligned(16))) bf16 sK[BN * KLD];
+  __shared__ __attribute__((aligned(16))) bf16 sV[BN * KLD];
+  __shared__ __attribute__((aligned(16))) bf16 sKT[D * VLD];
+
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, hh = lane >> 5, c32 = lane & 31;
+  const int logical = xcd_logical_id(blockIdx.x, gridDim.x);
+  const RowInfo ri = row_info(logical, nqb, Hkv, n_rep, bm_pos, S, w * 32 + c32);
+  const int bh = ri.b * Hkv + ri.g;
+  const int64_t bhq = (int64_t)ri.b * Hq + ri.hq;
+
+  bf16x8 qf[KS], df[KS];
+  float l2 = INFINITY, dl = 0.f;
+  if (ri.q_valid) {
+    const bf16* qr = qrot + (bhq * P + ri.pos) * D + 8 * hh;
+    const bf16* dr = don + (bhq * P + ri.pos) * D + 8 * hh;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      qf[ks] = as_bf16x8(*(const u32x4*)(qr + 16 * ks));
+      df[ks] = as_bf16x8(*(const u32x4*)(dr + 16 * ks));
+    }
+    l2 = lse2[bhq * P + ri.pos];
+    dl = delta[bhq * P + ri.pos];
+  } else {
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      qf[ks] = as_bf16x8(u32x4{0u, 0u, 0u, 0u});
+      df[ks] = qf[ks];
+    }
+  }
+
+  const int kend = causal ? min(S, ri.p0 + bm_pos) : S;
+  const int ntiles = (kend + BN - 1) / BN;
+  const bf16* kbase = krot + (int64_t)bh * P * D;
+  const bf16* vbase = vn + (int64_t)bh * P * D;
+  const bf16* tbase = kt + (int64_t)bh * D * P;
+
+  u32x4 rk[KCH], rv[KCH], rt[KCH];
+  auto gload = [&](int t) {
+#pragma unroll
+    for (int i = 0; i < KCH; ++i) {
+      const int id = tid + 256 * i, row = id / (D / 8), col = id % (D / 8);
+      rk[i] = *(const u32x4*)(kbase + (int64_t)(t * BN + row) * D + 8 * col);
+      rv[i] = *(const u32x4*)(vbase + (int64_t)(t * BN + row) * D + 8 * col);
+      const int trow = id / (BN / 8), tcol = id % (BN / 8);
+      rt[i] = *(const u32x4*)(tbase + (int64_t)trow * P + t * BN + 8 * tcol);
+    }
+  };
+  auto lstore = [&]() {
+#pragma unroll
+    for (int i = 0; i < KCH; ++i) {
+      const int id = tid + 256 * i, row = id / (D / 8), col = id % (D / 8);
+      *(u32x4*)(&sK[row * KLD + 8 * col]) = rk[i];
+      *(u32x4*)(&sV[row * KLD + 8 * col]) = rv[i];
+      const int trow = id / (BN / 8), tcol = id % (BN / 8);
+      *(u32x4*)(&sKT[trow * VLD + 8 * tcol]) = rt[i];
+    }
+  };
+
+  f32x16 acc[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[dt][i] = 0.f;
+
+  if (ntiles > 0) gload(0);
+  for (int t = 0; t < ntiles; ++t) {
+    __syncthreads();
+    lstore();
+    __syncthreads();
+    if (t + 1 < ntiles) gload(t + 1);
+
+    f32x16 s[2], dp[2];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        s[mt][i] = 0.f;
+        dp[mt][i] = 0.f;
+      }
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const bf16x8 ak = *(const bf16x8*)(&sK[(32 * mt + c32) * KLD + 16 * ks + 8 * hh]);
+        s[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ak, qf[ks], s[mt], 0, 0, 0);
+        const bf16x8 av = *(const bf16x8*)(&sV[(32 * mt + c32) * KLD + 16 * ks + 8 * hh]);
+        dp[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, df[ks], dp[mt], 0, 0, 0);
+      }
+    }
+    const int k0 = t * BN;
+    const bool need_mask = (causal && k0 + BN - 1 > ri.p0) || (k0 + BN > S);
+    u32x4 dsk[4];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int i = 0; i < 16; i += 2) {
+        float dsv[2];
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          float p = fast_exp2(s[mt][i + e] * scale_log2 - l2);
+          if (need_mask) {
+            const int key = k0 + 32 * mt + 8 * ((i + e) >> 2) + 4 * hh + ((i + e) & 3);
+            if ((causal && key > ri.pos) || key >= S) p = 0.f;
+          }
+          dsv[e] = p * (dp[mt][i + e] - dl);
+        }
+        dsk[2 * mt + (i >> 3)][(i & 7) >> 1] = pack2(dsv[0], dsv[1]);
+      }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const bf16x8 db = as_bf16x8(dsk[c]);
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        const bf16x8 a = *(const bf16x8*)(&sKT[(32 * dt + c32) * VLD + 16 * c + 8 * hh]);
+        acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, db, acc[dt], 0, 0, 0);
+      }
+    }
+  }
+
+  if (ri.q_valid) {
+    bf16* dqr = dq + (((int64_t)ri.b * S + ri.pos) * Hq + ri.hq) * D;
+    const float* cr = cos + (int64_t)ri.pos * HALF;
+    const float* sr = sin + (int64_t)ri.pos * HALF;
+#pragma unroll
+    for (int dt = 0; dt < DT / 2; ++dt)
+#pragma unroll
+      for (int gi = 0; gi < 4; ++gi) {
+        const int d = 32 * dt + 8 * gi + 4 * hh;
+        float lo[4], hi[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          rope_pair_bwd<bf16>(acc[dt][4 * gi + e] * scale, acc[dt + DT / 2][4 * gi + e] * scale,
+                              cr[d + e], sr[d + e], lo[e], hi[e]);
+        *(u32x2*)(dqr + d) = u32x2{pack2(lo[0], lo[1]), pack2(lo[2], lo[3])};
+        *(u32x2*)(dqr + d + HALF) = u32x2{pack2(hi[0], hi[1]), pack2(hi[2], hi[3])};
+      }
+  }
+}
+
+struct Ws {
+  bf16 *krot, *kt, *vn, *qrot, *qt, *don, *dot;
+  float *lse2, *delta;
+};
+
+Ws carve(void* base, int B, int S, int Hq, int Hkv, int D) {
+  const size_t P = (size_t)pad_len(S);
+  const size_t kv = (size_t)B * Hkv * P * D, qq = (size_t)B * Hq * P * D;
+  Ws w;
+  bf16* p = (bf16*)base;
+  w.krot = p; p += kv;
+  w.kt = p; p += kv;
+  w.vn = p; p += kv;
+  w.qrot = p; p += qq;
+  w.qt = p; p += qq;
+  w.don = p; p += qq;
+  w.dot = p; p += qq;
+  float* f = (float*)p;
+  w.lse2 = f; f += (size_t)B * Hq * P;
+  w.delta = f;
+  return w;
+}
+
+template <int D>
+int launch_bwd(const BwdArgs& a, void* workspace) {
+  const int P = pad_len(a.S);
+  const Ws w = carve(workspace, a.B, a.S, a.Hq, a.Hkv, D);
+  const int n_rep = a.Hq / a.Hkv;
+  const float scale_log2 = a.scale * kLog2e;
+  KF_LAUNCH("kv_prep_bwd", kv_prep_bwd_kernel<D>, dim3(P / BN, a.B * a.Hkv), dim3(256), 0, a.stream,
+                     (const bf16*)a.k, (const bf16*)a.v, a.cos, a.sin, w.krot, w.kt, w.vn, a.S, P,
+                     a.Hkv);
+  KF_CHECK_LAUNCH();
+  KF_LAUNCH("q_prep_bwd", q_prep_bwd_kernel<D>, dim3(P / BN, a.B * a.Hq), dim3(256), 0, a.stream,
+                     (const bf16*)a.q, (const bf16*)a.out, (const bf16*)a.dout, a.lse, a.cos,
+                     a.sin, w.qrot, w.qt, w.don, w.dot, w.lse2, w.delta, a.S, P, a.Hq);
+  KF_CHECK_LAUNCH();
+  const int nkb = P / BKV;
+  KF_LAUNCH("bwd_dkdv", bwd_dkdv_kernel<D>, dim3(nkb * a.B * a.Hkv), dim3(256), 0, a.stream,
+                     w.krot, w.vn, w.qrot, w.qt, w.don, w.dot, w.lse2, w.delta, a.cos, a.sin,
+                     (bf16*)a.dk, (bf16*)a.dv, a.S, P, a.Hq, a.Hkv, n_rep, nkb, scale_log2, a.scale,
+                     a.causal);
+  KF_CHECK_LAUNCH();
+  const int bm_pos = ROWS / n_rep;
+  const int nqb = (a.S + bm_pos - 1) / bm_pos;
+  KF_LAUNCH("bwd_dq", bwd_dq_kernel<D>, dim3(nqb * a.B * a.Hkv), dim3(256), 0, a.stream, w.qrot,
+                     w.don, w.lse2, w.delta, w.krot, w.vn, w.kt, a.cos, a.sin, (bf16*)a.dq, a.S, P,
+                     a.Hq, a.Hkv, n_rep, bm_pos, nqb, scale_log2, a.scale, a.causal);
+  KF_CHECK_LAUNCH();
+  return KF_OK;
+}
+
+}  // namespace
+
+bool bwd_mfma_supported(const BwdArgs& a) {
+  if (a.dtype != BF16 || (a.D != 64 && a.D != 128)) return false;
+  const int n_rep = a.Hq / a.Hkv;
+  if (n_rep < 1 || n_rep > ROWS) return false;
+  auto al16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
+  return al16(a.q) && al16(a.k) && al16(a.v) && al16(a.out) && al16(a.dout) && al16(a.dq) &&
+         al16(a.dk) && al16(a.dv) && al16(a.cos) && al16(a.sin);
+}
+
+size_t bwd_mfma_workspace(int B, int S, int Hq, int Hkv, int D) {
+  const size_t P = (size_t)pad_len(S);
+  return (3 * (size_t)B * Hkv + 4 * (size_t)B * Hq) * P * D * sizeof(uint16_t) +
+         2 * (size_t)B * Hq * P * sizeof(float);
+}
+
+int bwd_mfma(const BwdArgs& a, void* workspace) {
+  KF_CHECK_ARG((int64_t)pad_len(a.S) / BN * (int64_t)a.B * a.Hq < (1LL << 31), "grid too large");
+  return a.D == 128 ? launch_bwd<128>(a, workspace) : launch_bwd<64>(a, workspace);
 }
 
 }  // namespace kf

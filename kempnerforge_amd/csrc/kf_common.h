@@ -105,7 +105,22 @@ __device__ __forceinline__ u32x4 pack8(const float* f) {
 // ---------------------------------------------------------------- host side
 namespace kf {
 void set_error(const char* fmt, ...);
+namespace prof {
+bool enabled();
+void begin(const char* name, hipStream_t s);
+void end(hipStream_t s);
+}  // namespace prof
 }  // namespace kf
+
+// Launch a kernel; with kf_prof_enable(1) the launch is bracketed by HIP events
+// on `stream` and attributed to `name`.
+#define KF_LAUNCH(name, kernel, grid, block, shmem, stream, ...)          \
+  do {                                                                   \
+    const bool kf_prof_on_ = kf::prof::enabled();                        \
+    if (kf_prof_on_) kf::prof::begin(name, stream);                      \
+    hipLaunchKernelGGL(kernel, grid, block, shmem, stream, __VA_ARGS__); \
+    if (kf_prof_on_) kf::prof::end(stream);                              \
+  } while (0)
 
 #define KF_CHECK_ARG(cond, ...)          \
   do {                                   \

@@ -311,7 +311,7 @@ int launch_append(const T* k_new, const T* v_new, const float* cos, const float*
                   int max_len, int B, int Snew, int Hkv, int Smax, int D, hipStream_t stream) {
   const int64_t n = (int64_t)B * Snew * Hkv * (D / 2);
   if (n == 0) return KF_OK;
-  hipLaunchKernelGGL(append_kernel<T>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream,
+  KF_LAUNCH("kv_append", append_kernel<T>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream,
                      k_new, v_new, cos, sin, kc, vc, lens, start, row_offset, rope_rows, max_len,
                      B, Snew, Hkv, Smax, D);
   KF_CHECK_LAUNCH();
@@ -320,7 +320,7 @@ int launch_append(const T* k_new, const T* v_new, const float* cos, const float*
 
 template <int D, int NREP>
 int launch_split(const DecodeArgs& a, float* opart, float* mpart, float* lpart, int nsplit) {
-  hipLaunchKernelGGL((decode_split_kernel<D, NREP>), dim3(nsplit, a.B * a.Hkv), dim3(256), 0,
+  KF_LAUNCH("decode_split", (decode_split_kernel<D, NREP>), dim3(nsplit, a.B * a.Hkv), dim3(256), 0,
                      a.stream, (const bf16*)a.q_new, a.cos, a.sin, a.rope_row_offset,
                      a.rope_rows, a.max_len, (const bf16*)a.k_cache, (const bf16*)a.v_cache,
                      a.lens, opart, mpart, lpart, a.Hq, a.Hkv, a.Smax, nsplit,
@@ -357,13 +357,13 @@ int decode_typed(const DecodeArgs& a, void* workspace) {
     rc = a.D == 128 ? dispatch_nrep<128>(a, opart, mpart, lpart, nsplit)
                     : dispatch_nrep<64>(a, opart, mpart, lpart, nsplit);
     if (rc) return rc;
-    hipLaunchKernelGGL(decode_merge_kernel<T>, dim3(a.B * a.Hq), dim3(256), 0, a.stream, opart,
+    KF_LAUNCH("decode_merge", decode_merge_kernel<T>, dim3(a.B * a.Hq), dim3(256), 0, a.stream, opart,
                        mpart, lpart, a.lens, (T*)a.out, a.Hq, a.D, nsplit, a.max_len,
                        a.rope_row_offset, a.rope_rows);
     KF_CHECK_LAUNCH();
     return KF_OK;
   }
-  hipLaunchKernelGGL(decode_generic_kernel<T>, dim3((a.B * a.Hq + 3) / 4), dim3(256), 0,
+  KF_LAUNCH("decode_generic", decode_generic_kernel<T>, dim3((a.B * a.Hq + 3) / 4), dim3(256), 0,
                      a.stream, (const T*)a.q_new, a.cos, a.sin, a.rope_row_offset, a.rope_rows,
                      a.max_len, (const T*)a.k_cache, (const T*)a.v_cache, a.lens, (T*)a.out, a.B,
                      a.Hq, a.Hkv, a.Smax, a.D, a.scale);

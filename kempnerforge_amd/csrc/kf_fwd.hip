@@ -22,23 +22,13 @@
 // operands are always built with the same (h, j) -> k map.
 #include "kf_common.h"
 #include "kf_internal.h"
+#include "kf_mfma.h"
 
 namespace kf {
 
 namespace {
 
-constexpr int BN = 64;   // keys per tile
-constexpr int ROWS = 128;
-
-// Physical slot p (0..15) inside a 16-key group of the transposed V holds this
-// logical key: lane half h = p/8, slot j = p%8 of the P^T B-operand carries key
-// (j<4 ? 4h+j : 8+4h+j-4) because of the 32x32 C layout of S^T.
-__device__ __forceinline__ int vt_logical_key(int p) {
-  const int h = (p & 15) >> 3, j = p & 7;
-  return (p & ~15) + (j < 4 ? 4 * h + j : 8 + 4 * h + (j - 4));
-}
-
-__device__ __forceinline__ bf16x8 as_bf16x8(const u32x4& u) { return __builtin_bit_cast(bf16x8, u); }
+using namespace mfma;
 
 template <int D>
 __global__ __launch_bounds__(256) void kv_prep_kernel(
@@ -98,36 +88,6 @@ __global__ __launch_bounds__(256) void kv_prep_kernel(
     for (int j = 0; j < 8; ++j) f[j] = (float)sv[vt_logical_key(8 * pc + j) * VLD + d];
     *(u32x4*)(vt + ((int64_t)bh * D + d) * Skp + s0 + 8 * pc) = pack8(f);
   }
-}
-
-// Block-id remap so that the workgroups one XCD runs are a contiguous range of
-// logical ids (the dispatcher deals ids round-robin over the 8 XCDs): blocks of
-// one KV head then share that XCD's L2.
-__device__ __forceinline__ int xcd_logical_id(int L, int nblk) {
-  const int per = nblk / 8, rem = nblk % 8;
-  const int xcd = L % 8, idx = L / 8;
-  return xcd * per + min(xcd, rem) + idx;
-}
-
-struct RowInfo {
-  int b, g, hq, pos, p0;
-  bool q_valid;
-};
-
-__device__ __forceinline__ RowInfo row_info(int logical, int nqb, int Hkv, int n_rep, int bm_pos,
-                                            int Sq, int r) {
-  RowInfo ri;
-  const int bh = logical / nqb;
-  const int qb = nqb - 1 - (logical % nqb);  // longest causal rows first
-  ri.b = bh / Hkv;
-  ri.g = bh % Hkv;
-  ri.p0 = qb * bm_pos;
-  const bool row_valid = r < n_rep * bm_pos;
-  const int hl = row_valid ? r / bm_pos : 0;
-  ri.pos = ri.p0 + (row_valid ? r % bm_pos : 0);
-  ri.q_valid = row_valid && ri.pos < Sq;
-  ri.hq = ri.g * n_rep + hl;
-  return ri;
 }
 
 // Load this lane's rotated Q fragment: slots ks cover d = 16ks + 8h + 0..7.
@@ -418,11 +378,11 @@ size_t fwd_mfma_workspace(int B, int Sk, int Hkv, int D) {
 static int launch_kv_prep(const FwdArgs& a, bf16* krot, bf16* vt, int Skp) {
   dim3 grid(Skp / BN, a.B * a.Hkv);
   if (a.D == 128)
-    hipLaunchKernelGGL(kv_prep_kernel<128>, grid, dim3(256), 0, a.stream, (const bf16*)a.k,
+    KF_LAUNCH("kv_prep", kv_prep_kernel<128>, grid, dim3(256), 0, a.stream, (const bf16*)a.k,
                        (const bf16*)a.v, a.cos, a.sin, krot, vt, a.Sk, Skp, a.Hkv, a.ksb, a.kss,
                        a.ksh, a.vsb, a.vss, a.vsh, a.k_rotated);
   else
-    hipLaunchKernelGGL(kv_prep_kernel<64>, grid, dim3(256), 0, a.stream, (const bf16*)a.k,
+    KF_LAUNCH("kv_prep", kv_prep_kernel<64>, grid, dim3(256), 0, a.stream, (const bf16*)a.k,
                        (const bf16*)a.v, a.cos, a.sin, krot, vt, a.Sk, Skp, a.Hkv, a.ksb, a.kss,
                        a.ksh, a.vsb, a.vss, a.vsh, a.k_rotated);
   KF_CHECK_LAUNCH();
@@ -442,11 +402,11 @@ int fwd_mfma(const FwdArgs& a, void* workspace) {
   KF_CHECK_ARG(nblk < (1LL << 31), "grid too large");
   const float scale_log2 = a.scale * kLog2e;
   if (a.D == 128)
-    hipLaunchKernelGGL(fwd_mfma_kernel<128>, dim3((unsigned)nblk), dim3(256), 0, a.stream,
+    KF_LAUNCH("fwd_mfma", fwd_mfma_kernel<128>, dim3((unsigned)nblk), dim3(256), 0, a.stream,
                        (const bf16*)a.q, a.cos, a.sin, krot, vt, (bf16*)a.out, a.lse, a.Sq, a.Sk,
                        Skp, a.Hq, a.Hkv, n_rep, bm_pos, nqb, scale_log2, a.causal);
   else
-    hipLaunchKernelGGL(fwd_mfma_kernel<64>, dim3((unsigned)nblk), dim3(256), 0, a.stream,
+    KF_LAUNCH("fwd_mfma", fwd_mfma_kernel<64>, dim3((unsigned)nblk), dim3(256), 0, a.stream,
                        (const bf16*)a.q, a.cos, a.sin, krot, vt, (bf16*)a.out, a.lse, a.Sq, a.Sk,
                        Skp, a.Hq, a.Hkv, n_rep, bm_pos, nqb, scale_log2, a.causal);
   KF_CHECK_LAUNCH();
@@ -463,11 +423,11 @@ int capture_probs_mfma(const FwdArgs& a, const float* lse, float* probs, void* w
   const int64_t nblk = (int64_t)nqb * a.B * a.Hkv;
   const float scale_log2 = a.scale * kLog2e;
   if (a.D == 128)
-    hipLaunchKernelGGL(capture_probs_mfma_kernel<128>, dim3((unsigned)nblk), dim3(256), 0,
+    KF_LAUNCH("capture_probs_mfma", capture_probs_mfma_kernel<128>, dim3((unsigned)nblk), dim3(256), 0,
                        a.stream, (const bf16*)a.q, a.cos, a.sin, krot, lse, probs, a.Sq, a.Sk,
                        Skp, a.Hq, a.Hkv, n_rep, bm_pos, nqb, scale_log2, a.causal);
   else
-    hipLaunchKernelGGL(capture_probs_mfma_kernel<64>, dim3((unsigned)nblk), dim3(256), 0,
+    KF_LAUNCH("capture_probs_mfma", capture_probs_mfma_kernel<64>, dim3((unsigned)nblk), dim3(256), 0,
                        a.stream, (const bf16*)a.q, a.cos, a.sin, krot, lse, probs, a.Sq, a.Sk,
                        Skp, a.Hq, a.Hkv, n_rep, bm_pos, nqb, scale_log2, a.causal);
   KF_CHECK_LAUNCH();

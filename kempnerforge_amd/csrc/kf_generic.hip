@@ -291,7 +291,7 @@ template <typename T>
 int launch_fwd_generic(const FwdArgs& a) {
   const int64_t rows = (int64_t)a.B * a.Hq * a.Sq;
   dim3 grid((unsigned)((rows + 3) / 4));
-  hipLaunchKernelGGL((fwd_generic_kernel<T>), grid, dim3(256), 0, a.stream, (const T*)a.q,
+  KF_LAUNCH("fwd_generic", (fwd_generic_kernel<T>), grid, dim3(256), 0, a.stream, (const T*)a.q,
                      (const T*)a.k, (const T*)a.v, a.cos, a.sin, (T*)a.out, a.lse, a.B, a.Sq,
                      a.Sk, a.Hq, a.Hkv, a.D, a.ksb, a.kss, a.ksh, a.vsb, a.vss, a.vsh,
                      a.k_rotated, a.causal, a.scale);
@@ -303,15 +303,15 @@ template <typename T>
 int launch_bwd_generic(const BwdArgs& a, float* delta) {
   const int64_t qrows = (int64_t)a.B * a.Hq * a.S;
   const int64_t krows = (int64_t)a.B * a.Hkv * a.S;
-  hipLaunchKernelGGL((bwd_delta_kernel<T>), dim3((unsigned)((qrows + 3) / 4)), dim3(256), 0,
+  KF_LAUNCH("bwd_delta_generic", (bwd_delta_kernel<T>), dim3((unsigned)((qrows + 3) / 4)), dim3(256), 0,
                      a.stream, (const T*)a.out, (const T*)a.dout, delta, a.B, a.S, a.Hq, a.D);
   KF_CHECK_LAUNCH();
-  hipLaunchKernelGGL((bwd_dq_generic_kernel<T>), dim3((unsigned)((qrows + 3) / 4)), dim3(256), 0,
+  KF_LAUNCH("bwd_dq_generic", (bwd_dq_generic_kernel<T>), dim3((unsigned)((qrows + 3) / 4)), dim3(256), 0,
                      a.stream, (const T*)a.q, (const T*)a.k, (const T*)a.v, a.cos, a.sin,
                      (const T*)a.dout, a.lse, delta, (T*)a.dq, a.B, a.S, a.Hq, a.Hkv, a.D,
                      a.causal, a.scale);
   KF_CHECK_LAUNCH();
-  hipLaunchKernelGGL((bwd_dkdv_generic_kernel<T>), dim3((unsigned)((krows + 3) / 4)), dim3(256),
+  KF_LAUNCH("bwd_dkdv_generic", (bwd_dkdv_generic_kernel<T>), dim3((unsigned)((krows + 3) / 4)), dim3(256),
                      0, a.stream, (const T*)a.q, (const T*)a.k, (const T*)a.v, a.cos, a.sin,
                      (const T*)a.dout, a.lse, delta, (T*)a.dk, (T*)a.dv, a.B, a.S, a.Hq, a.Hkv,
                      a.D, a.causal, a.scale);
@@ -322,7 +322,7 @@ int launch_bwd_generic(const BwdArgs& a, float* delta) {
 template <typename T>
 int launch_capture_probs_generic(const FwdArgs& a, const float* lse, float* probs) {
   const int64_t rows = (int64_t)a.B * a.Hq * a.Sq;
-  hipLaunchKernelGGL((capture_probs_generic_kernel<T>), dim3((unsigned)((rows + 3) / 4)),
+  KF_LAUNCH("capture_probs_generic", (capture_probs_generic_kernel<T>), dim3((unsigned)((rows + 3) / 4)),
                      dim3(256), 0, a.stream, (const T*)a.q, (const T*)a.k, a.cos, a.sin, lse,
                      probs, a.B, a.Sq, a.Sk, a.Hq, a.Hkv, a.D, a.ksb, a.kss, a.ksh, a.k_rotated,
                      a.causal, a.scale);

@@ -63,3 +63,26 @@ def test_shapes(cfg, causal):
     assert rel_max(dq, dq_r) <= TOL[dtype]
     assert rel_max(dk, dk_r) <= TOL[dtype]
     assert rel_max(dv, dv_r) <= TOL[dtype]
+
+
+def test_llama8b_shape_one_group():
+    """C3 at full size (B=4, S=4096, Hq=32, Hkv=8, D=128): the backward of KV
+    group (b=1, g=6) against the oracle (groups are independent), plus
+    determinism of a second backward."""
+    B, S, Hq, Hkv, D = 4, 4096, 32, 8, 128
+    announce("bwd 8B shape")
+    q = seeded((B, S, Hq, D), 0, torch.bfloat16)
+    k = seeded((B, S, Hkv, D), 1, torch.bfloat16)
+    v = seeded((B, S, Hkv, D), 2, torch.bfloat16)
+    do = seeded((B, S, Hq, D), 3, torch.bfloat16)
+    cos, sin = ref.rope_tables(D, S, 5e5)
+    _, dq, dk, dv = _grads(q, k, v, do, cos, sin)
+    _, dq2, dk2, dv2 = _grads(q, k, v, do, cos, sin)
+    assert torch.equal(dq, dq2) and torch.equal(dk, dk2) and torch.equal(dv, dv2)
+    b, g = 1, 6
+    hs = slice(4 * g, 4 * g + 4)
+    dq_r, dk_r, dv_r = ref.attention_bwd(q[b:b + 1, :, hs], k[b:b + 1, :, g:g + 1],
+                                         v[b:b + 1, :, g:g + 1], cos, sin, do[b:b + 1, :, hs])
+    assert rel_max(dq[b:b + 1, :, hs], dq_r) <= 2e-2
+    assert rel_max(dk[b:b + 1, :, g:g + 1], dk_r) <= 2e-2
+    assert rel_max(dv[b:b + 1, :, g:g + 1], dv_r) <= 2e-2

@@ -103,6 +103,9 @@ def test_nan_propagates():
     out, _ = _run(q, k, v, cos, sin)
     torch.cuda.synchronize()
     o = out.cpu()
-    # rows >= 5 of the heads of KV group 1 see the NaN; earlier rows do not
-    assert torch.isnan(o[0, 5:, 2:4]).any() and not torch.isnan(o[0, :5]).any()
+    # every row of KV group 1's heads that attends key 5 is NaN (so a NaN detector
+    # fires); group 0 never reads that value.  Rows before 5 in the same key tile
+    # may also turn NaN because a masked probability 0 times NaN is NaN — the
+    # reference's SDPA kernels multiply P by V the same way.
+    assert torch.isnan(o[0, 5:, 2:4].float().sum(-1)).all()
     assert not torch.isnan(o[0, :, 0:2]).any()

@@ -7,7 +7,6 @@ from __future__ import annotations
 
 import pytest
 import torch
-import torch.nn.functional as F
 
 from gpu_util import DEV, announce, max_abs
 from kempnerforge_amd import Attention, KVCache, ops
@@ -161,4 +160,3 @@ def test_doc_ids_branch_kept():
     a = attn(x, cos, sin)
     b = attn(x, cos, sin, doc_ids=torch.zeros(2, 32, dtype=torch.long, device=DEV))
     assert torch.allclose(a, b, atol=1e-4)
-    del F
