@@ -161,13 +161,12 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_kernel(
     bf16* __restrict__ dv, int S, int P, int Hq, int Hkv, int n_rep, int nkb, float scale_log2,
     float scale, int causal) {
   constexpr int KS = D / 16, DT = D / 32, HALF = D / 2;
-  constexpr int KLD = D + 8, QLD = BQ + 8;
-  constexpr int RCH = BQ * D / 8 / 256;  // 16-byte chunks per thread per staged tile
-  __shared__ __attribute__((aligned(16))) bf16 sQ[BQ * KLD];
-  __shared__ __attribute__((aligned(16))) bf16 sDO[BQ * KLD];
-  __shared__ __attribute__((aligned(16))) bf16 sQT[D * QLD];
-  __shared__ __attribute__((aligned(16))) bf16 sDOT[D * QLD];
-  __shared__ float sL[BQ], sDl[BQ];
+  constexpr int KR = D / 8, QR = BQ / 8;  // chunks per [q][d] row / per [d][q] row
+  struct Stage {
+    bf16 q[BQ * D], o[BQ * D], qt[D * BQ], ot[D * BQ];
+    float l[BQ], dl[BQ];
+  };
+  __shared__ __attribute__((aligned(16))) Stage st[2];
 
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, hh = lane >> 5, c32 = lane & 31;
   const int logical = xcd_logical_id(blockIdx.x, gridDim.x);
@@ -176,6 +175,25 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_kernel(
   const int b = bh / Hkv, g = bh % Hkv;
   const int k0 = kb * BKV;
   const int key = k0 + 32 * w + c32;
+
+  const int nqt = (S + BQ - 1) / BQ;
+  const int qt0 = causal ? k0 / BQ : 0;
+  const int per_head = nqt - qt0;
+  const int total = per_head > 0 ? per_head * n_rep : 0;
+
+  auto stage = [&](int it, int buf) {
+    const int hl = it / per_head, qtile = qt0 + it % per_head;
+    const int64_t bhq = (int64_t)b * Hq + g * n_rep + hl;
+    const int q0 = qtile * BQ;
+    Stage& S_ = st[buf];
+    tile_to_lds<BQ, KR>(qrot + (bhq * P + q0) * D, D, S_.q, w, lane);
+    tile_to_lds<BQ, KR>(don + (bhq * P + q0) * D, D, S_.o, w, lane);
+    tile_to_lds<D, QR>(qt + bhq * D * P + q0, P, S_.qt, w, lane);
+    tile_to_lds<D, QR>(dot + bhq * D * P + q0, P, S_.ot, w, lane);
+    if (w == 0) row_to_lds(lse2 + bhq * P + q0, S_.l, lane);
+    if (w == 1) row_to_lds(delta + bhq * P + q0, S_.dl, lane);
+  };
+  if (total > 0) stage(0, 0);
 
   bf16x8 kf[KS], vf[KS];
   {
@@ -196,99 +214,68 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_kernel(
       adv[dt][i] = 0.f;
     }
 
-  const int nqt = (S + BQ - 1) / BQ;
-  const int qt0 = causal ? k0 / BQ : 0;
-  const int per_head = nqt - qt0;
-  const int total = per_head > 0 ? per_head * n_rep : 0;
-
-  u32x4 rq[RCH], rd[RCH], rqt[RCH], rdt[RCH];
-  float rl = 0.f;
-  auto gload = [&](int it) {
-    const int hl = it / per_head, qtile = qt0 + it % per_head;
-    const int64_t bhq = (int64_t)b * Hq + g * n_rep + hl;
-    const int q0 = qtile * BQ;
-#pragma unroll
-    for (int i = 0; i < RCH; ++i) {
-      const int id = tid + 256 * i;
-      const int row = id / (D / 8), col = id % (D / 8);
-      rq[i] = *(const u32x4*)(qrot + (bhq * P + q0 + row) * D + 8 * col);
-      rd[i] = *(const u32x4*)(don + (bhq * P + q0 + row) * D + 8 * col);
-      const int trow = id / (BQ / 8), tcol = id % (BQ / 8);
-      rqt[i] = *(const u32x4*)(qt + (bhq * D + trow) * P + q0 + 8 * tcol);
-      rdt[i] = *(const u32x4*)(dot + (bhq * D + trow) * P + q0 + 8 * tcol);
-    }
-    if (tid < BQ) rl = lse2[bhq * P + q0 + tid];
-    else if (tid < 2 * BQ) rl = delta[bhq * P + q0 + tid - BQ];
-  };
-  auto lstore = [&]() {
-#pragma unroll
-    for (int i = 0; i < RCH; ++i) {
-      const int id = tid + 256 * i;
-      const int row = id / (D / 8), col = id % (D / 8);
-      *(u32x4*)(&sQ[row * KLD + 8 * col]) = rq[i];
-      *(u32x4*)(&sDO[row * KLD + 8 * col]) = rd[i];
-      const int trow = id / (BQ / 8), tcol = id % (BQ / 8);
-      *(u32x4*)(&sQT[trow * QLD + 8 * tcol]) = rqt[i];
-      *(u32x4*)(&sDOT[trow * QLD + 8 * tcol]) = rdt[i];
-    }
-    if (tid < BQ) sL[tid] = rl;
-    else if (tid < 2 * BQ) sDl[tid - BQ] = rl;
-  };
-
-  if (total > 0) gload(0);
+  lds_copy_wait();
+  __syncthreads();
   for (int it = 0; it < total; ++it) {
+    const int buf = it & 1;
+    if (it + 1 < total) stage(it + 1, buf ^ 1);
+    const Stage& S_ = st[buf];
     const int q0 = (qt0 + it % per_head) * BQ;
-    __syncthreads();
-    lstore();
-    __syncthreads();
-    if (it + 1 < total) gload(it + 1);
 
-    f32x16 s[2], dp[2];
+    // key index relative to q0; rows r of this tile see the key when r >= rel
+    const int rel = key - q0;
+    const bool diag = causal && q0 < k0 + BKV;
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) {
+      f32x16 s, dp;
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        s[mt][i] = 0.f;
-        dp[mt][i] = 0.f;
+        s[i] = 0.f;
+        dp[i] = 0.f;
       }
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
-        const bf16x8 aq = *(const bf16x8*)(&sQ[(32 * mt + c32) * KLD + 16 * ks + 8 * hh]);
-        s[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(aq, kf[ks], s[mt], 0, 0, 0);
-        const bf16x8 ad = *(const bf16x8*)(&sDO[(32 * mt + c32) * KLD + 16 * ks + 8 * hh]);
-        dp[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ad, vf[ks], dp[mt], 0, 0, 0);
+        const bf16x8 aq = lds_frag<KR>(S_.q, 32 * mt + c32, 2 * ks + hh);
+        const bf16x8 ad = lds_frag<KR>(S_.o, 32 * mt + c32, 2 * ks + hh);
+        s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(aq, kf[ks], s, 0, 0, 0);
+        dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ad, vf[ks], dp, 0, 0, 0);
       }
-    }
-    const bool need_mask = causal && q0 < k0 + BKV;
-    u32x4 pk[4], dsk[4];
+      u32x4 pk[2], dsk[2];
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
+      for (int gq = 0; gq < 4; ++gq) {
+        // rows 32mt + 8gq + 4hh + (0..3): their lse / Delta as one 16-byte read each
+        const int r0 = 32 * mt + 8 * gq + 4 * hh;
+        const f32x4 l4 = *(const f32x4*)(&S_.l[r0]);
+        const f32x4 d4 = *(const f32x4*)(&S_.dl[r0]);
+        float pv[4], dsv[4];
 #pragma unroll
-      for (int i = 0; i < 16; i += 2) {
-        float pv[2], dsv[2];
-#pragma unroll
-        for (int e = 0; e < 2; ++e) {
-          const int r = 32 * mt + 8 * ((i + e) >> 2) + 4 * hh + ((i + e) & 3);
-          float p = fast_exp2(s[mt][i + e] * scale_log2 - sL[r]);
-          if (need_mask && key > q0 + r) p = 0.f;
+        for (int e = 0; e < 4; ++e) {
+          float p = fast_exp2(__builtin_fmaf(s[4 * gq + e], scale_log2, -l4[e]));
+          if (diag) p = (rel > r0 + e) ? 0.f : p;
           pv[e] = p;
-          dsv[e] = p * (dp[mt][i + e] - sDl[r]);
+          dsv[e] = p * (dp[4 * gq + e] - d4[e]);
         }
-        pk[2 * mt + (i >> 3)][(i & 7) >> 1] = pack2(pv[0], pv[1]);
-        dsk[2 * mt + (i >> 3)][(i & 7) >> 1] = pack2(dsv[0], dsv[1]);
+        pk[gq >> 1][2 * (gq & 1)] = pack2(pv[0], pv[1]);
+        pk[gq >> 1][2 * (gq & 1) + 1] = pack2(pv[2], pv[3]);
+        dsk[gq >> 1][2 * (gq & 1)] = pack2(dsv[0], dsv[1]);
+        dsk[gq >> 1][2 * (gq & 1) + 1] = pack2(dsv[2], dsv[3]);
       }
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const bf16x8 pb = as_bf16x8(pk[c]);
-      const bf16x8 db = as_bf16x8(dsk[c]);
+      for (int cc = 0; cc < 2; ++cc) {
+        const int c = 2 * mt + cc;
+        const bf16x8 pb = as_bf16x8(pk[cc]);
+        const bf16x8 db = as_bf16x8(dsk[cc]);
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt) {
-        const bf16x8 a1 = *(const bf16x8*)(&sDOT[(32 * dt + c32) * QLD + 16 * c + 8 * hh]);
-        adv[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, pb, adv[dt], 0, 0, 0);
-        const bf16x8 a2 = *(const bf16x8*)(&sQT[(32 * dt + c32) * QLD + 16 * c + 8 * hh]);
-        adk[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a2, db, adk[dt], 0, 0, 0);
+        for (int dt = 0; dt < DT; ++dt) {
+          const bf16x8 a1 = lds_frag<QR>(S_.ot, 32 * dt + c32, 2 * c + hh);
+          const bf16x8 a2 = lds_frag<QR>(S_.qt, 32 * dt + c32, 2 * c + hh);
+          adv[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, pb, adv[dt], 0, 0, 0);
+          adk[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a2, db, adk[dt], 0, 0, 0);
+        }
       }
     }
+    lds_copy_wait();
+    __syncthreads();
   }
 
   if (key < S) {
@@ -321,24 +308,36 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_kernel(
 }
 
 template <int D>
-__global__ __launch_bounds__(256, D == 128 ? 1 : 2) void bwd_dq_kernel(
+__global__ __launch_bounds__(256, 1) void bwd_dq_kernel(
     const bf16* __restrict__ qrot, const bf16* __restrict__ don, const float* __restrict__ lse2,
     const float* __restrict__ delta, const bf16* __restrict__ krot, const bf16* __restrict__ vn,
     const bf16* __restrict__ kt, const float* __restrict__ cos, const float* __restrict__ sin,
     bf16* __restrict__ dq, int S, int P, int Hq, int Hkv, int n_rep, int bm_pos, int nqb,
     float scale_log2, float scale, int causal) {
   constexpr int KS = D / 16, DT = D / 32, HALF = D / 2;
-  constexpr int KLD = D + 8, VLD = BN + 8;
-  constexpr int KCH = BN * D / 8 / 256;
-  __shared__ __attribute__((aligned(16))) bf16 sK[BN * KLD];
-  __shared__ __attribute__((aligned(16))) bf16 sV[BN * KLD];
-  __shared__ __attribute__((aligned(16))) bf16 sKT[D * VLD];
+  constexpr int KR = D / 8, TR = BN / 8;
+  struct Stage {
+    bf16 k[BN * D], v[BN * D], kt[D * BN];
+  };
+  __shared__ __attribute__((aligned(16))) Stage st[2];
 
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, hh = lane >> 5, c32 = lane & 31;
   const int logical = xcd_logical_id(blockIdx.x, gridDim.x);
   const RowInfo ri = row_info(logical, nqb, Hkv, n_rep, bm_pos, S, w * 32 + c32);
   const int bh = ri.b * Hkv + ri.g;
   const int64_t bhq = (int64_t)ri.b * Hq + ri.hq;
+
+  const int kend = causal ? min(S, ri.p0 + bm_pos) : S;
+  const int ntiles = (kend + BN - 1) / BN;
+  const bf16* kbase = krot + (int64_t)bh * P * D;
+  const bf16* vbase = vn + (int64_t)bh * P * D;
+  const bf16* tbase = kt + (int64_t)bh * D * P;
+  auto stage = [&](int t, int buf) {
+    tile_to_lds<BN, KR>(kbase + (int64_t)t * BN * D, D, st[buf].k, w, lane);
+    tile_to_lds<BN, KR>(vbase + (int64_t)t * BN * D, D, st[buf].v, w, lane);
+    tile_to_lds<D, TR>(tbase + t * BN, P, st[buf].kt, w, lane);
+  };
+  if (ntiles > 0) stage(0, 0);
 
   bf16x8 qf[KS], df[KS];
   float l2 = INFINITY, dl = 0.f;
@@ -360,91 +359,65 @@ __global__ __launch_bounds__(256, D == 128 ? 1 : 2) void bwd_dq_kernel(
     }
   }
 
-  const int kend = causal ? min(S, ri.p0 + bm_pos) : S;
-  const int ntiles = (kend + BN - 1) / BN;
-  const bf16* kbase = krot + (int64_t)bh * P * D;
-  const bf16* vbase = vn + (int64_t)bh * P * D;
-  const bf16* tbase = kt + (int64_t)bh * D * P;
-
-  u32x4 rk[KCH], rv[KCH], rt[KCH];
-  auto gload = [&](int t) {
-#pragma unroll
-    for (int i = 0; i < KCH; ++i) {
-      const int id = tid + 256 * i, row = id / (D / 8), col = id % (D / 8);
-      rk[i] = *(const u32x4*)(kbase + (int64_t)(t * BN + row) * D + 8 * col);
-      rv[i] = *(const u32x4*)(vbase + (int64_t)(t * BN + row) * D + 8 * col);
-      const int trow = id / (BN / 8), tcol = id % (BN / 8);
-      rt[i] = *(const u32x4*)(tbase + (int64_t)trow * P + t * BN + 8 * tcol);
-    }
-  };
-  auto lstore = [&]() {
-#pragma unroll
-    for (int i = 0; i < KCH; ++i) {
-      const int id = tid + 256 * i, row = id / (D / 8), col = id % (D / 8);
-      *(u32x4*)(&sK[row * KLD + 8 * col]) = rk[i];
-      *(u32x4*)(&sV[row * KLD + 8 * col]) = rv[i];
-      const int trow = id / (BN / 8), tcol = id % (BN / 8);
-      *(u32x4*)(&sKT[trow * VLD + 8 * tcol]) = rt[i];
-    }
-  };
-
   f32x16 acc[DT];
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
     for (int i = 0; i < 16; ++i) acc[dt][i] = 0.f;
 
-  if (ntiles > 0) gload(0);
+  lds_copy_wait();
+  __syncthreads();
   for (int t = 0; t < ntiles; ++t) {
-    __syncthreads();
-    lstore();
-    __syncthreads();
-    if (t + 1 < ntiles) gload(t + 1);
+    const int buf = t & 1;
+    if (t + 1 < ntiles) stage(t + 1, buf ^ 1);
+    const Stage& S_ = st[buf];
 
-    f32x16 s[2], dp[2];
+    const int k0 = t * BN;
+    const bool need_mask = (causal && k0 + BN - 1 > ri.p0) || (k0 + BN > S);
+    // last visible key of this lane's row, relative to k0
+    const int lim = (causal ? min(ri.pos, S - 1) : S - 1) - k0;
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) {
+      f32x16 s, dp;
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        s[mt][i] = 0.f;
-        dp[mt][i] = 0.f;
+        s[i] = 0.f;
+        dp[i] = 0.f;
       }
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
-        const bf16x8 ak = *(const bf16x8*)(&sK[(32 * mt + c32) * KLD + 16 * ks + 8 * hh]);
-        s[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ak, qf[ks], s[mt], 0, 0, 0);
-        const bf16x8 av = *(const bf16x8*)(&sV[(32 * mt + c32) * KLD + 16 * ks + 8 * hh]);
-        dp[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, df[ks], dp[mt], 0, 0, 0);
+        const bf16x8 ak = lds_frag<KR>(S_.k, 32 * mt + c32, 2 * ks + hh);
+        const bf16x8 av = lds_frag<KR>(S_.v, 32 * mt + c32, 2 * ks + hh);
+        s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ak, qf[ks], s, 0, 0, 0);
+        dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, df[ks], dp, 0, 0, 0);
       }
-    }
-    const int k0 = t * BN;
-    const bool need_mask = (causal && k0 + BN - 1 > ri.p0) || (k0 + BN > S);
-    u32x4 dsk[4];
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
+      u32x4 dsk[2];
 #pragma unroll
       for (int i = 0; i < 16; i += 2) {
         float dsv[2];
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
-          float p = fast_exp2(s[mt][i + e] * scale_log2 - l2);
+          float p = fast_exp2(__builtin_fmaf(s[i + e], scale_log2, -l2));
           if (need_mask) {
-            const int key = k0 + 32 * mt + 8 * ((i + e) >> 2) + 4 * hh + ((i + e) & 3);
-            if ((causal && key > ri.pos) || key >= S) p = 0.f;
+            const int local = 32 * mt + 8 * ((i + e) >> 2) + 4 * hh + ((i + e) & 3);
+            p = local > lim ? 0.f : p;
           }
-          dsv[e] = p * (dp[mt][i + e] - dl);
+          dsv[e] = p * (dp[i + e] - dl);
         }
-        dsk[2 * mt + (i >> 3)][(i & 7) >> 1] = pack2(dsv[0], dsv[1]);
+        dsk[i >> 3][(i & 7) >> 1] = pack2(dsv[0], dsv[1]);
       }
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const bf16x8 db = as_bf16x8(dsk[c]);
+      for (int cc = 0; cc < 2; ++cc) {
+        const bf16x8 db = as_bf16x8(dsk[cc]);
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt) {
-        const bf16x8 a = *(const bf16x8*)(&sKT[(32 * dt + c32) * VLD + 16 * c + 8 * hh]);
-        acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, db, acc[dt], 0, 0, 0);
+        for (int dt = 0; dt < DT; ++dt) {
+          const bf16x8 a = lds_frag<TR>(S_.kt, 32 * dt + c32, 2 * (2 * mt + cc) + hh);
+          acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, db, acc[dt], 0, 0, 0);
+        }
       }
     }
+    lds_copy_wait();
+    __syncthreads();
   }
 
   if (ri.q_valid) {

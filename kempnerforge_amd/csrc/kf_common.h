@@ -89,9 +89,12 @@ __device__ __forceinline__ void unpack8(const u32x4& u, float* f) {
     f[2 * i + 1] = __uint_as_float(u[i] & 0xffff0000u);
   }
 }
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+// Two floats -> two round-to-nearest-even bf16 in one dword (lo in bits 0-15).
 __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
-  bf16 a = (bf16)lo, b = (bf16)hi;
-  return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+  const f32x2 f = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2));
 }
 __device__ __forceinline__ u32x4 pack8(const float* f) {
   u32x4 u;

@@ -125,49 +125,27 @@ __global__ __launch_bounds__(256, 2) void fwd_mfma_kernel(
     float* __restrict__ lse, int Sq, int Sk, int Skp, int Hq, int Hkv, int n_rep, int bm_pos,
     int nqb, float scale_log2, int causal) {
   constexpr int KS = D / 16, DT = D / 32;
-  constexpr int KLD = D + 8, VLD = BN + 8;
-  constexpr int KCH = BN * D / 8 / 256, VCH = D * BN / 8 / 256;
-  __shared__ __attribute__((aligned(16))) bf16 sK[BN * KLD];
-  __shared__ __attribute__((aligned(16))) bf16 sV[D * VLD];
+  constexpr int KR = D / 8, VR = BN / 8;  // 16-byte chunks per K row / per V^T row
+  __shared__ __attribute__((aligned(16))) bf16 sK[2][BN * D];
+  __shared__ __attribute__((aligned(16))) bf16 sV[2][D * BN];
 
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, hh = lane >> 5, c32 = lane & 31;
   const int logical = xcd_logical_id(blockIdx.x, gridDim.x);
   const RowInfo ri = row_info(logical, nqb, Hkv, n_rep, bm_pos, Sq, w * 32 + c32);
   const int bh = ri.b * Hkv + ri.g;
 
-  bf16x8 qf[KS];
-  load_q_frag<D>(q, cos, sin, ri, Sq, Hq, hh, qf);
-
   const int kend = causal ? min(Sk, min(ri.p0 + bm_pos, Sq)) : Sk;
   const int ntiles = (kend + BN - 1) / BN;
   const bf16* kbase = krot + (int64_t)bh * Skp * D;
   const bf16* vbase = vt + (int64_t)bh * D * Skp;
+  auto stage = [&](int t, int buf) {
+    tile_to_lds<BN, KR>(kbase + (int64_t)t * BN * D, D, sK[buf], w, lane);
+    tile_to_lds<D, VR>(vbase + t * BN, Skp, sV[buf], w, lane);
+  };
+  if (ntiles > 0) stage(0, 0);
 
-  u32x4 rk[KCH], rv[VCH];
-  auto gload = [&](int t) {
-#pragma unroll
-    for (int i = 0; i < KCH; ++i) {
-      const int id = tid + 256 * i, row = id / (D / 8), col = id % (D / 8);
-      rk[i] = *(const u32x4*)(kbase + (int64_t)(t * BN + row) * D + 8 * col);
-    }
-#pragma unroll
-    for (int i = 0; i < VCH; ++i) {
-      const int id = tid + 256 * i, row = id / (BN / 8), col = id % (BN / 8);
-      rv[i] = *(const u32x4*)(vbase + (int64_t)row * Skp + t * BN + 8 * col);
-    }
-  };
-  auto lstore = [&]() {
-#pragma unroll
-    for (int i = 0; i < KCH; ++i) {
-      const int id = tid + 256 * i, row = id / (D / 8), col = id % (D / 8);
-      *(u32x4*)(&sK[row * KLD + 8 * col]) = rk[i];
-    }
-#pragma unroll
-    for (int i = 0; i < VCH; ++i) {
-      const int id = tid + 256 * i, row = id / (BN / 8), col = id % (BN / 8);
-      *(u32x4*)(&sV[row * VLD + 8 * col]) = rv[i];
-    }
-  };
+  bf16x8 qf[KS];
+  load_q_frag<D>(q, cos, sin, ri, Sq, Hq, hh, qf);
 
   float m = -INFINITY, lsum = 0.f;
   f32x16 acc[DT];
@@ -176,12 +154,13 @@ __global__ __launch_bounds__(256, 2) void fwd_mfma_kernel(
 #pragma unroll
     for (int i = 0; i < 16; ++i) acc[dt][i] = 0.f;
 
-  if (ntiles > 0) gload(0);
+  lds_copy_wait();
+  __syncthreads();
   for (int t = 0; t < ntiles; ++t) {
-    __syncthreads();
-    lstore();
-    __syncthreads();
-    if (t + 1 < ntiles) gload(t + 1);
+    const int buf = t & 1;
+    if (t + 1 < ntiles) stage(t + 1, buf ^ 1);
+    const bf16* tK = sK[buf];
+    const bf16* tV = sV[buf];
 
     f32x16 s[2];
 #pragma unroll
@@ -192,55 +171,67 @@ __global__ __launch_bounds__(256, 2) void fwd_mfma_kernel(
     for (int ks = 0; ks < KS; ++ks) {
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt) {
-        const bf16x8 a = *(const bf16x8*)(&sK[(32 * mt + c32) * KLD + 16 * ks + 8 * hh]);
+        const bf16x8 a = lds_frag<KR>(tK, 32 * mt + c32, 2 * ks + hh);
         s[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[ks], s[mt], 0, 0, 0);
       }
     }
 
     const int k0 = t * BN;
     const bool need_mask = (causal && k0 + BN - 1 > ri.p0) || (k0 + BN > Sk);
+    if (need_mask) {
+      // last visible key of this lane's row, relative to k0 (branch-free select)
+      const int lim = (causal ? min(ri.pos, Sk - 1) : Sk - 1) - k0;
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int local = 32 * mt + 8 * (i >> 2) + 4 * hh + (i & 3);
+          s[mt][i] = local > lim ? -INFINITY : s[mt][i];
+        }
+    }
     float tmax = -INFINITY;
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        float x = s[mt][i] * scale_log2;
-        if (need_mask) {
-          const int key = k0 + 32 * mt + 8 * (i >> 2) + 4 * hh + (i & 3);
-          if ((causal && key > ri.pos) || key >= Sk) x = -INFINITY;
-        }
-        s[mt][i] = x;
-        tmax = fmaxf(tmax, x);
-      }
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-    const float mnew = fmaxf(m, tmax);
-    const float alpha = fast_exp2(m - mnew);
+      for (int i = 0; i < 16; ++i) tmax = fmaxf(tmax, s[mt][i]);
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64)) * scale_log2;
+    // Rescale the running output only when some row's max grew: the exponent
+    // base m may lag the true max (exp2 arguments stay <= 0 either way, since
+    // m >= every score seen so far), and rows whose max did not move keep
+    // alpha = 1.  The branch is wavefront-uniform.
+    if (__builtin_amdgcn_ballot_w64(tmax > m) != 0) {
+      const float mnew = fmaxf(m, tmax);
+      const float alpha = fast_exp2(m - mnew);
+      lsum *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[dt][i] *= alpha;
+      m = mnew;
+    }
     float psum = 0.f;
     u32x4 pk[4];
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
       for (int i = 0; i < 16; i += 2) {
-        const float p0 = fast_exp2(s[mt][i] - mnew);
-        const float p1 = fast_exp2(s[mt][i + 1] - mnew);
+        const float p0 = fast_exp2(__builtin_fmaf(s[mt][i], scale_log2, -m));
+        const float p1 = fast_exp2(__builtin_fmaf(s[mt][i + 1], scale_log2, -m));
         psum += p0 + p1;
         pk[2 * mt + (i >> 3)][(i & 7) >> 1] = pack2(p0, p1);
       }
-    lsum = lsum * alpha + psum;
-    m = mnew;
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) acc[dt][i] *= alpha;
+    lsum += psum;
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       const bf16x8 pb = as_bf16x8(pk[c]);
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
-        const bf16x8 a = *(const bf16x8*)(&sV[(32 * dt + c32) * VLD + 16 * c + 8 * hh]);
+        const bf16x8 a = lds_frag<VR>(tV, 32 * dt + c32, 2 * c + hh);
         acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb, acc[dt], 0, 0, 0);
       }
     }
+    lds_copy_wait();
+    __syncthreads();
   }
 
   const float ltot = lsum + __shfl_xor(lsum, 32, 64);
@@ -275,9 +266,8 @@ __global__ __launch_bounds__(256, 2) void capture_probs_mfma_kernel(
     int Sq, int Sk, int Skp, int Hq, int Hkv, int n_rep, int bm_pos, int nqb, float scale_log2,
     int causal) {
   constexpr int KS = D / 16;
-  constexpr int KLD = D + 8;
-  constexpr int KCH = BN * D / 8 / 256;
-  __shared__ __attribute__((aligned(16))) bf16 sK[BN * KLD];
+  constexpr int KR = D / 8;
+  __shared__ __attribute__((aligned(16))) bf16 sK[BN * D];
   __shared__ float sL[ROWS];
   __shared__ int sRowOff[ROWS];  // row offset of (hq, pos) in units of Sk floats, or -1
 
@@ -305,12 +295,8 @@ __global__ __launch_bounds__(256, 2) void capture_probs_mfma_kernel(
 
   for (int t = 0; t < ntiles; ++t) {
     __syncthreads();
-#pragma unroll
-    for (int i = 0; i < KCH; ++i) {
-      const int id = tid + 256 * i, row = id / (D / 8), col = id % (D / 8);
-      *(u32x4*)(&sK[row * KLD + 8 * col]) =
-          *(const u32x4*)(kbase + (int64_t)(t * BN + row) * D + 8 * col);
-    }
+    tile_to_lds<BN, KR>(kbase + (int64_t)t * BN * D, D, sK, w, lane);
+    lds_copy_wait();
     __syncthreads();
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
@@ -319,7 +305,7 @@ __global__ __launch_bounds__(256, 2) void capture_probs_mfma_kernel(
       for (int i = 0; i < 16; ++i) s[i] = 0.f;
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
-        const bf16x8 bk = *(const bf16x8*)(&sK[(32 * nt + c32) * KLD + 16 * ks + 8 * hh]);
+        const bf16x8 bk = lds_frag<KR>(sK, 32 * nt + c32, 2 * ks + hh);
         s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qf[ks], bk, s, 0, 0, 0);
       }
       const int key = t * BN + 32 * nt + c32;

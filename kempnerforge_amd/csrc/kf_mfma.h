@@ -49,5 +49,44 @@ __device__ __forceinline__ RowInfo row_info(int logical, int nqb, int Hkv, int n
   return ri;
 }
 
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// LDS tiles are stored unpadded, [rows][R] 16-byte chunks, with chunk c of row
+// r at position c ^ (r % R): the 32 (or 8, 16) consecutive rows a fragment read
+// touches then land in distinct bank groups.  R is 8 or 16.
+template <int R>
+__device__ __forceinline__ const bf16x8& lds_frag(const bf16* tile, int row, int chunk) {
+  return *(const bf16x8*)(tile + (row * R + (chunk ^ (row % R))) * 8);
+}
+
+// Copy a [ROWS_T][R chunks] bf16 tile whose rows start `ld` elements apart in
+// global memory into a swizzled LDS tile with direct global->LDS loads: each
+// instruction moves 64 lanes x 16 bytes into 1 KB of contiguous LDS, so the
+// lane picks the global chunk that belongs at its LDS position.  The 4
+// wavefronts of the workgroup split the instructions.  Completion is tracked
+// by vmcnt: wait with lds_copy_wait() and a barrier before reading the tile.
+template <int ROWS_T, int R>
+__device__ __forceinline__ void tile_to_lds(const bf16* __restrict__ g, int64_t ld, bf16* lds,
+                                            int w, int lane) {
+  constexpr int TOTAL = ROWS_T * R / 64;
+  static_assert(TOTAL % 4 == 0, "tile must split over 4 wavefronts");
+  constexpr int PER = TOTAL / 4;
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const int L = (w * PER + j) * 64 + lane;
+    const int row = L / R, pc = L % R;
+    const int lc = pc ^ (row % R);
+    __builtin_amdgcn_global_load_lds((const void*)(g + row * ld + lc * 8),
+                                     (lds_ptr_t)(lds + (w * PER + j) * 512), 16, 0, 0);
+  }
+}
+
+// 64 consecutive floats (one per lane of one wavefront) straight into LDS.
+__device__ __forceinline__ void row_to_lds(const float* __restrict__ g, float* lds, int lane) {
+  __builtin_amdgcn_global_load_lds((const void*)(g + lane), (lds_ptr_t)lds, 4, 0, 0);
+}
+
+__device__ __forceinline__ void lds_copy_wait() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
 }  // namespace mfma
 }  // namespace kf
