@@ -152,29 +152,29 @@ __global__ __launch_bounds__(256) void q_prep_bwd_kernel(
   }
 }
 
+// dK/dV workgroup: 8 wavefronts on the same 128 keys.  Wavefronts 0-3 ("V
+// waves") compute S -> P -> dV^T += dO^T P; wavefronts 4-7 ("K waves") compute
+// S, dP -> dS -> dK^T += Q^T dS.  S is evaluated by both roles, which costs 25%
+// more MFMA work but lets each wavefront fit in 256 registers, so every SIMD
+// runs two wavefronts whose VALU, LDS and waits overlap the other's MFMAs.
 template <int D>
-__global__ __launch_bounds__(256, 1) void bwd_dkdv_kernel(
-    const bf16* __restrict__ krot, const bf16* __restrict__ vn, const bf16* __restrict__ qrot,
-    const bf16* __restrict__ qt, const bf16* __restrict__ don, const bf16* __restrict__ dot,
-    const float* __restrict__ lse2, const float* __restrict__ delta,
-    const float* __restrict__ cos, const float* __restrict__ sin, bf16* __restrict__ dk,
-    bf16* __restrict__ dv, int S, int P, int Hq, int Hkv, int n_rep, int nkb, float scale_log2,
-    float scale, int causal) {
-  constexpr int KS = D / 16, DT = D / 32, HALF = D / 2;
-  constexpr int KR = D / 8, QR = BQ / 8;  // chunks per [q][d] row / per [d][q] row
-  struct Stage {
-    bf16 q[BQ * D], o[BQ * D], qt[D * BQ], ot[D * BQ];
-    float l[BQ], dl[BQ];
-  };
-  __shared__ __attribute__((aligned(16))) Stage st[2];
+struct DkdvStage {
+  bf16 q[BQ * D], o[BQ * D], qt[D * BQ], ot[D * BQ];
+  float l[BQ], dl[BQ];
+};
 
-  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, hh = lane >> 5, c32 = lane & 31;
-  const int logical = xcd_logical_id(blockIdx.x, gridDim.x);
-  const int bh = logical / nkb;
-  const int kb = logical % nkb;  // ascending: the longest causal key tiles first
-  const int b = bh / Hkv, g = bh % Hkv;
-  const int k0 = kb * BKV;
-  const int key = k0 + 32 * w + c32;
+template <int D, bool KROLE>
+__device__ __forceinline__ void dkdv_role(
+    DkdvStage<D>* st, const bf16* __restrict__ krot, const bf16* __restrict__ vn,
+    const bf16* __restrict__ qrot, const bf16* __restrict__ qt, const bf16* __restrict__ don,
+    const bf16* __restrict__ dot, const float* __restrict__ lse2, const float* __restrict__ delta,
+    const float* __restrict__ cos, const float* __restrict__ sin, bf16* __restrict__ dk,
+    bf16* __restrict__ dv, int S, int P, int Hq, int Hkv, int n_rep, int b, int g, int bh, int k0,
+    int w, int lane, float scale_log2, float scale, int causal) {
+  constexpr int KS = D / 16, DT = D / 32, HALF = D / 2;
+  constexpr int KR = D / 8, QR = BQ / 8;
+  const int hh = lane >> 5, c32 = lane & 31;
+  const int key = k0 + 32 * (w & 3) + c32;
 
   const int nqt = (S + BQ - 1) / BQ;
   const int qt0 = causal ? k0 / BQ : 0;
@@ -185,11 +185,11 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_kernel(
     const int hl = it / per_head, qtile = qt0 + it % per_head;
     const int64_t bhq = (int64_t)b * Hq + g * n_rep + hl;
     const int q0 = qtile * BQ;
-    Stage& S_ = st[buf];
-    tile_to_lds<BQ, KR>(qrot + (bhq * P + q0) * D, D, S_.q, w, lane);
-    tile_to_lds<BQ, KR>(don + (bhq * P + q0) * D, D, S_.o, w, lane);
-    tile_to_lds<D, QR>(qt + bhq * D * P + q0, P, S_.qt, w, lane);
-    tile_to_lds<D, QR>(dot + bhq * D * P + q0, P, S_.ot, w, lane);
+    DkdvStage<D>& S_ = st[buf];
+    tile_to_lds<BQ, KR, 8>(qrot + (bhq * P + q0) * D, D, S_.q, w, lane);
+    tile_to_lds<BQ, KR, 8>(don + (bhq * P + q0) * D, D, S_.o, w, lane);
+    tile_to_lds<D, QR, 8>(qt + bhq * D * P + q0, P, S_.qt, w, lane);
+    tile_to_lds<D, QR, 8>(dot + bhq * D * P + q0, P, S_.ot, w, lane);
     if (w == 0) row_to_lds(lse2 + bhq * P + q0, S_.l, lane);
     if (w == 1) row_to_lds(delta + bhq * P + q0, S_.dl, lane);
   };
@@ -198,32 +198,28 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_kernel(
   bf16x8 kf[KS], vf[KS];
   {
     const bf16* kr = krot + ((int64_t)bh * P + key) * D + 8 * hh;
-    const bf16* vr = vn + ((int64_t)bh * P + key) * D + 8 * hh;
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      kf[ks] = as_bf16x8(*(const u32x4*)(kr + 16 * ks));
-      vf[ks] = as_bf16x8(*(const u32x4*)(vr + 16 * ks));
+    for (int ks = 0; ks < KS; ++ks) kf[ks] = as_bf16x8(*(const u32x4*)(kr + 16 * ks));
+    if (KROLE) {
+      const bf16* vr = vn + ((int64_t)bh * P + key) * D + 8 * hh;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) vf[ks] = as_bf16x8(*(const u32x4*)(vr + 16 * ks));
     }
   }
-  f32x16 adk[DT], adv[DT];
+  f32x16 acc[DT];
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      adk[dt][i] = 0.f;
-      adv[dt][i] = 0.f;
-    }
+    for (int i = 0; i < 16; ++i) acc[dt][i] = 0.f;
 
   lds_copy_wait();
   __syncthreads();
   for (int it = 0; it < total; ++it) {
     const int buf = it & 1;
     if (it + 1 < total) stage(it + 1, buf ^ 1);
-    const Stage& S_ = st[buf];
+    const DkdvStage<D>& S_ = st[buf];
     const int q0 = (qt0 + it % per_head) * BQ;
-
-    // key index relative to q0; rows r of this tile see the key when r >= rel
-    const int rel = key - q0;
+    const int rel = key - q0;  // rows r of this tile see the key when r >= rel
     const bool diag = causal && q0 < k0 + BKV;
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) {
@@ -233,54 +229,73 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_kernel(
         s[i] = 0.f;
         dp[i] = 0.f;
       }
+      {
+        constexpr int PF = 2;
+        bf16x8 fq[KS], fo[KS];
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        const bf16x8 aq = lds_frag<KR>(S_.q, 32 * mt + c32, 2 * ks + hh);
-        const bf16x8 ad = lds_frag<KR>(S_.o, 32 * mt + c32, 2 * ks + hh);
-        s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(aq, kf[ks], s, 0, 0, 0);
-        dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ad, vf[ks], dp, 0, 0, 0);
+        for (int ks = 0; ks < PF; ++ks) {
+          fq[ks] = lds_frag<KR>(S_.q, 32 * mt + c32, 2 * ks + hh);
+          if (KROLE) fo[ks] = lds_frag<KR>(S_.o, 32 * mt + c32, 2 * ks + hh);
+        }
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          __builtin_amdgcn_sched_barrier(0);
+          if (ks + PF < KS) {
+            fq[ks + PF] = lds_frag<KR>(S_.q, 32 * mt + c32, 2 * (ks + PF) + hh);
+            if (KROLE) fo[ks + PF] = lds_frag<KR>(S_.o, 32 * mt + c32, 2 * (ks + PF) + hh);
+          }
+          s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fq[ks], kf[ks], s, 0, 0, 0);
+          if (KROLE) dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fo[ks], vf[ks], dp, 0, 0, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
       }
-      u32x4 pk[2], dsk[2];
+      u32x4 pk[2];
 #pragma unroll
       for (int gq = 0; gq < 4; ++gq) {
-        // rows 32mt + 8gq + 4hh + (0..3): their lse / Delta as one 16-byte read each
+        // rows 32mt + 8gq + 4hh + (0..3): their lse (and Delta) as 16-byte reads
         const int r0 = 32 * mt + 8 * gq + 4 * hh;
         const f32x4 l4 = *(const f32x4*)(&S_.l[r0]);
-        const f32x4 d4 = *(const f32x4*)(&S_.dl[r0]);
-        float pv[4], dsv[4];
+        float v[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           float p = fast_exp2(__builtin_fmaf(s[4 * gq + e], scale_log2, -l4[e]));
           if (diag) p = (rel > r0 + e) ? 0.f : p;
-          pv[e] = p;
-          dsv[e] = p * (dp[4 * gq + e] - d4[e]);
+          v[e] = p;
         }
-        pk[gq >> 1][2 * (gq & 1)] = pack2(pv[0], pv[1]);
-        pk[gq >> 1][2 * (gq & 1) + 1] = pack2(pv[2], pv[3]);
-        dsk[gq >> 1][2 * (gq & 1)] = pack2(dsv[0], dsv[1]);
-        dsk[gq >> 1][2 * (gq & 1) + 1] = pack2(dsv[2], dsv[3]);
+        if (KROLE) {
+          const f32x4 d4 = *(const f32x4*)(&S_.dl[r0]);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] *= dp[4 * gq + e] - d4[e];
+        }
+        pk[gq >> 1][2 * (gq & 1)] = pack2(v[0], v[1]);
+        pk[gq >> 1][2 * (gq & 1) + 1] = pack2(v[2], v[3]);
       }
+      {
+        constexpr int NS = 2 * DT, PF = 2;
+        const bf16* tA = KROLE ? S_.qt : S_.ot;
+        bf16x8 fa[NS];
 #pragma unroll
-      for (int cc = 0; cc < 2; ++cc) {
-        const int c = 2 * mt + cc;
-        const bf16x8 pb = as_bf16x8(pk[cc]);
-        const bf16x8 db = as_bf16x8(dsk[cc]);
+        for (int n = 0; n < PF; ++n)
+          fa[n] = lds_frag<QR>(tA, 32 * (n % DT) + c32, 2 * (2 * mt + n / DT) + hh);
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
-          const bf16x8 a1 = lds_frag<QR>(S_.ot, 32 * dt + c32, 2 * c + hh);
-          const bf16x8 a2 = lds_frag<QR>(S_.qt, 32 * dt + c32, 2 * c + hh);
-          adv[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, pb, adv[dt], 0, 0, 0);
-          adk[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a2, db, adk[dt], 0, 0, 0);
+        for (int n = 0; n < NS; ++n) {
+          __builtin_amdgcn_sched_barrier(0);
+          if (n + PF < NS)
+            fa[n + PF] = lds_frag<QR>(tA, 32 * ((n + PF) % DT) + c32,
+                                      2 * (2 * mt + (n + PF) / DT) + hh);
+          acc[n % DT] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[n], as_bf16x8(pk[n / DT]),
+                                                               acc[n % DT], 0, 0, 0);
         }
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
     lds_copy_wait();
     __syncthreads();
   }
 
-  if (key < S) {
+  if (key >= S) return;
+  if (KROLE) {
     bf16* dkr = dk + (((int64_t)b * S + key) * Hkv + g) * D;
-    bf16* dvr = dv + (((int64_t)b * S + key) * Hkv + g) * D;
     const float* cr = cos + (int64_t)key * HALF;
     const float* sr = sin + (int64_t)key * HALF;
 #pragma unroll
@@ -291,24 +306,53 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_kernel(
         float lo[4], hi[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          rope_pair_bwd<bf16>(adk[dt][4 * gi + e] * scale, adk[dt + DT / 2][4 * gi + e] * scale,
+          rope_pair_bwd<bf16>(acc[dt][4 * gi + e] * scale, acc[dt + DT / 2][4 * gi + e] * scale,
                               cr[d + e], sr[d + e], lo[e], hi[e]);
         *(u32x2*)(dkr + d) = u32x2{pack2(lo[0], lo[1]), pack2(lo[2], lo[3])};
         *(u32x2*)(dkr + d + HALF) = u32x2{pack2(hi[0], hi[1]), pack2(hi[2], hi[3])};
       }
+  } else {
+    bf16* dvr = dv + (((int64_t)b * S + key) * Hkv + g) * D;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
       for (int gi = 0; gi < 4; ++gi) {
         const int d = 32 * dt + 8 * gi + 4 * hh;
-        *(u32x2*)(dvr + d) = u32x2{pack2(adv[dt][4 * gi], adv[dt][4 * gi + 1]),
-                                   pack2(adv[dt][4 * gi + 2], adv[dt][4 * gi + 3])};
+        *(u32x2*)(dvr + d) = u32x2{pack2(acc[dt][4 * gi], acc[dt][4 * gi + 1]),
+                                   pack2(acc[dt][4 * gi + 2], acc[dt][4 * gi + 3])};
       }
   }
 }
 
 template <int D>
-__global__ __launch_bounds__(256, 1) void bwd_dq_kernel(
+__global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(
+    const bf16* __restrict__ krot, const bf16* __restrict__ vn, const bf16* __restrict__ qrot,
+    const bf16* __restrict__ qt, const bf16* __restrict__ don, const bf16* __restrict__ dot,
+    const float* __restrict__ lse2, const float* __restrict__ delta,
+    const float* __restrict__ cos, const float* __restrict__ sin, bf16* __restrict__ dk,
+    bf16* __restrict__ dv, int S, int P, int Hq, int Hkv, int n_rep, int nkb, float scale_log2,
+    float scale, int causal) {
+  __shared__ __attribute__((aligned(16))) DkdvStage<D> st[2];
+  const int w = wave_id(), lane = threadIdx.x & 63;
+  const int logical = xcd_logical_id(blockIdx.x, gridDim.x);
+  const int bh = logical / nkb;
+  const int kb = logical % nkb;  // ascending: the longest causal key tiles first
+  const int b = bh / Hkv, g = bh % Hkv;
+  const int k0 = kb * BKV;
+  if (w >= 4)
+    dkdv_role<D, true>(st, krot, vn, qrot, qt, don, dot, lse2, delta, cos, sin, dk, dv, S, P, Hq,
+                       Hkv, n_rep, b, g, bh, k0, w, lane, scale_log2, scale, causal);
+  else
+    dkdv_role<D, false>(st, krot, vn, qrot, qt, don, dot, lse2, delta, cos, sin, dk, dv, S, P, Hq,
+                        Hkv, n_rep, b, g, bh, k0, w, lane, scale_log2, scale, causal);
+}
+
+// dQ workgroup: 8 wavefronts x 32 rows = 256 (query head, position) rows of one
+// KV group, all sharing each staged K / V / K^T tile (two wavefronts per SIMD).
+constexpr int DQ_ROWS = 256;
+
+template <int D>
+__global__ __launch_bounds__(512, 1) void bwd_dq_kernel(
     const bf16* __restrict__ qrot, const bf16* __restrict__ don, const float* __restrict__ lse2,
     const float* __restrict__ delta, const bf16* __restrict__ krot, const bf16* __restrict__ vn,
     const bf16* __restrict__ kt, const float* __restrict__ cos, const float* __restrict__ sin,
@@ -321,7 +365,7 @@ __global__ __launch_bounds__(256, 1) void bwd_dq_kernel(
   };
   __shared__ __attribute__((aligned(16))) Stage st[2];
 
-  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, hh = lane >> 5, c32 = lane & 31;
+  const int tid = threadIdx.x, w = wave_id(), lane = tid & 63, hh = lane >> 5, c32 = lane & 31;
   const int logical = xcd_logical_id(blockIdx.x, gridDim.x);
   const RowInfo ri = row_info(logical, nqb, Hkv, n_rep, bm_pos, S, w * 32 + c32);
   const int bh = ri.b * Hkv + ri.g;
@@ -333,9 +377,9 @@ __global__ __launch_bounds__(256, 1) void bwd_dq_kernel(
   const bf16* vbase = vn + (int64_t)bh * P * D;
   const bf16* tbase = kt + (int64_t)bh * D * P;
   auto stage = [&](int t, int buf) {
-    tile_to_lds<BN, KR>(kbase + (int64_t)t * BN * D, D, st[buf].k, w, lane);
-    tile_to_lds<BN, KR>(vbase + (int64_t)t * BN * D, D, st[buf].v, w, lane);
-    tile_to_lds<D, TR>(tbase + t * BN, P, st[buf].kt, w, lane);
+    tile_to_lds<BN, KR, 8>(kbase + (int64_t)t * BN * D, D, st[buf].k, w, lane);
+    tile_to_lds<BN, KR, 8>(vbase + (int64_t)t * BN * D, D, st[buf].v, w, lane);
+    tile_to_lds<D, TR, 8>(tbase + t * BN, P, st[buf].kt, w, lane);
   };
   if (ntiles > 0) stage(0, 0);
 
@@ -371,7 +415,6 @@ __global__ __launch_bounds__(256, 1) void bwd_dq_kernel(
     const int buf = t & 1;
     if (t + 1 < ntiles) stage(t + 1, buf ^ 1);
     const Stage& S_ = st[buf];
-
     const int k0 = t * BN;
     const bool need_mask = (causal && k0 + BN - 1 > ri.p0) || (k0 + BN > S);
     // last visible key of this lane's row, relative to k0
@@ -384,12 +427,26 @@ __global__ __launch_bounds__(256, 1) void bwd_dq_kernel(
         s[i] = 0.f;
         dp[i] = 0.f;
       }
+      {
+        // fragment reads run PF steps ahead of the MFMAs that consume them
+        constexpr int PF = 2;
+        bf16x8 fk[KS], fv[KS];
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        const bf16x8 ak = lds_frag<KR>(S_.k, 32 * mt + c32, 2 * ks + hh);
-        const bf16x8 av = lds_frag<KR>(S_.v, 32 * mt + c32, 2 * ks + hh);
-        s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ak, qf[ks], s, 0, 0, 0);
-        dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, df[ks], dp, 0, 0, 0);
+        for (int ks = 0; ks < PF; ++ks) {
+          fk[ks] = lds_frag<KR>(S_.k, 32 * mt + c32, 2 * ks + hh);
+          fv[ks] = lds_frag<KR>(S_.v, 32 * mt + c32, 2 * ks + hh);
+        }
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          __builtin_amdgcn_sched_barrier(0);
+          if (ks + PF < KS) {
+            fk[ks + PF] = lds_frag<KR>(S_.k, 32 * mt + c32, 2 * (ks + PF) + hh);
+            fv[ks + PF] = lds_frag<KR>(S_.v, 32 * mt + c32, 2 * (ks + PF) + hh);
+          }
+          s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fk[ks], qf[ks], s, 0, 0, 0);
+          dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fv[ks], df[ks], dp, 0, 0, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
       }
       u32x4 dsk[2];
 #pragma unroll
@@ -406,14 +463,22 @@ __global__ __launch_bounds__(256, 1) void bwd_dq_kernel(
         }
         dsk[i >> 3][(i & 7) >> 1] = pack2(dsv[0], dsv[1]);
       }
+      {
+        constexpr int NS = 2 * DT, PF = 2;
+        bf16x8 fa[NS];
 #pragma unroll
-      for (int cc = 0; cc < 2; ++cc) {
-        const bf16x8 db = as_bf16x8(dsk[cc]);
+        for (int n = 0; n < PF; ++n)
+          fa[n] = lds_frag<TR>(S_.kt, 32 * (n % DT) + c32, 2 * (2 * mt + n / DT) + hh);
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
-          const bf16x8 a = lds_frag<TR>(S_.kt, 32 * dt + c32, 2 * (2 * mt + cc) + hh);
-          acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, db, acc[dt], 0, 0, 0);
+        for (int n = 0; n < NS; ++n) {
+          __builtin_amdgcn_sched_barrier(0);
+          if (n + PF < NS)
+            fa[n + PF] = lds_frag<TR>(S_.kt, 32 * ((n + PF) % DT) + c32,
+                                      2 * (2 * mt + (n + PF) / DT) + hh);
+          acc[n % DT] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[n], as_bf16x8(dsk[n / DT]),
+                                                               acc[n % DT], 0, 0, 0);
         }
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
     lds_copy_wait();
@@ -478,14 +543,14 @@ int launch_bwd(const BwdArgs& a, void* workspace) {
                      a.sin, w.qrot, w.qt, w.don, w.dot, w.lse2, w.delta, a.S, P, a.Hq);
   KF_CHECK_LAUNCH();
   const int nkb = P / BKV;
-  KF_LAUNCH("bwd_dkdv", bwd_dkdv_kernel<D>, dim3(nkb * a.B * a.Hkv), dim3(256), 0, a.stream,
+  KF_LAUNCH("bwd_dkdv", bwd_dkdv_kernel<D>, dim3(nkb * a.B * a.Hkv), dim3(512), 0, a.stream,
                      w.krot, w.vn, w.qrot, w.qt, w.don, w.dot, w.lse2, w.delta, a.cos, a.sin,
                      (bf16*)a.dk, (bf16*)a.dv, a.S, P, a.Hq, a.Hkv, n_rep, nkb, scale_log2, a.scale,
                      a.causal);
   KF_CHECK_LAUNCH();
-  const int bm_pos = ROWS / n_rep;
+  const int bm_pos = DQ_ROWS / n_rep;
   const int nqb = (a.S + bm_pos - 1) / bm_pos;
-  KF_LAUNCH("bwd_dq", bwd_dq_kernel<D>, dim3(nqb * a.B * a.Hkv), dim3(256), 0, a.stream, w.qrot,
+  KF_LAUNCH("bwd_dq", bwd_dq_kernel<D>, dim3(nqb * a.B * a.Hkv), dim3(512), 0, a.stream, w.qrot,
                      w.don, w.lse2, w.delta, w.krot, w.vn, w.kt, a.cos, a.sin, (bf16*)a.dq, a.S, P,
                      a.Hq, a.Hkv, n_rep, bm_pos, nqb, scale_log2, a.scale, a.causal);
   KF_CHECK_LAUNCH();
@@ -497,7 +562,7 @@ int launch_bwd(const BwdArgs& a, void* workspace) {
 bool bwd_mfma_supported(const BwdArgs& a) {
   if (a.dtype != BF16 || (a.D != 64 && a.D != 128)) return false;
   const int n_rep = a.Hq / a.Hkv;
-  if (n_rep < 1 || n_rep > ROWS) return false;
+  if (n_rep < 1 || n_rep > ROWS) return false;  // also bounds DQ_ROWS / n_rep >= 2
   auto al16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
   return al16(a.q) && al16(a.k) && al16(a.v) && al16(a.out) && al16(a.dout) && al16(a.dq) &&
          al16(a.dk) && al16(a.dv) && al16(a.cos) && al16(a.sin);

@@ -129,7 +129,7 @@ __global__ __launch_bounds__(256, 2) void fwd_mfma_kernel(
   __shared__ __attribute__((aligned(16))) bf16 sK[2][BN * D];
   __shared__ __attribute__((aligned(16))) bf16 sV[2][D * BN];
 
-  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, hh = lane >> 5, c32 = lane & 31;
+  const int tid = threadIdx.x, w = wave_id(), lane = tid & 63, hh = lane >> 5, c32 = lane & 31;
   const int logical = xcd_logical_id(blockIdx.x, gridDim.x);
   const RowInfo ri = row_info(logical, nqb, Hkv, n_rep, bm_pos, Sq, w * 32 + c32);
   const int bh = ri.b * Hkv + ri.g;
@@ -271,7 +271,7 @@ __global__ __launch_bounds__(256, 2) void capture_probs_mfma_kernel(
   __shared__ float sL[ROWS];
   __shared__ int sRowOff[ROWS];  // row offset of (hq, pos) in units of Sk floats, or -1
 
-  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, hh = lane >> 5, c32 = lane & 31;
+  const int tid = threadIdx.x, w = wave_id(), lane = tid & 63, hh = lane >> 5, c32 = lane & 31;
   const int logical = xcd_logical_id(blockIdx.x, gridDim.x);
   const RowInfo ri = row_info(logical, nqb, Hkv, n_rep, bm_pos, Sq, w * 32 + c32);
   const int bh = ri.b * Hkv + ri.g;

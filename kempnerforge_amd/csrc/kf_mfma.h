@@ -65,18 +65,20 @@ __device__ __forceinline__ const bf16x8& lds_frag(const bf16* tile, int row, int
 // lane picks the global chunk that belongs at its LDS position.  The 4
 // wavefronts of the workgroup split the instructions.  Completion is tracked
 // by vmcnt: wait with lds_copy_wait() and a barrier before reading the tile.
-template <int ROWS_T, int R>
-__device__ __forceinline__ void tile_to_lds(const bf16* __restrict__ g, int64_t ld, bf16* lds,
+template <int ROWS_T, int R, int NW = 4>
+__device__ __forceinline__ void tile_to_lds(const bf16* __restrict__ g, uint32_t ld, bf16* lds,
                                             int w, int lane) {
   constexpr int TOTAL = ROWS_T * R / 64;
-  static_assert(TOTAL % 4 == 0, "tile must split over 4 wavefronts");
-  constexpr int PER = TOTAL / 4;
+  static_assert(TOTAL % NW == 0, "tile must split evenly over the wavefronts");
+  constexpr int PER = TOTAL / NW;
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
     const int L = (w * PER + j) * 64 + lane;
     const int row = L / R, pc = L % R;
     const int lc = pc ^ (row % R);
-    __builtin_amdgcn_global_load_lds((const void*)(g + row * ld + lc * 8),
+    // uniform base + 32-bit per-lane byte offset: the saddr form of the load
+    const uint32_t off = ((uint32_t)row * ld + (uint32_t)lc * 8u) * 2u;
+    __builtin_amdgcn_global_load_lds((const void*)((const char*)g + off),
                                      (lds_ptr_t)(lds + (w * PER + j) * 512), 16, 0, 0);
   }
 }
@@ -87,6 +89,10 @@ __device__ __forceinline__ void row_to_lds(const float* __restrict__ g, float* l
 }
 
 __device__ __forceinline__ void lds_copy_wait() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// Wavefront index as a scalar (SGPR) value, so per-wave LDS destinations and
+// global bases derived from it stay uniform.
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
 
 }  // namespace mfma
 }  // namespace kf
