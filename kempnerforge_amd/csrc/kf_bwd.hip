@@ -152,20 +152,22 @@ __global__ __launch_bounds__(256) void q_prep_bwd_kernel(
   }
 }
 
-// dK/dV workgroup: 8 wavefronts on the same 128 keys.  Wavefronts 0-3 ("V
-// waves") compute S -> P -> dV^T += dO^T P; wavefronts 4-7 ("K waves") compute
-// S, dP -> dS -> dK^T += Q^T dS.  S is evaluated by both roles, which costs 25%
-// more MFMA work but lets each wavefront fit in 256 registers, so every SIMD
-// runs two wavefronts whose VALU, LDS and waits overlap the other's MFMAs.
+// dK/dV workgroup: 8 wavefronts on the same 128 keys, two roles that split the
+// four products evenly.  Wavefronts 0-3 ("P waves") compute S = Q K^T, turn it
+// into P (bf16) and accumulate dV^T += dO^T P; they hand P to the wavefront of
+// the other role that owns the same 32 keys through LDS.  Wavefronts 4-7
+// ("dS waves") compute dP = dO V^T meanwhile, then dS = P o (dP - Delta) and
+// accumulate dK^T += Q^T dS.  Each role needs only its own B operands and
+// accumulators, so two wavefronts fit per SIMD and overlap each other.
 template <int D>
 struct DkdvStage {
   bf16 q[BQ * D], o[BQ * D], qt[D * BQ], ot[D * BQ];
   float l[BQ], dl[BQ];
 };
 
-template <int D, bool KROLE>
+template <int D, bool DSROLE>
 __device__ __forceinline__ void dkdv_role(
-    DkdvStage<D>* st, const bf16* __restrict__ krot, const bf16* __restrict__ vn,
+    DkdvStage<D>* st, u32x4* sP, const bf16* __restrict__ krot, const bf16* __restrict__ vn,
     const bf16* __restrict__ qrot, const bf16* __restrict__ qt, const bf16* __restrict__ don,
     const bf16* __restrict__ dot, const float* __restrict__ lse2, const float* __restrict__ delta,
     const float* __restrict__ cos, const float* __restrict__ sin, bf16* __restrict__ dk,
@@ -173,8 +175,10 @@ __device__ __forceinline__ void dkdv_role(
     int w, int lane, float scale_log2, float scale, int causal) {
   constexpr int KS = D / 16, DT = D / 32, HALF = D / 2;
   constexpr int KR = D / 8, QR = BQ / 8;
+  constexpr int PF = 3;  // fragment reads run PF MFMAs ahead
   const int hh = lane >> 5, c32 = lane & 31;
-  const int key = k0 + 32 * (w & 3) + c32;
+  const int kw = w & 3;
+  const int key = k0 + 32 * kw + c32;
 
   const int nqt = (S + BQ - 1) / BQ;
   const int qt0 = causal ? k0 / BQ : 0;
@@ -195,22 +199,23 @@ __device__ __forceinline__ void dkdv_role(
   };
   if (total > 0) stage(0, 0);
 
-  bf16x8 kf[KS], vf[KS];
+  // this role's register-resident B operand: K for P waves, V for dS waves
+  bf16x8 bf[KS];
   {
-    const bf16* kr = krot + ((int64_t)bh * P + key) * D + 8 * hh;
+    const bf16* src = (DSROLE ? vn : krot) + ((int64_t)bh * P + key) * D + 8 * hh;
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) kf[ks] = as_bf16x8(*(const u32x4*)(kr + 16 * ks));
-    if (KROLE) {
-      const bf16* vr = vn + ((int64_t)bh * P + key) * D + 8 * hh;
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) vf[ks] = as_bf16x8(*(const u32x4*)(vr + 16 * ks));
-    }
+    for (int ks = 0; ks < KS; ++ks) bf[ks] = as_bf16x8(*(const u32x4*)(src + 16 * ks));
   }
   f32x16 acc[DT];
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
     for (int i = 0; i < 16; ++i) acc[dt][i] = 0.f;
+
+  // A-operand tiles of the two products of this role
+  auto first_tile = [](const DkdvStage<D>& S_) -> const bf16* { return DSROLE ? S_.o : S_.q; };
+  auto second_tile = [](const DkdvStage<D>& S_) -> const bf16* { return DSROLE ? S_.qt : S_.ot; };
+  u32x4* myP = sP + kw * 4 * 64 + lane;  // chunk c at myP[c * 64]
 
   lds_copy_wait();
   __syncthreads();
@@ -221,80 +226,96 @@ __device__ __forceinline__ void dkdv_role(
     const int q0 = (qt0 + it % per_head) * BQ;
     const int rel = key - q0;  // rows r of this tile see the key when r >= rel
     const bool diag = causal && q0 < k0 + BKV;
+
+    // phase 1: S (P waves) or dP (dS waves) for both 32-row halves
+    f32x16 x[2];
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) {
-      f32x16 s, dp;
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        s[i] = 0.f;
-        dp[i] = 0.f;
+      for (int i = 0; i < 16; ++i) x[mt][i] = 0.f;
+      const bf16* tA = first_tile(S_);
+      bf16x8 fa[KS];
+#pragma unroll
+      for (int ks = 0; ks < PF; ++ks) fa[ks] = lds_frag<KR>(tA, 32 * mt + c32, 2 * ks + hh);
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        __builtin_amdgcn_sched_barrier(0);
+        if (ks + PF < KS) fa[ks + PF] = lds_frag<KR>(tA, 32 * mt + c32, 2 * (ks + PF) + hh);
+        x[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[ks], bf[ks], x[mt], 0, 0, 0);
       }
-      {
-        constexpr int PF = 2;
-        bf16x8 fq[KS], fo[KS];
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    u32x4 pk[4];
+    if (!DSROLE) {
 #pragma unroll
-        for (int ks = 0; ks < PF; ++ks) {
-          fq[ks] = lds_frag<KR>(S_.q, 32 * mt + c32, 2 * ks + hh);
-          if (KROLE) fo[ks] = lds_frag<KR>(S_.o, 32 * mt + c32, 2 * ks + hh);
-        }
+      for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-          __builtin_amdgcn_sched_barrier(0);
-          if (ks + PF < KS) {
-            fq[ks + PF] = lds_frag<KR>(S_.q, 32 * mt + c32, 2 * (ks + PF) + hh);
-            if (KROLE) fo[ks + PF] = lds_frag<KR>(S_.o, 32 * mt + c32, 2 * (ks + PF) + hh);
+        for (int gq = 0; gq < 4; ++gq) {
+          const int r0 = 32 * mt + 8 * gq + 4 * hh;
+          const f32x4 l4 = *(const f32x4*)(&S_.l[r0]);
+          float v[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            float p = fast_exp2(__builtin_fmaf(x[mt][4 * gq + e], scale_log2, -l4[e]));
+            if (diag) p = (rel > r0 + e) ? 0.f : p;
+            v[e] = p;
           }
-          s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fq[ks], kf[ks], s, 0, 0, 0);
-          if (KROLE) dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fo[ks], vf[ks], dp, 0, 0, 0);
+          pk[2 * mt + (gq >> 1)][2 * (gq & 1)] = pack2(v[0], v[1]);
+          pk[2 * mt + (gq >> 1)][2 * (gq & 1) + 1] = pack2(v[2], v[3]);
         }
+#pragma unroll
+      for (int c = 0; c < 4; ++c) myP[c * 64] = pk[c];
+    }
+    __syncthreads();  // P of this tile is in LDS
+    if (DSROLE) {
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int cc = 0; cc < 2; ++cc) {
+          const u32x4 pp = myP[(2 * mt + cc) * 64];
+#pragma unroll
+          for (int half = 0; half < 2; ++half) {
+            const int gq = 2 * cc + half;
+            const int r0 = 32 * mt + 8 * gq + 4 * hh;
+            const f32x4 d4 = *(const f32x4*)(&S_.dl[r0]);
+            float v[4];
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+              const uint32_t word = pp[2 * half + e];
+              v[2 * e] = __uint_as_float(word << 16);
+              v[2 * e + 1] = __uint_as_float(word & 0xffff0000u);
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] *= x[mt][4 * gq + e] - d4[e];
+            pk[2 * mt + cc][2 * half] = pack2(v[0], v[1]);
+            pk[2 * mt + cc][2 * half + 1] = pack2(v[2], v[3]);
+          }
+        }
+    }
+    // phase 2: dV^T += dO^T P (P waves) or dK^T += Q^T dS (dS waves)
+    {
+      constexpr int NS = 4 * DT;
+      const bf16* tA = second_tile(S_);
+      bf16x8 fa[NS];
+#pragma unroll
+      for (int n = 0; n < PF; ++n)
+        fa[n] = lds_frag<QR>(tA, 32 * (n % DT) + c32, 2 * (n / DT) + hh);
+#pragma unroll
+      for (int n = 0; n < NS; ++n) {
         __builtin_amdgcn_sched_barrier(0);
+        if (n + PF < NS)
+          fa[n + PF] = lds_frag<QR>(tA, 32 * ((n + PF) % DT) + c32, 2 * ((n + PF) / DT) + hh);
+        acc[n % DT] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[n], as_bf16x8(pk[n / DT]),
+                                                             acc[n % DT], 0, 0, 0);
       }
-      u32x4 pk[2];
-#pragma unroll
-      for (int gq = 0; gq < 4; ++gq) {
-        // rows 32mt + 8gq + 4hh + (0..3): their lse (and Delta) as 16-byte reads
-        const int r0 = 32 * mt + 8 * gq + 4 * hh;
-        const f32x4 l4 = *(const f32x4*)(&S_.l[r0]);
-        float v[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          float p = fast_exp2(__builtin_fmaf(s[4 * gq + e], scale_log2, -l4[e]));
-          if (diag) p = (rel > r0 + e) ? 0.f : p;
-          v[e] = p;
-        }
-        if (KROLE) {
-          const f32x4 d4 = *(const f32x4*)(&S_.dl[r0]);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) v[e] *= dp[4 * gq + e] - d4[e];
-        }
-        pk[gq >> 1][2 * (gq & 1)] = pack2(v[0], v[1]);
-        pk[gq >> 1][2 * (gq & 1) + 1] = pack2(v[2], v[3]);
-      }
-      {
-        constexpr int NS = 2 * DT, PF = 2;
-        const bf16* tA = KROLE ? S_.qt : S_.ot;
-        bf16x8 fa[NS];
-#pragma unroll
-        for (int n = 0; n < PF; ++n)
-          fa[n] = lds_frag<QR>(tA, 32 * (n % DT) + c32, 2 * (2 * mt + n / DT) + hh);
-#pragma unroll
-        for (int n = 0; n < NS; ++n) {
-          __builtin_amdgcn_sched_barrier(0);
-          if (n + PF < NS)
-            fa[n + PF] = lds_frag<QR>(tA, 32 * ((n + PF) % DT) + c32,
-                                      2 * (2 * mt + (n + PF) / DT) + hh);
-          acc[n % DT] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[n], as_bf16x8(pk[n / DT]),
-                                                               acc[n % DT], 0, 0, 0);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-      }
+      __builtin_amdgcn_sched_barrier(0);
     }
     lds_copy_wait();
     __syncthreads();
   }
 
   if (key >= S) return;
-  if (KROLE) {
+  if (DSROLE) {
     bf16* dkr = dk + (((int64_t)b * S + key) * Hkv + g) * D;
     const float* cr = cos + (int64_t)key * HALF;
     const float* sr = sin + (int64_t)key * HALF;
@@ -333,6 +354,7 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(
     bf16* __restrict__ dv, int S, int P, int Hq, int Hkv, int n_rep, int nkb, float scale_log2,
     float scale, int causal) {
   __shared__ __attribute__((aligned(16))) DkdvStage<D> st[2];
+  __shared__ __attribute__((aligned(16))) u32x4 sP[4 * 4 * 64];  // [key group][chunk][lane]
   const int w = wave_id(), lane = threadIdx.x & 63;
   const int logical = xcd_logical_id(blockIdx.x, gridDim.x);
   const int bh = logical / nkb;
@@ -340,10 +362,10 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(
   const int b = bh / Hkv, g = bh % Hkv;
   const int k0 = kb * BKV;
   if (w >= 4)
-    dkdv_role<D, true>(st, krot, vn, qrot, qt, don, dot, lse2, delta, cos, sin, dk, dv, S, P, Hq,
+    dkdv_role<D, true>(st, sP, krot, vn, qrot, qt, don, dot, lse2, delta, cos, sin, dk, dv, S, P, Hq,
                        Hkv, n_rep, b, g, bh, k0, w, lane, scale_log2, scale, causal);
   else
-    dkdv_role<D, false>(st, krot, vn, qrot, qt, don, dot, lse2, delta, cos, sin, dk, dv, S, P, Hq,
+    dkdv_role<D, false>(st, sP, krot, vn, qrot, qt, don, dot, lse2, delta, cos, sin, dk, dv, S, P, Hq,
                         Hkv, n_rep, b, g, bh, k0, w, lane, scale_log2, scale, causal);
 }
 
