@@ -1,12 +1,13 @@
 // bf16 MFMA backward attention for gfx950 (head_dim 64 or 128).
 //
 // Four launches, no atomics (bit-deterministic):
-//  kv_prep_bwd  per KV head: K rotated (eager bf16 RoPE) [bh][P][D], its
-//               transpose with the 16-key quad swizzle [bh][D][P], V [bh][P][D].
-//  q_prep_bwd   per query head: Q rotated [bhq][P][D] and swizzled transpose
-//               [bhq][D][P]; dO [bhq][P][D] and swizzled transpose; lse*log2(e)
+//  kv_prep      (shared with the forward) per KV head: K rotated (eager bf16
+//               RoPE) and V, both [bh][P][D].
+//  q_prep_bwd   per query head: Q rotated and dO, both [bhq][P][D]; lse*log2(e)
 //               and Delta = rowsum(dO o O) [bhq][P].  P = S rounded up to 128;
 //               padded rows are zero with lse = +inf, so they contribute nothing.
+//  Transposed operands (K^T, Q^T, dO^T) are never stored: they are read from
+//  the row-major LDS tiles with ds_read_b64_tr_b16 (lds_frag_t).
 //  dkdv         workgroup = 128 keys of one KV head (4 wavefronts x 32 keys,
 //               K and V held in registers as MFMA B operands), looping over every
 //               query head of the group and every query tile of 64: the
@@ -36,61 +37,12 @@ constexpr int BQ = 64;    // queries per dK/dV tile
 __host__ __device__ constexpr int pad_len(int S) { return (S + BKV - 1) / BKV * BKV; }
 
 template <int D>
-__global__ __launch_bounds__(256) void kv_prep_bwd_kernel(
-    const bf16* __restrict__ k, const bf16* __restrict__ v, const float* __restrict__ cos,
-    const float* __restrict__ sin, bf16* __restrict__ krot, bf16* __restrict__ kt,
-    bf16* __restrict__ vn, int S, int P, int Hkv) {
-  constexpr int HALF = D / 2, CP = HALF / 8, LD = D + 8;
-  __shared__ __attribute__((aligned(16))) bf16 sk[BN * LD];
-  const int s0 = blockIdx.x * BN, bh = blockIdx.y, b = bh / Hkv, g = bh % Hkv;
-  const int tid = threadIdx.x;
-  for (int it = tid; it < BN * CP; it += 256) {
-    const int row = it / CP, c = it % CP, s = s0 + row;
-    u32x4 o1 = {0u, 0u, 0u, 0u}, o2 = {0u, 0u, 0u, 0u};
-    if (s < S) {
-      const bf16* src = k + (((int64_t)b * S + s) * Hkv + g) * D;
-      float x1[8], x2[8], r1[8], r2[8];
-      unpack8(*(const u32x4*)(src + 8 * c), x1);
-      unpack8(*(const u32x4*)(src + 8 * c + HALF), x2);
-      const float* cr = cos + (int64_t)s * HALF + 8 * c;
-      const float* sr = sin + (int64_t)s * HALF + 8 * c;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) rope_pair<bf16>(x1[j], x2[j], cr[j], sr[j], r1[j], r2[j]);
-      o1 = pack8(r1);
-      o2 = pack8(r2);
-    }
-    bf16* dst = krot + ((int64_t)bh * P + s) * D;
-    *(u32x4*)(dst + 8 * c) = o1;
-    *(u32x4*)(dst + 8 * c + HALF) = o2;
-    *(u32x4*)(&sk[row * LD + 8 * c]) = o1;
-    *(u32x4*)(&sk[row * LD + 8 * c + HALF]) = o2;
-  }
-  for (int it = tid; it < BN * (D / 8); it += 256) {
-    const int row = it / (D / 8), c = it % (D / 8), s = s0 + row;
-    u32x4 a = {0u, 0u, 0u, 0u};
-    if (s < S) a = *(const u32x4*)(v + (((int64_t)b * S + s) * Hkv + g) * D + 8 * c);
-    *(u32x4*)(vn + ((int64_t)bh * P + s) * D + 8 * c) = a;
-  }
-  __syncthreads();
-  for (int it = tid; it < D * (BN / 8); it += 256) {
-    const int d = it / (BN / 8), pc = it % (BN / 8);
-    float f[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) f[j] = (float)sk[vt_logical_key(8 * pc + j) * LD + d];
-    *(u32x4*)(kt + ((int64_t)bh * D + d) * P + s0 + 8 * pc) = pack8(f);
-  }
-}
-
-template <int D>
 __global__ __launch_bounds__(256) void q_prep_bwd_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ out, const bf16* __restrict__ dout,
     const float* __restrict__ lse, const float* __restrict__ cos, const float* __restrict__ sin,
-    bf16* __restrict__ qrot, bf16* __restrict__ qt, bf16* __restrict__ don,
-    bf16* __restrict__ dot, float* __restrict__ lse2, float* __restrict__ delta, int S, int P,
-    int Hq) {
-  constexpr int HALF = D / 2, CP = HALF / 8, LD = D + 8, TPR = D / 8;
-  __shared__ __attribute__((aligned(16))) bf16 sq[BN * LD];
-  __shared__ __attribute__((aligned(16))) bf16 sd[BN * LD];
+    bf16* __restrict__ qrot, bf16* __restrict__ don, float* __restrict__ lse2,
+    float* __restrict__ delta, int S, int P, int Hq) {
+  constexpr int HALF = D / 2, CP = HALF / 8, TPR = D / 8;
   const int s0 = blockIdx.x * BN, bhq = blockIdx.y, b = bhq / Hq, h = bhq % Hq;
   const int tid = threadIdx.x;
   for (int it = tid; it < BN * CP; it += 256) {
@@ -111,8 +63,6 @@ __global__ __launch_bounds__(256) void q_prep_bwd_kernel(
     bf16* dst = qrot + ((int64_t)bhq * P + s) * D;
     *(u32x4*)(dst + 8 * c) = o1;
     *(u32x4*)(dst + 8 * c + HALF) = o2;
-    *(u32x4*)(&sq[row * LD + 8 * c]) = o1;
-    *(u32x4*)(&sq[row * LD + 8 * c + HALF]) = o2;
   }
   // dO copy + Delta (TPR consecutive lanes own one row)
   for (int it = tid; it < BN * TPR; it += 256) {
@@ -131,24 +81,10 @@ __global__ __launch_bounds__(256) void q_prep_bwd_kernel(
 #pragma unroll
     for (int o = 1; o < TPR; o <<= 1) part += __shfl_xor(part, o, 64);
     *(u32x4*)(don + ((int64_t)bhq * P + s) * D + 8 * c) = a;
-    *(u32x4*)(&sd[row * LD + 8 * c]) = a;
     if (c == 0) {
       delta[(int64_t)bhq * P + s] = part;
       lse2[(int64_t)bhq * P + s] = s < S ? lse[(int64_t)bhq * S + s] * kLog2e : INFINITY;
     }
-  }
-  __syncthreads();
-  for (int it = tid; it < D * (BN / 8); it += 256) {
-    const int d = it / (BN / 8), pc = it % (BN / 8);
-    float fq[8], fd[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int r = vt_logical_key(8 * pc + j);
-      fq[j] = (float)sq[r * LD + d];
-      fd[j] = (float)sd[r * LD + d];
-    }
-    *(u32x4*)(qt + ((int64_t)bhq * D + d) * P + s0 + 8 * pc) = pack8(fq);
-    *(u32x4*)(dot + ((int64_t)bhq * D + d) * P + s0 + 8 * pc) = pack8(fd);
   }
 }
 
@@ -161,20 +97,20 @@ __global__ __launch_bounds__(256) void q_prep_bwd_kernel(
 // accumulators, so two wavefronts fit per SIMD and overlap each other.
 template <int D>
 struct DkdvStage {
-  bf16 q[BQ * D], o[BQ * D], qt[D * BQ], ot[D * BQ];
+  bf16 q[BQ * D], o[BQ * D];
   float l[BQ], dl[BQ];
 };
 
 template <int D, bool DSROLE>
 __device__ __forceinline__ void dkdv_role(
     DkdvStage<D>* st, u32x4* sP, const bf16* __restrict__ krot, const bf16* __restrict__ vn,
-    const bf16* __restrict__ qrot, const bf16* __restrict__ qt, const bf16* __restrict__ don,
-    const bf16* __restrict__ dot, const float* __restrict__ lse2, const float* __restrict__ delta,
+    const bf16* __restrict__ qrot, const bf16* __restrict__ don,
+    const float* __restrict__ lse2, const float* __restrict__ delta,
     const float* __restrict__ cos, const float* __restrict__ sin, bf16* __restrict__ dk,
     bf16* __restrict__ dv, int S, int P, int Hq, int Hkv, int n_rep, int b, int g, int bh, int k0,
     int w, int lane, float scale_log2, float scale, int causal) {
   constexpr int KS = D / 16, DT = D / 32, HALF = D / 2;
-  constexpr int KR = D / 8, QR = BQ / 8;
+  constexpr int KR = D / 8;
   constexpr int PF = 3;  // fragment reads run PF MFMAs ahead
   const int hh = lane >> 5, c32 = lane & 31;
   const int kw = w & 3;
@@ -192,8 +128,6 @@ __device__ __forceinline__ void dkdv_role(
     DkdvStage<D>& S_ = st[buf];
     tile_to_lds<BQ, KR, 8>(qrot + (bhq * P + q0) * D, D, S_.q, w, lane);
     tile_to_lds<BQ, KR, 8>(don + (bhq * P + q0) * D, D, S_.o, w, lane);
-    tile_to_lds<D, QR, 8>(qt + bhq * D * P + q0, P, S_.qt, w, lane);
-    tile_to_lds<D, QR, 8>(dot + bhq * D * P + q0, P, S_.ot, w, lane);
     if (w == 0) row_to_lds(lse2 + bhq * P + q0, S_.l, lane);
     if (w == 1) row_to_lds(delta + bhq * P + q0, S_.dl, lane);
   };
@@ -214,8 +148,9 @@ __device__ __forceinline__ void dkdv_role(
 
   // A-operand tiles of the two products of this role
   auto first_tile = [](const DkdvStage<D>& S_) -> const bf16* { return DSROLE ? S_.o : S_.q; };
-  auto second_tile = [](const DkdvStage<D>& S_) -> const bf16* { return DSROLE ? S_.qt : S_.ot; };
+  auto second_tile = [](const DkdvStage<D>& S_) -> const bf16* { return DSROLE ? S_.q : S_.o; };
   u32x4* myP = sP + kw * 4 * 64 + lane;  // chunk c at myP[c * 64]
+  const TrOffsets<D> tro = tr_offsets<D>(lane);
 
   lds_copy_wait();
   __syncthreads();
@@ -298,13 +233,12 @@ __device__ __forceinline__ void dkdv_role(
       const bf16* tA = second_tile(S_);
       bf16x8 fa[NS];
 #pragma unroll
-      for (int n = 0; n < PF; ++n)
-        fa[n] = lds_frag<QR>(tA, 32 * (n % DT) + c32, 2 * (n / DT) + hh);
+      for (int n = 0; n < PF; ++n) fa[n] = lds_frag_t<D>(tA, tro, n / DT, n % DT);
 #pragma unroll
       for (int n = 0; n < NS; ++n) {
         __builtin_amdgcn_sched_barrier(0);
         if (n + PF < NS)
-          fa[n + PF] = lds_frag<QR>(tA, 32 * ((n + PF) % DT) + c32, 2 * ((n + PF) / DT) + hh);
+          fa[n + PF] = lds_frag_t<D>(tA, tro, (n + PF) / DT, (n + PF) % DT);
         acc[n % DT] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[n], as_bf16x8(pk[n / DT]),
                                                              acc[n % DT], 0, 0, 0);
       }
@@ -348,8 +282,7 @@ __device__ __forceinline__ void dkdv_role(
 template <int D>
 __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(
     const bf16* __restrict__ krot, const bf16* __restrict__ vn, const bf16* __restrict__ qrot,
-    const bf16* __restrict__ qt, const bf16* __restrict__ don, const bf16* __restrict__ dot,
-    const float* __restrict__ lse2, const float* __restrict__ delta,
+    const bf16* __restrict__ don, const float* __restrict__ lse2, const float* __restrict__ delta,
     const float* __restrict__ cos, const float* __restrict__ sin, bf16* __restrict__ dk,
     bf16* __restrict__ dv, int S, int P, int Hq, int Hkv, int n_rep, int nkb, float scale_log2,
     float scale, int causal) {
@@ -362,10 +295,10 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(
   const int b = bh / Hkv, g = bh % Hkv;
   const int k0 = kb * BKV;
   if (w >= 4)
-    dkdv_role<D, true>(st, sP, krot, vn, qrot, qt, don, dot, lse2, delta, cos, sin, dk, dv, S, P, Hq,
+    dkdv_role<D, true>(st, sP, krot, vn, qrot, don, lse2, delta, cos, sin, dk, dv, S, P, Hq,
                        Hkv, n_rep, b, g, bh, k0, w, lane, scale_log2, scale, causal);
   else
-    dkdv_role<D, false>(st, sP, krot, vn, qrot, qt, don, dot, lse2, delta, cos, sin, dk, dv, S, P, Hq,
+    dkdv_role<D, false>(st, sP, krot, vn, qrot, don, lse2, delta, cos, sin, dk, dv, S, P, Hq,
                         Hkv, n_rep, b, g, bh, k0, w, lane, scale_log2, scale, causal);
 }
 
@@ -377,13 +310,12 @@ template <int D>
 __global__ __launch_bounds__(512, 1) void bwd_dq_kernel(
     const bf16* __restrict__ qrot, const bf16* __restrict__ don, const float* __restrict__ lse2,
     const float* __restrict__ delta, const bf16* __restrict__ krot, const bf16* __restrict__ vn,
-    const bf16* __restrict__ kt, const float* __restrict__ cos, const float* __restrict__ sin,
-    bf16* __restrict__ dq, int S, int P, int Hq, int Hkv, int n_rep, int bm_pos, int nqb,
+    const float* __restrict__ cos, const float* __restrict__ sin, bf16* __restrict__ dq, int S, int P, int Hq, int Hkv, int n_rep, int bm_pos, int nqb,
     float scale_log2, float scale, int causal) {
   constexpr int KS = D / 16, DT = D / 32, HALF = D / 2;
-  constexpr int KR = D / 8, TR = BN / 8;
+  constexpr int KR = D / 8;
   struct Stage {
-    bf16 k[BN * D], v[BN * D], kt[D * BN];
+    bf16 k[BN * D], v[BN * D];
   };
   __shared__ __attribute__((aligned(16))) Stage st[2];
 
@@ -397,11 +329,9 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_kernel(
   const int ntiles = (kend + BN - 1) / BN;
   const bf16* kbase = krot + (int64_t)bh * P * D;
   const bf16* vbase = vn + (int64_t)bh * P * D;
-  const bf16* tbase = kt + (int64_t)bh * D * P;
   auto stage = [&](int t, int buf) {
     tile_to_lds<BN, KR, 8>(kbase + (int64_t)t * BN * D, D, st[buf].k, w, lane);
     tile_to_lds<BN, KR, 8>(vbase + (int64_t)t * BN * D, D, st[buf].v, w, lane);
-    tile_to_lds<D, TR, 8>(tbase + t * BN, P, st[buf].kt, w, lane);
   };
   if (ntiles > 0) stage(0, 0);
 
@@ -430,6 +360,7 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_kernel(
   for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
     for (int i = 0; i < 16; ++i) acc[dt][i] = 0.f;
+  const TrOffsets<D> tro = tr_offsets<D>(lane);
 
   lds_copy_wait();
   __syncthreads();
@@ -486,17 +417,16 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_kernel(
         dsk[i >> 3][(i & 7) >> 1] = pack2(dsv[0], dsv[1]);
       }
       {
-        constexpr int NS = 2 * DT, PF = 2;
+        constexpr int NS = 2 * DT, PF = 1;
         bf16x8 fa[NS];
 #pragma unroll
         for (int n = 0; n < PF; ++n)
-          fa[n] = lds_frag<TR>(S_.kt, 32 * (n % DT) + c32, 2 * (2 * mt + n / DT) + hh);
+          fa[n] = lds_frag_t<D>(S_.k, tro, 2 * mt + n / DT, n % DT);
 #pragma unroll
         for (int n = 0; n < NS; ++n) {
           __builtin_amdgcn_sched_barrier(0);
           if (n + PF < NS)
-            fa[n + PF] = lds_frag<TR>(S_.kt, 32 * ((n + PF) % DT) + c32,
-                                      2 * (2 * mt + (n + PF) / DT) + hh);
+            fa[n + PF] = lds_frag_t<D>(S_.k, tro, 2 * mt + (n + PF) / DT, (n + PF) % DT);
           acc[n % DT] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[n], as_bf16x8(dsk[n / DT]),
                                                                acc[n % DT], 0, 0, 0);
         }
@@ -528,7 +458,7 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_kernel(
 }
 
 struct Ws {
-  bf16 *krot, *kt, *vn, *qrot, *qt, *don, *dot;
+  bf16 *krot, *vn, *qrot, *don;
   float *lse2, *delta;
 };
 
@@ -538,12 +468,9 @@ Ws carve(void* base, int B, int S, int Hq, int Hkv, int D) {
   Ws w;
   bf16* p = (bf16*)base;
   w.krot = p; p += kv;
-  w.kt = p; p += kv;
   w.vn = p; p += kv;
   w.qrot = p; p += qq;
-  w.qt = p; p += qq;
   w.don = p; p += qq;
-  w.dot = p; p += qq;
   float* f = (float*)p;
   w.lse2 = f; f += (size_t)B * Hq * P;
   w.delta = f;
@@ -556,25 +483,29 @@ int launch_bwd(const BwdArgs& a, void* workspace) {
   const Ws w = carve(workspace, a.B, a.S, a.Hq, a.Hkv, D);
   const int n_rep = a.Hq / a.Hkv;
   const float scale_log2 = a.scale * kLog2e;
-  KF_LAUNCH("kv_prep_bwd", kv_prep_bwd_kernel<D>, dim3(P / BN, a.B * a.Hkv), dim3(256), 0, a.stream,
-                     (const bf16*)a.k, (const bf16*)a.v, a.cos, a.sin, w.krot, w.kt, w.vn, a.S, P,
-                     a.Hkv);
-  KF_CHECK_LAUNCH();
+  FwdArgs fa{};
+  fa.k = a.k; fa.v = a.v; fa.cos = a.cos; fa.sin = a.sin;
+  fa.B = a.B; fa.Sq = a.S; fa.Sk = a.S; fa.Hq = a.Hq; fa.Hkv = a.Hkv; fa.D = D;
+  fa.ksb = fa.vsb = (int64_t)a.S * a.Hkv * D;
+  fa.kss = fa.vss = (int64_t)a.Hkv * D;
+  fa.ksh = fa.vsh = D;
+  fa.k_rotated = 0; fa.dtype = BF16; fa.stream = a.stream;
+  int rc = launch_kv_prep(fa, w.krot, w.vn, P);
+  if (rc) return rc;
   KF_LAUNCH("q_prep_bwd", q_prep_bwd_kernel<D>, dim3(P / BN, a.B * a.Hq), dim3(256), 0, a.stream,
-                     (const bf16*)a.q, (const bf16*)a.out, (const bf16*)a.dout, a.lse, a.cos,
-                     a.sin, w.qrot, w.qt, w.don, w.dot, w.lse2, w.delta, a.S, P, a.Hq);
+            (const bf16*)a.q, (const bf16*)a.out, (const bf16*)a.dout, a.lse, a.cos, a.sin,
+            w.qrot, w.don, w.lse2, w.delta, a.S, P, a.Hq);
   KF_CHECK_LAUNCH();
   const int nkb = P / BKV;
   KF_LAUNCH("bwd_dkdv", bwd_dkdv_kernel<D>, dim3(nkb * a.B * a.Hkv), dim3(512), 0, a.stream,
-                     w.krot, w.vn, w.qrot, w.qt, w.don, w.dot, w.lse2, w.delta, a.cos, a.sin,
-                     (bf16*)a.dk, (bf16*)a.dv, a.S, P, a.Hq, a.Hkv, n_rep, nkb, scale_log2, a.scale,
-                     a.causal);
+            w.krot, w.vn, w.qrot, w.don, w.lse2, w.delta, a.cos, a.sin, (bf16*)a.dk,
+            (bf16*)a.dv, a.S, P, a.Hq, a.Hkv, n_rep, nkb, scale_log2, a.scale, a.causal);
   KF_CHECK_LAUNCH();
   const int bm_pos = DQ_ROWS / n_rep;
   const int nqb = (a.S + bm_pos - 1) / bm_pos;
   KF_LAUNCH("bwd_dq", bwd_dq_kernel<D>, dim3(nqb * a.B * a.Hkv), dim3(512), 0, a.stream, w.qrot,
-                     w.don, w.lse2, w.delta, w.krot, w.vn, w.kt, a.cos, a.sin, (bf16*)a.dq, a.S, P,
-                     a.Hq, a.Hkv, n_rep, bm_pos, nqb, scale_log2, a.scale, a.causal);
+            w.don, w.lse2, w.delta, w.krot, w.vn, a.cos, a.sin, (bf16*)a.dq, a.S, P, a.Hq, a.Hkv,
+            n_rep, bm_pos, nqb, scale_log2, a.scale, a.causal);
   KF_CHECK_LAUNCH();
   return KF_OK;
 }
@@ -592,7 +523,7 @@ bool bwd_mfma_supported(const BwdArgs& a) {
 
 size_t bwd_mfma_workspace(int B, int S, int Hq, int Hkv, int D) {
   const size_t P = (size_t)pad_len(S);
-  return (3 * (size_t)B * Hkv + 4 * (size_t)B * Hq) * P * D * sizeof(uint16_t) +
+  return (2 * (size_t)B * Hkv + 2 * (size_t)B * Hq) * P * D * sizeof(uint16_t) +
          2 * (size_t)B * Hq * P * sizeof(float);
 }
 

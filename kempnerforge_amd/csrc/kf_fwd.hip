@@ -2,10 +2,8 @@
 //
 // Two kernels:
 //  kv_prep   stages one KV head's keys and values in the layout the MFMA loop
-//            reads: K rotated by RoPE (eager bf16 rounding) as [bh][Skp][D], and
-//            V transposed as [bh][D][Skp] with a quad swizzle inside every 16
-//            keys (see vt_logical_key) so that each lane's B-operand slots of
-//            the P·V product are one 16-byte read.  Keys >= Sk are zero.
+//            reads: K rotated by RoPE (eager bf16 rounding) and V, both
+//            [bh][Skp][D] with keys >= Sk zeroed.  The backward uses it too.
 //  fwd_mfma  flash forward.  One workgroup = 4 wavefronts = 128 "rows", where
 //            a row is (query head of the KV group, position): every K/V tile in
 //            LDS is shared by all n_rep query heads of the group.  Each wave
@@ -13,7 +11,8 @@
 //            v_mfma_f32_32x32x16_bf16, so a lane holds one query's 32 scores of
 //            a 64-key tile: the online-softmax max/sum is lane-local plus one
 //            exchange with lane^32.  O^T = V^T·P^T accumulates in 16 fp32
-//            registers per 32-d tile.  RoPE of q happens at the Q load.
+//            registers per 32-d tile; its V^T operand comes from the row-major
+//            V tile through LDS transpose reads.  RoPE of q happens at the Q load.
 //
 // MFMA 32x32x16 operand layout used (lane l, h = l/32, slot j = 0..7):
 //   A[m][k]: m = l%32, k = 8h + j     B[k][n]: n = l%32, k = 8h + j
@@ -33,13 +32,11 @@ using namespace mfma;
 template <int D>
 __global__ __launch_bounds__(256) void kv_prep_kernel(
     const bf16* __restrict__ k, const bf16* __restrict__ v, const float* __restrict__ cos,
-    const float* __restrict__ sin, bf16* __restrict__ krot, bf16* __restrict__ vt, int Sk,
+    const float* __restrict__ sin, bf16* __restrict__ krot, bf16* __restrict__ vn, int Sk,
     int Skp, int Hkv, int64_t ksb, int64_t kss, int64_t ksh, int64_t vsb, int64_t vss,
     int64_t vsh, int k_rotated) {
   constexpr int HALF = D / 2;
   constexpr int CP = HALF / 8;
-  constexpr int VLD = D + 8;
-  __shared__ __attribute__((aligned(16))) bf16 sv[BN * VLD];
   const int s0 = blockIdx.x * BN;
   const int bh = blockIdx.y;
   const int b = bh / Hkv, g = bh % Hkv;
@@ -72,21 +69,12 @@ __global__ __launch_bounds__(256) void kv_prep_kernel(
     *(u32x4*)(dst + 8 * c) = o1;
     *(u32x4*)(dst + 8 * c + HALF) = o2;
   }
-
   for (int it = tid; it < BN * (D / 8); it += 256) {
     const int key = it / (D / 8), c = it % (D / 8);
     const int s = s0 + key;
     u32x4 a = {0u, 0u, 0u, 0u};
     if (s < Sk) a = *(const u32x4*)(v + b * vsb + (int64_t)s * vss + g * vsh + 8 * c);
-    *(u32x4*)(&sv[key * VLD + 8 * c]) = a;
-  }
-  __syncthreads();
-  for (int it = tid; it < D * (BN / 8); it += 256) {
-    const int d = it / (BN / 8), pc = it % (BN / 8);
-    float f[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) f[j] = (float)sv[vt_logical_key(8 * pc + j) * VLD + d];
-    *(u32x4*)(vt + ((int64_t)bh * D + d) * Skp + s0 + 8 * pc) = pack8(f);
+    *(u32x4*)(vn + ((int64_t)bh * Skp + s) * D + 8 * c) = a;
   }
 }
 
@@ -121,13 +109,13 @@ __device__ __forceinline__ void load_q_frag(const bf16* __restrict__ q,
 template <int D>
 __global__ __launch_bounds__(256, 2) void fwd_mfma_kernel(
     const bf16* __restrict__ q, const float* __restrict__ cos, const float* __restrict__ sin,
-    const bf16* __restrict__ krot, const bf16* __restrict__ vt, bf16* __restrict__ out,
+    const bf16* __restrict__ krot, const bf16* __restrict__ vn, bf16* __restrict__ out,
     float* __restrict__ lse, int Sq, int Sk, int Skp, int Hq, int Hkv, int n_rep, int bm_pos,
     int nqb, float scale_log2, int causal) {
   constexpr int KS = D / 16, DT = D / 32;
-  constexpr int KR = D / 8, VR = BN / 8;  // 16-byte chunks per K row / per V^T row
+  constexpr int KR = D / 8;  // 16-byte chunks per K / V row
   __shared__ __attribute__((aligned(16))) bf16 sK[2][BN * D];
-  __shared__ __attribute__((aligned(16))) bf16 sV[2][D * BN];
+  __shared__ __attribute__((aligned(16))) bf16 sV[2][BN * D];
 
   const int tid = threadIdx.x, w = wave_id(), lane = tid & 63, hh = lane >> 5, c32 = lane & 31;
   const int logical = xcd_logical_id(blockIdx.x, gridDim.x);
@@ -137,15 +125,16 @@ __global__ __launch_bounds__(256, 2) void fwd_mfma_kernel(
   const int kend = causal ? min(Sk, min(ri.p0 + bm_pos, Sq)) : Sk;
   const int ntiles = (kend + BN - 1) / BN;
   const bf16* kbase = krot + (int64_t)bh * Skp * D;
-  const bf16* vbase = vt + (int64_t)bh * D * Skp;
+  const bf16* vbase = vn + (int64_t)bh * Skp * D;
   auto stage = [&](int t, int buf) {
     tile_to_lds<BN, KR>(kbase + (int64_t)t * BN * D, D, sK[buf], w, lane);
-    tile_to_lds<D, VR>(vbase + t * BN, Skp, sV[buf], w, lane);
+    tile_to_lds<BN, KR>(vbase + (int64_t)t * BN * D, D, sV[buf], w, lane);
   };
   if (ntiles > 0) stage(0, 0);
 
   bf16x8 qf[KS];
   load_q_frag<D>(q, cos, sin, ri, Sq, Hq, hh, qf);
+  const TrOffsets<D> tro = tr_offsets<D>(lane);
 
   float m = -INFINITY, lsum = 0.f;
   f32x16 acc[DT];
@@ -226,7 +215,7 @@ __global__ __launch_bounds__(256, 2) void fwd_mfma_kernel(
       const bf16x8 pb = as_bf16x8(pk[c]);
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
-        const bf16x8 a = lds_frag<VR>(tV, 32 * dt + c32, 2 * c + hh);
+        const bf16x8 a = lds_frag_t<D>(tV, tro, c, dt);
         acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb, acc[dt], 0, 0, 0);
       }
     }
@@ -361,15 +350,17 @@ size_t fwd_mfma_workspace(int B, int Sk, int Hkv, int D) {
   return 2 * (size_t)B * Hkv * Skp * D * sizeof(uint16_t);
 }
 
-static int launch_kv_prep(const FwdArgs& a, bf16* krot, bf16* vt, int Skp) {
+int launch_kv_prep(const FwdArgs& a, void* krot_, void* vn_, int Skp) {
+  bf16* krot = (bf16*)krot_;
+  bf16* vn = (bf16*)vn_;
   dim3 grid(Skp / BN, a.B * a.Hkv);
   if (a.D == 128)
     KF_LAUNCH("kv_prep", kv_prep_kernel<128>, grid, dim3(256), 0, a.stream, (const bf16*)a.k,
-                       (const bf16*)a.v, a.cos, a.sin, krot, vt, a.Sk, Skp, a.Hkv, a.ksb, a.kss,
+                       (const bf16*)a.v, a.cos, a.sin, krot, vn, a.Sk, Skp, a.Hkv, a.ksb, a.kss,
                        a.ksh, a.vsb, a.vss, a.vsh, a.k_rotated);
   else
     KF_LAUNCH("kv_prep", kv_prep_kernel<64>, grid, dim3(256), 0, a.stream, (const bf16*)a.k,
-                       (const bf16*)a.v, a.cos, a.sin, krot, vt, a.Sk, Skp, a.Hkv, a.ksb, a.kss,
+                       (const bf16*)a.v, a.cos, a.sin, krot, vn, a.Sk, Skp, a.Hkv, a.ksb, a.kss,
                        a.ksh, a.vsb, a.vss, a.vsh, a.k_rotated);
   KF_CHECK_LAUNCH();
   return KF_OK;
@@ -378,8 +369,8 @@ static int launch_kv_prep(const FwdArgs& a, bf16* krot, bf16* vt, int Skp) {
 int fwd_mfma(const FwdArgs& a, void* workspace) {
   const int Skp = (a.Sk + BN - 1) / BN * BN;
   bf16* krot = (bf16*)workspace;
-  bf16* vt = krot + (size_t)a.B * a.Hkv * Skp * a.D;
-  int rc = launch_kv_prep(a, krot, vt, Skp);
+  bf16* vn = krot + (size_t)a.B * a.Hkv * Skp * a.D;
+  int rc = launch_kv_prep(a, krot, vn, Skp);
   if (rc) return rc;
   const int n_rep = a.Hq / a.Hkv;
   const int bm_pos = pick_bm_pos(n_rep);
@@ -389,11 +380,11 @@ int fwd_mfma(const FwdArgs& a, void* workspace) {
   const float scale_log2 = a.scale * kLog2e;
   if (a.D == 128)
     KF_LAUNCH("fwd_mfma", fwd_mfma_kernel<128>, dim3((unsigned)nblk), dim3(256), 0, a.stream,
-                       (const bf16*)a.q, a.cos, a.sin, krot, vt, (bf16*)a.out, a.lse, a.Sq, a.Sk,
+                       (const bf16*)a.q, a.cos, a.sin, krot, vn, (bf16*)a.out, a.lse, a.Sq, a.Sk,
                        Skp, a.Hq, a.Hkv, n_rep, bm_pos, nqb, scale_log2, a.causal);
   else
     KF_LAUNCH("fwd_mfma", fwd_mfma_kernel<64>, dim3((unsigned)nblk), dim3(256), 0, a.stream,
-                       (const bf16*)a.q, a.cos, a.sin, krot, vt, (bf16*)a.out, a.lse, a.Sq, a.Sk,
+                       (const bf16*)a.q, a.cos, a.sin, krot, vn, (bf16*)a.out, a.lse, a.Sq, a.Sk,
                        Skp, a.Hq, a.Hkv, n_rep, bm_pos, nqb, scale_log2, a.causal);
   KF_CHECK_LAUNCH();
   return KF_OK;

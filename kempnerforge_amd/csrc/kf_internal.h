@@ -6,7 +6,7 @@
 #include <stddef.h>
 #include <stdint.h>
 
-#include "../../include/kf_attn.h"
+#include "kf_attn.h"
 
 namespace kf {
 
@@ -47,6 +47,8 @@ int capture_probs_generic(const FwdArgs& a, const float* lse, float* probs);
 
 // bf16 MFMA kernels (kf_fwd.hip, kf_bwd.hip, kf_capture.hip)
 bool fwd_mfma_supported(const FwdArgs& a);
+// Rotated K and zero-padded V, both [B*Hkv][Skp][D] bf16 (Skp a multiple of 64).
+int launch_kv_prep(const FwdArgs& a, void* krot, void* vn, int Skp);
 size_t fwd_mfma_workspace(int B, int Sk, int Hkv, int D);
 int fwd_mfma(const FwdArgs& a, void* workspace);
 int capture_probs_mfma(const FwdArgs& a, const float* lse, float* probs, void* workspace);

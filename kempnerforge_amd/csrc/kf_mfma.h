@@ -9,14 +9,6 @@ namespace mfma {
 constexpr int BN = 64;     // keys per tile
 constexpr int ROWS = 128;  // (query head, position) rows per workgroup
 
-// Physical slot p (0..15) inside a 16-key group of the transposed V holds this
-// logical key: lane half h = p/8, slot j = p%8 of the P^T B-operand carries key
-// (j<4 ? 4h+j : 8+4h+j-4) because of the 32x32 C layout of S^T.
-__device__ __forceinline__ int vt_logical_key(int p) {
-  const int h = (p & 15) >> 3, j = p & 7;
-  return (p & ~15) + (j < 4 ? 4 * h + j : 8 + 4 * h + (j - 4));
-}
-
 __device__ __forceinline__ bf16x8 as_bf16x8(const u32x4& u) { return __builtin_bit_cast(bf16x8, u); }
 
 // Block-id remap so that the workgroups one XCD runs are a contiguous range of
@@ -51,12 +43,21 @@ __device__ __forceinline__ RowInfo row_info(int logical, int nqb, int Hkv, int n
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
-// LDS tiles are stored unpadded, [rows][R] 16-byte chunks, with chunk c of row
-// r at position c ^ (r % R): the 32 (or 8, 16) consecutive rows a fragment read
-// touches then land in distinct bank groups.  R is 8 or 16.
+// LDS tiles are stored unpadded, [rows][R] 16-byte chunks (R = 8 or 16), with
+// chunk c of row r at position c ^ swz<R>(r).  swz spreads the rows of a
+// fragment read over distinct 16-byte bank groups for both access patterns the
+// kernels use: ds_read_b128 with one row per lane (measured at the LDS peak of
+// ~128 B/clk/CU on MI355X) and ds_read_b64_tr_b16 with 4 rows x 32 bytes per
+// 16-lane group (~100 B/clk/CU; the plain c ^ (r % R) swizzle reaches only ~58
+// there).
+template <int R>
+__device__ __forceinline__ int swz(int row) {
+  return R == 16 ? (((row & 7) << 1) | ((row >> 3) & 1)) : (((row & 3) << 1) | ((row >> 2) & 1));
+}
+
 template <int R>
 __device__ __forceinline__ const bf16x8& lds_frag(const bf16* tile, int row, int chunk) {
-  return *(const bf16x8*)(tile + (row * R + (chunk ^ (row % R))) * 8);
+  return *(const bf16x8*)(tile + (row * R + (chunk ^ swz<R>(row))) * 8);
 }
 
 // Copy a [ROWS_T][R chunks] bf16 tile whose rows start `ld` elements apart in
@@ -75,12 +76,79 @@ __device__ __forceinline__ void tile_to_lds(const bf16* __restrict__ g, uint32_t
   for (int j = 0; j < PER; ++j) {
     const int L = (w * PER + j) * 64 + lane;
     const int row = L / R, pc = L % R;
-    const int lc = pc ^ (row % R);
+    const int lc = pc ^ swz<R>(row);
     // uniform base + 32-bit per-lane byte offset: the saddr form of the load
     const uint32_t off = ((uint32_t)row * ld + (uint32_t)lc * 8u) * 2u;
     __builtin_amdgcn_global_load_lds((const void*)((const char*)g + off),
                                      (lds_ptr_t)(lds + (w * PER + j) * 512), 16, 0, 0);
   }
+}
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4* lds_s16x4_ptr;
+
+// A-operand fragment of a transposed product, read from a row-major swizzled
+// [rows][R chunks] LDS tile with two ds_read_b64_tr_b16.
+//
+// ds_read_b64_tr_b16 works on groups of 16 lanes: address-lane a of a group
+// fetches 4 contiguous 16-bit elements, and result-lane i receives element
+// (i % 4) of the chunk fetched by address-lane 4e + i/4, for e = 0..3 (the 16
+// lanes' 64 elements read as a 4x16 block, one column per lane).  Address-lane
+// a = 4e + k of group G therefore fetches row r0 + 4h + e (h = lane / 32),
+// columns c0 + 16 (G % 2) + 4k .. +3, and result-lane l ends up holding column
+// c0 + l % 32 of rows r0 + 4h + e: exactly slots j = 0..3 of the fragment whose
+// slot (h, j) carries row r0 + (j < 4 ? 4h + j : 8 + 4h + j - 4).  The second
+// read (rows + 8) fills slots 4..7.  That is the slot order of the P^T / dS
+// B operands built from the 32x32 C layout, so the products line up.
+// Per-lane byte offsets for lds_frag_t on a [rows][D] tile: fragment (c, dt)
+// covers rows 16c..16c+15 and columns 32dt..32dt+31.  Rows are 16-aligned, so
+// the swizzle term does not depend on c and each lane needs only one
+// offset per (dt, first/second read); c adds a compile-time 16-row step
+// (swz depends on row % 16 only).
+template <int D>
+struct TrOffsets {
+  uint32_t o[D / 32][2];
+};
+
+template <int D>
+__device__ __forceinline__ TrOffsets<D> tr_offsets(int lane) {
+  constexpr int R = D / 8;
+  const int G = lane >> 4, a = lane & 15;
+  const int rowA = 4 * (lane >> 5) + (a >> 2), rowB = rowA + 8;
+  const int x = 2 * (G & 1) + ((a & 3) >> 1);  // 16-byte chunk inside the 32-column block
+  const int within = 4 * (a & 1);              // element inside the chunk
+  TrOffsets<D> t;
+#pragma unroll
+  for (int dt = 0; dt < D / 32; ++dt) {
+    const int ch = 4 * dt + x;
+    t.o[dt][0] = (uint32_t)(((rowA * R + (ch ^ swz<R>(rowA))) * 8 + within) * 2);
+    t.o[dt][1] = (uint32_t)(((rowB * R + (ch ^ swz<R>(rowB))) * 8 + within) * 2);
+  }
+  return t;
+}
+
+// A-operand fragment of a transposed product, read from a row-major swizzled
+// [rows][D] LDS tile with two ds_read_b64_tr_b16.
+//
+// ds_read_b64_tr_b16 works on groups of 16 lanes: address-lane a of a group
+// fetches 4 contiguous 16-bit elements, and result-lane i receives element
+// (i % 4) of the chunk fetched by address-lane 4e + i/4, for e = 0..3 (the 16
+// lanes' 64 elements read as a 4x16 block, one column per lane).  Address-lane
+// a = 4e + k of group G therefore fetches row 16c + 4h + e (h = lane / 32),
+// columns 32dt + 16 (G % 2) + 4k .. +3, and result-lane l ends up holding column
+// 32dt + l % 32 of rows 16c + 4h + e: exactly slots j = 0..3 of the fragment
+// whose slot (h, j) carries row 16c + (j < 4 ? 4h + j : 8 + 4h + j - 4).  The
+// second read (rows + 8) fills slots 4..7.  That is the slot order of the P^T /
+// dS B operands built from the 32x32 C layout, so the products line up.
+template <int D>
+__device__ __forceinline__ bf16x8 lds_frag_t(const bf16* tile, const TrOffsets<D>& t, int c,
+                                             int dt) {
+  const char* base = (const char*)tile + c * 16 * D * 2;
+  const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)(base + t.o[dt][0]));
+  const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)(base + t.o[dt][1]));
+  typedef short s16x8 __attribute__((ext_vector_type(8)));
+  const s16x8 v = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+  return __builtin_bit_cast(bf16x8, v);
 }
 
 // 64 consecutive floats (one per lane of one wavefront) straight into LDS.
