@@ -1,25 +1,27 @@
 // KV-cache decode (one new token per sequence) and cache append.
 //
-// decode = three launches on the caller's stream:
-//  1. append   rotate k_new at position lens[b] (eager RoPE rounding) and write
-//              it and v_new into the caches (the reference's KVCache.update).
-//  2. split    split-K attention: workgroup (split, b, kv head) streams CH keys
+// decode = two launches on the caller's stream:
+//  1. split    split-K attention: workgroup (split, b, kv head) streams CH keys
 //              of one KV head once and serves all n_rep query heads of the
 //              group from that single read (the reference expands the cache
 //              n_rep times first).  D/8 threads share a key row, each loading
 //              16 contiguous bytes, so a pass reads whole rows coalesced.
-//              Writes partial (o, m, l) per (b, hq, split) in float32.
-//  3. merge    one workgroup per (b, hq) rescales and sums the partials.
+//              Writes partial (o, m, l) per (b, hq, split) in float32.  The
+//              split holding position lens[b] rotates k_new (eager RoPE
+//              rounding) and writes it and v_new into the caches (the
+//              reference's KVCache.update) instead of reading that row.
+//  2. merge    one wavefront per (b, hq) rescales and sums the partials.
 // Shapes outside the fast path (dtype other than bf16, D not in {64, 128}, or
-// n_rep not in {1, 2, 4, 8}) use decode_generic: one wavefront per (b, hq).
+// n_rep > 32) use decode_generic: one wavefront per (b, hq).
 #include "kf_common.h"
 #include "kf_internal.h"
+#include "kf_mfma.h"
 
 namespace kf {
 
 namespace {
 
-constexpr int CH = 256;  // keys per split
+constexpr int CH = 512;  // keys per split
 
 // A device-side cache length is usable when the new token's position fits the
 // grid (len + 1 <= max_len <= Smax) and its RoPE row lies inside the table.
@@ -68,153 +70,306 @@ __global__ __launch_bounds__(256) void append_kernel(const T* __restrict__ k_new
   vc[dst + d + half] = v_new[src + d + half];
 }
 
-template <int D, int NREP>
-__global__ __launch_bounds__(256) void decode_split_kernel(
-    const bf16* __restrict__ q_new, const float* __restrict__ cos, const float* __restrict__ sin,
-    int64_t row_offset, int64_t rope_rows, int max_len, const bf16* __restrict__ kc,
-    const bf16* __restrict__ vc, const int32_t* __restrict__ lens, float* __restrict__ opart,
-    float* __restrict__ mpart, float* __restrict__ lpart, int Hq, int Hkv, int Smax, int nsplit,
+// Split-K decode on MFMA.  Workgroup = (split of CH keys, b, KV head), 4
+// independent wavefronts of NCH chunks x KC keys each.  Per chunk:
+//   S^T = K q^T   v_mfma_f32_32x32x16_bf16, the KV group's n_rep query heads
+//                 as the B-operand columns (zero-padded to 32), so a lane owns
+//                 one head and the online softmax is lane-local; K rows go
+//                 from HBM straight into A-operand registers.
+//   O^T += V^T P^T  V rows staged in LDS by direct global->LDS loads and read
+//                 transposed (ds_read_b64_tr_b16).
+// Loads run one chunk ahead (K registers and V LDS buffers double-buffered),
+// so every wavefront keeps a chunk in flight while it computes the previous.
+// Chunks past the split's end load a clamped row (L2 hits) and are not
+// computed, which keeps the memory-counter accounting static.  The
+// wavefronts' (m, l, o) are merged in LDS into one partial per
+// (b, head, split).  The wavefront owning position lens[b] rotates k_new,
+// writes k and v into the caches and uses them in place of that row.
+// 16-byte global load issued from inline asm, so that the compiler's
+// memory-counter bookkeeping does not see it: the caller waits with
+// wait_vm<N>() and passes the destination through it before any use.  (The
+// compiler cannot pipeline register loads with the direct-to-LDS loads in
+// flight: it answers every register dependency with vmcnt(0) while one is
+// pending.)
+template <int OFF>
+__device__ __forceinline__ void gload16(u32x4& r, uint32_t voff, const void* base) {
+  asm volatile("global_load_dwordx4 %0, %1, %2 offset:%3"
+               : "=v"(r)
+               : "v"(voff), "s"(base), "n"(OFF)
+               : "memory");
+}
+template <int N, int I = 0>
+__device__ __forceinline__ void gload16_row(u32x4* r, uint32_t voff, const void* base) {
+  if constexpr (I < N) {
+    gload16<32 * I>(r[I], voff, base);
+    gload16_row<N, I + 1>(r, voff, base);
+  }
+}
+// Direct global->LDS 16-byte load (LDS destination M0 + 16 * lane), also
+// issued from inline asm: the compiler's own tracking of these would make
+// every LDS read that may alias a pending one wait for all of them.
+__device__ __forceinline__ void dma16(uint32_t lds_addr, uint32_t voff, const void* base) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
+               :
+               : "s"(lds_addr), "v"(voff), "s"(base)
+               : "memory", "m0");
+}
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+// s_waitcnt vmcnt(N), then the registers in r[0..n) count as written here
+template <int N, int n>
+__device__ __forceinline__ void wait_vm(u32x4* r) {
+  asm volatile("s_waitcnt vmcnt(%1)" : "+v"(r[0]) : "n"(N) : "memory");
+#pragma unroll
+  for (int i = 1; i < n; ++i) asm volatile("" : "+v"(r[i])::"memory");
+}
+
+constexpr int DEC_WAVES = 4;
+constexpr int KC = 32;                    // keys per chunk
+constexpr int NCH = CH / (DEC_WAVES * KC);  // chunks per wavefront
+
+template <int D>
+__global__ __launch_bounds__(256, 2) void decode_split_kernel(
+    const bf16* __restrict__ q_new, const bf16* __restrict__ k_new,
+    const bf16* __restrict__ v_new, const float* __restrict__ cos, const float* __restrict__ sin,
+    int64_t row_offset, int64_t rope_rows, int max_len, bf16* kc, bf16* vc,
+    const int32_t* __restrict__ lens, float* __restrict__ opart, float* __restrict__ mpart,
+    float* __restrict__ lpart, int Hq, int Hkv, int Smax, int nsplit, int n_rep,
     float scale_log2) {
-  constexpr int TPR = D / 8;        // threads per key row (16 bytes each)
-  constexpr int RPP = 256 / TPR;    // rows per pass
-  constexpr int NP = CH / RPP;      // passes per split
-  constexpr int HALF = D / 2;
-  __shared__ float sq[NREP][D];
-  __shared__ float sp[NREP][CH];
-  __shared__ float so[4][NREP * D];  // per-wavefront partial o
-  __shared__ float sm[NREP], sl[NREP];
+  using namespace mfma;
+  constexpr int KS = D / 16, DT = D / 32, KR = D / 8, HALF = D / 2;
+  constexpr int WKEYS = NCH * KC;      // keys per wavefront
+  constexpr int VI = KC * KR / 64;     // LDS copies per V chunk
+  constexpr int PER_CHUNK = KS + VI;   // vector-memory instructions per chunk
+  static_assert(PER_CHUNK < 64, "vmcnt range");
+  __shared__ __attribute__((aligned(16))) bf16 sV[DEC_WAVES][2][KC * D];
+  __shared__ __attribute__((aligned(16))) bf16 sNew[2][D];
+  __shared__ float sML[DEC_WAVES][2][32];
+  static_assert(sizeof(sV) >= DEC_WAVES * 32 * D * sizeof(float), "merge buffer");
 
   const int sp_idx = blockIdx.x;
   const int bg = blockIdx.y;
   const int b = bg / Hkv, g = bg % Hkv;
   if (!decode_len_ok(lens[b], max_len, row_offset, rope_rows)) return;
   const int L = lens[b] + 1;
+  const int newrow = L - 1;  // the token being decoded
   const int k0 = sp_idx * CH;
   if (k0 >= L) return;
   const int k1 = min(k0 + CH, L);
-  const int tid = threadIdx.x;
-  const int c = tid % TPR, rg = tid / TPR;
-  const int w = tid >> 6, lane = tid & 63;
+  const int w = wave_id(), lane = threadIdx.x & 63, hh = lane >> 5, c32 = lane & 31;
+  const int64_t trow = (int64_t)newrow - row_offset;
+  const int kw0 = k0 + w * WKEYS;                                   // first key of the wavefront
+  const int nvc = min(max((k1 - kw0 + KC - 1) / KC, 0), NCH);       // chunks holding keys
+  const bool own_new = newrow >= kw0 && newrow < kw0 + WKEYS;
 
-  const bf16* kb = kc + ((int64_t)b * Hkv + g) * Smax * D;
-  const bf16* vb = vc + ((int64_t)b * Hkv + g) * Smax * D;
-  // issue the whole split's K reads first (NP x 16 bytes per thread in flight)
-  u32x4 kr[NP];
-#pragma unroll
-  for (int p = 0; p < NP; ++p) {
-    const int row = k0 + p * RPP + rg;
-    kr[p] = row < k1 ? *(const u32x4*)(kb + (int64_t)row * D + 8 * c) : u32x4{0u, 0u, 0u, 0u};
-  }
+  bf16* kb = kc + ((int64_t)b * Hkv + g) * Smax * D;
+  bf16* vb = vc + ((int64_t)b * Hkv + g) * Smax * D;
+  const float* cr = cos + trow * HALF;
+  const float* sr = sin + trow * HALF;
 
-  // rotated queries of the group, float32 in LDS
-  const int64_t trow = (int64_t)(L - 1) - row_offset;
-  for (int it = tid; it < NREP * HALF; it += 256) {
-    const int hr = it / HALF, d = it % HALF;
-    const bf16* qr = q_new + ((int64_t)b * Hq + g * NREP + hr) * D;
-    float r1, r2;
-    rope_pair<bf16>((float)qr[d], (float)qr[d + HALF], cos[trow * HALF + d],
-                    sin[trow * HALF + d], r1, r2);
-    sq[hr][d] = r1;
-    sq[hr][d + HALF] = r2;
+  // the new token: rotated k and v into the caches and into sNew
+  if (own_new) {
+    const bf16* kn = k_new + ((int64_t)b * Hkv + g) * D;
+    const bf16* vn = v_new + ((int64_t)b * Hkv + g) * D;
+    if (lane < HALF / 8) {
+      const int d0 = 8 * lane;
+      float x1[8], x2[8], r1[8], r2[8];
+      unpack8(*(const u32x4*)(kn + d0), x1);
+      unpack8(*(const u32x4*)(kn + d0 + HALF), x2);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) rope_pair<bf16>(x1[j], x2[j], cr[d0 + j], sr[d0 + j], r1[j], r2[j]);
+      const u32x4 a1 = pack8(r1), a2 = pack8(r2);
+      *(u32x4*)(sNew[0] + d0) = a1;
+      *(u32x4*)(sNew[0] + d0 + HALF) = a2;
+      *(u32x4*)(kb + (int64_t)newrow * D + d0) = a1;
+      *(u32x4*)(kb + (int64_t)newrow * D + d0 + HALF) = a2;
+    } else if (lane >= 32 && lane < 32 + KR) {
+      const int d0 = 8 * (lane - 32);
+      const u32x4 x = *(const u32x4*)(vn + d0);
+      *(u32x4*)(sNew[1] + d0) = x;
+      *(u32x4*)(vb + (int64_t)newrow * D + d0) = x;
+    }
   }
-  __syncthreads();
-  float qreg[NREP][8];
+  // query fragment (B operand): column = head of the group, slots = d
+  u32x4 qf[KS];
+  if (c32 < n_rep) {
+    const bf16* qr = q_new + ((int64_t)b * Hq + g * n_rep + c32) * D;
 #pragma unroll
-  for (int hr = 0; hr < NREP; ++hr)
+    for (int ks = 0; ks < KS / 2; ++ks) {
+      const int d0 = 16 * ks + 8 * hh;
+      float x1[8], x2[8], r1[8], r2[8];
+      unpack8(*(const u32x4*)(qr + d0), x1);
+      unpack8(*(const u32x4*)(qr + d0 + HALF), x2);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) qreg[hr][e] = sq[hr][8 * c + e];
+      for (int j = 0; j < 8; ++j) rope_pair<bf16>(x1[j], x2[j], cr[d0 + j], sr[d0 + j], r1[j], r2[j]);
+      qf[ks] = pack8(r1);
+      qf[ks + KS / 2] = pack8(r2);
+    }
+  } else {
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) qf[ks] = u32x4{0u, 0u, 0u, 0u};
+  }
+  // finish every tracked load's consumer before the first direct-to-LDS load
+  // is issued (see gload16)
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) asm volatile("" : "+v"(qf[ks])::"memory");
 
+  // chunk loads: K rows into registers, V rows into this wavefront's LDS buffer
+  u32x4 kreg[2][KS];
+  auto issue = [&](int c, u32x4 (&kr)[KS], bf16* tV) {
+    const int r0 = kw0 + c * KC;
+    const int key = min(r0 + c32, k1 - 1);
+    gload16_row<KS>(kr, (uint32_t)(key * D + 8 * hh) * 2u, kb);
+    const uint32_t tva = lds_addr(tV);
 #pragma unroll
-  for (int p = 0; p < NP; ++p) {
-    const int row = k0 + p * RPP + rg;
-    float kf[8];
-    unpack8(kr[p], kf);
-    float part[NREP];
-#pragma unroll
-    for (int hr = 0; hr < NREP; ++hr) {
-      float s = 0.f;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) s += qreg[hr][e] * kf[e];
-      part[hr] = s;
+    for (int j = 0; j < VI; ++j) {
+      const int Lc = j * 64 + lane;
+      const int row = Lc / KR, pc = Lc % KR;
+      const int lc = pc ^ swz<KR>(row);
+      const uint32_t grow = (uint32_t)min(r0 + row, k1 - 1);
+      dma16(tva + j * 1024, (grow * D + (uint32_t)lc * 8u) * 2u, vb);
     }
+  };
+
+  const TrOffsets<D> tro = tr_offsets<D>(lane);
+  float m = -INFINITY, lsum = 0.f;
+  f32x16 acc[DT];
 #pragma unroll
-    for (int o = 1; o < TPR; o <<= 1)
+  for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-      for (int hr = 0; hr < NREP; ++hr) part[hr] += __shfl_xor(part[hr], o, 64);
-    if (c == 0 && row < k1) {
+    for (int i = 0; i < 16; ++i) acc[dt][i] = 0.f;
+
+  issue(0, kreg[0], sV[w][0]);
 #pragma unroll
-      for (int hr = 0; hr < NREP; ++hr) sp[hr][row - k0] = part[hr] * scale_log2;
+  for (int c = 0; c < NCH; ++c) {
+    if (c + 1 < NCH) issue(c + 1, kreg[(c + 1) & 1], sV[w][(c + 1) & 1]);
+    // K of chunk c has landed once only V(c) and the next chunk are pending;
+    // waited on every path, so the registers stay owned until they land
+    if (c + 1 < NCH)
+      wait_vm<VI + PER_CHUNK, KS>(kreg[c & 1]);
+    else
+      wait_vm<VI, KS>(kreg[c & 1]);
+    if (c < nvc) {
+      const int r0 = kw0 + c * KC;
+      bf16* tV = sV[w][c & 1];
+      const bool has_new = own_new && newrow >= r0 && newrow < r0 + KC;
+      // the new row's lane takes k from sNew (a select, so that no load
+      // target is overwritten under divergence, which would force a full
+      // memory-counter wait)
+      u32x4 nk[KS];
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) nk[ks] = u32x4{0u, 0u, 0u, 0u};
+      if (has_new) {
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) nk[ks] = *(const u32x4*)(sNew[0] + 16 * ks + 8 * hh);
+      }
+      const bool is_new = has_new && c32 == newrow - r0;
+      bf16x8 kf[KS];
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) kf[ks] = as_bf16x8(is_new ? nk[ks] : kreg[c & 1][ks]);
+      f32x16 sc;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) sc[i] = 0.f;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+        sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[ks], as_bf16x8(qf[ks]), sc, 0, 0, 0);
+      const int lim = k1 - 1 - r0;  // last valid key of the chunk, local
+      float tmax = -INFINITY;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int local = 8 * (i >> 2) + 4 * hh + (i & 3);
+        sc[i] = local > lim ? -INFINITY : sc[i] * scale_log2;
+        tmax = fmaxf(tmax, sc[i]);
+      }
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+      const float mnew = fmaxf(m, tmax);  // finite: key r0 is valid
+      const float alpha = fast_exp2(m - mnew);
+      float psum = 0.f;
+      u32x4 pk[2];
+#pragma unroll
+      for (int i = 0; i < 16; i += 2) {
+        const float p0 = fast_exp2(sc[i] - mnew), p1 = fast_exp2(sc[i + 1] - mnew);
+        psum += p0 + p1;
+        pk[i >> 3][(i & 7) >> 1] = pack2(p0, p1);
+      }
+      lsum = lsum * alpha + psum;
+      m = mnew;
+      // V of chunk c has landed once only the next chunk's loads are pending
+      if (c + 1 < NCH)
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(PER_CHUNK) : "memory");
+      else
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      if (lim < KC - 1) {
+        // rows past the split's end hold clamped copies of a row that may be
+        // stale (the slot being written): zero them so 0 * V stays 0
+        for (int Lc = (lim + 1) * KR + lane; Lc < KC * KR; Lc += 64)
+          *(u32x4*)(tV + Lc * 8) = u32x4{0u, 0u, 0u, 0u};
+      }
+      if (has_new && lane < KR) {
+        const int row = newrow - r0;
+        *(u32x4*)(tV + (row * KR + (lane ^ swz<KR>(row))) * 8) = *(const u32x4*)(sNew[1] + 8 * lane);
+      }
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[dt][i] *= alpha;
+#pragma unroll
+      for (int cc = 0; cc < 2; ++cc)
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+          const bf16x8 a = lds_frag_t<D>(tV, tro, cc, dt);
+          acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, as_bf16x8(pk[cc]), acc[dt], 0, 0, 0);
+        }
     }
   }
-  // V reads overlap the softmax below
-  u32x4 vr[NP];
-#pragma unroll
-  for (int p = 0; p < NP; ++p) {
-    const int row = k0 + p * RPP + rg;
-    vr[p] = row < k1 ? *(const u32x4*)(vb + (int64_t)row * D + 8 * c) : u32x4{0u, 0u, 0u, 0u};
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  const float ltot = lsum + __shfl_xor(lsum, 32, 64);
+  // merge the wavefronts: (m, l) per head, then o through LDS (reuses sV)
+  if (hh == 0) {
+    sML[w][0][c32] = m;
+    sML[w][1][c32] = ltot;
   }
   __syncthreads();
-  // softmax over this split, one wavefront per query head
-  for (int hr = w; hr < NREP; hr += 4) {
-    float mx = -INFINITY;
-    for (int j = lane; j < k1 - k0; j += 64) mx = fmaxf(mx, sp[hr][j]);
-    mx = wave_max(mx);
-    float sum = 0.f;
-    for (int j = lane; j < CH; j += 64) {
-      const float p = j < k1 - k0 ? fast_exp2(sp[hr][j] - mx) : 0.f;
-      sp[hr][j] = p;
-      sum += p;
+  // [wave][D][32 heads], head index XOR-swizzled by d so that both the column
+  // writes below and the row reads after are conflict-free
+  float* so = (float*)&sV[0][0][0];
+  auto so_at = [&](int ww, int d, int h) { return ((ww * D + d) << 5) + (h ^ ((d >> 1) & 31)); };
+  float M = -INFINITY;
+#pragma unroll
+  for (int ww = 0; ww < DEC_WAVES; ++ww) M = fmaxf(M, sML[ww][0][c32]);
+  const float wgt = m == -INFINITY ? 0.f : fast_exp2(m - M);
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int d = 32 * dt + 8 * (i >> 2) + 4 * hh + (i & 3);
+      so[so_at(w, d, c32)] = acc[dt][i] * wgt;
     }
-    sum = wave_sum(sum);
-    if (lane == 0) {
-      sm[hr] = mx;
-      sl[hr] = sum;
-    }
-  }
   __syncthreads();
-  float acc[NREP][8];
-#pragma unroll
-  for (int hr = 0; hr < NREP; ++hr)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc[hr][e] = 0.f;
-#pragma unroll
-  for (int p = 0; p < NP; ++p) {
-    const int j = p * RPP + rg;  // rows past k1 hold zeros and p = 0
-    float vf[8];
-    unpack8(vr[p], vf);
-#pragma unroll
-    for (int hr = 0; hr < NREP; ++hr) {
-      const float pr = sp[hr][j];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) acc[hr][e] += pr * vf[e];
-    }
-  }
-  // reduce over the row groups: first inside the wavefront, then across the 4
-#pragma unroll
-  for (int o = TPR; o < 64; o <<= 1)
-#pragma unroll
-    for (int hr = 0; hr < NREP; ++hr)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) acc[hr][e] += __shfl_xor(acc[hr][e], o, 64);
-  if (lane < TPR) {
-#pragma unroll
-    for (int hr = 0; hr < NREP; ++hr)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) so[w][hr * D + 8 * c + e] = acc[hr][e];
-  }
-  __syncthreads();
-  for (int it = tid; it < NREP * D; it += 256) {
+  for (int it = threadIdx.x; it < n_rep * D; it += 256) {
     const int hr = it / D, d = it % D;
-    const float s = so[0][it] + so[1][it] + so[2][it] + so[3][it];
-    const int64_t ph = ((int64_t)b * Hq + g * NREP + hr) * nsplit + sp_idx;
-    opart[ph * D + d] = s;
+    float o = 0.f;
+#pragma unroll
+    for (int ww = 0; ww < DEC_WAVES; ++ww) o += so[so_at(ww, d, hr)];
+    const int64_t ph = ((int64_t)b * Hq + g * n_rep + hr) * nsplit + sp_idx;
+    opart[ph * D + d] = o;
     if (d == 0) {
-      mpart[ph] = sm[hr];
-      lpart[ph] = sl[hr];
+      float Mh = -INFINITY;
+#pragma unroll
+      for (int ww = 0; ww < DEC_WAVES; ++ww) Mh = fmaxf(Mh, sML[ww][0][hr]);
+      float lh = 0.f;
+#pragma unroll
+      for (int ww = 0; ww < DEC_WAVES; ++ww)
+        lh += sML[ww][0][hr] == -INFINITY ? 0.f : sML[ww][1][hr] * fast_exp2(sML[ww][0][hr] - Mh);
+      mpart[ph] = Mh;
+      lpart[ph] = lh;
     }
   }
 }
 
+// One workgroup of D threads per (b, hq): every thread rescales and sums its
+// output element over the splits (independent loads, unrolled).
 template <typename T>
 __global__ __launch_bounds__(256) void decode_merge_kernel(const float* __restrict__ opart,
                                                            const float* __restrict__ mpart,
@@ -224,24 +379,42 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const float* __restri
                                                            int nsplit, int max_len,
                                                            int64_t row_offset,
                                                            int64_t rope_rows) {
+  __shared__ float sw[1024];
+  __shared__ float sinv;
   const int bh = blockIdx.x;
   const int b = bh / Hq;
+  const int d = threadIdx.x;
   if (!decode_len_ok(lens[b], max_len, row_offset, rope_rows)) {
-    for (int d = threadIdx.x; d < D; d += 256) out[(int64_t)bh * D + d] = from_f32<T>(NAN);
+    if (d < D) out[(int64_t)bh * D + d] = from_f32<T>(NAN);
     return;
   }
-  const int ns = (lens[b] + 1 + CH - 1) / CH;  // <= nsplit because lens[b] < max_len
+  const int ns = min((lens[b] + 1 + CH - 1) / CH, 1024);  // <= nsplit (lens[b] < max_len)
   const int64_t base = (int64_t)bh * nsplit;
-  float M = -INFINITY;
-  for (int s = 0; s < ns; ++s) M = fmaxf(M, mpart[base + s]);
-  float lt = 0.f;
-  for (int s = 0; s < ns; ++s) lt += lpart[base + s] * fast_exp2(mpart[base + s] - M);
-  const float inv = 1.f / lt;
-  for (int d = threadIdx.x; d < D; d += 256) {
-    float o = 0.f;
-    for (int s = 0; s < ns; ++s) o += opart[(base + s) * D + d] * fast_exp2(mpart[base + s] - M);
-    out[(int64_t)bh * D + d] = from_f32<T>(o * inv);
+  if (threadIdx.x < 64) {
+    const int lane = threadIdx.x;
+    float M = -INFINITY;
+    for (int s0 = lane; s0 < ns; s0 += 64) M = fmaxf(M, mpart[base + s0]);
+    M = wave_max(M);
+    float lt = 0.f;
+    for (int s0 = lane; s0 < ns; s0 += 64) {
+      const float wgt = fast_exp2(mpart[base + s0] - M);
+      sw[s0] = wgt;
+      lt += lpart[base + s0] * wgt;
+    }
+    lt = wave_sum(lt);
+    if (lane == 0) sinv = 1.f / lt;
   }
+  __syncthreads();
+  if (d >= D) return;
+  float o = 0.f;
+  int s = 0;
+  for (; s + 4 <= ns; s += 4) {
+    const float a0 = opart[(base + s) * D + d], a1 = opart[(base + s + 1) * D + d];
+    const float a2 = opart[(base + s + 2) * D + d], a3 = opart[(base + s + 3) * D + d];
+    o += a0 * sw[s] + a1 * sw[s + 1] + a2 * sw[s + 2] + a3 * sw[s + 3];
+  }
+  for (; s < ns; ++s) o += opart[(base + s) * D + d] * sw[s];
+  out[(int64_t)bh * D + d] = from_f32<T>(o * sinv);
 }
 
 // One wavefront per (b, hq); keys 0..lens[b] read from the (already appended)
@@ -318,51 +491,43 @@ int launch_append(const T* k_new, const T* v_new, const float* cos, const float*
   return KF_OK;
 }
 
-template <int D, int NREP>
+template <int D>
 int launch_split(const DecodeArgs& a, float* opart, float* mpart, float* lpart, int nsplit) {
-  KF_LAUNCH("decode_split", (decode_split_kernel<D, NREP>), dim3(nsplit, a.B * a.Hkv), dim3(256), 0,
-                     a.stream, (const bf16*)a.q_new, a.cos, a.sin, a.rope_row_offset,
-                     a.rope_rows, a.max_len, (const bf16*)a.k_cache, (const bf16*)a.v_cache,
-                     a.lens, opart, mpart, lpart, a.Hq, a.Hkv, a.Smax, nsplit,
-                     a.scale * kLog2e);
+  KF_LAUNCH("decode_split", decode_split_kernel<D>, dim3(nsplit, a.B * a.Hkv), dim3(256), 0,
+            a.stream, (const bf16*)a.q_new, (const bf16*)a.k_new, (const bf16*)a.v_new, a.cos,
+            a.sin, a.rope_row_offset, a.rope_rows, a.max_len, (bf16*)a.k_cache, (bf16*)a.v_cache,
+            a.lens, opart, mpart, lpart, a.Hq, a.Hkv, a.Smax, nsplit, a.Hq / a.Hkv,
+            a.scale * kLog2e);
   KF_CHECK_LAUNCH();
   return KF_OK;
 }
 
-template <int D>
-int dispatch_nrep(const DecodeArgs& a, float* opart, float* mpart, float* lpart, int nsplit) {
-  switch (a.Hq / a.Hkv) {
-    case 1: return launch_split<D, 1>(a, opart, mpart, lpart, nsplit);
-    case 2: return launch_split<D, 2>(a, opart, mpart, lpart, nsplit);
-    case 4: return launch_split<D, 4>(a, opart, mpart, lpart, nsplit);
-    case 8: return launch_split<D, 8>(a, opart, mpart, lpart, nsplit);
-  }
-  return KF_ERR_UNSUPPORTED;
-}
-
 template <typename T>
 int decode_typed(const DecodeArgs& a, void* workspace) {
-  int rc = launch_append<T>((const T*)a.k_new, (const T*)a.v_new, a.cos, a.sin, (T*)a.k_cache,
-                            (T*)a.v_cache, a.lens, 0, a.rope_row_offset, a.rope_rows, a.max_len,
-                            a.B, 1, a.Hkv, a.Smax, a.D, a.stream);
-  if (rc) return rc;
+  int rc = KF_OK;
   const int n_rep = a.Hq / a.Hkv;
-  const bool fast = __is_same(T, bf16) && (a.D == 64 || a.D == 128) &&
-                    (n_rep == 1 || n_rep == 2 || n_rep == 4 || n_rep == 8);
+  const bool fast = __is_same(T, bf16) && (a.D == 64 || a.D == 128) && n_rep <= 32 &&
+                    (a.max_len + CH - 1) / CH <= 1024 &&
+                    ((uintptr_t)a.q_new | (uintptr_t)a.k_new | (uintptr_t)a.v_new |
+                     (uintptr_t)a.k_cache | (uintptr_t)a.v_cache) % 16 == 0;
   if (fast) {
     const int nsplit = (a.max_len + CH - 1) / CH;
     float* opart = (float*)workspace;
     float* mpart = opart + (size_t)a.B * a.Hq * nsplit * a.D;
     float* lpart = mpart + (size_t)a.B * a.Hq * nsplit;
-    rc = a.D == 128 ? dispatch_nrep<128>(a, opart, mpart, lpart, nsplit)
-                    : dispatch_nrep<64>(a, opart, mpart, lpart, nsplit);
+    rc = a.D == 128 ? launch_split<128>(a, opart, mpart, lpart, nsplit)
+                    : launch_split<64>(a, opart, mpart, lpart, nsplit);
     if (rc) return rc;
-    KF_LAUNCH("decode_merge", decode_merge_kernel<T>, dim3(a.B * a.Hq), dim3(256), 0, a.stream, opart,
-                       mpart, lpart, a.lens, (T*)a.out, a.Hq, a.D, nsplit, a.max_len,
-                       a.rope_row_offset, a.rope_rows);
+    KF_LAUNCH("decode_merge", decode_merge_kernel<T>, dim3(a.B * a.Hq), dim3(a.D), 0, a.stream,
+              opart, mpart, lpart, a.lens, (T*)a.out, a.Hq, a.D, nsplit, a.max_len,
+              a.rope_row_offset, a.rope_rows);
     KF_CHECK_LAUNCH();
     return KF_OK;
   }
+  rc = launch_append<T>((const T*)a.k_new, (const T*)a.v_new, a.cos, a.sin, (T*)a.k_cache,
+                        (T*)a.v_cache, a.lens, 0, a.rope_row_offset, a.rope_rows, a.max_len, a.B,
+                        1, a.Hkv, a.Smax, a.D, a.stream);
+  if (rc) return rc;
   KF_LAUNCH("decode_generic", decode_generic_kernel<T>, dim3((a.B * a.Hq + 3) / 4), dim3(256), 0,
                      a.stream, (const T*)a.q_new, a.cos, a.sin, a.rope_row_offset, a.rope_rows,
                      a.max_len, (const T*)a.k_cache, (const T*)a.v_cache, a.lens, (T*)a.out, a.B,

@@ -39,7 +39,10 @@ def test_fixture():
     (torch.bfloat16, 3, 8, 8, 64, 1, 300, 400),      # MHA fast path, D=64
     (torch.bfloat16, 2, 16, 2, 128, 255, 257, 300),  # split boundaries (CH=256)
     (torch.bfloat16, 2, 8, 1, 128, 0, 3, 8),         # empty cache (len 0) and tiny
-    (torch.bfloat16, 2, 6, 2, 128, 10, 90, 100),     # n_rep 3 -> generic kernel
+    (torch.bfloat16, 2, 6, 2, 128, 10, 90, 100),     # n_rep 3 (padded MFMA columns)
+    (torch.bfloat16, 2, 32, 1, 128, 500, 700, 800),  # n_rep 32, the widest fast case
+    (torch.bfloat16, 1, 64, 8, 128, 1000, 1300, 1400),  # 70B heads, n_rep 8
+    (torch.bfloat16, 2, 64, 1, 64, 10, 90, 100),     # n_rep 64 -> generic kernel
     (torch.float32, 2, 4, 2, 64, 10, 90, 100),       # fp32 -> generic kernel
     (torch.bfloat16, 2, 4, 2, 32, 10, 90, 100),      # D=32 -> generic kernel
 ], ids=lambda c: "-".join(map(str, c)))
@@ -99,3 +102,28 @@ def test_cache_append_bit_exact():
     assert torch.equal(kc.cpu()[:, :, start:start + S], want)
     assert torch.equal(vc.cpu()[:, :, start:start + S], vn.transpose(1, 2))
     assert (kc.cpu()[:, :, :start] == 0).all() and (kc.cpu()[:, :, start + S:] == 0).all()
+
+
+def test_stale_rows_are_not_read():
+    """Cache rows past each sequence's length hold NaN; the output and the
+    written rows must not see them (the reference reads rows <= len only)."""
+    B, Hq, Hkv, D, Smax = 3, 8, 2, 128, 700
+    announce("decode stale NaN rows")
+    lens = torch.tensor([0, 255, 600], dtype=torch.int32)
+    q = seeded((B, 1, Hq, D), 0, torch.bfloat16)
+    kn = seeded((B, 1, Hkv, D), 1, torch.bfloat16)
+    vn = seeded((B, 1, Hkv, D), 2, torch.bfloat16)
+    kc = seeded((B, Hkv, Smax, D), 5, torch.bfloat16)
+    vc = seeded((B, Hkv, Smax, D), 6, torch.bfloat16)
+    for b in range(B):
+        kc[b, :, int(lens[b]):] = float("nan")
+        vc[b, :, int(lens[b]):] = float("nan")
+    cos, sin = ref.rope_tables(D, Smax, 5e5)
+    out, kcd, vcd = _decode(q, kn, vn, kc, vc, lens, cos, sin, Smax)
+    o_ref, kc_ref, vc_ref = ref.decode_step(q, kn, vn, kc, vc, lens, cos, sin)
+    assert torch.isfinite(out.cpu().float()).all()
+    assert max_abs(out, o_ref) <= 2e-2
+    for b in range(B):
+        L = int(lens[b]) + 1
+        assert torch.equal(kcd.cpu()[b, :, :L], kc_ref[b, :, :L])
+        assert torch.equal(vcd.cpu()[b, :, :L], vc_ref[b, :, :L])
