@@ -87,10 +87,8 @@ __global__ __launch_bounds__(256) void append_kernel(const T* __restrict__ k_new
 // writes k and v into the caches and uses them in place of that row.
 // 16-byte global load issued from inline asm, so that the compiler's
 // memory-counter bookkeeping does not see it: the caller waits with
-// wait_vm<N>() and passes the destination through it before any use.  (The
-// compiler cannot pipeline register loads with the direct-to-LDS loads in
-// flight: it answers every register dependency with vmcnt(0) while one is
-// pending.)
+// wait_vm<N>() and passes the destination through it before any use.  (Its
+// own count would be off by the untracked direct-to-LDS loads in between.)
 template <int OFF>
 __device__ __forceinline__ void gload16(u32x4& r, uint32_t voff, const void* base) {
   asm volatile("global_load_dwordx4 %0, %1, %2 offset:%3"
@@ -104,18 +102,6 @@ __device__ __forceinline__ void gload16_row(u32x4* r, uint32_t voff, const void*
     gload16<32 * I>(r[I], voff, base);
     gload16_row<N, I + 1>(r, voff, base);
   }
-}
-// Direct global->LDS 16-byte load (LDS destination M0 + 16 * lane), also
-// issued from inline asm: the compiler's own tracking of these would make
-// every LDS read that may alias a pending one wait for all of them.
-__device__ __forceinline__ void dma16(uint32_t lds_addr, uint32_t voff, const void* base) {
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
-               :
-               : "s"(lds_addr), "v"(voff), "s"(base)
-               : "memory", "m0");
-}
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
 }
 // s_waitcnt vmcnt(N), then the registers in r[0..n) count as written here
 template <int N, int n>

@@ -60,6 +60,31 @@ __device__ __forceinline__ const bf16x8& lds_frag(const bf16* tile, int row, int
   return *(const bf16x8*)(tile + (row * R + (chunk ^ swz<R>(row))) * 8);
 }
 
+// LDS byte address of a __shared__ object.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+// Direct global->LDS loads: lane i's bytes land at lds + size * i.  Issued
+// from inline asm so that the compiler does not track them: tracked, every
+// LDS read behind one waits for all outstanding LDS reads (lgkmcnt(0)) or for
+// all of them to land (vmcnt(0)), which serialises software-pipelined LDS
+// fragment reads.  Completion is therefore the caller's: an explicit
+// s_waitcnt vmcnt (lds_copy_wait) and, across wavefronts, a barrier, before
+// the data is read.  `lds` and `base` must be wavefront-uniform.
+__device__ __forceinline__ void dma16(uint32_t lds, uint32_t voff, const void* base) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
+               :
+               : "s"(lds), "v"(voff), "s"(base)
+               : "memory", "m0");
+}
+__device__ __forceinline__ void dma4(uint32_t lds, uint32_t voff, const void* base) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, %2"
+               :
+               : "s"(lds), "v"(voff), "s"(base)
+               : "memory", "m0");
+}
+
 // Copy a [ROWS_T][R chunks] bf16 tile whose rows start `ld` elements apart in
 // global memory into a swizzled LDS tile with direct global->LDS loads: each
 // instruction moves 64 lanes x 16 bytes into 1 KB of contiguous LDS, so the
@@ -79,8 +104,7 @@ __device__ __forceinline__ void tile_to_lds(const bf16* __restrict__ g, uint32_t
     const int lc = pc ^ swz<R>(row);
     // uniform base + 32-bit per-lane byte offset: the saddr form of the load
     const uint32_t off = ((uint32_t)row * ld + (uint32_t)lc * 8u) * 2u;
-    __builtin_amdgcn_global_load_lds((const void*)((const char*)g + off),
-                                     (lds_ptr_t)(lds + (w * PER + j) * 512), 16, 0, 0);
+    dma16(lds_addr(lds + (w * PER + j) * 512), off, g);
   }
 }
 
@@ -153,7 +177,7 @@ __device__ __forceinline__ bf16x8 lds_frag_t(const bf16* tile, const TrOffsets<D
 
 // 64 consecutive floats (one per lane of one wavefront) straight into LDS.
 __device__ __forceinline__ void row_to_lds(const float* __restrict__ g, float* lds, int lane) {
-  __builtin_amdgcn_global_load_lds((const void*)(g + lane), (lds_ptr_t)lds, 4, 0, 0);
+  dma4(lds_addr(lds), (uint32_t)lane * 4u, g);
 }
 
 __device__ __forceinline__ void lds_copy_wait() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
