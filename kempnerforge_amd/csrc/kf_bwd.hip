@@ -154,6 +154,8 @@ __device__ __forceinline__ void dkdv_role(
 
   lds_copy_wait();
   __syncthreads();
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) settle(bf[ks]);
   for (int it = 0; it < total; ++it) {
     const int buf = it & 1;
     if (it + 1 < total) stage(it + 1, buf ^ 1);
@@ -364,6 +366,13 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_kernel(
 
   lds_copy_wait();
   __syncthreads();
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    settle(qf[ks]);
+    settle(df[ks]);
+  }
+  settle(l2);
+  settle(dl);
   for (int t = 0; t < ntiles; ++t) {
     const int buf = t & 1;
     if (t + 1 < ntiles) stage(t + 1, buf ^ 1);

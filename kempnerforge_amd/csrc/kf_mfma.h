@@ -182,6 +182,14 @@ __device__ __forceinline__ void row_to_lds(const float* __restrict__ g, float* l
 
 __device__ __forceinline__ void lds_copy_wait() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
+// Pin a loaded value at this point: the compiler waits for its load here, not
+// at its first use, which may sit inside a loop that keeps direct-to-LDS
+// loads in flight (a wait there would stall on those every iteration).
+template <typename T>
+__device__ __forceinline__ void settle(T& x) {
+  asm volatile("" : "+v"(x));
+}
+
 // Wavefront index as a scalar (SGPR) value, so per-wave LDS destinations and
 // global bases derived from it stay uniform.
 __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
