@@ -8,9 +8,11 @@ with P = B*Hq*S*(S+1)/2 causal (query, key) pairs (forward 4*D*P, backward
 10*D*P; GQA not discounted).
 
 Also reported: per-kernel HIP-event timings (the library brackets each launch
-on its own stream), the roofline of the dominant kernel, the KV-cache decode
-configuration C4 in GB/s, and the reference's PyTorch path timed on the host
-CPU on a bounded sample of the same workload.
+on its own stream), the roofline of the dominant kernel, the forward alone
+(C2), the Llama-3-70B shape fwd+bwd (C5: B=1, S=16384, 64 query heads) and its
+2048-token probability capture (C5-cap), the KV-cache decode configuration C4
+in GB/s, and the reference's PyTorch path timed on the host CPU on a bounded
+sample of the same workload.
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline]
 """
@@ -33,6 +35,7 @@ PEAK_HBM_GBPS = 8000.0
 
 C3 = dict(B=4, S=4096, Hq=32, Hkv=8, D=128, theta=500000.0)
 C4 = dict(B=32, Hq=32, Hkv=8, D=128, lo=1024, hi=8192, theta=500000.0)
+C5 = dict(B=1, S=16384, Hq=64, Hkv=8, D=128, theta=500000.0, cap_tokens=2048)
 
 
 def pairs(B, Hq, S):
@@ -112,6 +115,52 @@ def main() -> int:
                 "avg_us": round(kstats[dom]["avg_us"], 1)}
     fwd_us = kstats.get("fwd_mfma", {}).get("avg_us")
 
+    def wall(fn, warm, iters):
+        for _ in range(warm):
+            fn()
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        for _ in range(iters):
+            fn()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t) / iters
+
+    # C2: forward only (out + LSE) on the same tensors
+    qn_, kn_, vn_ = q.detach(), k.detach(), v.detach()
+    c2_s = wall(lambda: ops.fwd_raw(qn_, kn_, vn_, cos, sin, causal=True, k_rotated=False),
+                args.warmup, args.steps)
+    c2 = {"config": "C2 llama3-8b fwd B=4 S=4096 Hq=32 Hkv=8 D=128", "ms": round(c2_s * 1e3, 4),
+          "TFLOP/s": round(4.0 * D * P / c2_s / 1e12, 1)}
+
+    # C5: llama3-70b shape fwd+bwd, and C5-cap (probabilities of its first 2048 tokens)
+    B5, S5, Hq5, Hkv5 = C5["B"], C5["S"], C5["Hq"], C5["Hkv"]
+    q5 = seeded((B5, S5, Hq5, D), 0, bf16, dev).requires_grad_(True)
+    k5 = seeded((B5, S5, Hkv5, D), 1, bf16, dev).requires_grad_(True)
+    v5 = seeded((B5, S5, Hkv5, D), 2, bf16, dev).requires_grad_(True)
+    do5 = seeded((B5, S5, Hq5, D), 3, bf16, dev)
+    cos5, sin5 = precompute_rope_frequencies(D, S5, C5["theta"])
+    cos5, sin5 = cos5.to(dev), sin5.to(dev)
+
+    def step5():
+        out5 = ops.attention(q5, k5, v5, cos5, sin5, causal=True)
+        torch.autograd.grad(out5, (q5, k5, v5), do5)
+
+    c5_s = wall(step5, 2, max(5, args.steps // 2))
+    P5 = pairs(B5, Hq5, S5)
+    c5 = {"config": "C5 llama3-70b fwd+bwd B=1 S=16384 Hq=64 Hkv=8 D=128",
+          "ms": round(c5_s * 1e3, 3), "TFLOP/s": round(14.0 * D * P5 / c5_s / 1e12, 1),
+          "frac_of_peak": round(14.0 * D * P5 / c5_s / 1e12 / PEAK_BF16_TFLOPS, 4)}
+    Sc = C5["cap_tokens"]
+    qc, kc_, vc_ = (t.detach()[:, :Sc].contiguous() for t in (q5, k5, v5))
+    cap_s = wall(lambda: ops.capture_raw(qc, kc_, vc_, cos5[:Sc], sin5[:Sc], causal=True,
+                                         k_rotated=False), 2, args.steps)
+    cap_bytes = 4 * Hq5 * Sc * Sc + Sc * (Hq5 + 2 * Hkv5) * D * 2 + Sc * Hq5 * D * 2
+    c5cap = {"config": "C5-cap first 2048 tokens of C5, P [1,64,2048,2048] fp32",
+             "us": round(cap_s * 1e6, 1), "bytes": cap_bytes,
+             "GB/s": round(cap_bytes / cap_s / 1e9, 1),
+             "frac_of_hbm_peak": round(cap_bytes / cap_s / 1e9 / PEAK_HBM_GBPS, 4)}
+    del q5, k5, v5, do5, qc, kc_, vc_
+
     # decode (C4)
     g = torch.Generator().manual_seed(4)
     Bd, Hqd, Hkvd, Dd = C4["B"], C4["Hq"], C4["Hkv"], C4["D"]
@@ -183,6 +232,9 @@ def main() -> int:
         "frac_of_peak_step": round(value / PEAK_BF16_TFLOPS, 4),
         "kernels_us": {n: round(s["avg_us"], 1) for n, s in kstats.items()},
         "fwd_tflops": round(4.0 * D * P / (fwd_us * 1e-6) / 1e12, 1) if fwd_us else None,
+        "c2_fwd": c2,
+        "c5": c5,
+        "c5_cap": c5cap,
         "decode": {"config": "C4 B=32 Hq=32 Hkv=8 D=128 L~U[1024,8192] seed 4",
                    "bytes": dec_bytes, "us_per_step": round(dec_us, 1),
                    "GB/s": round(dec_bytes / (dec_us * 1e-6) / 1e9, 1),

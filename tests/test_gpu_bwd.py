@@ -11,7 +11,7 @@ import pytest
 import torch
 
 import make_fixtures as mf
-from gpu_util import DEV, announce, load_fixture, rel_max, seeded
+from gpu_util import DEV, announce, load_fixture, max_abs, rel_max, seeded
 from kempnerforge_amd import ops
 from oracle import attention_ref as ref
 
@@ -86,3 +86,59 @@ def test_llama8b_shape_one_group():
     assert rel_max(dq[b:b + 1, :, hs], dq_r) <= 2e-2
     assert rel_max(dk[b:b + 1, :, g:g + 1], dk_r) <= 2e-2
     assert rel_max(dv[b:b + 1, :, g:g + 1], dv_r) <= 2e-2
+
+
+def test_llama70b_shape_prefix_and_identities():
+    """C5 at full size (B=1, S=16384, Hq=64, Hkv=8, D=128), fwd+bwd.
+
+    The oracle cannot hold this size, so it is tied to one it can:
+    * causal prefix: rows < 2048 of out, LSE and dQ depend only on the first
+      2048 positions, so they equal (bitwise) a run on that prefix, which is
+      checked against the oracle for one KV group;
+    * dV: rows of P sum to one, so sum_j dV_j = sum over the group's query
+      heads and positions of dO;
+    * dK: rows of dS sum to zero, so the RoPE-rotated dK sums to zero over keys.
+    """
+    B, S, Hq, Hkv, D, Sp = 1, 16384, 64, 8, 128, 2048
+    n_rep = Hq // Hkv
+    announce("bwd 70B shape")
+    q = seeded((B, S, Hq, D), 0, torch.bfloat16)
+    k = seeded((B, S, Hkv, D), 1, torch.bfloat16)
+    v = seeded((B, S, Hkv, D), 2, torch.bfloat16)
+    do = seeded((B, S, Hq, D), 3, torch.bfloat16)
+    cos, sin = ref.rope_tables(D, S, 5e5)
+    qd, kd, vd = (t.to(DEV).requires_grad_(True) for t in (q, k, v))
+    out, lse = ops.fwd_raw(qd.detach(), kd.detach(), vd.detach(), cos.to(DEV), sin.to(DEV),
+                           causal=True, k_rotated=False)
+    out_a = ops.attention(qd, kd, vd, cos.to(DEV), sin.to(DEV), causal=True)
+    out_a.backward(do.to(DEV))
+    torch.cuda.synchronize()
+    assert torch.equal(out, out_a.detach())
+    dq, dk, dv = qd.grad, kd.grad, vd.grad
+    assert all(torch.isfinite(t.float()).all() for t in (out, dq, dk, dv))
+
+    # causal prefix
+    out_p, lse_p = ops.fwd_raw(q[:, :Sp].to(DEV), k[:, :Sp].to(DEV), v[:, :Sp].to(DEV),
+                               cos[:Sp].to(DEV), sin[:Sp].to(DEV), causal=True, k_rotated=False)
+    _, dq_p, dk_p, dv_p = _grads(q[:, :Sp], k[:, :Sp], v[:, :Sp], do[:, :Sp], cos[:Sp], sin[:Sp])
+    assert torch.equal(out[:, :Sp], out_p)
+    assert torch.equal(lse[:, :, :Sp], lse_p)
+    assert torch.equal(dq[:, :Sp], dq_p)
+    g = 5
+    hs = slice(n_rep * g, n_rep * g + n_rep)
+    args = (q[:, :Sp, hs], k[:, :Sp, g:g + 1], v[:, :Sp, g:g + 1], cos[:Sp], sin[:Sp])
+    o_r, _ = ref.attention_fwd(*args)
+    dq_r, dk_r, dv_r = ref.attention_bwd(*args, do[:, :Sp, hs])
+    assert max_abs(out_p[:, :, hs], o_r) <= 2e-2
+    assert rel_max(dq_p[:, :, hs], dq_r) <= 2e-2
+    assert rel_max(dk_p[:, :, g:g + 1], dk_r) <= 2e-2
+    assert rel_max(dv_p[:, :, g:g + 1], dv_r) <= 2e-2
+
+    # sum identities at full length, per KV head
+    dv_sum = dv.float().sum(dim=1)                                   # [B, Hkv, D]
+    do_sum = do.to(DEV).float().view(B, S, Hkv, n_rep, D).sum(dim=(1, 3))
+    assert (dv_sum - do_sum).abs().max() <= 2e-2 * max(1.0, do_sum.abs().max().item())
+    dk_rot = ref.apply_rope(dk.float().transpose(1, 2).cpu(), cos, sin)   # [B, Hkv, S, D]
+    resid = dk_rot.sum(dim=2).abs().max().item()
+    scale = dk_rot.pow(2).sum(dim=2).sqrt().max().item()
+    assert resid <= 2e-2 * scale
