@@ -42,6 +42,17 @@ def pairs(B, Hq, S):
     return B * Hq * S * (S + 1) // 2
 
 
+def measured_traffic():
+    """HBM bytes per launch of each kernel per workload, from the rocprofv3
+    FETCH_SIZE / WRITE_SIZE runs recorded in profiles/hbm_traffic.json (scaled by
+    a device copy of known size); {} when that file is absent."""
+    path = os.path.join(ROOT, "profiles", "hbm_traffic.json")
+    if not os.path.exists(path):
+        return {}
+    with open(path) as f:
+        return {k: v["bytes"] for k, v in json.load(f)["kernels"].items()}
+
+
 def seeded(shape, seed, dtype, dev):
     import torch
 
@@ -56,6 +67,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="first run one 256 MiB device-to-device copy (a kernel of known "
+                         "traffic, for scaling HBM byte counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the attention path "
@@ -70,6 +84,12 @@ def main() -> int:
 
     dev = torch.device("cuda:0")
     bf16 = torch.bfloat16
+    if args.copy_calibration:
+        src = torch.ones(64 * 1024 * 1024, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     B, S, Hq, Hkv, D = (C3[k] for k in ("B", "S", "Hq", "Hkv", "D"))
     q = seeded((B, S, Hq, D), 0, bf16, dev).requires_grad_(True)
     k = seeded((B, S, Hkv, D), 1, bf16, dev).requires_grad_(True)
@@ -106,12 +126,14 @@ def main() -> int:
     # 4*D*P of recomputed S and dP plus dV, dK -> dkdv kernel 8*D*P; dQ 2*D*P)
     algo = {"fwd_mfma": 4.0 * D * P, "bwd_dkdv": 8.0 * D * P, "bwd_dq": 2.0 * D * P}
     dom = max(kstats, key=lambda n: kstats[n]["avg_us"] * kstats[n]["launches"])
+    traffic = measured_traffic()
     roof = None
     if dom in algo:
         ach = algo[dom] / (kstats[dom]["avg_us"] * 1e-6) / 1e12
         roof = {"kernel": dom, "bound": "mfma", "achieved": round(ach, 1),
                 "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                "frac": round(ach / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                "frac": round(ach / PEAK_BF16_TFLOPS, 4),
+                "traffic": traffic.get(f"{dom}@C3"),
                 "avg_us": round(kstats[dom]["avg_us"], 1)}
     fwd_us = kstats.get("fwd_mfma", {}).get("avg_us")
 
@@ -158,7 +180,8 @@ def main() -> int:
     c5cap = {"config": "C5-cap first 2048 tokens of C5, P [1,64,2048,2048] fp32",
              "us": round(cap_s * 1e6, 1), "bytes": cap_bytes,
              "GB/s": round(cap_bytes / cap_s / 1e9, 1),
-             "frac_of_hbm_peak": round(cap_bytes / cap_s / 1e9 / PEAK_HBM_GBPS, 4)}
+             "frac_of_hbm_peak": round(cap_bytes / cap_s / 1e9 / PEAK_HBM_GBPS, 4),
+             "capture_kernel_traffic": traffic.get("capture_probs@C5-cap")}
     del q5, k5, v5, do5, qc, kc_, vc_
 
     # decode (C4)
@@ -241,7 +264,8 @@ def main() -> int:
                    "frac_of_hbm_peak": round(dec_bytes / (dec_us * 1e-6) / 1e9 / PEAK_HBM_GBPS, 4),
                    "kernels_us": {n: round(s["avg_us"], 1) for n, s in dstats.items()},
                    "split_kernel_GB/s": round(dec_bytes / (split_us * 1e-6) / 1e9, 1)
-                   if split_us else None},
+                   if split_us else None,
+                   "split_kernel_traffic": traffic.get("decode_split@C4")},
     }
     print(json.dumps(line), flush=True)
     return 0
