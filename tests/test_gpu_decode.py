@@ -127,3 +127,39 @@ def test_stale_rows_are_not_read():
         L = int(lens[b]) + 1
         assert torch.equal(kcd.cpu()[b, :, :L], kc_ref[b, :, :L])
         assert torch.equal(vcd.cpu()[b, :, :L], vc_ref[b, :, :L])
+
+
+def test_consecutive_steps_and_bad_length():
+    """Three decode steps in a row on the same caches (the workspace's
+    completion counters must come back to zero after every call), one sequence
+    with an out-of-range length (NaN output, caches untouched)."""
+    B, Hq, Hkv, D, Smax = 3, 8, 2, 128, 1200
+    announce("decode consecutive steps")
+    cos, sin = ref.rope_tables(D, Smax, 5e5)
+    kc = seeded((B, Hkv, Smax, D), 5, torch.bfloat16)
+    vc = seeded((B, Hkv, Smax, D), 6, torch.bfloat16)
+    kcd, vcd = kc.to(DEV), vc.to(DEV)
+    lens = torch.tensor([700, 1023, 5], dtype=torch.int32)
+    for step in range(3):
+        q = seeded((B, 1, Hq, D), 10 + step, torch.bfloat16)
+        kn = seeded((B, 1, Hkv, D), 20 + step, torch.bfloat16)
+        vn = seeded((B, 1, Hkv, D), 30 + step, torch.bfloat16)
+        o_ref, kc, vc = ref.decode_step(q, kn, vn, kc, vc, lens, cos, sin)
+        out = ops.decode_raw(q.to(DEV), kn.to(DEV), vn.to(DEV), kcd, vcd, lens.to(DEV),
+                             cos.to(DEV), sin.to(DEV), rope_row_offset=0, max_len=1100)
+        torch.cuda.synchronize()
+        assert max_abs(out, o_ref) <= 2e-2
+        assert torch.equal(kcd.cpu(), kc) and torch.equal(vcd.cpu(), vc)
+        lens = lens + 1
+    # lens[1] + 1 > max_len: that sequence gets NaN and no cache write
+    lens = torch.tensor([10, 1100, 20], dtype=torch.int32)
+    q = seeded((B, 1, Hq, D), 40, torch.bfloat16)
+    kn = seeded((B, 1, Hkv, D), 41, torch.bfloat16)
+    vn = seeded((B, 1, Hkv, D), 42, torch.bfloat16)
+    before = kcd.clone()
+    out = ops.decode_raw(q.to(DEV), kn.to(DEV), vn.to(DEV), kcd, vcd, lens.to(DEV),
+                         cos.to(DEV), sin.to(DEV), rope_row_offset=0, max_len=1100)
+    torch.cuda.synchronize()
+    assert torch.isnan(out[1].float()).all()
+    assert torch.isfinite(out[0].float()).all() and torch.isfinite(out[2].float()).all()
+    assert torch.equal(kcd[1], before[1])
