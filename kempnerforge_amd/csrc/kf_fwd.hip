@@ -256,7 +256,7 @@ __global__ __launch_bounds__(256, 2) void capture_probs_mfma_kernel(
     int causal) {
   constexpr int KS = D / 16;
   constexpr int KR = D / 8;
-  __shared__ __attribute__((aligned(16))) bf16 sK[BN * D];
+  __shared__ __attribute__((aligned(16))) bf16 sK[2][BN * D];
   __shared__ float sL[ROWS];
   __shared__ int sRowOff[ROWS];  // row offset of (hq, pos) in units of Sk floats, or -1
 
@@ -275,38 +275,54 @@ __global__ __launch_bounds__(256, 2) void capture_probs_mfma_kernel(
   load_q_frag<D>(q, cos, sin, ri, Sq, Hq, hh, qf);
   __syncthreads();
 
-  // per-lane rows this lane stores (register i -> row 8*(i/4)+4h+(i%4) of the wave)
+  // per-lane rows this lane stores (register i -> row 8*(i/4)+4h+(i%4) of the
+  // wave): their P row pointers, log2-domain LSE and positions, hoisted out of
+  // the tile loop
   const int qmax = min(ri.p0 + bm_pos, Sq) - 1;  // largest position in the block
   const int ntiles_all = (Sk + BN - 1) / BN;
   const int ntiles = causal ? min(ntiles_all, (qmax + BN) / BN) : ntiles_all;
   const bf16* kbase = krot + (int64_t)bh * Skp * D;
   float* pbase = probs + (((int64_t)ri.b * Hq + (int64_t)ri.g * n_rep) * Sq + ri.p0) * Sk;
+  float* prow[16];
+  float lrow[16];
+  int posr[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int r = w * 32 + 8 * (i >> 2) + 4 * hh + (i & 3);
+    const int off = sRowOff[r];
+    prow[i] = off < 0 ? nullptr : pbase + (int64_t)off * Sk;
+    lrow[i] = sL[r];
+    posr[i] = ri.p0 + (r % bm_pos);
+  }
 
+  // K tiles double-buffered: tile t+1 loads while tile t is computed and stored
+  if (ntiles > 0) tile_to_lds<BN, KR>(kbase, D, sK[0], w, lane);
   for (int t = 0; t < ntiles; ++t) {
-    __syncthreads();
-    tile_to_lds<BN, KR>(kbase + (int64_t)t * BN * D, D, sK, w, lane);
     lds_copy_wait();
     __syncthreads();
+    if (t + 1 < ntiles) tile_to_lds<BN, KR>(kbase + (int64_t)(t + 1) * BN * D, D, sK[(t + 1) & 1], w, lane);
+    const bf16* tK = sK[t & 1];
+    const bool diag = (causal && t * BN + BN - 1 > ri.p0) || t * BN + BN > Sk;
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
-      f32x16 s;
+      f32x16 sv;
 #pragma unroll
-      for (int i = 0; i < 16; ++i) s[i] = 0.f;
+      for (int i = 0; i < 16; ++i) sv[i] = 0.f;
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
-        const bf16x8 bk = lds_frag<KR>(sK, 32 * nt + c32, 2 * ks + hh);
-        s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qf[ks], bk, s, 0, 0, 0);
+        const bf16x8 bk = lds_frag<KR>(tK, 32 * nt + c32, 2 * ks + hh);
+        sv = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qf[ks], bk, sv, 0, 0, 0);
       }
       const int key = t * BN + 32 * nt + c32;
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        const int r = w * 32 + 8 * (i >> 2) + 4 * hh + (i & 3);
-        const int off = sRowOff[r];
-        if (off < 0 || key >= Sk) continue;
-        const int pos = ri.p0 + (r % bm_pos);
-        float p = fast_exp2(s[i] * scale_log2 - sL[r]);
-        if (causal && key > pos) p = 0.f;
-        __builtin_nontemporal_store(p, pbase + (int64_t)off * Sk + key);
+        if (prow[i] == nullptr) continue;
+        float p = fast_exp2(sv[i] * scale_log2 - lrow[i]);
+        if (diag) {
+          if (key >= Sk) continue;
+          if (causal && key > posr[i]) p = 0.f;
+        }
+        __builtin_nontemporal_store(p, prow[i] + key);
       }
     }
   }
