@@ -522,6 +522,7 @@ int launch_bwd(const BwdArgs& a, void* workspace) {
 }  // namespace
 
 bool bwd_mfma_supported(const BwdArgs& a) {
+  if (a.doc) return false;
   if (a.dtype != BF16 || (a.D != 64 && a.D != 128)) return false;
   const int n_rep = a.Hq / a.Hkv;
   if (n_rep < 1 || n_rep > ROWS) return false;  // also bounds DQ_ROWS / n_rep >= 2

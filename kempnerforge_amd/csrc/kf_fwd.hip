@@ -352,6 +352,7 @@ int pick_bm_pos(int n_rep) { return n_rep <= ROWS ? ROWS / n_rep : 0; }
 
 bool fwd_mfma_supported(const FwdArgs& a) {
   if (a.dtype != BF16 || (a.D != 64 && a.D != 128)) return false;
+  if (a.doc) return false;
   const int n_rep = a.Hq / a.Hkv;
   if (n_rep < 1 || n_rep > ROWS) return false;
   auto al16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };

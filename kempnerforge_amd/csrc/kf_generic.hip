@@ -86,7 +86,7 @@ __global__ __launch_bounds__(256) void fwd_generic_kernel(
     const float* __restrict__ cos, const float* __restrict__ sin, T* __restrict__ out,
     float* __restrict__ lse, int B, int Sq, int Sk, int Hq, int Hkv, int D, int64_t ksb,
     int64_t kss, int64_t ksh, int64_t vsb, int64_t vss, int64_t vsh, int k_rotated, int causal,
-    float scale) {
+    const int32_t* __restrict__ doc, float scale) {
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= (int64_t)B * Hq * Sq) return;
@@ -101,7 +101,9 @@ __global__ __launch_bounds__(256) void fwd_generic_kernel(
   float acc[kMaxPer] = {0.f, 0.f, 0.f, 0.f};
   float m = -INFINITY, l = 0.f;
   const int kend = causal ? min(Sk, i + 1) : Sk;
+  const int di = doc ? doc[(int64_t)b * Sq + i] : 0;
   for (int j = 0; j < kend; ++j) {
+    if (doc && doc[(int64_t)b * Sk + j] != di) continue;  // another document
     float kr[kMaxPer], vv[kMaxPer];
     load_row<T>(k + b * ksb + j * kss + g * ksh, cos, sin, j, D, !k_rotated, lane, kr);
     load_row<T>(v + b * vsb + j * vss + g * vsh, cos, sin, 0, D, false, lane, vv);
@@ -152,7 +154,7 @@ __global__ __launch_bounds__(256) void bwd_dq_generic_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
     const float* __restrict__ cos, const float* __restrict__ sin, const T* __restrict__ dout,
     const float* __restrict__ lse, const float* __restrict__ delta, T* __restrict__ dq, int B,
-    int S, int Hq, int Hkv, int D, int causal, float scale) {
+    int S, int Hq, int Hkv, int D, int causal, const int32_t* __restrict__ doc, float scale) {
   __shared__ float lds[4][256];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int64_t row = (int64_t)blockIdx.x * 4 + w;
@@ -169,7 +171,9 @@ __global__ __launch_bounds__(256) void bwd_dq_generic_kernel(
   const float Di = delta[((int64_t)b * Hq + hq) * S + i];
   float acc[kMaxPer] = {0.f, 0.f, 0.f, 0.f};
   const int kend = causal ? i + 1 : S;
+  const int di = doc ? doc[(int64_t)b * S + i] : 0;
   for (int j = 0; j < kend; ++j) {
+    if (doc && doc[(int64_t)b * S + j] != di) continue;
     const int64_t koff = (((int64_t)b * S + j) * Hkv + g) * D;
     float kr[kMaxPer], vv[kMaxPer];
     load_row<T>(k + koff, cos, sin, j, D, true, lane, kr);
@@ -192,7 +196,8 @@ __global__ __launch_bounds__(256) void bwd_dkdv_generic_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
     const float* __restrict__ cos, const float* __restrict__ sin, const T* __restrict__ dout,
     const float* __restrict__ lse, const float* __restrict__ delta, T* __restrict__ dk,
-    T* __restrict__ dv, int B, int S, int Hq, int Hkv, int D, int causal, float scale) {
+    T* __restrict__ dv, int B, int S, int Hq, int Hkv, int D, int causal,
+    const int32_t* __restrict__ doc, float scale) {
   __shared__ float lds[4][256];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int64_t row = (int64_t)blockIdx.x * 4 + w;
@@ -206,9 +211,11 @@ __global__ __launch_bounds__(256) void bwd_dkdv_generic_kernel(
   load_row<T>(k + koff, cos, sin, j, D, true, lane, kr);
   load_row<T>(v + koff, cos, sin, 0, D, false, lane, vv);
   float adk[kMaxPer] = {0.f, 0.f, 0.f, 0.f}, adv[kMaxPer] = {0.f, 0.f, 0.f, 0.f};
+  const int dj = doc ? doc[(int64_t)b * S + j] : 0;
   for (int hl = 0; hl < n_rep; ++hl) {
     const int hq = g * n_rep + hl;
     for (int i = causal ? j : 0; i < S; ++i) {
+      if (doc && doc[(int64_t)b * S + i] != dj) continue;
       const int64_t qoff = (((int64_t)b * S + i) * Hq + hq) * D;
       float qr[kMaxPer], dor[kMaxPer];
       load_row<T>(q + qoff, cos, sin, i, D, true, lane, qr);
@@ -243,7 +250,7 @@ __global__ __launch_bounds__(256) void capture_probs_generic_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const float* __restrict__ cos,
     const float* __restrict__ sin, const float* __restrict__ lse, float* __restrict__ probs,
     int B, int Sq, int Sk, int Hq, int Hkv, int D, int64_t ksb, int64_t kss, int64_t ksh,
-    int k_rotated, int causal, float scale) {
+    int k_rotated, int causal, const int32_t* __restrict__ doc, float scale) {
   __shared__ float lds[4][256];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int64_t row = (int64_t)blockIdx.x * 4 + w;
@@ -265,9 +272,10 @@ __global__ __launch_bounds__(256) void capture_probs_generic_kernel(
   const float L = lse[((int64_t)b * Hq + hq) * Sq + i];
   float* prow = probs + row * Sk;
   const int half = D / 2;
+  const int di = doc ? doc[(int64_t)b * Sq + i] : 0;
   for (int j = lane; j < Sk; j += 64) {
     float p = 0.f;
-    if (!causal || j <= i) {
+    if ((!causal || j <= i) && (!doc || doc[(int64_t)b * Sk + j] == di)) {
       const T* kr = k + b * ksb + j * kss + g * ksh;
       float s = 0.f;
       for (int d = 0; d < half; ++d) {
@@ -294,7 +302,7 @@ int launch_fwd_generic(const FwdArgs& a) {
   KF_LAUNCH("fwd_generic", (fwd_generic_kernel<T>), grid, dim3(256), 0, a.stream, (const T*)a.q,
                      (const T*)a.k, (const T*)a.v, a.cos, a.sin, (T*)a.out, a.lse, a.B, a.Sq,
                      a.Sk, a.Hq, a.Hkv, a.D, a.ksb, a.kss, a.ksh, a.vsb, a.vss, a.vsh,
-                     a.k_rotated, a.causal, a.scale);
+                     a.k_rotated, a.causal, a.doc, a.scale);
   KF_CHECK_LAUNCH();
   return KF_OK;
 }
@@ -309,12 +317,12 @@ int launch_bwd_generic(const BwdArgs& a, float* delta) {
   KF_LAUNCH("bwd_dq_generic", (bwd_dq_generic_kernel<T>), dim3((unsigned)((qrows + 3) / 4)), dim3(256), 0,
                      a.stream, (const T*)a.q, (const T*)a.k, (const T*)a.v, a.cos, a.sin,
                      (const T*)a.dout, a.lse, delta, (T*)a.dq, a.B, a.S, a.Hq, a.Hkv, a.D,
-                     a.causal, a.scale);
+                     a.causal, a.doc, a.scale);
   KF_CHECK_LAUNCH();
   KF_LAUNCH("bwd_dkdv_generic", (bwd_dkdv_generic_kernel<T>), dim3((unsigned)((krows + 3) / 4)), dim3(256),
                      0, a.stream, (const T*)a.q, (const T*)a.k, (const T*)a.v, a.cos, a.sin,
                      (const T*)a.dout, a.lse, delta, (T*)a.dk, (T*)a.dv, a.B, a.S, a.Hq, a.Hkv,
-                     a.D, a.causal, a.scale);
+                     a.D, a.causal, a.doc, a.scale);
   KF_CHECK_LAUNCH();
   return KF_OK;
 }
@@ -325,7 +333,7 @@ int launch_capture_probs_generic(const FwdArgs& a, const float* lse, float* prob
   KF_LAUNCH("capture_probs_generic", (capture_probs_generic_kernel<T>), dim3((unsigned)((rows + 3) / 4)),
                      dim3(256), 0, a.stream, (const T*)a.q, (const T*)a.k, a.cos, a.sin, lse,
                      probs, a.B, a.Sq, a.Sk, a.Hq, a.Hkv, a.D, a.ksb, a.kss, a.ksh, a.k_rotated,
-                     a.causal, a.scale);
+                     a.causal, a.doc, a.scale);
   KF_CHECK_LAUNCH();
   return KF_OK;
 }

@@ -22,6 +22,8 @@ struct FwdArgs {
   int64_t ksb, kss, ksh, vsb, vss, vsh;
   int k_rotated;      // 1: k already holds post-RoPE keys (KV-cache contents)
   int causal;         // 1: top-left causal mask (query i sees keys j <= i)
+  const int32_t* doc; // [B, S] document id per position (packed sequences) or null;
+                      // query i then also needs doc[i] == doc[j] (requires Sq == Sk)
   int dtype;
   float scale;        // softmax scale, D^-1/2
   hipStream_t stream;
@@ -36,6 +38,7 @@ struct BwdArgs {
   void *dq, *dk, *dv;     // pre-RoPE gradients, same layouts as q, k, v
   int B, S, Hq, Hkv, D;
   int causal, dtype;
+  const int32_t* doc;     // [B, S] document ids or null (see FwdArgs::doc)
   float scale;
   hipStream_t stream;
 };

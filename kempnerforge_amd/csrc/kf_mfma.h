@@ -111,19 +111,6 @@ __device__ __forceinline__ void tile_to_lds(const bf16* __restrict__ g, uint32_t
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4* lds_s16x4_ptr;
 
-// A-operand fragment of a transposed product, read from a row-major swizzled
-// [rows][R chunks] LDS tile with two ds_read_b64_tr_b16.
-//
-// ds_read_b64_tr_b16 works on groups of 16 lanes: address-lane a of a group
-// fetches 4 contiguous 16-bit elements, and result-lane i receives element
-// (i % 4) of the chunk fetched by address-lane 4e + i/4, for e = 0..3 (the 16
-// lanes' 64 elements read as a 4x16 block, one column per lane).  Address-lane
-// a = 4e + k of group G therefore fetches row r0 + 4h + e (h = lane / 32),
-// columns c0 + 16 (G % 2) + 4k .. +3, and result-lane l ends up holding column
-// c0 + l % 32 of rows r0 + 4h + e: exactly slots j = 0..3 of the fragment whose
-// slot (h, j) carries row r0 + (j < 4 ? 4h + j : 8 + 4h + j - 4).  The second
-// read (rows + 8) fills slots 4..7.  That is the slot order of the P^T / dS
-// B operands built from the 32x32 C layout, so the products line up.
 // Per-lane byte offsets for lds_frag_t on a [rows][D] tile: fragment (c, dt)
 // covers rows 16c..16c+15 and columns 32dt..32dt+31.  Rows are 16-aligned, so
 // the swizzle term does not depend on c and each lane needs only one

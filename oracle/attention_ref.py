@@ -100,15 +100,27 @@ def _causal_mask(sq: int, sk: int) -> torch.Tensor:
     return torch.ones(sq, sk, dtype=torch.bool).triu(diagonal=1)
 
 
-def _scores(qf, kf, causal):
+def _doc_mask(doc_ids) -> torch.Tensor:
+    """True where masked: query ``i`` and key ``j`` of a packed sequence belong
+    to different documents (``doc_ids[b,i] != doc_ids[b,j]``), ``[B,1,S,S]``.
+    Follows ``kempnerforge/model/attention.py:211-216``: the explicit mask is
+    ``causal & (doc_ids[:, :, None] == doc_ids[:, None, :])``."""
+    d = torch.as_tensor(doc_ids)
+    return (d.unsqueeze(2) != d.unsqueeze(1)).unsqueeze(1)
+
+
+def _scores(qf, kf, causal, doc_ids=None):
     d = qf.shape[-1]
     s = torch.matmul(qf, kf.transpose(-2, -1)) * (d ** -0.5)
     if causal:
         s = s.masked_fill(_causal_mask(s.shape[-2], s.shape[-1]), float("-inf"))
+    if doc_ids is not None:
+        s = s.masked_fill(_doc_mask(doc_ids), float("-inf"))
     return s
 
 
-def attention_fwd(q, k, v, cos, sin, *, causal: bool = True, compute_dtype=torch.float64):
+def attention_fwd(q, k, v, cos, sin, *, causal: bool = True, compute_dtype=torch.float64,
+                  doc_ids=None):
     """Causal GQA attention with fused RoPE; returns ``(out, lse)``.
 
     q ``[B,Sq,Hq,D]``, k/v ``[B,Sk,Hkv,D]`` (pre-RoPE), cos/sin ``[S, D/2]``
@@ -119,14 +131,15 @@ def attention_fwd(q, k, v, cos, sin, *, causal: bool = True, compute_dtype=torch
     Follows ``kempnerforge/model/attention.py:160-175`` (transpose, RoPE, GQA
     expansion) and ``:228-231`` (``F.scaled_dot_product_attention`` with default
     scale ``D^-1/2`` and ``is_causal``).  The reference returns no LSE; it is the
-    closed form ``log sum_j exp(s_ij)``.
+    closed form ``log sum_j exp(s_ij)``.  With ``doc_ids [B,S]`` (packed
+    sequences, ``:204-227``) a query also sees only keys of its own document.
     """
     qr, kr, vt = _rotated_bhsd(q, k, v, cos, sin)
     n_rep = qr.shape[1] // kr.shape[1]
     qf = qr.to(compute_dtype)
     kf = gqa_expand(kr, n_rep).to(compute_dtype)
     vf = gqa_expand(vt, n_rep).to(compute_dtype)
-    s = _scores(qf, kf, causal)
+    s = _scores(qf, kf, causal, doc_ids)
     lse = torch.logsumexp(s, dim=-1)
     p = torch.exp(s - lse.unsqueeze(-1))
     out = torch.matmul(p, vf)
@@ -182,7 +195,8 @@ def attention_fwd_rotated(q, k_cache, v_cache, cos, sin, *, causal: bool = True,
     return out.transpose(1, 2).contiguous(), lse
 
 
-def attention_bwd(q, k, v, cos, sin, dout, *, causal: bool = True, compute_dtype=torch.float64):
+def attention_bwd(q, k, v, cos, sin, dout, *, causal: bool = True, compute_dtype=torch.float64,
+                  doc_ids=None):
     """Gradients ``(dq, dk, dv)`` of :func:`attention_fwd`'s output, pre-RoPE, BSHD.
 
     The reference gets these from autograd (``scripts/train.py:850``) through
@@ -199,7 +213,7 @@ def attention_bwd(q, k, v, cos, sin, dout, *, causal: bool = True, compute_dtype
     kf = kr.to(compute_dtype).detach().requires_grad_(True)
     vf = vt.to(compute_dtype).detach().requires_grad_(True)
     with torch.enable_grad():
-        s = _scores(qf, gqa_expand(kf, n_rep), causal)
+        s = _scores(qf, gqa_expand(kf, n_rep), causal, doc_ids)
         p = torch.softmax(s, dim=-1)
         out = torch.matmul(p, gqa_expand(vf, n_rep))
         out.backward(dout.transpose(1, 2).to(compute_dtype))
@@ -249,7 +263,8 @@ def decode_step(q_new, k_new, v_new, k_cache, v_cache, lens, cos_table, sin_tabl
     return torch.cat(outs, dim=0), k_cache, v_cache
 
 
-def capture(q, k, v, cos, sin, *, causal: bool = True, compute_dtype=torch.float64):
+def capture(q, k, v, cos, sin, *, causal: bool = True, compute_dtype=torch.float64,
+            doc_ids=None):
     """Materialised attention probabilities; returns ``(out BSHD, P [B,Hq,Sq,Sk])``.
 
     Follows ``kempnerforge/model/attention.py:238-280``: ``QK^T * D^-1/2``
@@ -262,7 +277,7 @@ def capture(q, k, v, cos, sin, *, causal: bool = True, compute_dtype=torch.float
     qf = qr.to(compute_dtype)
     kf = gqa_expand(kr, n_rep).to(compute_dtype)
     vf = gqa_expand(vt, n_rep).to(compute_dtype)
-    p = torch.softmax(_scores(qf, kf, causal), dim=-1)
+    p = torch.softmax(_scores(qf, kf, causal, doc_ids), dim=-1)
     out = torch.matmul(p, vf)
     return out.transpose(1, 2).contiguous(), p
 

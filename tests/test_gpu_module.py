@@ -149,9 +149,10 @@ def test_generate_style_decode_matches_full_forward():
         attn(x[:, :1], cos[:1], sin[:1], kv_cache=cache)
 
 
-def test_doc_ids_branch_kept():
-    # explicit-mask branch (reference :190-227); one document equals causal
-    # (reference tests/unit/test_packing.py:269-277)
+def test_one_document_equals_causal():
+    # packed-document path (reference :190-227) with one document equals plain
+    # causal (reference tests/unit/test_packing.py:269-277); an all-True
+    # key_padding_mask (the explicit-mask branch kept in PyTorch) too
     torch.manual_seed(0)
     attn = Attention(128, 4, 2).to(DEV)
     cos, sin = precompute_rope_frequencies(32, 32)
@@ -159,4 +160,6 @@ def test_doc_ids_branch_kept():
     x = torch.randn(2, 32, 128, device=DEV)
     a = attn(x, cos, sin)
     b = attn(x, cos, sin, doc_ids=torch.zeros(2, 32, dtype=torch.long, device=DEV))
+    c = attn(x, cos, sin, key_padding_mask=torch.ones(2, 32, dtype=torch.bool, device=DEV))
     assert torch.allclose(a, b, atol=1e-4)
+    assert torch.allclose(a, c, atol=1e-4)

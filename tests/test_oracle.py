@@ -284,6 +284,83 @@ class TestBackward:
         assert torch.allclose(dv, vv.grad, atol=1e-10)
 
 
+# --------------------------------------------------------------------------- packed documents
+def _packed_doc_ids(B, lengths_per_row):
+    """[B, S] int64 document ids, contiguous increasing segments per row (what
+    the packing dataset produces, kempnerforge/data/dataset.py:27-65)."""
+    rows = []
+    for lens in lengths_per_row:
+        rows.append(torch.cat([torch.full((n,), d, dtype=torch.long) for d, n in enumerate(lens)]))
+    return torch.stack(rows)
+
+
+def _sdpa_doc_reference(q, k, v, cos, sin, doc_ids):
+    """The reference's packed-sequence branch with PyTorch's library SDPA in
+    float64: explicit bool mask causal & same-document
+    (kempnerforge/model/attention.py:204-227)."""
+    qr = ref.apply_rope(q.transpose(1, 2), cos, sin).double()
+    kr = ref.apply_rope(k.transpose(1, 2), cos, sin).double()
+    vt = v.transpose(1, 2).double()
+    n_rep = q.shape[2] // k.shape[2]
+    kr = kr.repeat_interleave(n_rep, dim=1)
+    vt = vt.repeat_interleave(n_rep, dim=1)
+    S = q.shape[1]
+    causal = torch.ones(S, S, dtype=torch.bool).tril().unsqueeze(0).unsqueeze(0)
+    mask = causal & (doc_ids.unsqueeze(2) == doc_ids.unsqueeze(1)).unsqueeze(1)
+    mask = mask | ~mask.any(dim=-1, keepdim=True)
+    return F.scaled_dot_product_attention(qr, kr, vt, attn_mask=mask).transpose(1, 2)
+
+
+class TestPackedDocuments:
+    def test_matches_library_sdpa_with_explicit_mask(self):
+        q, k, v, cos, sin = _inputs(2, 29, 4, 2, 16, torch.bfloat16, seed=21)
+        doc = _packed_doc_ids(2, [[7, 1, 13, 8], [29]])
+        out, _ = ref.attention_fwd(q, k, v, cos, sin, doc_ids=doc)
+        assert torch.allclose(out, _sdpa_doc_reference(q, k, v, cos, sin, doc), atol=1e-12)
+
+    def test_equals_separate_documents(self):
+        # rows of document d equal attention over that document alone (same
+        # absolute RoPE positions): documents are independent
+        q, k, v, cos, sin = _inputs(1, 24, 4, 1, 8, torch.float32, seed=22)
+        lens = [5, 11, 8]
+        doc = _packed_doc_ids(1, [lens])
+        out, lse = ref.attention_fwd(q, k, v, cos, sin, doc_ids=doc)
+        start = 0
+        for n in lens:
+            sl = slice(start, start + n)
+            o_d, l_d = ref.attention_fwd(q[:, sl], k[:, sl], v[:, sl], cos[sl], sin[sl])
+            assert torch.allclose(out[:, sl], o_d, atol=1e-13)
+            assert torch.allclose(lse[:, :, sl], l_d, atol=1e-13)
+            start += n
+
+    def test_single_document_is_plain_causal(self):
+        q, k, v, cos, sin = _inputs(2, 17, 4, 2, 8, torch.float32, seed=23)
+        out_d, lse_d = ref.attention_fwd(q, k, v, cos, sin, doc_ids=torch.zeros(2, 17, dtype=torch.long))
+        out, lse = ref.attention_fwd(q, k, v, cos, sin)
+        assert torch.equal(out_d, out) and torch.equal(lse_d, lse)
+
+    def test_backward_matches_library_autograd(self):
+        B, S, Hq, Hkv, D = 2, 21, 4, 2, 8
+        q, k, v, cos, sin = _inputs(B, S, Hq, Hkv, D, torch.float64, seed=24)
+        cos, sin = cos.double(), sin.double()
+        doc = _packed_doc_ids(B, [[4, 9, 8], [21]])
+        do = torch.randn(B, S, Hq, D, generator=torch.Generator().manual_seed(25),
+                         dtype=torch.float64)
+        qq, kk, vv = (t.clone().requires_grad_(True) for t in (q, k, v))
+        _sdpa_doc_reference(qq, kk, vv, cos, sin, doc).backward(do)
+        dq, dk, dv = ref.attention_bwd(q, k, v, cos, sin, do, doc_ids=doc)
+        assert torch.allclose(dq, qq.grad, atol=1e-10)
+        assert torch.allclose(dk, kk.grad, atol=1e-10)
+        assert torch.allclose(dv, vv.grad, atol=1e-10)
+
+    def test_capture_rows_and_zeros(self):
+        q, k, v, cos, sin = _inputs(1, 12, 2, 1, 8, torch.float32, seed=26)
+        doc = _packed_doc_ids(1, [[5, 7]])
+        _, P = ref.capture(q, k, v, cos, sin, doc_ids=doc)
+        assert torch.allclose(P.sum(-1), torch.ones_like(P.sum(-1)), atol=1e-12)
+        assert torch.all(P[..., 5:, :5] == 0) and torch.all(P[..., :5, 5:] == 0)
+
+
 # --------------------------------------------------------------------------- decode
 class TestDecode:
     def _setup(self, lens, Smax=24, B=3, Hq=4, Hkv=2, D=8, dtype=torch.float32):
