@@ -21,6 +21,11 @@
 //               RoPE backward is applied at the dQ store.
 // The algorithm is the standard flash-attention backward (recompute P from the
 // saved log-sum-exp; dS = P o (dP - Delta)).
+//
+// Packed documents (DOC): kv_prep records each 64-position tile's document-id
+// range.  dkdv walks only the query tiles whose range meets its key block's,
+// dq only the key tiles whose range meets its rows'; tiles not entirely in the
+// workgroup's single document get P = 0 where doc[query] != doc[key].
 #include "kf_common.h"
 #include "kf_internal.h"
 #include "kf_mfma.h"
@@ -101,14 +106,17 @@ struct DkdvStage {
   float l[BQ], dl[BQ];
 };
 
-template <int D, bool DSROLE>
+// DOC: qlist[0, nlist) holds the listed query tiles (DOC_MASK_FLAG: needs the
+// element test), sQD the staged query documents, drow the batch row's ids.
+template <int D, bool DSROLE, bool DOC>
 __device__ __forceinline__ void dkdv_role(
     DkdvStage<D>* st, u32x4* sP, const bf16* __restrict__ krot, const bf16* __restrict__ vn,
     const bf16* __restrict__ qrot, const bf16* __restrict__ don,
     const float* __restrict__ lse2, const float* __restrict__ delta,
     const float* __restrict__ cos, const float* __restrict__ sin, bf16* __restrict__ dk,
     bf16* __restrict__ dv, int S, int P, int Hq, int Hkv, int n_rep, int b, int g, int bh, int k0,
-    int w, int lane, float scale_log2, float scale, int causal) {
+    int w, int lane, float scale_log2, float scale, int causal, const int32_t* __restrict__ drow,
+    const uint16_t* qlist, int nlist, int32_t (*sQD)[BQ]) {
   constexpr int KS = D / 16, DT = D / 32, HALF = D / 2;
   constexpr int KR = D / 8;
   constexpr int PF = 3;  // fragment reads run PF MFMAs ahead
@@ -118,11 +126,17 @@ __device__ __forceinline__ void dkdv_role(
 
   const int nqt = (S + BQ - 1) / BQ;
   const int qt0 = causal ? k0 / BQ : 0;
-  const int per_head = nqt - qt0;
+  const int per_head = DOC ? nlist : nqt - qt0;
   const int total = per_head > 0 ? per_head * n_rep : 0;
+  // iteration -> query tile entry (tile | DOC_MASK_FLAG for DOC), head-major
+  auto entry = [&](int it) -> int {
+    return DOC ? __builtin_amdgcn_readfirstlane((int)qlist[it % per_head]) : qt0 + it % per_head;
+  };
+  auto tile_of = [](int e) -> int { return DOC ? e & ~DOC_MASK_FLAG : e; };
+  const int kdoc = DOC ? drow[min(key, S - 1)] : 0;
 
   auto stage = [&](int it, int buf) {
-    const int hl = it / per_head, qtile = qt0 + it % per_head;
+    const int hl = it / per_head, qtile = tile_of(entry(it));
     const int64_t bhq = (int64_t)b * Hq + g * n_rep + hl;
     const int q0 = qtile * BQ;
     DkdvStage<D>& S_ = st[buf];
@@ -130,6 +144,7 @@ __device__ __forceinline__ void dkdv_role(
     tile_to_lds<BQ, KR, 8>(don + (bhq * P + q0) * D, D, S_.o, w, lane);
     if (w == 0) row_to_lds(lse2 + bhq * P + q0, S_.l, lane);
     if (w == 1) row_to_lds(delta + bhq * P + q0, S_.dl, lane);
+    if (DOC && w == 2) dma4(lds_addr(sQD[buf]), (uint32_t)min(q0 + lane, S - 1) * 4u, drow);
   };
   if (total > 0) stage(0, 0);
 
@@ -160,9 +175,11 @@ __device__ __forceinline__ void dkdv_role(
     const int buf = it & 1;
     if (it + 1 < total) stage(it + 1, buf ^ 1);
     const DkdvStage<D>& S_ = st[buf];
-    const int q0 = (qt0 + it % per_head) * BQ;
+    const int e = entry(it);
+    const int q0 = tile_of(e) * BQ;
     const int rel = key - q0;  // rows r of this tile see the key when r >= rel
     const bool diag = causal && q0 < k0 + BKV;
+    const bool dmask = DOC && (e & DOC_MASK_FLAG);
 
     // phase 1: S (P waves) or dP (dS waves) for both 32-row halves
     f32x16 x[2];
@@ -192,10 +209,15 @@ __device__ __forceinline__ void dkdv_role(
           const f32x4 l4 = *(const f32x4*)(&S_.l[r0]);
           float v[4];
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            float p = fast_exp2(__builtin_fmaf(x[mt][4 * gq + e], scale_log2, -l4[e]));
-            if (diag) p = (rel > r0 + e) ? 0.f : p;
-            v[e] = p;
+          for (int j = 0; j < 4; ++j) {
+            float p = fast_exp2(__builtin_fmaf(x[mt][4 * gq + j], scale_log2, -l4[j]));
+            if (diag) p = (rel > r0 + j) ? 0.f : p;
+            v[j] = p;
+          }
+          if (dmask) {
+            const i32x4 qd = *(const i32x4*)&sQD[buf][r0];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) v[j] = qd[j] != kdoc ? 0.f : v[j];
           }
           pk[2 * mt + (gq >> 1)][2 * (gq & 1)] = pack2(v[0], v[1]);
           pk[2 * mt + (gq >> 1)][2 * (gq & 1) + 1] = pack2(v[2], v[3]);
@@ -217,13 +239,13 @@ __device__ __forceinline__ void dkdv_role(
             const f32x4 d4 = *(const f32x4*)(&S_.dl[r0]);
             float v[4];
 #pragma unroll
-            for (int e = 0; e < 2; ++e) {
-              const uint32_t word = pp[2 * half + e];
-              v[2 * e] = __uint_as_float(word << 16);
-              v[2 * e + 1] = __uint_as_float(word & 0xffff0000u);
+            for (int j = 0; j < 2; ++j) {
+              const uint32_t word = pp[2 * half + j];
+              v[2 * j] = __uint_as_float(word << 16);
+              v[2 * j + 1] = __uint_as_float(word & 0xffff0000u);
             }
 #pragma unroll
-            for (int e = 0; e < 4; ++e) v[e] *= x[mt][4 * gq + e] - d4[e];
+            for (int j = 0; j < 4; ++j) v[j] *= x[mt][4 * gq + j] - d4[j];
             pk[2 * mt + cc][2 * half] = pack2(v[0], v[1]);
             pk[2 * mt + cc][2 * half + 1] = pack2(v[2], v[3]);
           }
@@ -281,45 +303,66 @@ __device__ __forceinline__ void dkdv_role(
   }
 }
 
-template <int D>
+template <int D, bool DOC>
 __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(
     const bf16* __restrict__ krot, const bf16* __restrict__ vn, const bf16* __restrict__ qrot,
     const bf16* __restrict__ don, const float* __restrict__ lse2, const float* __restrict__ delta,
     const float* __restrict__ cos, const float* __restrict__ sin, bf16* __restrict__ dk,
     bf16* __restrict__ dv, int S, int P, int Hq, int Hkv, int n_rep, int nkb, float scale_log2,
-    float scale, int causal) {
+    float scale, int causal, const int32_t* __restrict__ doc, const int2* __restrict__ ranges) {
   __shared__ __attribute__((aligned(16))) DkdvStage<D> st[2];
   __shared__ __attribute__((aligned(16))) u32x4 sP[4 * 4 * 64];  // [key group][chunk][lane]
+  __shared__ __attribute__((aligned(16))) int32_t sQD[2][BQ];   // DOC: query document ids
+  __shared__ uint16_t sList[DOC_MAX_TILES];                      // DOC: listed query tiles
+  __shared__ int sCount;
   const int w = wave_id(), lane = threadIdx.x & 63;
   const int logical = xcd_logical_id(blockIdx.x, gridDim.x);
   const int bh = logical / nkb;
   const int kb = logical % nkb;  // ascending: the longest causal key tiles first
   const int b = bh / Hkv, g = bh % Hkv;
   const int k0 = kb * BKV;
+  const int32_t* drow = DOC ? doc + (int64_t)b * S : nullptr;
+  int nlist = 0;
+  if constexpr (DOC) {
+    if (w == 0) {
+      const int2 span = doc_span(drow, k0, min(k0 + BKV, S), lane);
+      const int n = doc_tile_list(ranges + (int64_t)b * (P / BN), causal ? k0 / BQ : 0,
+                                  (S + BQ - 1) / BQ, span, sList, lane);
+      if (lane == 0) sCount = n;
+    }
+    __syncthreads();
+    nlist = __builtin_amdgcn_readfirstlane(sCount);
+  }
   if (w >= 4)
-    dkdv_role<D, true>(st, sP, krot, vn, qrot, don, lse2, delta, cos, sin, dk, dv, S, P, Hq,
-                       Hkv, n_rep, b, g, bh, k0, w, lane, scale_log2, scale, causal);
+    dkdv_role<D, true, DOC>(st, sP, krot, vn, qrot, don, lse2, delta, cos, sin, dk, dv, S, P, Hq,
+                            Hkv, n_rep, b, g, bh, k0, w, lane, scale_log2, scale, causal, drow,
+                            sList, nlist, sQD);
   else
-    dkdv_role<D, false>(st, sP, krot, vn, qrot, don, lse2, delta, cos, sin, dk, dv, S, P, Hq,
-                        Hkv, n_rep, b, g, bh, k0, w, lane, scale_log2, scale, causal);
+    dkdv_role<D, false, DOC>(st, sP, krot, vn, qrot, don, lse2, delta, cos, sin, dk, dv, S, P,
+                             Hq, Hkv, n_rep, b, g, bh, k0, w, lane, scale_log2, scale, causal,
+                             drow, sList, nlist, sQD);
 }
 
 // dQ workgroup: 8 wavefronts x 32 rows = 256 (query head, position) rows of one
 // KV group, all sharing each staged K / V / K^T tile (two wavefronts per SIMD).
 constexpr int DQ_ROWS = 256;
 
-template <int D>
+template <int D, bool DOC>
 __global__ __launch_bounds__(512, 1) void bwd_dq_kernel(
     const bf16* __restrict__ qrot, const bf16* __restrict__ don, const float* __restrict__ lse2,
     const float* __restrict__ delta, const bf16* __restrict__ krot, const bf16* __restrict__ vn,
-    const float* __restrict__ cos, const float* __restrict__ sin, bf16* __restrict__ dq, int S, int P, int Hq, int Hkv, int n_rep, int bm_pos, int nqb,
-    float scale_log2, float scale, int causal) {
+    const float* __restrict__ cos, const float* __restrict__ sin, bf16* __restrict__ dq, int S,
+    int P, int Hq, int Hkv, int n_rep, int bm_pos, int nqb, float scale_log2, float scale,
+    int causal, const int32_t* __restrict__ doc, const int2* __restrict__ ranges) {
   constexpr int KS = D / 16, DT = D / 32, HALF = D / 2;
   constexpr int KR = D / 8;
   struct Stage {
     bf16 k[BN * D], v[BN * D];
   };
   __shared__ __attribute__((aligned(16))) Stage st[2];
+  __shared__ __attribute__((aligned(16))) int32_t sKD[2][BN];  // DOC: key document ids
+  __shared__ uint16_t sList[DOC_MAX_TILES];                     // DOC: listed key tiles
+  __shared__ int sCount;
 
   const int tid = threadIdx.x, w = wave_id(), lane = tid & 63, hh = lane >> 5, c32 = lane & 31;
   const int logical = xcd_logical_id(blockIdx.x, gridDim.x);
@@ -328,14 +371,31 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_kernel(
   const int64_t bhq = (int64_t)ri.b * Hq + ri.hq;
 
   const int kend = causal ? min(S, ri.p0 + bm_pos) : S;
-  const int ntiles = (kend + BN - 1) / BN;
+  int ntiles = (kend + BN - 1) / BN;
+  const int32_t* drow = DOC ? doc + (int64_t)ri.b * S : nullptr;
+  int di = 0;
+  if constexpr (DOC) {
+    di = drow[min(ri.pos, S - 1)];
+    if (w == 0) {
+      const int2 span = doc_span(drow, ri.p0, min(ri.p0 + bm_pos, S), lane);
+      const int n = doc_tile_list(ranges + (int64_t)ri.b * (P / BN), 0, ntiles, span, sList, lane);
+      if (lane == 0) sCount = n;
+    }
+    __syncthreads();
+    ntiles = __builtin_amdgcn_readfirstlane(sCount);
+  }
+  auto entry = [&](int it) -> int {
+    return DOC ? __builtin_amdgcn_readfirstlane((int)sList[it]) : it;
+  };
+  auto tile_of = [](int e) -> int { return DOC ? e & ~DOC_MASK_FLAG : e; };
   const bf16* kbase = krot + (int64_t)bh * P * D;
   const bf16* vbase = vn + (int64_t)bh * P * D;
   auto stage = [&](int t, int buf) {
     tile_to_lds<BN, KR, 8>(kbase + (int64_t)t * BN * D, D, st[buf].k, w, lane);
     tile_to_lds<BN, KR, 8>(vbase + (int64_t)t * BN * D, D, st[buf].v, w, lane);
+    if (DOC && w == 0) dma4(lds_addr(sKD[buf]), (uint32_t)min(t * BN + lane, S - 1) * 4u, drow);
   };
-  if (ntiles > 0) stage(0, 0);
+  if (ntiles > 0) stage(tile_of(entry(0)), 0);
 
   bf16x8 qf[KS], df[KS];
   float l2 = INFINITY, dl = 0.f;
@@ -373,12 +433,15 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_kernel(
   }
   settle(l2);
   settle(dl);
-  for (int t = 0; t < ntiles; ++t) {
-    const int buf = t & 1;
-    if (t + 1 < ntiles) stage(t + 1, buf ^ 1);
+  for (int it = 0; it < ntiles; ++it) {
+    const int buf = it & 1;
+    const int e = entry(it);
+    const int t = tile_of(e);
+    if (it + 1 < ntiles) stage(tile_of(entry(it + 1)), buf ^ 1);
     const Stage& S_ = st[buf];
     const int k0 = t * BN;
-    const bool need_mask = (causal && k0 + BN - 1 > ri.p0) || (k0 + BN > S);
+    const bool dmask = DOC && (e & DOC_MASK_FLAG);
+    const bool need_mask = (causal && k0 + BN - 1 > ri.p0) || (k0 + BN > S) || dmask;
     // last visible key of this lane's row, relative to k0
     const int lim = (causal ? min(ri.pos, S - 1) : S - 1) - k0;
 #pragma unroll
@@ -414,14 +477,22 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_kernel(
 #pragma unroll
       for (int i = 0; i < 16; i += 2) {
         float dsv[2];
+        // DOC: documents of this pair's two keys (adjacent: i even)
+        int kd[2] = {0, 0};
+        if (dmask) {
+          const int local0 = 32 * mt + 8 * (i >> 2) + 4 * hh + (i & 3);
+          kd[0] = sKD[buf][local0];
+          kd[1] = sKD[buf][local0 + 1];
+        }
 #pragma unroll
-        for (int e = 0; e < 2; ++e) {
-          float p = fast_exp2(__builtin_fmaf(s[i + e], scale_log2, -l2));
+        for (int j = 0; j < 2; ++j) {
+          float p = fast_exp2(__builtin_fmaf(s[i + j], scale_log2, -l2));
           if (need_mask) {
-            const int local = 32 * mt + 8 * ((i + e) >> 2) + 4 * hh + ((i + e) & 3);
+            const int local = 32 * mt + 8 * ((i + j) >> 2) + 4 * hh + ((i + j) & 3);
             p = local > lim ? 0.f : p;
+            if (dmask) p = kd[j] != di ? 0.f : p;
           }
-          dsv[e] = p * (dp[i + e] - dl);
+          dsv[j] = p * (dp[i + j] - dl);
         }
         dsk[i >> 3][(i & 7) >> 1] = pack2(dsv[0], dsv[1]);
       }
@@ -469,6 +540,7 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_kernel(
 struct Ws {
   bf16 *krot, *vn, *qrot, *don;
   float *lse2, *delta;
+  int2* ranges;  // [B][P/64] document-id range per tile (packed documents only)
 };
 
 Ws carve(void* base, int B, int S, int Hq, int Hkv, int D) {
@@ -482,7 +554,8 @@ Ws carve(void* base, int B, int S, int Hq, int Hkv, int D) {
   w.don = p; p += qq;
   float* f = (float*)p;
   w.lse2 = f; f += (size_t)B * Hq * P;
-  w.delta = f;
+  w.delta = f; f += (size_t)B * Hq * P;
+  w.ranges = (int2*)f;
   return w;
 }
 
@@ -499,22 +572,26 @@ int launch_bwd(const BwdArgs& a, void* workspace) {
   fa.kss = fa.vss = (int64_t)a.Hkv * D;
   fa.ksh = fa.vsh = D;
   fa.k_rotated = 0; fa.dtype = BF16; fa.stream = a.stream;
-  int rc = launch_kv_prep(fa, w.krot, w.vn, P);
+  fa.doc = a.doc; fa.causal = a.causal;
+  int rc = launch_kv_prep(fa, w.krot, w.vn, P, w.ranges);
   if (rc) return rc;
   KF_LAUNCH("q_prep_bwd", q_prep_bwd_kernel<D>, dim3(P / BN, a.B * a.Hq), dim3(256), 0, a.stream,
             (const bf16*)a.q, (const bf16*)a.out, (const bf16*)a.dout, a.lse, a.cos, a.sin,
             w.qrot, w.don, w.lse2, w.delta, a.S, P, a.Hq);
   KF_CHECK_LAUNCH();
   const int nkb = P / BKV;
-  KF_LAUNCH("bwd_dkdv", bwd_dkdv_kernel<D>, dim3(nkb * a.B * a.Hkv), dim3(512), 0, a.stream,
-            w.krot, w.vn, w.qrot, w.don, w.lse2, w.delta, a.cos, a.sin, (bf16*)a.dk,
-            (bf16*)a.dv, a.S, P, a.Hq, a.Hkv, n_rep, nkb, scale_log2, a.scale, a.causal);
+  const bool doc = a.doc != nullptr;
+  KF_LAUNCH("bwd_dkdv", (doc ? bwd_dkdv_kernel<D, true> : bwd_dkdv_kernel<D, false>),
+            dim3(nkb * a.B * a.Hkv), dim3(512), 0, a.stream, w.krot, w.vn, w.qrot, w.don, w.lse2,
+            w.delta, a.cos, a.sin, (bf16*)a.dk, (bf16*)a.dv, a.S, P, a.Hq, a.Hkv, n_rep, nkb,
+            scale_log2, a.scale, a.causal, a.doc, w.ranges);
   KF_CHECK_LAUNCH();
   const int bm_pos = DQ_ROWS / n_rep;
   const int nqb = (a.S + bm_pos - 1) / bm_pos;
-  KF_LAUNCH("bwd_dq", bwd_dq_kernel<D>, dim3(nqb * a.B * a.Hkv), dim3(512), 0, a.stream, w.qrot,
-            w.don, w.lse2, w.delta, w.krot, w.vn, a.cos, a.sin, (bf16*)a.dq, a.S, P, a.Hq, a.Hkv,
-            n_rep, bm_pos, nqb, scale_log2, a.scale, a.causal);
+  KF_LAUNCH("bwd_dq", (doc ? bwd_dq_kernel<D, true> : bwd_dq_kernel<D, false>),
+            dim3(nqb * a.B * a.Hkv), dim3(512), 0, a.stream, w.qrot, w.don, w.lse2, w.delta,
+            w.krot, w.vn, a.cos, a.sin, (bf16*)a.dq, a.S, P, a.Hq, a.Hkv, n_rep, bm_pos, nqb,
+            scale_log2, a.scale, a.causal, a.doc, w.ranges);
   KF_CHECK_LAUNCH();
   return KF_OK;
 }
@@ -522,7 +599,7 @@ int launch_bwd(const BwdArgs& a, void* workspace) {
 }  // namespace
 
 bool bwd_mfma_supported(const BwdArgs& a) {
-  if (a.doc) return false;
+  if (a.doc && pad_len(a.S) / BN > DOC_MAX_TILES) return false;
   if (a.dtype != BF16 || (a.D != 64 && a.D != 128)) return false;
   const int n_rep = a.Hq / a.Hkv;
   if (n_rep < 1 || n_rep > ROWS) return false;  // also bounds DQ_ROWS / n_rep >= 2
@@ -534,7 +611,7 @@ bool bwd_mfma_supported(const BwdArgs& a) {
 size_t bwd_mfma_workspace(int B, int S, int Hq, int Hkv, int D) {
   const size_t P = (size_t)pad_len(S);
   return (2 * (size_t)B * Hkv + 2 * (size_t)B * Hq) * P * D * sizeof(uint16_t) +
-         2 * (size_t)B * Hq * P * sizeof(float);
+         2 * (size_t)B * Hq * P * sizeof(float) + (size_t)B * (P / BN) * sizeof(int2);
 }
 
 int bwd_mfma(const BwdArgs& a, void* workspace) {

@@ -4,6 +4,7 @@
 //  kv_prep   stages one KV head's keys and values in the layout the MFMA loop
 //            reads: K rotated by RoPE (eager bf16 rounding) and V, both
 //            [bh][Skp][D] with keys >= Sk zeroed.  The backward uses it too.
+//            With document ids it also records each 64-key tile's id range.
 //  fwd_mfma  flash forward.  One workgroup = 4 wavefronts = 128 "rows", where
 //            a row is (query head of the KV group, position): every K/V tile in
 //            LDS is shared by all n_rep query heads of the group.  Each wave
@@ -34,13 +35,21 @@ __global__ __launch_bounds__(256) void kv_prep_kernel(
     const bf16* __restrict__ k, const bf16* __restrict__ v, const float* __restrict__ cos,
     const float* __restrict__ sin, bf16* __restrict__ krot, bf16* __restrict__ vn, int Sk,
     int Skp, int Hkv, int64_t ksb, int64_t kss, int64_t ksh, int64_t vsb, int64_t vss,
-    int64_t vsh, int k_rotated) {
+    int64_t vsh, int k_rotated, const int32_t* __restrict__ doc, int2* __restrict__ ranges) {
   constexpr int HALF = D / 2;
   constexpr int CP = HALF / 8;
   const int s0 = blockIdx.x * BN;
   const int bh = blockIdx.y;
   const int b = bh / Hkv, g = bh % Hkv;
   const int tid = threadIdx.x;
+
+  if (doc != nullptr && g == 0 && tid < 64) {
+    // document-id range of this tile (empty: min > max, when all keys >= Sk)
+    const int s = s0 + tid;
+    const int d = s < Sk ? doc[(int64_t)b * Sk + s] : 0;
+    const int lo = wave_min_i(s < Sk ? d : INT_MAX), hi = wave_max_i(s < Sk ? d : INT_MIN);
+    if (tid == 0) ranges[(int64_t)b * gridDim.x + blockIdx.x] = make_int2(lo, hi);
+  }
 
   for (int it = tid; it < BN * CP; it += 256) {
     const int key = it / CP, c = it % CP;
@@ -106,16 +115,26 @@ __device__ __forceinline__ void load_q_frag(const bf16* __restrict__ q,
   }
 }
 
-template <int D>
+// DOC: packed documents (doc != null, causal, Sq == Sk).  The workgroup walks
+// only the key tiles listed by doc_tile_list; listed tiles carrying the mask
+// flag get the element test doc[key] == doc[query] next to the causal one.
+// The running max starts at -1e30 instead of -inf there, because a row can see
+// no key at all in a listed tile (exp2 of -inf - -inf would be NaN); every row
+// sees at least its own position, so the final max is a real score.
+template <int D, bool DOC>
 __global__ __launch_bounds__(256, 2) void fwd_mfma_kernel(
     const bf16* __restrict__ q, const float* __restrict__ cos, const float* __restrict__ sin,
     const bf16* __restrict__ krot, const bf16* __restrict__ vn, bf16* __restrict__ out,
     float* __restrict__ lse, int Sq, int Sk, int Skp, int Hq, int Hkv, int n_rep, int bm_pos,
-    int nqb, float scale_log2, int causal) {
+    int nqb, float scale_log2, int causal, const int32_t* __restrict__ doc,
+    const int2* __restrict__ ranges) {
   constexpr int KS = D / 16, DT = D / 32;
   constexpr int KR = D / 8;  // 16-byte chunks per K / V row
   __shared__ __attribute__((aligned(16))) bf16 sK[2][BN * D];
   __shared__ __attribute__((aligned(16))) bf16 sV[2][BN * D];
+  __shared__ __attribute__((aligned(16))) int32_t sKD[2][BN];  // DOC: key document ids
+  __shared__ uint16_t sList[DOC_MAX_TILES];                     // DOC: listed key tiles
+  __shared__ int sCount;
 
   const int tid = threadIdx.x, w = wave_id(), lane = tid & 63, hh = lane >> 5, c32 = lane & 31;
   const int logical = xcd_logical_id(blockIdx.x, gridDim.x);
@@ -123,20 +142,38 @@ __global__ __launch_bounds__(256, 2) void fwd_mfma_kernel(
   const int bh = ri.b * Hkv + ri.g;
 
   const int kend = causal ? min(Sk, min(ri.p0 + bm_pos, Sq)) : Sk;
-  const int ntiles = (kend + BN - 1) / BN;
+  int ntiles = (kend + BN - 1) / BN;
+  const int32_t* drow = DOC ? doc + (int64_t)ri.b * Sk : nullptr;
+  int di = 0;
+  if constexpr (DOC) {
+    di = drow[min(ri.pos, Sq - 1)];
+    if (w == 0) {
+      const int2 span = doc_span(drow, ri.p0, min(ri.p0 + bm_pos, Sq), lane);
+      const int n = doc_tile_list(ranges + (int64_t)ri.b * (Skp / BN), 0, ntiles, span, sList, lane);
+      if (lane == 0) sCount = n;
+    }
+    __syncthreads();
+    ntiles = __builtin_amdgcn_readfirstlane(sCount);
+  }
+  // list position -> entry (tile | DOC_MASK_FLAG when it needs the document test)
+  auto entry = [&](int it) -> int {
+    return DOC ? __builtin_amdgcn_readfirstlane((int)sList[it]) : it;
+  };
+  auto tile_of = [](int e) -> int { return DOC ? e & ~DOC_MASK_FLAG : e; };
   const bf16* kbase = krot + (int64_t)bh * Skp * D;
   const bf16* vbase = vn + (int64_t)bh * Skp * D;
   auto stage = [&](int t, int buf) {
     tile_to_lds<BN, KR>(kbase + (int64_t)t * BN * D, D, sK[buf], w, lane);
     tile_to_lds<BN, KR>(vbase + (int64_t)t * BN * D, D, sV[buf], w, lane);
+    if (DOC && w == 0) dma4(lds_addr(sKD[buf]), (uint32_t)min(t * BN + lane, Sk - 1) * 4u, drow);
   };
-  if (ntiles > 0) stage(0, 0);
+  if (ntiles > 0) stage(tile_of(entry(0)), 0);
 
   bf16x8 qf[KS];
   load_q_frag<D>(q, cos, sin, ri, Sq, Hq, hh, qf);
   const TrOffsets<D> tro = tr_offsets<D>(lane);
 
-  float m = -INFINITY, lsum = 0.f;
+  float m = DOC ? -1e30f : -INFINITY, lsum = 0.f;
   f32x16 acc[DT];
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt)
@@ -145,9 +182,11 @@ __global__ __launch_bounds__(256, 2) void fwd_mfma_kernel(
 
   lds_copy_wait();
   __syncthreads();
-  for (int t = 0; t < ntiles; ++t) {
-    const int buf = t & 1;
-    if (t + 1 < ntiles) stage(t + 1, buf ^ 1);
+  for (int it = 0; it < ntiles; ++it) {
+    const int buf = it & 1;
+    const int e = entry(it);
+    const int t = tile_of(e);
+    if (it + 1 < ntiles) stage(tile_of(entry(it + 1)), buf ^ 1);
     const bf16* tK = sK[buf];
     const bf16* tV = sV[buf];
 
@@ -167,7 +206,21 @@ __global__ __launch_bounds__(256, 2) void fwd_mfma_kernel(
 
     const int k0 = t * BN;
     const bool need_mask = (causal && k0 + BN - 1 > ri.p0) || (k0 + BN > Sk);
-    if (need_mask) {
+    if (DOC && (e & DOC_MASK_FLAG)) {
+      const int lim = min(ri.pos, Sk - 1) - k0;
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int g4 = 0; g4 < 4; ++g4) {
+          const i32x4 kd = *(const i32x4*)&sKD[buf][32 * mt + 8 * g4 + 4 * hh];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int local = 32 * mt + 8 * g4 + 4 * hh + j;
+            const int i = 4 * g4 + j;
+            s[mt][i] = (local > lim || kd[j] != di) ? -INFINITY : s[mt][i];
+          }
+        }
+    } else if (need_mask) {
       // last visible key of this lane's row, relative to k0 (branch-free select)
       const int lim = (causal ? min(ri.pos, Sk - 1) : Sk - 1) - k0;
 #pragma unroll
@@ -247,13 +300,15 @@ __global__ __launch_bounds__(256, 2) void fwd_mfma_kernel(
 // A operand: row = l%32, k = 8h + j) and K^T the B operand read from LDS, so a
 // C register i holds (query row 8*(i/4)+4h+(i%4), key l%32): for a fixed i the
 // 32 lanes of one half write 32 consecutive floats of one row.  Key tiles fully
-// above the diagonal are written as zeros without computing.
-template <int D>
+// above the diagonal are written as zeros without computing.  DOC: keys of
+// another document get probability 0 (each lane tests its one key per 32-key
+// half against the document of each of its 16 rows).
+template <int D, bool DOC>
 __global__ __launch_bounds__(256, 2) void capture_probs_mfma_kernel(
     const bf16* __restrict__ q, const float* __restrict__ cos, const float* __restrict__ sin,
     const bf16* __restrict__ krot, const float* __restrict__ lse, float* __restrict__ probs,
     int Sq, int Sk, int Skp, int Hq, int Hkv, int n_rep, int bm_pos, int nqb, float scale_log2,
-    int causal) {
+    int causal, const int32_t* __restrict__ doc) {
   constexpr int KS = D / 16;
   constexpr int KR = D / 8;
   __shared__ __attribute__((aligned(16))) bf16 sK[2][BN * D];
@@ -286,6 +341,8 @@ __global__ __launch_bounds__(256, 2) void capture_probs_mfma_kernel(
   float* prow[16];
   float lrow[16];
   int posr[16];
+  int drw[16];  // DOC: document of each row
+  const int32_t* drow = DOC ? doc + (int64_t)ri.b * Sk : nullptr;
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     const int r = w * 32 + 8 * (i >> 2) + 4 * hh + (i & 3);
@@ -293,6 +350,7 @@ __global__ __launch_bounds__(256, 2) void capture_probs_mfma_kernel(
     prow[i] = off < 0 ? nullptr : pbase + (int64_t)off * Sk;
     lrow[i] = sL[r];
     posr[i] = ri.p0 + (r % bm_pos);
+    drw[i] = DOC ? drow[min(posr[i], Sq - 1)] : 0;
   }
 
   // K tiles double-buffered: tile t+1 loads while tile t is computed and stored
@@ -314,6 +372,7 @@ __global__ __launch_bounds__(256, 2) void capture_probs_mfma_kernel(
         sv = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qf[ks], bk, sv, 0, 0, 0);
       }
       const int key = t * BN + 32 * nt + c32;
+      const int kd = DOC ? drow[min(key, Sk - 1)] : 0;
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         if (prow[i] == nullptr) continue;
@@ -322,6 +381,7 @@ __global__ __launch_bounds__(256, 2) void capture_probs_mfma_kernel(
           if (key >= Sk) continue;
           if (causal && key > posr[i]) p = 0.f;
         }
+        if (DOC && kd != drw[i]) p = 0.f;
         __builtin_nontemporal_store(p, prow[i] + key);
       }
     }
@@ -352,7 +412,7 @@ int pick_bm_pos(int n_rep) { return n_rep <= ROWS ? ROWS / n_rep : 0; }
 
 bool fwd_mfma_supported(const FwdArgs& a) {
   if (a.dtype != BF16 || (a.D != 64 && a.D != 128)) return false;
-  if (a.doc) return false;
+  if (a.doc && (a.Sk + BN - 1) / BN > DOC_MAX_TILES) return false;
   const int n_rep = a.Hq / a.Hkv;
   if (n_rep < 1 || n_rep > ROWS) return false;
   auto al16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
@@ -362,47 +422,79 @@ bool fwd_mfma_supported(const FwdArgs& a) {
   return true;
 }
 
+// krot and vn ([B*Hkv][Skp][D] bf16 each), then the per-tile document ranges
+// ([B][Skp/64] int2, written only for packed documents).
 size_t fwd_mfma_workspace(int B, int Sk, int Hkv, int D) {
   const size_t Skp = (size_t)((Sk + BN - 1) / BN) * BN;
-  return 2 * (size_t)B * Hkv * Skp * D * sizeof(uint16_t);
+  return 2 * (size_t)B * Hkv * Skp * D * sizeof(uint16_t) + (size_t)B * (Skp / BN) * sizeof(int2);
 }
 
-int launch_kv_prep(const FwdArgs& a, void* krot_, void* vn_, int Skp) {
+int launch_kv_prep(const FwdArgs& a, void* krot_, void* vn_, int Skp, int2* ranges) {
   bf16* krot = (bf16*)krot_;
   bf16* vn = (bf16*)vn_;
   dim3 grid(Skp / BN, a.B * a.Hkv);
   if (a.D == 128)
     KF_LAUNCH("kv_prep", kv_prep_kernel<128>, grid, dim3(256), 0, a.stream, (const bf16*)a.k,
                        (const bf16*)a.v, a.cos, a.sin, krot, vn, a.Sk, Skp, a.Hkv, a.ksb, a.kss,
-                       a.ksh, a.vsb, a.vss, a.vsh, a.k_rotated);
+                       a.ksh, a.vsb, a.vss, a.vsh, a.k_rotated, a.doc, ranges);
   else
     KF_LAUNCH("kv_prep", kv_prep_kernel<64>, grid, dim3(256), 0, a.stream, (const bf16*)a.k,
                        (const bf16*)a.v, a.cos, a.sin, krot, vn, a.Sk, Skp, a.Hkv, a.ksb, a.kss,
-                       a.ksh, a.vsb, a.vss, a.vsh, a.k_rotated);
+                       a.ksh, a.vsb, a.vss, a.vsh, a.k_rotated, a.doc, ranges);
   KF_CHECK_LAUNCH();
   return KF_OK;
 }
 
+namespace {
+
+struct FwdWs {
+  bf16 *krot, *vn;
+  int2* ranges;
+};
+
+FwdWs carve_fwd(const FwdArgs& a, void* workspace, int Skp) {
+  FwdWs w;
+  w.krot = (bf16*)workspace;
+  w.vn = w.krot + (size_t)a.B * a.Hkv * Skp * a.D;
+  w.ranges = (int2*)(w.vn + (size_t)a.B * a.Hkv * Skp * a.D);
+  return w;
+}
+
+template <int D, bool DOC>
+void launch_fwd_kernel(const FwdArgs& a, const FwdWs& w, int Skp, int n_rep, int bm_pos, int nqb,
+                       unsigned nblk) {
+  KF_LAUNCH("fwd_mfma", (fwd_mfma_kernel<D, DOC>), dim3(nblk), dim3(256), 0, a.stream,
+            (const bf16*)a.q, a.cos, a.sin, w.krot, w.vn, (bf16*)a.out, a.lse, a.Sq, a.Sk, Skp,
+            a.Hq, a.Hkv, n_rep, bm_pos, nqb, a.scale * kLog2e, a.causal, a.doc, w.ranges);
+}
+
+template <int D, bool DOC>
+void launch_capture_kernel(const FwdArgs& a, const FwdWs& w, const float* lse, float* probs,
+                           int Skp, int n_rep, int bm_pos, int nqb, unsigned nblk) {
+  KF_LAUNCH("capture_probs_mfma", (capture_probs_mfma_kernel<D, DOC>), dim3(nblk), dim3(256), 0,
+            a.stream, (const bf16*)a.q, a.cos, a.sin, w.krot, lse, probs, a.Sq, a.Sk, Skp, a.Hq,
+            a.Hkv, n_rep, bm_pos, nqb, a.scale * kLog2e, a.causal, a.doc);
+}
+
+}  // namespace
+
 int fwd_mfma(const FwdArgs& a, void* workspace) {
   const int Skp = (a.Sk + BN - 1) / BN * BN;
-  bf16* krot = (bf16*)workspace;
-  bf16* vn = krot + (size_t)a.B * a.Hkv * Skp * a.D;
-  int rc = launch_kv_prep(a, krot, vn, Skp);
+  const FwdWs w = carve_fwd(a, workspace, Skp);
+  int rc = launch_kv_prep(a, w.krot, w.vn, Skp, w.ranges);
   if (rc) return rc;
   const int n_rep = a.Hq / a.Hkv;
   const int bm_pos = pick_bm_pos(n_rep);
   const int nqb = (a.Sq + bm_pos - 1) / bm_pos;
   const int64_t nblk = (int64_t)nqb * a.B * a.Hkv;
   KF_CHECK_ARG(nblk < (1LL << 31), "grid too large");
-  const float scale_log2 = a.scale * kLog2e;
-  if (a.D == 128)
-    KF_LAUNCH("fwd_mfma", fwd_mfma_kernel<128>, dim3((unsigned)nblk), dim3(256), 0, a.stream,
-                       (const bf16*)a.q, a.cos, a.sin, krot, vn, (bf16*)a.out, a.lse, a.Sq, a.Sk,
-                       Skp, a.Hq, a.Hkv, n_rep, bm_pos, nqb, scale_log2, a.causal);
-  else
-    KF_LAUNCH("fwd_mfma", fwd_mfma_kernel<64>, dim3((unsigned)nblk), dim3(256), 0, a.stream,
-                       (const bf16*)a.q, a.cos, a.sin, krot, vn, (bf16*)a.out, a.lse, a.Sq, a.Sk,
-                       Skp, a.Hq, a.Hkv, n_rep, bm_pos, nqb, scale_log2, a.causal);
+  if (a.D == 128) {
+    if (a.doc) launch_fwd_kernel<128, true>(a, w, Skp, n_rep, bm_pos, nqb, (unsigned)nblk);
+    else launch_fwd_kernel<128, false>(a, w, Skp, n_rep, bm_pos, nqb, (unsigned)nblk);
+  } else {
+    if (a.doc) launch_fwd_kernel<64, true>(a, w, Skp, n_rep, bm_pos, nqb, (unsigned)nblk);
+    else launch_fwd_kernel<64, false>(a, w, Skp, n_rep, bm_pos, nqb, (unsigned)nblk);
+  }
   KF_CHECK_LAUNCH();
   return KF_OK;
 }
@@ -410,20 +502,18 @@ int fwd_mfma(const FwdArgs& a, void* workspace) {
 // Requires fwd_mfma to have run with the same workspace (krot is reused).
 int capture_probs_mfma(const FwdArgs& a, const float* lse, float* probs, void* workspace) {
   const int Skp = (a.Sk + BN - 1) / BN * BN;
-  const bf16* krot = (const bf16*)workspace;
+  const FwdWs w = carve_fwd(a, workspace, Skp);
   const int n_rep = a.Hq / a.Hkv;
   const int bm_pos = pick_bm_pos(n_rep);
   const int nqb = (a.Sq + bm_pos - 1) / bm_pos;
-  const int64_t nblk = (int64_t)nqb * a.B * a.Hkv;
-  const float scale_log2 = a.scale * kLog2e;
-  if (a.D == 128)
-    KF_LAUNCH("capture_probs_mfma", capture_probs_mfma_kernel<128>, dim3((unsigned)nblk), dim3(256), 0,
-                       a.stream, (const bf16*)a.q, a.cos, a.sin, krot, lse, probs, a.Sq, a.Sk,
-                       Skp, a.Hq, a.Hkv, n_rep, bm_pos, nqb, scale_log2, a.causal);
-  else
-    KF_LAUNCH("capture_probs_mfma", capture_probs_mfma_kernel<64>, dim3((unsigned)nblk), dim3(256), 0,
-                       a.stream, (const bf16*)a.q, a.cos, a.sin, krot, lse, probs, a.Sq, a.Sk,
-                       Skp, a.Hq, a.Hkv, n_rep, bm_pos, nqb, scale_log2, a.causal);
+  const unsigned nblk = (unsigned)((int64_t)nqb * a.B * a.Hkv);
+  if (a.D == 128) {
+    if (a.doc) launch_capture_kernel<128, true>(a, w, lse, probs, Skp, n_rep, bm_pos, nqb, nblk);
+    else launch_capture_kernel<128, false>(a, w, lse, probs, Skp, n_rep, bm_pos, nqb, nblk);
+  } else {
+    if (a.doc) launch_capture_kernel<64, true>(a, w, lse, probs, Skp, n_rep, bm_pos, nqb, nblk);
+    else launch_capture_kernel<64, false>(a, w, lse, probs, Skp, n_rep, bm_pos, nqb, nblk);
+  }
   KF_CHECK_LAUNCH();
   return KF_OK;
 }

@@ -50,8 +50,9 @@ int capture_probs_generic(const FwdArgs& a, const float* lse, float* probs);
 
 // bf16 MFMA kernels (kf_fwd.hip, kf_bwd.hip, kf_capture.hip)
 bool fwd_mfma_supported(const FwdArgs& a);
-// Rotated K and zero-padded V, both [B*Hkv][Skp][D] bf16 (Skp a multiple of 64).
-int launch_kv_prep(const FwdArgs& a, void* krot, void* vn, int Skp);
+// Rotated K and zero-padded V, both [B*Hkv][Skp][D] bf16 (Skp a multiple of 64);
+// with a.doc also the [min, max] document id of each 64-key tile, [B][Skp/64].
+int launch_kv_prep(const FwdArgs& a, void* krot, void* vn, int Skp, int2* ranges);
 size_t fwd_mfma_workspace(int B, int Sk, int Hkv, int D);
 int fwd_mfma(const FwdArgs& a, void* workspace);
 int capture_probs_mfma(const FwdArgs& a, const float* lse, float* probs, void* workspace);

@@ -1,6 +1,8 @@
 // MFMA-path helpers shared by the forward, capture and backward kernels.
 #pragma once
 
+#include <climits>
+
 #include "kf_common.h"
 
 namespace kf {
@@ -180,6 +182,68 @@ __device__ __forceinline__ void settle(T& x) {
 // Wavefront index as a scalar (SGPR) value, so per-wave LDS destinations and
 // global bases derived from it stay uniform.
 __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
+
+// ---- packed documents -----------------------------------------------------
+// With per-position document ids a query sees a key only inside its own
+// document.  kv_prep records each 64-position tile's [min, max] document id;
+// a workgroup lists the tiles whose range meets its own range (skipping the
+// rest) and applies the element-wise test only to tiles that are not entirely
+// in the workgroup's single document.  Min/max ranges make this exact for any
+// id pattern, not only contiguous segments.
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int DOC_MAX_TILES = 4096;      // capacity of a workgroup's tile list
+constexpr int DOC_MASK_FLAG = 0x8000;    // list entry: tile needs the element test
+
+__device__ __forceinline__ int wave_min_i(int v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = min(v, __shfl_xor(v, o, 64));
+  return v;
+}
+__device__ __forceinline__ int wave_max_i(int v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = max(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+// [min, max] of doc[begin, end) (end > begin), computed by one wavefront;
+// the result is wavefront-uniform.
+__device__ __forceinline__ int2 doc_span(const int32_t* __restrict__ doc, int begin, int end,
+                                         int lane) {
+  int lo = INT_MAX, hi = INT_MIN;
+  for (int i = begin + lane; i < end; i += 64) {
+    const int d = doc[i];
+    lo = min(lo, d);
+    hi = max(hi, d);
+  }
+  return make_int2(__builtin_amdgcn_readfirstlane(wave_min_i(lo)),
+                   __builtin_amdgcn_readfirstlane(wave_max_i(hi)));
+}
+
+// Writes, in ascending order, the tiles t in [t0, t1) whose range meets `span`
+// to list[] (t | DOC_MASK_FLAG unless the tile and the span are one and the
+// same document) and returns their number.  Called by one wavefront; the
+// caller publishes the count and synchronises before others read the list.
+__device__ __forceinline__ int doc_tile_list(const int2* __restrict__ ranges, int t0, int t1,
+                                             int2 span, uint16_t* list, int lane) {
+  int n = 0;
+  for (int base = t0; base < t1; base += 64) {
+    const int t = base + lane;
+    bool vis = false, whole = false;
+    if (t < t1) {
+      const int2 r = ranges[t];
+      vis = r.x <= span.y && r.y >= span.x;
+      whole = r.x == r.y && span.x == span.y && r.x == span.x;
+    }
+    const uint64_t m = __builtin_amdgcn_ballot_w64(vis);
+    const int below = __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                                __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0));
+    if (vis && n + below < DOC_MAX_TILES)
+      list[n + below] = (uint16_t)(t | (whole ? 0 : DOC_MASK_FLAG));
+    n += __builtin_popcountll(m);
+  }
+  return min(n, DOC_MAX_TILES);
+}
 
 }  // namespace mfma
 }  // namespace kf

@@ -52,7 +52,8 @@ def test_host_only_calls():
     assert lib.kf_version() >= 100
     n = _lib.size_out()
     assert lib.kf_attn_fwd_workspace_size(4, 4096, 4096, 32, 8, 128, 1, ctypes.byref(n)) == 0
-    assert n.value == 2 * 4 * 8 * 4096 * 128 * 2
+    # rotated K and V (bf16), then one int2 document range per batch row and 64-key tile
+    assert n.value == 2 * 4 * 8 * 4096 * 128 * 2 + 4 * 64 * 8
     assert lib.kf_attn_fwd_workspace_size(1, 8, 8, 6, 4, 64, 1, ctypes.byref(n)) == 1
     assert b"multiple" in lib.kf_last_error()
     assert lib.kf_attn_fwd_workspace_size(1, 8, 8, 4, 4, 63, 1, ctypes.byref(n)) == 1

@@ -62,6 +62,9 @@ CASES = [
     (torch.bfloat16, 2, 190, 4, 2, 128, "reused_ids"),
     (torch.float32, 1, 150, 8, 2, 128, "random"),
     (torch.float32, 2, 96, 4, 1, 64, "tile_edges"),
+    # more than 64 tiles: the tile lists span several 64-tile words
+    (torch.bfloat16, 1, 4500, 2, 1, 64, "random"),
+    (torch.bfloat16, 1, 4200, 2, 2, 128, "reused_ids"),
 ]
 
 
