@@ -9,7 +9,8 @@ with P = B*Hq*S*(S+1)/2 causal (query, key) pairs (forward 4*D*P, backward
 
 Also reported: per-kernel HIP-event timings (the library brackets each launch
 on its own stream), the roofline of the dominant kernel, the forward alone
-(C2), the Llama-3-70B shape fwd+bwd (C5: B=1, S=16384, 64 query heads) and its
+(C2), the C3 step on packed documents (C3-doc; flops of same-document pairs
+only), the Llama-3-70B shape fwd+bwd (C5: B=1, S=16384, 64 query heads) and its
 2048-token probability capture (C5-cap), the KV-cache decode configuration C4
 in GB/s, and the reference's PyTorch path timed on the host CPU on a bounded
 sample of the same workload.
@@ -154,6 +155,33 @@ def main() -> int:
     c2 = {"config": "C2 llama3-8b fwd B=4 S=4096 Hq=32 Hkv=8 D=128", "ms": round(c2_s * 1e3, 4),
           "TFLOP/s": round(4.0 * D * P / c2_s / 1e12, 1)}
 
+    # C3-doc: the C3 step on packed sequences (documents of 64..2048 tokens, seeded);
+    # flops count only same-document causal pairs, so the rate compares with C3's
+    g = torch.Generator().manual_seed(7)
+    doc_rows, doc_pairs = [], 0
+    for _ in range(B):
+        lens_, left = [], S
+        while left:
+            n = min(left, int(torch.randint(64, 2049, (1,), generator=g)))
+            lens_.append(n)
+            left -= n
+        doc_pairs += Hq * sum(n * (n + 1) // 2 for n in lens_)
+        doc_rows.append(torch.cat([torch.full((n,), i, dtype=torch.int32)
+                                   for i, n in enumerate(lens_)]))
+    doc_ids = torch.stack(doc_rows).to(dev)
+
+    def step_doc():
+        out = ops.attention(q, k, v, cos, sin, causal=True, doc_ids=doc_ids)
+        torch.autograd.grad(out, (q, k, v), do)
+
+    doc_s = wall(step_doc, args.warmup, args.steps)
+    c3doc = {"config": "C3-doc C3 with packed documents of 64..2048 tokens (seed 7), "
+                       f"{sum(int(r.max()) + 1 for r in doc_rows)} documents",
+             "ms": round(doc_s * 1e3, 4),
+             "TFLOP/s": round(14.0 * D * doc_pairs / doc_s / 1e12, 1),
+             "visible_pair_frac": round(doc_pairs / P, 4),
+             "speedup_vs_dense_causal": round(ms_step / (doc_s * 1e3), 2)}
+
     # C5: llama3-70b shape fwd+bwd, and C5-cap (probabilities of its first 2048 tokens)
     B5, S5, Hq5, Hkv5 = C5["B"], C5["S"], C5["Hq"], C5["Hkv"]
     q5 = seeded((B5, S5, Hq5, D), 0, bf16, dev).requires_grad_(True)
@@ -256,6 +284,7 @@ def main() -> int:
         "kernels_us": {n: round(s["avg_us"], 1) for n, s in kstats.items()},
         "fwd_tflops": round(4.0 * D * P / (fwd_us * 1e-6) / 1e12, 1) if fwd_us else None,
         "c2_fwd": c2,
+        "c3_doc": c3doc,
         "c5": c5,
         "c5_cap": c5cap,
         "decode": {"config": "C4 B=32 Hq=32 Hkv=8 D=128 L~U[1024,8192] seed 4",

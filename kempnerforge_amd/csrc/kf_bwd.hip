@@ -107,7 +107,9 @@ struct DkdvStage {
 };
 
 // DOC: qlist[0, nlist) holds the listed query tiles (DOC_MASK_FLAG: needs the
-// element test), sQD the staged query documents, drow the batch row's ids.
+// element test), sQD the staged query documents, drow the batch row's ids; the
+// caller has already staged iteration 0 (head 0, the diagonal tile qt0, which
+// is always listed first) with dkdv_stage_first.
 template <int D, bool DSROLE, bool DOC>
 __device__ __forceinline__ void dkdv_role(
     DkdvStage<D>* st, u32x4* sP, const bf16* __restrict__ krot, const bf16* __restrict__ vn,
@@ -135,8 +137,7 @@ __device__ __forceinline__ void dkdv_role(
   auto tile_of = [](int e) -> int { return DOC ? e & ~DOC_MASK_FLAG : e; };
   const int kdoc = DOC ? drow[min(key, S - 1)] : 0;
 
-  auto stage = [&](int it, int buf) {
-    const int hl = it / per_head, qtile = tile_of(entry(it));
+  auto stage_tile = [&](int hl, int qtile, int buf) {
     const int64_t bhq = (int64_t)b * Hq + g * n_rep + hl;
     const int q0 = qtile * BQ;
     DkdvStage<D>& S_ = st[buf];
@@ -146,7 +147,9 @@ __device__ __forceinline__ void dkdv_role(
     if (w == 1) row_to_lds(delta + bhq * P + q0, S_.dl, lane);
     if (DOC && w == 2) dma4(lds_addr(sQD[buf]), (uint32_t)min(q0 + lane, S - 1) * 4u, drow);
   };
-  if (total > 0) stage(0, 0);
+  auto stage = [&](int it, int buf) { stage_tile(it / per_head, tile_of(entry(it)), buf); };
+  // DOC: the first tile was staged by the caller before the list was built
+  if (!DOC && total > 0) stage(0, 0);
 
   // this role's register-resident B operand: K for P waves, V for dS waves
   bf16x8 bf[KS];
@@ -303,6 +306,22 @@ __device__ __forceinline__ void dkdv_role(
   }
 }
 
+// Stage query tile q0 of query head bhq into buffer 0 (what dkdv_role's
+// iteration 0 reads) with its document ids.
+template <int D>
+__device__ __forceinline__ void dkdv_stage_first(
+    DkdvStage<D>* st, const bf16* __restrict__ qrot, const bf16* __restrict__ don,
+    const float* __restrict__ lse2, const float* __restrict__ delta,
+    const int32_t* __restrict__ drow, int S, int P, int64_t bhq, int q0, int32_t* sqd, int w,
+    int lane) {
+  constexpr int KR = D / 8;
+  tile_to_lds<BQ, KR, 8>(qrot + (bhq * P + q0) * D, D, st[0].q, w, lane);
+  tile_to_lds<BQ, KR, 8>(don + (bhq * P + q0) * D, D, st[0].o, w, lane);
+  if (w == 0) row_to_lds(lse2 + bhq * P + q0, st[0].l, lane);
+  if (w == 1) row_to_lds(delta + bhq * P + q0, st[0].dl, lane);
+  if (w == 2) dma4(lds_addr(sqd), (uint32_t)min(q0 + lane, S - 1) * 4u, drow);
+}
+
 template <int D, bool DOC>
 __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(
     const bf16* __restrict__ krot, const bf16* __restrict__ vn, const bf16* __restrict__ qrot,
@@ -324,10 +343,12 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(
   const int32_t* drow = DOC ? doc + (int64_t)b * S : nullptr;
   int nlist = 0;
   if constexpr (DOC) {
+    const int qt0 = k0 / BQ;  // the diagonal query tile: always listed, first
+    dkdv_stage_first<D>(st, qrot, don, lse2, delta, drow, S, P, (int64_t)b * Hq + g * n_rep,
+                        qt0 * BQ, sQD[0], w, lane);
     if (w == 0) {
-      const int2 span = doc_span(drow, k0, min(k0 + BKV, S), lane);
-      const int n = doc_tile_list(ranges + (int64_t)b * (P / BN), causal ? k0 / BQ : 0,
-                                  (S + BQ - 1) / BQ, span, sList, lane);
+      const int n = doc_tile_list(drow, k0, min(k0 + BKV, S), ranges + (int64_t)b * (P / BN),
+                                  qt0, (S + BQ - 1) / BQ, sList, lane);
       if (lane == 0) sCount = n;
     }
     __syncthreads();
@@ -345,6 +366,7 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(
 
 // dQ workgroup: 8 wavefronts x 32 rows = 256 (query head, position) rows of one
 // KV group, all sharing each staged K / V / K^T tile (two wavefronts per SIMD).
+// DOC walks the listed key tiles last to first, like the forward.
 constexpr int DQ_ROWS = 256;
 
 template <int D, bool DOC>
@@ -373,21 +395,6 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_kernel(
   const int kend = causal ? min(S, ri.p0 + bm_pos) : S;
   int ntiles = (kend + BN - 1) / BN;
   const int32_t* drow = DOC ? doc + (int64_t)ri.b * S : nullptr;
-  int di = 0;
-  if constexpr (DOC) {
-    di = drow[min(ri.pos, S - 1)];
-    if (w == 0) {
-      const int2 span = doc_span(drow, ri.p0, min(ri.p0 + bm_pos, S), lane);
-      const int n = doc_tile_list(ranges + (int64_t)ri.b * (P / BN), 0, ntiles, span, sList, lane);
-      if (lane == 0) sCount = n;
-    }
-    __syncthreads();
-    ntiles = __builtin_amdgcn_readfirstlane(sCount);
-  }
-  auto entry = [&](int it) -> int {
-    return DOC ? __builtin_amdgcn_readfirstlane((int)sList[it]) : it;
-  };
-  auto tile_of = [](int e) -> int { return DOC ? e & ~DOC_MASK_FLAG : e; };
   const bf16* kbase = krot + (int64_t)bh * P * D;
   const bf16* vbase = vn + (int64_t)bh * P * D;
   auto stage = [&](int t, int buf) {
@@ -395,7 +402,26 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_kernel(
     tile_to_lds<BN, KR, 8>(vbase + (int64_t)t * BN * D, D, st[buf].v, w, lane);
     if (DOC && w == 0) dma4(lds_addr(sKD[buf]), (uint32_t)min(t * BN + lane, S - 1) * 4u, drow);
   };
-  if (ntiles > 0) stage(tile_of(entry(0)), 0);
+  int di = 0;
+  if constexpr (DOC) {
+    // walked backwards, as in the forward: the always-listed last tile loads
+    // while the list is built
+    if (ntiles > 0) stage(ntiles - 1, 0);
+    di = drow[min(ri.pos, S - 1)];
+    if (w == 0) {
+      const int n = doc_tile_list(drow, ri.p0, min(ri.p0 + bm_pos, S),
+                                  ranges + (int64_t)ri.b * (P / BN), 0, ntiles, sList, lane);
+      if (lane == 0) sCount = n;
+    }
+    __syncthreads();
+    ntiles = __builtin_amdgcn_readfirstlane(sCount);
+  } else {
+    if (ntiles > 0) stage(0, 0);
+  }
+  auto entry = [&](int it) -> int {
+    return DOC ? __builtin_amdgcn_readfirstlane((int)sList[ntiles - 1 - it]) : it;
+  };
+  auto tile_of = [](int e) -> int { return DOC ? e & ~DOC_MASK_FLAG : e; };
 
   bf16x8 qf[KS], df[KS];
   float l2 = INFINITY, dl = 0.f;

@@ -116,8 +116,9 @@ __device__ __forceinline__ void load_q_frag(const bf16* __restrict__ q,
 }
 
 // DOC: packed documents (doc != null, causal, Sq == Sk).  The workgroup walks
-// only the key tiles listed by doc_tile_list; listed tiles carrying the mask
-// flag get the element test doc[key] == doc[query] next to the causal one.
+// only the key tiles listed by doc_tile_list, last to first; listed tiles
+// carrying the mask flag get the element test doc[key] == doc[query] next to
+// the causal one.
 // The running max starts at -1e30 instead of -inf there, because a row can see
 // no key at all in a listed tile (exp2 of -inf - -inf would be NaN); every row
 // sees at least its own position, so the final max is a real score.
@@ -144,22 +145,6 @@ __global__ __launch_bounds__(256, 2) void fwd_mfma_kernel(
   const int kend = causal ? min(Sk, min(ri.p0 + bm_pos, Sq)) : Sk;
   int ntiles = (kend + BN - 1) / BN;
   const int32_t* drow = DOC ? doc + (int64_t)ri.b * Sk : nullptr;
-  int di = 0;
-  if constexpr (DOC) {
-    di = drow[min(ri.pos, Sq - 1)];
-    if (w == 0) {
-      const int2 span = doc_span(drow, ri.p0, min(ri.p0 + bm_pos, Sq), lane);
-      const int n = doc_tile_list(ranges + (int64_t)ri.b * (Skp / BN), 0, ntiles, span, sList, lane);
-      if (lane == 0) sCount = n;
-    }
-    __syncthreads();
-    ntiles = __builtin_amdgcn_readfirstlane(sCount);
-  }
-  // list position -> entry (tile | DOC_MASK_FLAG when it needs the document test)
-  auto entry = [&](int it) -> int {
-    return DOC ? __builtin_amdgcn_readfirstlane((int)sList[it]) : it;
-  };
-  auto tile_of = [](int e) -> int { return DOC ? e & ~DOC_MASK_FLAG : e; };
   const bf16* kbase = krot + (int64_t)bh * Skp * D;
   const bf16* vbase = vn + (int64_t)bh * Skp * D;
   auto stage = [&](int t, int buf) {
@@ -167,7 +152,27 @@ __global__ __launch_bounds__(256, 2) void fwd_mfma_kernel(
     tile_to_lds<BN, KR>(vbase + (int64_t)t * BN * D, D, sV[buf], w, lane);
     if (DOC && w == 0) dma4(lds_addr(sKD[buf]), (uint32_t)min(t * BN + lane, Sk - 1) * 4u, drow);
   };
-  if (ntiles > 0) stage(tile_of(entry(0)), 0);
+  int di = 0;
+  if constexpr (DOC) {
+    // The list is walked backwards.  Its last tile, the one holding the
+    // block's last position, is always listed: it loads while the list is built.
+    if (ntiles > 0) stage(ntiles - 1, 0);
+    di = drow[min(ri.pos, Sq - 1)];
+    if (w == 0) {
+      const int n = doc_tile_list(drow, ri.p0, min(ri.p0 + bm_pos, Sq),
+                                  ranges + (int64_t)ri.b * (Skp / BN), 0, ntiles, sList, lane);
+      if (lane == 0) sCount = n;
+    }
+    __syncthreads();
+    ntiles = __builtin_amdgcn_readfirstlane(sCount);
+  } else {
+    if (ntiles > 0) stage(0, 0);
+  }
+  // iteration -> entry (tile | DOC_MASK_FLAG when it needs the document test)
+  auto entry = [&](int it) -> int {
+    return DOC ? __builtin_amdgcn_readfirstlane((int)sList[ntiles - 1 - it]) : it;
+  };
+  auto tile_of = [](int e) -> int { return DOC ? e & ~DOC_MASK_FLAG : e; };
 
   bf16x8 qf[KS];
   load_q_frag<D>(q, cos, sin, ri, Sq, Hq, hh, qf);

@@ -206,35 +206,36 @@ __device__ __forceinline__ int wave_max_i(int v) {
   return v;
 }
 
-// [min, max] of doc[begin, end) (end > begin), computed by one wavefront;
-// the result is wavefront-uniform.
-__device__ __forceinline__ int2 doc_span(const int32_t* __restrict__ doc, int begin, int end,
-                                         int lane) {
-  int lo = INT_MAX, hi = INT_MIN;
-  for (int i = begin + lane; i < end; i += 64) {
-    const int d = doc[i];
-    lo = min(lo, d);
-    hi = max(hi, d);
-  }
-  return make_int2(__builtin_amdgcn_readfirstlane(wave_min_i(lo)),
-                   __builtin_amdgcn_readfirstlane(wave_max_i(hi)));
-}
-
-// Writes, in ascending order, the tiles t in [t0, t1) whose range meets `span`
-// to list[] (t | DOC_MASK_FLAG unless the tile and the span are one and the
-// same document) and returns their number.  Called by one wavefront; the
+// Lists, in ascending order, the tiles t in [t0, t1) whose document range
+// meets that of rows [p_begin, p_end) (at most 256 rows, p_end > p_begin):
+// list[] gets t | DOC_MASK_FLAG, or plain t when the tile and the rows are one
+// and the same document.  Returns the count.  Called by one wavefront; the
 // caller publishes the count and synchronises before others read the list.
-__device__ __forceinline__ int doc_tile_list(const int2* __restrict__ ranges, int t0, int t1,
-                                             int2 span, uint16_t* list, int lane) {
+// The rows' ids and the first 64 tile ranges are loaded together, so the list
+// costs one memory round trip for up to 64 tiles.
+__device__ __forceinline__ int doc_tile_list(const int32_t* __restrict__ drow, int p_begin,
+                                             int p_end, const int2* __restrict__ ranges, int t0,
+                                             int t1, uint16_t* list, int lane) {
+  int2 r = make_int2(INT_MAX, INT_MIN);
+  if (t0 + lane < t1) r = ranges[t0 + lane];
+  int lo = INT_MAX, hi = INT_MIN;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int p = p_begin + 64 * j + lane;
+    if (p < p_end) {
+      const int d = drow[p];
+      lo = min(lo, d);
+      hi = max(hi, d);
+    }
+  }
+  lo = __builtin_amdgcn_readfirstlane(wave_min_i(lo));
+  hi = __builtin_amdgcn_readfirstlane(wave_max_i(hi));
   int n = 0;
   for (int base = t0; base < t1; base += 64) {
     const int t = base + lane;
-    bool vis = false, whole = false;
-    if (t < t1) {
-      const int2 r = ranges[t];
-      vis = r.x <= span.y && r.y >= span.x;
-      whole = r.x == r.y && span.x == span.y && r.x == span.x;
-    }
+    if (base != t0) r = t < t1 ? ranges[t] : make_int2(INT_MAX, INT_MIN);
+    const bool vis = t < t1 && r.x <= hi && r.y >= lo;
+    const bool whole = r.x == r.y && lo == hi && r.x == lo;
     const uint64_t m = __builtin_amdgcn_ballot_w64(vis);
     const int below = __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
                                                 __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0));
