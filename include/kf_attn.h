@@ -69,13 +69,20 @@ int kf_attn_fwd_workspace_size(int B, int Sq, int Sk, int Hq, int Hkv, int D, in
  *   doc_ids[b][j]: the explicit mask of the reference's packed-sequence branch
  *   (kempnerforge/model/attention.py:204-227, doc_ids from
  *   kempnerforge/data/dataset.py:27-65).  Needs causal = 1, k_rotated = 0.
+ *   key_valid  [B, S] int32, 1 = the key may be attended (key_padding_mask),
+ *   or NULL.  Given, query i also needs key_valid[b][j] != 0; a query that
+ *   sees no key at all is unmasked entirely and attends every key, the NaN
+ *   guard of the reference's explicit-mask branches (kempnerforge/model/
+ *   attention.py:214-225, kempnerforge/model/mot.py:188-198).  Needs
+ *   causal = 1, k_rotated = 0; combines with doc_ids.
  * Query head h reads KV head h / (Hq / Hkv).  Scale is D^-1/2.
  */
 int kf_attn_fwd(const void* q, const void* k, const void* v, const float* rope_cos,
                 const float* rope_sin, void* out, float* lse, void* workspace,
                 size_t workspace_bytes, int B, int Sq, int Sk, int Hq, int Hkv, int D,
                 int64_t ksb, int64_t kss, int64_t ksh, int64_t vsb, int64_t vss, int64_t vsh,
-                int k_rotated, int causal, const int32_t* doc_ids, int dtype, void* stream);
+                int k_rotated, int causal, const int32_t* doc_ids, const int32_t* key_valid,
+                int dtype, void* stream);
 
 /* Workspace bytes kf_attn_bwd needs. */
 int kf_attn_bwd_workspace_size(int B, int S, int Hq, int Hkv, int D, int dtype, size_t* bytes);
@@ -91,13 +98,13 @@ int kf_attn_bwd_workspace_size(int B, int S, int Hq, int Hkv, int D, int dtype, 
  *   dq        [B, S, Hq, D]  gradient w.r.t. q before RoPE
  *   dk, dv    [B, S, Hkv, D] gradients w.r.t. k (before RoPE) and v, summed
  *             over the Hq/Hkv query heads of each KV group
- *   doc_ids   as for kf_attn_fwd (NULL or the ids the forward used)
+ *   doc_ids, key_valid  as for kf_attn_fwd (NULL or what the forward used)
  */
 int kf_attn_bwd(const void* q, const void* k, const void* v, const float* rope_cos,
                 const float* rope_sin, const void* out, const float* lse, const void* dout,
                 void* dq, void* dk, void* dv, void* workspace, size_t workspace_bytes, int B,
-                int S, int Hq, int Hkv, int D, int causal, const int32_t* doc_ids, int dtype,
-                void* stream);
+                int S, int Hq, int Hkv, int D, int causal, const int32_t* doc_ids,
+                const int32_t* key_valid, int dtype, void* stream);
 
 /* Workspace bytes kf_attn_decode needs; max_len bounds lens[b] + 1. */
 int kf_attn_decode_workspace_size(int B, int Hq, int Hkv, int D, int max_len, int dtype,
@@ -156,8 +163,8 @@ int kf_attn_capture(const void* q, const void* k, const void* v, const float* ro
                     const float* rope_sin, float* probs, void* out, float* lse, void* workspace,
                     size_t workspace_bytes, int B, int Sq, int Sk, int Hq, int Hkv, int D,
                     int64_t ksb, int64_t kss, int64_t ksh, int64_t vsb, int64_t vss,
-                    int64_t vsh, int k_rotated, int causal, const int32_t* doc_ids, int dtype,
-                    void* stream);
+                    int64_t vsh, int k_rotated, int causal, const int32_t* doc_ids,
+                    const int32_t* key_valid, int dtype, void* stream);
 
 /* ---- Measurement hooks.  No counterpart in the reference: they exist so a
  * benchmark can time each kernel of the library on the stream it runs on. */

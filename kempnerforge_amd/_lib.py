@@ -24,17 +24,17 @@ SIGNATURES = {
     "kf_last_error": ([], ctypes.c_char_p),
     "kf_attn_fwd_workspace_size": ([_c_int] * 7 + [_szp], _c_int),
     "kf_attn_fwd": ([_vp, _vp, _vp, _fp, _fp, _vp, _fp, _vp, _c_sz] + [_c_int] * 6
-                    + [_c_i64] * 6 + [_c_int] * 2 + [_vp, _c_int, _vp], _c_int),
+                    + [_c_i64] * 6 + [_c_int] * 2 + [_vp, _vp, _c_int, _vp], _c_int),
     "kf_attn_bwd_workspace_size": ([_c_int] * 6 + [_szp], _c_int),
     "kf_attn_bwd": ([_vp, _vp, _vp, _fp, _fp, _vp, _fp, _vp, _vp, _vp, _vp, _vp, _c_sz]
-                    + [_c_int] * 6 + [_vp, _c_int, _vp], _c_int),
+                    + [_c_int] * 6 + [_vp, _vp, _c_int, _vp], _c_int),
     "kf_attn_decode_workspace_size": ([_c_int] * 6 + [_szp], _c_int),
     "kf_attn_decode": ([_vp, _vp, _vp, _vp, _vp, _vp, _fp, _fp, _c_i64, _c_i64, _vp, _vp, _c_sz]
                        + [_c_int] * 7 + [_vp], _c_int),
     "kf_kv_cache_append": ([_vp, _vp, _fp, _fp, _vp, _vp] + [_c_int] * 7 + [_vp], _c_int),
     "kf_attn_capture_workspace_size": ([_c_int] * 7 + [_szp], _c_int),
     "kf_attn_capture": ([_vp, _vp, _vp, _fp, _fp, _fp, _vp, _fp, _vp, _c_sz] + [_c_int] * 6
-                        + [_c_i64] * 6 + [_c_int] * 2 + [_vp, _c_int, _vp], _c_int),
+                        + [_c_i64] * 6 + [_c_int] * 2 + [_vp, _vp, _c_int, _vp], _c_int),
     "kf_prof_enable": ([_c_int], _c_int),
     "kf_prof_collect": ([ctypes.c_char_p, ctypes.POINTER(ctypes.c_float),
                          ctypes.POINTER(ctypes.c_int), _c_int], _c_int),

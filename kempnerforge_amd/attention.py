@@ -15,12 +15,12 @@ Paths (reference lines in ``kempnerforge/model/attention.py``):
 * prefill with a cache (``:169-175,229-231``): ``kf_kv_cache_append`` then the
   forward over the cache with the reference's top-left causal alignment;
 * capture (``:184-189,238-280``): ``kf_attn_capture``;
-* packed documents, ``doc_ids`` without a cache (``:190-227``): the same
-  kernels with the same-document condition applied per tile, so no
+* explicit masks without a cache (``:190-227``): ``doc_ids`` (packed
+  documents) and ``key_padding_mask`` (padded keys, with the reference's NaN
+  guard) run in the same kernels, the conditions applied per tile, so no
   ``[B,1,S,S]`` mask is built (capture included).
 
-The ``key_padding_mask`` branch (``:190-227``), and ``doc_ids`` capture with a
-cache, keep the reference's PyTorch code.
+Capture with a cache and an explicit mask keeps the reference's PyTorch code.
 """
 
 from __future__ import annotations
@@ -164,22 +164,22 @@ class Attention(nn.Module):
             q = self.q_norm(q)
             k = self.k_norm(k)  # type: ignore[reportOptionalCall]
 
+        masked = doc_ids is not None or key_padding_mask is not None
         if self.capture_attention_weights:
-            if key_padding_mask is not None or (doc_ids is not None and kv_cache is not None):
+            if masked and kv_cache is not None:
                 out = self._masked_attention(q, k, v, rope_cos, rope_sin, seq_len, doc_ids,
                                              kv_cache, key_padding_mask)
             else:
-                out, probs = self._capture(q, k, v, rope_cos, rope_sin, kv_cache, doc_ids)
+                out, probs = self._capture(q, k, v, rope_cos, rope_sin, kv_cache, doc_ids,
+                                           key_padding_mask)
                 self.last_attention_weights = probs.to(q.dtype).detach().cpu()
-        elif key_padding_mask is not None:
-            out = self._masked_attention(q, k, v, rope_cos, rope_sin, seq_len, doc_ids,
-                                         kv_cache, key_padding_mask)
-        elif doc_ids is not None:
+        elif masked:
             assert kv_cache is None, (
                 "doc_ids / key_padding_mask are not supported with kv_cache decode "
                 "(would build an incorrect causal mask)."
             )
-            out = ops.attention(q, k, v, rope_cos, rope_sin, causal=True, doc_ids=doc_ids)
+            out = ops.attention(q, k, v, rope_cos, rope_sin, causal=True, doc_ids=doc_ids,
+                                key_padding_mask=key_padding_mask)
         elif kv_cache is None:
             out = ops.attention(q, k, v, rope_cos, rope_sin, causal=True)
         elif seq_len == 1:
@@ -206,11 +206,13 @@ class Attention(nn.Module):
         end = kv_cache.seq_len
         return kv_cache.k[:, :, :end], kv_cache.v[:, :, :end]
 
-    def _capture(self, q, k, v, rope_cos, rope_sin, kv_cache, doc_ids=None):
+    def _capture(self, q, k, v, rope_cos, rope_sin, kv_cache, doc_ids=None,
+                 key_padding_mask=None):
         """Manual-attention replacement (``kempnerforge/model/attention.py:238-280``)."""
         if kv_cache is None:
             out, probs, _ = ops.capture_raw(q, k, v, rope_cos, rope_sin, causal=True,
-                                            k_rotated=False, doc_ids=doc_ids)
+                                            k_rotated=False, doc_ids=doc_ids,
+                                            key_padding_mask=key_padding_mask)
             return out, probs
         seq_len = q.shape[1]
         kc, vc = self._append(k, v, rope_cos, rope_sin, kv_cache)
@@ -220,9 +222,9 @@ class Attention(nn.Module):
 
     def _masked_attention(self, q, k, v, rope_cos, rope_sin, seq_len, doc_ids, kv_cache,
                           key_padding_mask):
-        """Explicit-mask branch, kept as the reference's PyTorch code
-        (``kempnerforge/model/attention.py:190-227``, manual variant ``:262-271``;
-        the manual variant appends to a cache first, as the reference does)."""
+        """Capture with a cache and an explicit mask, kept as the reference's
+        PyTorch code (``kempnerforge/model/attention.py:238-271``): the manual
+        variant appends to the cache first, as the reference does."""
         batch = q.shape[0]
         q = _apply_rope_torch(q.transpose(1, 2), rope_cos, rope_sin)
         if self.capture_attention_weights and kv_cache is not None:

@@ -32,23 +32,25 @@ static FwdArgs make_fwd(const void* q, const void* k, const void* v, const float
                         const float* sin, void* out, float* lse, int B, int Sq, int Sk, int Hq,
                         int Hkv, int D, int64_t ksb, int64_t kss, int64_t ksh, int64_t vsb,
                         int64_t vss, int64_t vsh, int k_rotated, int causal,
-                        const int32_t* doc, int dtype, void* stream) {
+                        const int32_t* doc, const int32_t* kvalid, int dtype, void* stream) {
   FwdArgs a;
   a.q = q; a.k = k; a.v = v; a.cos = cos; a.sin = sin; a.out = out; a.lse = lse;
   a.B = B; a.Sq = Sq; a.Sk = Sk; a.Hq = Hq; a.Hkv = Hkv; a.D = D;
   a.ksb = ksb; a.kss = kss; a.ksh = ksh; a.vsb = vsb; a.vss = vss; a.vsh = vsh;
-  a.k_rotated = k_rotated; a.causal = causal; a.doc = doc; a.dtype = dtype;
+  a.k_rotated = k_rotated; a.causal = causal; a.doc = doc; a.kvalid = kvalid; a.dtype = dtype;
   a.scale = 1.0f / sqrtf((float)D);
   a.stream = (hipStream_t)stream;
   return a;
 }
 
-// Packed documents: the reference builds causal & same-document masks only for
-// full-sequence self-attention (kempnerforge/model/attention.py:204-227).
-static int check_doc(const int32_t* doc, int causal, int Sq, int Sk, int k_rotated) {
-  if (!doc) return KF_OK;
+// Explicit masks: the reference builds causal & same-document & valid-key
+// masks only for full-sequence self-attention (kempnerforge/model/
+// attention.py:204-227, kempnerforge/model/mot.py:188-198).
+static int check_masks(const int32_t* doc, const int32_t* kvalid, int causal, int Sq, int Sk,
+                       int k_rotated) {
+  if (!doc && !kvalid) return KF_OK;
   KF_CHECK_ARG(causal && Sq == Sk && !k_rotated,
-               "doc_ids need causal self-attention over un-rotated keys (Sq == Sk)");
+               "doc_ids / key_valid need causal self-attention over un-rotated keys (Sq == Sk)");
   return KF_OK;
 }
 
@@ -75,7 +77,8 @@ int kf_attn_fwd_workspace_size(int B, int Sq, int Sk, int Hq, int Hkv, int D, in
   // a call that falls back to the generic kernels needs no workspace.
   FwdArgs a = make_fwd((void*)16, (void*)16, (void*)16, (float*)16, (float*)16, (void*)16,
                        nullptr, B, Sq, Sk, Hq, Hkv, D, (int64_t)Sk * Hkv * D, (int64_t)Hkv * D, D,
-                       (int64_t)Sk * Hkv * D, (int64_t)Hkv * D, D, 0, 1, nullptr, dtype, nullptr);
+                       (int64_t)Sk * Hkv * D, (int64_t)Hkv * D, D, 0, 1, nullptr, nullptr, dtype,
+                       nullptr);
   *bytes = fwd_ws(a);
   return KF_OK;
 }
@@ -84,15 +87,16 @@ int kf_attn_fwd(const void* q, const void* k, const void* v, const float* rope_c
                 const float* rope_sin, void* out, float* lse, void* workspace,
                 size_t workspace_bytes, int B, int Sq, int Sk, int Hq, int Hkv, int D,
                 int64_t ksb, int64_t kss, int64_t ksh, int64_t vsb, int64_t vss, int64_t vsh,
-                int k_rotated, int causal, const int32_t* doc_ids, int dtype, void* stream) {
+                int k_rotated, int causal, const int32_t* doc_ids, const int32_t* key_valid,
+                int dtype, void* stream) {
   int rc = check_common(B, Sq, Sk, Hq, Hkv, D, dtype);
   if (rc) return rc;
   KF_CHECK_ARG(q && k && v && rope_cos && rope_sin && out, "null tensor pointer");
   KF_CHECK_ARG(k_rotated || Sk == Sq, "un-rotated keys need Sk == Sq (got %d, %d)", Sk, Sq);
-  rc = check_doc(doc_ids, causal, Sq, Sk, k_rotated);
+  rc = check_masks(doc_ids, key_valid, causal, Sq, Sk, k_rotated);
   if (rc) return rc;
   FwdArgs a = make_fwd(q, k, v, rope_cos, rope_sin, out, lse, B, Sq, Sk, Hq, Hkv, D, ksb, kss,
-                       ksh, vsb, vss, vsh, k_rotated, causal, doc_ids, dtype, stream);
+                       ksh, vsb, vss, vsh, k_rotated, causal, doc_ids, key_valid, dtype, stream);
   if (fwd_mfma_supported(a)) {
     const size_t need = fwd_mfma_workspace(B, Sk, Hkv, D);
     if (workspace_bytes < need || (need && !workspace)) {
@@ -114,26 +118,27 @@ int kf_attn_bwd_workspace_size(int B, int S, int Hq, int Hkv, int D, int dtype, 
   a.dq = a.dk = a.dv = (void*)16;
   a.cos = a.sin = (float*)16;
   *bytes = bwd_mfma_supported(a) ? bwd_mfma_workspace(B, S, Hq, Hkv, D)
-                                 : (size_t)B * Hq * S * sizeof(float);
+                                 : bwd_generic_workspace(B, S, Hq);
   return KF_OK;
 }
 
 int kf_attn_bwd(const void* q, const void* k, const void* v, const float* rope_cos,
                 const float* rope_sin, const void* out, const float* lse, const void* dout,
                 void* dq, void* dk, void* dv, void* workspace, size_t workspace_bytes, int B,
-                int S, int Hq, int Hkv, int D, int causal, const int32_t* doc_ids, int dtype,
-                void* stream) {
+                int S, int Hq, int Hkv, int D, int causal, const int32_t* doc_ids,
+                const int32_t* key_valid, int dtype, void* stream) {
   int rc = check_common(B, S, S, Hq, Hkv, D, dtype);
   if (rc) return rc;
   KF_CHECK_ARG(q && k && v && rope_cos && rope_sin && out && lse && dout && dq && dk && dv,
                "null tensor pointer");
-  rc = check_doc(doc_ids, causal, S, S, 0);
+  rc = check_masks(doc_ids, key_valid, causal, S, S, 0);
   if (rc) return rc;
   BwdArgs a;
   a.q = q; a.k = k; a.v = v; a.cos = rope_cos; a.sin = rope_sin; a.out = out; a.lse = lse;
   a.dout = dout; a.dq = dq; a.dk = dk; a.dv = dv;
   a.B = B; a.S = S; a.Hq = Hq; a.Hkv = Hkv; a.D = D; a.causal = causal; a.dtype = dtype;
   a.doc = doc_ids;
+  a.kvalid = key_valid;
   a.scale = 1.0f / sqrtf((float)D);
   a.stream = (hipStream_t)stream;
   if (bwd_mfma_supported(a)) {
@@ -144,12 +149,12 @@ int kf_attn_bwd(const void* q, const void* k, const void* v, const float* rope_c
     }
     return bwd_mfma(a, workspace);
   }
-  const size_t need = (size_t)B * Hq * S * sizeof(float);
+  const size_t need = bwd_generic_workspace(B, S, Hq);
   if (workspace_bytes < need || !workspace) {
     set_error("workspace too small: need %zu bytes, got %zu", need, workspace_bytes);
     return KF_ERR_WORKSPACE;
   }
-  return bwd_generic(a, (float*)workspace);
+  return bwd_generic(a, workspace);
 }
 
 int kf_attn_decode_workspace_size(int B, int Hq, int Hkv, int D, int max_len, int dtype,
@@ -210,16 +215,16 @@ int kf_attn_capture(const void* q, const void* k, const void* v, const float* ro
                     const float* rope_sin, float* probs, void* out, float* lse, void* workspace,
                     size_t workspace_bytes, int B, int Sq, int Sk, int Hq, int Hkv, int D,
                     int64_t ksb, int64_t kss, int64_t ksh, int64_t vsb, int64_t vss,
-                    int64_t vsh, int k_rotated, int causal, const int32_t* doc_ids, int dtype,
-                    void* stream) {
+                    int64_t vsh, int k_rotated, int causal, const int32_t* doc_ids,
+                    const int32_t* key_valid, int dtype, void* stream) {
   int rc = check_common(B, Sq, Sk, Hq, Hkv, D, dtype);
   if (rc) return rc;
   KF_CHECK_ARG(q && k && v && rope_cos && rope_sin && out && probs && lse, "null tensor pointer");
   KF_CHECK_ARG(k_rotated || Sk == Sq, "un-rotated keys need Sk == Sq (got %d, %d)", Sk, Sq);
-  rc = check_doc(doc_ids, causal, Sq, Sk, k_rotated);
+  rc = check_masks(doc_ids, key_valid, causal, Sq, Sk, k_rotated);
   if (rc) return rc;
   FwdArgs a = make_fwd(q, k, v, rope_cos, rope_sin, out, lse, B, Sq, Sk, Hq, Hkv, D, ksb, kss,
-                       ksh, vsb, vss, vsh, k_rotated, causal, doc_ids, dtype, stream);
+                       ksh, vsb, vss, vsh, k_rotated, causal, doc_ids, key_valid, dtype, stream);
   if (fwd_mfma_supported(a) && ((uintptr_t)probs & 15) == 0) {
     const size_t need = fwd_mfma_workspace(B, Sk, Hkv, D);
     if (workspace_bytes < need || !workspace) {

@@ -22,10 +22,14 @@
 // The algorithm is the standard flash-attention backward (recompute P from the
 // saved log-sum-exp; dS = P o (dP - Delta)).
 //
-// Packed documents (DOC): kv_prep records each 64-position tile's document-id
-// range.  dkdv walks only the query tiles whose range meets its key block's,
-// dq only the key tiles whose range meets its rows'; tiles not entirely in the
-// workgroup's single document get P = 0 where doc[query] != doc[key].
+// Packed documents (MASK_DOC): kv_prep records each 64-position tile's
+// document-id range.  dkdv walks only the query tiles whose range meets its key
+// block's, dq only the key tiles whose range meets its rows'; tiles not
+// entirely in the workgroup's single document get P = 0 where doc[query] !=
+// doc[key].  Key padding (MASK_KPM): kv_prep records each tile's valid-key
+// count and first valid key; tiles without a valid key are skipped, rows before
+// the batch row's first valid key (guarded) see every key, the others need
+// the key valid.
 #include "kf_common.h"
 #include "kf_internal.h"
 #include "kf_mfma.h"
@@ -106,11 +110,14 @@ struct DkdvStage {
   float l[BQ], dl[BQ];
 };
 
-// DOC: qlist[0, nlist) holds the listed query tiles (DOC_MASK_FLAG: needs the
-// element test), sQD the staged query documents, drow the batch row's ids; the
-// caller has already staged iteration 0 (head 0, the diagonal tile qt0, which
-// is always listed first) with dkdv_stage_first.
-template <int D, bool DSROLE, bool DOC>
+// MASK_DOC: qlist[0, nlist) holds the listed query tiles (DOC_MASK_FLAG: needs
+// the element test), sQD the staged query documents, drow the batch row's ids;
+// the caller has already staged iteration 0 (head 0, the diagonal tile qt0,
+// which is always listed first) with dkdv_stage_first.
+// MASK_KPM: qlist as above, drow the key-validity row, fv the first valid
+// key's position: query rows before it (guarded) see every key, other rows
+// need the key valid and not after them.
+template <int D, bool DSROLE, int MODE>
 __device__ __forceinline__ void dkdv_role(
     DkdvStage<D>* st, u32x4* sP, const bf16* __restrict__ krot, const bf16* __restrict__ vn,
     const bf16* __restrict__ qrot, const bf16* __restrict__ don,
@@ -118,7 +125,8 @@ __device__ __forceinline__ void dkdv_role(
     const float* __restrict__ cos, const float* __restrict__ sin, bf16* __restrict__ dk,
     bf16* __restrict__ dv, int S, int P, int Hq, int Hkv, int n_rep, int b, int g, int bh, int k0,
     int w, int lane, float scale_log2, float scale, int causal, const int32_t* __restrict__ drow,
-    const uint16_t* qlist, int nlist, int32_t (*sQD)[BQ]) {
+    const uint16_t* qlist, int nlist, int32_t (*sQD)[BQ], int fv) {
+  constexpr bool DOC = MODE == MASK_DOC, KPM = MODE == MASK_KPM, LIST = DOC || KPM;
   constexpr int KS = D / 16, DT = D / 32, HALF = D / 2;
   constexpr int KR = D / 8;
   constexpr int PF = 3;  // fragment reads run PF MFMAs ahead
@@ -128,14 +136,15 @@ __device__ __forceinline__ void dkdv_role(
 
   const int nqt = (S + BQ - 1) / BQ;
   const int qt0 = causal ? k0 / BQ : 0;
-  const int per_head = DOC ? nlist : nqt - qt0;
+  const int per_head = LIST ? nlist : nqt - qt0;
   const int total = per_head > 0 ? per_head * n_rep : 0;
-  // iteration -> query tile entry (tile | DOC_MASK_FLAG for DOC), head-major
+  // iteration -> query tile entry (tile | DOC_MASK_FLAG when listed), head-major
   auto entry = [&](int it) -> int {
-    return DOC ? __builtin_amdgcn_readfirstlane((int)qlist[it % per_head]) : qt0 + it % per_head;
+    return LIST ? __builtin_amdgcn_readfirstlane((int)qlist[it % per_head]) : qt0 + it % per_head;
   };
-  auto tile_of = [](int e) -> int { return DOC ? e & ~DOC_MASK_FLAG : e; };
-  const int kdoc = DOC ? drow[min(key, S - 1)] : 0;
+  auto tile_of = [](int e) -> int { return LIST ? e & ~DOC_MASK_FLAG : e; };
+  // DOC: this lane's key's document; KPM: 1 if this lane's key is valid
+  const int kdoc = DOC ? drow[min(key, S - 1)] : KPM ? (key < S && drow[min(key, S - 1)] != 0) : 0;
 
   auto stage_tile = [&](int hl, int qtile, int buf) {
     const int64_t bhq = (int64_t)b * Hq + g * n_rep + hl;
@@ -182,7 +191,7 @@ __device__ __forceinline__ void dkdv_role(
     const int q0 = tile_of(e) * BQ;
     const int rel = key - q0;  // rows r of this tile see the key when r >= rel
     const bool diag = causal && q0 < k0 + BKV;
-    const bool dmask = DOC && (e & DOC_MASK_FLAG);
+    const bool dmask = LIST && (e & DOC_MASK_FLAG);
 
     // phase 1: S (P waves) or dP (dS waves) for both 32-row halves
     f32x16 x[2];
@@ -214,13 +223,21 @@ __device__ __forceinline__ void dkdv_role(
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
             float p = fast_exp2(__builtin_fmaf(x[mt][4 * gq + j], scale_log2, -l4[j]));
-            if (diag) p = (rel > r0 + j) ? 0.f : p;
+            if (!(KPM && dmask) && diag) p = (rel > r0 + j) ? 0.f : p;
             v[j] = p;
           }
-          if (dmask) {
+          if (DOC && dmask) {
             const i32x4 qd = *(const i32x4*)&sQD[buf][r0];
 #pragma unroll
             for (int j = 0; j < 4; ++j) v[j] = qd[j] != kdoc ? 0.f : v[j];
+          }
+          if (KPM && dmask) {
+            // guarded rows keep every key; the others need it valid and not later
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              const bool guarded = q0 + r0 + j < fv;
+              v[j] = (!guarded && (rel > r0 + j || !kdoc)) ? 0.f : v[j];
+            }
           }
           pk[2 * mt + (gq >> 1)][2 * (gq & 1)] = pack2(v[0], v[1]);
           pk[2 * mt + (gq >> 1)][2 * (gq & 1) + 1] = pack2(v[2], v[3]);
@@ -322,26 +339,52 @@ __device__ __forceinline__ void dkdv_stage_first(
   if (w == 2) dma4(lds_addr(sqd), (uint32_t)min(q0 + lane, S - 1) * 4u, drow);
 }
 
-template <int D, bool DOC>
+template <int D, int MODE>
 __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(
     const bf16* __restrict__ krot, const bf16* __restrict__ vn, const bf16* __restrict__ qrot,
     const bf16* __restrict__ don, const float* __restrict__ lse2, const float* __restrict__ delta,
     const float* __restrict__ cos, const float* __restrict__ sin, bf16* __restrict__ dk,
     bf16* __restrict__ dv, int S, int P, int Hq, int Hkv, int n_rep, int nkb, float scale_log2,
-    float scale, int causal, const int32_t* __restrict__ doc, const int2* __restrict__ ranges) {
+    float scale, int causal, const int32_t* __restrict__ aux, const int2* __restrict__ ranges) {
+  constexpr bool DOC = MODE == MASK_DOC, KPM = MODE == MASK_KPM;
   __shared__ __attribute__((aligned(16))) DkdvStage<D> st[2];
   __shared__ __attribute__((aligned(16))) u32x4 sP[4 * 4 * 64];  // [key group][chunk][lane]
   __shared__ __attribute__((aligned(16))) int32_t sQD[2][BQ];   // DOC: query document ids
-  __shared__ uint16_t sList[DOC_MAX_TILES];                      // DOC: listed query tiles
-  __shared__ int sCount;
+  __shared__ uint16_t sList[DOC_MAX_TILES];                      // listed query tiles
+  __shared__ int sCount, sFirst;
   const int w = wave_id(), lane = threadIdx.x & 63;
   const int logical = xcd_logical_id(blockIdx.x, gridDim.x);
   const int bh = logical / nkb;
   const int kb = logical % nkb;  // ascending: the longest causal key tiles first
   const int b = bh / Hkv, g = bh % Hkv;
   const int k0 = kb * BKV;
-  const int32_t* drow = DOC ? doc + (int64_t)b * S : nullptr;
-  int nlist = 0;
+  const int32_t* drow = DOC || KPM ? aux + (int64_t)b * S : nullptr;
+  const int2* rec = ranges + (int64_t)b * (P / BN);
+  int nlist = 0, fv = 0;
+  if constexpr (KPM) {
+    if (w == 0) {
+      const int f = kpm_first_valid(rec, P / BN, lane);
+      // valid keys in this block (its two 64-key tiles) against its keys below S
+      const int t0 = k0 / BN;
+      const int nval = rec[t0].x + (t0 + 1 < P / BN ? rec[t0 + 1].x : 0);
+      const int nkeys = min(BKV, S - k0);
+      const int qt0 = k0 / BQ;
+      // query tiles holding guarded rows, then the causal ones if a key is valid
+      const int n = kpm_tile_list(
+          rec, 0, (S + BQ - 1) / BQ,
+          [&](int t, int2) {
+            return t * BQ < f ? 2 : (t >= qt0 && nval > 0) ? (nval < nkeys ? 2 : 1) : 0;
+          },
+          sList, lane);
+      if (lane == 0) {
+        sCount = n;
+        sFirst = f;
+      }
+    }
+    __syncthreads();
+    nlist = __builtin_amdgcn_readfirstlane(sCount);
+    fv = __builtin_amdgcn_readfirstlane(sFirst);
+  }
   if constexpr (DOC) {
     const int qt0 = k0 / BQ;  // the diagonal query tile: always listed, first
     dkdv_stage_first<D>(st, qrot, don, lse2, delta, drow, S, P, (int64_t)b * Hq + g * n_rep,
@@ -355,13 +398,13 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(
     nlist = __builtin_amdgcn_readfirstlane(sCount);
   }
   if (w >= 4)
-    dkdv_role<D, true, DOC>(st, sP, krot, vn, qrot, don, lse2, delta, cos, sin, dk, dv, S, P, Hq,
-                            Hkv, n_rep, b, g, bh, k0, w, lane, scale_log2, scale, causal, drow,
-                            sList, nlist, sQD);
-  else
-    dkdv_role<D, false, DOC>(st, sP, krot, vn, qrot, don, lse2, delta, cos, sin, dk, dv, S, P,
+    dkdv_role<D, true, MODE>(st, sP, krot, vn, qrot, don, lse2, delta, cos, sin, dk, dv, S, P,
                              Hq, Hkv, n_rep, b, g, bh, k0, w, lane, scale_log2, scale, causal,
-                             drow, sList, nlist, sQD);
+                             drow, sList, nlist, sQD, fv);
+  else
+    dkdv_role<D, false, MODE>(st, sP, krot, vn, qrot, don, lse2, delta, cos, sin, dk, dv, S, P,
+                              Hq, Hkv, n_rep, b, g, bh, k0, w, lane, scale_log2, scale, causal,
+                              drow, sList, nlist, sQD, fv);
 }
 
 // dQ workgroup: 8 wavefronts x 32 rows = 256 (query head, position) rows of one
@@ -369,22 +412,23 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(
 // DOC walks the listed key tiles last to first, like the forward.
 constexpr int DQ_ROWS = 256;
 
-template <int D, bool DOC>
+template <int D, int MODE>
 __global__ __launch_bounds__(512, 1) void bwd_dq_kernel(
     const bf16* __restrict__ qrot, const bf16* __restrict__ don, const float* __restrict__ lse2,
     const float* __restrict__ delta, const bf16* __restrict__ krot, const bf16* __restrict__ vn,
     const float* __restrict__ cos, const float* __restrict__ sin, bf16* __restrict__ dq, int S,
     int P, int Hq, int Hkv, int n_rep, int bm_pos, int nqb, float scale_log2, float scale,
-    int causal, const int32_t* __restrict__ doc, const int2* __restrict__ ranges) {
+    int causal, const int32_t* __restrict__ aux, const int2* __restrict__ ranges) {
+  constexpr bool DOC = MODE == MASK_DOC, KPM = MODE == MASK_KPM, LIST = DOC || KPM;
   constexpr int KS = D / 16, DT = D / 32, HALF = D / 2;
   constexpr int KR = D / 8;
   struct Stage {
     bf16 k[BN * D], v[BN * D];
   };
   __shared__ __attribute__((aligned(16))) Stage st[2];
-  __shared__ __attribute__((aligned(16))) int32_t sKD[2][BN];  // DOC: key document ids
-  __shared__ uint16_t sList[DOC_MAX_TILES];                     // DOC: listed key tiles
-  __shared__ int sCount;
+  __shared__ __attribute__((aligned(16))) int32_t sKD[2][BN];  // LIST: per-key aux values
+  __shared__ uint16_t sList[DOC_MAX_TILES];                     // LIST: listed key tiles
+  __shared__ int sCount, sFirst;
 
   const int tid = threadIdx.x, w = wave_id(), lane = tid & 63, hh = lane >> 5, c32 = lane & 31;
   const int logical = xcd_logical_id(blockIdx.x, gridDim.x);
@@ -394,34 +438,54 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_kernel(
 
   const int kend = causal ? min(S, ri.p0 + bm_pos) : S;
   int ntiles = (kend + BN - 1) / BN;
-  const int32_t* drow = DOC ? doc + (int64_t)ri.b * S : nullptr;
+  const int32_t* drow = LIST ? aux + (int64_t)ri.b * S : nullptr;
+  const int2* rec = ranges + (int64_t)ri.b * (P / BN);
   const bf16* kbase = krot + (int64_t)bh * P * D;
   const bf16* vbase = vn + (int64_t)bh * P * D;
   auto stage = [&](int t, int buf) {
     tile_to_lds<BN, KR, 8>(kbase + (int64_t)t * BN * D, D, st[buf].k, w, lane);
     tile_to_lds<BN, KR, 8>(vbase + (int64_t)t * BN * D, D, st[buf].v, w, lane);
-    if (DOC && w == 0) dma4(lds_addr(sKD[buf]), (uint32_t)min(t * BN + lane, S - 1) * 4u, drow);
+    if (LIST && w == 0) dma4(lds_addr(sKD[buf]), (uint32_t)min(t * BN + lane, S - 1) * 4u, drow);
   };
-  int di = 0;
+  int di = 0;        // DOC: this row's document
+  bool grd = false;  // KPM: this row is guarded (before the first valid key)
   if constexpr (DOC) {
     // walked backwards, as in the forward: the always-listed last tile loads
     // while the list is built
     if (ntiles > 0) stage(ntiles - 1, 0);
     di = drow[min(ri.pos, S - 1)];
     if (w == 0) {
-      const int n = doc_tile_list(drow, ri.p0, min(ri.p0 + bm_pos, S),
-                                  ranges + (int64_t)ri.b * (P / BN), 0, ntiles, sList, lane);
+      const int n = doc_tile_list(drow, ri.p0, min(ri.p0 + bm_pos, S), rec, 0, ntiles, sList,
+                                  lane);
       if (lane == 0) sCount = n;
     }
     __syncthreads();
     ntiles = __builtin_amdgcn_readfirstlane(sCount);
+  } else if constexpr (KPM) {
+    const int nall = (S + BN - 1) / BN;
+    if (w == 0) {
+      const int f = kpm_first_valid(rec, P / BN, lane);
+      const bool guard_block = ri.p0 < f;  // a guarded row needs every key tile
+      const int n = kpm_tile_list(rec, 0, guard_block ? nall : ntiles,
+                                  [&](int, int2 r) { return guard_block ? 2 : r.x == 0 ? 0 : r.x < BN ? 2 : 1; },
+                                  sList, lane);
+      if (lane == 0) {
+        sCount = n;
+        sFirst = f;
+      }
+    }
+    __syncthreads();
+    ntiles = __builtin_amdgcn_readfirstlane(sCount);
+    grd = ri.pos < sFirst;
   } else {
     if (ntiles > 0) stage(0, 0);
   }
   auto entry = [&](int it) -> int {
-    return DOC ? __builtin_amdgcn_readfirstlane((int)sList[ntiles - 1 - it]) : it;
+    return DOC ? __builtin_amdgcn_readfirstlane((int)sList[ntiles - 1 - it])
+               : KPM ? __builtin_amdgcn_readfirstlane((int)sList[it]) : it;
   };
-  auto tile_of = [](int e) -> int { return DOC ? e & ~DOC_MASK_FLAG : e; };
+  auto tile_of = [](int e) -> int { return LIST ? e & ~DOC_MASK_FLAG : e; };
+  if (KPM && ntiles > 0) stage(tile_of(entry(0)), 0);
 
   bf16x8 qf[KS], df[KS];
   float l2 = INFINITY, dl = 0.f;
@@ -466,10 +530,10 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_kernel(
     if (it + 1 < ntiles) stage(tile_of(entry(it + 1)), buf ^ 1);
     const Stage& S_ = st[buf];
     const int k0 = t * BN;
-    const bool dmask = DOC && (e & DOC_MASK_FLAG);
+    const bool dmask = LIST && (e & DOC_MASK_FLAG);
     const bool need_mask = (causal && k0 + BN - 1 > ri.p0) || (k0 + BN > S) || dmask;
-    // last visible key of this lane's row, relative to k0
-    const int lim = (causal ? min(ri.pos, S - 1) : S - 1) - k0;
+    // last visible key of this lane's row, relative to k0 (a guarded row: any below S)
+    const int lim = (causal && !grd ? min(ri.pos, S - 1) : S - 1) - k0;
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) {
       f32x16 s, dp;
@@ -516,7 +580,8 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_kernel(
           if (need_mask) {
             const int local = 32 * mt + 8 * ((i + j) >> 2) + 4 * hh + ((i + j) & 3);
             p = local > lim ? 0.f : p;
-            if (dmask) p = kd[j] != di ? 0.f : p;
+            if (DOC && dmask) p = kd[j] != di ? 0.f : p;
+            if (KPM && dmask && !grd) p = kd[j] == 0 ? 0.f : p;
           }
           dsv[j] = p * (dp[i + j] - dl);
         }
@@ -598,7 +663,7 @@ int launch_bwd(const BwdArgs& a, void* workspace) {
   fa.kss = fa.vss = (int64_t)a.Hkv * D;
   fa.ksh = fa.vsh = D;
   fa.k_rotated = 0; fa.dtype = BF16; fa.stream = a.stream;
-  fa.doc = a.doc; fa.causal = a.causal;
+  fa.doc = a.doc; fa.kvalid = a.kvalid; fa.causal = a.causal;
   int rc = launch_kv_prep(fa, w.krot, w.vn, P, w.ranges);
   if (rc) return rc;
   KF_LAUNCH("q_prep_bwd", q_prep_bwd_kernel<D>, dim3(P / BN, a.B * a.Hq), dim3(256), 0, a.stream,
@@ -606,18 +671,25 @@ int launch_bwd(const BwdArgs& a, void* workspace) {
             w.qrot, w.don, w.lse2, w.delta, a.S, P, a.Hq);
   KF_CHECK_LAUNCH();
   const int nkb = P / BKV;
-  const bool doc = a.doc != nullptr;
-  KF_LAUNCH("bwd_dkdv", (doc ? bwd_dkdv_kernel<D, true> : bwd_dkdv_kernel<D, false>),
+  const int mode = a.doc ? MASK_DOC : a.kvalid ? MASK_KPM : MASK_NONE;
+  const int32_t* aux = a.doc ? a.doc : a.kvalid;
+  KF_LAUNCH("bwd_dkdv",
+            (mode == MASK_DOC   ? bwd_dkdv_kernel<D, MASK_DOC>
+             : mode == MASK_KPM ? bwd_dkdv_kernel<D, MASK_KPM>
+                                : bwd_dkdv_kernel<D, MASK_NONE>),
             dim3(nkb * a.B * a.Hkv), dim3(512), 0, a.stream, w.krot, w.vn, w.qrot, w.don, w.lse2,
             w.delta, a.cos, a.sin, (bf16*)a.dk, (bf16*)a.dv, a.S, P, a.Hq, a.Hkv, n_rep, nkb,
-            scale_log2, a.scale, a.causal, a.doc, w.ranges);
+            scale_log2, a.scale, a.causal, aux, w.ranges);
   KF_CHECK_LAUNCH();
   const int bm_pos = DQ_ROWS / n_rep;
   const int nqb = (a.S + bm_pos - 1) / bm_pos;
-  KF_LAUNCH("bwd_dq", (doc ? bwd_dq_kernel<D, true> : bwd_dq_kernel<D, false>),
+  KF_LAUNCH("bwd_dq",
+            (mode == MASK_DOC   ? bwd_dq_kernel<D, MASK_DOC>
+             : mode == MASK_KPM ? bwd_dq_kernel<D, MASK_KPM>
+                                : bwd_dq_kernel<D, MASK_NONE>),
             dim3(nqb * a.B * a.Hkv), dim3(512), 0, a.stream, w.qrot, w.don, w.lse2, w.delta,
             w.krot, w.vn, a.cos, a.sin, (bf16*)a.dq, a.S, P, a.Hq, a.Hkv, n_rep, bm_pos, nqb,
-            scale_log2, a.scale, a.causal, a.doc, w.ranges);
+            scale_log2, a.scale, a.causal, aux, w.ranges);
   KF_CHECK_LAUNCH();
   return KF_OK;
 }
@@ -625,7 +697,8 @@ int launch_bwd(const BwdArgs& a, void* workspace) {
 }  // namespace
 
 bool bwd_mfma_supported(const BwdArgs& a) {
-  if (a.doc && pad_len(a.S) / BN > DOC_MAX_TILES) return false;
+  if (a.doc && a.kvalid) return false;  // one explicit mask kind at a time
+  if ((a.doc || a.kvalid) && pad_len(a.S) / BN > DOC_MAX_TILES) return false;
   if (a.dtype != BF16 || (a.D != 64 && a.D != 128)) return false;
   const int n_rep = a.Hq / a.Hkv;
   if (n_rep < 1 || n_rep > ROWS) return false;  // also bounds DQ_ROWS / n_rep >= 2

@@ -4,7 +4,8 @@
 //  kv_prep   stages one KV head's keys and values in the layout the MFMA loop
 //            reads: K rotated by RoPE (eager bf16 rounding) and V, both
 //            [bh][Skp][D] with keys >= Sk zeroed.  The backward uses it too.
-//            With document ids it also records each 64-key tile's id range.
+//            With document ids it also records each 64-key tile's id range,
+//            with a key-validity mask its valid-key count and first valid key.
 //  fwd_mfma  flash forward.  One workgroup = 4 wavefronts = 128 "rows", where
 //            a row is (query head of the KV group, position): every K/V tile in
 //            LDS is shared by all n_rep query heads of the group.  Each wave
@@ -35,7 +36,8 @@ __global__ __launch_bounds__(256) void kv_prep_kernel(
     const bf16* __restrict__ k, const bf16* __restrict__ v, const float* __restrict__ cos,
     const float* __restrict__ sin, bf16* __restrict__ krot, bf16* __restrict__ vn, int Sk,
     int Skp, int Hkv, int64_t ksb, int64_t kss, int64_t ksh, int64_t vsb, int64_t vss,
-    int64_t vsh, int k_rotated, const int32_t* __restrict__ doc, int2* __restrict__ ranges) {
+    int64_t vsh, int k_rotated, const int32_t* __restrict__ doc, const int32_t* __restrict__ kvalid,
+    int2* __restrict__ ranges) {
   constexpr int HALF = D / 2;
   constexpr int CP = HALF / 8;
   const int s0 = blockIdx.x * BN;
@@ -49,6 +51,14 @@ __global__ __launch_bounds__(256) void kv_prep_kernel(
     const int d = s < Sk ? doc[(int64_t)b * Sk + s] : 0;
     const int lo = wave_min_i(s < Sk ? d : INT_MAX), hi = wave_max_i(s < Sk ? d : INT_MIN);
     if (tid == 0) ranges[(int64_t)b * gridDim.x + blockIdx.x] = make_int2(lo, hi);
+  } else if (kvalid != nullptr && g == 0 && tid < 64) {
+    // number of valid keys in this tile and the first one's position
+    const int s = s0 + tid;
+    const bool ok = s < Sk && kvalid[(int64_t)b * Sk + s] != 0;
+    const uint64_t m = __builtin_amdgcn_ballot_w64(ok);
+    if (tid == 0)
+      ranges[(int64_t)b * gridDim.x + blockIdx.x] =
+          make_int2(__builtin_popcountll(m), m ? s0 + __builtin_ctzll(m) : INT_MAX);
   }
 
   for (int it = tid; it < BN * CP; it += 256) {
@@ -115,27 +125,33 @@ __device__ __forceinline__ void load_q_frag(const bf16* __restrict__ q,
   }
 }
 
-// DOC: packed documents (doc != null, causal, Sq == Sk).  The workgroup walks
-// only the key tiles listed by doc_tile_list, last to first; listed tiles
-// carrying the mask flag get the element test doc[key] == doc[query] next to
-// the causal one.
-// The running max starts at -1e30 instead of -inf there, because a row can see
-// no key at all in a listed tile (exp2 of -inf - -inf would be NaN); every row
-// sees at least its own position, so the final max is a real score.
-template <int D, bool DOC>
+// MODE selects the explicit mask (causal self-attention, Sq == Sk):
+//  MASK_DOC  packed documents (aux = document ids).  The workgroup walks only
+//            the key tiles listed by doc_tile_list, last to first; listed tiles
+//            carrying the mask flag get the element test doc[key] == doc[query]
+//            next to the causal one.
+//  MASK_KPM  key padding (aux = 1 for a valid key).  Tiles without a valid key
+//            are skipped; tiles with some padded keys get the element test.
+//            Rows before the first valid key (the guarded prefix) attend every
+//            key, so a workgroup holding one walks all tiles.
+// The running max starts at -1e30 instead of -inf in both, because a row can
+// see no key at all in a listed tile (exp2 of -inf - -inf would be NaN); every
+// row sees some key in some tile, so the final max is a real score.
+template <int D, int MODE>
 __global__ __launch_bounds__(256, 2) void fwd_mfma_kernel(
     const bf16* __restrict__ q, const float* __restrict__ cos, const float* __restrict__ sin,
     const bf16* __restrict__ krot, const bf16* __restrict__ vn, bf16* __restrict__ out,
     float* __restrict__ lse, int Sq, int Sk, int Skp, int Hq, int Hkv, int n_rep, int bm_pos,
-    int nqb, float scale_log2, int causal, const int32_t* __restrict__ doc,
+    int nqb, float scale_log2, int causal, const int32_t* __restrict__ aux,
     const int2* __restrict__ ranges) {
+  constexpr bool DOC = MODE == MASK_DOC, KPM = MODE == MASK_KPM, LIST = DOC || KPM;
   constexpr int KS = D / 16, DT = D / 32;
   constexpr int KR = D / 8;  // 16-byte chunks per K / V row
   __shared__ __attribute__((aligned(16))) bf16 sK[2][BN * D];
   __shared__ __attribute__((aligned(16))) bf16 sV[2][BN * D];
-  __shared__ __attribute__((aligned(16))) int32_t sKD[2][BN];  // DOC: key document ids
-  __shared__ uint16_t sList[DOC_MAX_TILES];                     // DOC: listed key tiles
-  __shared__ int sCount;
+  __shared__ __attribute__((aligned(16))) int32_t sKD[2][BN];  // LIST: per-key aux values
+  __shared__ uint16_t sList[DOC_MAX_TILES];                     // LIST: listed key tiles
+  __shared__ int sCount, sFirst;
 
   const int tid = threadIdx.x, w = wave_id(), lane = tid & 63, hh = lane >> 5, c32 = lane & 31;
   const int logical = xcd_logical_id(blockIdx.x, gridDim.x);
@@ -144,41 +160,62 @@ __global__ __launch_bounds__(256, 2) void fwd_mfma_kernel(
 
   const int kend = causal ? min(Sk, min(ri.p0 + bm_pos, Sq)) : Sk;
   int ntiles = (kend + BN - 1) / BN;
-  const int32_t* drow = DOC ? doc + (int64_t)ri.b * Sk : nullptr;
+  const int32_t* arow = LIST ? aux + (int64_t)ri.b * Sk : nullptr;
+  const int2* rec = ranges + (int64_t)ri.b * (Skp / BN);
   const bf16* kbase = krot + (int64_t)bh * Skp * D;
   const bf16* vbase = vn + (int64_t)bh * Skp * D;
   auto stage = [&](int t, int buf) {
     tile_to_lds<BN, KR>(kbase + (int64_t)t * BN * D, D, sK[buf], w, lane);
     tile_to_lds<BN, KR>(vbase + (int64_t)t * BN * D, D, sV[buf], w, lane);
-    if (DOC && w == 0) dma4(lds_addr(sKD[buf]), (uint32_t)min(t * BN + lane, Sk - 1) * 4u, drow);
+    if (LIST && w == 0) dma4(lds_addr(sKD[buf]), (uint32_t)min(t * BN + lane, Sk - 1) * 4u, arow);
   };
-  int di = 0;
+  int di = 0;       // DOC: this row's document
+  bool grd = false;  // KPM: this row is in the guarded prefix
   if constexpr (DOC) {
     // The list is walked backwards.  Its last tile, the one holding the
     // block's last position, is always listed: it loads while the list is built.
     if (ntiles > 0) stage(ntiles - 1, 0);
-    di = drow[min(ri.pos, Sq - 1)];
+    di = arow[min(ri.pos, Sq - 1)];
     if (w == 0) {
-      const int n = doc_tile_list(drow, ri.p0, min(ri.p0 + bm_pos, Sq),
-                                  ranges + (int64_t)ri.b * (Skp / BN), 0, ntiles, sList, lane);
+      const int n = doc_tile_list(arow, ri.p0, min(ri.p0 + bm_pos, Sq), rec, 0, ntiles, sList,
+                                  lane);
       if (lane == 0) sCount = n;
     }
     __syncthreads();
     ntiles = __builtin_amdgcn_readfirstlane(sCount);
+  } else if constexpr (KPM) {
+    const int nall = Skp / BN;
+    if (w == 0) {
+      const int fv = kpm_first_valid(rec, nall, lane);
+      // a guarded row attends every key: list (and test) every tile
+      const bool guard_block = ri.p0 < fv;
+      const int n = kpm_tile_list(rec, 0, guard_block ? nall : ntiles,
+                                  [&](int, int2 r) { return guard_block ? 2 : r.x == 0 ? 0 : r.x < BN ? 2 : 1; },
+                                  sList, lane);
+      if (lane == 0) {
+        sCount = n;
+        sFirst = fv;
+      }
+    }
+    __syncthreads();
+    ntiles = __builtin_amdgcn_readfirstlane(sCount);
+    grd = ri.pos < sFirst;
   } else {
     if (ntiles > 0) stage(0, 0);
   }
-  // iteration -> entry (tile | DOC_MASK_FLAG when it needs the document test)
+  // iteration -> entry (tile | DOC_MASK_FLAG when it needs the element test)
   auto entry = [&](int it) -> int {
-    return DOC ? __builtin_amdgcn_readfirstlane((int)sList[ntiles - 1 - it]) : it;
+    return DOC ? __builtin_amdgcn_readfirstlane((int)sList[ntiles - 1 - it])
+               : KPM ? __builtin_amdgcn_readfirstlane((int)sList[it]) : it;
   };
-  auto tile_of = [](int e) -> int { return DOC ? e & ~DOC_MASK_FLAG : e; };
+  auto tile_of = [](int e) -> int { return LIST ? e & ~DOC_MASK_FLAG : e; };
+  if (KPM && ntiles > 0) stage(tile_of(entry(0)), 0);
 
   bf16x8 qf[KS];
   load_q_frag<D>(q, cos, sin, ri, Sq, Hq, hh, qf);
   const TrOffsets<D> tro = tr_offsets<D>(lane);
 
-  float m = DOC ? -1e30f : -INFINITY, lsum = 0.f;
+  float m = LIST ? -1e30f : -INFINITY, lsum = 0.f;
   f32x16 acc[DT];
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt)
@@ -211,8 +248,10 @@ __global__ __launch_bounds__(256, 2) void fwd_mfma_kernel(
 
     const int k0 = t * BN;
     const bool need_mask = (causal && k0 + BN - 1 > ri.p0) || (k0 + BN > Sk);
-    if (DOC && (e & DOC_MASK_FLAG)) {
-      const int lim = min(ri.pos, Sk - 1) - k0;
+    if (LIST && (e & DOC_MASK_FLAG)) {
+      // DOC: causal and same document; KPM: causal and valid, or anything
+      // below Sk for a guarded row
+      const int lim = (grd ? Sk - 1 : min(ri.pos, Sk - 1)) - k0;
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
@@ -222,7 +261,8 @@ __global__ __launch_bounds__(256, 2) void fwd_mfma_kernel(
           for (int j = 0; j < 4; ++j) {
             const int local = 32 * mt + 8 * g4 + 4 * hh + j;
             const int i = 4 * g4 + j;
-            s[mt][i] = (local > lim || kd[j] != di) ? -INFINITY : s[mt][i];
+            const bool other = DOC ? kd[j] != di : (!grd && kd[j] == 0);
+            s[mt][i] = (local > lim || other) ? -INFINITY : s[mt][i];
           }
         }
     } else if (need_mask) {
@@ -305,15 +345,18 @@ __global__ __launch_bounds__(256, 2) void fwd_mfma_kernel(
 // A operand: row = l%32, k = 8h + j) and K^T the B operand read from LDS, so a
 // C register i holds (query row 8*(i/4)+4h+(i%4), key l%32): for a fixed i the
 // 32 lanes of one half write 32 consecutive floats of one row.  Key tiles fully
-// above the diagonal are written as zeros without computing.  DOC: keys of
-// another document get probability 0 (each lane tests its one key per 32-key
-// half against the document of each of its 16 rows).
-template <int D, bool DOC>
+// above the diagonal are written as zeros without computing.  MASK_DOC: keys
+// of another document get probability 0 (each lane tests its one key per
+// 32-key half against the document of each of its 16 rows).  MASK_KPM: padded
+// keys get 0, except in guarded rows (before the first valid key), which
+// attend every key; a workgroup holding one computes every tile.
+template <int D, int MODE>
 __global__ __launch_bounds__(256, 2) void capture_probs_mfma_kernel(
     const bf16* __restrict__ q, const float* __restrict__ cos, const float* __restrict__ sin,
     const bf16* __restrict__ krot, const float* __restrict__ lse, float* __restrict__ probs,
     int Sq, int Sk, int Skp, int Hq, int Hkv, int n_rep, int bm_pos, int nqb, float scale_log2,
-    int causal, const int32_t* __restrict__ doc) {
+    int causal, const int32_t* __restrict__ aux, const int2* __restrict__ ranges) {
+  constexpr bool DOC = MODE == MASK_DOC, KPM = MODE == MASK_KPM;
   constexpr int KS = D / 16;
   constexpr int KR = D / 8;
   __shared__ __attribute__((aligned(16))) bf16 sK[2][BN * D];
@@ -340,14 +383,17 @@ __global__ __launch_bounds__(256, 2) void capture_probs_mfma_kernel(
   // the tile loop
   const int qmax = min(ri.p0 + bm_pos, Sq) - 1;  // largest position in the block
   const int ntiles_all = (Sk + BN - 1) / BN;
-  const int ntiles = causal ? min(ntiles_all, (qmax + BN) / BN) : ntiles_all;
+  // KPM: first valid key of the batch row; rows before it are guarded
+  const int fv = KPM ? kpm_first_valid(ranges + (int64_t)ri.b * (Skp / BN), Skp / BN, lane) : 0;
+  const int ntiles = causal && !(KPM && ri.p0 < fv) ? min(ntiles_all, (qmax + BN) / BN)
+                                                      : ntiles_all;
   const bf16* kbase = krot + (int64_t)bh * Skp * D;
   float* pbase = probs + (((int64_t)ri.b * Hq + (int64_t)ri.g * n_rep) * Sq + ri.p0) * Sk;
   float* prow[16];
   float lrow[16];
   int posr[16];
-  int drw[16];  // DOC: document of each row
-  const int32_t* drow = DOC ? doc + (int64_t)ri.b * Sk : nullptr;
+  int drw[16];  // DOC: document of each row; KPM: 1 for a guarded row
+  const int32_t* drow = DOC || KPM ? aux + (int64_t)ri.b * Sk : nullptr;
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     const int r = w * 32 + 8 * (i >> 2) + 4 * hh + (i & 3);
@@ -355,7 +401,7 @@ __global__ __launch_bounds__(256, 2) void capture_probs_mfma_kernel(
     prow[i] = off < 0 ? nullptr : pbase + (int64_t)off * Sk;
     lrow[i] = sL[r];
     posr[i] = ri.p0 + (r % bm_pos);
-    drw[i] = DOC ? drow[min(posr[i], Sq - 1)] : 0;
+    drw[i] = DOC ? drow[min(posr[i], Sq - 1)] : KPM ? (int)(posr[i] < fv) : 0;
   }
 
   // K tiles double-buffered: tile t+1 loads while tile t is computed and stored
@@ -377,16 +423,18 @@ __global__ __launch_bounds__(256, 2) void capture_probs_mfma_kernel(
         sv = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qf[ks], bk, sv, 0, 0, 0);
       }
       const int key = t * BN + 32 * nt + c32;
-      const int kd = DOC ? drow[min(key, Sk - 1)] : 0;
+      const int kd = DOC || KPM ? drow[min(key, Sk - 1)] : 0;
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         if (prow[i] == nullptr) continue;
         float p = fast_exp2(sv[i] * scale_log2 - lrow[i]);
+        const bool guarded = KPM && drw[i];
         if (diag) {
           if (key >= Sk) continue;
-          if (causal && key > posr[i]) p = 0.f;
+          if (causal && key > posr[i] && !guarded) p = 0.f;
         }
         if (DOC && kd != drw[i]) p = 0.f;
+        if (KPM && !guarded && kd == 0) p = 0.f;
         __builtin_nontemporal_store(p, prow[i] + key);
       }
     }
@@ -417,7 +465,9 @@ int pick_bm_pos(int n_rep) { return n_rep <= ROWS ? ROWS / n_rep : 0; }
 
 bool fwd_mfma_supported(const FwdArgs& a) {
   if (a.dtype != BF16 || (a.D != 64 && a.D != 128)) return false;
-  if (a.doc && (a.Sk + BN - 1) / BN > DOC_MAX_TILES) return false;
+  // one explicit mask kind at a time, with a tile list that fits
+  if (a.doc && a.kvalid) return false;
+  if ((a.doc || a.kvalid) && (a.Sk + BN - 1) / BN > DOC_MAX_TILES) return false;
   const int n_rep = a.Hq / a.Hkv;
   if (n_rep < 1 || n_rep > ROWS) return false;
   auto al16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
@@ -441,11 +491,11 @@ int launch_kv_prep(const FwdArgs& a, void* krot_, void* vn_, int Skp, int2* rang
   if (a.D == 128)
     KF_LAUNCH("kv_prep", kv_prep_kernel<128>, grid, dim3(256), 0, a.stream, (const bf16*)a.k,
                        (const bf16*)a.v, a.cos, a.sin, krot, vn, a.Sk, Skp, a.Hkv, a.ksb, a.kss,
-                       a.ksh, a.vsb, a.vss, a.vsh, a.k_rotated, a.doc, ranges);
+                       a.ksh, a.vsb, a.vss, a.vsh, a.k_rotated, a.doc, a.kvalid, ranges);
   else
     KF_LAUNCH("kv_prep", kv_prep_kernel<64>, grid, dim3(256), 0, a.stream, (const bf16*)a.k,
                        (const bf16*)a.v, a.cos, a.sin, krot, vn, a.Sk, Skp, a.Hkv, a.ksb, a.kss,
-                       a.ksh, a.vsb, a.vss, a.vsh, a.k_rotated, a.doc, ranges);
+                       a.ksh, a.vsb, a.vss, a.vsh, a.k_rotated, a.doc, a.kvalid, ranges);
   KF_CHECK_LAUNCH();
   return KF_OK;
 }
@@ -465,20 +515,48 @@ FwdWs carve_fwd(const FwdArgs& a, void* workspace, int Skp) {
   return w;
 }
 
-template <int D, bool DOC>
+int mask_mode(const FwdArgs& a) { return a.doc ? MASK_DOC : a.kvalid ? MASK_KPM : MASK_NONE; }
+
+template <int D, int MODE>
 void launch_fwd_kernel(const FwdArgs& a, const FwdWs& w, int Skp, int n_rep, int bm_pos, int nqb,
                        unsigned nblk) {
-  KF_LAUNCH("fwd_mfma", (fwd_mfma_kernel<D, DOC>), dim3(nblk), dim3(256), 0, a.stream,
+  KF_LAUNCH("fwd_mfma", (fwd_mfma_kernel<D, MODE>), dim3(nblk), dim3(256), 0, a.stream,
             (const bf16*)a.q, a.cos, a.sin, w.krot, w.vn, (bf16*)a.out, a.lse, a.Sq, a.Sk, Skp,
-            a.Hq, a.Hkv, n_rep, bm_pos, nqb, a.scale * kLog2e, a.causal, a.doc, w.ranges);
+            a.Hq, a.Hkv, n_rep, bm_pos, nqb, a.scale * kLog2e, a.causal,
+            a.doc ? a.doc : a.kvalid, w.ranges);
 }
 
-template <int D, bool DOC>
+template <int D>
+void launch_fwd_mode(const FwdArgs& a, const FwdWs& w, int Skp, int n_rep, int bm_pos, int nqb,
+                     unsigned nblk) {
+  switch (mask_mode(a)) {
+    case MASK_DOC: launch_fwd_kernel<D, MASK_DOC>(a, w, Skp, n_rep, bm_pos, nqb, nblk); break;
+    case MASK_KPM: launch_fwd_kernel<D, MASK_KPM>(a, w, Skp, n_rep, bm_pos, nqb, nblk); break;
+    default: launch_fwd_kernel<D, MASK_NONE>(a, w, Skp, n_rep, bm_pos, nqb, nblk);
+  }
+}
+
+template <int D, int MODE>
 void launch_capture_kernel(const FwdArgs& a, const FwdWs& w, const float* lse, float* probs,
                            int Skp, int n_rep, int bm_pos, int nqb, unsigned nblk) {
-  KF_LAUNCH("capture_probs_mfma", (capture_probs_mfma_kernel<D, DOC>), dim3(nblk), dim3(256), 0,
+  KF_LAUNCH("capture_probs_mfma", (capture_probs_mfma_kernel<D, MODE>), dim3(nblk), dim3(256), 0,
             a.stream, (const bf16*)a.q, a.cos, a.sin, w.krot, lse, probs, a.Sq, a.Sk, Skp, a.Hq,
-            a.Hkv, n_rep, bm_pos, nqb, a.scale * kLog2e, a.causal, a.doc);
+            a.Hkv, n_rep, bm_pos, nqb, a.scale * kLog2e, a.causal, a.doc ? a.doc : a.kvalid,
+            w.ranges);
+}
+
+template <int D>
+void launch_capture_mode(const FwdArgs& a, const FwdWs& w, const float* lse, float* probs,
+                         int Skp, int n_rep, int bm_pos, int nqb, unsigned nblk) {
+  switch (mask_mode(a)) {
+    case MASK_DOC:
+      launch_capture_kernel<D, MASK_DOC>(a, w, lse, probs, Skp, n_rep, bm_pos, nqb, nblk);
+      break;
+    case MASK_KPM:
+      launch_capture_kernel<D, MASK_KPM>(a, w, lse, probs, Skp, n_rep, bm_pos, nqb, nblk);
+      break;
+    default: launch_capture_kernel<D, MASK_NONE>(a, w, lse, probs, Skp, n_rep, bm_pos, nqb, nblk);
+  }
 }
 
 }  // namespace
@@ -493,13 +571,8 @@ int fwd_mfma(const FwdArgs& a, void* workspace) {
   const int nqb = (a.Sq + bm_pos - 1) / bm_pos;
   const int64_t nblk = (int64_t)nqb * a.B * a.Hkv;
   KF_CHECK_ARG(nblk < (1LL << 31), "grid too large");
-  if (a.D == 128) {
-    if (a.doc) launch_fwd_kernel<128, true>(a, w, Skp, n_rep, bm_pos, nqb, (unsigned)nblk);
-    else launch_fwd_kernel<128, false>(a, w, Skp, n_rep, bm_pos, nqb, (unsigned)nblk);
-  } else {
-    if (a.doc) launch_fwd_kernel<64, true>(a, w, Skp, n_rep, bm_pos, nqb, (unsigned)nblk);
-    else launch_fwd_kernel<64, false>(a, w, Skp, n_rep, bm_pos, nqb, (unsigned)nblk);
-  }
+  if (a.D == 128) launch_fwd_mode<128>(a, w, Skp, n_rep, bm_pos, nqb, (unsigned)nblk);
+  else launch_fwd_mode<64>(a, w, Skp, n_rep, bm_pos, nqb, (unsigned)nblk);
   KF_CHECK_LAUNCH();
   return KF_OK;
 }
@@ -512,13 +585,8 @@ int capture_probs_mfma(const FwdArgs& a, const float* lse, float* probs, void* w
   const int bm_pos = pick_bm_pos(n_rep);
   const int nqb = (a.Sq + bm_pos - 1) / bm_pos;
   const unsigned nblk = (unsigned)((int64_t)nqb * a.B * a.Hkv);
-  if (a.D == 128) {
-    if (a.doc) launch_capture_kernel<128, true>(a, w, lse, probs, Skp, n_rep, bm_pos, nqb, nblk);
-    else launch_capture_kernel<128, false>(a, w, lse, probs, Skp, n_rep, bm_pos, nqb, nblk);
-  } else {
-    if (a.doc) launch_capture_kernel<64, true>(a, w, lse, probs, Skp, n_rep, bm_pos, nqb, nblk);
-    else launch_capture_kernel<64, false>(a, w, lse, probs, Skp, n_rep, bm_pos, nqb, nblk);
-  }
+  if (a.D == 128) launch_capture_mode<128>(a, w, lse, probs, Skp, n_rep, bm_pos, nqb, nblk);
+  else launch_capture_mode<64>(a, w, lse, probs, Skp, n_rep, bm_pos, nqb, nblk);
   KF_CHECK_LAUNCH();
   return KF_OK;
 }

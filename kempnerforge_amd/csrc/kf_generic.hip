@@ -76,6 +76,30 @@ __device__ __forceinline__ void store_row_rope_bwd(float* __restrict__ lds_row, 
   }
 }
 
+// Explicit masks (doc ids, key validity; each may be null) for query i, key j
+// of the batch row whose ids start at roff; di = doc[i].
+__device__ __forceinline__ bool sees(const int32_t* __restrict__ doc,
+                                     const int32_t* __restrict__ kv, int64_t roff, int i, int j,
+                                     int causal, int di) {
+  return (!causal || j <= i) && (!doc || doc[roff + j] == di) && (!kv || kv[roff + j] != 0);
+}
+
+// Whether query i sees any key at all (wavefront-uniform).  Only a key
+// validity mask can leave a row empty; such a row attends every key instead
+// (the reference's NaN guard, mask | ~mask.any(-1)).
+__device__ __forceinline__ bool sees_any(const int32_t* __restrict__ doc,
+                                         const int32_t* __restrict__ kv, int64_t roff, int i,
+                                         int Sk, int causal, int di, int lane) {
+  if (!kv) return true;
+  const int end = causal ? min(Sk, i + 1) : Sk;
+  for (int j0 = 0; j0 < end; j0 += 64) {
+    const int j = j0 + lane;
+    if (__builtin_amdgcn_ballot_w64(j < end && sees(doc, kv, roff, i, j, causal, di)) != 0)
+      return true;
+  }
+  return false;
+}
+
 }  // namespace
 
 // ------------------------------------------------------------------ forward
@@ -86,7 +110,7 @@ __global__ __launch_bounds__(256) void fwd_generic_kernel(
     const float* __restrict__ cos, const float* __restrict__ sin, T* __restrict__ out,
     float* __restrict__ lse, int B, int Sq, int Sk, int Hq, int Hkv, int D, int64_t ksb,
     int64_t kss, int64_t ksh, int64_t vsb, int64_t vss, int64_t vsh, int k_rotated, int causal,
-    const int32_t* __restrict__ doc, float scale) {
+    const int32_t* __restrict__ doc, const int32_t* __restrict__ kv, float scale) {
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= (int64_t)B * Hq * Sq) return;
@@ -100,10 +124,12 @@ __global__ __launch_bounds__(256) void fwd_generic_kernel(
 
   float acc[kMaxPer] = {0.f, 0.f, 0.f, 0.f};
   float m = -INFINITY, l = 0.f;
-  const int kend = causal ? min(Sk, i + 1) : Sk;
-  const int di = doc ? doc[(int64_t)b * Sq + i] : 0;
+  const int64_t roff = (int64_t)b * Sk;
+  const int di = doc ? doc[roff + i] : 0;
+  const bool guard = !sees_any(doc, kv, roff, i, Sk, causal, di, lane);
+  const int kend = causal && !guard ? min(Sk, i + 1) : Sk;
   for (int j = 0; j < kend; ++j) {
-    if (doc && doc[(int64_t)b * Sk + j] != di) continue;  // another document
+    if (!guard && !sees(doc, kv, roff, i, j, causal, di)) continue;  // masked key
     float kr[kMaxPer], vv[kMaxPer];
     load_row<T>(k + b * ksb + j * kss + g * ksh, cos, sin, j, D, !k_rotated, lane, kr);
     load_row<T>(v + b * vsb + j * vss + g * vsh, cos, sin, 0, D, false, lane, vv);
@@ -128,11 +154,16 @@ __global__ __launch_bounds__(256) void fwd_generic_kernel(
 
 // ------------------------------------------------------------------ backward
 // delta[b,h,i] = sum_d dO[b,i,h,d] * O[b,i,h,d]
+// With explicit masks it also writes guard[b, i] (1: row i sees no key and
+// attends every key), once per (b, i).
 template <typename T>
 __global__ __launch_bounds__(256) void bwd_delta_kernel(const T* __restrict__ o,
                                                         const T* __restrict__ dout,
-                                                        float* __restrict__ delta, int B, int S,
-                                                        int Hq, int D) {
+                                                        float* __restrict__ delta,
+                                                        int32_t* __restrict__ guard, int B, int S,
+                                                        int Hq, int D, int causal,
+                                                        const int32_t* __restrict__ doc,
+                                                        const int32_t* __restrict__ kv) {
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= (int64_t)B * S * Hq) return;  // row enumerates (b, i, h) in BSHD order
@@ -140,11 +171,15 @@ __global__ __launch_bounds__(256) void bwd_delta_kernel(const T* __restrict__ o,
   float s = 0.f;
   for (int d = lane; d < D; d += 64) s += to_f32(o[base + d]) * to_f32(dout[base + d]);
   s = wave_sum(s);
-  if (lane == 0) {
-    const int h = (int)(row % Hq);
-    const int i = (int)((row / Hq) % S);
-    const int b = (int)(row / ((int64_t)Hq * S));
-    delta[((int64_t)b * Hq + h) * S + i] = s;
+  const int h = (int)(row % Hq);
+  const int i = (int)((row / Hq) % S);
+  const int b = (int)(row / ((int64_t)Hq * S));
+  if (lane == 0) delta[((int64_t)b * Hq + h) * S + i] = s;
+  if (h == 0) {
+    const int64_t roff = (int64_t)b * S;
+    const int di = doc ? doc[roff + i] : 0;
+    const bool g = !sees_any(doc, kv, roff, i, S, causal, di, lane);
+    if (lane == 0) guard[roff + i] = g;
   }
 }
 
@@ -154,7 +189,8 @@ __global__ __launch_bounds__(256) void bwd_dq_generic_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
     const float* __restrict__ cos, const float* __restrict__ sin, const T* __restrict__ dout,
     const float* __restrict__ lse, const float* __restrict__ delta, T* __restrict__ dq, int B,
-    int S, int Hq, int Hkv, int D, int causal, const int32_t* __restrict__ doc, float scale) {
+    int S, int Hq, int Hkv, int D, int causal, const int32_t* __restrict__ doc,
+    const int32_t* __restrict__ kv, const int32_t* __restrict__ guard, float scale) {
   __shared__ float lds[4][256];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int64_t row = (int64_t)blockIdx.x * 4 + w;
@@ -170,10 +206,12 @@ __global__ __launch_bounds__(256) void bwd_dq_generic_kernel(
   const float L = lse[((int64_t)b * Hq + hq) * S + i];
   const float Di = delta[((int64_t)b * Hq + hq) * S + i];
   float acc[kMaxPer] = {0.f, 0.f, 0.f, 0.f};
-  const int kend = causal ? i + 1 : S;
-  const int di = doc ? doc[(int64_t)b * S + i] : 0;
+  const int64_t roff = (int64_t)b * S;
+  const int di = doc ? doc[roff + i] : 0;
+  const bool grd = guard[roff + i] != 0;
+  const int kend = causal && !grd ? i + 1 : S;
   for (int j = 0; j < kend; ++j) {
-    if (doc && doc[(int64_t)b * S + j] != di) continue;
+    if (!grd && !sees(doc, kv, roff, i, j, causal, di)) continue;
     const int64_t koff = (((int64_t)b * S + j) * Hkv + g) * D;
     float kr[kMaxPer], vv[kMaxPer];
     load_row<T>(k + koff, cos, sin, j, D, true, lane, kr);
@@ -197,7 +235,8 @@ __global__ __launch_bounds__(256) void bwd_dkdv_generic_kernel(
     const float* __restrict__ cos, const float* __restrict__ sin, const T* __restrict__ dout,
     const float* __restrict__ lse, const float* __restrict__ delta, T* __restrict__ dk,
     T* __restrict__ dv, int B, int S, int Hq, int Hkv, int D, int causal,
-    const int32_t* __restrict__ doc, float scale) {
+    const int32_t* __restrict__ doc, const int32_t* __restrict__ kv,
+    const int32_t* __restrict__ guard, float scale) {
   __shared__ float lds[4][256];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int64_t row = (int64_t)blockIdx.x * 4 + w;
@@ -211,11 +250,13 @@ __global__ __launch_bounds__(256) void bwd_dkdv_generic_kernel(
   load_row<T>(k + koff, cos, sin, j, D, true, lane, kr);
   load_row<T>(v + koff, cos, sin, 0, D, false, lane, vv);
   float adk[kMaxPer] = {0.f, 0.f, 0.f, 0.f}, adv[kMaxPer] = {0.f, 0.f, 0.f, 0.f};
-  const int dj = doc ? doc[(int64_t)b * S + j] : 0;
+  const int64_t roff = (int64_t)b * S;
   for (int hl = 0; hl < n_rep; ++hl) {
     const int hq = g * n_rep + hl;
-    for (int i = causal ? j : 0; i < S; ++i) {
-      if (doc && doc[(int64_t)b * S + i] != dj) continue;
+    // a guarded row (with a validity mask) may sit before j
+    for (int i = causal && !kv ? j : 0; i < S; ++i) {
+      const int di = doc ? doc[roff + i] : 0;
+      if (!guard[roff + i] && !sees(doc, kv, roff, i, j, causal, di)) continue;
       const int64_t qoff = (((int64_t)b * S + i) * Hq + hq) * D;
       float qr[kMaxPer], dor[kMaxPer];
       load_row<T>(q + qoff, cos, sin, i, D, true, lane, qr);
@@ -250,7 +291,8 @@ __global__ __launch_bounds__(256) void capture_probs_generic_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const float* __restrict__ cos,
     const float* __restrict__ sin, const float* __restrict__ lse, float* __restrict__ probs,
     int B, int Sq, int Sk, int Hq, int Hkv, int D, int64_t ksb, int64_t kss, int64_t ksh,
-    int k_rotated, int causal, const int32_t* __restrict__ doc, float scale) {
+    int k_rotated, int causal, const int32_t* __restrict__ doc, const int32_t* __restrict__ kv,
+    float scale) {
   __shared__ float lds[4][256];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int64_t row = (int64_t)blockIdx.x * 4 + w;
@@ -272,10 +314,12 @@ __global__ __launch_bounds__(256) void capture_probs_generic_kernel(
   const float L = lse[((int64_t)b * Hq + hq) * Sq + i];
   float* prow = probs + row * Sk;
   const int half = D / 2;
-  const int di = doc ? doc[(int64_t)b * Sq + i] : 0;
+  const int64_t roff = (int64_t)b * Sk;
+  const int di = doc ? doc[roff + i] : 0;
+  const bool guard = !sees_any(doc, kv, roff, i, Sk, causal, di, lane);
   for (int j = lane; j < Sk; j += 64) {
     float p = 0.f;
-    if ((!causal || j <= i) && (!doc || doc[(int64_t)b * Sk + j] == di)) {
+    if (guard || sees(doc, kv, roff, i, j, causal, di)) {
       const T* kr = k + b * ksb + j * kss + g * ksh;
       float s = 0.f;
       for (int d = 0; d < half; ++d) {
@@ -302,27 +346,30 @@ int launch_fwd_generic(const FwdArgs& a) {
   KF_LAUNCH("fwd_generic", (fwd_generic_kernel<T>), grid, dim3(256), 0, a.stream, (const T*)a.q,
                      (const T*)a.k, (const T*)a.v, a.cos, a.sin, (T*)a.out, a.lse, a.B, a.Sq,
                      a.Sk, a.Hq, a.Hkv, a.D, a.ksb, a.kss, a.ksh, a.vsb, a.vss, a.vsh,
-                     a.k_rotated, a.causal, a.doc, a.scale);
+                     a.k_rotated, a.causal, a.doc, a.kvalid, a.scale);
   KF_CHECK_LAUNCH();
   return KF_OK;
 }
 
 template <typename T>
-int launch_bwd_generic(const BwdArgs& a, float* delta) {
+int launch_bwd_generic(const BwdArgs& a, void* workspace) {
+  float* delta = (float*)workspace;
+  int32_t* guard = (int32_t*)(delta + (size_t)a.B * a.Hq * a.S);
   const int64_t qrows = (int64_t)a.B * a.Hq * a.S;
   const int64_t krows = (int64_t)a.B * a.Hkv * a.S;
   KF_LAUNCH("bwd_delta_generic", (bwd_delta_kernel<T>), dim3((unsigned)((qrows + 3) / 4)), dim3(256), 0,
-                     a.stream, (const T*)a.out, (const T*)a.dout, delta, a.B, a.S, a.Hq, a.D);
+                     a.stream, (const T*)a.out, (const T*)a.dout, delta, guard, a.B, a.S, a.Hq,
+                     a.D, a.causal, a.doc, a.kvalid);
   KF_CHECK_LAUNCH();
   KF_LAUNCH("bwd_dq_generic", (bwd_dq_generic_kernel<T>), dim3((unsigned)((qrows + 3) / 4)), dim3(256), 0,
                      a.stream, (const T*)a.q, (const T*)a.k, (const T*)a.v, a.cos, a.sin,
                      (const T*)a.dout, a.lse, delta, (T*)a.dq, a.B, a.S, a.Hq, a.Hkv, a.D,
-                     a.causal, a.doc, a.scale);
+                     a.causal, a.doc, a.kvalid, guard, a.scale);
   KF_CHECK_LAUNCH();
   KF_LAUNCH("bwd_dkdv_generic", (bwd_dkdv_generic_kernel<T>), dim3((unsigned)((krows + 3) / 4)), dim3(256),
                      0, a.stream, (const T*)a.q, (const T*)a.k, (const T*)a.v, a.cos, a.sin,
                      (const T*)a.dout, a.lse, delta, (T*)a.dk, (T*)a.dv, a.B, a.S, a.Hq, a.Hkv,
-                     a.D, a.causal, a.doc, a.scale);
+                     a.D, a.causal, a.doc, a.kvalid, guard, a.scale);
   KF_CHECK_LAUNCH();
   return KF_OK;
 }
@@ -333,7 +380,7 @@ int launch_capture_probs_generic(const FwdArgs& a, const float* lse, float* prob
   KF_LAUNCH("capture_probs_generic", (capture_probs_generic_kernel<T>), dim3((unsigned)((rows + 3) / 4)),
                      dim3(256), 0, a.stream, (const T*)a.q, (const T*)a.k, a.cos, a.sin, lse,
                      probs, a.B, a.Sq, a.Sk, a.Hq, a.Hkv, a.D, a.ksb, a.kss, a.ksh, a.k_rotated,
-                     a.causal, a.doc, a.scale);
+                     a.causal, a.doc, a.kvalid, a.scale);
   KF_CHECK_LAUNCH();
   return KF_OK;
 }
@@ -348,11 +395,15 @@ int fwd_generic(const FwdArgs& a) {
   return KF_ERR_UNSUPPORTED;
 }
 
-int bwd_generic(const BwdArgs& a, float* delta) {
+size_t bwd_generic_workspace(int B, int S, int Hq) {
+  return (size_t)B * Hq * S * sizeof(float) + (size_t)B * S * sizeof(int32_t);
+}
+
+int bwd_generic(const BwdArgs& a, void* workspace) {
   switch (a.dtype) {
-    case F32: return launch_bwd_generic<float>(a, delta);
-    case BF16: return launch_bwd_generic<bf16>(a, delta);
-    case F16: return launch_bwd_generic<_Float16>(a, delta);
+    case F32: return launch_bwd_generic<float>(a, workspace);
+    case BF16: return launch_bwd_generic<bf16>(a, workspace);
+    case F16: return launch_bwd_generic<_Float16>(a, workspace);
   }
   set_error("unsupported dtype %d", a.dtype);
   return KF_ERR_UNSUPPORTED;

@@ -24,6 +24,9 @@ struct FwdArgs {
   int causal;         // 1: top-left causal mask (query i sees keys j <= i)
   const int32_t* doc; // [B, S] document id per position (packed sequences) or null;
                       // query i then also needs doc[i] == doc[j] (requires Sq == Sk)
+  const int32_t* kvalid;  // [B, S] 1 = valid key (key padding mask) or null; query i
+                          // then needs kvalid[j], and a query that sees no key at
+                          // all attends every key (requires Sq == Sk)
   int dtype;
   float scale;        // softmax scale, D^-1/2
   hipStream_t stream;
@@ -39,13 +42,16 @@ struct BwdArgs {
   int B, S, Hq, Hkv, D;
   int causal, dtype;
   const int32_t* doc;     // [B, S] document ids or null (see FwdArgs::doc)
+  const int32_t* kvalid;  // [B, S] key validity or null (see FwdArgs::kvalid)
   float scale;
   hipStream_t stream;
 };
 
 // generic kernels (kf_generic.hip)
 int fwd_generic(const FwdArgs& a);
-int bwd_generic(const BwdArgs& a, float* delta);
+// workspace: delta [B*Hq*S] float32, then one guard flag per (b, position)
+size_t bwd_generic_workspace(int B, int S, int Hq);
+int bwd_generic(const BwdArgs& a, void* workspace);
 int capture_probs_generic(const FwdArgs& a, const float* lse, float* probs);
 
 // bf16 MFMA kernels (kf_fwd.hip, kf_bwd.hip, kf_capture.hip)

@@ -192,6 +192,9 @@ __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane
 // id pattern, not only contiguous segments.
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 
+// explicit-mask kinds of the MFMA kernels (one at a time)
+enum { MASK_NONE = 0, MASK_DOC = 1, MASK_KPM = 2 };
+
 constexpr int DOC_MAX_TILES = 4096;      // capacity of a workgroup's tile list
 constexpr int DOC_MASK_FLAG = 0x8000;    // list entry: tile needs the element test
 
@@ -241,6 +244,45 @@ __device__ __forceinline__ int doc_tile_list(const int32_t* __restrict__ drow, i
                                                 __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0));
     if (vis && n + below < DOC_MAX_TILES)
       list[n + below] = (uint16_t)(t | (whole ? 0 : DOC_MASK_FLAG));
+    n += __builtin_popcountll(m);
+  }
+  return min(n, DOC_MAX_TILES);
+}
+
+// ---- key padding ------------------------------------------------------------
+// With a key-validity mask (1 = attend) a query sees key j when j <= i and
+// key j is valid.  A row that sees no key at all (i before the first valid
+// key) is unmasked entirely instead, as the reference's NaN guard does
+// (mask | ~mask.any(-1)): it attends every key, future and padded ones
+// included.  kv_prep records each 64-key tile's {number of valid keys, first
+// valid position or INT_MAX}; the first valid key of the batch row, and with
+// it the guarded rows (a prefix), follow from those records.
+
+// First valid key position of the row (INT_MAX if none), from the records of
+// tiles [0, ntiles).  Wavefront-uniform.
+__device__ __forceinline__ int kpm_first_valid(const int2* __restrict__ rec, int ntiles, int lane) {
+  for (int base = 0; base < ntiles; base += 64) {
+    const int t = base + lane;
+    const int f = __builtin_amdgcn_readfirstlane(wave_min_i(t < ntiles ? rec[t].y : INT_MAX));
+    if (f != INT_MAX) return f;
+  }
+  return INT_MAX;
+}
+
+// Lists, in ascending order, tiles t in [t0, t1) for which pick(t, rec[t])
+// returns nonzero (2: with DOC_MASK_FLAG).  Same contract as doc_tile_list.
+template <typename Pick>
+__device__ __forceinline__ int kpm_tile_list(const int2* __restrict__ rec, int t0, int t1,
+                                             Pick pick, uint16_t* list, int lane) {
+  int n = 0;
+  for (int base = t0; base < t1; base += 64) {
+    const int t = base + lane;
+    const int sel = t < t1 ? pick(t, rec[t]) : 0;
+    const uint64_t m = __builtin_amdgcn_ballot_w64(sel != 0);
+    const int below = __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                                __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0));
+    if (sel && n + below < DOC_MAX_TILES)
+      list[n + below] = (uint16_t)(t | (sel == 2 ? DOC_MASK_FLAG : 0));
     n += __builtin_popcountll(m);
   }
   return min(n, DOC_MAX_TILES);

@@ -16,18 +16,17 @@ modality.  With that, one ``kf::attn_fwd`` / ``kf::attn_bwd`` over the
 concatenated sequence is the reference's RoPE + ``torch.cat`` +
 ``repeat_interleave`` + SDPA (``:162-186``), forward and backward.
 
-The ``key_padding_mask`` branch (``:188-198``) keeps the reference's PyTorch
-code.
+With ``key_padding_mask`` (``:188-198``: causal AND valid keys, the NaN guard
+unmasking rows that see no key) the same kernels apply the validity test per
+tile instead of materialising the ``(B, 1, S, S)`` mask.
 """
 
 from __future__ import annotations
 
 import torch
 import torch.nn as nn
-import torch.nn.functional as F
 
 from kempnerforge_amd import ops
-from kempnerforge_amd.attention import _apply_rope_torch
 from kempnerforge_amd.norm import RMSNorm
 
 
@@ -116,7 +115,9 @@ class MoTAttention(nn.Module):
         cos = torch.cat(coss, dim=0)
         sin = torch.cat(sins, dim=0)
         if key_padding_mask is not None:
-            out = self._masked(q, k, v, cos, sin, key_padding_mask)
+            # the reference's explicit mask is always causal (is_causal unused)
+            out = ops.attention(q, k, v, cos, sin, causal=True,
+                                key_padding_mask=key_padding_mask)
         else:
             out = ops.attention(q, k, v, cos, sin, causal=is_causal)
         out_streams: dict[str, torch.Tensor] = {}
@@ -126,19 +127,3 @@ class MoTAttention(nn.Module):
             out_streams[m] = self.o_proj[m](o_m)
             offset += t_m
         return out_streams
-
-    def _masked(self, q, k, v, cos, sin, key_padding_mask):
-        """Causal AND valid-key mask with the NaN guard, kept as the reference's
-        PyTorch code (``kempnerforge/model/mot.py:188-198``); BSHD out."""
-        batch, total, _, _ = q.shape
-        q = _apply_rope_torch(q.transpose(1, 2), cos, sin)
-        k = _apply_rope_torch(k.transpose(1, 2), cos, sin)
-        v = v.transpose(1, 2)
-        if self.n_rep > 1:
-            k = k.repeat_interleave(self.n_rep, dim=1)
-            v = v.repeat_interleave(self.n_rep, dim=1)
-        causal = torch.ones(total, total, dtype=torch.bool, device=q.device).tril()
-        mask = causal.unsqueeze(0).unsqueeze(0) & key_padding_mask.view(batch, 1, 1, total)
-        mask = mask | ~mask.any(dim=-1, keepdim=True)
-        out = F.scaled_dot_product_attention(q, k, v, attn_mask=mask)
-        return out.transpose(1, 2)

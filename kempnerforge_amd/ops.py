@@ -64,6 +64,18 @@ def _doc_ids(doc_ids, B: int, S: int, device) -> torch.Tensor | None:
     return doc_ids.to(torch.int32).contiguous()
 
 
+def _key_valid(key_padding_mask, B: int, S: int, device) -> torch.Tensor | None:
+    """``key_padding_mask [B, S]`` (True = attend) as the int32 flags the kernels read."""
+    if key_padding_mask is None:
+        return None
+    if tuple(key_padding_mask.shape) != (B, S):
+        raise ValueError(f"key_padding_mask must be [batch, seq_len] = [{B}, {S}] "
+                         f"(got {tuple(key_padding_mask.shape)})")
+    if key_padding_mask.device != device:
+        raise RuntimeError("key_padding_mask must be on the same device as q")
+    return key_padding_mask.to(torch.int32).contiguous()
+
+
 def _rope_table(t: torch.Tensor, rows: int, half: int, name: str) -> torch.Tensor:
     if t.dtype != torch.float32:
         t = t.float()
@@ -75,14 +87,15 @@ def _rope_table(t: torch.Tensor, rows: int, half: int, name: str) -> torch.Tenso
 
 # --------------------------------------------------------------------------- raw calls
 def fwd_raw(q, k, v, cos, sin, *, causal: bool, k_rotated: bool, k_layout: str = "bshd",
-            doc_ids=None):
+            doc_ids=None, key_padding_mask=None):
     """out, lse = attention(q, k, v) with RoPE fused (``kf_attn_fwd``).
 
     q ``[B,Sq,Hq,D]``; k/v ``[B,Sk,Hkv,D]`` (``k_layout="bshd"``) or
     ``[B,Hkv,Sk,D]`` views into a KV cache (``k_layout="bhsd"``, keys already
     rotated).  ``doc_ids [B,S]`` restricts each query to keys of its own
-    document (packed sequences).  Returns out ``[B,Sq,Hq,D]`` and lse
-    ``[B,Hq,Sq]`` float32.
+    document (packed sequences), ``key_padding_mask [B,S]`` (True = attend) to
+    valid keys, a row left with no key attending every key.  Returns out
+    ``[B,Sq,Hq,D]`` and lse ``[B,Hq,Sq]`` float32.
     """
     _require_gpu(q, k, v)
     lib = _lib.load()
@@ -103,6 +116,7 @@ def fwd_raw(q, k, v, cos, sin, *, causal: bool, k_rotated: bool, k_layout: str =
     cos = _rope_table(cos, Sq, D // 2, "rope_cos")
     sin = _rope_table(sin, Sq, D // 2, "rope_sin")
     doc = _doc_ids(doc_ids, B, Sq, q.device)
+    kv = _key_valid(key_padding_mask, B, Sq, q.device)
     dt = _dtype_code(q)
     out = torch.empty_like(q)
     lse = torch.empty(B, Hq, Sq, dtype=torch.float32, device=q.device)
@@ -112,12 +126,14 @@ def fwd_raw(q, k, v, cos, sin, *, causal: bool, k_rotated: bool, k_layout: str =
     ws = _workspace(nbytes.value, q.device)
     _lib.check(lib.kf_attn_fwd(_ptr(q), _ptr(k), _ptr(v), _ptr(cos), _ptr(sin), _ptr(out),
                                _ptr(lse), _ptr(ws), ws.numel(), B, Sq, Sk, Hq, Hkv, D, *kstr,
-                               *vstr, int(k_rotated), int(causal), _ptr(doc), dt, _stream(q)),
+                               *vstr, int(k_rotated), int(causal), _ptr(doc), _ptr(kv), dt,
+                               _stream(q)),
                "kf_attn_fwd")
     return out, lse
 
 
-def bwd_raw(q, k, v, cos, sin, out, lse, dout, *, causal: bool, doc_ids=None):
+def bwd_raw(q, k, v, cos, sin, out, lse, dout, *, causal: bool, doc_ids=None,
+            key_padding_mask=None):
     """dq, dk, dv for :func:`fwd_raw` with un-rotated BSHD k (``kf_attn_bwd``)."""
     _require_gpu(q, k, v, out, lse, dout)
     lib = _lib.load()
@@ -128,6 +144,7 @@ def bwd_raw(q, k, v, cos, sin, out, lse, dout, *, causal: bool, doc_ids=None):
     cos = _rope_table(cos, S, D // 2, "rope_cos")
     sin = _rope_table(sin, S, D // 2, "rope_sin")
     doc = _doc_ids(doc_ids, B, S, q.device)
+    kv = _key_valid(key_padding_mask, B, S, q.device)
     dt = _dtype_code(q)
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
     nbytes = _lib.size_out()
@@ -136,8 +153,8 @@ def bwd_raw(q, k, v, cos, sin, out, lse, dout, *, causal: bool, doc_ids=None):
     ws = _workspace(nbytes.value, q.device)
     _lib.check(lib.kf_attn_bwd(_ptr(q), _ptr(k), _ptr(v), _ptr(cos), _ptr(sin), _ptr(out),
                                _ptr(lse), _ptr(dout), _ptr(dq), _ptr(dk), _ptr(dv), _ptr(ws),
-                               ws.numel(), B, S, Hq, Hkv, D, int(causal), _ptr(doc), dt,
-                               _stream(q)),
+                               ws.numel(), B, S, Hq, Hkv, D, int(causal), _ptr(doc), _ptr(kv),
+                               dt, _stream(q)),
                "kf_attn_bwd")
     return dq, dk, dv
 
@@ -188,7 +205,7 @@ def cache_append_raw(k_new, v_new, cos, sin, k_cache, v_cache, start: int) -> No
 
 
 def capture_raw(q, k, v, cos, sin, *, causal: bool, k_rotated: bool, k_layout: str = "bshd",
-                doc_ids=None):
+                doc_ids=None, key_padding_mask=None):
     """out, probs, lse with probs the float32 softmax matrix ``[B,Hq,Sq,Sk]``
     (``kf_attn_capture``)."""
     _require_gpu(q, k, v)
@@ -208,6 +225,7 @@ def capture_raw(q, k, v, cos, sin, *, causal: bool, k_rotated: bool, k_layout: s
     cos = _rope_table(cos, Sq, D // 2, "rope_cos")
     sin = _rope_table(sin, Sq, D // 2, "rope_sin")
     doc = _doc_ids(doc_ids, B, Sq, q.device)
+    kv = _key_valid(key_padding_mask, B, Sq, q.device)
     dt = _dtype_code(q)
     out = torch.empty_like(q)
     lse = torch.empty(B, Hq, Sq, dtype=torch.float32, device=q.device)
@@ -218,8 +236,8 @@ def capture_raw(q, k, v, cos, sin, *, causal: bool, k_rotated: bool, k_layout: s
     ws = _workspace(nbytes.value, q.device)
     _lib.check(lib.kf_attn_capture(_ptr(q), _ptr(k), _ptr(v), _ptr(cos), _ptr(sin), _ptr(probs),
                                    _ptr(out), _ptr(lse), _ptr(ws), ws.numel(), B, Sq, Sk, Hq, Hkv,
-                                   D, *kstr, *vstr, int(k_rotated), int(causal), _ptr(doc), dt,
-                                   _stream(q)),
+                                   D, *kstr, *vstr, int(k_rotated), int(causal), _ptr(doc),
+                                   _ptr(kv), dt, _stream(q)),
                "kf_attn_capture")
     return out, probs, lse
 
@@ -227,13 +245,15 @@ def capture_raw(q, k, v, cos, sin, *, causal: bool, k_rotated: bool, k_layout: s
 # --------------------------------------------------------------------------- custom ops
 @torch.library.custom_op("kf::attn_fwd", mutates_args=(), device_types="cuda")
 def attn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos: torch.Tensor,
-             sin: torch.Tensor, causal: bool,
-             doc_ids: Optional[torch.Tensor] = None) -> tuple[torch.Tensor, torch.Tensor]:
-    return fwd_raw(q, k, v, cos, sin, causal=causal, k_rotated=False, doc_ids=doc_ids)
+             sin: torch.Tensor, causal: bool, doc_ids: Optional[torch.Tensor] = None,
+             key_padding_mask: Optional[torch.Tensor] = None
+             ) -> tuple[torch.Tensor, torch.Tensor]:
+    return fwd_raw(q, k, v, cos, sin, causal=causal, k_rotated=False, doc_ids=doc_ids,
+                   key_padding_mask=key_padding_mask)
 
 
 @attn_fwd.register_fake
-def _(q, k, v, cos, sin, causal, doc_ids=None):
+def _(q, k, v, cos, sin, causal, doc_ids=None, key_padding_mask=None):
     B, S, Hq, _ = q.shape
     return torch.empty_like(q), q.new_empty(B, Hq, S, dtype=torch.float32)
 
@@ -241,33 +261,37 @@ def _(q, k, v, cos, sin, causal, doc_ids=None):
 @torch.library.custom_op("kf::attn_bwd", mutates_args=(), device_types="cuda")
 def attn_bwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos: torch.Tensor,
              sin: torch.Tensor, out: torch.Tensor, lse: torch.Tensor, dout: torch.Tensor,
-             causal: bool, doc_ids: Optional[torch.Tensor] = None
+             causal: bool, doc_ids: Optional[torch.Tensor] = None,
+             key_padding_mask: Optional[torch.Tensor] = None
              ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
-    return bwd_raw(q, k, v, cos, sin, out, lse, dout, causal=causal, doc_ids=doc_ids)
+    return bwd_raw(q, k, v, cos, sin, out, lse, dout, causal=causal, doc_ids=doc_ids,
+                   key_padding_mask=key_padding_mask)
 
 
 @attn_bwd.register_fake
-def _(q, k, v, cos, sin, out, lse, dout, causal, doc_ids=None):
+def _(q, k, v, cos, sin, out, lse, dout, causal, doc_ids=None, key_padding_mask=None):
     return torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
 
 
 def _setup_context(ctx, inputs, output):
-    q, k, v, cos, sin, causal, doc_ids = inputs
+    q, k, v, cos, sin, causal, doc_ids, key_padding_mask = inputs
     out, lse = output
-    ctx.save_for_backward(q, k, v, cos, sin, out, lse, doc_ids)
+    ctx.save_for_backward(q, k, v, cos, sin, out, lse, doc_ids, key_padding_mask)
     ctx.causal = causal
 
 
 def _backward(ctx, dout, dlse):
-    q, k, v, cos, sin, out, lse, doc_ids = ctx.saved_tensors
-    dq, dk, dv = attn_bwd(q, k, v, cos, sin, out, lse, dout.contiguous(), ctx.causal, doc_ids)
-    return dq, dk, dv, None, None, None, None
+    q, k, v, cos, sin, out, lse, doc_ids, key_padding_mask = ctx.saved_tensors
+    dq, dk, dv = attn_bwd(q, k, v, cos, sin, out, lse, dout.contiguous(), ctx.causal, doc_ids,
+                          key_padding_mask)
+    return dq, dk, dv, None, None, None, None, None
 
 
 attn_fwd.register_autograd(_backward, setup_context=_setup_context)
 
 
-def attention(q, k, v, rope_cos, rope_sin, *, causal: bool = True, doc_ids=None) -> torch.Tensor:
+def attention(q, k, v, rope_cos, rope_sin, *, causal: bool = True, doc_ids=None,
+              key_padding_mask=None) -> torch.Tensor:
     """Differentiable RoPE + GQA + (causal) attention on BSHD tensors.
 
     Equivalent to the reference's ``apply_rope`` on q and k
@@ -275,7 +299,9 @@ def attention(q, k, v, rope_cos, rope_sin, *, causal: bool = True, doc_ids=None)
     (``:173-175``) and ``F.scaled_dot_product_attention(..., is_causal=causal)``
     (``:231``), returning BSHD instead of BHSD.  With ``doc_ids [B,S]`` it is the
     reference's packed-sequence branch instead (``:204-227``): causal and
-    same-document, without materialising the ``[B,1,S,S]`` mask.
+    same-document, without materialising the ``[B,1,S,S]`` mask; with
+    ``key_padding_mask [B,S]`` (True = attend) its padded-key branch
+    (``:214-225``, ``kempnerforge/model/mot.py:188-198``), NaN guard included.
     """
-    out, _ = attn_fwd(q, k, v, rope_cos, rope_sin, causal, doc_ids)
+    out, _ = attn_fwd(q, k, v, rope_cos, rope_sin, causal, doc_ids, key_padding_mask)
     return out

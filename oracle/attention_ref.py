@@ -109,18 +109,34 @@ def _doc_mask(doc_ids) -> torch.Tensor:
     return (d.unsqueeze(2) != d.unsqueeze(1)).unsqueeze(1)
 
 
-def _scores(qf, kf, causal, doc_ids=None):
+def _scores(qf, kf, causal, doc_ids=None, key_padding_mask=None):
+    """Scaled scores with the masked entries at -inf.
+
+    With ``doc_ids`` or ``key_padding_mask`` this is the reference's
+    explicit-mask branch (``kempnerforge/model/attention.py:209-225``;
+    ``kempnerforge/model/mot.py:188-196``): allowed = causal AND same document
+    AND ``key_padding_mask[b, j]``, then the NaN guard ``allowed | ~allowed.any(
+    -1)``, which unmasks a row that allows no key at all."""
     d = qf.shape[-1]
     s = torch.matmul(qf, kf.transpose(-2, -1)) * (d ** -0.5)
+    if doc_ids is None and key_padding_mask is None:
+        if causal:
+            s = s.masked_fill(_causal_mask(s.shape[-2], s.shape[-1]), float("-inf"))
+        return s
+    masked = torch.zeros(1, 1, s.shape[-2], s.shape[-1], dtype=torch.bool)
     if causal:
-        s = s.masked_fill(_causal_mask(s.shape[-2], s.shape[-1]), float("-inf"))
+        masked = masked | _causal_mask(s.shape[-2], s.shape[-1])
     if doc_ids is not None:
-        s = s.masked_fill(_doc_mask(doc_ids), float("-inf"))
-    return s
+        masked = masked | _doc_mask(doc_ids)
+    if key_padding_mask is not None:
+        kpm = torch.as_tensor(key_padding_mask).bool()
+        masked = masked | ~kpm.view(kpm.shape[0], 1, 1, -1)
+    masked = masked & ~masked.all(dim=-1, keepdim=True)  # NaN guard
+    return s.masked_fill(masked, float("-inf"))
 
 
 def attention_fwd(q, k, v, cos, sin, *, causal: bool = True, compute_dtype=torch.float64,
-                  doc_ids=None):
+                  doc_ids=None, key_padding_mask=None):
     """Causal GQA attention with fused RoPE; returns ``(out, lse)``.
 
     q ``[B,Sq,Hq,D]``, k/v ``[B,Sk,Hkv,D]`` (pre-RoPE), cos/sin ``[S, D/2]``
@@ -132,14 +148,16 @@ def attention_fwd(q, k, v, cos, sin, *, causal: bool = True, compute_dtype=torch
     expansion) and ``:228-231`` (``F.scaled_dot_product_attention`` with default
     scale ``D^-1/2`` and ``is_causal``).  The reference returns no LSE; it is the
     closed form ``log sum_j exp(s_ij)``.  With ``doc_ids [B,S]`` (packed
-    sequences, ``:204-227``) a query also sees only keys of its own document.
+    sequences, ``:204-227``) a query also sees only keys of its own document;
+    with ``key_padding_mask [B,S]`` (True = attend) only valid keys, and a row
+    left with none attends every key (the NaN guard).
     """
     qr, kr, vt = _rotated_bhsd(q, k, v, cos, sin)
     n_rep = qr.shape[1] // kr.shape[1]
     qf = qr.to(compute_dtype)
     kf = gqa_expand(kr, n_rep).to(compute_dtype)
     vf = gqa_expand(vt, n_rep).to(compute_dtype)
-    s = _scores(qf, kf, causal, doc_ids)
+    s = _scores(qf, kf, causal, doc_ids, key_padding_mask)
     lse = torch.logsumexp(s, dim=-1)
     p = torch.exp(s - lse.unsqueeze(-1))
     out = torch.matmul(p, vf)
@@ -196,7 +214,7 @@ def attention_fwd_rotated(q, k_cache, v_cache, cos, sin, *, causal: bool = True,
 
 
 def attention_bwd(q, k, v, cos, sin, dout, *, causal: bool = True, compute_dtype=torch.float64,
-                  doc_ids=None):
+                  doc_ids=None, key_padding_mask=None):
     """Gradients ``(dq, dk, dv)`` of :func:`attention_fwd`'s output, pre-RoPE, BSHD.
 
     The reference gets these from autograd (``scripts/train.py:850``) through
@@ -213,7 +231,7 @@ def attention_bwd(q, k, v, cos, sin, dout, *, causal: bool = True, compute_dtype
     kf = kr.to(compute_dtype).detach().requires_grad_(True)
     vf = vt.to(compute_dtype).detach().requires_grad_(True)
     with torch.enable_grad():
-        s = _scores(qf, gqa_expand(kf, n_rep), causal, doc_ids)
+        s = _scores(qf, gqa_expand(kf, n_rep), causal, doc_ids, key_padding_mask)
         p = torch.softmax(s, dim=-1)
         out = torch.matmul(p, gqa_expand(vf, n_rep))
         out.backward(dout.transpose(1, 2).to(compute_dtype))
@@ -264,7 +282,7 @@ def decode_step(q_new, k_new, v_new, k_cache, v_cache, lens, cos_table, sin_tabl
 
 
 def capture(q, k, v, cos, sin, *, causal: bool = True, compute_dtype=torch.float64,
-            doc_ids=None):
+            doc_ids=None, key_padding_mask=None):
     """Materialised attention probabilities; returns ``(out BSHD, P [B,Hq,Sq,Sk])``.
 
     Follows ``kempnerforge/model/attention.py:238-280``: ``QK^T * D^-1/2``
@@ -277,7 +295,7 @@ def capture(q, k, v, cos, sin, *, causal: bool = True, compute_dtype=torch.float
     qf = qr.to(compute_dtype)
     kf = gqa_expand(kr, n_rep).to(compute_dtype)
     vf = gqa_expand(vt, n_rep).to(compute_dtype)
-    p = torch.softmax(_scores(qf, kf, causal, doc_ids), dim=-1)
+    p = torch.softmax(_scores(qf, kf, causal, doc_ids, key_padding_mask), dim=-1)
     out = torch.matmul(p, vf)
     return out.transpose(1, 2).contiguous(), p
 

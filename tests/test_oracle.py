@@ -361,6 +361,101 @@ class TestPackedDocuments:
         assert torch.all(P[..., 5:, :5] == 0) and torch.all(P[..., :5, 5:] == 0)
 
 
+def _sdpa_masked_reference(q, k, v, cos, sin, doc_ids=None, key_padding_mask=None):
+    """The reference's explicit-mask branch literally, with PyTorch's library
+    SDPA in float64 (kempnerforge/model/attention.py:209-226): causal AND
+    same-document AND valid key, NaN guard, attn_mask=."""
+    qr = ref.apply_rope(q.transpose(1, 2), cos, sin).double()
+    kr = ref.apply_rope(k.transpose(1, 2), cos, sin).double()
+    vt = v.transpose(1, 2).double()
+    n_rep = q.shape[2] // k.shape[2]
+    kr = kr.repeat_interleave(n_rep, dim=1)
+    vt = vt.repeat_interleave(n_rep, dim=1)
+    B, S = q.shape[0], q.shape[1]
+    mask = torch.ones(S, S, dtype=torch.bool).tril().unsqueeze(0).unsqueeze(0)
+    if doc_ids is not None:
+        mask = mask & (doc_ids.unsqueeze(2) == doc_ids.unsqueeze(1)).unsqueeze(1)
+    if key_padding_mask is not None:
+        mask = mask & key_padding_mask.view(B, 1, 1, S)
+    mask = mask | ~mask.any(dim=-1, keepdim=True)
+    return F.scaled_dot_product_attention(qr, kr, vt, attn_mask=mask).transpose(1, 2)
+
+
+def _kpm(B, S, padded):
+    """[B, S] bool key_padding_mask (True = attend) with the listed positions of
+    each row padded."""
+    m = torch.ones(B, S, dtype=torch.bool)
+    for b, pos in enumerate(padded):
+        m[b, list(pos)] = False
+    return m
+
+
+class TestKeyPadding:
+    def test_matches_library_sdpa_with_explicit_mask(self):
+        # middle frames padded, leading positions padded (guarded rows), and a
+        # row with no valid key at all
+        q, k, v, cos, sin = _inputs(3, 23, 4, 2, 16, torch.bfloat16, seed=31)
+        kpm = _kpm(3, 23, [range(6, 11), range(0, 5), range(0, 23)])
+        out, _ = ref.attention_fwd(q, k, v, cos, sin, key_padding_mask=kpm)
+        want = _sdpa_masked_reference(q, k, v, cos, sin, key_padding_mask=kpm)
+        assert torch.allclose(out, want, atol=1e-12)
+
+    def test_all_valid_is_plain_causal(self):
+        q, k, v, cos, sin = _inputs(2, 17, 4, 2, 8, torch.float32, seed=32)
+        out_m, lse_m = ref.attention_fwd(q, k, v, cos, sin,
+                                         key_padding_mask=torch.ones(2, 17, dtype=torch.bool))
+        out, lse = ref.attention_fwd(q, k, v, cos, sin)
+        assert torch.equal(out_m, out) and torch.equal(lse_m, lse)
+
+    def test_guarded_rows_attend_every_key(self):
+        # rows before the first valid key see no key: the guard unmasks them
+        # entirely, so they equal non-causal attention over the whole sequence;
+        # the other rows equal attention restricted to valid keys j <= i
+        q, k, v, cos, sin = _inputs(1, 14, 2, 1, 8, torch.float32, seed=33)
+        kpm = _kpm(1, 14, [[0, 1, 2, 3, 9]])
+        out, _ = ref.attention_fwd(q, k, v, cos, sin, key_padding_mask=kpm)
+        full, _ = ref.attention_fwd(q, k, v, cos, sin, causal=False)
+        assert torch.allclose(out[:, :4], full[:, :4], atol=1e-13)
+        keep = [j for j in range(14) if j not in (0, 1, 2, 3, 9)]
+        qr, kr, vt = ref._rotated_bhsd(q, k, v, cos, sin)
+        kr, vt = kr[:, :, keep].double(), vt[:, :, keep].double()
+        for i in range(4, 14):
+            cols = [c for c, j in enumerate(keep) if j <= i]
+            s = (qr[:, :, i:i + 1].double() @ kr[:, :, cols].transpose(-1, -2)) * 8 ** -0.5
+            o = torch.softmax(s, -1) @ vt[:, :, cols]
+            assert torch.allclose(out[:, i], o[:, :, 0], atol=1e-13)
+
+    def test_with_documents(self):
+        q, k, v, cos, sin = _inputs(2, 26, 4, 2, 8, torch.float32, seed=34)
+        doc = _packed_doc_ids(2, [[9, 6, 11], [26]])
+        kpm = _kpm(2, 26, [[9, 10, 11, 20], [0, 1, 2]])
+        out, _ = ref.attention_fwd(q, k, v, cos, sin, doc_ids=doc, key_padding_mask=kpm)
+        want = _sdpa_masked_reference(q, k, v, cos, sin, doc, kpm)
+        assert torch.allclose(out, want, atol=1e-12)
+
+    def test_backward_matches_library_autograd(self):
+        B, S, Hq, Hkv, D = 2, 19, 4, 2, 8
+        q, k, v, cos, sin = _inputs(B, S, Hq, Hkv, D, torch.float64, seed=35)
+        cos, sin = cos.double(), sin.double()
+        kpm = _kpm(B, S, [range(0, 4), [5, 6, 12]])
+        do = torch.randn(B, S, Hq, D, generator=torch.Generator().manual_seed(36),
+                         dtype=torch.float64)
+        qq, kk, vv = (t.clone().requires_grad_(True) for t in (q, k, v))
+        _sdpa_masked_reference(qq, kk, vv, cos, sin, key_padding_mask=kpm).backward(do)
+        dq, dk, dv = ref.attention_bwd(q, k, v, cos, sin, do, key_padding_mask=kpm)
+        assert torch.allclose(dq, qq.grad, atol=1e-10)
+        assert torch.allclose(dk, kk.grad, atol=1e-10)
+        assert torch.allclose(dv, vv.grad, atol=1e-10)
+
+    def test_capture_zeros_padded_keys(self):
+        q, k, v, cos, sin = _inputs(1, 12, 2, 1, 8, torch.float32, seed=37)
+        kpm = _kpm(1, 12, [[0, 1, 7]])
+        _, P = ref.capture(q, k, v, cos, sin, key_padding_mask=kpm)
+        assert torch.allclose(P.sum(-1), torch.ones_like(P.sum(-1)), atol=1e-12)
+        assert torch.all(P[..., 2:, 0:2] == 0) and torch.all(P[..., 2:, 7] == 0)
+        assert torch.all(P[..., :2, :] > 0)  # guarded rows: every key
+
+
 # --------------------------------------------------------------------------- decode
 class TestDecode:
     def _setup(self, lens, Smax=24, B=3, Hq=4, Hkv=2, D=8, dtype=torch.float32):
