@@ -125,7 +125,14 @@ int kf_attn_decode_workspace_size(int B, int Hq, int Hkv, int D, int max_len, in
  *   rope_cos/sin [rope_rows, D/2]: sequence b uses row lens[b] - rope_row_offset
  *   out  [B, 1, Hq, D]
  *   max_len  an upper bound on lens[b] + 1 (<= Smax); sizes the grid
+ *   q_norm_weight, k_norm_weight  [D] float32 per-head RMSNorm weights, or
+ *       both NULL: given, q_new and k_new are normalised first, as the
+ *       reference's q_norm / k_norm do before RoPE (kempnerforge/model/
+ *       attention.py:155-157; norm.py:22-27, eps = norm_eps), inside the
+ *       decode launches instead of separate ones
  * lens is not modified.  Attention covers keys 0..lens[b] with no mask.
+ * lens may differ per sequence (a ragged batch): each sequence attends its
+ * own prefix at its own RoPE position.
  * lens lives on the device, so it cannot be validated before the launch: a
  * sequence whose lens[b] + 1 exceeds max_len, or whose table row falls outside
  * [0, rope_rows), gets NaN outputs and no cache write instead of a fault.
@@ -135,6 +142,7 @@ int kf_attn_decode(const void* q_new, const void* k_new, const void* v_new, void
                    const float* rope_sin, int64_t rope_row_offset, int64_t rope_rows, void* out,
                    void* workspace,
                    size_t workspace_bytes, int B, int Smax, int Hq, int Hkv, int D, int max_len,
+                   const float* q_norm_weight, const float* k_norm_weight, float norm_eps,
                    int dtype, void* stream);
 
 /* Append Snew tokens to a KV cache at positions start .. start+Snew-1.

@@ -48,8 +48,14 @@ class KVCache:
 
     Same storage and API as ``kempnerforge/model/attention.py:29-70``: keys are
     stored after RoPE and before GQA expansion; ``seq_len`` is the batch's fill
-    level.  ``lens`` is the same fill level per sequence as an int32 device
-    tensor, which the decode kernel reads without a host synchronisation.
+    level.  ``lens`` is the fill level per sequence as an int32 device tensor,
+    which the decode kernel reads without a host synchronisation.
+
+    Beyond the reference (whose single ``seq_len`` forces one length for the
+    whole batch): ``set_lengths`` gives each sequence its own fill level (a
+    ragged batch, e.g. right-padded prompts of different lengths), and
+    ``use_rope_tables`` hands over the full RoPE tables so that each sequence
+    decodes at its own position.  ``seq_len`` is then the longest fill level.
     """
 
     def __init__(
@@ -67,6 +73,8 @@ class KVCache:
                              device=device)
         self.seq_len = 0
         self.lens = torch.zeros(batch_size, dtype=torch.int32, device=device)
+        self.rope_tables: tuple[torch.Tensor, torch.Tensor] | None = None
+        self.ragged = False
 
     @property
     def max_seq_len(self) -> int:
@@ -82,6 +90,35 @@ class KVCache:
         self.v[:, :, self.seq_len : end] = v_new
         self._advance(new_len)
         return self.k[:, :, :end], self.v[:, :, :end]
+
+    def set_lengths(self, lengths) -> None:
+        """Per-sequence fill levels (a list of ints, or an int tensor at the
+        cost of one host synchronisation).  Positions at or past a sequence's
+        level are free: its next decode step writes there."""
+        if isinstance(lengths, torch.Tensor):
+            lengths = [int(x) for x in lengths.tolist()]
+        lengths = [int(x) for x in lengths]
+        if len(lengths) != self.lens.shape[0]:
+            raise ValueError(f"need {self.lens.shape[0]} lengths (got {len(lengths)})")
+        if min(lengths) < 0 or max(lengths) > self.max_seq_len:
+            raise ValueError(f"lengths must lie in [0, {self.max_seq_len}]")
+        self.lens.copy_(torch.tensor(lengths, dtype=torch.int32))
+        self.seq_len = max(lengths)
+        self.ragged = len(set(lengths)) > 1
+
+    def use_rope_tables(self, cos: torch.Tensor, sin: torch.Tensor) -> None:
+        """Full ``(positions, head_dim // 2)`` RoPE tables; decode then rotates
+        each sequence at its own position ``lens[b]`` (needed for a ragged cache)."""
+        self.rope_tables = (cos, sin)
+
+    def _decode_tables(self, cos: torch.Tensor, sin: torch.Tensor):
+        """(cos, sin, row offset) for a decode step: the caller's tables start
+        at position ``seq_len``; attached full tables start at 0."""
+        if self.rope_tables is not None:
+            return self.rope_tables[0], self.rope_tables[1], 0
+        if self.ragged:
+            raise ValueError("a ragged KV cache needs the full RoPE tables: call use_rope_tables")
+        return cos, sin, self.seq_len
 
     def _check_room(self, new_len: int) -> None:
         if self.seq_len + new_len > self.max_seq_len:
@@ -160,11 +197,16 @@ class Attention(nn.Module):
         q = self.q_proj(x).view(batch, seq_len, -1, self.head_dim)
         k = self.k_proj(x).view(batch, seq_len, -1, self.head_dim)
         v = self.v_proj(x).view(batch, seq_len, -1, self.head_dim)
-        if self.q_norm is not None:
+        masked = doc_ids is not None or key_padding_mask is not None
+        decode = (kv_cache is not None and seq_len == 1 and not masked
+                  and not self.capture_attention_weights)
+        # decode applies the QK-norm inside its kernels (one eps for both)
+        fuse_norm = (decode and self.q_norm is not None
+                     and self.q_norm.eps == self.k_norm.eps)  # type: ignore[union-attr]
+        if self.q_norm is not None and not fuse_norm:
             q = self.q_norm(q)
             k = self.k_norm(k)  # type: ignore[reportOptionalCall]
 
-        masked = doc_ids is not None or key_padding_mask is not None
         if self.capture_attention_weights:
             if masked and kv_cache is not None:
                 out = self._masked_attention(q, k, v, rope_cos, rope_sin, seq_len, doc_ids,
@@ -184,9 +226,13 @@ class Attention(nn.Module):
             out = ops.attention(q, k, v, rope_cos, rope_sin, causal=True)
         elif seq_len == 1:
             kv_cache._check_room(1)
-            out = ops.decode_raw(q, k, v, kv_cache.k, kv_cache.v, kv_cache.lens, rope_cos,
-                                 rope_sin, rope_row_offset=kv_cache.seq_len,
-                                 max_len=kv_cache.seq_len + 1)
+            cos_t, sin_t, row0 = kv_cache._decode_tables(rope_cos, rope_sin)
+            out = ops.decode_raw(
+                q, k, v, kv_cache.k, kv_cache.v, kv_cache.lens, cos_t, sin_t,
+                rope_row_offset=row0, max_len=kv_cache.seq_len + 1,
+                q_norm_weight=self.q_norm.weight if fuse_norm else None,  # type: ignore[union-attr]
+                k_norm_weight=self.k_norm.weight if fuse_norm else None,  # type: ignore[union-attr]
+                norm_eps=self.q_norm.eps if fuse_norm else 1e-5)  # type: ignore[union-attr]
             kv_cache._advance(1)
         else:
             kc, vc = self._append(k, v, rope_cos, rope_sin, kv_cache)
@@ -199,6 +245,9 @@ class Attention(nn.Module):
     @staticmethod
     def _append(k, v, rope_cos, rope_sin, kv_cache: KVCache):
         new_len = k.shape[1]
+        if kv_cache.ragged:
+            raise ValueError("prefill into a ragged KV cache is not supported; prefill the "
+                             "right-padded batch first, then call set_lengths")
         kv_cache._check_room(new_len)
         start = kv_cache.seq_len
         ops.cache_append_raw(k, v, rope_cos, rope_sin, kv_cache.k, kv_cache.v, start)

@@ -171,12 +171,15 @@ int kf_attn_decode(const void* q_new, const void* k_new, const void* v_new, void
                    const float* rope_sin, int64_t rope_row_offset, int64_t rope_rows, void* out,
                    void* workspace,
                    size_t workspace_bytes, int B, int Smax, int Hq, int Hkv, int D, int max_len,
+                   const float* q_norm_weight, const float* k_norm_weight, float norm_eps,
                    int dtype, void* stream) {
   int rc = check_common(B, 1, max_len, Hq, Hkv, D, dtype);
   if (rc) return rc;
   KF_CHECK_ARG(q_new && k_new && v_new && k_cache && v_cache && lens && rope_cos && rope_sin &&
                    out,
                "null tensor pointer");
+  KF_CHECK_ARG(!q_norm_weight == !k_norm_weight,
+               "QK-norm needs both q_norm_weight and k_norm_weight (or neither)");
   KF_CHECK_ARG(max_len <= Smax, "max_len (%d) exceeds the cache length (%d)", max_len, Smax);
   const size_t need = decode_workspace(B, Hq, D, max_len);
   if (workspace_bytes < need || !workspace) {
@@ -189,6 +192,7 @@ int kf_attn_decode(const void* q_new, const void* k_new, const void* v_new, void
   a.lens = lens; a.cos = rope_cos; a.sin = rope_sin; a.rope_row_offset = rope_row_offset;
   a.rope_rows = rope_rows;
   a.out = out; a.B = B; a.Smax = Smax; a.Hq = Hq; a.Hkv = Hkv; a.D = D; a.max_len = max_len;
+  a.q_norm_w = q_norm_weight; a.k_norm_w = k_norm_weight; a.norm_eps = norm_eps;
   a.dtype = dtype; a.scale = 1.0f / sqrtf((float)D); a.stream = (hipStream_t)stream;
   return decode(a, workspace);
 }

@@ -11,6 +11,9 @@
 //              rounding) and writes it and v_new into the caches (the
 //              reference's KVCache.update) instead of reading that row.
 //  2. merge    one wavefront per (b, hq) rescales and sums the partials.
+// With QK-norm weights the per-head RMSNorm of q_new and k_new (the
+// reference's q_norm / k_norm, applied before RoPE) happens where the rows
+// are loaded, instead of in separate launches.
 // Shapes outside the fast path (dtype other than bf16, D not in {64, 128}, or
 // n_rep > 32) use decode_generic: one wavefront per (b, hq).
 #include "kf_common.h"
@@ -22,6 +25,15 @@ namespace kf {
 namespace {
 
 constexpr int CH = 512;  // keys per split
+
+// RMSNorm of one element given its row's sum of squares, as the reference's
+// RMSNorm computes it (kempnerforge/model/norm.py:22-27): float32
+// x * rsqrt(mean(x^2) + eps), times the weight, rounded to the storage type.
+template <typename T>
+__device__ __forceinline__ float rms_scale(float x, float ss, int D, float eps, float w) {
+  const float r = rsqrtf(ss / (float)D + eps);
+  return round_to<T>((x * r) * w);
+}
 
 // A device-side cache length is usable when the new token's position fits the
 // grid (len + 1 <= max_len <= Smax) and its RoPE row lies inside the table.
@@ -46,7 +58,8 @@ __global__ __launch_bounds__(256) void append_kernel(const T* __restrict__ k_new
                                                      const int32_t* __restrict__ lens, int start,
                                                      int64_t row_offset, int64_t rope_rows,
                                                      int max_len, int B, int Snew, int Hkv,
-                                                     int Smax, int D) {
+                                                     int Smax, int D,
+                                                     const float* __restrict__ knw, float eps) {
   const int half = D / 2;
   const int64_t n = (int64_t)B * Snew * Hkv * half;
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -61,9 +74,18 @@ __global__ __launch_bounds__(256) void append_kernel(const T* __restrict__ k_new
   const int64_t src = (((int64_t)b * Snew + i) * Hkv + g) * D;
   const int64_t dst = (((int64_t)b * Hkv + g) * Smax + pos) * D;
   const int64_t trow = pos - row_offset;
+  float x1 = to_f32(k_new[src + d]), x2 = to_f32(k_new[src + d + half]);
+  if (knw != nullptr) {  // QK-norm of the key row (the whole row's sum of squares)
+    float ss = 0.f;
+    for (int e = 0; e < D; ++e) {
+      const float x = to_f32(k_new[src + e]);
+      ss += x * x;
+    }
+    x1 = rms_scale<T>(x1, ss, D, eps, knw[d]);
+    x2 = rms_scale<T>(x2, ss, D, eps, knw[d + half]);
+  }
   float r1, r2;
-  rope_pair<T>(to_f32(k_new[src + d]), to_f32(k_new[src + d + half]), cos[trow * half + d],
-               sin[trow * half + d], r1, r2);
+  rope_pair<T>(x1, x2, cos[trow * half + d], sin[trow * half + d], r1, r2);
   kc[dst + d] = from_f32<T>(r1);
   kc[dst + d + half] = from_f32<T>(r2);
   vc[dst + d] = v_new[src + d];
@@ -115,14 +137,14 @@ constexpr int DEC_WAVES = 4;
 constexpr int KC = 32;                    // keys per chunk
 constexpr int NCH = CH / (DEC_WAVES * KC);  // chunks per wavefront
 
-template <int D>
+template <int D, bool QKN>
 __global__ __launch_bounds__(256, 2) void decode_split_kernel(
     const bf16* __restrict__ q_new, const bf16* __restrict__ k_new,
     const bf16* __restrict__ v_new, const float* __restrict__ cos, const float* __restrict__ sin,
     int64_t row_offset, int64_t rope_rows, int max_len, bf16* kc, bf16* vc,
     const int32_t* __restrict__ lens, float* __restrict__ opart, float* __restrict__ mpart,
     float* __restrict__ lpart, int Hq, int Hkv, int Smax, int nsplit, int n_rep,
-    float scale_log2) {
+    float scale_log2, const float* __restrict__ qnw, const float* __restrict__ knw, float eps) {
   using namespace mfma;
   constexpr int KS = D / 16, DT = D / 32, KR = D / 8, HALF = D / 2;
   constexpr int WKEYS = NCH * KC;      // keys per wavefront
@@ -158,11 +180,30 @@ __global__ __launch_bounds__(256, 2) void decode_split_kernel(
   if (own_new) {
     const bf16* kn = k_new + ((int64_t)b * Hkv + g) * D;
     const bf16* vn = v_new + ((int64_t)b * Hkv + g) * D;
-    if (lane < HALF / 8) {
-      const int d0 = 8 * lane;
-      float x1[8], x2[8], r1[8], r2[8];
+    // lanes 0 .. HALF/8-1 hold elements d0..d0+7 and d0+HALF..+7 of the key
+    const bool kl = lane < HALF / 8;
+    const int d0 = kl ? 8 * lane : 0;
+    float x1[8], x2[8];
+    if (kl) {
       unpack8(*(const u32x4*)(kn + d0), x1);
       unpack8(*(const u32x4*)(kn + d0 + HALF), x2);
+    }
+    if constexpr (QKN) {
+      float ss = 0.f;
+      if (kl)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) ss += x1[j] * x1[j] + x2[j] * x2[j];
+#pragma unroll
+      for (int o = 1; o < HALF / 8; o <<= 1) ss += __shfl_xor(ss, o, 64);
+      if (kl)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          x1[j] = rms_scale<bf16>(x1[j], ss, D, eps, knw[d0 + j]);
+          x2[j] = rms_scale<bf16>(x2[j], ss, D, eps, knw[d0 + HALF + j]);
+        }
+    }
+    if (kl) {
+      float r1[8], r2[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) rope_pair<bf16>(x1[j], x2[j], cr[d0 + j], sr[d0 + j], r1[j], r2[j]);
       const u32x4 a1 = pack8(r1), a2 = pack8(r2);
@@ -179,7 +220,42 @@ __global__ __launch_bounds__(256, 2) void decode_split_kernel(
   }
   // query fragment (B operand): column = head of the group, slots = d
   u32x4 qf[KS];
-  if (c32 < n_rep) {
+  if constexpr (QKN) {
+    // lanes l and l ^ 32 hold the two halves of one query row: both load,
+    // one exchange completes the row's sum of squares
+    const bool ql = c32 < n_rep;
+    const bf16* qr = q_new + ((int64_t)b * Hq + g * n_rep + (ql ? c32 : 0)) * D;
+    u32x4 ra[KS / 2], rb[KS / 2];
+    float ss = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < KS / 2; ++ks) {
+      const int d0 = 16 * ks + 8 * hh;
+      ra[ks] = *(const u32x4*)(qr + d0);
+      rb[ks] = *(const u32x4*)(qr + d0 + HALF);
+      float x1[8], x2[8];
+      unpack8(ra[ks], x1);
+      unpack8(rb[ks], x2);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) ss += x1[j] * x1[j] + x2[j] * x2[j];
+    }
+    ss += __shfl_xor(ss, 32, 64);
+#pragma unroll
+    for (int ks = 0; ks < KS / 2; ++ks) {
+      const int d0 = 16 * ks + 8 * hh;
+      float x1[8], x2[8], r1[8], r2[8];
+      unpack8(ra[ks], x1);
+      unpack8(rb[ks], x2);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        x1[j] = rms_scale<bf16>(x1[j], ss, D, eps, qnw[d0 + j]);
+        x2[j] = rms_scale<bf16>(x2[j], ss, D, eps, qnw[d0 + HALF + j]);
+        rope_pair<bf16>(x1[j], x2[j], cr[d0 + j], sr[d0 + j], r1[j], r2[j]);
+      }
+      const u32x4 z = {0u, 0u, 0u, 0u};
+      qf[ks] = ql ? pack8(r1) : z;
+      qf[ks + KS / 2] = ql ? pack8(r2) : z;
+    }
+  } else if (c32 < n_rep) {
     const bf16* qr = q_new + ((int64_t)b * Hq + g * n_rep + c32) * D;
 #pragma unroll
     for (int ks = 0; ks < KS / 2; ++ks) {
@@ -410,7 +486,7 @@ __global__ __launch_bounds__(256) void decode_generic_kernel(
     const T* __restrict__ q_new, const float* __restrict__ cos, const float* __restrict__ sin,
     int64_t row_offset, int64_t rope_rows, int max_len, const T* __restrict__ kc,
     const T* __restrict__ vc, const int32_t* __restrict__ lens, T* __restrict__ out, int B,
-    int Hq, int Hkv, int Smax, int D, float scale) {
+    int Hq, int Hkv, int Smax, int D, float scale, const float* __restrict__ qnw, float eps) {
   const int lane = threadIdx.x & 63;
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= B * Hq) return;
@@ -423,6 +499,11 @@ __global__ __launch_bounds__(256) void decode_generic_kernel(
   const int half = D / 2;
   const int64_t trow = (int64_t)(L - 1) - row_offset;
   const T* qr = q_new + (int64_t)row * D;
+  float ss = 0.f;  // QK-norm: the query row's sum of squares
+  if (qnw != nullptr) {
+    for (int d = lane; d < D; d += 64) ss += to_f32(qr[d]) * to_f32(qr[d]);
+    ss = wave_sum(ss);
+  }
   float qv[4], acc[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -430,9 +511,13 @@ __global__ __launch_bounds__(256) void decode_generic_kernel(
     qv[i] = 0.f;
     if (d < D) {
       const int j = d < half ? d : d - half;
+      float x1 = to_f32(qr[j]), x2 = to_f32(qr[j + half]);
+      if (qnw != nullptr) {
+        x1 = rms_scale<T>(x1, ss, D, eps, qnw[j]);
+        x2 = rms_scale<T>(x2, ss, D, eps, qnw[j + half]);
+      }
       float r1, r2;
-      rope_pair<T>(to_f32(qr[j]), to_f32(qr[j + half]), cos[trow * half + j],
-                   sin[trow * half + j], r1, r2);
+      rope_pair<T>(x1, x2, cos[trow * half + j], sin[trow * half + j], r1, r2);
       qv[i] = d < half ? r1 : r2;
     }
   }
@@ -467,23 +552,26 @@ __global__ __launch_bounds__(256) void decode_generic_kernel(
 template <typename T>
 int launch_append(const T* k_new, const T* v_new, const float* cos, const float* sin, T* kc,
                   T* vc, const int32_t* lens, int start, int64_t row_offset, int64_t rope_rows,
-                  int max_len, int B, int Snew, int Hkv, int Smax, int D, hipStream_t stream) {
+                  int max_len, int B, int Snew, int Hkv, int Smax, int D, hipStream_t stream,
+                  const float* knw = nullptr, float eps = 0.f) {
   const int64_t n = (int64_t)B * Snew * Hkv * (D / 2);
   if (n == 0) return KF_OK;
   KF_LAUNCH("kv_append", append_kernel<T>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream,
                      k_new, v_new, cos, sin, kc, vc, lens, start, row_offset, rope_rows, max_len,
-                     B, Snew, Hkv, Smax, D);
+                     B, Snew, Hkv, Smax, D, knw, eps);
   KF_CHECK_LAUNCH();
   return KF_OK;
 }
 
 template <int D>
 int launch_split(const DecodeArgs& a, float* opart, float* mpart, float* lpart, int nsplit) {
-  KF_LAUNCH("decode_split", decode_split_kernel<D>, dim3(nsplit, a.B * a.Hkv), dim3(256), 0,
+  const bool qkn = a.q_norm_w != nullptr;
+  KF_LAUNCH("decode_split", (qkn ? decode_split_kernel<D, true> : decode_split_kernel<D, false>),
+            dim3(nsplit, a.B * a.Hkv), dim3(256), 0,
             a.stream, (const bf16*)a.q_new, (const bf16*)a.k_new, (const bf16*)a.v_new, a.cos,
             a.sin, a.rope_row_offset, a.rope_rows, a.max_len, (bf16*)a.k_cache, (bf16*)a.v_cache,
             a.lens, opart, mpart, lpart, a.Hq, a.Hkv, a.Smax, nsplit, a.Hq / a.Hkv,
-            a.scale * kLog2e);
+            a.scale * kLog2e, a.q_norm_w, a.k_norm_w, a.norm_eps);
   KF_CHECK_LAUNCH();
   return KF_OK;
 }
@@ -512,12 +600,12 @@ int decode_typed(const DecodeArgs& a, void* workspace) {
   }
   rc = launch_append<T>((const T*)a.k_new, (const T*)a.v_new, a.cos, a.sin, (T*)a.k_cache,
                         (T*)a.v_cache, a.lens, 0, a.rope_row_offset, a.rope_rows, a.max_len, a.B,
-                        1, a.Hkv, a.Smax, a.D, a.stream);
+                        1, a.Hkv, a.Smax, a.D, a.stream, a.k_norm_w, a.norm_eps);
   if (rc) return rc;
   KF_LAUNCH("decode_generic", decode_generic_kernel<T>, dim3((a.B * a.Hq + 3) / 4), dim3(256), 0,
                      a.stream, (const T*)a.q_new, a.cos, a.sin, a.rope_row_offset, a.rope_rows,
                      a.max_len, (const T*)a.k_cache, (const T*)a.v_cache, a.lens, (T*)a.out, a.B,
-                     a.Hq, a.Hkv, a.Smax, a.D, a.scale);
+                     a.Hq, a.Hkv, a.Smax, a.D, a.scale, a.q_norm_w, a.norm_eps);
   KF_CHECK_LAUNCH();
   return KF_OK;
 }

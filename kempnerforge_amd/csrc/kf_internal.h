@@ -77,6 +77,8 @@ struct DecodeArgs {
   int64_t rope_rows;                  // rows in the tables
   void* out;                          // [B, 1, Hq, D]
   int B, Smax, Hq, Hkv, D, max_len;   // max_len >= lens[b] + 1 for every b
+  const float *q_norm_w, *k_norm_w;   // [D] float32 QK-norm weights, or both null
+  float norm_eps;
   int dtype;
   float scale;
   hipStream_t stream;

@@ -15,6 +15,7 @@ only accept GPU tensors: there is no CPU path.
 from __future__ import annotations
 
 import ctypes
+import weakref
 from typing import Optional
 
 import torch
@@ -160,9 +161,11 @@ def bwd_raw(q, k, v, cos, sin, out, lse, dout, *, causal: bool, doc_ids=None,
 
 
 def decode_raw(q_new, k_new, v_new, k_cache, v_cache, lens, cos, sin, *, rope_row_offset: int,
-               max_len: int):
+               max_len: int, q_norm_weight=None, k_norm_weight=None, norm_eps: float = 1e-5):
     """One decode step (``kf_attn_decode``); writes the rotated new k and v into
-    the caches at ``lens[b]`` and returns out ``[B,1,Hq,D]``."""
+    the caches at ``lens[b]`` and returns out ``[B,1,Hq,D]``.  With the QK-norm
+    weights (``[D]``, any float dtype) q_new and k_new are RMS-normalised in the
+    kernels first, as ``Attention.q_norm`` / ``k_norm`` would."""
     _require_gpu(q_new, k_new, v_new, k_cache, v_cache, lens)
     lib = _lib.load()
     q_new, k_new, v_new = (t.contiguous() for t in (q_new, k_new, v_new))
@@ -174,6 +177,11 @@ def decode_raw(q_new, k_new, v_new, k_cache, v_cache, lens, cos, sin, *, rope_ro
     Hkv, Smax = k_cache.shape[1], k_cache.shape[2]
     cos = _rope_table(cos, 1, D // 2, "rope_cos")
     sin = _rope_table(sin, 1, D // 2, "rope_sin")
+    if (q_norm_weight is None) != (k_norm_weight is None):
+        raise ValueError("QK-norm needs both q_norm_weight and k_norm_weight")
+    qnw = knw = None
+    if q_norm_weight is not None:
+        qnw, knw = (_norm_weight(w, D, q_new.device) for w in (q_norm_weight, k_norm_weight))
     dt = _dtype_code(q_new)
     out = torch.empty_like(q_new)
     nbytes = _lib.size_out()
@@ -182,10 +190,35 @@ def decode_raw(q_new, k_new, v_new, k_cache, v_cache, lens, cos, sin, *, rope_ro
     ws = _workspace(nbytes.value, q_new.device)
     _lib.check(lib.kf_attn_decode(_ptr(q_new), _ptr(k_new), _ptr(v_new), _ptr(k_cache),
                                   _ptr(v_cache), _ptr(lens), _ptr(cos), _ptr(sin),
-                                  int(rope_row_offset), cos.shape[0], _ptr(out), _ptr(ws), ws.numel(), B, Smax,
-                                  Hq, Hkv, D, int(max_len), dt, _stream(q_new)),
+                                  int(rope_row_offset), cos.shape[0], _ptr(out), _ptr(ws),
+                                  ws.numel(), B, Smax, Hq, Hkv, D, int(max_len), _ptr(qnw),
+                                  _ptr(knw), float(norm_eps), dt, _stream(q_new)),
                "kf_attn_decode")
     return out
+
+
+_NORM_CACHE: dict[int, tuple] = {}  # id(weight) -> (weakref, version, float32 copy)
+
+
+def _norm_weight(w: torch.Tensor, D: int, device) -> torch.Tensor:
+    """RMSNorm weight as the float32 [D] vector the kernels read (exact for any
+    float storage dtype), cached per parameter version so that a decode step
+    does not launch the conversion again."""
+    if w.shape != (D,):
+        raise ValueError(f"QK-norm weight must be [{D}] (got {tuple(w.shape)})")
+    if w.device != device:
+        raise RuntimeError("QK-norm weight must be on the same device as q")
+    if w.dtype == torch.float32 and w.is_contiguous():
+        return w
+    hit = _NORM_CACHE.get(id(w))
+    if hit is not None and hit[0]() is w and hit[1] == w._version:
+        return hit[2]
+    f = w.detach().to(torch.float32).contiguous()
+    if len(_NORM_CACHE) > 1024:  # drop entries of freed weights
+        for k in [k for k, e in _NORM_CACHE.items() if e[0]() is None]:
+            del _NORM_CACHE[k]
+    _NORM_CACHE[id(w)] = (weakref.ref(w), w._version, f)
+    return f
 
 
 def cache_append_raw(k_new, v_new, cos, sin, k_cache, v_cache, start: int) -> None:
