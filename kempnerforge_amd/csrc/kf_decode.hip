@@ -238,7 +238,7 @@ __global__ __launch_bounds__(256, 2) void decode_split_kernel(
 #pragma unroll
       for (int j = 0; j < 8; ++j) ss += x1[j] * x1[j] + x2[j] * x2[j];
     }
-    ss += __shfl_xor(ss, 32, 64);
+    ss = pair_sum32(ss);
 #pragma unroll
     for (int ks = 0; ks < KS / 2; ++ks) {
       const int d0 = 16 * ks + 8 * hh;
@@ -344,7 +344,7 @@ __global__ __launch_bounds__(256, 2) void decode_split_kernel(
         sc[i] = local > lim ? -INFINITY : sc[i] * scale_log2;
         tmax = fmaxf(tmax, sc[i]);
       }
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+      tmax = pair_max32(tmax);
       const float mnew = fmaxf(m, tmax);  // finite: key r0 is valid
       const float alpha = fast_exp2(m - mnew);
       float psum = 0.f;
@@ -386,7 +386,7 @@ __global__ __launch_bounds__(256, 2) void decode_split_kernel(
     }
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  const float ltot = lsum + __shfl_xor(lsum, 32, 64);
+  const float ltot = pair_sum32(lsum);
   // merge the wavefronts: (m, l) per head, then o through LDS (reuses sV)
   if (hh == 0) {
     sML[w][0][c32] = m;

@@ -281,7 +281,7 @@ __global__ __launch_bounds__(256, 2) void fwd_mfma_kernel(
     for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
       for (int i = 0; i < 16; ++i) tmax = fmaxf(tmax, s[mt][i]);
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64)) * scale_log2;
+    tmax = pair_max32(tmax) * scale_log2;
     // Rescale the running output only when some row's max grew: the exponent
     // base m may lag the true max (exp2 arguments stay <= 0 either way, since
     // m >= every score seen so far), and rows whose max did not move keep
@@ -321,7 +321,7 @@ __global__ __launch_bounds__(256, 2) void fwd_mfma_kernel(
     __syncthreads();
   }
 
-  const float ltot = lsum + __shfl_xor(lsum, 32, 64);
+  const float ltot = pair_sum32(lsum);
   const float inv = 1.f / ltot;
   if (ri.q_valid) {
     bf16* orow = out + (((int64_t)ri.b * Sq + ri.pos) * Hq + ri.hq) * D;

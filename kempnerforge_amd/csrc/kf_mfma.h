@@ -179,6 +179,22 @@ __device__ __forceinline__ void settle(T& x) {
   asm volatile("" : "+v"(x));
 }
 
+// x combined over lanes l and l ^ 32 (the two halves of a 32x32 C column) with
+// v_permlane32_swap, a VALU op, instead of __shfl_xor's LDS permute (which
+// queues behind the fragment reads).  The swap leaves lanes 0-31 holding
+// (x[l], x[l+32]) and lanes 32-63 (x[l-32], x[l]), so max and sum come out as
+// max / sum of the pair on both lanes, as with x op __shfl_xor(x, 32).
+__device__ __forceinline__ float pair_max32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float pair_sum32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 // Wavefront index as a scalar (SGPR) value, so per-wave LDS destinations and
 // global bases derived from it stay uniform.
 __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
