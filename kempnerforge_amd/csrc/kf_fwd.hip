@@ -37,8 +37,9 @@ __global__ __launch_bounds__(256) void kv_prep_kernel(
     const float* __restrict__ sin, bf16* __restrict__ krot, bf16* __restrict__ vn, int Sk,
     int Skp, int Hkv, int64_t ksb, int64_t kss, int64_t ksh, int64_t vsb, int64_t vss,
     int64_t vsh, int k_rotated, const int32_t* __restrict__ doc, const int32_t* __restrict__ kvalid,
-    int2* __restrict__ ranges) {
+    int2* __restrict__ ranges, int v_transposed) {
   constexpr int HALF = D / 2;
+  __shared__ __attribute__((aligned(16))) bf16 sVt[D * BN];  // v_transposed: [d][key slot]
   constexpr int CP = HALF / 8;
   const int s0 = blockIdx.x * BN;
   const int bh = blockIdx.y;
@@ -88,12 +89,35 @@ __global__ __launch_bounds__(256) void kv_prep_kernel(
     *(u32x4*)(dst + 8 * c) = o1;
     *(u32x4*)(dst + 8 * c + HALF) = o2;
   }
+  if (!v_transposed) {
+    for (int it = tid; it < BN * (D / 8); it += 256) {
+      const int key = it / (D / 8), c = it % (D / 8);
+      const int s = s0 + key;
+      u32x4 a = {0u, 0u, 0u, 0u};
+      if (s < Sk) a = *(const u32x4*)(v + b * vsb + (int64_t)s * vss + g * vsh + 8 * c);
+      *(u32x4*)(vn + ((int64_t)bh * Skp + s) * D + 8 * c) = a;
+    }
+    return;
+  }
+  // V^T: [bh][D][Skp], keys of each 16-key group stored in the order
+  // 0-3, 8-11, 4-7, 12-15 (bits 2 and 3 of the key index swapped).  That is the
+  // key order of a P^T fragment built from the 32x32 C layout (lane half h holds
+  // keys 4h..4h+3 and 8+4h..8+4h+3 of each 16), so one 16-byte read of a V^T row
+  // is a complete A fragment of O^T += V^T P^T.
   for (int it = tid; it < BN * (D / 8); it += 256) {
     const int key = it / (D / 8), c = it % (D / 8);
     const int s = s0 + key;
     u32x4 a = {0u, 0u, 0u, 0u};
     if (s < Sk) a = *(const u32x4*)(v + b * vsb + (int64_t)s * vss + g * vsh + 8 * c);
-    *(u32x4*)(vn + ((int64_t)bh * Skp + s) * D + 8 * c) = a;
+    const int slot = (key & ~12) | ((key & 4) << 1) | ((key & 8) >> 1);
+    const bf16* e = (const bf16*)&a;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) sVt[(8 * c + j) * BN + slot] = e[j];
+  }
+  __syncthreads();
+  for (int it = tid; it < D * (BN / 8); it += 256) {
+    const int d = it / (BN / 8), c = it % (BN / 8);
+    *(u32x4*)(vn + ((int64_t)bh * D + d) * Skp + s0 + 8 * c) = *(const u32x4*)&sVt[d * BN + 8 * c];
   }
 }
 
@@ -163,10 +187,10 @@ __global__ __launch_bounds__(256, 2) void fwd_mfma_kernel(
   const int32_t* arow = LIST ? aux + (int64_t)ri.b * Sk : nullptr;
   const int2* rec = ranges + (int64_t)ri.b * (Skp / BN);
   const bf16* kbase = krot + (int64_t)bh * Skp * D;
-  const bf16* vbase = vn + (int64_t)bh * Skp * D;
+  const bf16* vbase = vn + (int64_t)bh * D * Skp;  // V^T, keys in fragment order
   auto stage = [&](int t, int buf) {
     tile_to_lds<BN, KR>(kbase + (int64_t)t * BN * D, D, sK[buf], w, lane);
-    tile_to_lds<BN, KR>(vbase + (int64_t)t * BN * D, D, sV[buf], w, lane);
+    tile_to_lds<D, BN / 8>(vbase + (int64_t)t * BN, Skp, sV[buf], w, lane);
     if (LIST && w == 0) dma4(lds_addr(sKD[buf]), (uint32_t)min(t * BN + lane, Sk - 1) * 4u, arow);
   };
   int di = 0;       // DOC: this row's document
@@ -213,7 +237,6 @@ __global__ __launch_bounds__(256, 2) void fwd_mfma_kernel(
 
   bf16x8 qf[KS];
   load_q_frag<D>(q, cos, sin, ri, Sq, Hq, hh, qf);
-  const TrOffsets<D> tro = tr_offsets<D>(lane);
 
   float m = LIST ? -1e30f : -INFINITY, lsum = 0.f;
   f32x16 acc[DT];
@@ -313,7 +336,7 @@ __global__ __launch_bounds__(256, 2) void fwd_mfma_kernel(
       const bf16x8 pb = as_bf16x8(pk[c]);
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
-        const bf16x8 a = lds_frag_t<D>(tV, tro, c, dt);
+        const bf16x8 a = lds_frag<BN / 8>(tV, 32 * dt + c32, 2 * c + hh);
         acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb, acc[dt], 0, 0, 0);
       }
     }
@@ -484,18 +507,21 @@ size_t fwd_mfma_workspace(int B, int Sk, int Hkv, int D) {
   return 2 * (size_t)B * Hkv * Skp * D * sizeof(uint16_t) + (size_t)B * (Skp / BN) * sizeof(int2);
 }
 
-int launch_kv_prep(const FwdArgs& a, void* krot_, void* vn_, int Skp, int2* ranges) {
+int launch_kv_prep(const FwdArgs& a, void* krot_, void* vn_, int Skp, int2* ranges,
+                   int v_transposed) {
   bf16* krot = (bf16*)krot_;
   bf16* vn = (bf16*)vn_;
   dim3 grid(Skp / BN, a.B * a.Hkv);
   if (a.D == 128)
     KF_LAUNCH("kv_prep", kv_prep_kernel<128>, grid, dim3(256), 0, a.stream, (const bf16*)a.k,
                        (const bf16*)a.v, a.cos, a.sin, krot, vn, a.Sk, Skp, a.Hkv, a.ksb, a.kss,
-                       a.ksh, a.vsb, a.vss, a.vsh, a.k_rotated, a.doc, a.kvalid, ranges);
+                       a.ksh, a.vsb, a.vss, a.vsh, a.k_rotated, a.doc, a.kvalid, ranges,
+                       v_transposed);
   else
     KF_LAUNCH("kv_prep", kv_prep_kernel<64>, grid, dim3(256), 0, a.stream, (const bf16*)a.k,
                        (const bf16*)a.v, a.cos, a.sin, krot, vn, a.Sk, Skp, a.Hkv, a.ksb, a.kss,
-                       a.ksh, a.vsb, a.vss, a.vsh, a.k_rotated, a.doc, a.kvalid, ranges);
+                       a.ksh, a.vsb, a.vss, a.vsh, a.k_rotated, a.doc, a.kvalid, ranges,
+                       v_transposed);
   KF_CHECK_LAUNCH();
   return KF_OK;
 }
@@ -564,7 +590,7 @@ void launch_capture_mode(const FwdArgs& a, const FwdWs& w, const float* lse, flo
 int fwd_mfma(const FwdArgs& a, void* workspace) {
   const int Skp = (a.Sk + BN - 1) / BN * BN;
   const FwdWs w = carve_fwd(a, workspace, Skp);
-  int rc = launch_kv_prep(a, w.krot, w.vn, Skp, w.ranges);
+  int rc = launch_kv_prep(a, w.krot, w.vn, Skp, w.ranges, 1);
   if (rc) return rc;
   const int n_rep = a.Hq / a.Hkv;
   const int bm_pos = pick_bm_pos(n_rep);
