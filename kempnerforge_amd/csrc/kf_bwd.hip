@@ -193,6 +193,16 @@ __device__ __forceinline__ void dkdv_role(
     const bool diag = causal && q0 < k0 + BKV;
     const bool dmask = LIST && (e & DOC_MASK_FLAG);
 
+    // this lane's 32 rows' log-sum-exp (P waves) or Delta (dS waves), read
+    // before the phase-1 products so the reads complete under them: read at
+    // the point of use they queue behind the fragment reads of the other role
+    f32x4 rowv[8];
+    {
+      const float* src = DSROLE ? S_.dl : S_.l;
+#pragma unroll
+      for (int r = 0; r < 8; ++r) rowv[r] = *(const f32x4*)(&src[8 * r + 4 * hh]);
+    }
+
     // phase 1: S (P waves) or dP (dS waves) for both 32-row halves
     f32x16 x[2];
 #pragma unroll
@@ -218,7 +228,7 @@ __device__ __forceinline__ void dkdv_role(
 #pragma unroll
         for (int gq = 0; gq < 4; ++gq) {
           const int r0 = 32 * mt + 8 * gq + 4 * hh;
-          const f32x4 l4 = *(const f32x4*)(&S_.l[r0]);
+          const f32x4 l4 = rowv[4 * mt + gq];
           float v[4];
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
@@ -255,8 +265,7 @@ __device__ __forceinline__ void dkdv_role(
 #pragma unroll
           for (int half = 0; half < 2; ++half) {
             const int gq = 2 * cc + half;
-            const int r0 = 32 * mt + 8 * gq + 4 * hh;
-            const f32x4 d4 = *(const f32x4*)(&S_.dl[r0]);
+            const f32x4 d4 = rowv[4 * mt + gq];
             float v[4];
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
