@@ -3,9 +3,11 @@
 // Four launches, no atomics (bit-deterministic):
 //  kv_prep      (shared with the forward) per KV head: K rotated (eager bf16
 //               RoPE) and V, both [bh][P][D].
-//  q_prep_bwd   per query head: Q rotated and dO, both [bhq][P][D]; lse*log2(e)
-//               and Delta = rowsum(dO o O) [bhq][P].  P = S rounded up to 128;
-//               padded rows are zero with lse = +inf, so they contribute nothing.
+//  q_prep_bwd   per query head: Q rotated [bhq][P][D]; lse*log2(e) and Delta =
+//               rowsum(dO o O) [bhq][P].  P = S rounded up to 128; padded rows
+//               are zero with lse = +inf, so they contribute nothing.  dO is read
+//               in place ([B, S, Hq, D]) by the kernels below, rows past S
+//               repeating row S - 1.
 //  Transposed operands (K^T, Q^T, dO^T) are never stored: they are read from
 //  the row-major LDS tiles with ds_read_b64_tr_b16 (lds_frag_t).
 //  dkdv         workgroup = 128 keys of one KV head (4 wavefronts x 32 keys,
@@ -49,8 +51,8 @@ template <int D>
 __global__ __launch_bounds__(256) void q_prep_bwd_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ out, const bf16* __restrict__ dout,
     const float* __restrict__ lse, const float* __restrict__ cos, const float* __restrict__ sin,
-    bf16* __restrict__ qrot, bf16* __restrict__ don, float* __restrict__ lse2,
-    float* __restrict__ delta, int S, int P, int Hq) {
+    bf16* __restrict__ qrot, float* __restrict__ lse2, float* __restrict__ delta, int S, int P,
+    int Hq) {
   constexpr int HALF = D / 2, CP = HALF / 8, TPR = D / 8;
   const int s0 = blockIdx.x * BN, bhq = blockIdx.y, b = bhq / Hq, h = bhq % Hq;
   const int tid = threadIdx.x;
@@ -73,23 +75,21 @@ __global__ __launch_bounds__(256) void q_prep_bwd_kernel(
     *(u32x4*)(dst + 8 * c) = o1;
     *(u32x4*)(dst + 8 * c + HALF) = o2;
   }
-  // dO copy + Delta (TPR consecutive lanes own one row)
+  // Delta (TPR consecutive lanes own one row); dO itself is read in place by
+  // the dK/dV and dQ kernels
   for (int it = tid; it < BN * TPR; it += 256) {
     const int row = it / TPR, c = it % TPR, s = s0 + row;
-    u32x4 a = {0u, 0u, 0u, 0u};
     float part = 0.f;
     if (s < S) {
       const int64_t off = (((int64_t)b * S + s) * Hq + h) * D + 8 * c;
-      a = *(const u32x4*)(dout + off);
       float fd[8], fo[8];
-      unpack8(a, fd);
+      unpack8(*(const u32x4*)(dout + off), fd);
       unpack8(*(const u32x4*)(out + off), fo);
 #pragma unroll
       for (int j = 0; j < 8; ++j) part += fd[j] * fo[j];
     }
 #pragma unroll
     for (int o = 1; o < TPR; o <<= 1) part += __shfl_xor(part, o, 64);
-    *(u32x4*)(don + ((int64_t)bhq * P + s) * D + 8 * c) = a;
     if (c == 0) {
       delta[(int64_t)bhq * P + s] = part;
       lse2[(int64_t)bhq * P + s] = s < S ? lse[(int64_t)bhq * S + s] * kLog2e : INFINITY;
@@ -120,7 +120,7 @@ struct DkdvStage {
 template <int D, bool DSROLE, int MODE>
 __device__ __forceinline__ void dkdv_role(
     DkdvStage<D>* st, u32x4* sP, const bf16* __restrict__ krot, const bf16* __restrict__ vn,
-    const bf16* __restrict__ qrot, const bf16* __restrict__ don,
+    const bf16* __restrict__ qrot, const bf16* __restrict__ dout,
     const float* __restrict__ lse2, const float* __restrict__ delta,
     const float* __restrict__ cos, const float* __restrict__ sin, bf16* __restrict__ dk,
     bf16* __restrict__ dv, int S, int P, int Hq, int Hkv, int n_rep, int b, int g, int bh, int k0,
@@ -147,11 +147,15 @@ __device__ __forceinline__ void dkdv_role(
   const int kdoc = DOC ? drow[min(key, S - 1)] : KPM ? (key < S && drow[min(key, S - 1)] != 0) : 0;
 
   auto stage_tile = [&](int hl, int qtile, int buf) {
-    const int64_t bhq = (int64_t)b * Hq + g * n_rep + hl;
+    const int hq = g * n_rep + hl;
+    const int64_t bhq = (int64_t)b * Hq + hq;
     const int q0 = qtile * BQ;
     DkdvStage<D>& S_ = st[buf];
     tile_to_lds<BQ, KR, 8>(qrot + (bhq * P + q0) * D, D, S_.q, w, lane);
-    tile_to_lds<BQ, KR, 8>(don + (bhq * P + q0) * D, D, S_.o, w, lane);
+    // dO in place ([B, S, Hq, D]): rows past S repeat row S - 1 (their lse is
+    // +inf, so they contribute nothing)
+    tile_to_lds<BQ, KR, 8>(dout + (((int64_t)b * S + q0) * Hq + hq) * D, Hq * D, S_.o, w, lane,
+                           S - q0);
     if (w == 0) row_to_lds(lse2 + bhq * P + q0, S_.l, lane);
     if (w == 1) row_to_lds(delta + bhq * P + q0, S_.dl, lane);
     if (DOC && w == 2) dma4(lds_addr(sQD[buf]), (uint32_t)min(q0 + lane, S - 1) * 4u, drow);
@@ -336,13 +340,15 @@ __device__ __forceinline__ void dkdv_role(
 // iteration 0 reads) with its document ids.
 template <int D>
 __device__ __forceinline__ void dkdv_stage_first(
-    DkdvStage<D>* st, const bf16* __restrict__ qrot, const bf16* __restrict__ don,
+    DkdvStage<D>* st, const bf16* __restrict__ qrot, const bf16* __restrict__ dout,
     const float* __restrict__ lse2, const float* __restrict__ delta,
-    const int32_t* __restrict__ drow, int S, int P, int64_t bhq, int q0, int32_t* sqd, int w,
-    int lane) {
+    const int32_t* __restrict__ drow, int S, int P, int Hq, int b, int hq, int q0, int32_t* sqd,
+    int w, int lane) {
   constexpr int KR = D / 8;
+  const int64_t bhq = (int64_t)b * Hq + hq;
   tile_to_lds<BQ, KR, 8>(qrot + (bhq * P + q0) * D, D, st[0].q, w, lane);
-  tile_to_lds<BQ, KR, 8>(don + (bhq * P + q0) * D, D, st[0].o, w, lane);
+  tile_to_lds<BQ, KR, 8>(dout + (((int64_t)b * S + q0) * Hq + hq) * D, Hq * D, st[0].o, w, lane,
+                         S - q0);
   if (w == 0) row_to_lds(lse2 + bhq * P + q0, st[0].l, lane);
   if (w == 1) row_to_lds(delta + bhq * P + q0, st[0].dl, lane);
   if (w == 2) dma4(lds_addr(sqd), (uint32_t)min(q0 + lane, S - 1) * 4u, drow);
@@ -351,7 +357,7 @@ __device__ __forceinline__ void dkdv_stage_first(
 template <int D, int MODE>
 __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(
     const bf16* __restrict__ krot, const bf16* __restrict__ vn, const bf16* __restrict__ qrot,
-    const bf16* __restrict__ don, const float* __restrict__ lse2, const float* __restrict__ delta,
+    const bf16* __restrict__ dout, const float* __restrict__ lse2, const float* __restrict__ delta,
     const float* __restrict__ cos, const float* __restrict__ sin, bf16* __restrict__ dk,
     bf16* __restrict__ dv, int S, int P, int Hq, int Hkv, int n_rep, int nkb, float scale_log2,
     float scale, int causal, const int32_t* __restrict__ aux, const int2* __restrict__ ranges) {
@@ -396,7 +402,7 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(
   }
   if constexpr (DOC) {
     const int qt0 = k0 / BQ;  // the diagonal query tile: always listed, first
-    dkdv_stage_first<D>(st, qrot, don, lse2, delta, drow, S, P, (int64_t)b * Hq + g * n_rep,
+    dkdv_stage_first<D>(st, qrot, dout, lse2, delta, drow, S, P, Hq, b, g * n_rep,
                         qt0 * BQ, sQD[0], w, lane);
     if (w == 0) {
       const int n = doc_tile_list(drow, k0, min(k0 + BKV, S), ranges + (int64_t)b * (P / BN),
@@ -407,11 +413,11 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(
     nlist = __builtin_amdgcn_readfirstlane(sCount);
   }
   if (w >= 4)
-    dkdv_role<D, true, MODE>(st, sP, krot, vn, qrot, don, lse2, delta, cos, sin, dk, dv, S, P,
+    dkdv_role<D, true, MODE>(st, sP, krot, vn, qrot, dout, lse2, delta, cos, sin, dk, dv, S, P,
                              Hq, Hkv, n_rep, b, g, bh, k0, w, lane, scale_log2, scale, causal,
                              drow, sList, nlist, sQD, fv);
   else
-    dkdv_role<D, false, MODE>(st, sP, krot, vn, qrot, don, lse2, delta, cos, sin, dk, dv, S, P,
+    dkdv_role<D, false, MODE>(st, sP, krot, vn, qrot, dout, lse2, delta, cos, sin, dk, dv, S, P,
                               Hq, Hkv, n_rep, b, g, bh, k0, w, lane, scale_log2, scale, causal,
                               drow, sList, nlist, sQD, fv);
 }
@@ -423,7 +429,7 @@ constexpr int DQ_ROWS = 256;
 
 template <int D, int MODE>
 __global__ __launch_bounds__(512, 1) void bwd_dq_kernel(
-    const bf16* __restrict__ qrot, const bf16* __restrict__ don, const float* __restrict__ lse2,
+    const bf16* __restrict__ qrot, const bf16* __restrict__ dout, const float* __restrict__ lse2,
     const float* __restrict__ delta, const bf16* __restrict__ krot, const bf16* __restrict__ vn,
     const float* __restrict__ cos, const float* __restrict__ sin, bf16* __restrict__ dq, int S,
     int P, int Hq, int Hkv, int n_rep, int bm_pos, int nqb, float scale_log2, float scale,
@@ -500,7 +506,7 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_kernel(
   float l2 = INFINITY, dl = 0.f;
   if (ri.q_valid) {
     const bf16* qr = qrot + (bhq * P + ri.pos) * D + 8 * hh;
-    const bf16* dr = don + (bhq * P + ri.pos) * D + 8 * hh;
+    const bf16* dr = dout + (((int64_t)ri.b * S + ri.pos) * Hq + ri.hq) * D + 8 * hh;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       qf[ks] = as_bf16x8(*(const u32x4*)(qr + 16 * ks));
@@ -638,7 +644,7 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_kernel(
 }
 
 struct Ws {
-  bf16 *krot, *vn, *qrot, *don;
+  bf16 *krot, *vn, *qrot;
   float *lse2, *delta;
   int2* ranges;  // [B][P/64] document-id range per tile (packed documents only)
 };
@@ -651,7 +657,6 @@ Ws carve(void* base, int B, int S, int Hq, int Hkv, int D) {
   w.krot = p; p += kv;
   w.vn = p; p += kv;
   w.qrot = p; p += qq;
-  w.don = p; p += qq;
   float* f = (float*)p;
   w.lse2 = f; f += (size_t)B * Hq * P;
   w.delta = f; f += (size_t)B * Hq * P;
@@ -677,7 +682,7 @@ int launch_bwd(const BwdArgs& a, void* workspace) {
   if (rc) return rc;
   KF_LAUNCH("q_prep_bwd", q_prep_bwd_kernel<D>, dim3(P / BN, a.B * a.Hq), dim3(256), 0, a.stream,
             (const bf16*)a.q, (const bf16*)a.out, (const bf16*)a.dout, a.lse, a.cos, a.sin,
-            w.qrot, w.don, w.lse2, w.delta, a.S, P, a.Hq);
+            w.qrot, w.lse2, w.delta, a.S, P, a.Hq);
   KF_CHECK_LAUNCH();
   const int nkb = P / BKV;
   const int mode = a.doc ? MASK_DOC : a.kvalid ? MASK_KPM : MASK_NONE;
@@ -686,7 +691,7 @@ int launch_bwd(const BwdArgs& a, void* workspace) {
             (mode == MASK_DOC   ? bwd_dkdv_kernel<D, MASK_DOC>
              : mode == MASK_KPM ? bwd_dkdv_kernel<D, MASK_KPM>
                                 : bwd_dkdv_kernel<D, MASK_NONE>),
-            dim3(nkb * a.B * a.Hkv), dim3(512), 0, a.stream, w.krot, w.vn, w.qrot, w.don, w.lse2,
+            dim3(nkb * a.B * a.Hkv), dim3(512), 0, a.stream, w.krot, w.vn, w.qrot, (const bf16*)a.dout, w.lse2,
             w.delta, a.cos, a.sin, (bf16*)a.dk, (bf16*)a.dv, a.S, P, a.Hq, a.Hkv, n_rep, nkb,
             scale_log2, a.scale, a.causal, aux, w.ranges);
   KF_CHECK_LAUNCH();
@@ -696,7 +701,7 @@ int launch_bwd(const BwdArgs& a, void* workspace) {
             (mode == MASK_DOC   ? bwd_dq_kernel<D, MASK_DOC>
              : mode == MASK_KPM ? bwd_dq_kernel<D, MASK_KPM>
                                 : bwd_dq_kernel<D, MASK_NONE>),
-            dim3(nqb * a.B * a.Hkv), dim3(512), 0, a.stream, w.qrot, w.don, w.lse2, w.delta,
+            dim3(nqb * a.B * a.Hkv), dim3(512), 0, a.stream, w.qrot, (const bf16*)a.dout, w.lse2, w.delta,
             w.krot, w.vn, a.cos, a.sin, (bf16*)a.dq, a.S, P, a.Hq, a.Hkv, n_rep, bm_pos, nqb,
             scale_log2, a.scale, a.causal, aux, w.ranges);
   KF_CHECK_LAUNCH();
@@ -718,7 +723,7 @@ bool bwd_mfma_supported(const BwdArgs& a) {
 
 size_t bwd_mfma_workspace(int B, int S, int Hq, int Hkv, int D) {
   const size_t P = (size_t)pad_len(S);
-  return (2 * (size_t)B * Hkv + 2 * (size_t)B * Hq) * P * D * sizeof(uint16_t) +
+  return (2 * (size_t)B * Hkv + (size_t)B * Hq) * P * D * sizeof(uint16_t) +
          2 * (size_t)B * Hq * P * sizeof(float) + (size_t)B * (P / BN) * sizeof(int2);
 }
 

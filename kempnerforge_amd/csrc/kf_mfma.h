@@ -93,9 +93,11 @@ __device__ __forceinline__ void dma4(uint32_t lds, uint32_t voff, const void* ba
 // lane picks the global chunk that belongs at its LDS position.  The 4
 // wavefronts of the workgroup split the instructions.  Completion is tracked
 // by vmcnt: wait with lds_copy_wait() and a barrier before reading the tile.
+// Rows at or beyond `rows` (when given) repeat global row rows - 1: a tile
+// that runs past the end of an unpadded tensor stays in bounds.
 template <int ROWS_T, int R, int NW = 4>
 __device__ __forceinline__ void tile_to_lds(const bf16* __restrict__ g, uint32_t ld, bf16* lds,
-                                            int w, int lane) {
+                                            int w, int lane, int rows = ROWS_T) {
   constexpr int TOTAL = ROWS_T * R / 64;
   static_assert(TOTAL % NW == 0, "tile must split evenly over the wavefronts");
   constexpr int PER = TOTAL / NW;
@@ -105,7 +107,7 @@ __device__ __forceinline__ void tile_to_lds(const bf16* __restrict__ g, uint32_t
     const int row = L / R, pc = L % R;
     const int lc = pc ^ swz<R>(row);
     // uniform base + 32-bit per-lane byte offset: the saddr form of the load
-    const uint32_t off = ((uint32_t)row * ld + (uint32_t)lc * 8u) * 2u;
+    const uint32_t off = ((uint32_t)min(row, rows - 1) * ld + (uint32_t)lc * 8u) * 2u;
     dma16(lds_addr(lds + (w * PER + j) * 512), off, g);
   }
 }
