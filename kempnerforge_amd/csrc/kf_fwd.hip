@@ -2,8 +2,9 @@
 //
 // Two kernels:
 //  kv_prep   stages one KV head's keys and values in the layout the MFMA loop
-//            reads: K rotated by RoPE (eager bf16 rounding) and V, both
-//            [bh][Skp][D] with keys >= Sk zeroed.  The backward uses it too.
+//            reads: K rotated by RoPE (eager bf16 rounding) [bh][Skp][D], and V
+//            either as V^T [bh][D][Skp] in P^T fragment key order (forward) or
+//            row-major [bh][Skp][D] (backward); keys >= Sk zeroed.
 //            With document ids it also records each 64-key tile's id range,
 //            with a key-validity mask its valid-key count and first valid key.
 //  fwd_mfma  flash forward.  One workgroup = 4 wavefronts = 128 "rows", where
@@ -13,8 +14,8 @@
 //            v_mfma_f32_32x32x16_bf16, so a lane holds one query's 32 scores of
 //            a 64-key tile: the online-softmax max/sum is lane-local plus one
 //            exchange with lane^32.  O^T = V^T·P^T accumulates in 16 fp32
-//            registers per 32-d tile; its V^T operand comes from the row-major
-//            V tile through LDS transpose reads.  RoPE of q happens at the Q load.
+//            registers per 32-d tile; its V^T operand is one ds_read_b128 of
+//            the staged V^T tile.  RoPE of q happens at the Q load.
 //
 // MFMA 32x32x16 operand layout used (lane l, h = l/32, slot j = 0..7):
 //   A[m][k]: m = l%32, k = 8h + j     B[k][n]: n = l%32, k = 8h + j
@@ -500,8 +501,8 @@ bool fwd_mfma_supported(const FwdArgs& a) {
   return true;
 }
 
-// krot and vn ([B*Hkv][Skp][D] bf16 each), then the per-tile document ranges
-// ([B][Skp/64] int2, written only for packed documents).
+// krot ([B*Hkv][Skp][D] bf16) and V^T ([B*Hkv][D][Skp] bf16), then the per-tile
+// records ([B][Skp/64] int2, written only with an explicit mask).
 size_t fwd_mfma_workspace(int B, int Sk, int Hkv, int D) {
   const size_t Skp = (size_t)((Sk + BN - 1) / BN) * BN;
   return 2 * (size_t)B * Hkv * Skp * D * sizeof(uint16_t) + (size_t)B * (Skp / BN) * sizeof(int2);
