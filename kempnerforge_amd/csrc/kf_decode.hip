@@ -24,7 +24,7 @@ namespace kf {
 
 namespace {
 
-constexpr int CH = 512;  // keys per split
+constexpr int CH = 1024;  // keys per split
 
 // RMSNorm of one element given its row's sum of squares, as the reference's
 // RMSNorm computes it (kempnerforge/model/norm.py:22-27): float32

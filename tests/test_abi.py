@@ -58,7 +58,7 @@ def test_host_only_calls():
     assert b"multiple" in lib.kf_last_error()
     assert lib.kf_attn_fwd_workspace_size(1, 8, 8, 4, 4, 63, 1, ctypes.byref(n)) == 1
     assert lib.kf_attn_decode_workspace_size(32, 32, 8, 128, 8193, 1, ctypes.byref(n)) == 0
-    assert n.value == 32 * 32 * 17 * 130 * 4  # ceil(8193 / 512) splits of (o[D], m, l)
+    assert n.value == 32 * 32 * 9 * 130 * 4  # ceil(8193 / 1024) splits of (o[D], m, l)
     # kv-cache overflow is rejected on the host (reference generate.py:92-96 guard)
     rc = lib.kf_kv_cache_append(ctypes.c_void_p(16), ctypes.c_void_p(16), ctypes.c_void_p(16),
                                 ctypes.c_void_p(16), ctypes.c_void_p(16), ctypes.c_void_p(16),
