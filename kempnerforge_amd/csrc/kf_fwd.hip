@@ -459,7 +459,7 @@ __global__ __launch_bounds__(256, 2) void capture_probs_mfma_kernel(
         }
         if (DOC && kd != drw[i]) p = 0.f;
         if (KPM && !guarded && kd == 0) p = 0.f;
-        __builtin_nontemporal_store(p, prow[i] + key);
+        prow[i][key] = p;
       }
     }
   }
@@ -473,9 +473,9 @@ __global__ __launch_bounds__(256, 2) void capture_probs_mfma_kernel(
         float* prow = pbase + (int64_t)off * Sk;
         for (int key = zstart + tid * 4; key < Sk; key += 256 * 4) {
           if (key + 3 < Sk && (Sk & 3) == 0) {
-            __builtin_nontemporal_store(f32x4{0.f, 0.f, 0.f, 0.f}, (f32x4*)(prow + key));
+            *(f32x4*)(prow + key) = f32x4{0.f, 0.f, 0.f, 0.f};
           } else {
-            for (int e = key; e < min(key + 4, Sk); ++e) __builtin_nontemporal_store(0.f, prow + e);
+            for (int e = key; e < min(key + 4, Sk); ++e) prow[e] = 0.f;
           }
         }
       }
