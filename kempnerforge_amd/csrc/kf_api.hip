@@ -7,9 +7,25 @@
 #include "kf_common.h"
 #include "kf_internal.h"
 
+#include <atomic>
+
 namespace kf {
 
 static thread_local char g_err[512] = "";
+
+int device_cu_count() {
+  static std::atomic<int> cached[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int n = cached[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n <= 0)
+      n = 256;
+    cached[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
 
 void set_error(const char* fmt, ...) {
   va_list ap;

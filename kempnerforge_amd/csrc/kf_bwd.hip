@@ -36,6 +36,8 @@
 #include "kf_internal.h"
 #include "kf_mfma.h"
 
+#include <algorithm>
+
 namespace kf {
 
 namespace {
@@ -359,7 +361,8 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(
     const bf16* __restrict__ krot, const bf16* __restrict__ vn, const bf16* __restrict__ qrot,
     const bf16* __restrict__ dout, const float* __restrict__ lse2, const float* __restrict__ delta,
     const float* __restrict__ cos, const float* __restrict__ sin, bf16* __restrict__ dk,
-    bf16* __restrict__ dv, int S, int P, int Hq, int Hkv, int n_rep, int nkb, float scale_log2,
+    bf16* __restrict__ dv, int S, int P, int Hq, int Hkv, int n_rep, int nkb, int nitems,
+    float scale_log2,
     float scale, int causal, const int32_t* __restrict__ aux, const int2* __restrict__ ranges) {
   constexpr bool DOC = MODE == MASK_DOC, KPM = MODE == MASK_KPM;
   __shared__ __attribute__((aligned(16))) DkdvStage<D> st[2];
@@ -368,58 +371,64 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(
   __shared__ uint16_t sList[DOC_MAX_TILES];                      // listed query tiles
   __shared__ int sCount, sFirst;
   const int w = wave_id(), lane = threadIdx.x & 63;
-  const int logical = xcd_logical_id(blockIdx.x, gridDim.x);
-  const int bh = logical / nkb;
-  const int kb = logical % nkb;  // ascending: the longest causal key tiles first
-  const int b = bh / Hkv, g = bh % Hkv;
-  const int k0 = kb * BKV;
-  const int32_t* drow = DOC || KPM ? aux + (int64_t)b * S : nullptr;
-  const int2* rec = ranges + (int64_t)b * (P / BN);
-  int nlist = 0, fv = 0;
-  if constexpr (KPM) {
-    if (w == 0) {
-      const int f = kpm_first_valid(rec, P / BN, lane);
-      // valid keys in this block (its two 64-key tiles) against its keys below S
-      const int t0 = k0 / BN;
-      const int nval = rec[t0].x + (t0 + 1 < P / BN ? rec[t0 + 1].x : 0);
-      const int nkeys = min(BKV, S - k0);
-      const int qt0 = k0 / BQ;
-      // query tiles holding guarded rows, then the causal ones if a key is valid
-      const int n = kpm_tile_list(
-          rec, 0, (S + BQ - 1) / BQ,
-          [&](int t, int2) {
-            return t * BQ < f ? 2 : (t >= qt0 && nval > 0) ? (nval < nkeys ? 2 : 1) : 0;
-          },
-          sList, lane);
-      if (lane == 0) {
-        sCount = n;
-        sFirst = f;
+  // persistent: one (key block, KV head) item per round
+  const XcdItems xi = xcd_items(nitems);
+  for (int rnd = 0;; ++rnd) {
+    const int logical = xcd_item(xi, rnd);
+    if (logical < 0) break;
+    const int bh = logical / nkb;
+    const int kb = logical % nkb;  // ascending: the longest causal key tiles first
+    const int b = bh / Hkv, g = bh % Hkv;
+    const int k0 = kb * BKV;
+    const int32_t* drow = DOC || KPM ? aux + (int64_t)b * S : nullptr;
+    const int2* rec = ranges + (int64_t)b * (P / BN);
+    int nlist = 0, fv = 0;
+    if constexpr (KPM) {
+      if (w == 0) {
+        const int f = kpm_first_valid(rec, P / BN, lane);
+        // valid keys in this block (its two 64-key tiles) against its keys below S
+        const int t0 = k0 / BN;
+        const int nval = rec[t0].x + (t0 + 1 < P / BN ? rec[t0 + 1].x : 0);
+        const int nkeys = min(BKV, S - k0);
+        const int qt0 = k0 / BQ;
+        // query tiles holding guarded rows, then the causal ones if a key is valid
+        const int n = kpm_tile_list(
+            rec, 0, (S + BQ - 1) / BQ,
+            [&](int t, int2) {
+              return t * BQ < f ? 2 : (t >= qt0 && nval > 0) ? (nval < nkeys ? 2 : 1) : 0;
+            },
+            sList, lane);
+        if (lane == 0) {
+          sCount = n;
+          sFirst = f;
+        }
       }
+      __syncthreads();
+      nlist = __builtin_amdgcn_readfirstlane(sCount);
+      fv = __builtin_amdgcn_readfirstlane(sFirst);
     }
-    __syncthreads();
-    nlist = __builtin_amdgcn_readfirstlane(sCount);
-    fv = __builtin_amdgcn_readfirstlane(sFirst);
-  }
-  if constexpr (DOC) {
-    const int qt0 = k0 / BQ;  // the diagonal query tile: always listed, first
-    dkdv_stage_first<D>(st, qrot, dout, lse2, delta, drow, S, P, Hq, b, g * n_rep,
-                        qt0 * BQ, sQD[0], w, lane);
-    if (w == 0) {
-      const int n = doc_tile_list(drow, k0, min(k0 + BKV, S), ranges + (int64_t)b * (P / BN),
-                                  qt0, (S + BQ - 1) / BQ, sList, lane);
-      if (lane == 0) sCount = n;
+    if constexpr (DOC) {
+      const int qt0 = k0 / BQ;  // the diagonal query tile: always listed, first
+      dkdv_stage_first<D>(st, qrot, dout, lse2, delta, drow, S, P, Hq, b, g * n_rep,
+                          qt0 * BQ, sQD[0], w, lane);
+      if (w == 0) {
+        const int n = doc_tile_list(drow, k0, min(k0 + BKV, S), ranges + (int64_t)b * (P / BN),
+                                    qt0, (S + BQ - 1) / BQ, sList, lane);
+        if (lane == 0) sCount = n;
+      }
+      __syncthreads();
+      nlist = __builtin_amdgcn_readfirstlane(sCount);
     }
-    __syncthreads();
-    nlist = __builtin_amdgcn_readfirstlane(sCount);
+    if (w >= 4)
+      dkdv_role<D, true, MODE>(st, sP, krot, vn, qrot, dout, lse2, delta, cos, sin, dk, dv, S, P,
+                               Hq, Hkv, n_rep, b, g, bh, k0, w, lane, scale_log2, scale, causal,
+                               drow, sList, nlist, sQD, fv);
+    else
+      dkdv_role<D, false, MODE>(st, sP, krot, vn, qrot, dout, lse2, delta, cos, sin, dk, dv, S, P,
+                                Hq, Hkv, n_rep, b, g, bh, k0, w, lane, scale_log2, scale, causal,
+                                drow, sList, nlist, sQD, fv);
+    __syncthreads();  // LDS of this item is free for the next
   }
-  if (w >= 4)
-    dkdv_role<D, true, MODE>(st, sP, krot, vn, qrot, dout, lse2, delta, cos, sin, dk, dv, S, P,
-                             Hq, Hkv, n_rep, b, g, bh, k0, w, lane, scale_log2, scale, causal,
-                             drow, sList, nlist, sQD, fv);
-  else
-    dkdv_role<D, false, MODE>(st, sP, krot, vn, qrot, dout, lse2, delta, cos, sin, dk, dv, S, P,
-                              Hq, Hkv, n_rep, b, g, bh, k0, w, lane, scale_log2, scale, causal,
-                              drow, sList, nlist, sQD, fv);
 }
 
 // dQ workgroup: 8 wavefronts x 32 rows = 256 (query head, position) rows of one
@@ -432,8 +441,8 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_kernel(
     const bf16* __restrict__ qrot, const bf16* __restrict__ dout, const float* __restrict__ lse2,
     const float* __restrict__ delta, const bf16* __restrict__ krot, const bf16* __restrict__ vn,
     const float* __restrict__ cos, const float* __restrict__ sin, bf16* __restrict__ dq, int S,
-    int P, int Hq, int Hkv, int n_rep, int bm_pos, int nqb, float scale_log2, float scale,
-    int causal, const int32_t* __restrict__ aux, const int2* __restrict__ ranges) {
+    int P, int Hq, int Hkv, int n_rep, int bm_pos, int nqb, int nitems, float scale_log2,
+    float scale, int causal, const int32_t* __restrict__ aux, const int2* __restrict__ ranges) {
   constexpr bool DOC = MODE == MASK_DOC, KPM = MODE == MASK_KPM, LIST = DOC || KPM;
   constexpr int KS = D / 16, DT = D / 32, HALF = D / 2;
   constexpr int KR = D / 8;
@@ -446,200 +455,206 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_kernel(
   __shared__ int sCount, sFirst;
 
   const int tid = threadIdx.x, w = wave_id(), lane = tid & 63, hh = lane >> 5, c32 = lane & 31;
-  const int logical = xcd_logical_id(blockIdx.x, gridDim.x);
-  const RowInfo ri = row_info(logical, nqb, Hkv, n_rep, bm_pos, S, w * 32 + c32);
-  const int bh = ri.b * Hkv + ri.g;
-  const int64_t bhq = (int64_t)ri.b * Hq + ri.hq;
+  // persistent: one block of rows per round
+  const XcdItems xi = xcd_items(nitems);
+  for (int rnd = 0;; ++rnd) {
+    const int logical = xcd_item(xi, rnd);
+    if (logical < 0) break;
+    const RowInfo ri = row_info(logical, nqb, Hkv, n_rep, bm_pos, S, w * 32 + c32);
+    const int bh = ri.b * Hkv + ri.g;
+    const int64_t bhq = (int64_t)ri.b * Hq + ri.hq;
 
-  const int kend = causal ? min(S, ri.p0 + bm_pos) : S;
-  int ntiles = (kend + BN - 1) / BN;
-  const int32_t* drow = LIST ? aux + (int64_t)ri.b * S : nullptr;
-  const int2* rec = ranges + (int64_t)ri.b * (P / BN);
-  const bf16* kbase = krot + (int64_t)bh * P * D;
-  const bf16* vbase = vn + (int64_t)bh * P * D;
-  auto stage = [&](int t, int buf) {
-    tile_to_lds<BN, KR, 8>(kbase + (int64_t)t * BN * D, D, st[buf].k, w, lane);
-    tile_to_lds<BN, KR, 8>(vbase + (int64_t)t * BN * D, D, st[buf].v, w, lane);
-    if (LIST && w == 0) dma4(lds_addr(sKD[buf]), (uint32_t)min(t * BN + lane, S - 1) * 4u, drow);
-  };
-  int di = 0;        // DOC: this row's document
-  bool grd = false;  // KPM: this row is guarded (before the first valid key)
-  if constexpr (DOC) {
-    // walked backwards, as in the forward: the always-listed last tile loads
-    // while the list is built
-    if (ntiles > 0) stage(ntiles - 1, 0);
-    di = drow[min(ri.pos, S - 1)];
-    if (w == 0) {
-      const int n = doc_tile_list(drow, ri.p0, min(ri.p0 + bm_pos, S), rec, 0, ntiles, sList,
-                                  lane);
-      if (lane == 0) sCount = n;
-    }
-    __syncthreads();
-    ntiles = __builtin_amdgcn_readfirstlane(sCount);
-  } else if constexpr (KPM) {
-    const int nall = (S + BN - 1) / BN;
-    if (w == 0) {
-      const int f = kpm_first_valid(rec, P / BN, lane);
-      const bool guard_block = ri.p0 < f;  // a guarded row needs every key tile
-      const int n = kpm_tile_list(rec, 0, guard_block ? nall : ntiles,
-                                  [&](int, int2 r) { return guard_block ? 2 : r.x == 0 ? 0 : r.x < BN ? 2 : 1; },
-                                  sList, lane);
-      if (lane == 0) {
-        sCount = n;
-        sFirst = f;
+    const int kend = causal ? min(S, ri.p0 + bm_pos) : S;
+    int ntiles = (kend + BN - 1) / BN;
+    const int32_t* drow = LIST ? aux + (int64_t)ri.b * S : nullptr;
+    const int2* rec = ranges + (int64_t)ri.b * (P / BN);
+    const bf16* kbase = krot + (int64_t)bh * P * D;
+    const bf16* vbase = vn + (int64_t)bh * P * D;
+    auto stage = [&](int t, int buf) {
+      tile_to_lds<BN, KR, 8>(kbase + (int64_t)t * BN * D, D, st[buf].k, w, lane);
+      tile_to_lds<BN, KR, 8>(vbase + (int64_t)t * BN * D, D, st[buf].v, w, lane);
+      if (LIST && w == 0) dma4(lds_addr(sKD[buf]), (uint32_t)min(t * BN + lane, S - 1) * 4u, drow);
+    };
+    int di = 0;        // DOC: this row's document
+    bool grd = false;  // KPM: this row is guarded (before the first valid key)
+    if constexpr (DOC) {
+      // walked backwards, as in the forward: the always-listed last tile loads
+      // while the list is built
+      if (ntiles > 0) stage(ntiles - 1, 0);
+      di = drow[min(ri.pos, S - 1)];
+      if (w == 0) {
+        const int n = doc_tile_list(drow, ri.p0, min(ri.p0 + bm_pos, S), rec, 0, ntiles, sList,
+                                    lane);
+        if (lane == 0) sCount = n;
       }
+      __syncthreads();
+      ntiles = __builtin_amdgcn_readfirstlane(sCount);
+    } else if constexpr (KPM) {
+      const int nall = (S + BN - 1) / BN;
+      if (w == 0) {
+        const int f = kpm_first_valid(rec, P / BN, lane);
+        const bool guard_block = ri.p0 < f;  // a guarded row needs every key tile
+        const int n = kpm_tile_list(rec, 0, guard_block ? nall : ntiles,
+                                    [&](int, int2 r) { return guard_block ? 2 : r.x == 0 ? 0 : r.x < BN ? 2 : 1; },
+                                    sList, lane);
+        if (lane == 0) {
+          sCount = n;
+          sFirst = f;
+        }
+      }
+      __syncthreads();
+      ntiles = __builtin_amdgcn_readfirstlane(sCount);
+      grd = ri.pos < sFirst;
+    } else {
+      if (ntiles > 0) stage(0, 0);
     }
-    __syncthreads();
-    ntiles = __builtin_amdgcn_readfirstlane(sCount);
-    grd = ri.pos < sFirst;
-  } else {
-    if (ntiles > 0) stage(0, 0);
-  }
-  auto entry = [&](int it) -> int {
-    return DOC ? __builtin_amdgcn_readfirstlane((int)sList[ntiles - 1 - it])
-               : KPM ? __builtin_amdgcn_readfirstlane((int)sList[it]) : it;
-  };
-  auto tile_of = [](int e) -> int { return LIST ? e & ~DOC_MASK_FLAG : e; };
-  if (KPM && ntiles > 0) stage(tile_of(entry(0)), 0);
+    auto entry = [&](int it) -> int {
+      return DOC ? __builtin_amdgcn_readfirstlane((int)sList[ntiles - 1 - it])
+                 : KPM ? __builtin_amdgcn_readfirstlane((int)sList[it]) : it;
+    };
+    auto tile_of = [](int e) -> int { return LIST ? e & ~DOC_MASK_FLAG : e; };
+    if (KPM && ntiles > 0) stage(tile_of(entry(0)), 0);
 
-  bf16x8 qf[KS], df[KS];
-  float l2 = INFINITY, dl = 0.f;
-  if (ri.q_valid) {
-    const bf16* qr = qrot + (bhq * P + ri.pos) * D + 8 * hh;
-    const bf16* dr = dout + (((int64_t)ri.b * S + ri.pos) * Hq + ri.hq) * D + 8 * hh;
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      qf[ks] = as_bf16x8(*(const u32x4*)(qr + 16 * ks));
-      df[ks] = as_bf16x8(*(const u32x4*)(dr + 16 * ks));
+    bf16x8 qf[KS], df[KS];
+    float l2 = INFINITY, dl = 0.f;
+    if (ri.q_valid) {
+      const bf16* qr = qrot + (bhq * P + ri.pos) * D + 8 * hh;
+      const bf16* dr = dout + (((int64_t)ri.b * S + ri.pos) * Hq + ri.hq) * D + 8 * hh;
+  #pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        qf[ks] = as_bf16x8(*(const u32x4*)(qr + 16 * ks));
+        df[ks] = as_bf16x8(*(const u32x4*)(dr + 16 * ks));
+      }
+      l2 = lse2[bhq * P + ri.pos];
+      dl = delta[bhq * P + ri.pos];
+    } else {
+  #pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        qf[ks] = as_bf16x8(u32x4{0u, 0u, 0u, 0u});
+        df[ks] = qf[ks];
+      }
     }
-    l2 = lse2[bhq * P + ri.pos];
-    dl = delta[bhq * P + ri.pos];
-  } else {
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      qf[ks] = as_bf16x8(u32x4{0u, 0u, 0u, 0u});
-      df[ks] = qf[ks];
-    }
-  }
 
-  f32x16 acc[DT];
-#pragma unroll
-  for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-    for (int i = 0; i < 16; ++i) acc[dt][i] = 0.f;
-  const TrOffsets<D> tro = tr_offsets<D>(lane);
+    f32x16 acc[DT];
+  #pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+  #pragma unroll
+      for (int i = 0; i < 16; ++i) acc[dt][i] = 0.f;
+    const TrOffsets<D> tro = tr_offsets<D>(lane);
 
-  lds_copy_wait();
-  __syncthreads();
-#pragma unroll
-  for (int ks = 0; ks < KS; ++ks) {
-    settle(qf[ks]);
-    settle(df[ks]);
-  }
-  settle(l2);
-  settle(dl);
-  for (int it = 0; it < ntiles; ++it) {
-    const int buf = it & 1;
-    const int e = entry(it);
-    const int t = tile_of(e);
-    if (it + 1 < ntiles) stage(tile_of(entry(it + 1)), buf ^ 1);
-    const Stage& S_ = st[buf];
-    const int k0 = t * BN;
-    const bool dmask = LIST && (e & DOC_MASK_FLAG);
-    const bool need_mask = (causal && k0 + BN - 1 > ri.p0) || (k0 + BN > S) || dmask;
-    // last visible key of this lane's row, relative to k0 (a guarded row: any below S)
-    const int lim = (causal && !grd ? min(ri.pos, S - 1) : S - 1) - k0;
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
-      f32x16 s, dp;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        s[i] = 0.f;
-        dp[i] = 0.f;
-      }
-      {
-        // fragment reads run PF steps ahead of the MFMAs that consume them
-        constexpr int PF = 2;
-        bf16x8 fk[KS], fv[KS];
-#pragma unroll
-        for (int ks = 0; ks < PF; ++ks) {
-          fk[ks] = lds_frag<KR>(S_.k, 32 * mt + c32, 2 * ks + hh);
-          fv[ks] = lds_frag<KR>(S_.v, 32 * mt + c32, 2 * ks + hh);
-        }
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-          __builtin_amdgcn_sched_barrier(0);
-          if (ks + PF < KS) {
-            fk[ks + PF] = lds_frag<KR>(S_.k, 32 * mt + c32, 2 * (ks + PF) + hh);
-            fv[ks + PF] = lds_frag<KR>(S_.v, 32 * mt + c32, 2 * (ks + PF) + hh);
-          }
-          s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fk[ks], qf[ks], s, 0, 0, 0);
-          dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fv[ks], df[ks], dp, 0, 0, 0);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-      }
-      u32x4 dsk[2];
-#pragma unroll
-      for (int i = 0; i < 16; i += 2) {
-        float dsv[2];
-        // DOC: documents of this pair's two keys (adjacent: i even)
-        int kd[2] = {0, 0};
-        if (dmask) {
-          const int local0 = 32 * mt + 8 * (i >> 2) + 4 * hh + (i & 3);
-          kd[0] = sKD[buf][local0];
-          kd[1] = sKD[buf][local0 + 1];
-        }
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          float p = fast_exp2(__builtin_fmaf(s[i + j], scale_log2, -l2));
-          if (need_mask) {
-            const int local = 32 * mt + 8 * ((i + j) >> 2) + 4 * hh + ((i + j) & 3);
-            p = local > lim ? 0.f : p;
-            if (DOC && dmask) p = kd[j] != di ? 0.f : p;
-            if (KPM && dmask && !grd) p = kd[j] == 0 ? 0.f : p;
-          }
-          dsv[j] = p * (dp[i + j] - dl);
-        }
-        dsk[i >> 3][(i & 7) >> 1] = pack2(dsv[0], dsv[1]);
-      }
-      {
-        constexpr int NS = 2 * DT, PF = 1;
-        bf16x8 fa[NS];
-#pragma unroll
-        for (int n = 0; n < PF; ++n)
-          fa[n] = lds_frag_t<D>(S_.k, tro, 2 * mt + n / DT, n % DT);
-#pragma unroll
-        for (int n = 0; n < NS; ++n) {
-          __builtin_amdgcn_sched_barrier(0);
-          if (n + PF < NS)
-            fa[n + PF] = lds_frag_t<D>(S_.k, tro, 2 * mt + (n + PF) / DT, (n + PF) % DT);
-          acc[n % DT] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[n], as_bf16x8(dsk[n / DT]),
-                                                               acc[n % DT], 0, 0, 0);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-      }
-    }
     lds_copy_wait();
     __syncthreads();
-  }
-
-  if (ri.q_valid) {
-    bf16* dqr = dq + (((int64_t)ri.b * S + ri.pos) * Hq + ri.hq) * D;
-    const float* cr = cos + (int64_t)ri.pos * HALF;
-    const float* sr = sin + (int64_t)ri.pos * HALF;
-#pragma unroll
-    for (int dt = 0; dt < DT / 2; ++dt)
-#pragma unroll
-      for (int gi = 0; gi < 4; ++gi) {
-        const int d = 32 * dt + 8 * gi + 4 * hh;
-        float lo[4], hi[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          rope_pair_bwd<bf16>(acc[dt][4 * gi + e] * scale, acc[dt + DT / 2][4 * gi + e] * scale,
-                              cr[d + e], sr[d + e], lo[e], hi[e]);
-        *(u32x2*)(dqr + d) = u32x2{pack2(lo[0], lo[1]), pack2(lo[2], lo[3])};
-        *(u32x2*)(dqr + d + HALF) = u32x2{pack2(hi[0], hi[1]), pack2(hi[2], hi[3])};
+  #pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      settle(qf[ks]);
+      settle(df[ks]);
+    }
+    settle(l2);
+    settle(dl);
+    for (int it = 0; it < ntiles; ++it) {
+      const int buf = it & 1;
+      const int e = entry(it);
+      const int t = tile_of(e);
+      if (it + 1 < ntiles) stage(tile_of(entry(it + 1)), buf ^ 1);
+      const Stage& S_ = st[buf];
+      const int k0 = t * BN;
+      const bool dmask = LIST && (e & DOC_MASK_FLAG);
+      const bool need_mask = (causal && k0 + BN - 1 > ri.p0) || (k0 + BN > S) || dmask;
+      // last visible key of this lane's row, relative to k0 (a guarded row: any below S)
+      const int lim = (causal && !grd ? min(ri.pos, S - 1) : S - 1) - k0;
+  #pragma unroll
+      for (int mt = 0; mt < 2; ++mt) {
+        f32x16 s, dp;
+  #pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          s[i] = 0.f;
+          dp[i] = 0.f;
+        }
+        {
+          // fragment reads run PF steps ahead of the MFMAs that consume them
+          constexpr int PF = 2;
+          bf16x8 fk[KS], fv[KS];
+  #pragma unroll
+          for (int ks = 0; ks < PF; ++ks) {
+            fk[ks] = lds_frag<KR>(S_.k, 32 * mt + c32, 2 * ks + hh);
+            fv[ks] = lds_frag<KR>(S_.v, 32 * mt + c32, 2 * ks + hh);
+          }
+  #pragma unroll
+          for (int ks = 0; ks < KS; ++ks) {
+            __builtin_amdgcn_sched_barrier(0);
+            if (ks + PF < KS) {
+              fk[ks + PF] = lds_frag<KR>(S_.k, 32 * mt + c32, 2 * (ks + PF) + hh);
+              fv[ks + PF] = lds_frag<KR>(S_.v, 32 * mt + c32, 2 * (ks + PF) + hh);
+            }
+            s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fk[ks], qf[ks], s, 0, 0, 0);
+            dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fv[ks], df[ks], dp, 0, 0, 0);
+          }
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        u32x4 dsk[2];
+  #pragma unroll
+        for (int i = 0; i < 16; i += 2) {
+          float dsv[2];
+          // DOC: documents of this pair's two keys (adjacent: i even)
+          int kd[2] = {0, 0};
+          if (dmask) {
+            const int local0 = 32 * mt + 8 * (i >> 2) + 4 * hh + (i & 3);
+            kd[0] = sKD[buf][local0];
+            kd[1] = sKD[buf][local0 + 1];
+          }
+  #pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            float p = fast_exp2(__builtin_fmaf(s[i + j], scale_log2, -l2));
+            if (need_mask) {
+              const int local = 32 * mt + 8 * ((i + j) >> 2) + 4 * hh + ((i + j) & 3);
+              p = local > lim ? 0.f : p;
+              if (DOC && dmask) p = kd[j] != di ? 0.f : p;
+              if (KPM && dmask && !grd) p = kd[j] == 0 ? 0.f : p;
+            }
+            dsv[j] = p * (dp[i + j] - dl);
+          }
+          dsk[i >> 3][(i & 7) >> 1] = pack2(dsv[0], dsv[1]);
+        }
+        {
+          constexpr int NS = 2 * DT, PF = 1;
+          bf16x8 fa[NS];
+  #pragma unroll
+          for (int n = 0; n < PF; ++n)
+            fa[n] = lds_frag_t<D>(S_.k, tro, 2 * mt + n / DT, n % DT);
+  #pragma unroll
+          for (int n = 0; n < NS; ++n) {
+            __builtin_amdgcn_sched_barrier(0);
+            if (n + PF < NS)
+              fa[n + PF] = lds_frag_t<D>(S_.k, tro, 2 * mt + (n + PF) / DT, (n + PF) % DT);
+            acc[n % DT] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[n], as_bf16x8(dsk[n / DT]),
+                                                                 acc[n % DT], 0, 0, 0);
+          }
+          __builtin_amdgcn_sched_barrier(0);
+        }
       }
+      lds_copy_wait();
+      __syncthreads();
+    }
+
+    if (ri.q_valid) {
+      bf16* dqr = dq + (((int64_t)ri.b * S + ri.pos) * Hq + ri.hq) * D;
+      const float* cr = cos + (int64_t)ri.pos * HALF;
+      const float* sr = sin + (int64_t)ri.pos * HALF;
+  #pragma unroll
+      for (int dt = 0; dt < DT / 2; ++dt)
+  #pragma unroll
+        for (int gi = 0; gi < 4; ++gi) {
+          const int d = 32 * dt + 8 * gi + 4 * hh;
+          float lo[4], hi[4];
+  #pragma unroll
+          for (int e = 0; e < 4; ++e)
+            rope_pair_bwd<bf16>(acc[dt][4 * gi + e] * scale, acc[dt + DT / 2][4 * gi + e] * scale,
+                                cr[d + e], sr[d + e], lo[e], hi[e]);
+          *(u32x2*)(dqr + d) = u32x2{pack2(lo[0], lo[1]), pack2(lo[2], lo[3])};
+          *(u32x2*)(dqr + d + HALF) = u32x2{pack2(hi[0], hi[1]), pack2(hi[2], hi[3])};
+        }
+    }
+    __syncthreads();  // LDS of this item is free for the next
   }
 }
 
@@ -685,14 +700,17 @@ int launch_bwd(const BwdArgs& a, void* workspace) {
             w.qrot, w.lse2, w.delta, a.S, P, a.Hq);
   KF_CHECK_LAUNCH();
   const int nkb = P / BKV;
+  // persistent grids: one workgroup per CU (a multiple of 8, one share per XCD)
+  const int grid_cap = device_cu_count() / 8 * 8;
   const int mode = a.doc ? MASK_DOC : a.kvalid ? MASK_KPM : MASK_NONE;
   const int32_t* aux = a.doc ? a.doc : a.kvalid;
   KF_LAUNCH("bwd_dkdv",
             (mode == MASK_DOC   ? bwd_dkdv_kernel<D, MASK_DOC>
              : mode == MASK_KPM ? bwd_dkdv_kernel<D, MASK_KPM>
                                 : bwd_dkdv_kernel<D, MASK_NONE>),
-            dim3(nkb * a.B * a.Hkv), dim3(512), 0, a.stream, w.krot, w.vn, w.qrot, (const bf16*)a.dout, w.lse2,
-            w.delta, a.cos, a.sin, (bf16*)a.dk, (bf16*)a.dv, a.S, P, a.Hq, a.Hkv, n_rep, nkb,
+            dim3(std::min(nkb * a.B * a.Hkv, grid_cap)), dim3(512), 0, a.stream, w.krot, w.vn,
+            w.qrot, (const bf16*)a.dout, w.lse2, w.delta, a.cos, a.sin, (bf16*)a.dk,
+            (bf16*)a.dv, a.S, P, a.Hq, a.Hkv, n_rep, nkb, nkb * a.B * a.Hkv,
             scale_log2, a.scale, a.causal, aux, w.ranges);
   KF_CHECK_LAUNCH();
   const int bm_pos = DQ_ROWS / n_rep;
@@ -701,9 +719,10 @@ int launch_bwd(const BwdArgs& a, void* workspace) {
             (mode == MASK_DOC   ? bwd_dq_kernel<D, MASK_DOC>
              : mode == MASK_KPM ? bwd_dq_kernel<D, MASK_KPM>
                                 : bwd_dq_kernel<D, MASK_NONE>),
-            dim3(nqb * a.B * a.Hkv), dim3(512), 0, a.stream, w.qrot, (const bf16*)a.dout, w.lse2, w.delta,
-            w.krot, w.vn, a.cos, a.sin, (bf16*)a.dq, a.S, P, a.Hq, a.Hkv, n_rep, bm_pos, nqb,
-            scale_log2, a.scale, a.causal, aux, w.ranges);
+            dim3(std::min(nqb * a.B * a.Hkv, grid_cap)), dim3(512), 0, a.stream, w.qrot,
+            (const bf16*)a.dout, w.lse2, w.delta, w.krot, w.vn, a.cos, a.sin, (bf16*)a.dq, a.S, P,
+            a.Hq, a.Hkv, n_rep, bm_pos, nqb, nqb * a.B * a.Hkv, scale_log2, a.scale, a.causal,
+            aux, w.ranges);
   KF_CHECK_LAUNCH();
   return KF_OK;
 }

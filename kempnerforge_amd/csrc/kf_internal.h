@@ -61,6 +61,8 @@ bool fwd_mfma_supported(const FwdArgs& a);
 // order 0-3, 8-11, 4-7, 12-15 (what the forward kernel reads).  With a.doc also
 // the [min, max] document id of each 64-key tile, [B][Skp/64] (a.kvalid: valid
 // count and first valid key).
+// Compute units of the current device (cached per device), to size persistent grids.
+int device_cu_count();
 int launch_kv_prep(const FwdArgs& a, void* krot, void* vn, int Skp, int2* ranges,
                    int v_transposed = 0);
 size_t fwd_mfma_workspace(int B, int Sk, int Hkv, int D);

@@ -22,6 +22,26 @@ __device__ __forceinline__ int xcd_logical_id(int L, int nblk) {
   return xcd * per + min(xcd, rem) + idx;
 }
 
+// Persistent schedule over nitems work items, numbered as xcd_logical_id numbers
+// workgroups (XCD x owns a contiguous range of them).  With G workgroups per
+// XCD (grid = 8G, or grid = nitems for one item each), round r gives the
+// workgroup of in-XCD index wi the item r*G + wi of its XCD's range in even
+// rounds and r*G + G-1-wi in odd ones: with items ordered longest first, each
+// workgroup's rounds pair long items with short ones, so the shares balance.
+struct XcdItems {
+  int lo, cnt, G, wi;
+};
+__device__ __forceinline__ XcdItems xcd_items(int nitems) {
+  const int per = nitems / 8, rem = nitems % 8, xcd = blockIdx.x % 8;
+  return XcdItems{xcd * per + min(xcd, rem), per + (xcd < rem ? 1 : 0),
+                  (int)(gridDim.x + 7) / 8, (int)blockIdx.x / 8};
+}
+// logical item of round r, or -1 when this workgroup is done
+__device__ __forceinline__ int xcd_item(const XcdItems& x, int r) {
+  const int j = r * x.G + ((r & 1) ? x.G - 1 - x.wi : x.wi);
+  return j < x.cnt ? x.lo + j : -1;
+}
+
 struct RowInfo {
   int b, g, hq, pos, p0;
   bool q_valid;
