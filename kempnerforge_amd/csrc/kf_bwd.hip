@@ -520,7 +520,7 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_kernel(
     if (ri.q_valid) {
       const bf16* qr = qrot + (bhq * P + ri.pos) * D + 8 * hh;
       const bf16* dr = dout + (((int64_t)ri.b * S + ri.pos) * Hq + ri.hq) * D + 8 * hh;
-  #pragma unroll
+#pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
         qf[ks] = as_bf16x8(*(const u32x4*)(qr + 16 * ks));
         df[ks] = as_bf16x8(*(const u32x4*)(dr + 16 * ks));
@@ -528,7 +528,7 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_kernel(
       l2 = lse2[bhq * P + ri.pos];
       dl = delta[bhq * P + ri.pos];
     } else {
-  #pragma unroll
+#pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
         qf[ks] = as_bf16x8(u32x4{0u, 0u, 0u, 0u});
         df[ks] = qf[ks];
@@ -536,15 +536,15 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_kernel(
     }
 
     f32x16 acc[DT];
-  #pragma unroll
+#pragma unroll
     for (int dt = 0; dt < DT; ++dt)
-  #pragma unroll
+#pragma unroll
       for (int i = 0; i < 16; ++i) acc[dt][i] = 0.f;
     const TrOffsets<D> tro = tr_offsets<D>(lane);
 
     lds_copy_wait();
     __syncthreads();
-  #pragma unroll
+#pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       settle(qf[ks]);
       settle(df[ks]);
@@ -562,10 +562,10 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_kernel(
       const bool need_mask = (causal && k0 + BN - 1 > ri.p0) || (k0 + BN > S) || dmask;
       // last visible key of this lane's row, relative to k0 (a guarded row: any below S)
       const int lim = (causal && !grd ? min(ri.pos, S - 1) : S - 1) - k0;
-  #pragma unroll
+#pragma unroll
       for (int mt = 0; mt < 2; ++mt) {
         f32x16 s, dp;
-  #pragma unroll
+#pragma unroll
         for (int i = 0; i < 16; ++i) {
           s[i] = 0.f;
           dp[i] = 0.f;
@@ -574,12 +574,12 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_kernel(
           // fragment reads run PF steps ahead of the MFMAs that consume them
           constexpr int PF = 2;
           bf16x8 fk[KS], fv[KS];
-  #pragma unroll
+#pragma unroll
           for (int ks = 0; ks < PF; ++ks) {
             fk[ks] = lds_frag<KR>(S_.k, 32 * mt + c32, 2 * ks + hh);
             fv[ks] = lds_frag<KR>(S_.v, 32 * mt + c32, 2 * ks + hh);
           }
-  #pragma unroll
+#pragma unroll
           for (int ks = 0; ks < KS; ++ks) {
             __builtin_amdgcn_sched_barrier(0);
             if (ks + PF < KS) {
@@ -592,7 +592,7 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_kernel(
           __builtin_amdgcn_sched_barrier(0);
         }
         u32x4 dsk[2];
-  #pragma unroll
+#pragma unroll
         for (int i = 0; i < 16; i += 2) {
           float dsv[2];
           // DOC: documents of this pair's two keys (adjacent: i even)
@@ -602,7 +602,7 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_kernel(
             kd[0] = sKD[buf][local0];
             kd[1] = sKD[buf][local0 + 1];
           }
-  #pragma unroll
+#pragma unroll
           for (int j = 0; j < 2; ++j) {
             float p = fast_exp2(__builtin_fmaf(s[i + j], scale_log2, -l2));
             if (need_mask) {
@@ -618,10 +618,10 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_kernel(
         {
           constexpr int NS = 2 * DT, PF = 1;
           bf16x8 fa[NS];
-  #pragma unroll
+#pragma unroll
           for (int n = 0; n < PF; ++n)
             fa[n] = lds_frag_t<D>(S_.k, tro, 2 * mt + n / DT, n % DT);
-  #pragma unroll
+#pragma unroll
           for (int n = 0; n < NS; ++n) {
             __builtin_amdgcn_sched_barrier(0);
             if (n + PF < NS)
@@ -640,13 +640,13 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_kernel(
       bf16* dqr = dq + (((int64_t)ri.b * S + ri.pos) * Hq + ri.hq) * D;
       const float* cr = cos + (int64_t)ri.pos * HALF;
       const float* sr = sin + (int64_t)ri.pos * HALF;
-  #pragma unroll
+#pragma unroll
       for (int dt = 0; dt < DT / 2; ++dt)
-  #pragma unroll
+#pragma unroll
         for (int gi = 0; gi < 4; ++gi) {
           const int d = 32 * dt + 8 * gi + 4 * hh;
           float lo[4], hi[4];
-  #pragma unroll
+#pragma unroll
           for (int e = 0; e < 4; ++e)
             rope_pair_bwd<bf16>(acc[dt][4 * gi + e] * scale, acc[dt + DT / 2][4 * gi + e] * scale,
                                 cr[d + e], sr[d + e], lo[e], hi[e]);
