@@ -700,8 +700,10 @@ int launch_bwd(const BwdArgs& a, void* workspace) {
             w.qrot, w.lse2, w.delta, a.S, P, a.Hq);
   KF_CHECK_LAUNCH();
   const int nkb = P / BKV;
-  // persistent grids: one workgroup per CU (a multiple of 8, one share per XCD)
-  const int grid_cap = device_cu_count() / 8 * 8;
+  // persistent grids: one workgroup per CU (a multiple of 8, one share per XCD).
+  // With an explicit mask the items' lengths no longer fall in launch order, so
+  // the zigzag shares would not balance: one workgroup per item there.
+  const int grid_cap = a.doc || a.kvalid ? INT_MAX : device_cu_count() / 8 * 8;
   const int mode = a.doc ? MASK_DOC : a.kvalid ? MASK_KPM : MASK_NONE;
   const int32_t* aux = a.doc ? a.doc : a.kvalid;
   KF_LAUNCH("bwd_dkdv",
