@@ -155,6 +155,27 @@ def main() -> int:
     c2 = {"config": "C2 llama3-8b fwd B=4 S=4096 Hq=32 Hkv=8 D=128", "ms": round(c2_s * 1e3, 4),
           "TFLOP/s": round(4.0 * D * P / c2_s / 1e12, 1)}
 
+    # C3 replayed from a HIP graph (the raw forward + backward calls captured
+    # once): the same kernels without per-launch host overhead or autograd
+    def raw_step():
+        o, l = ops.fwd_raw(qn_, kn_, vn_, cos, sin, causal=True, k_rotated=False)
+        return ops.bwd_raw(qn_, kn_, vn_, cos, sin, o, l, do, causal=True)
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            raw_step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        raw_step()
+    c3g_s = wall(graph.replay, args.warmup, args.steps)
+    c3_graph = {"config": "C3 step as one HIP graph replay (fwd_raw + bwd_raw)",
+                "ms": round(c3g_s * 1e3, 4), "TFLOP/s": round(flops_step / c3g_s / 1e12, 1)}
+    del graph
+
     # C3-doc: the C3 step on packed sequences (documents of 64..2048 tokens, seeded);
     # flops count only same-document causal pairs, so the rate compares with C3's
     g = torch.Generator().manual_seed(7)
@@ -284,6 +305,7 @@ def main() -> int:
         "kernels_us": {n: round(s["avg_us"], 1) for n, s in kstats.items()},
         "fwd_tflops": round(4.0 * D * P / (fwd_us * 1e-6) / 1e12, 1) if fwd_us else None,
         "c2_fwd": c2,
+        "c3_graph": c3_graph,
         "c3_doc": c3doc,
         "c5": c5,
         "c5_cap": c5cap,
