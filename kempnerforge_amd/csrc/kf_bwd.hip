@@ -79,14 +79,26 @@ __global__ __launch_bounds__(256) void q_prep_bwd_kernel(
   }
   // Delta (TPR consecutive lanes own one row); dO itself is read in place by
   // the dK/dV and dQ kernels
-  for (int it = tid; it < BN * TPR; it += 256) {
+  // all of a thread's dO and O loads are issued before the first reduction
+  constexpr int NIT = BN * TPR / 256;
+  u32x4 ad[NIT], ao[NIT];
+#pragma unroll
+  for (int k = 0; k < NIT; ++k) {
+    const int it = tid + 256 * k;
+    const int row = it / TPR, c = it % TPR, s = s0 + row;
+    const int64_t off = (((int64_t)b * S + min(s, S - 1)) * Hq + h) * D + 8 * c;
+    ad[k] = *(const u32x4*)(dout + off);
+    ao[k] = *(const u32x4*)(out + off);
+  }
+#pragma unroll
+  for (int k = 0; k < NIT; ++k) {
+    const int it = tid + 256 * k;
     const int row = it / TPR, c = it % TPR, s = s0 + row;
     float part = 0.f;
     if (s < S) {
-      const int64_t off = (((int64_t)b * S + s) * Hq + h) * D + 8 * c;
       float fd[8], fo[8];
-      unpack8(*(const u32x4*)(dout + off), fd);
-      unpack8(*(const u32x4*)(out + off), fo);
+      unpack8(ad[k], fd);
+      unpack8(ao[k], fo);
 #pragma unroll
       for (int j = 0; j < 8; ++j) part += fd[j] * fo[j];
     }
