@@ -18,9 +18,12 @@
 //               layout with one key per lane; P and dS then feed dV^T += dO^T P
 //               and dK^T += Q^T dS as B operands directly.  RoPE backward and the
 //               softmax scale are applied at the dK store.
-//  dq           forward-shaped: 128 (head, position) rows per workgroup sharing
+//  dq           forward-shaped: 256 (head, position) rows per workgroup sharing
 //               each K/V tile; S^T = K Q^T, dP^T = V dO^T, dQ^T += K^T dS^T.
 //               RoPE backward is applied at the dQ store.
+//  Without an explicit mask both run persistent, one workgroup per CU walking
+//  its XCD's items in the zigzag order of xcd_item (long causal items paired
+//  with short ones).
 // The algorithm is the standard flash-attention backward (recompute P from the
 // saved log-sum-exp; dS = P o (dP - Delta)).
 //
