@@ -125,7 +125,8 @@ def main() -> int:
     kstats = {n: {"avg_us": t / c * 1e3, "launches": c} for n, (t, c) in kt.stats.items()}
     # algorithmic flops per launch of each MFMA kernel (the backward's 10*D*P is
     # 4*D*P of recomputed S and dP plus dV, dK -> dkdv kernel 8*D*P; dQ 2*D*P)
-    algo = {"fwd_mfma": 4.0 * D * P, "bwd_dkdv": 8.0 * D * P, "bwd_dq": 2.0 * D * P}
+    algo = {"fwd_mfma": 4.0 * D * P, "bwd_dkdv": 8.0 * D * P, "bwd_dq": 2.0 * D * P,
+            "bwd_dq_ds": 2.0 * D * P}
     dom = max(kstats, key=lambda n: kstats[n]["avg_us"] * kstats[n]["launches"])
     traffic = measured_traffic()
     roof = None

@@ -87,6 +87,17 @@ int kf_attn_fwd(const void* q, const void* k, const void* v, const float* rope_c
 /* Workspace bytes kf_attn_bwd needs. */
 int kf_attn_bwd_workspace_size(int B, int S, int Hq, int Hkv, int D, int dtype, size_t* bytes);
 
+/* Workspace bytes with which kf_attn_bwd keeps the bf16 dS tiles of the dK/dV
+ * pass for dQ instead of recomputing S and dP (one fewer pass over the
+ * attention matrix; B*Hq*P*(P+64) bytes extra for causal, 2*B*Hq*P*P for full
+ * attention, P = S rounded up to 128).  Applies to the bf16 kernels without
+ * doc_ids / key_valid and up to 32 GiB of tiles; otherwise this equals
+ * kf_attn_bwd_workspace_size.  kf_attn_bwd takes the faster path whenever
+ * workspace_bytes reaches this size.  No counterpart in the reference (its
+ * SDPA backward manages its own memory). */
+int kf_attn_bwd_workspace_size_ds(int B, int S, int Hq, int Hkv, int D, int dtype, int causal,
+                                  size_t* bytes);
+
 /* Backward of kf_attn_fwd (k_rotated = 0, Sq == Sk == S, contiguous BSHD).
  *
  * Replaces the autograd backward the reference gets from

@@ -26,6 +26,7 @@ SIGNATURES = {
     "kf_attn_fwd": ([_vp, _vp, _vp, _fp, _fp, _vp, _fp, _vp, _c_sz] + [_c_int] * 6
                     + [_c_i64] * 6 + [_c_int] * 2 + [_vp, _vp, _c_int, _vp], _c_int),
     "kf_attn_bwd_workspace_size": ([_c_int] * 6 + [_szp], _c_int),
+    "kf_attn_bwd_workspace_size_ds": ([_c_int] * 7 + [_szp], _c_int),
     "kf_attn_bwd": ([_vp, _vp, _vp, _fp, _fp, _vp, _fp, _vp, _vp, _vp, _vp, _vp, _c_sz]
                     + [_c_int] * 6 + [_vp, _vp, _c_int, _vp], _c_int),
     "kf_attn_decode_workspace_size": ([_c_int] * 6 + [_szp], _c_int),

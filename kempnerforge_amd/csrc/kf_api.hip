@@ -124,17 +124,35 @@ int kf_attn_fwd(const void* q, const void* k, const void* v, const float* rope_c
   return fwd_generic(a);
 }
 
+namespace {
+// Sizing stand-in for a backward call: aligned non-null pointers, no masks.
+kf::BwdArgs sizing_args(int B, int S, int Hq, int Hkv, int D, int dtype, int causal) {
+  kf::BwdArgs a{};
+  a.B = B; a.S = S; a.Hq = Hq; a.Hkv = Hkv; a.D = D; a.dtype = dtype; a.causal = causal;
+  a.q = a.k = a.v = a.out = a.dout = (void*)16;
+  a.dq = a.dk = a.dv = (void*)16;
+  a.cos = a.sin = (float*)16;
+  return a;
+}
+}  // namespace
+
 int kf_attn_bwd_workspace_size(int B, int S, int Hq, int Hkv, int D, int dtype, size_t* bytes) {
   int rc = check_common(B, S, S, Hq, Hkv, D, dtype);
   if (rc) return rc;
   KF_CHECK_ARG(bytes != nullptr, "bytes is null");
-  BwdArgs a{};
-  a.B = B; a.S = S; a.Hq = Hq; a.Hkv = Hkv; a.D = D; a.dtype = dtype; a.causal = 1;
-  a.q = a.k = a.v = a.out = a.dout = (void*)16;
-  a.dq = a.dk = a.dv = (void*)16;
-  a.cos = a.sin = (float*)16;
+  const BwdArgs a = sizing_args(B, S, Hq, Hkv, D, dtype, 1);
   *bytes = bwd_mfma_supported(a) ? bwd_mfma_workspace(B, S, Hq, Hkv, D)
                                  : bwd_generic_workspace(B, S, Hq);
+  return KF_OK;
+}
+
+int kf_attn_bwd_workspace_size_ds(int B, int S, int Hq, int Hkv, int D, int dtype, int causal,
+                                  size_t* bytes) {
+  int rc = check_common(B, S, S, Hq, Hkv, D, dtype);
+  if (rc) return rc;
+  KF_CHECK_ARG(bytes != nullptr, "bytes is null");
+  const BwdArgs a = sizing_args(B, S, Hq, Hkv, D, dtype, causal);
+  *bytes = bwd_mfma_supported(a) ? bwd_mfma_workspace_ds(a) : bwd_generic_workspace(B, S, Hq);
   return KF_OK;
 }
 
@@ -163,7 +181,7 @@ int kf_attn_bwd(const void* q, const void* k, const void* v, const float* rope_c
       set_error("workspace too small: need %zu bytes, got %zu", need, workspace_bytes);
       return KF_ERR_WORKSPACE;
     }
-    return bwd_mfma(a, workspace);
+    return bwd_mfma(a, workspace, workspace_bytes);
   }
   const size_t need = bwd_generic_workspace(B, S, Hq);
   if (workspace_bytes < need || !workspace) {

@@ -17,13 +17,18 @@
 //               accumulators.  S = Q K^T and dP = dO V^T land in the 32x32 C
 //               layout with one key per lane; P and dS then feed dV^T += dO^T P
 //               and dK^T += Q^T dS as B operands directly.  RoPE backward and the
-//               softmax scale are applied at the dK store.
-//  dq           forward-shaped: 256 (head, position) rows per workgroup sharing
-//               each K/V tile; S^T = K Q^T, dP^T = V dO^T, dQ^T += K^T dS^T.
-//               RoPE backward is applied at the dQ store.
-//  Without an explicit mask both run persistent, one workgroup per CU walking
-//  its XCD's items in the zigzag order of xcd_item (long causal items paired
-//  with short ones).
+//               softmax scale are applied at the dK store.  Without an explicit
+//               mask, and when the caller's workspace holds them, it also writes
+//               every dS tile (bf16) to a record for dQ.
+//  dq_ds        (dS records kept) dQ^T += K^T dS^T from the records: one
+//               product per element and one read of the dS bytes, HBM-bound.
+//  dq           (otherwise) forward-shaped: 256 (head, position) rows per
+//               workgroup sharing each K/V tile; recomputes S^T = K Q^T and
+//               dP^T = V dO^T, then dQ^T += K^T dS^T.
+//               Both apply RoPE backward at the dQ store.
+//  Without an explicit mask dkdv and dq run persistent, one workgroup per CU
+//  walking its XCD's items in the zigzag order of xcd_item (long causal items
+//  paired with short ones).
 // The algorithm is the standard flash-attention backward (recompute P from the
 // saved log-sum-exp; dS = P o (dP - Delta)).
 //
@@ -51,6 +56,23 @@ constexpr int BKV = 128;  // keys per dK/dV workgroup
 constexpr int BQ = 64;    // queries per dK/dV tile
 
 __host__ __device__ constexpr int pad_len(int S) { return (S + BKV - 1) / BKV * BKV; }
+
+// dS records.  Without an explicit mask the dK/dV kernel writes every dS tile
+// it computes, bf16, for the dQ kernel to read instead of recomputing S and dP.
+// A record is one dS wavefront's tile: DSQ query positions x DSK keys of one
+// query head, 4 KB, stored as that wavefront's four MFMA B operands exactly as
+// they sit in registers: [chunk c][lane][8 bf16], lane = 32*hh + key, slot
+// 4*half + j = row 16c + 8*half + 4*hh + j.  Records are ordered (KV head,
+// query tile, key column, query head of the group); with a causal mask only
+// the key columns k32 <= 2*qt + 1 that the tile's rows can see exist.
+constexpr int DSQ = 64;  // query positions per record (= BQ)
+constexpr int DSK = 32;  // keys per record (one dS wavefront)
+
+// record pair index of (KV head bh, query tile qt, key column k32); nqtp = P / DSQ
+__host__ __device__ inline int64_t ds_pair(int bh, int qt, int k32, int nqtp, int causal) {
+  return causal ? (int64_t)bh * nqtp * (nqtp + 1) + (int64_t)qt * (qt + 1) + k32
+                : ((int64_t)bh * nqtp + qt) * (2 * nqtp) + k32;
+}
 
 template <int D>
 __global__ __launch_bounds__(256) void q_prep_bwd_kernel(
@@ -134,7 +156,7 @@ struct DkdvStage {
 // MASK_KPM: qlist as above, drow the key-validity row, fv the first valid
 // key's position: query rows before it (guarded) see every key, other rows
 // need the key valid and not after them.
-template <int D, bool DSROLE, int MODE>
+template <int D, bool DSROLE, int MODE, bool STORE>
 __device__ __forceinline__ void dkdv_role(
     DkdvStage<D>* st, u32x4* sP, const bf16* __restrict__ krot, const bf16* __restrict__ vn,
     const bf16* __restrict__ qrot, const bf16* __restrict__ dout,
@@ -142,8 +164,10 @@ __device__ __forceinline__ void dkdv_role(
     const float* __restrict__ cos, const float* __restrict__ sin, bf16* __restrict__ dk,
     bf16* __restrict__ dv, int S, int P, int Hq, int Hkv, int n_rep, int b, int g, int bh, int k0,
     int w, int lane, float scale_log2, float scale, int causal, const int32_t* __restrict__ drow,
-    const uint16_t* qlist, int nlist, int32_t (*sQD)[BQ], int fv) {
+    const uint16_t* qlist, int nlist, int32_t (*sQD)[BQ], int fv, u32x4* __restrict__ dsb,
+    int nqtp) {
   constexpr bool DOC = MODE == MASK_DOC, KPM = MODE == MASK_KPM, LIST = DOC || KPM;
+  static_assert(!(STORE && LIST), "dS records are kept for unmasked launches only");
   constexpr int KS = D / 16, DT = D / 32, HALF = D / 2;
   constexpr int KR = D / 8;
   constexpr int PF = 3;  // fragment reads run PF MFMAs ahead
@@ -200,6 +224,17 @@ __device__ __forceinline__ void dkdv_role(
   u32x4* myP = sP + kw * 4 * 64 + lane;  // chunk c at myP[c * 64]
   const TrOffsets<D> tro = tr_offsets<D>(lane);
 
+  // STORE (dS waves): the dS tile of an iteration is written to its record at
+  // the start of the next one, so the stores have a whole iteration to
+  // complete before the end-of-iteration wait for the staging loads
+  u32x4 dsv[4];
+  u32x4* dsdst = nullptr;
+  auto put_ds = [&]() {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) __builtin_nontemporal_store(dsv[c], &dsdst[c * 64]);
+  };
+  const int k32 = k0 / DSK + kw;  // this wavefront's 32-key record column
+
   lds_copy_wait();
   __syncthreads();
 #pragma unroll
@@ -207,6 +242,10 @@ __device__ __forceinline__ void dkdv_role(
   for (int it = 0; it < total; ++it) {
     const int buf = it & 1;
     if (it + 1 < total) stage(it + 1, buf ^ 1);
+    if (STORE && DSROLE && dsdst != nullptr) {
+      put_ds();
+      dsdst = nullptr;
+    }
     const DkdvStage<D>& S_ = st[buf];
     const int e = entry(it);
     const int q0 = tile_of(e) * BQ;
@@ -300,6 +339,14 @@ __device__ __forceinline__ void dkdv_role(
             pk[2 * mt + cc][2 * half + 1] = pack2(v[2], v[3]);
           }
         }
+      if (STORE) {
+        const int qt = q0 / DSQ;
+        if (!causal || k32 <= 2 * qt + 1) {
+#pragma unroll
+          for (int c = 0; c < 4; ++c) dsv[c] = pk[c];
+          dsdst = dsb + (ds_pair(bh, qt, k32, nqtp, causal) * n_rep + it / per_head) * 256 + lane;
+        }
+      }
     }
     // phase 2: dV^T += dO^T P (P waves) or dK^T += Q^T dS (dS waves)
     {
@@ -321,6 +368,7 @@ __device__ __forceinline__ void dkdv_role(
     lds_copy_wait();
     __syncthreads();
   }
+  if (STORE && DSROLE && dsdst != nullptr) put_ds();
 
   if (key >= S) return;
   if (DSROLE) {
@@ -371,14 +419,15 @@ __device__ __forceinline__ void dkdv_stage_first(
   if (w == 2) dma4(lds_addr(sqd), (uint32_t)min(q0 + lane, S - 1) * 4u, drow);
 }
 
-template <int D, int MODE>
+template <int D, int MODE, bool STORE>
 __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(
     const bf16* __restrict__ krot, const bf16* __restrict__ vn, const bf16* __restrict__ qrot,
     const bf16* __restrict__ dout, const float* __restrict__ lse2, const float* __restrict__ delta,
     const float* __restrict__ cos, const float* __restrict__ sin, bf16* __restrict__ dk,
     bf16* __restrict__ dv, int S, int P, int Hq, int Hkv, int n_rep, int nkb, int nitems,
     float scale_log2,
-    float scale, int causal, const int32_t* __restrict__ aux, const int2* __restrict__ ranges) {
+    float scale, int causal, const int32_t* __restrict__ aux, const int2* __restrict__ ranges,
+    u32x4* __restrict__ dsb) {
   constexpr bool DOC = MODE == MASK_DOC, KPM = MODE == MASK_KPM;
   __shared__ __attribute__((aligned(16))) DkdvStage<D> st[2];
   __shared__ __attribute__((aligned(16))) u32x4 sP[4 * 4 * 64];  // [key group][chunk][lane]
@@ -435,13 +484,15 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(
       nlist = __builtin_amdgcn_readfirstlane(sCount);
     }
     if (w >= 4)
-      dkdv_role<D, true, MODE>(st, sP, krot, vn, qrot, dout, lse2, delta, cos, sin, dk, dv, S, P,
-                               Hq, Hkv, n_rep, b, g, bh, k0, w, lane, scale_log2, scale, causal,
-                               drow, sList, nlist, sQD, fv);
+      dkdv_role<D, true, MODE, STORE>(st, sP, krot, vn, qrot, dout, lse2, delta, cos, sin, dk,
+                                      dv, S, P, Hq, Hkv, n_rep, b, g, bh, k0, w, lane,
+                                      scale_log2, scale, causal, drow, sList, nlist, sQD, fv,
+                                      dsb, P / DSQ);
     else
-      dkdv_role<D, false, MODE>(st, sP, krot, vn, qrot, dout, lse2, delta, cos, sin, dk, dv, S, P,
-                                Hq, Hkv, n_rep, b, g, bh, k0, w, lane, scale_log2, scale, causal,
-                                drow, sList, nlist, sQD, fv);
+      dkdv_role<D, false, MODE, STORE>(st, sP, krot, vn, qrot, dout, lse2, delta, cos, sin, dk,
+                                       dv, S, P, Hq, Hkv, n_rep, b, g, bh, k0, w, lane,
+                                       scale_log2, scale, causal, drow, sList, nlist, sQD, fv,
+                                       dsb, P / DSQ);
     __syncthreads();  // LDS of this item is free for the next
   }
 }
@@ -673,11 +724,194 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_kernel(
   }
 }
 
+// dma16 with the nontemporal (streaming) cache policy, for data read once
+__device__ __forceinline__ void dma16_nt(uint32_t lds, uint32_t voff, const void* base) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2 nt"
+               :
+               : "s"(lds), "v"(voff), "s"(base)
+               : "memory", "m0");
+}
+
+// s_waitcnt vmcnt(n) for a wavefront-uniform n in [0, 15]
+__device__ __forceinline__ void wait_vm(int n) {
+  switch (n) {
+    case 0: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
+    case 1: asm volatile("s_waitcnt vmcnt(1)" ::: "memory"); break;
+    case 2: asm volatile("s_waitcnt vmcnt(2)" ::: "memory"); break;
+    case 3: asm volatile("s_waitcnt vmcnt(3)" ::: "memory"); break;
+    case 4: asm volatile("s_waitcnt vmcnt(4)" ::: "memory"); break;
+    case 5: asm volatile("s_waitcnt vmcnt(5)" ::: "memory"); break;
+    case 6: asm volatile("s_waitcnt vmcnt(6)" ::: "memory"); break;
+    case 7: asm volatile("s_waitcnt vmcnt(7)" ::: "memory"); break;
+    case 8: asm volatile("s_waitcnt vmcnt(8)" ::: "memory"); break;
+    case 9: asm volatile("s_waitcnt vmcnt(9)" ::: "memory"); break;
+    case 10: asm volatile("s_waitcnt vmcnt(10)" ::: "memory"); break;
+    case 11: asm volatile("s_waitcnt vmcnt(11)" ::: "memory"); break;
+    case 12: asm volatile("s_waitcnt vmcnt(12)" ::: "memory"); break;
+    case 13: asm volatile("s_waitcnt vmcnt(13)" ::: "memory"); break;
+    case 14: asm volatile("s_waitcnt vmcnt(14)" ::: "memory"); break;
+    default: asm volatile("s_waitcnt vmcnt(15)" ::: "memory"); break;
+  }
+}
+
+// dQ from the dS records: workgroup = HB query heads of one KV group x DSQ
+// positions, one wavefront per head (its 64 rows as two 32-row blocks, so each
+// K^T fragment feeds two products).  Per DSK-key step it stages the rotated K
+// rows [DSK][D] and the HB records into LDS (a ring of NBUF, loads issued
+// NBUF - 1 steps ahead) and accumulates dQ^T += K^T dS^T: K^T comes from the K
+// rows by ds_read_b64_tr_b16 (lds_frag_t), dS^T from the records by the same
+// instruction, which turns a record's one-key-per-lane layout into one row per
+// lane.  The kernel moves the dS bytes once and does one product per element;
+// it is bound by HBM.
+template <int D, int HB>
+__global__ __launch_bounds__(64 * HB) void bwd_dq_ds_kernel(
+    const u32x4* __restrict__ dsb, const bf16* __restrict__ krot, const float* __restrict__ cos,
+    const float* __restrict__ sin, bf16* __restrict__ dq, int S, int P, int Hq, int Hkv,
+    int n_rep, int nqt, int causal, float scale) {
+  constexpr int NW = HB, KR = D / 8, DT = D / 32, HALF = D / 2;
+  constexpr int NBUF = 3;
+  constexpr int KI = DSK * KR / 64;  // 1 KB load instructions per K step
+  static_assert(KI % NW == 0, "K rows must split evenly over the wavefronts");
+  // load instructions per wavefront and step: its share of K, its record's 4 KB
+  constexpr int NLOAD = KI / NW + 4;
+  static_assert(NLOAD <= 15, "wait_vm range");
+  struct Stage {
+    bf16 k[DSK * D];
+    u32x4 ds[HB * 256];
+  };
+  __shared__ __attribute__((aligned(16))) Stage st[NBUF];
+  const int w = wave_id(), lane = threadIdx.x & 63, hh = lane >> 5, c32 = lane & 31;
+  // item (KV head, head group, query tile): one XCD runs a contiguous range, a
+  // KV head's tiles longest-causal-row first
+  const int ngrp = n_rep / HB;
+  const int logical = xcd_logical_id(blockIdx.x, gridDim.x);
+  const int qt = nqt - 1 - logical % nqt;
+  const int hg = (logical / nqt) % ngrp, bh = logical / nqt / ngrp;
+  const int b = bh / Hkv, g = bh % Hkv;
+  const int nqtp = P / DSQ;
+  const int nk = causal ? min(2 * qt + 2, (S + DSK - 1) / DSK) : (S + DSK - 1) / DSK;
+  const u32x4* rec0 = dsb + (ds_pair(bh, qt, 0, nqtp, causal) * n_rep + hg * HB) * 256;
+  const bf16* kbase = krot + (int64_t)bh * P * D;
+  auto stage = [&](int t, int buf) {
+#pragma unroll
+    for (int jj = 0; jj < KI / NW; ++jj) {
+      const int j = w * (KI / NW) + jj;
+      const int L = j * 64 + lane, row = L / KR, pc = L % KR;
+      const uint32_t off =
+          ((uint32_t)(t * DSK + row) * D + (uint32_t)(pc ^ swz<KR>(row)) * 8u) * 2u;
+      dma16(lds_addr(st[buf].k + j * 512), off, kbase);
+    }
+    // this wavefront's record (read once: streaming loads), 4 x 1 KB of 64
+    // 16-byte B-operand pieces; lane i of an LDS copy takes piece i ^ 4*(i >> 5),
+    // so that the two 32-lane halves a transposed read combines sit in
+    // different bank halves
+    const u32x4* src = rec0 + ((int64_t)t * n_rep + w) * 256;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      dma16_nt(lds_addr(st[buf].ds + w * 256 + j * 64),
+            (uint32_t)((j * 64 + (lane ^ ((lane >> 5) << 2))) * 16), src);
+  };
+
+  // transposed-read address of this lane inside its record (row block mh adds
+  // 2048 bytes, key chunk c 256, the second read of a chunk 128): address-lane
+  // 4e + k of group G fetches rows 16(G&1) + 4k .. +3 of key 4(G>>1) + e
+  uint32_t ds_off;
+  {
+    const int G = lane >> 4, a = lane & 15, e = a >> 2, k = a & 3;
+    const int piece = 32 * (k & 1) + 4 * ((G >> 1) ^ (k & 1)) + e;
+    ds_off = (uint32_t)(w * 4096 + (G & 1) * 1024 + piece * 16 + 8 * (k >> 1));
+  }
+  const TrOffsets<D> tro = tr_offsets<D>(lane);
+  f32x16 acc[2][DT];
+#pragma unroll
+  for (int mh = 0; mh < 2; ++mh)
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc[mh][dt][i] = 0.f;
+
+#pragma unroll
+  for (int t = 0; t < NBUF - 1; ++t)
+    if (t < nk) stage(t, t);
+  for (int t = 0; t < nk; ++t) {
+    // step t's loads are in; the next step's may still fly
+    wait_vm(t + 1 < nk ? NLOAD : 0);
+    __syncthreads();  // every wavefront's share landed; step t - 1's buffer is free
+    if (t + NBUF - 1 < nk) stage(t + NBUF - 1, (t + NBUF - 1) % NBUF);
+    const Stage& S_ = st[t % NBUF];
+    const char* dsl = (const char*)S_.ds + ds_off;
+#pragma unroll
+    for (int c = 0; c < DSK / 16; ++c) {
+      bf16x8 bds[2];
+#pragma unroll
+      for (int mh = 0; mh < 2; ++mh) {
+        const char* p = dsl + 2048 * mh + 256 * c;
+        const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)p);
+        const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)(p + 128));
+        bds[mh] = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5,
+                                                                     6, 7));
+      }
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        const bf16x8 ak = lds_frag_t<D>(S_.k, tro, c, dt);
+#pragma unroll
+        for (int mh = 0; mh < 2; ++mh)
+          acc[mh][dt] =
+              __builtin_amdgcn_mfma_f32_32x32x16_bf16(ak, bds[mh], acc[mh][dt], 0, 0, 0);
+      }
+    }
+  }
+
+  const int hq = g * n_rep + hg * HB + w;
+#pragma unroll
+  for (int mh = 0; mh < 2; ++mh) {
+    const int pos = qt * DSQ + 32 * mh + c32;
+    if (pos >= S) break;
+    bf16* dqr = dq + (((int64_t)b * S + pos) * Hq + hq) * D;
+    const float* cr = cos + (int64_t)pos * HALF;
+    const float* sr = sin + (int64_t)pos * HALF;
+#pragma unroll
+    for (int dt = 0; dt < DT / 2; ++dt)
+#pragma unroll
+      for (int gi = 0; gi < 4; ++gi) {
+        const int d = 32 * dt + 8 * gi + 4 * hh;
+        float lo[4], hi[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          rope_pair_bwd<bf16>(acc[mh][dt][4 * gi + e] * scale,
+                              acc[mh][dt + DT / 2][4 * gi + e] * scale, cr[d + e], sr[d + e],
+                              lo[e], hi[e]);
+        *(u32x2*)(dqr + d) = u32x2{pack2(lo[0], lo[1]), pack2(lo[2], lo[3])};
+        *(u32x2*)(dqr + d + HALF) = u32x2{pack2(hi[0], hi[1]), pack2(hi[2], hi[3])};
+      }
+  }
+}
+
 struct Ws {
   bf16 *krot, *vn, *qrot;
   float *lse2, *delta;
   int2* ranges;  // [B][P/64] document-id range per tile (packed documents only)
+  u32x4* dsb;    // dS records (when kept)
 };
+
+size_t base_bytes(int B, int S, int Hq, int Hkv, int D) {
+  const size_t P = (size_t)pad_len(S);
+  return (2 * (size_t)B * Hkv + (size_t)B * Hq) * P * D * sizeof(uint16_t) +
+         2 * (size_t)B * Hq * P * sizeof(float) + (size_t)B * (P / BN) * sizeof(int2);
+}
+size_t align256(size_t n) { return (n + 255) / 256 * 256; }
+
+// Largest dS record store the backward uses; past it dQ recomputes S and dP.
+constexpr size_t DS_STORE_MAX = (size_t)32 << 30;
+
+// bytes of the dS records of this launch, or 0 when they are not kept
+size_t ds_bytes(const BwdArgs& a) {
+  if (a.doc || a.kvalid) return 0;
+  const size_t nqtp = (size_t)pad_len(a.S) / DSQ;
+  const size_t pairs = a.causal ? nqtp * (nqtp + 1) : 2 * nqtp * nqtp;
+  const size_t bytes = (size_t)a.B * a.Hq * pairs * 4096;
+  return bytes <= DS_STORE_MAX ? bytes : 0;
+}
 
 Ws carve(void* base, int B, int S, int Hq, int Hkv, int D) {
   const size_t P = (size_t)pad_len(S);
@@ -691,11 +925,22 @@ Ws carve(void* base, int B, int S, int Hq, int Hkv, int D) {
   w.lse2 = f; f += (size_t)B * Hq * P;
   w.delta = f; f += (size_t)B * Hq * P;
   w.ranges = (int2*)f;
+  w.dsb = (u32x4*)((char*)base + align256(base_bytes(B, S, Hq, Hkv, D)));
   return w;
 }
 
+template <int D, int HB>
+int launch_dq_ds(const BwdArgs& a, const Ws& w) {
+  const int P = pad_len(a.S), n_rep = a.Hq / a.Hkv, nqt = (a.S + DSQ - 1) / DSQ;
+  KF_LAUNCH("bwd_dq_ds", (bwd_dq_ds_kernel<D, HB>), dim3(a.B * a.Hkv * (n_rep / HB) * nqt),
+            dim3(64 * HB), 0, a.stream, w.dsb, w.krot, a.cos, a.sin, (bf16*)a.dq, a.S, P, a.Hq,
+            a.Hkv, n_rep, nqt, a.causal, a.scale);
+  KF_CHECK_LAUNCH();
+  return KF_OK;
+}
+
 template <int D>
-int launch_bwd(const BwdArgs& a, void* workspace) {
+int launch_bwd(const BwdArgs& a, void* workspace, bool keep_ds) {
   const int P = pad_len(a.S);
   const Ws w = carve(workspace, a.B, a.S, a.Hq, a.Hkv, D);
   const int n_rep = a.Hq / a.Hkv;
@@ -722,14 +967,19 @@ int launch_bwd(const BwdArgs& a, void* workspace) {
   const int mode = a.doc ? MASK_DOC : a.kvalid ? MASK_KPM : MASK_NONE;
   const int32_t* aux = a.doc ? a.doc : a.kvalid;
   KF_LAUNCH("bwd_dkdv",
-            (mode == MASK_DOC   ? bwd_dkdv_kernel<D, MASK_DOC>
-             : mode == MASK_KPM ? bwd_dkdv_kernel<D, MASK_KPM>
-                                : bwd_dkdv_kernel<D, MASK_NONE>),
+            (mode == MASK_DOC   ? bwd_dkdv_kernel<D, MASK_DOC, false>
+             : mode == MASK_KPM ? bwd_dkdv_kernel<D, MASK_KPM, false>
+             : keep_ds          ? bwd_dkdv_kernel<D, MASK_NONE, true>
+                                : bwd_dkdv_kernel<D, MASK_NONE, false>),
             dim3(std::min(nkb * a.B * a.Hkv, grid_cap)), dim3(512), 0, a.stream, w.krot, w.vn,
             w.qrot, (const bf16*)a.dout, w.lse2, w.delta, a.cos, a.sin, (bf16*)a.dk,
             (bf16*)a.dv, a.S, P, a.Hq, a.Hkv, n_rep, nkb, nkb * a.B * a.Hkv,
-            scale_log2, a.scale, a.causal, aux, w.ranges);
+            scale_log2, a.scale, a.causal, aux, w.ranges, w.dsb);
   KF_CHECK_LAUNCH();
+  if (keep_ds)
+    return n_rep % 4 == 0   ? launch_dq_ds<D, 4>(a, w)
+           : n_rep % 2 == 0 ? launch_dq_ds<D, 2>(a, w)
+                            : launch_dq_ds<D, 1>(a, w);
   const int bm_pos = DQ_ROWS / n_rep;
   const int nqb = (a.S + bm_pos - 1) / bm_pos;
   KF_LAUNCH("bwd_dq",
@@ -758,14 +1008,19 @@ bool bwd_mfma_supported(const BwdArgs& a) {
 }
 
 size_t bwd_mfma_workspace(int B, int S, int Hq, int Hkv, int D) {
-  const size_t P = (size_t)pad_len(S);
-  return (2 * (size_t)B * Hkv + (size_t)B * Hq) * P * D * sizeof(uint16_t) +
-         2 * (size_t)B * Hq * P * sizeof(float) + (size_t)B * (P / BN) * sizeof(int2);
+  return base_bytes(B, S, Hq, Hkv, D);
 }
 
-int bwd_mfma(const BwdArgs& a, void* workspace) {
+size_t bwd_mfma_workspace_ds(const BwdArgs& a) {
+  const size_t base = base_bytes(a.B, a.S, a.Hq, a.Hkv, a.D), ds = ds_bytes(a);
+  return ds ? align256(base) + ds : base;
+}
+
+int bwd_mfma(const BwdArgs& a, void* workspace, size_t workspace_bytes) {
   KF_CHECK_ARG((int64_t)pad_len(a.S) / BN * (int64_t)a.B * a.Hq < (1LL << 31), "grid too large");
-  return a.D == 128 ? launch_bwd<128>(a, workspace) : launch_bwd<64>(a, workspace);
+  const bool keep_ds = ds_bytes(a) != 0 && workspace_bytes >= bwd_mfma_workspace_ds(a);
+  return a.D == 128 ? launch_bwd<128>(a, workspace, keep_ds)
+                    : launch_bwd<64>(a, workspace, keep_ds);
 }
 
 }  // namespace kf

@@ -71,7 +71,11 @@ int capture_probs_mfma(const FwdArgs& a, const float* lse, float* probs, void* w
 
 bool bwd_mfma_supported(const BwdArgs& a);
 size_t bwd_mfma_workspace(int B, int S, int Hq, int Hkv, int D);
-int bwd_mfma(const BwdArgs& a, void* workspace);
+// Workspace with which bwd_mfma stores the dS tiles once for dQ instead of
+// recomputing S and dP (unmasked launches up to a size cap); otherwise
+// bwd_mfma_workspace.  bwd_mfma takes that path when workspace_bytes allows.
+size_t bwd_mfma_workspace_ds(const BwdArgs& a);
+int bwd_mfma(const BwdArgs& a, void* workspace, size_t workspace_bytes);
 
 // decode (kf_decode.hip)
 struct DecodeArgs {

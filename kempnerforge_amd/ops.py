@@ -133,9 +133,27 @@ def fwd_raw(q, k, v, cos, sin, *, causal: bool, k_rotated: bool, k_layout: str =
     return out, lse
 
 
+_BWD_LOW_MEMORY = False
+
+
+def set_backward_low_memory(enabled: bool) -> None:
+    """Default of ``bwd_raw``'s ``low_memory`` (and so of the autograd backward of
+    :func:`attention` and the ``Attention`` module): True trades ~5-11% of
+    backward time for not holding the kept dS tiles (about B*Hq*S*S bytes)."""
+    global _BWD_LOW_MEMORY
+    _BWD_LOW_MEMORY = bool(enabled)
+
+
 def bwd_raw(q, k, v, cos, sin, out, lse, dout, *, causal: bool, doc_ids=None,
-            key_padding_mask=None):
-    """dq, dk, dv for :func:`fwd_raw` with un-rotated BSHD k (``kf_attn_bwd``)."""
+            key_padding_mask=None, low_memory: bool | None = None):
+    """dq, dk, dv for :func:`fwd_raw` with un-rotated BSHD k (``kf_attn_bwd``).
+
+    By default the workspace is sized so that the dK/dV pass keeps its bf16 dS
+    tiles for dQ (``kf_attn_bwd_workspace_size_ds``: about B*Hq*S*S bytes
+    for causal attention, 2.1 GB at B=4, S=4096, Hq=32); ``low_memory=True``
+    passes the minimal workspace, and dQ recomputes S and dP instead (None:
+    the default set by :func:`set_backward_low_memory`, initially False).
+    """
     _require_gpu(q, k, v, out, lse, dout)
     lib = _lib.load()
     q, k, v, out, dout = (t.contiguous() for t in (q, k, v, out, dout))
@@ -149,8 +167,14 @@ def bwd_raw(q, k, v, cos, sin, out, lse, dout, *, causal: bool, doc_ids=None,
     dt = _dtype_code(q)
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
     nbytes = _lib.size_out()
-    _lib.check(lib.kf_attn_bwd_workspace_size(B, S, Hq, Hkv, D, dt, ctypes.byref(nbytes)),
-               "kf_attn_bwd_workspace_size")
+    low_memory = _BWD_LOW_MEMORY if low_memory is None else low_memory
+    if low_memory or doc is not None or kv is not None:  # masked calls never keep dS
+        _lib.check(lib.kf_attn_bwd_workspace_size(B, S, Hq, Hkv, D, dt, ctypes.byref(nbytes)),
+                   "kf_attn_bwd_workspace_size")
+    else:
+        _lib.check(lib.kf_attn_bwd_workspace_size_ds(B, S, Hq, Hkv, D, dt, int(causal),
+                                                     ctypes.byref(nbytes)),
+                   "kf_attn_bwd_workspace_size_ds")
     ws = _workspace(nbytes.value, q.device)
     _lib.check(lib.kf_attn_bwd(_ptr(q), _ptr(k), _ptr(v), _ptr(cos), _ptr(sin), _ptr(out),
                                _ptr(lse), _ptr(dout), _ptr(dq), _ptr(dk), _ptr(dv), _ptr(ws),

@@ -59,6 +59,24 @@ def test_host_only_calls():
     assert lib.kf_attn_fwd_workspace_size(1, 8, 8, 4, 4, 63, 1, ctypes.byref(n)) == 1
     assert lib.kf_attn_decode_workspace_size(32, 32, 8, 128, 8193, 1, ctypes.byref(n)) == 0
     assert n.value == 32 * 32 * 9 * 130 * 4  # ceil(8193 / 1024) splits of (o[D], m, l)
+    # backward: rotated K, V (per KV head) and Q (per query head) bf16 [P][D], then
+    # lse and Delta float32 [P] per query head, then the int2 tile records
+    B, S, Hq, Hkv, D, P = 4, 4096, 32, 8, 128, 4096
+    base = (2 * B * Hkv + B * Hq) * P * D * 2 + 2 * B * Hq * P * 4 + B * (P // 64) * 8
+    assert lib.kf_attn_bwd_workspace_size(B, S, Hq, Hkv, D, 1, ctypes.byref(n)) == 0
+    assert n.value == base
+    # kept dS tiles: bf16 over the causal 64-row x 32-key blocks, P * (P + 64) bytes per
+    # query head, after the base rounded up to 256 bytes; full attention: 2 * P * P
+    assert lib.kf_attn_bwd_workspace_size_ds(B, S, Hq, Hkv, D, 1, 1, ctypes.byref(n)) == 0
+    assert n.value == (base + 255) // 256 * 256 + B * Hq * P * (P + 64)
+    assert lib.kf_attn_bwd_workspace_size_ds(B, 4000, Hq, Hkv, D, 1, 0, ctypes.byref(n)) == 0
+    assert n.value == (base + 255) // 256 * 256 + B * Hq * 2 * P * P  # P = 4096 for S = 4000
+    # fp32 runs the generic kernels (no tiles kept); past 32 GiB of tiles dQ recomputes
+    for args in ((B, S, Hq, Hkv, D, 0, 1), (1, 65536, 32, 8, 128, 1, 1)):
+        small, big = _lib.size_out(), _lib.size_out()
+        assert lib.kf_attn_bwd_workspace_size(*args[:6], ctypes.byref(small)) == 0
+        assert lib.kf_attn_bwd_workspace_size_ds(*args, ctypes.byref(big)) == 0
+        assert big.value == small.value
     # kv-cache overflow is rejected on the host (reference generate.py:92-96 guard)
     rc = lib.kf_kv_cache_append(ctypes.c_void_p(16), ctypes.c_void_p(16), ctypes.c_void_p(16),
                                 ctypes.c_void_p(16), ctypes.c_void_p(16), ctypes.c_void_p(16),

@@ -65,6 +65,43 @@ def test_shapes(cfg, causal):
     assert rel_max(dv, dv_r) <= TOL[dtype]
 
 
+# n_rep 1, 2, 3, 4 and 8 (the dQ kernel groups 4, 2 or 1 query heads per
+# workgroup); lengths off the 64-position tiles and 128-key blocks
+DS_SHAPES = [
+    (1, 333, 2, 2, 128),
+    (2, 200, 4, 2, 64),
+    (1, 130, 6, 2, 128),
+    (1, 257, 8, 2, 128),
+    (1, 190, 16, 2, 64),
+]
+
+
+@pytest.mark.parametrize("cfg", DS_SHAPES, ids=lambda c: "-".join(map(str, c)))
+@pytest.mark.parametrize("causal", [True, False])
+def test_kept_and_recomputed_ds(cfg, causal):
+    """Both backward paths against the oracle: the default workspace, with which
+    the dK/dV pass keeps its dS tiles for dQ, and the minimal one (low_memory),
+    with which dQ recomputes S and dP.  dK and dV come from the same arithmetic
+    either way (bitwise equal)."""
+    B, S, Hq, Hkv, D = cfg
+    announce(f"bwd kept/recomputed dS {cfg} causal={causal}")
+    q = seeded((B, S, Hq, D), 10, torch.bfloat16)
+    k = seeded((B, S, Hkv, D), 11, torch.bfloat16)
+    v = seeded((B, S, Hkv, D), 12, torch.bfloat16)
+    do = seeded((B, S, Hq, D), 13, torch.bfloat16)
+    cos, sin = ref.rope_tables(D, S, 5e5)
+    args = [t.to(DEV) for t in (q, k, v, cos, sin)]
+    out, lse = ops.fwd_raw(*args, causal=causal, k_rotated=False)
+    kept = ops.bwd_raw(*args, out, lse, do.to(DEV), causal=causal)
+    recomputed = ops.bwd_raw(*args, out, lse, do.to(DEV), causal=causal, low_memory=True)
+    torch.cuda.synchronize()
+    assert torch.equal(kept[1], recomputed[1]) and torch.equal(kept[2], recomputed[2])
+    refs = ref.attention_bwd(q, k, v, cos, sin, do, causal=causal)
+    for grads in (kept, recomputed):
+        for got, want, name in zip(grads, refs, ("dq", "dk", "dv")):
+            assert rel_max(got, want) <= 2e-2, name
+
+
 def test_llama8b_shape_one_group():
     """C3 at full size (B=4, S=4096, Hq=32, Hkv=8, D=128): the backward of KV
     group (b=1, g=6) against the oracle (groups are independent), plus
