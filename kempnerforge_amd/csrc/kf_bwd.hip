@@ -224,16 +224,14 @@ __device__ __forceinline__ void dkdv_role(
   u32x4* myP = sP + kw * 4 * 64 + lane;  // chunk c at myP[c * 64]
   const TrOffsets<D> tro = tr_offsets<D>(lane);
 
-  // STORE (dS waves): the dS tile of an iteration is written to its record at
-  // the start of the next one, so the stores have a whole iteration to
-  // complete before the end-of-iteration wait for the staging loads
-  u32x4 dsv[4];
-  u32x4* dsdst = nullptr;
-  auto put_ds = [&]() {
-#pragma unroll
-    for (int c = 0; c < 4; ++c) __builtin_nontemporal_store(dsv[c], &dsdst[c * 64]);
-  };
+  // STORE (dS waves): each dS tile goes to its record right after it is formed
+  // (non-temporal: the records are read once, by the dQ kernel).  The record's
+  // index is scalar work done before the mid-tile barrier, where the dS waves
+  // wait for P anyway, not between dS and the dK products.
   const int k32 = k0 / DSK + kw;  // this wavefront's 32-key record column
+  const int nqtp2 = 2 * nqtp;
+  const int64_t rec_bh = (int64_t)bh * nqtp * (causal ? nqtp + 1 : nqtp2);
+  int rec_head = 0, rec_tile = 0;  // head and tile count of iteration it (no division)
 
   lds_copy_wait();
   __syncthreads();
@@ -242,10 +240,6 @@ __device__ __forceinline__ void dkdv_role(
   for (int it = 0; it < total; ++it) {
     const int buf = it & 1;
     if (it + 1 < total) stage(it + 1, buf ^ 1);
-    if (STORE && DSROLE && dsdst != nullptr) {
-      put_ds();
-      dsdst = nullptr;
-    }
     const DkdvStage<D>& S_ = st[buf];
     const int e = entry(it);
     const int q0 = tile_of(e) * BQ;
@@ -315,6 +309,15 @@ __device__ __forceinline__ void dkdv_role(
 #pragma unroll
       for (int c = 0; c < 4; ++c) myP[c * 64] = pk[c];
     }
+    // record of this tile (-1: above the causal diagonal, nothing to keep)
+    int64_t rec = -1;
+    if (STORE && DSROLE) {
+      const int qt = q0 / DSQ;
+      if (!causal || k32 <= 2 * qt + 1)
+        rec = ((rec_bh + (causal ? (int64_t)qt * (qt + 1) : (int64_t)qt * nqtp2) + k32) * n_rep +
+               rec_head) * 256;
+      asm volatile("" : "+s"(rec));
+    }
     __syncthreads();  // P of this tile is in LDS
     if (DSROLE) {
 #pragma unroll
@@ -339,13 +342,9 @@ __device__ __forceinline__ void dkdv_role(
             pk[2 * mt + cc][2 * half + 1] = pack2(v[2], v[3]);
           }
         }
-      if (STORE) {
-        const int qt = q0 / DSQ;
-        if (!causal || k32 <= 2 * qt + 1) {
+      if (STORE && rec >= 0) {
 #pragma unroll
-          for (int c = 0; c < 4; ++c) dsv[c] = pk[c];
-          dsdst = dsb + (ds_pair(bh, qt, k32, nqtp, causal) * n_rep + it / per_head) * 256 + lane;
-        }
+        for (int c = 0; c < 4; ++c) __builtin_nontemporal_store(pk[c], dsb + rec + c * 64 + lane);
       }
     }
     // phase 2: dV^T += dO^T P (P waves) or dK^T += Q^T dS (dS waves)
@@ -365,10 +364,13 @@ __device__ __forceinline__ void dkdv_role(
       }
       __builtin_amdgcn_sched_barrier(0);
     }
+    if (STORE && ++rec_tile == per_head) {
+      rec_tile = 0;
+      ++rec_head;
+    }
     lds_copy_wait();
     __syncthreads();
   }
-  if (STORE && DSROLE && dsdst != nullptr) put_ds();
 
   if (key >= S) return;
   if (DSROLE) {
