@@ -133,6 +133,60 @@ __device__ __forceinline__ void wait_vm(u32x4* r) {
   for (int i = 1; i < n; ++i) asm volatile("" : "+v"(r[i])::"memory");
 }
 
+// Longest-processing-time-first order of the split grid.  A full split of CH
+// keys takes ~40 us of one workgroup slot's share of HBM at C4's size, and the
+// grid runs in 2-3 rounds of slots, so a round that ends on full splits idles
+// half the machine for tens of microseconds.  Flat block id f maps to: first
+// every full split (b, g, k < len_b / CH), then each sequence's partial split
+// (len_b % CH keys) ordered by size, largest first, so the last workgroups
+// dispatched are the shortest.  One wavefront computes it (lane = batch row,
+// B <= 64) and leaves {split, b, g} in job[], split = -1 for no work.
+__device__ __forceinline__ void decode_job(const int32_t* __restrict__ lens, int B, int Hkv,
+                                           int max_len, int64_t row_offset, int64_t rope_rows,
+                                           int f, int lane, int* job) {
+  int Lb = 0;
+  if (lane < B) {
+    const int len = lens[lane];
+    Lb = decode_len_ok(len, max_len, row_offset, rope_rows) ? len + 1 : 0;
+  }
+  const int nf = Lb / CH, r = Lb % CH;
+  int incl = nf * Hkv;  // inclusive prefix of full splits over the batch rows
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(incl, o, 64);
+    if (lane >= o) incl += y;
+  }
+  const int F = __shfl(incl, 63, 64);
+  int sp = -1, bb = 0, gg = 0;
+  if (f < F) {
+    const uint64_t m = __builtin_amdgcn_ballot_w64(incl - nf * Hkv <= f && f < incl);
+    bb = (int)__builtin_ctzll(m);
+    const int nfb = __shfl(nf, bb, 64);
+    const int within = f - (__shfl(incl, bb, 64) - nfb * Hkv);
+    sp = within % nfb;
+    gg = within / nfb;
+  } else {
+    const int p = (f - F) / Hkv;
+    gg = (f - F) % Hkv;
+    // rank of this row's partial split: larger first, ties by row
+    int rank = 0;
+    for (int j = 0; j < B; ++j) {
+      const int rj = __shfl(r, j, 64);
+      rank += (rj > r) || (rj == r && j < lane);
+    }
+    const uint64_t m = __builtin_amdgcn_ballot_w64(r > 0 && rank == p);
+    if (m) {
+      bb = (int)__builtin_ctzll(m);
+      sp = __shfl(nf, bb, 64);
+    }
+  }
+  if (lane == 0) {
+    job[0] = sp;
+    job[1] = bb;
+    job[2] = gg;
+  }
+}
+
 constexpr int DEC_WAVES = 4;
 constexpr int KC = 32;                    // keys per chunk
 constexpr int NCH = CH / (DEC_WAVES * KC);  // chunks per wavefront
@@ -156,9 +210,22 @@ __global__ __launch_bounds__(256, 2) void decode_split_kernel(
   __shared__ float sML[DEC_WAVES][2][32];
   static_assert(sizeof(sV) >= DEC_WAVES * 32 * D * sizeof(float), "merge buffer");
 
-  const int sp_idx = blockIdx.x;
-  const int bg = blockIdx.y;
-  const int b = bg / Hkv, g = bg % Hkv;
+  // which split this workgroup computes: longest first (see decode_job)
+  __shared__ int sJob[3];
+  const int B = gridDim.y / Hkv;
+  if (B <= 64) {
+    if (threadIdx.x < 64)
+      decode_job(lens, B, Hkv, max_len, row_offset, rope_rows,
+                 blockIdx.y * gridDim.x + blockIdx.x, threadIdx.x, sJob);
+  } else if (threadIdx.x == 0) {
+    sJob[0] = blockIdx.x;
+    sJob[1] = blockIdx.y / Hkv;
+    sJob[2] = blockIdx.y % Hkv;
+  }
+  __syncthreads();
+  const int sp_idx = sJob[0];
+  if (sp_idx < 0) return;
+  const int b = sJob[1], g = sJob[2];
   if (!decode_len_ok(lens[b], max_len, row_offset, rope_rows)) return;
   const int L = lens[b] + 1;
   const int newrow = L - 1;  // the token being decoded

@@ -37,7 +37,10 @@ def test_fixture():
 @pytest.mark.parametrize("cfg", [
     # dtype, B, Hq, Hkv, D, lo, hi, Smax
     (torch.bfloat16, 3, 8, 8, 64, 1, 300, 400),      # MHA fast path, D=64
-    (torch.bfloat16, 2, 16, 2, 128, 255, 257, 300),  # split boundaries (CH=256)
+    (torch.bfloat16, 2, 16, 2, 128, 255, 257, 300),  # sub-split lengths
+    (torch.bfloat16, 6, 16, 2, 128, 1022, 1025, 1100),  # split boundaries (1024 keys)
+    (torch.bfloat16, 40, 8, 2, 64, 900, 3100, 3200),  # longest-first split order (B <= 64)
+    (torch.bfloat16, 70, 8, 2, 64, 900, 2200, 2300),  # plain split order (B > 64)
     (torch.bfloat16, 2, 8, 1, 128, 0, 3, 8),         # empty cache (len 0) and tiny
     (torch.bfloat16, 2, 6, 2, 128, 10, 90, 100),     # n_rep 3 (padded MFMA columns)
     (torch.bfloat16, 2, 32, 1, 128, 500, 700, 800),  # n_rep 32, the widest fast case
