@@ -91,7 +91,8 @@ int kf_attn_bwd_workspace_size(int B, int S, int Hq, int Hkv, int D, int dtype, 
  * pass for dQ instead of recomputing S and dP (one fewer pass over the
  * attention matrix; B*Hq*P*(P+64) bytes extra for causal, 2*B*Hq*P*P for full
  * attention, P = S rounded up to 128).  Applies to the bf16 kernels without
- * doc_ids / key_valid and up to 32 GiB of tiles; otherwise this equals
+ * key_valid, up to 32 GiB of tiles (and S <= 65536 with doc_ids, whose tiles
+ * are then written only where documents meet); otherwise this equals
  * kf_attn_bwd_workspace_size.  kf_attn_bwd takes the faster path whenever
  * workspace_bytes reaches this size.  No counterpart in the reference (its
  * SDPA backward manages its own memory). */

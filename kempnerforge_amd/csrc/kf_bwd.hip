@@ -67,6 +67,7 @@ __host__ __device__ constexpr int pad_len(int S) { return (S + BKV - 1) / BKV * 
 // the key columns k32 <= 2*qt + 1 that the tile's rows can see exist.
 constexpr int DSQ = 64;  // query positions per record (= BQ)
 constexpr int DSK = 32;  // keys per record (one dS wavefront)
+constexpr int DS_DOC_MAX_TILES = 1024;  // packed documents keep records up to S = 65536
 
 // record pair index of (KV head bh, query tile qt, key column k32); nqtp = P / DSQ
 __host__ __device__ inline int64_t ds_pair(int bh, int qt, int k32, int nqtp, int causal) {
@@ -167,7 +168,7 @@ __device__ __forceinline__ void dkdv_role(
     const uint16_t* qlist, int nlist, int32_t (*sQD)[BQ], int fv, u32x4* __restrict__ dsb,
     int nqtp) {
   constexpr bool DOC = MODE == MASK_DOC, KPM = MODE == MASK_KPM, LIST = DOC || KPM;
-  static_assert(!(STORE && LIST), "dS records are kept for unmasked launches only");
+  static_assert(!(STORE && KPM), "dS records are not kept with key padding");
   constexpr int KS = D / 16, DT = D / 32, HALF = D / 2;
   constexpr int KR = D / 8;
   constexpr int PF = 3;  // fragment reads run PF MFMAs ahead
@@ -765,11 +766,12 @@ __device__ __forceinline__ void wait_vm(int n) {
 // instruction, which turns a record's one-key-per-lane layout into one row per
 // lane.  The kernel moves the dS bytes once and does one product per element;
 // it is bound by HBM.
-template <int D, int HB>
+template <int D, int HB, bool DOC>
 __global__ __launch_bounds__(64 * HB) void bwd_dq_ds_kernel(
     const u32x4* __restrict__ dsb, const bf16* __restrict__ krot, const float* __restrict__ cos,
     const float* __restrict__ sin, bf16* __restrict__ dq, int S, int P, int Hq, int Hkv,
-    int n_rep, int nqt, int causal, float scale) {
+    int n_rep, int nqt, int causal, float scale, const int32_t* __restrict__ doc,
+    const int2* __restrict__ ranges) {
   constexpr int NW = HB, KR = D / 8, DT = D / 32, HALF = D / 2;
   constexpr int NBUF = 3;
   constexpr int KI = DSK * KR / 64;  // 1 KB load instructions per K step
@@ -791,10 +793,30 @@ __global__ __launch_bounds__(64 * HB) void bwd_dq_ds_kernel(
   const int hg = (logical / nqt) % ngrp, bh = logical / nqt / ngrp;
   const int b = bh / Hkv, g = bh % Hkv;
   const int nqtp = P / DSQ;
-  const int nk = causal ? min(2 * qt + 2, (S + DSK - 1) / DSK) : (S + DSK - 1) / DSK;
+  int nk = causal ? min(2 * qt + 2, (S + DSK - 1) / DSK) : (S + DSK - 1) / DSK;
+  // DOC: the 64-key tiles whose document range meets this tile's rows (the
+  // dK/dV pass listed this query tile for their key blocks, so their records
+  // exist); each listed tile is two steps.  Causal: tiles 0 .. qt.
+  __shared__ uint16_t sList[DOC ? DS_DOC_MAX_TILES : 1];
+  __shared__ int sCount;
+  if constexpr (DOC) {
+    if (w == 0) {
+      const int n = doc_tile_list(doc + (int64_t)b * S, qt * DSQ, min(qt * DSQ + DSQ, S),
+                                  ranges + (int64_t)b * (P / BN), 0, qt + 1, sList, lane);
+      if (lane == 0) sCount = n;
+    }
+    __syncthreads();
+    nk = 2 * __builtin_amdgcn_readfirstlane(sCount);
+  }
+  // record column (32 keys) of step t
+  auto col = [&](int t) -> int {
+    return DOC ? 2 * (__builtin_amdgcn_readfirstlane((int)sList[t >> 1]) & ~DOC_MASK_FLAG) + (t & 1)
+               : t;
+  };
   const u32x4* rec0 = dsb + (ds_pair(bh, qt, 0, nqtp, causal) * n_rep + hg * HB) * 256;
   const bf16* kbase = krot + (int64_t)bh * P * D;
-  auto stage = [&](int t, int buf) {
+  auto stage = [&](int t_, int buf) {
+    const int t = col(t_);
 #pragma unroll
     for (int jj = 0; jj < KI / NW; ++jj) {
       const int j = w * (KI / NW) + jj;
@@ -811,7 +833,7 @@ __global__ __launch_bounds__(64 * HB) void bwd_dq_ds_kernel(
 #pragma unroll
     for (int j = 0; j < 4; ++j)
       dma16_nt(lds_addr(st[buf].ds + w * 256 + j * 64),
-            (uint32_t)((j * 64 + (lane ^ ((lane >> 5) << 2))) * 16), src);
+               (uint32_t)((j * 64 + (lane ^ ((lane >> 5) << 2))) * 16), src);
   };
 
   // transposed-read address of this lane inside its record (row block mh adds
@@ -908,7 +930,7 @@ constexpr size_t DS_STORE_MAX = (size_t)32 << 30;
 
 // bytes of the dS records of this launch, or 0 when they are not kept
 size_t ds_bytes(const BwdArgs& a) {
-  if (a.doc || a.kvalid) return 0;
+  if (a.kvalid || (a.doc && pad_len(a.S) / DSQ > DS_DOC_MAX_TILES)) return 0;
   const size_t nqtp = (size_t)pad_len(a.S) / DSQ;
   const size_t pairs = a.causal ? nqtp * (nqtp + 1) : 2 * nqtp * nqtp;
   const size_t bytes = (size_t)a.B * a.Hq * pairs * 4096;
@@ -934,9 +956,10 @@ Ws carve(void* base, int B, int S, int Hq, int Hkv, int D) {
 template <int D, int HB>
 int launch_dq_ds(const BwdArgs& a, const Ws& w) {
   const int P = pad_len(a.S), n_rep = a.Hq / a.Hkv, nqt = (a.S + DSQ - 1) / DSQ;
-  KF_LAUNCH("bwd_dq_ds", (bwd_dq_ds_kernel<D, HB>), dim3(a.B * a.Hkv * (n_rep / HB) * nqt),
-            dim3(64 * HB), 0, a.stream, w.dsb, w.krot, a.cos, a.sin, (bf16*)a.dq, a.S, P, a.Hq,
-            a.Hkv, n_rep, nqt, a.causal, a.scale);
+  KF_LAUNCH("bwd_dq_ds", (a.doc ? bwd_dq_ds_kernel<D, HB, true> : bwd_dq_ds_kernel<D, HB, false>),
+            dim3(a.B * a.Hkv * (n_rep / HB) * nqt), dim3(64 * HB), 0, a.stream, w.dsb, w.krot,
+            a.cos, a.sin, (bf16*)a.dq, a.S, P, a.Hq, a.Hkv, n_rep, nqt, a.causal, a.scale,
+            a.doc, w.ranges);
   KF_CHECK_LAUNCH();
   return KF_OK;
 }
@@ -969,7 +992,8 @@ int launch_bwd(const BwdArgs& a, void* workspace, bool keep_ds) {
   const int mode = a.doc ? MASK_DOC : a.kvalid ? MASK_KPM : MASK_NONE;
   const int32_t* aux = a.doc ? a.doc : a.kvalid;
   KF_LAUNCH("bwd_dkdv",
-            (mode == MASK_DOC   ? bwd_dkdv_kernel<D, MASK_DOC, false>
+            (mode == MASK_DOC   ? (keep_ds ? bwd_dkdv_kernel<D, MASK_DOC, true>
+                                           : bwd_dkdv_kernel<D, MASK_DOC, false>)
              : mode == MASK_KPM ? bwd_dkdv_kernel<D, MASK_KPM, false>
              : keep_ds          ? bwd_dkdv_kernel<D, MASK_NONE, true>
                                 : bwd_dkdv_kernel<D, MASK_NONE, false>),

@@ -168,7 +168,7 @@ def bwd_raw(q, k, v, cos, sin, out, lse, dout, *, causal: bool, doc_ids=None,
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
     nbytes = _lib.size_out()
     low_memory = _BWD_LOW_MEMORY if low_memory is None else low_memory
-    if low_memory or doc is not None or kv is not None:  # masked calls never keep dS
+    if low_memory or kv is not None:  # key padding never keeps dS
         _lib.check(lib.kf_attn_bwd_workspace_size(B, S, Hq, Hkv, D, dt, ctypes.byref(nbytes)),
                    "kf_attn_bwd_workspace_size")
     else:

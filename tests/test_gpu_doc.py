@@ -117,6 +117,32 @@ def test_backward(cfg):
         assert rel_max(got, want) <= TOL[dtype], name
 
 
+BF16_CASES = [c for c in CASES if c[0] == torch.bfloat16]
+
+
+@pytest.mark.parametrize("cfg", BF16_CASES, ids=lambda c: "-".join(map(str, c)))
+def test_backward_kept_and_recomputed_ds(cfg):
+    """Packed documents through both dQ paths: the dS tiles the dK/dV pass keeps
+    (written only for the listed query tiles; dQ reads only the listed key tiles)
+    and the minimal workspace, where dQ recomputes S and dP.  dK and dV are the
+    same arithmetic either way (bitwise equal)."""
+    dtype, B, S, Hq, Hkv, D, layout = cfg
+    announce(f"doc bwd kept/recomputed dS {cfg}")
+    q, k, v, do, cos, sin = _inputs(dtype, B, S, Hq, Hkv, D)
+    doc = _doc_ids(B, S, layout).to(DEV)
+    args = [t.to(DEV) for t in (q, k, v, cos, sin)]
+    out, lse = ops.fwd_raw(*args, causal=True, k_rotated=False, doc_ids=doc)
+    kept = ops.bwd_raw(*args, out, lse, do.to(DEV), causal=True, doc_ids=doc)
+    recomputed = ops.bwd_raw(*args, out, lse, do.to(DEV), causal=True, doc_ids=doc,
+                             low_memory=True)
+    torch.cuda.synchronize()
+    assert torch.equal(kept[1], recomputed[1]) and torch.equal(kept[2], recomputed[2])
+    refs = ref.attention_bwd(q, k, v, cos, sin, do, doc_ids=doc.cpu())
+    for grads in (kept, recomputed):
+        for got, want, name in zip(grads, refs, ("dq", "dk", "dv")):
+            assert rel_max(got, want) <= TOL[dtype], name
+
+
 @pytest.mark.parametrize("cfg", [CASES[0], CASES[3], CASES[5]], ids=lambda c: "-".join(map(str, c)))
 def test_capture(cfg):
     dtype, B, S, Hq, Hkv, D, layout = cfg
