@@ -765,7 +765,8 @@ __device__ __forceinline__ void wait_vm(int n) {
 // rows by ds_read_b64_tr_b16 (lds_frag_t), dS^T from the records by the same
 // instruction, which turns a record's one-key-per-lane layout into one row per
 // lane.  The kernel moves the dS bytes once and does one product per element;
-// it is bound by HBM.
+// it is bound by HBM.  With packed documents (DOC) the steps walk only the key
+// tiles listed for the query tile, two record columns per 64-key tile.
 template <int D, int HB, bool DOC>
 __global__ __launch_bounds__(64 * HB) void bwd_dq_ds_kernel(
     const u32x4* __restrict__ dsb, const bf16* __restrict__ krot, const float* __restrict__ cos,
