@@ -735,51 +735,37 @@ __device__ __forceinline__ void dma16_nt(uint32_t lds, uint32_t voff, const void
                : "memory", "m0");
 }
 
-// s_waitcnt vmcnt(n) for a wavefront-uniform n in [0, 15]
-__device__ __forceinline__ void wait_vm(int n) {
-  switch (n) {
-    case 0: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
-    case 1: asm volatile("s_waitcnt vmcnt(1)" ::: "memory"); break;
-    case 2: asm volatile("s_waitcnt vmcnt(2)" ::: "memory"); break;
-    case 3: asm volatile("s_waitcnt vmcnt(3)" ::: "memory"); break;
-    case 4: asm volatile("s_waitcnt vmcnt(4)" ::: "memory"); break;
-    case 5: asm volatile("s_waitcnt vmcnt(5)" ::: "memory"); break;
-    case 6: asm volatile("s_waitcnt vmcnt(6)" ::: "memory"); break;
-    case 7: asm volatile("s_waitcnt vmcnt(7)" ::: "memory"); break;
-    case 8: asm volatile("s_waitcnt vmcnt(8)" ::: "memory"); break;
-    case 9: asm volatile("s_waitcnt vmcnt(9)" ::: "memory"); break;
-    case 10: asm volatile("s_waitcnt vmcnt(10)" ::: "memory"); break;
-    case 11: asm volatile("s_waitcnt vmcnt(11)" ::: "memory"); break;
-    case 12: asm volatile("s_waitcnt vmcnt(12)" ::: "memory"); break;
-    case 13: asm volatile("s_waitcnt vmcnt(13)" ::: "memory"); break;
-    case 14: asm volatile("s_waitcnt vmcnt(14)" ::: "memory"); break;
-    default: asm volatile("s_waitcnt vmcnt(15)" ::: "memory"); break;
-  }
+// s_waitcnt vmcnt(N)
+template <int N>
+__device__ __forceinline__ void vm_wait() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
 // dQ from the dS records: workgroup = HB query heads of one KV group x DSQ
 // positions, one wavefront per head (its 64 rows as two 32-row blocks, so each
 // K^T fragment feeds two products).  Per DSK-key step it stages the rotated K
 // rows [DSK][D] and the HB records into LDS (a ring of NBUF, loads issued
-// NBUF - 1 steps ahead) and accumulates dQ^T += K^T dS^T: K^T comes from the K
+// NBUF - 1 steps ahead: 4 for short sequences with 4 heads per workgroup,
+// where one workgroup per CU with three steps in flight does best, otherwise 3,
+// two workgroups per CU with two steps each) and accumulates dQ^T += K^T dS^T: K^T comes from the K
 // rows by ds_read_b64_tr_b16 (lds_frag_t), dS^T from the records by the same
 // instruction, which turns a record's one-key-per-lane layout into one row per
 // lane.  The kernel moves the dS bytes once and does one product per element;
 // it is bound by HBM.  With packed documents (DOC) the steps walk only the key
 // tiles listed for the query tile, two record columns per 64-key tile.
-template <int D, int HB, bool DOC>
+template <int D, int HB, bool DOC, int NBUF>
 __global__ __launch_bounds__(64 * HB) void bwd_dq_ds_kernel(
     const u32x4* __restrict__ dsb, const bf16* __restrict__ krot, const float* __restrict__ cos,
     const float* __restrict__ sin, bf16* __restrict__ dq, int S, int P, int Hq, int Hkv,
     int n_rep, int nqt, int causal, float scale, const int32_t* __restrict__ doc,
     const int2* __restrict__ ranges) {
   constexpr int NW = HB, KR = D / 8, DT = D / 32, HALF = D / 2;
-  constexpr int NBUF = 3;
+  static_assert(NBUF == 3 || NBUF == 4, "ring depth");
   constexpr int KI = DSK * KR / 64;  // 1 KB load instructions per K step
   static_assert(KI % NW == 0, "K rows must split evenly over the wavefronts");
   // load instructions per wavefront and step: its share of K, its record's 4 KB
   constexpr int NLOAD = KI / NW + 4;
-  static_assert(NLOAD <= 15, "wait_vm range");
   struct Stage {
     bf16 k[DSK * D];
     u32x4 ds[HB * 256];
@@ -859,8 +845,14 @@ __global__ __launch_bounds__(64 * HB) void bwd_dq_ds_kernel(
   for (int t = 0; t < NBUF - 1; ++t)
     if (t < nk) stage(t, t);
   for (int t = 0; t < nk; ++t) {
-    // step t's loads are in; the next step's may still fly
-    wait_vm(t + 1 < nk ? NLOAD : 0);
+    // step t's loads are in; those of up to NBUF - 2 later steps may still fly
+    const int ahead = min(NBUF - 2, nk - 1 - t);
+    if (ahead >= 2)
+      vm_wait<2 * NLOAD>();
+    else if (ahead == 1)
+      vm_wait<NLOAD>();
+    else
+      vm_wait<0>();
     __syncthreads();  // every wavefront's share landed; step t - 1's buffer is free
     if (t + NBUF - 1 < nk) stage(t + NBUF - 1, (t + NBUF - 1) % NBUF);
     const Stage& S_ = st[t % NBUF];
@@ -957,7 +949,12 @@ Ws carve(void* base, int B, int S, int Hq, int Hkv, int D) {
 template <int D, int HB>
 int launch_dq_ds(const BwdArgs& a, const Ws& w) {
   const int P = pad_len(a.S), n_rep = a.Hq / a.Hkv, nqt = (a.S + DSQ - 1) / DSQ;
-  KF_LAUNCH("bwd_dq_ds", (a.doc ? bwd_dq_ds_kernel<D, HB, true> : bwd_dq_ds_kernel<D, HB, false>),
+  // ring depth by sequence length (measured with 4 heads per workgroup: 4
+  // buffers 485 against 517 us at S = 4096, 3115 against 2967 at S = 16384)
+  const bool deep = HB == 4 && a.S <= 8192;
+  KF_LAUNCH("bwd_dq_ds",
+            (a.doc ? (deep ? bwd_dq_ds_kernel<D, HB, true, 4> : bwd_dq_ds_kernel<D, HB, true, 3>)
+                   : (deep ? bwd_dq_ds_kernel<D, HB, false, 4> : bwd_dq_ds_kernel<D, HB, false, 3>)),
             dim3(a.B * a.Hkv * (n_rep / HB) * nqt), dim3(64 * HB), 0, a.stream, w.dsb, w.krot,
             a.cos, a.sin, (bf16*)a.dq, a.S, P, a.Hq, a.Hkv, n_rep, nqt, a.causal, a.scale,
             a.doc, w.ranges);
