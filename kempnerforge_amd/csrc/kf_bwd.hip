@@ -319,6 +319,17 @@ __device__ __forceinline__ void dkdv_role(
                rec_head) * 256;
       asm volatile("" : "+s"(rec));
     }
+    if (DSROLE) {
+      // dP - Delta while P is still on its way: only the product with P is
+      // left between the barrier and the dK products
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int gq = 0; gq < 4; ++gq)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) x[mt][4 * gq + j] -= rowv[4 * mt + gq][j];
+      asm volatile("" : "+v"(x[0]), "+v"(x[1]));
+    }
     __syncthreads();  // P of this tile is in LDS
     if (DSROLE) {
 #pragma unroll
@@ -329,7 +340,6 @@ __device__ __forceinline__ void dkdv_role(
 #pragma unroll
           for (int half = 0; half < 2; ++half) {
             const int gq = 2 * cc + half;
-            const f32x4 d4 = rowv[4 * mt + gq];
             float v[4];
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
@@ -338,7 +348,7 @@ __device__ __forceinline__ void dkdv_role(
               v[2 * j + 1] = __uint_as_float(word & 0xffff0000u);
             }
 #pragma unroll
-            for (int j = 0; j < 4; ++j) v[j] *= x[mt][4 * gq + j] - d4[j];
+            for (int j = 0; j < 4; ++j) v[j] *= x[mt][4 * gq + j];
             pk[2 * mt + cc][2 * half] = pack2(v[0], v[1]);
             pk[2 * mt + cc][2 * half + 1] = pack2(v[2], v[3]);
           }
