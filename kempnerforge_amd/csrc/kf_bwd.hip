@@ -310,6 +310,7 @@ __device__ __forceinline__ void dkdv_role(
 #pragma unroll
       for (int c = 0; c < 4; ++c) myP[c * 64] = pk[c];
     }
+    bf16x8 fpre[PF];  // dS waves: first phase-2 fragments, read before the barrier
     // record of this tile (-1: above the causal diagonal, nothing to keep)
     int64_t rec = -1;
     if (STORE && DSROLE) {
@@ -320,8 +321,8 @@ __device__ __forceinline__ void dkdv_role(
       asm volatile("" : "+s"(rec));
     }
     if (DSROLE) {
-      // dP - Delta while P is still on its way: only the product with P is
-      // left between the barrier and the dK products
+      // dP - Delta and the first dK fragments while P is still on its way:
+      // only the product with P is left between the barrier and the dK products
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
@@ -329,6 +330,8 @@ __device__ __forceinline__ void dkdv_role(
 #pragma unroll
           for (int j = 0; j < 4; ++j) x[mt][4 * gq + j] -= rowv[4 * mt + gq][j];
       asm volatile("" : "+v"(x[0]), "+v"(x[1]));
+#pragma unroll
+      for (int n = 0; n < PF; ++n) fpre[n] = lds_frag_t<D>(second_tile(S_), tro, n / DT, n % DT);
     }
     __syncthreads();  // P of this tile is in LDS
     if (DSROLE) {
@@ -364,7 +367,8 @@ __device__ __forceinline__ void dkdv_role(
       const bf16* tA = second_tile(S_);
       bf16x8 fa[NS];
 #pragma unroll
-      for (int n = 0; n < PF; ++n) fa[n] = lds_frag_t<D>(tA, tro, n / DT, n % DT);
+      for (int n = 0; n < PF; ++n)
+        fa[n] = DSROLE ? fpre[n] : lds_frag_t<D>(tA, tro, n / DT, n % DT);
 #pragma unroll
       for (int n = 0; n < NS; ++n) {
         __builtin_amdgcn_sched_barrier(0);
