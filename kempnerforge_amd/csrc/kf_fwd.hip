@@ -402,9 +402,14 @@ __global__ __launch_bounds__(256, 2) void capture_probs_mfma_kernel(
   load_q_frag<D>(q, cos, sin, ri, Sq, Hq, hh, qf);
   __syncthreads();
 
-  // per-lane rows this lane stores (register i -> row 8*(i/4)+4h+(i%4) of the
-  // wave): their P row pointers, log2-domain LSE and positions, hoisted out of
-  // the tile loop
+  // per-lane rows of the C layout (register i -> row 8*(i/4)+4h+(i%4) of the
+  // wave): log2-domain LSE, positions and (DOC/KPM) document or guard flag,
+  // hoisted out of the tile loop.  After the probabilities of both 32-key
+  // halves of a tile are formed, v_permlane32_swap exchanges the upper half of
+  // register i of the first with the lower half of the second, so each register
+  // then holds 64 consecutive keys of one row (row 8*(i/4)+(i%4) in the first,
+  // +4 in the second): one store writes 256 contiguous bytes.  Those rows are
+  // wavefront-uniform, so their P offsets live in scalar registers.
   const int qmax = min(ri.p0 + bm_pos, Sq) - 1;  // largest position in the block
   const int ntiles_all = (Sk + BN - 1) / BN;
   // KPM: first valid key of the batch row; rows before it are guarded
@@ -413,19 +418,20 @@ __global__ __launch_bounds__(256, 2) void capture_probs_mfma_kernel(
                                                       : ntiles_all;
   const bf16* kbase = krot + (int64_t)bh * Skp * D;
   float* pbase = probs + (((int64_t)ri.b * Hq + (int64_t)ri.g * n_rep) * Sq + ri.p0) * Sk;
-  float* prow[16];
   float lrow[16];
   int posr[16];
   int drw[16];  // DOC: document of each row; KPM: 1 for a guarded row
+  int roff[16][2];  // P row offset (Sk floats) of the stored rows, -1: no row
   const int32_t* drow = DOC || KPM ? aux + (int64_t)ri.b * Sk : nullptr;
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     const int r = w * 32 + 8 * (i >> 2) + 4 * hh + (i & 3);
-    const int off = sRowOff[r];
-    prow[i] = off < 0 ? nullptr : pbase + (int64_t)off * Sk;
     lrow[i] = sL[r];
     posr[i] = ri.p0 + (r % bm_pos);
     drw[i] = DOC ? drow[min(posr[i], Sq - 1)] : KPM ? (int)(posr[i] < fv) : 0;
+#pragma unroll
+    for (int h2 = 0; h2 < 2; ++h2)
+      roff[i][h2] = __builtin_amdgcn_readfirstlane(sRowOff[w * 32 + 8 * (i >> 2) + 4 * h2 + (i & 3)]);
   }
 
   // K tiles double-buffered: tile t+1 loads while tile t is computed and stored
@@ -436,6 +442,7 @@ __global__ __launch_bounds__(256, 2) void capture_probs_mfma_kernel(
     if (t + 1 < ntiles) tile_to_lds<BN, KR>(kbase + (int64_t)(t + 1) * BN * D, D, sK[(t + 1) & 1], w, lane);
     const bf16* tK = sK[t & 1];
     const bool diag = (causal && t * BN + BN - 1 > ri.p0) || t * BN + BN > Sk;
+    f32x16 pv[2];
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
       f32x16 sv;
@@ -450,16 +457,24 @@ __global__ __launch_bounds__(256, 2) void capture_probs_mfma_kernel(
       const int kd = DOC || KPM ? drow[min(key, Sk - 1)] : 0;
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        if (prow[i] == nullptr) continue;
         float p = fast_exp2(sv[i] * scale_log2 - lrow[i]);
         const bool guarded = KPM && drw[i];
-        if (diag) {
-          if (key >= Sk) continue;
-          if (causal && key > posr[i] && !guarded) p = 0.f;
-        }
+        if (diag && causal && key > posr[i] && !guarded) p = 0.f;
         if (DOC && kd != drw[i]) p = 0.f;
         if (KPM && !guarded && kd == 0) p = 0.f;
-        prow[i][key] = p;
+        pv[nt][i] = p;
+      }
+    }
+    const int key = t * BN + lane;  // this lane's key after the swap
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(pv[0][i]),
+                                                       __float_as_uint(pv[1][i]), false, false);
+#pragma unroll
+      for (int h2 = 0; h2 < 2; ++h2) {
+        if (roff[i][h2] < 0) continue;
+        if (diag && key >= Sk) continue;
+        pbase[(int64_t)roff[i][h2] * Sk + key] = __uint_as_float(sw[h2]);
       }
     }
   }
