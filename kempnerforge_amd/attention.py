@@ -18,9 +18,14 @@ Paths (reference lines in ``kempnerforge/model/attention.py``):
 * explicit masks without a cache (``:190-227``): ``doc_ids`` (packed
   documents) and ``key_padding_mask`` (padded keys, with the reference's NaN
   guard) run in the same kernels, the conditions applied per tile, so no
-  ``[B,1,S,S]`` mask is built (capture included).
-
-Capture with a cache and an explicit mask keeps the reference's PyTorch code.
+  ``[B,1,S,S]`` mask is built (capture included);
+* capture with a cache and an explicit mask (``:169-170,252-271``): the
+  reference appends to the cache and then builds an ``[S, S_kv]`` mask that
+  only broadcasts against the ``[B,1,S,S]`` document / padding masks when the
+  cache was empty.  Here the new tokens are appended likewise; on an empty
+  cache the capture kernel runs with the masks (the cache then holds exactly
+  this call's rotated keys), on a non-empty one a RuntimeError is raised, as
+  the reference's mask construction raises one.
 """
 
 from __future__ import annotations
@@ -29,7 +34,6 @@ import contextlib
 
 import torch
 import torch.nn as nn
-import torch.nn.functional as F
 from torch.nn.attention import SDPBackend, sdpa_kernel
 
 from kempnerforge_amd import ops
@@ -71,14 +75,31 @@ class KVCache:
                              device=device)
         self.v = torch.zeros(batch_size, n_kv_heads, max_seq_len, head_dim, dtype=dtype,
                              device=device)
-        self.seq_len = 0
         self.lens = torch.zeros(batch_size, dtype=torch.int32, device=device)
+        self._seq_len = 0
         self.rope_tables: tuple[torch.Tensor, torch.Tensor] | None = None
         self.ragged = False
 
     @property
     def max_seq_len(self) -> int:
         return self.k.shape[2]
+
+    @property
+    def seq_len(self) -> int:
+        """Fill level of the batch (the longest sequence's for a ragged cache)."""
+        return self._seq_len
+
+    @seq_len.setter
+    def seq_len(self, value: int) -> None:
+        """Writable as in the reference (a caller may rewind a cache to reuse
+        it): every sequence is set to this fill level, so the per-sequence
+        ``lens`` the decode kernel reads follow (no host synchronisation)."""
+        value = int(value)
+        if not 0 <= value <= self.max_seq_len:
+            raise ValueError(f"seq_len must lie in [0, {self.max_seq_len}] (got {value})")
+        self._seq_len = value
+        self.lens.fill_(value)
+        self.ragged = False
 
     def update(self, k_new: torch.Tensor, v_new: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
         """Append already-rotated ``(B, n_kv_heads, new_len, head_dim)`` keys and
@@ -103,7 +124,7 @@ class KVCache:
         if min(lengths) < 0 or max(lengths) > self.max_seq_len:
             raise ValueError(f"lengths must lie in [0, {self.max_seq_len}]")
         self.lens.copy_(torch.tensor(lengths, dtype=torch.int32))
-        self.seq_len = max(lengths)
+        self._seq_len = max(lengths)
         self.ragged = len(set(lengths)) > 1
 
     def use_rope_tables(self, cos: torch.Tensor, sin: torch.Tensor) -> None:
@@ -128,19 +149,8 @@ class KVCache:
             )
 
     def _advance(self, new_len: int) -> None:
-        self.seq_len += new_len
+        self._seq_len += new_len
         self.lens.add_(new_len)
-
-
-def _apply_rope_torch(x, cos, sin):
-    """The reference's ``apply_rope`` (``kempnerforge/model/position.py:43-71``),
-    used only by the explicit-mask branch, which is outside the kernel path."""
-    d = x.shape[-1] // 2
-    x1, x2 = x[..., :d], x[..., d:]
-    shape = [1] * (x.ndim - 2) + list(cos.shape)
-    c = cos.view(*shape).to(x.dtype)
-    s = sin.view(*shape).to(x.dtype)
-    return torch.cat([x1 * c - x2 * s, x2 * c + x1 * s], dim=-1)
 
 
 class Attention(nn.Module):
@@ -209,12 +219,19 @@ class Attention(nn.Module):
 
         if self.capture_attention_weights:
             if masked and kv_cache is not None:
-                out = self._masked_attention(q, k, v, rope_cos, rope_sin, seq_len, doc_ids,
-                                             kv_cache, key_padding_mask)
-            else:
-                out, probs = self._capture(q, k, v, rope_cos, rope_sin, kv_cache, doc_ids,
-                                           key_padding_mask)
-                self.last_attention_weights = probs.to(q.dtype).detach().cpu()
+                # the reference appends first (:169-170), then builds the masks
+                start = kv_cache.seq_len
+                self._append(k, v, rope_cos, rope_sin, kv_cache)
+                if start != 0:
+                    raise RuntimeError(
+                        "capture with doc_ids / key_padding_mask over a non-empty KV cache: "
+                        f"the causal mask is [{seq_len}, {start + seq_len}] but the "
+                        f"document / padding masks cover {seq_len} keys")
+                # empty cache: its keys are this call's, rotated as the kernel rotates them
+                kv_cache = None
+            out, probs = self._capture(q, k, v, rope_cos, rope_sin, kv_cache, doc_ids,
+                                       key_padding_mask)
+            self.last_attention_weights = probs.to(q.dtype).detach().cpu()
         elif masked:
             assert kv_cache is None, (
                 "doc_ids / key_padding_mask are not supported with kv_cache decode "
@@ -268,41 +285,3 @@ class Attention(nn.Module):
         out, probs, _ = ops.capture_raw(q, kc, vc, rope_cos, rope_sin, causal=seq_len > 1,
                                         k_rotated=True, k_layout="bhsd")
         return out, probs
-
-    def _masked_attention(self, q, k, v, rope_cos, rope_sin, seq_len, doc_ids, kv_cache,
-                          key_padding_mask):
-        """Capture with a cache and an explicit mask, kept as the reference's
-        PyTorch code (``kempnerforge/model/attention.py:238-271``): the manual
-        variant appends to the cache first, as the reference does."""
-        batch = q.shape[0]
-        q = _apply_rope_torch(q.transpose(1, 2), rope_cos, rope_sin)
-        if self.capture_attention_weights and kv_cache is not None:
-            kc, vc = self._append(k, v, rope_cos, rope_sin, kv_cache)
-            k, v = kc, vc
-        else:
-            assert kv_cache is None, (
-                "doc_ids / key_padding_mask are not supported with kv_cache decode "
-                "(would build an incorrect causal mask)."
-            )
-            k = _apply_rope_torch(k.transpose(1, 2), rope_cos, rope_sin)
-            v = v.transpose(1, 2)
-        if self.n_rep > 1:
-            k = k.repeat_interleave(self.n_rep, dim=1)
-            v = v.repeat_interleave(self.n_rep, dim=1)
-        seq_len_kv = k.shape[2]
-        mask = torch.ones(seq_len, seq_len_kv, dtype=torch.bool, device=q.device).tril()
-        mask = mask.unsqueeze(0).unsqueeze(0)
-        if doc_ids is not None:
-            mask = mask & (doc_ids.unsqueeze(2) == doc_ids.unsqueeze(1)).unsqueeze(1)
-        if key_padding_mask is not None:
-            mask = mask & key_padding_mask.view(batch, 1, 1, seq_len_kv)
-        mask = mask | ~mask.any(dim=-1, keepdim=True)
-        if self.capture_attention_weights:
-            attn = torch.matmul(q, k.transpose(-2, -1)) * self.head_dim**-0.5
-            attn = F.softmax(attn.masked_fill(~mask, float("-inf")), dim=-1)
-            self.last_attention_weights = attn.detach().cpu()
-            out = torch.matmul(attn, v)
-        else:
-            with self._sdpa_context():
-                out = F.scaled_dot_product_attention(q, k, v, attn_mask=mask)
-        return out.transpose(1, 2)

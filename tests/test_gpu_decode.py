@@ -133,9 +133,10 @@ def test_stale_rows_are_not_read():
 
 
 def test_consecutive_steps_and_bad_length():
-    """Three decode steps in a row on the same caches (the workspace's
-    completion counters must come back to zero after every call), one sequence
-    with an out-of-range length (NaN output, caches untouched)."""
+    """Three decode steps in a row on the same caches and a fresh workspace
+    each (nothing one call leaves behind may change the next one's result),
+    then one sequence with an out-of-range length (NaN output, caches
+    untouched)."""
     B, Hq, Hkv, D, Smax = 3, 8, 2, 128, 1200
     announce("decode consecutive steps")
     cos, sin = ref.rope_tables(D, Smax, 5e5)

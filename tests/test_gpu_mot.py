@@ -179,5 +179,9 @@ def test_backward_matches_and_reaches_every_projection():
     for name, p in attn.named_parameters():
         want = dict(cpu.named_parameters())[name].grad
         assert p.grad is not None and p.grad.abs().sum() > 0, name
-        scale = max(1.0, want.abs().max().item())
-        assert max_abs(p.grad, want) <= 1e-4 * scale, name
+        # weight gradients sum over every position: per-element 1e-4 absolute
+        # plus 1e-4 relative (module level, after the fp32 projections)
+        err = (p.grad.detach().cpu().double() - want).abs()
+        ratio = (err / (1e-4 * (1.0 + want.abs()))).max().item()
+        print(f"[{name}] max-abs err {err.max().item():.3e}; worst err/bound {ratio:.3f}")
+        assert ratio <= 1.0, name

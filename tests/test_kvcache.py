@@ -51,3 +51,21 @@ def test_set_lengths_validation():
         c.set_lengths([1, 2])
     with pytest.raises(ValueError):
         c.set_lengths([1, 2, 17])
+
+
+def test_seq_len_is_writable_and_moves_lens():
+    """The reference's seq_len is a plain attribute a caller may rewind to reuse
+    a cache; lens (what the decode kernel reads) must follow it."""
+    c = _cache()
+    c.update(torch.randn(3, 2, 7, 8), torch.randn(3, 2, 7, 8))
+    c.seq_len = 2
+    assert c.seq_len == 2 and c.lens.tolist() == [2, 2, 2] and not c.ragged
+    c.set_lengths([1, 5, 3])
+    c.seq_len = 0  # rewinding a ragged cache makes it uniform again
+    assert c.lens.tolist() == [0, 0, 0] and not c.ragged
+    c.update(torch.randn(3, 2, 4, 8), torch.randn(3, 2, 4, 8))
+    assert c.seq_len == 4 and c.lens.tolist() == [4, 4, 4]
+    with pytest.raises(ValueError):
+        c.seq_len = 17
+    with pytest.raises(ValueError):
+        c.seq_len = -1
