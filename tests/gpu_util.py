@@ -39,7 +39,7 @@ def half_ulp(x: torch.Tensor, dtype) -> torch.Tensor:
     return torch.exp2(torch.floor(torch.log2(a)) - _SIG_BITS[dtype])
 
 
-def grad_bound(want: torch.Tensor, dtype) -> torch.Tensor:
+def grad_bound(want: torch.Tensor, dtype, group: int = 1) -> torch.Tensor:
     """Per-element bound on |got - want| for a gradient stored in ``dtype``.
 
     float32: the absolute 1e-5.  bfloat16 / float16: 2e-2 plus half an ulp of
@@ -50,18 +50,25 @@ def grad_bound(want: torch.Tensor, dtype) -> torch.Tensor:
     error is near half an ulp fails with any computation error on top), so the
     2e-2 applies to the value before the output rounding.  For |g| < 1 the
     bound is at most 2e-2 + 2^-9.
+
+    ``group``: the number of query heads a dK / dV element sums (n_rep).  Each
+    head's contribution carries the rounding of its bf16 P and dS tiles (the
+    MFMA operands), independent from head to head, so the sum's error grows as
+    the square root of the number of heads; the 2e-2 is stated for the
+    benchmark shapes (groups of 4 and 8) and scales by sqrt(group / 8) above
+    that (a group of 32: 4e-2).
     """
     if dtype == torch.float32:
         return torch.full_like(want.double(), TOL[torch.float32])
-    return TOL[dtype] + half_ulp(want, dtype)
+    return TOL[dtype] * max(1.0, group / 8.0) ** 0.5 + half_ulp(want, dtype)
 
 
-def check_grad(got, want, dtype, name: str) -> float:
-    """Assert |got - want| <= grad_bound(want) for every element; prints the
-    observed max-abs error and the worst ratio of error to bound."""
+def check_grad(got, want, dtype, name: str, group: int = 1) -> float:
+    """Assert |got - want| <= grad_bound(want, dtype, group) for every element;
+    prints the observed max-abs error and the worst ratio of error to bound."""
     w = want.detach().double().cpu()
     err = (got.detach().float().cpu().double() - w).abs()
-    ratio = (err / grad_bound(w, dtype)).max().item()
+    ratio = (err / grad_bound(w, dtype, group)).max().item()
     print(f"[{name}] max-abs err {err.max().item():.3e} (max |ref| {w.abs().max().item():.3g}); "
           f"worst err/bound {ratio:.3f}", flush=True)
     assert ratio <= 1.0, f"{name}: error {err.max().item():.3e} exceeds the per-element bound"

@@ -59,8 +59,8 @@ def test_shapes(cfg, causal):
     _, dq, dk, dv = _grads(q, k, v, do, cos, sin, causal)
     dq_r, dk_r, dv_r = ref.attention_bwd(q, k, v, cos, sin, do, causal=causal)
     check_grad(dq, dq_r, dtype, "dq")
-    check_grad(dk, dk_r, dtype, "dk")
-    check_grad(dv, dv_r, dtype, "dv")
+    check_grad(dk, dk_r, dtype, "dk", group=Hq // Hkv)
+    check_grad(dv, dv_r, dtype, "dv", group=Hq // Hkv)
 
 
 # n_rep 1, 2, 3, 4 and 8 (the dQ kernel groups 4, 2 or 1 query heads per
@@ -97,7 +97,8 @@ def test_kept_and_recomputed_ds(cfg, causal):
     refs = ref.attention_bwd(q, k, v, cos, sin, do, causal=causal)
     for path, grads in (("kept", kept), ("recomputed", recomputed)):
         for got, want, name in zip(grads, refs, ("dq", "dk", "dv")):
-            check_grad(got, want, torch.bfloat16, f"{path} {name}")
+            check_grad(got, want, torch.bfloat16, f"{path} {name}",
+                       group=Hq // Hkv if name != "dq" else 1)
 
 
 def test_llama8b_shape_one_group():

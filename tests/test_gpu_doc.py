@@ -113,7 +113,7 @@ def test_backward(cfg):
     torch.cuda.synchronize()
     dq, dk, dv = ref.attention_bwd(q, k, v, cos, sin, do, doc_ids=doc)
     for got, want, name in ((qd.grad, dq, "dq"), (kd.grad, dk, "dk"), (vd.grad, dv, "dv")):
-        check_grad(got, want, dtype, name)
+        check_grad(got, want, dtype, name, group=Hq // Hkv if name != "dq" else 1)
 
 
 BF16_CASES = [c for c in CASES if c[0] == torch.bfloat16]
@@ -139,7 +139,7 @@ def test_backward_kept_and_recomputed_ds(cfg):
     refs = ref.attention_bwd(q, k, v, cos, sin, do, doc_ids=doc.cpu())
     for path, grads in (("kept", kept), ("recomputed", recomputed)):
         for got, want, name in zip(grads, refs, ("dq", "dk", "dv")):
-            check_grad(got, want, dtype, f"{path} {name}")
+            check_grad(got, want, dtype, f"{path} {name}", group=Hq // Hkv if name != "dq" else 1)
 
 
 @pytest.mark.parametrize("cfg", [CASES[0], CASES[3], CASES[5]], ids=lambda c: "-".join(map(str, c)))

@@ -91,7 +91,7 @@ def test_backward(cfg):
     torch.cuda.synchronize()
     dq, dk, dv = ref.attention_bwd(q, k, v, cos, sin, do, key_padding_mask=kpm)
     for got, want, name in ((qd.grad, dq, "dq"), (kd.grad, dk, "dk"), (vd.grad, dv, "dv")):
-        check_grad(got, want, dtype, name)
+        check_grad(got, want, dtype, name, group=Hq // Hkv if name != "dq" else 1)
 
 
 @pytest.mark.parametrize("cfg", [CASES[1], CASES[3], CASES[4], CASES[5]],
@@ -128,7 +128,7 @@ def test_with_documents(dtype):
     torch.cuda.synchronize()
     assert max_abs(out, o_ref) <= TOL[dtype]
     for got, want, name in ((qd.grad, dq, "dq"), (kd.grad, dk, "dk"), (vd.grad, dv, "dv")):
-        check_grad(got, want, dtype, name)
+        check_grad(got, want, dtype, name, group=Hq // Hkv if name != "dq" else 1)
 
 
 def test_llama8b_shape_padded_keys_drop_out():
