@@ -134,14 +134,51 @@ def fwd_raw(q, k, v, cos, sin, *, causal: bool, k_rotated: bool, k_layout: str =
 
 
 _BWD_LOW_MEMORY = False
+# Largest share of the memory available to the caching allocator (free device
+# memory plus what it holds unused) that the kept dS tiles may take.
+_DS_BUDGET_FRACTION = 0.5
 
 
 def set_backward_low_memory(enabled: bool) -> None:
     """Default of ``bwd_raw``'s ``low_memory`` (and so of the autograd backward of
-    :func:`attention` and the ``Attention`` module): True trades ~5-11% of
-    backward time for not holding the kept dS tiles (about B*Hq*S*S bytes)."""
+    :func:`attention` and the ``Attention`` module): True never keeps the dS
+    tiles (about B*Hq*S*S bytes), trading ~5-11% of backward time for memory."""
     global _BWD_LOW_MEMORY
     _BWD_LOW_MEMORY = bool(enabled)
+
+
+def set_backward_ds_budget(fraction: float) -> None:
+    """Share (0..1] of the memory the allocator can still hand out that the
+    backward's kept dS tiles may take (default 0.5); above it the backward
+    falls back to recomputing S and dP for dQ."""
+    global _DS_BUDGET_FRACTION
+    if not 0.0 < fraction <= 1.0:
+        raise ValueError(f"fraction must lie in (0, 1] (got {fraction})")
+    _DS_BUDGET_FRACTION = float(fraction)
+
+
+def available_bytes(device) -> int | None:
+    """Bytes the caching allocator can hand out without growing past the
+    device: free device memory plus memory it reserves but does not use
+    (None if the runtime cannot say, e.g. inside some stream captures)."""
+    try:
+        free, _ = torch.cuda.mem_get_info(device)
+    except RuntimeError:
+        return None
+    idle = torch.cuda.memory_reserved(device) - torch.cuda.memory_allocated(device)
+    return int(free) + max(int(idle), 0)
+
+
+def keep_ds_tiles(extra_bytes: int, available: int | None, fraction: float | None = None) -> bool:
+    """Whether the backward keeps its dS tiles: their ``extra_bytes`` must fit in
+    ``fraction`` of the ``available`` bytes (the memory-aware default; the
+    reference's SDPA backward needs O(S) memory, so an unconditional O(S^2)
+    store could run a model that fits with the reference out of memory).
+    Unknown availability keeps them if the library offers them."""
+    fraction = _DS_BUDGET_FRACTION if fraction is None else fraction
+    if extra_bytes <= 0:
+        return False
+    return available is None or extra_bytes <= fraction * available
 
 
 def bwd_raw(q, k, v, cos, sin, out, lse, dout, *, causal: bool, doc_ids=None,
@@ -150,9 +187,12 @@ def bwd_raw(q, k, v, cos, sin, out, lse, dout, *, causal: bool, doc_ids=None,
 
     By default the workspace is sized so that the dK/dV pass keeps its bf16 dS
     tiles for dQ (``kf_attn_bwd_workspace_size_ds``: about B*Hq*S*S bytes
-    for causal attention, 2.1 GB at B=4, S=4096, Hq=32); ``low_memory=True``
-    passes the minimal workspace, and dQ recomputes S and dP instead (None:
-    the default set by :func:`set_backward_low_memory`, initially False).
+    for causal attention, 2.2 GB at B=4, S=4096, Hq=32) when those fit in the
+    budget of :func:`set_backward_ds_budget` (half the memory the allocator can
+    still hand out); otherwise, or with ``low_memory=True``, it passes the
+    minimal workspace and dQ recomputes S and dP (None: the default set by
+    :func:`set_backward_low_memory`, initially False).  dK and dV are the same
+    bits either way.
     """
     _require_gpu(q, k, v, out, lse, dout)
     lib = _lib.load()
@@ -167,14 +207,16 @@ def bwd_raw(q, k, v, cos, sin, out, lse, dout, *, causal: bool, doc_ids=None,
     dt = _dtype_code(q)
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
     nbytes = _lib.size_out()
+    _lib.check(lib.kf_attn_bwd_workspace_size(B, S, Hq, Hkv, D, dt, ctypes.byref(nbytes)),
+               "kf_attn_bwd_workspace_size")
     low_memory = _BWD_LOW_MEMORY if low_memory is None else low_memory
-    if low_memory or kv is not None:  # key padding never keeps dS
-        _lib.check(lib.kf_attn_bwd_workspace_size(B, S, Hq, Hkv, D, dt, ctypes.byref(nbytes)),
-                   "kf_attn_bwd_workspace_size")
-    else:
+    if not low_memory and kv is None:  # key padding never keeps dS
+        with_ds = _lib.size_out()
         _lib.check(lib.kf_attn_bwd_workspace_size_ds(B, S, Hq, Hkv, D, dt, int(causal),
-                                                     ctypes.byref(nbytes)),
+                                                     ctypes.byref(with_ds)),
                    "kf_attn_bwd_workspace_size_ds")
+        if keep_ds_tiles(with_ds.value - nbytes.value, available_bytes(q.device)):
+            nbytes = with_ds
     ws = _workspace(nbytes.value, q.device)
     _lib.check(lib.kf_attn_bwd(_ptr(q), _ptr(k), _ptr(v), _ptr(cos), _ptr(sin), _ptr(out),
                                _ptr(lse), _ptr(dout), _ptr(dq), _ptr(dk), _ptr(dv), _ptr(ws),

@@ -128,3 +128,18 @@ def test_oracle_not_imported_by_product():
             if f.endswith(".py"):
                 src = open(os.path.join(dirpath, f)).read()
                 assert "oracle" not in src, f
+
+
+def test_kept_ds_budget_decision():
+    """The backward keeps its dS tiles only within the memory budget (half of
+    what the allocator can still hand out by default)."""
+    from kempnerforge_amd import ops
+
+    gib = 1 << 30
+    assert ops.keep_ds_tiles(2 * gib, 10 * gib)
+    assert not ops.keep_ds_tiles(6 * gib, 10 * gib)
+    assert ops.keep_ds_tiles(6 * gib, 10 * gib, fraction=0.8)
+    assert not ops.keep_ds_tiles(0, 10 * gib)  # the library offers none (key padding, caps)
+    assert ops.keep_ds_tiles(1, None)          # availability unknown: keep
+    with pytest.raises(ValueError):
+        ops.set_backward_ds_budget(0.0)

@@ -101,6 +101,32 @@ def test_kept_and_recomputed_ds(cfg, causal):
                        group=Hq // Hkv if name != "dq" else 1)
 
 
+def test_ds_budget_switches_paths():
+    """The memory-aware default: with a budget too small for the dS tiles the
+    default backward takes the recomputing path (dQ equals low_memory=True bit
+    for bit), with a large one the kept-tile path; dK and dV are the same bits
+    on both paths."""
+    B, S, Hq, Hkv, D = 1, 1024, 8, 2, 128
+    announce("bwd dS budget switch")
+    q, k, v, do = (seeded((B, S, h, D), 20 + i, torch.bfloat16).to(DEV)
+                   for i, h in enumerate((Hq, Hkv, Hkv, Hq)))
+    cos, sin = (t.to(DEV) for t in ref.rope_tables(D, S, 5e5))
+    out, lse = ops.fwd_raw(q, k, v, cos, sin, causal=True, k_rotated=False)
+    rec = ops.bwd_raw(q, k, v, cos, sin, out, lse, do, causal=True, low_memory=True)
+    try:
+        ops.set_backward_ds_budget(1e-9)
+        small = ops.bwd_raw(q, k, v, cos, sin, out, lse, do, causal=True)
+        ops.set_backward_ds_budget(1.0)
+        large = ops.bwd_raw(q, k, v, cos, sin, out, lse, do, causal=True)
+    finally:
+        ops.set_backward_ds_budget(0.5)
+    torch.cuda.synchronize()
+    assert torch.equal(small[0], rec[0])
+    assert not torch.equal(large[0], rec[0])  # the kept tiles' dQ is other arithmetic
+    for a, b in ((small, rec), (large, rec)):
+        assert torch.equal(a[1], b[1]) and torch.equal(a[2], b[2])
+
+
 def test_llama8b_shape_one_group():
     """C3 at full size (B=4, S=4096, Hq=32, Hkv=8, D=128): the backward of KV
     group (b=1, g=6) against the oracle (groups are independent), plus
