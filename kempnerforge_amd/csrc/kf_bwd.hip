@@ -743,10 +743,8 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_kernel(
 
 // dma16 with the nontemporal (streaming) cache policy, for data read once
 __device__ __forceinline__ void dma16_nt(uint32_t lds, uint32_t voff, const void* base) {
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2 nt"
-               :
-               : "s"(lds), "v"(voff), "s"(base)
-               : "memory", "m0");
+  asm volatile("global_load_lds_dwordx4 %0, %1 nt" : : "v"(voff), "s"(base), "{m0}"(lds)
+               : "memory");
 }
 
 // s_waitcnt vmcnt(N)

@@ -93,18 +93,15 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 // all of them to land (vmcnt(0)), which serialises software-pipelined LDS
 // fragment reads.  Completion is therefore the caller's: an explicit
 // s_waitcnt vmcnt (lds_copy_wait) and, across wavefronts, a barrier, before
-// the data is read.  `lds` and `base` must be wavefront-uniform.
+// the data is read.  `lds` and `base` must be wavefront-uniform.  The LDS
+// address goes in m0 as an input operand bound to that register, so the
+// compiler itself writes m0 and knows its value (a clobber inside the asm
+// would leave any m0 value the compiler keeps live silently overwritten).
 __device__ __forceinline__ void dma16(uint32_t lds, uint32_t voff, const void* base) {
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
-               :
-               : "s"(lds), "v"(voff), "s"(base)
-               : "memory", "m0");
+  asm volatile("global_load_lds_dwordx4 %0, %1" : : "v"(voff), "s"(base), "{m0}"(lds) : "memory");
 }
 __device__ __forceinline__ void dma4(uint32_t lds, uint32_t voff, const void* base) {
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, %2"
-               :
-               : "s"(lds), "v"(voff), "s"(base)
-               : "memory", "m0");
+  asm volatile("global_load_lds_dword %0, %1" : : "v"(voff), "s"(base), "{m0}"(lds) : "memory");
 }
 
 // Copy a [ROWS_T][R chunks] bf16 tile whose rows start `ld` elements apart in
