@@ -12,17 +12,27 @@ on its own stream), the roofline of the dominant kernel, the forward alone
 (C2), the C3 step on packed documents (C3-doc; flops of same-document pairs
 only), the Llama-3-70B shape fwd+bwd (C5: B=1, S=16384, 64 query heads) and its
 2048-token probability capture (C5-cap), the KV-cache decode configuration C4
-in GB/s, and the reference's PyTorch path timed on the host CPU on a bounded
-sample of the same workload.
+in GB/s, and the reference's PyTorch paths timed on the host CPU (C3 sample,
+C4 decode, C5-cap capture) next to them.
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline]
+    python bench.py --only c3|c2|c3doc|c5|c5cap|c4 [--steps K] [--warmup W]
+        one workload: W untimed steps, K timed steps, then K steps with the
+        per-kernel event timing (the shape profiling runs use)
+    python bench.py --rocprof-summary DIR [DIR ...] --warmup W --steps K
+        markdown table of rocprofv3 outputs of --only runs (kernel trace and
+        --pmc counter collections), launches of the W warm-up steps dropped
 """
 
 from __future__ import annotations
 
 import argparse
+import csv
+import glob
 import json
 import os
+import re
+import statistics
 import sys
 import time
 
@@ -38,9 +48,20 @@ C3 = dict(B=4, S=4096, Hq=32, Hkv=8, D=128, theta=500000.0)
 C4 = dict(B=32, Hq=32, Hkv=8, D=128, lo=1024, hi=8192, theta=500000.0)
 C5 = dict(B=1, S=16384, Hq=64, Hkv=8, D=128, theta=500000.0, cap_tokens=2048)
 
+# what bounds each kernel (the roofline its "achieved" figure is quoted on)
+BOUND = {"fwd_mfma": "mfma", "bwd_dkdv": "mfma", "bwd_dq": "mfma", "bwd_dq_ds": "hbm",
+         "q_prep_bwd": "hbm", "kv_prep": "hbm", "decode_split": "hbm", "decode_merge": "hbm",
+         "capture_probs": "hbm", "capture_lse": "mfma"}
+
 
 def pairs(B, Hq, S):
     return B * Hq * S * (S + 1) // 2
+
+
+def ds_record_bytes(B, Hq, S):
+    """Bytes of the dS records the dK/dV kernel keeps for a causal launch."""
+    P = (S + 127) // 128 * 128
+    return B * Hq * P * (P + 64)
 
 
 def measured_traffic():
@@ -61,228 +82,325 @@ def seeded(shape, seed, dtype, dev):
     return torch.randn(*shape, generator=g).to(dtype).to(dev)
 
 
-def main() -> int:
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
-    ap.add_argument("--copy-calibration", action="store_true",
-                    help="first run one 256 MiB device-to-device copy (a kernel of known "
-                         "traffic, for scaling HBM byte counters)")
-    args = ap.parse_args()
-    if args.gpus != 1:
-        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the attention path "
-              "shards over (batch x KV-head group) with no exchange, so each GPU runs this "
-              "same single-GPU workload.", file=sys.stderr)
-        return 2
+# --------------------------------------------------------------------------- workloads
+class Workloads:
+    """Inputs and step functions of every benchmarked configuration."""
 
-    import torch
+    def __init__(self, dev):
+        import torch
 
-    from kempnerforge_amd import _lib, ops
-    from kempnerforge_amd.position import precompute_rope_frequencies
+        from kempnerforge_amd import ops
+        from kempnerforge_amd.position import precompute_rope_frequencies
 
-    dev = torch.device("cuda:0")
-    bf16 = torch.bfloat16
-    if args.copy_calibration:
-        src = torch.ones(64 * 1024 * 1024, dtype=torch.float32, device=dev)
-        dst = torch.empty_like(src)
-        dst.copy_(src)
-        torch.cuda.synchronize()
-        del src, dst
-    B, S, Hq, Hkv, D = (C3[k] for k in ("B", "S", "Hq", "Hkv", "D"))
-    q = seeded((B, S, Hq, D), 0, bf16, dev).requires_grad_(True)
-    k = seeded((B, S, Hkv, D), 1, bf16, dev).requires_grad_(True)
-    v = seeded((B, S, Hkv, D), 2, bf16, dev).requires_grad_(True)
-    do = seeded((B, S, Hq, D), 3, bf16, dev)
-    cos, sin = precompute_rope_frequencies(D, S, C3["theta"])
-    cos, sin = cos.to(dev), sin.to(dev)
-    P = pairs(B, Hq, S)
-    flops_step = 14.0 * D * P
+        self.torch, self.ops, self.dev = torch, ops, dev
+        self.rope = precompute_rope_frequencies
+        self.bf16 = torch.bfloat16
+        self._c3 = self._c5 = self._c4 = self._doc = None
 
-    def step():
-        out = ops.attention(q, k, v, cos, sin, causal=True)
-        torch.autograd.grad(out, (q, k, v), do)
+    # C3 / C2 / C3-doc share the 8B-shape tensors
+    def c3_inputs(self):
+        if self._c3 is None:
+            B, S, Hq, Hkv, D = (C3[k] for k in ("B", "S", "Hq", "Hkv", "D"))
+            q = seeded((B, S, Hq, D), 0, self.bf16, self.dev).requires_grad_(True)
+            k = seeded((B, S, Hkv, D), 1, self.bf16, self.dev).requires_grad_(True)
+            v = seeded((B, S, Hkv, D), 2, self.bf16, self.dev).requires_grad_(True)
+            do = seeded((B, S, Hq, D), 3, self.bf16, self.dev)
+            cos, sin = self.rope(D, S, C3["theta"])
+            self._c3 = (q, k, v, do, cos.to(self.dev), sin.to(self.dev))
+        return self._c3
 
-    for _ in range(args.warmup):
-        step()
+    def c3_step(self):
+        q, k, v, do, cos, sin = self.c3_inputs()
+        out = self.ops.attention(q, k, v, cos, sin, causal=True)
+        self.torch.autograd.grad(out, (q, k, v), do)
+
+    def c2_step(self):
+        q, k, v, _, cos, sin = self.c3_inputs()
+        self.ops.fwd_raw(q.detach(), k.detach(), v.detach(), cos, sin, causal=True,
+                         k_rotated=False)
+
+    def c3_raw_step(self):
+        q, k, v, do, cos, sin = self.c3_inputs()
+        qn, kn, vn = q.detach(), k.detach(), v.detach()
+        o, l = self.ops.fwd_raw(qn, kn, vn, cos, sin, causal=True, k_rotated=False)
+        return self.ops.bwd_raw(qn, kn, vn, cos, sin, o, l, do, causal=True)
+
+    def doc_inputs(self):
+        """C3 on packed sequences: documents of 64..2048 tokens (seed 7)."""
+        if self._doc is None:
+            torch = self.torch
+            B, S, Hq = C3["B"], C3["S"], C3["Hq"]
+            g = torch.Generator().manual_seed(7)
+            rows, vis = [], 0
+            for _ in range(B):
+                lens, left = [], S
+                while left:
+                    n = min(left, int(torch.randint(64, 2049, (1,), generator=g)))
+                    lens.append(n)
+                    left -= n
+                vis += Hq * sum(n * (n + 1) // 2 for n in lens)
+                rows.append(torch.cat([torch.full((n,), i, dtype=torch.int32)
+                                       for i, n in enumerate(lens)]))
+            ndocs = sum(int(r.max()) + 1 for r in rows)
+            self._doc = (torch.stack(rows).to(self.dev), vis, ndocs)
+        return self._doc
+
+    def c3doc_step(self):
+        q, k, v, do, cos, sin = self.c3_inputs()
+        doc = self.doc_inputs()[0]
+        out = self.ops.attention(q, k, v, cos, sin, causal=True, doc_ids=doc)
+        self.torch.autograd.grad(out, (q, k, v), do)
+
+    def c5_inputs(self):
+        if self._c5 is None:
+            B, S, Hq, Hkv, D = (C5[k] for k in ("B", "S", "Hq", "Hkv", "D"))
+            q = seeded((B, S, Hq, D), 0, self.bf16, self.dev).requires_grad_(True)
+            k = seeded((B, S, Hkv, D), 1, self.bf16, self.dev).requires_grad_(True)
+            v = seeded((B, S, Hkv, D), 2, self.bf16, self.dev).requires_grad_(True)
+            do = seeded((B, S, Hq, D), 3, self.bf16, self.dev)
+            cos, sin = self.rope(D, S, C5["theta"])
+            Sc = C5["cap_tokens"]
+            cap = tuple(t.detach()[:, :Sc].contiguous() for t in (q, k, v))
+            self._c5 = (q, k, v, do, cos.to(self.dev), sin.to(self.dev), cap)
+        return self._c5
+
+    def c5_step(self):
+        q, k, v, do, cos, sin, _ = self.c5_inputs()
+        out = self.ops.attention(q, k, v, cos, sin, causal=True)
+        self.torch.autograd.grad(out, (q, k, v), do)
+
+    def c5cap_step(self):
+        _, _, _, _, cos, sin, (qc, kc, vc) = self.c5_inputs()
+        Sc = C5["cap_tokens"]
+        self.ops.capture_raw(qc, kc, vc, cos[:Sc], sin[:Sc], causal=True, k_rotated=False)
+
+    def c5_free(self):
+        self._c5 = None
+
+    def c4_inputs(self):
+        if self._c4 is None:
+            torch = self.torch
+            g = torch.Generator().manual_seed(4)
+            B, Hq, Hkv, D = C4["B"], C4["Hq"], C4["Hkv"], C4["D"]
+            lens = torch.randint(C4["lo"], C4["hi"] + 1, (B,), generator=g, dtype=torch.int32)
+            Smax = C4["hi"] + 1
+            qn = seeded((B, 1, Hq, D), 0, self.bf16, self.dev)
+            kn = seeded((B, 1, Hkv, D), 1, self.bf16, self.dev)
+            vn = seeded((B, 1, Hkv, D), 2, self.bf16, self.dev)
+            kc = torch.randn(B, Hkv, Smax, D, device=self.dev, dtype=self.bf16)
+            vc = torch.randn(B, Hkv, Smax, D, device=self.dev, dtype=self.bf16)
+            cos, sin = self.rope(D, Smax, C4["theta"])
+            nbytes = sum(4 * (int(L) + 1) * Hkv * D for L in lens) + 4 * B * Hq * D \
+                + 4 * B * Hkv * D
+            self._c4 = (qn, kn, vn, kc, vc, lens, lens.to(self.dev), cos.to(self.dev),
+                        sin.to(self.dev), Smax, nbytes)
+        return self._c4
+
+    def c4_step(self):
+        qn, kn, vn, kc, vc, _, lens_d, cos, sin, Smax, _ = self.c4_inputs()
+        self.ops.decode_raw(qn, kn, vn, kc, vc, lens_d, cos, sin, rope_row_offset=0,
+                            max_len=Smax)
+
+
+def timed(torch, fn, warm, iters):
+    """Seconds per call of fn over iters calls after warm untimed ones,
+    bracketed by device synchronisations."""
+    for _ in range(warm):
+        fn()
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step()
+    t = time.perf_counter()
+    for _ in range(iters):
+        fn()
     torch.cuda.synchronize()
-    secs = time.perf_counter() - t0
-    ms_step = secs / args.steps * 1e3
-    value = flops_step / (ms_step * 1e-3) / 1e12
+    return (time.perf_counter() - t) / iters
 
-    # per-kernel timing over the same number of steps (separate pass: the event
-    # records would otherwise sit inside the timed region)
+
+def kernel_stats(torch, fn, iters):
+    """Per-kernel HIP-event averages over iters calls of fn."""
+    from kempnerforge_amd import _lib
+
     with _lib.KernelTimer() as kt:
-        for _ in range(args.steps):
-            step()
-        torch.cuda.synchronize()
-    kstats = {n: {"avg_us": t / c * 1e3, "launches": c} for n, (t, c) in kt.stats.items()}
-    # algorithmic flops per launch of each MFMA kernel (the backward's 10*D*P is
-    # 4*D*P of recomputed S and dP plus dV, dK -> dkdv kernel 8*D*P; dQ 2*D*P)
-    algo = {"fwd_mfma": 4.0 * D * P, "bwd_dkdv": 8.0 * D * P, "bwd_dq": 2.0 * D * P,
-            "bwd_dq_ds": 2.0 * D * P}
-    dom = max(kstats, key=lambda n: kstats[n]["avg_us"] * kstats[n]["launches"])
-    traffic = measured_traffic()
-    roof = None
-    if dom in algo:
-        ach = algo[dom] / (kstats[dom]["avg_us"] * 1e-6) / 1e12
-        roof = {"kernel": dom, "bound": "mfma", "achieved": round(ach, 1),
-                "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                "frac": round(ach / PEAK_BF16_TFLOPS, 4),
-                "traffic": traffic.get(f"{dom}@C3"),
-                "avg_us": round(kstats[dom]["avg_us"], 1)}
-    fwd_us = kstats.get("fwd_mfma", {}).get("avg_us")
-
-    def wall(fn, warm, iters):
-        for _ in range(warm):
-            fn()
-        torch.cuda.synchronize()
-        t = time.perf_counter()
         for _ in range(iters):
             fn()
         torch.cuda.synchronize()
-        return (time.perf_counter() - t) / iters
+    return {n: {"avg_us": t / c * 1e3, "launches": c} for n, (t, c) in kt.stats.items()}
+
+
+def roofline(kstats, algo, traffic, suffix):
+    """Roofline object of the kernel taking the most time: algorithmic flops
+    (mfma) or bytes (hbm) per launch over its event-timed average duration."""
+    dom = max(kstats, key=lambda n: kstats[n]["avg_us"] * kstats[n]["launches"])
+    if dom not in algo:
+        return None
+    bound = BOUND.get(dom, "mfma")
+    secs = kstats[dom]["avg_us"] * 1e-6
+    if bound == "mfma":
+        ach, peak, unit = algo[dom] / secs / 1e12, PEAK_BF16_TFLOPS, "TFLOP/s"
+    else:
+        ach, peak, unit = algo[dom] / secs / 1e9, PEAK_HBM_GBPS, "GB/s"
+    return {"kernel": dom, "bound": bound, "achieved": round(ach, 1), "peak": peak,
+            "unit": unit, "frac": round(ach / peak, 4),
+            "traffic": traffic.get(f"{dom}@{suffix}"),
+            "traffic_source": "profiles/hbm_traffic.json (rocprofv3 --pmc FETCH_SIZE, "
+                              "WRITE_SIZE; scaled by a device copy)",
+            "avg_us": round(kstats[dom]["avg_us"], 1)}
+
+
+# --------------------------------------------------------------------------- CPU legs
+def cpu_legs(args, torch, wl):
+    """The reference's PyTorch paths on the host CPU, on bounded samples."""
+    from oracle import cpu_baseline as cb
+
+    cores = cb.cpu_threads()
+    model = cb.cpu_model()
+    bf16 = torch.bfloat16
+    D = C3["D"]
+    out = {}
+    # C3: 1/16 of the step (one batch row, one KV group pair)
+    sample = dict(B=1, S=C3["S"], Hq=8, Hkv=2)
+    secs, reps, used = cb.time_fwd_bwd(sample["B"], sample["S"], sample["Hq"], sample["Hkv"], D,
+                                       C3["theta"], bf16, min_seconds=args.cpu_seconds)
+    fl = 14.0 * D * pairs(sample["B"], sample["Hq"], sample["S"])
+    out["c3"] = {"value": round(fl / secs / 1e12, 4), "unit": "TFLOP/s", "cores": cores,
+                 "kind": "port", "cpu": model,
+                 "sample": (f"reference PyTorch path (apply_rope -> repeat_interleave -> SDPA "
+                            f"is_causal, autograd) fwd+bwd on CPU, {str(used)[6:]}, B=1 "
+                            f"S={sample['S']} Hq=8 Hkv=2 D={D} (1/16 of C3), median of {reps}")}
+    # C4: the whole decode batch, one sequence at a time
+    lens = [int(x) for x in wl.c4_inputs()[5]]
+    Hq, Hkv = C4["Hq"], C4["Hkv"]
+    secs, reps, used = cb.time_decode(lens, Hq, Hkv, D, C4["theta"], bf16,
+                                      min_seconds=args.cpu_seconds, max_reps=10)
+    nbytes = wl.c4_inputs()[-1]
+    out["c4"] = {"value": round(nbytes / secs / 1e9, 3), "unit": "GB/s", "cores": cores,
+                 "kind": "port", "cpu": model,
+                 "sample": (f"reference decode step (RoPE at L_b, KVCache.update, "
+                            f"repeat_interleave of the cache, SDPA is_causal=False) on CPU, "
+                            f"{str(used)[6:]}, all {len(lens)} C4 sequences one at a time, "
+                            f"median of {reps}")}
+    # C5-cap: the whole 2048-token capture
+    Sc = C5["cap_tokens"]
+    secs, reps, used = cb.time_capture(Sc, C5["Hq"], C5["Hkv"], D, C5["theta"], bf16,
+                                       min_seconds=args.cpu_seconds, max_reps=10)
+    cap_bytes = capture_bytes()
+    out["c5cap"] = {"value": round(cap_bytes / secs / 1e9, 3), "unit": "GB/s", "cores": cores,
+                    "kind": "port", "cpu": model,
+                    "sample": (f"reference _attention_with_weights (matmul, scale, "
+                               f"masked_fill, softmax, matmul) on CPU, {str(used)[6:]}, the "
+                               f"full C5-cap slice [1,64,2048,2048], median of {reps}; bytes "
+                               f"counted as for the GPU (fp32 P written)")}
+    return out
+
+
+def capture_bytes():
+    Sc, Hq, Hkv, D = C5["cap_tokens"], C5["Hq"], C5["Hkv"], C5["D"]
+    return 4 * Hq * Sc * Sc + Sc * (Hq + 2 * Hkv) * D * 2 + Sc * Hq * D * 2
+
+
+# --------------------------------------------------------------------------- modes
+def run_only(args, torch, wl):
+    """One workload: W untimed steps, K timed steps, K event-timed steps."""
+    steps = {"c3": wl.c3_step, "c2": wl.c2_step, "c3doc": wl.c3doc_step, "c5": wl.c5_step,
+             "c5cap": wl.c5cap_step, "c4": wl.c4_step}
+    fn = steps[args.only]
+    secs = timed(torch, fn, args.warmup, args.steps)
+    ks = kernel_stats(torch, fn, args.steps)
+    print(json.dumps({"workload": args.only, "steps": args.steps, "warmup": args.warmup,
+                      "ms_per_step": round(secs * 1e3, 4),
+                      "kernels_us": {n: round(s["avg_us"], 1) for n, s in ks.items()},
+                      "launches": {n: s["launches"] for n, s in ks.items()}}), flush=True)
+    return 0
+
+
+def run_full(args, torch, wl):
+    B, S, Hq, Hkv, D = (C3[k] for k in ("B", "S", "Hq", "Hkv", "D"))
+    P = pairs(B, Hq, S)
+    flops_step = 14.0 * D * P
+    traffic = measured_traffic()
+
+    # C3: the headline step (autograd forward + backward)
+    secs = timed(torch, wl.c3_step, args.warmup, args.steps)
+    ms_step = secs * 1e3
+    value = flops_step / secs / 1e12
+    kstats = kernel_stats(torch, wl.c3_step, args.steps)
+    algo = {"fwd_mfma": 4.0 * D * P, "bwd_dkdv": 8.0 * D * P, "bwd_dq": 2.0 * D * P,
+            "bwd_dq_ds": float(ds_record_bytes(B, Hq, S))}
+    roof = roofline(kstats, algo, traffic, "C3")
+    fwd_us = kstats.get("fwd_mfma", {}).get("avg_us")
 
     # C2: forward only (out + LSE) on the same tensors
-    qn_, kn_, vn_ = q.detach(), k.detach(), v.detach()
-    c2_s = wall(lambda: ops.fwd_raw(qn_, kn_, vn_, cos, sin, causal=True, k_rotated=False),
-                args.warmup, args.steps)
+    c2_s = timed(torch, wl.c2_step, args.warmup, args.steps)
     c2 = {"config": "C2 llama3-8b fwd B=4 S=4096 Hq=32 Hkv=8 D=128", "ms": round(c2_s * 1e3, 4),
           "TFLOP/s": round(4.0 * D * P / c2_s / 1e12, 1)}
 
-    # C3 replayed from a HIP graph (the raw forward + backward calls captured
-    # once): the same kernels without per-launch host overhead or autograd
-    def raw_step():
-        o, l = ops.fwd_raw(qn_, kn_, vn_, cos, sin, causal=True, k_rotated=False)
-        return ops.bwd_raw(qn_, kn_, vn_, cos, sin, o, l, do, causal=True)
-
+    # C3 replayed from a HIP graph (the raw forward + backward captured once):
+    # the same kernels without per-launch host overhead or autograd
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):
         for _ in range(2):
-            raw_step()
+            wl.c3_raw_step()
     torch.cuda.current_stream().wait_stream(side)
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
-        raw_step()
-    c3g_s = wall(graph.replay, args.warmup, args.steps)
+        wl.c3_raw_step()
+    c3g_s = timed(torch, graph.replay, args.warmup, args.steps)
     c3_graph = {"config": "C3 step as one HIP graph replay (fwd_raw + bwd_raw)",
                 "ms": round(c3g_s * 1e3, 4), "TFLOP/s": round(flops_step / c3g_s / 1e12, 1)}
     del graph
 
-    # C3-doc: the C3 step on packed sequences (documents of 64..2048 tokens, seeded);
-    # flops count only same-document causal pairs, so the rate compares with C3's
-    g = torch.Generator().manual_seed(7)
-    doc_rows, doc_pairs = [], 0
-    for _ in range(B):
-        lens_, left = [], S
-        while left:
-            n = min(left, int(torch.randint(64, 2049, (1,), generator=g)))
-            lens_.append(n)
-            left -= n
-        doc_pairs += Hq * sum(n * (n + 1) // 2 for n in lens_)
-        doc_rows.append(torch.cat([torch.full((n,), i, dtype=torch.int32)
-                                   for i, n in enumerate(lens_)]))
-    doc_ids = torch.stack(doc_rows).to(dev)
-
-    def step_doc():
-        out = ops.attention(q, k, v, cos, sin, causal=True, doc_ids=doc_ids)
-        torch.autograd.grad(out, (q, k, v), do)
-
-    doc_s = wall(step_doc, args.warmup, args.steps)
-    c3doc = {"config": "C3-doc C3 with packed documents of 64..2048 tokens (seed 7), "
-                       f"{sum(int(r.max()) + 1 for r in doc_rows)} documents",
-             "ms": round(doc_s * 1e3, 4),
-             "TFLOP/s": round(14.0 * D * doc_pairs / doc_s / 1e12, 1),
-             "visible_pair_frac": round(doc_pairs / P, 4),
+    # C3-doc: flops count only same-document causal pairs
+    _, vis, ndocs = wl.doc_inputs()
+    doc_s = timed(torch, wl.c3doc_step, args.warmup, args.steps)
+    c3doc = {"config": f"C3-doc C3 with packed documents of 64..2048 tokens (seed 7), "
+                       f"{ndocs} documents",
+             "ms": round(doc_s * 1e3, 4), "TFLOP/s": round(14.0 * D * vis / doc_s / 1e12, 1),
+             "visible_pair_frac": round(vis / P, 4),
              "speedup_vs_dense_causal": round(ms_step / (doc_s * 1e3), 2)}
 
-    # C5: llama3-70b shape fwd+bwd, and C5-cap (probabilities of its first 2048 tokens)
-    B5, S5, Hq5, Hkv5 = C5["B"], C5["S"], C5["Hq"], C5["Hkv"]
-    q5 = seeded((B5, S5, Hq5, D), 0, bf16, dev).requires_grad_(True)
-    k5 = seeded((B5, S5, Hkv5, D), 1, bf16, dev).requires_grad_(True)
-    v5 = seeded((B5, S5, Hkv5, D), 2, bf16, dev).requires_grad_(True)
-    do5 = seeded((B5, S5, Hq5, D), 3, bf16, dev)
-    cos5, sin5 = precompute_rope_frequencies(D, S5, C5["theta"])
-    cos5, sin5 = cos5.to(dev), sin5.to(dev)
-
-    def step5():
-        out5 = ops.attention(q5, k5, v5, cos5, sin5, causal=True)
-        torch.autograd.grad(out5, (q5, k5, v5), do5)
-
-    c5_s = wall(step5, 2, max(5, args.steps // 2))
-    P5 = pairs(B5, Hq5, S5)
+    # C5 and C5-cap
+    P5 = pairs(C5["B"], C5["Hq"], C5["S"])
+    c5_s = timed(torch, wl.c5_step, 2, max(5, args.steps // 2))
+    k5 = kernel_stats(torch, wl.c5_step, max(3, args.steps // 4))
+    algo5 = {"fwd_mfma": 4.0 * D * P5, "bwd_dkdv": 8.0 * D * P5, "bwd_dq": 2.0 * D * P5,
+             "bwd_dq_ds": float(ds_record_bytes(C5["B"], C5["Hq"], C5["S"]))}
     c5 = {"config": "C5 llama3-70b fwd+bwd B=1 S=16384 Hq=64 Hkv=8 D=128",
           "ms": round(c5_s * 1e3, 3), "TFLOP/s": round(14.0 * D * P5 / c5_s / 1e12, 1),
-          "frac_of_peak": round(14.0 * D * P5 / c5_s / 1e12 / PEAK_BF16_TFLOPS, 4)}
-    Sc = C5["cap_tokens"]
-    qc, kc_, vc_ = (t.detach()[:, :Sc].contiguous() for t in (q5, k5, v5))
-    cap_s = wall(lambda: ops.capture_raw(qc, kc_, vc_, cos5[:Sc], sin5[:Sc], causal=True,
-                                         k_rotated=False), 2, args.steps)
-    cap_bytes = 4 * Hq5 * Sc * Sc + Sc * (Hq5 + 2 * Hkv5) * D * 2 + Sc * Hq5 * D * 2
+          "frac_of_peak": round(14.0 * D * P5 / c5_s / 1e12 / PEAK_BF16_TFLOPS, 4),
+          "kernels_us": {n: round(s["avg_us"], 1) for n, s in k5.items()},
+          "roofline": roofline(k5, algo5, traffic, "C5")}
+    cap_s = timed(torch, wl.c5cap_step, 2, args.steps)
+    kcap = kernel_stats(torch, wl.c5cap_step, args.steps)
+    cap_b = capture_bytes()
     c5cap = {"config": "C5-cap first 2048 tokens of C5, P [1,64,2048,2048] fp32",
-             "us": round(cap_s * 1e6, 1), "bytes": cap_bytes,
-             "GB/s": round(cap_bytes / cap_s / 1e9, 1),
-             "frac_of_hbm_peak": round(cap_bytes / cap_s / 1e9 / PEAK_HBM_GBPS, 4),
+             "us": round(cap_s * 1e6, 1), "bytes": cap_b, "GB/s": round(cap_b / cap_s / 1e9, 1),
+             "frac_of_hbm_peak": round(cap_b / cap_s / 1e9 / PEAK_HBM_GBPS, 4),
+             "kernels_us": {n: round(s["avg_us"], 1) for n, s in kcap.items()},
              "capture_kernel_traffic": traffic.get("capture_probs@C5-cap")}
-    del q5, k5, v5, do5, qc, kc_, vc_
+    wl.c5_free()
 
-    # decode (C4)
-    g = torch.Generator().manual_seed(4)
-    Bd, Hqd, Hkvd, Dd = C4["B"], C4["Hq"], C4["Hkv"], C4["D"]
-    lens = torch.randint(C4["lo"], C4["hi"] + 1, (Bd,), generator=g, dtype=torch.int32)
-    Smax = C4["hi"] + 1
-    qn = seeded((Bd, 1, Hqd, Dd), 0, bf16, dev)
-    kn = seeded((Bd, 1, Hkvd, Dd), 1, bf16, dev)
-    vn = seeded((Bd, 1, Hkvd, Dd), 2, bf16, dev)
-    kc = torch.randn(Bd, Hkvd, Smax, Dd, device=dev, dtype=bf16)
-    vc = torch.randn(Bd, Hkvd, Smax, Dd, device=dev, dtype=bf16)
-    dcos, dsin = precompute_rope_frequencies(Dd, Smax, C4["theta"])
-    dcos, dsin = dcos.to(dev), dsin.to(dev)
-    lens_d = lens.to(dev)
-    dec_bytes = sum(4 * (int(L) + 1) * Hkvd * Dd for L in lens) + 4 * Bd * Hqd * Dd \
-        + 4 * Bd * Hkvd * Dd
-
-    def dstep():
-        ops.decode_raw(qn, kn, vn, kc, vc, lens_d, dcos, dsin, rope_row_offset=0, max_len=Smax)
-
-    for _ in range(args.warmup):
-        dstep()
-    torch.cuda.synchronize()
+    # C4 decode
+    dec_bytes = wl.c4_inputs()[-1]
     n_dec = max(args.steps, 50)
-    t0 = time.perf_counter()
-    for _ in range(n_dec):
-        dstep()
-    torch.cuda.synchronize()
-    dec_us = (time.perf_counter() - t0) / n_dec * 1e6
-    with _lib.KernelTimer() as kt2:
-        for _ in range(n_dec):
-            dstep()
-        torch.cuda.synchronize()
-    dstats = {n: {"avg_us": t / c * 1e3, "launches": c} for n, (t, c) in kt2.stats.items()}
+    dec_s = timed(torch, wl.c4_step, args.warmup, n_dec)
+    dstats = kernel_stats(torch, wl.c4_step, n_dec)
     split_us = dstats.get("decode_split", {}).get("avg_us")
+    decode = {"config": "C4 B=32 Hq=32 Hkv=8 D=128 L~U[1024,8192] seed 4",
+              "bytes": dec_bytes, "us_per_step": round(dec_s * 1e6, 1),
+              "GB/s": round(dec_bytes / dec_s / 1e9, 1),
+              "frac_of_hbm_peak": round(dec_bytes / dec_s / 1e9 / PEAK_HBM_GBPS, 4),
+              "kernels_us": {n: round(s["avg_us"], 1) for n, s in dstats.items()},
+              "split_kernel_GB/s": round(dec_bytes / (split_us * 1e-6) / 1e9, 1)
+              if split_us else None,
+              "split_kernel_traffic": traffic.get("decode_split@C4")}
 
     cpu = None
     if not args.no_cpu_baseline:
-        from oracle import cpu_baseline
-
-        sample = dict(B=1, S=C3["S"], Hq=8, Hkv=2, D=D)
-        secs_cpu, reps, used = cpu_baseline.time_fwd_bwd(
-            sample["B"], sample["S"], sample["Hq"], sample["Hkv"], sample["D"], C3["theta"],
-            bf16, min_seconds=args.cpu_seconds)
-        fl = 14.0 * D * pairs(sample["B"], sample["Hq"], sample["S"])
-        cpu = {"value": round(fl / secs_cpu / 1e12, 4), "unit": "TFLOP/s",
-               "cores": torch.get_num_threads(), "kind": "port",
-               "sample": (f"reference PyTorch path (apply_rope -> repeat_interleave -> SDPA "
-                          f"is_causal, autograd) fwd+bwd on CPU, {str(used).replace('torch.', '')},"
-                          f" B=1 S={sample['S']} Hq=8 Hkv=2 D={D} (1/16 of C3), median of {reps}")}
+        legs = cpu_legs(args, torch, wl)
+        cpu = legs["c3"]
+        decode["cpu_baseline"] = legs["c4"]
+        c5cap["cpu_baseline"] = legs["c5cap"]
 
     line = {
         "metric": METRIC,
@@ -310,17 +428,118 @@ def main() -> int:
         "c3_doc": c3doc,
         "c5": c5,
         "c5_cap": c5cap,
-        "decode": {"config": "C4 B=32 Hq=32 Hkv=8 D=128 L~U[1024,8192] seed 4",
-                   "bytes": dec_bytes, "us_per_step": round(dec_us, 1),
-                   "GB/s": round(dec_bytes / (dec_us * 1e-6) / 1e9, 1),
-                   "frac_of_hbm_peak": round(dec_bytes / (dec_us * 1e-6) / 1e9 / PEAK_HBM_GBPS, 4),
-                   "kernels_us": {n: round(s["avg_us"], 1) for n, s in dstats.items()},
-                   "split_kernel_GB/s": round(dec_bytes / (split_us * 1e-6) / 1e9, 1)
-                   if split_us else None,
-                   "split_kernel_traffic": traffic.get("decode_split@C4")},
+        "decode": decode,
     }
     print(json.dumps(line), flush=True)
     return 0
+
+
+# --------------------------------------------------------------------------- rocprof summary
+def _short(name: str) -> str:
+    """Kernel symbol -> the launcher's name (kf::..._kernel<...> -> ...)."""
+    m = re.search(r"(kv_prep|fwd_mfma|q_prep_bwd|bwd_dkdv|bwd_dq_ds|bwd_dq|decode_split|"
+                  r"decode_merge|capture_probs_mfma|capture_lse|kv_append|append)_kernel", name)
+    if m:
+        return {"capture_probs_mfma": "capture_probs", "append": "kv_append"}.get(m.group(1),
+                                                                                 m.group(1))
+    return "copy" if "copyBuffer" in name else name[:40]
+
+
+def _drop_warmup(rows, warmup, steps, key):
+    """Per kernel, drop the launches of the warm-up steps (the first
+    warmup * launches-per-step of that kernel)."""
+    by = {}
+    for r in rows:
+        by.setdefault(key(r), []).append(r)
+    out = {}
+    for k, rs in by.items():
+        per = len(rs) // (warmup + 2 * steps) if len(rs) % (warmup + 2 * steps) == 0 else 0
+        out[k] = rs[warmup * per:] if per else rs
+    return out
+
+
+def rocprof_summary(dirs, warmup, steps):
+    lines = []
+    for d in dirs:
+        wl = os.path.basename(d.rstrip("/"))
+        trace = sorted(glob.glob(os.path.join(d, "**", "*kernel_trace.csv"), recursive=True))
+        pmc = sorted(glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True))
+        if trace:
+            with open(trace[0]) as f:
+                rows = [r for r in csv.DictReader(f) if "_ZN2kf" in r["Kernel_Name"]]
+            rows.sort(key=lambda r: int(r["Start_Timestamp"]))
+            by = _drop_warmup(rows, warmup, steps, lambda r: _short(r["Kernel_Name"]))
+            lines.append(f"\n{wl}: kernel trace ({trace[0]})\n")
+            lines.append("| kernel | launches | avg us | median us | min us | VGPR | AGPR | LDS B |")
+            lines.append("|---|---|---|---|---|---|---|---|")
+            for k, rs in sorted(by.items(), key=lambda kv: -sum(
+                    int(r["End_Timestamp"]) - int(r["Start_Timestamp"]) for r in kv[1])):
+                us = [(int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3 for r in rs]
+                r0 = rs[0]
+                lines.append(f"| {k} | {len(us)} | {statistics.mean(us):.1f} | "
+                             f"{statistics.median(us):.1f} | {min(us):.1f} | {r0['VGPR_Count']} |"
+                             f" {r0['Accum_VGPR_Count']} | {r0['LDS_Block_Size']} |")
+        for path in pmc:
+            with open(path) as f:
+                rows = list(csv.DictReader(f))
+            calib = {}
+            for r in rows:
+                if "copyBuffer" in r["Kernel_Name"]:
+                    calib[r["Counter_Name"]] = float(r["Counter_Value"])
+            rows = [r for r in rows if "_ZN2kf" in r["Kernel_Name"]]
+            disp = {}
+            for r in rows:
+                disp.setdefault((int(r["Dispatch_Id"]), _short(r["Kernel_Name"])), {})[
+                    r["Counter_Name"]] = float(r["Counter_Value"])
+            items = [(k[1], v) for k, v in sorted(disp.items())]
+            by = _drop_warmup(items, warmup, steps, lambda it: it[0])
+            names = sorted({c for _, v in items for c in v})
+            lines.append(f"\n{wl}: counters ({path})"
+                         + (f"; copy calibration {calib}" if calib else "") + "\n")
+            lines.append("| kernel | dispatches | " + " | ".join(names) + " |")
+            lines.append("|---|---|" + "---|" * len(names))
+            for k, its in sorted(by.items()):
+                vals = [statistics.mean(v[c] for _, v in its if c in v) for c in names]
+                lines.append(f"| {k} | {len(its)} | " + " | ".join(f"{x:.6g}" for x in vals)
+                             + " |")
+    print("\n".join(lines))
+    return 0
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--only", choices=("c3", "c2", "c3doc", "c5", "c5cap", "c4"))
+    ap.add_argument("--rocprof-summary", nargs="+", metavar="DIR")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="first run one 256 MiB device-to-device copy (a kernel of known "
+                         "traffic, for scaling HBM byte counters)")
+    args = ap.parse_args()
+    if args.rocprof_summary:
+        return rocprof_summary(args.rocprof_summary, args.warmup, args.steps)
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the attention path "
+              "shards over (batch x KV-head group) with no exchange, so each GPU runs this "
+              "same single-GPU workload.", file=sys.stderr)
+        return 2
+
+    import torch
+
+    dev = torch.device("cuda:0")
+    if args.copy_calibration:
+        src = torch.ones(64 * 1024 * 1024, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+    wl = Workloads(dev)
+    if args.only:
+        return run_only(args, torch, wl)
+    return run_full(args, torch, wl)
 
 
 if __name__ == "__main__":

@@ -743,8 +743,8 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_kernel(
 
 // dma16 with the nontemporal (streaming) cache policy, for data read once
 __device__ __forceinline__ void dma16_nt(uint32_t lds, uint32_t voff, const void* base) {
-  asm volatile("global_load_lds_dwordx4 %0, %1 nt" : : "v"(voff), "s"(base), "{m0}"(lds)
-               : "memory");
+  asm volatile(KF_VMEM_ASM_NOPS "global_load_lds_dwordx4 %0, %1 nt"
+               : : "v"(voff), "s"(base), "{m0}"(lds) : "memory");
 }
 
 // s_waitcnt vmcnt(N)

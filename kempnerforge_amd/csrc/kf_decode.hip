@@ -113,7 +113,7 @@ __global__ __launch_bounds__(256) void append_kernel(const T* __restrict__ k_new
 // own count would be off by the untracked direct-to-LDS loads in between.)
 template <int OFF>
 __device__ __forceinline__ void gload16(u32x4& r, uint32_t voff, const void* base) {
-  asm volatile("global_load_dwordx4 %0, %1, %2 offset:%3"
+  asm volatile(KF_VMEM_ASM_NOPS "global_load_dwordx4 %0, %1, %2 offset:%3"
                : "=v"(r)
                : "v"(voff), "s"(base), "n"(OFF)
                : "memory");

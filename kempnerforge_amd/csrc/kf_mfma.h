@@ -97,11 +97,22 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 // address goes in m0 as an input operand bound to that register, so the
 // compiler itself writes m0 and knows its value (a clobber inside the asm
 // would leave any m0 value the compiler keeps live silently overwritten).
+//
+// KF_VMEM_ASM_NOPS opens every inline-asm memory instruction: the compiler
+// cannot see the operands an asm statement reads, so it does not insert the
+// wait states the ISA requires between a VALU write of an SGPR (v_readlane,
+// v_readfirstlane, e.g. when it reloads a spilled SGPR) and a vector memory
+// instruction reading that SGPR as its address base (5), or between an SALU
+// write of m0 and an LDS DMA reading it (1).  Without them the load can use
+// the stale base and fault.
+#define KF_VMEM_ASM_NOPS "s_nop 4\n\t"
 __device__ __forceinline__ void dma16(uint32_t lds, uint32_t voff, const void* base) {
-  asm volatile("global_load_lds_dwordx4 %0, %1" : : "v"(voff), "s"(base), "{m0}"(lds) : "memory");
+  asm volatile(KF_VMEM_ASM_NOPS "global_load_lds_dwordx4 %0, %1"
+               : : "v"(voff), "s"(base), "{m0}"(lds) : "memory");
 }
 __device__ __forceinline__ void dma4(uint32_t lds, uint32_t voff, const void* base) {
-  asm volatile("global_load_lds_dword %0, %1" : : "v"(voff), "s"(base), "{m0}"(lds) : "memory");
+  asm volatile(KF_VMEM_ASM_NOPS "global_load_lds_dword %0, %1"
+               : : "v"(voff), "s"(base), "{m0}"(lds) : "memory");
 }
 
 // Copy a [ROWS_T][R chunks] bf16 tile whose rows start `ld` elements apart in
