@@ -458,10 +458,28 @@ def _drop_warmup(rows, warmup, steps, key):
     return out
 
 
-def rocprof_summary(dirs, warmup, steps):
+def _run_shape(d, warmup, steps):
+    """(warmup, steps) of the --only run profiled into d, read from the JSON
+    line it printed into d + ".log" when present."""
+    log = d.rstrip("/") + ".log"
+    if os.path.exists(log):
+        with open(log) as f:
+            for line in f:
+                if line.startswith("{") and '"warmup"' in line:
+                    j = json.loads(line)
+                    return j["warmup"], j["steps"]
+    return warmup, steps
+
+
+COPY_KIB = 262144.0  # --copy-calibration copies 256 MiB
+
+
+def rocprof_summary(dirs, warmup, steps, traffic_json=None):
     lines = []
+    traffic = {}
     for d in dirs:
         wl = os.path.basename(d.rstrip("/"))
+        warmup, steps = _run_shape(d, warmup, steps)
         trace = sorted(glob.glob(os.path.join(d, "**", "*kernel_trace.csv"), recursive=True))
         pmc = sorted(glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True))
         if trace:
@@ -482,15 +500,18 @@ def rocprof_summary(dirs, warmup, steps):
         for path in pmc:
             with open(path) as f:
                 rows = list(csv.DictReader(f))
+            # the 256 MiB device copy of --copy-calibration (the largest copy)
             calib = {}
             for r in rows:
                 if "copyBuffer" in r["Kernel_Name"]:
-                    calib[r["Counter_Name"]] = float(r["Counter_Value"])
+                    calib[r["Counter_Name"]] = max(calib.get(r["Counter_Name"], 0.0),
+                                                   float(r["Counter_Value"]))
             rows = [r for r in rows if "_ZN2kf" in r["Kernel_Name"]]
             disp = {}
             for r in rows:
-                disp.setdefault((int(r["Dispatch_Id"]), _short(r["Kernel_Name"])), {})[
-                    r["Counter_Name"]] = float(r["Counter_Value"])
+                e = disp.setdefault((int(r["Dispatch_Id"]), _short(r["Kernel_Name"])), {})
+                e[r["Counter_Name"]] = float(r["Counter_Value"])
+                e["dispatch_us"] = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
             items = [(k[1], v) for k, v in sorted(disp.items())]
             by = _drop_warmup(items, warmup, steps, lambda it: it[0])
             names = sorted({c for _, v in items for c in v})
@@ -498,11 +519,31 @@ def rocprof_summary(dirs, warmup, steps):
                          + (f"; copy calibration {calib}" if calib else "") + "\n")
             lines.append("| kernel | dispatches | " + " | ".join(names) + " |")
             lines.append("|---|---|" + "---|" * len(names))
+            # byte counters scaled by what they read for the copy of known size
+            scale = {c: COPY_KIB / calib[c] * 1024 for c in ("FETCH_SIZE", "WRITE_SIZE")
+                     if calib.get(c, 0) > COPY_KIB / 4}
+            if scale:
+                names += [f"{c} bytes" for c in scale]
+                lines[-2] = "| kernel | dispatches | " + " | ".join(names) + " |"
+                lines[-1] = "|---|---|" + "---|" * len(names)
             for k, its in sorted(by.items()):
-                vals = [statistics.mean(v[c] for _, v in its if c in v) for c in names]
+                vals = [statistics.mean(v[c] for _, v in its if c in v)
+                        for c in names if not c.endswith(" bytes")]
+                vals += [statistics.mean(v[c] for _, v in its) * f for c, f in scale.items()]
                 lines.append(f"| {k} | {len(its)} | " + " | ".join(f"{x:.6g}" for x in vals)
                              + " |")
+                for c, f in scale.items():
+                    traffic.setdefault(f"{k}@{wl.split('_')[-1].upper()}", {})[c] = round(
+                        statistics.mean(v[c] for _, v in its) * f)
     print("\n".join(lines))
+    if traffic_json:
+        out = {k: {"bytes": v.get("FETCH_SIZE", 0) + v.get("WRITE_SIZE", 0),
+                   "fetch_bytes": v.get("FETCH_SIZE"), "write_bytes": v.get("WRITE_SIZE")}
+               for k, v in sorted(traffic.items())}
+        with open(traffic_json, "w") as f:
+            json.dump({"source": "rocprofv3 --pmc FETCH_SIZE and --pmc WRITE_SIZE of bench.py "
+                                 "--only runs, scaled by a 256 MiB device copy in the same run",
+                       "kernels": out}, f, indent=1)
     return 0
 
 
@@ -515,12 +556,14 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--only", choices=("c3", "c2", "c3doc", "c5", "c5cap", "c4"))
     ap.add_argument("--rocprof-summary", nargs="+", metavar="DIR")
+    ap.add_argument("--traffic-json", metavar="PATH",
+                    help="with --rocprof-summary: write HBM bytes per launch per kernel")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run one 256 MiB device-to-device copy (a kernel of known "
                          "traffic, for scaling HBM byte counters)")
     args = ap.parse_args()
     if args.rocprof_summary:
-        return rocprof_summary(args.rocprof_summary, args.warmup, args.steps)
+        return rocprof_summary(args.rocprof_summary, args.warmup, args.steps, args.traffic_json)
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the attention path "
               "shards over (batch x KV-head group) with no exchange, so each GPU runs this "

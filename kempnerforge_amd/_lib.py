@@ -11,7 +11,10 @@ import ctypes
 import os
 import threading
 
-LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib", "libkf_attn.so")
+# In-tree build; KF_ATTN_LIB may name another build of the same library (an
+# A/B comparison of two builds of the kernels on one device).
+LIB_PATH = os.environ.get("KF_ATTN_LIB") or os.path.join(
+    os.path.dirname(os.path.abspath(__file__)), "lib", "libkf_attn.so")
 
 DTYPE_F32, DTYPE_BF16, DTYPE_F16 = 0, 1, 2
 
