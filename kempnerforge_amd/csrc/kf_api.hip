@@ -196,17 +196,20 @@ int kf_attn_decode_workspace_size(int B, int Hq, int Hkv, int D, int max_len, in
   int rc = check_common(B, 1, max_len, Hq, Hkv, D, dtype);
   if (rc) return rc;
   KF_CHECK_ARG(bytes != nullptr, "bytes is null");
-  *bytes = decode_workspace(B, Hq, D, max_len);
+  *bytes = decode_workspace(B, Hq, Hkv, D, max_len);
   return KF_OK;
 }
 
-int kf_attn_decode(const void* q_new, const void* k_new, const void* v_new, void* k_cache,
-                   void* v_cache, const int32_t* lens, const float* rope_cos,
-                   const float* rope_sin, int64_t rope_row_offset, int64_t rope_rows, void* out,
-                   void* workspace,
-                   size_t workspace_bytes, int B, int Smax, int Hq, int Hkv, int D, int max_len,
-                   const float* q_norm_weight, const float* k_norm_weight, float norm_eps,
-                   int dtype, void* stream) {
+}  // extern "C"
+
+namespace {
+// Checks shared by both decode entry points; fills *a.
+int decode_args(kf::DecodeArgs* a, const void* q_new, const void* k_new, const void* v_new,
+                void* k_cache, void* v_cache, const int32_t* lens, const float* rope_cos,
+                const float* rope_sin, int64_t rope_row_offset, int64_t rope_rows, void* out,
+                int B, int Smax, int Hq, int Hkv, int D, int max_len,
+                const float* q_norm_weight, const float* k_norm_weight, float norm_eps,
+                int dtype, void* stream) {
   int rc = check_common(B, 1, max_len, Hq, Hkv, D, dtype);
   if (rc) return rc;
   KF_CHECK_ARG(q_new && k_new && v_new && k_cache && v_cache && lens && rope_cos && rope_sin &&
@@ -215,19 +218,38 @@ int kf_attn_decode(const void* q_new, const void* k_new, const void* v_new, void
   KF_CHECK_ARG(!q_norm_weight == !k_norm_weight,
                "QK-norm needs both q_norm_weight and k_norm_weight (or neither)");
   KF_CHECK_ARG(max_len <= Smax, "max_len (%d) exceeds the cache length (%d)", max_len, Smax);
-  const size_t need = decode_workspace(B, Hq, D, max_len);
+  KF_CHECK_ARG(rope_rows > 0, "rope tables must have at least one row");
+  a->q_new = q_new; a->k_new = k_new; a->v_new = v_new; a->k_cache = k_cache;
+  a->v_cache = v_cache;
+  a->lens = lens; a->cos = rope_cos; a->sin = rope_sin; a->rope_row_offset = rope_row_offset;
+  a->rope_rows = rope_rows;
+  a->out = out; a->B = B; a->Smax = Smax; a->Hq = Hq; a->Hkv = Hkv; a->D = D;
+  a->max_len = max_len;
+  a->q_norm_w = q_norm_weight; a->k_norm_w = k_norm_weight; a->norm_eps = norm_eps;
+  a->dtype = dtype; a->scale = 1.0f / sqrtf((float)D); a->stream = (hipStream_t)stream;
+  return KF_OK;
+}
+}  // namespace
+
+extern "C" {
+
+int kf_attn_decode(const void* q_new, const void* k_new, const void* v_new, void* k_cache,
+                   void* v_cache, const int32_t* lens, const float* rope_cos,
+                   const float* rope_sin, int64_t rope_row_offset, int64_t rope_rows, void* out,
+                   void* workspace,
+                   size_t workspace_bytes, int B, int Smax, int Hq, int Hkv, int D, int max_len,
+                   const float* q_norm_weight, const float* k_norm_weight, float norm_eps,
+                   int dtype, void* stream) {
+  DecodeArgs a;
+  int rc = decode_args(&a, q_new, k_new, v_new, k_cache, v_cache, lens, rope_cos, rope_sin,
+                       rope_row_offset, rope_rows, out, B, Smax, Hq, Hkv, D, max_len,
+                       q_norm_weight, k_norm_weight, norm_eps, dtype, stream);
+  if (rc) return rc;
+  const size_t need = decode_workspace(B, Hq, Hkv, D, max_len);
   if (workspace_bytes < need || !workspace) {
     set_error("workspace too small: need %zu bytes, got %zu", need, workspace_bytes);
     return KF_ERR_WORKSPACE;
   }
-  DecodeArgs a;
-  a.q_new = q_new; a.k_new = k_new; a.v_new = v_new; a.k_cache = k_cache; a.v_cache = v_cache;
-  KF_CHECK_ARG(rope_rows > 0, "rope tables must have at least one row");
-  a.lens = lens; a.cos = rope_cos; a.sin = rope_sin; a.rope_row_offset = rope_row_offset;
-  a.rope_rows = rope_rows;
-  a.out = out; a.B = B; a.Smax = Smax; a.Hq = Hq; a.Hkv = Hkv; a.D = D; a.max_len = max_len;
-  a.q_norm_w = q_norm_weight; a.k_norm_w = k_norm_weight; a.norm_eps = norm_eps;
-  a.dtype = dtype; a.scale = 1.0f / sqrtf((float)D); a.stream = (hipStream_t)stream;
   return decode(a, workspace);
 }
 

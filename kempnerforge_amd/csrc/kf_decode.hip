@@ -1,30 +1,33 @@
 // KV-cache decode (one new token per sequence) and cache append.
 //
 // decode = two launches on the caller's stream:
-//  1. split    split-K attention: workgroup (split, b, kv head) streams CH keys
-//              of one KV head once and serves all n_rep query heads of the
-//              group from that single read (the reference expands the cache
-//              n_rep times first).  D/8 threads share a key row, each loading
-//              16 contiguous bytes, so a pass reads whole rows coalesced.
-//              Writes partial (o, m, l) per (b, hq, split) in float32.  The
-//              split holding position lens[b] rotates k_new (eager RoPE
-//              rounding) and writes it and v_new into the caches (the
-//              reference's KVCache.update) instead of reading that row.
-//  2. merge    one wavefront per (b, hq) rescales and sums the partials.
+//  1. stream   persistent split-K attention: the key chunks of every
+//              (sequence, KV head) pair form one list that the grid's
+//              wavefronts split into equal contiguous ranges; each wavefront
+//              streams its range once, serving all n_rep query heads of a
+//              pair from that single read (the reference expands the cache
+//              n_rep times first), and writes one partial (o, m, l) per pair
+//              it touches, in float32.  The wavefront holding position
+//              lens[b] rotates k_new (eager RoPE rounding) and writes it and
+//              v_new into the caches (the reference's KVCache.update) instead
+//              of reading that row.
+//  2. merge    one workgroup per (b, hq) rescales and sums the partials.
 // With QK-norm weights the per-head RMSNorm of q_new and k_new (the
 // reference's q_norm / k_norm, applied before RoPE) happens where the rows
 // are loaded, instead of in separate launches.
 // Shapes outside the fast path (dtype other than bf16, D not in {64, 128}, or
-// n_rep > 32) use decode_generic: one wavefront per (b, hq).
+// n_rep > 16) use decode_generic: one wavefront per (b, hq).
 #include "kf_common.h"
 #include "kf_internal.h"
 #include "kf_mfma.h"
 
+#include <algorithm>
+#include <climits>
+#include <type_traits>
+
 namespace kf {
 
 namespace {
-
-constexpr int CH = 1024;  // keys per split
 
 // RMSNorm of one element given its row's sum of squares, as the reference's
 // RMSNorm computes it (kempnerforge/model/norm.py:22-27): float32
@@ -92,457 +95,509 @@ __global__ __launch_bounds__(256) void append_kernel(const T* __restrict__ k_new
   vc[dst + d + half] = v_new[src + d + half];
 }
 
-// Split-K decode on MFMA.  Workgroup = (split of CH keys, b, KV head), 4
-// independent wavefronts of NCH chunks x KC keys each.  Per chunk:
-//   S^T = K q^T   v_mfma_f32_32x32x16_bf16, the KV group's n_rep query heads
-//                 as the B-operand columns (zero-padded to 32), so a lane owns
-//                 one head and the online softmax is lane-local; K rows go
-//                 from HBM straight into A-operand registers.
-//   O^T += V^T P^T  V rows staged in LDS by direct global->LDS loads and read
-//                 transposed (ds_read_b64_tr_b16).
-// Loads run one chunk ahead (K registers and V LDS buffers double-buffered),
-// so every wavefront keeps a chunk in flight while it computes the previous.
-// Chunks past the split's end load a clamped row (L2 hits) and are not
-// computed, which keeps the memory-counter accounting static.  The
-// wavefronts' (m, l, o) are merged in LDS into one partial per
-// (b, head, split).  The wavefront owning position lens[b] rotates k_new,
-// writes k and v into the caches and uses them in place of that row.
-// 16-byte global load issued from inline asm, so that the compiler's
-// memory-counter bookkeeping does not see it: the caller waits with
-// wait_vm<N>() and passes the destination through it before any use.  (Its
-// own count would be off by the untracked direct-to-LDS loads in between.)
-template <int OFF>
-__device__ __forceinline__ void gload16(u32x4& r, uint32_t voff, const void* base) {
-  asm volatile(KF_VMEM_ASM_NOPS "global_load_dwordx4 %0, %1, %2 offset:%3"
-               : "=v"(r)
-               : "v"(voff), "s"(base), "n"(OFF)
-               : "memory");
-}
-template <int N, int I = 0>
-__device__ __forceinline__ void gload16_row(u32x4* r, uint32_t voff, const void* base) {
-  if constexpr (I < N) {
-    gload16<32 * I>(r[I], voff, base);
-    gload16_row<N, I + 1>(r, voff, base);
+// ---- streaming schedule -----------------------------------------------------
+// Every (sequence b, KV head g) pair p = b * Hkv + g holds nck(b) = ceil((lens[b]
+// + 1) / KC) chunks of KC keys (0 when the length is unusable).  The chunks of
+// all pairs, in (b, g, key) order, form one list of C chunks, and wavefront w
+// of the NW in the grid streams the contiguous range [w C / NW, (w + 1) C / NW):
+// every wavefront reads the same number of bytes (to one chunk), whatever the
+// lengths, and keeps its loads in flight across pair boundaries.  A wavefront
+// writes one partial (o, m, l) per pair it touches, in slot w + p: the pairs a
+// wavefront touches are consecutive and the wavefronts touching a pair are
+// consecutive, so (w, p) -> w + p is one-to-one; NW + B * Hkv slots suffice.
+constexpr int KC = 32;          // keys per chunk
+constexpr int DEC_WAVES = 4;    // independent wavefronts per workgroup
+constexpr int DEC_GRID_MAX = 512;
+
+struct DecodeSched {
+  const int32_t* lens;
+  int B, Hkv, max_len;
+  int64_t row_offset, rope_rows;
+  __device__ __forceinline__ int nck(int b) const {
+    const int len = lens[b];
+    return decode_len_ok(len, max_len, row_offset, rope_rows) ? (len + KC) / KC : 0;
   }
-}
-// s_waitcnt vmcnt(N), then the registers in r[0..n) count as written here
-template <int N, int n>
-__device__ __forceinline__ void wait_vm(u32x4* r) {
-  asm volatile("s_waitcnt vmcnt(%1)" : "+v"(r[0]) : "n"(N) : "memory");
+};
+
+__device__ __forceinline__ int wave_sum_int(int v) {
 #pragma unroll
-  for (int i = 1; i < n; ++i) asm volatile("" : "+v"(r[i])::"memory");
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+  return __builtin_amdgcn_readfirstlane(v);
 }
 
-// Longest-processing-time-first order of the split grid.  A full split of CH
-// keys takes ~40 us of one workgroup slot's share of HBM at C4's size, and the
-// grid runs in 2-3 rounds of slots, so a round that ends on full splits idles
-// half the machine for tens of microseconds.  Flat block id f maps to: first
-// every full split (b, g, k < len_b / CH), then each sequence's partial split
-// (len_b % CH keys) ordered by size, largest first, so the last workgroups
-// dispatched are the shortest.  One wavefront computes it (lane = batch row,
-// B <= 64) and leaves {split, b, g} in job[], split = -1 for no work.
-__device__ __forceinline__ void decode_job(const int32_t* __restrict__ lens, int B, int Hkv,
-                                           int max_len, int64_t row_offset, int64_t rope_rows,
-                                           int f, int lane, int* job) {
-  int Lb = 0;
-  if (lane < B) {
-    const int len = lens[lane];
-    Lb = decode_len_ok(len, max_len, row_offset, rope_rows) ? len + 1 : 0;
-  }
-  const int nf = Lb / CH, r = Lb % CH;
-  int incl = nf * Hkv;  // inclusive prefix of full splits over the batch rows
+// Total chunks C over all pairs (wavefront-uniform).
+__device__ __forceinline__ int total_chunks(const DecodeSched& s, int lane) {
+  int tot = 0;
+  for (int b0 = 0; b0 < s.B; b0 += 64) tot += wave_sum_int(b0 + lane < s.B ? s.nck(b0 + lane) : 0);
+  return tot * s.Hkv;
+}
+
+// Sequence holding global chunk c (0 <= c < C) and the index of its first
+// chunk, Hkv * (chunks of the sequences before it).  Wavefront-uniform.
+__device__ __forceinline__ void locate_chunk(const DecodeSched& s, int c, int lane, int& b_out,
+                                             int& base_out) {
+  int run = 0;
+  b_out = 0;
+  base_out = 0;
+  for (int b0 = 0; b0 < s.B; b0 += 64) {
+    const int b = b0 + lane;
+    const int n = (b < s.B ? s.nck(b) : 0) * s.Hkv;
+    int incl = n;
 #pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int y = __shfl_up(incl, o, 64);
-    if (lane >= o) incl += y;
-  }
-  const int F = __shfl(incl, 63, 64);
-  int sp = -1, bb = 0, gg = 0;
-  if (f < F) {
-    const uint64_t m = __builtin_amdgcn_ballot_w64(incl - nf * Hkv <= f && f < incl);
-    bb = (int)__builtin_ctzll(m);
-    const int nfb = __shfl(nf, bb, 64);
-    const int within = f - (__shfl(incl, bb, 64) - nfb * Hkv);
-    sp = within % nfb;
-    gg = within / nfb;
-  } else {
-    const int p = (f - F) / Hkv;
-    gg = (f - F) % Hkv;
-    // rank of this row's partial split: larger first, ties by row
-    int rank = 0;
-    for (int j = 0; j < B; ++j) {
-      const int rj = __shfl(r, j, 64);
-      rank += (rj > r) || (rj == r && j < lane);
+    for (int o = 1; o < 64; o <<= 1) {
+      const int y = __shfl_up(incl, o, 64);
+      if (lane >= o) incl += y;
     }
-    const uint64_t m = __builtin_amdgcn_ballot_w64(r > 0 && rank == p);
+    const uint64_t m = __builtin_amdgcn_ballot_w64(n > 0 && run + incl - n <= c && c < run + incl);
     if (m) {
-      bb = (int)__builtin_ctzll(m);
-      sp = __shfl(nf, bb, 64);
+      const int l = (int)__builtin_ctzll(m);
+      b_out = b0 + l;
+      base_out = run + __shfl(incl - n, l, 64);
+      b_out = __builtin_amdgcn_readfirstlane(b_out);
+      base_out = __builtin_amdgcn_readfirstlane(base_out);
+      return;
     }
-  }
-  if (lane == 0) {
-    job[0] = sp;
-    job[1] = bb;
-    job[2] = gg;
+    run += __builtin_amdgcn_readfirstlane(__shfl(incl, 63, 64));
   }
 }
 
-constexpr int DEC_WAVES = 4;
-constexpr int KC = 32;                    // keys per chunk
-constexpr int NCH = CH / (DEC_WAVES * KC);  // chunks per wavefront
+// The wavefront whose range holds chunk c: the largest w with w C / NW <= c.
+__device__ __forceinline__ int chunk_owner(int c, int C, int NW) {
+  return (int)((((int64_t)c + 1) * NW - 1) / C);
+}
+
+// Position in the chunk list: pair (b, g), local chunk lc of nck, new-token
+// position len (keys 0 .. len are attended).
+struct Cursor {
+  int b, g, lc, nck, len;
+};
+
+__device__ __forceinline__ Cursor cursor_at(const DecodeSched& s, int c, int lane) {
+  Cursor cur;
+  int base;
+  locate_chunk(s, c, lane, cur.b, base);
+  cur.nck = max(s.nck(cur.b), 1);  // >= 1 for any c < C
+  cur.len = s.lens[cur.b];
+  const int rem = c - base;
+  cur.g = rem / cur.nck;
+  cur.lc = rem % cur.nck;
+  return cur;
+}
+
+__device__ __forceinline__ void cursor_next(Cursor& cur, const DecodeSched& s) {
+  if (++cur.lc < cur.nck) return;
+  cur.lc = 0;
+  if (++cur.g < s.Hkv) return;
+  cur.g = 0;
+  for (++cur.b; cur.b < s.B; ++cur.b) {
+    cur.nck = s.nck(cur.b);
+    if (cur.nck > 0) break;
+  }
+  if (cur.b < s.B) cur.len = s.lens[cur.b];
+}
+
+// Streaming split-K decode on MFMA.  Each wavefront walks its chunk range
+// independently (no workgroup barriers).  Per chunk of KC = 32 keys of pair
+// (b, g), with v_mfma_f32_16x16x32_bf16 (operand layout below):
+//   S^T = K q^T   two 16-key blocks; the pair's n_rep <= 16 query heads are the
+//                 B-operand columns (zero-padded to 16), so one read of the KV
+//                 head serves every head of the group
+//   O^T += V^T P^T  V rows go to the wavefront's LDS tile and come back
+//                 transposed (ds_read_b64_tr_b16) as the A operand; P^T is the
+//                 B operand straight from the S registers
+// Every global load is an ordinary compiler-tracked load into registers: the
+// next chunk's K rows, V rows and, at a pair's first chunk, its q rows and
+// RoPE table row (at the chunk holding position lens[b], the new token's k and
+// v) are loaded while the current chunk is computed, and the compiler's own
+// memory-counter waits cover them exactly.  A pair's start turns the q rows
+// into the rotated q operand (RMS-normalised first with QK-norm weights); the
+// chunk holding the new token rotates k_new, writes the new k / v rows into
+// the caches (the reference's KVCache.update) and uses them in place of that
+// row.  Rows past the pair's last key are loaded clamped and zeroed on the way
+// into LDS (a clamped copy of a stale row times a zero probability stays 0).
+//
+// MFMA 16x16x32 operand layout (lane l, q4 = l / 16, j = 0..7):
+//   A[m][k]: m = l % 16, k = 8 q4 + j     B[k][n]: n = l % 16, k = 8 q4 + j
+//   C[m][n]: n = l % 16, register i holds m = 4 q4 + i
+// S^T: m = key, n = head, k = head dim (32 ks + 8 q4 + j); the lane's C
+// registers hold keys 4 q4 + i of each 16-key block, which, read as slots
+// j < 4 (block 0) and j >= 4 (block 1), are the B operand of O^T += V^T P^T
+// with k slot j <-> key (j < 4 ? 4 q4 + j : 16 + 4 q4 + j - 4).
+typedef float f32x4v __attribute__((ext_vector_type(4)));
 
 template <int D, bool QKN>
-__global__ __launch_bounds__(256, 2) void decode_split_kernel(
+__global__ __launch_bounds__(256, 2) void decode_stream_kernel(
     const bf16* __restrict__ q_new, const bf16* __restrict__ k_new,
     const bf16* __restrict__ v_new, const float* __restrict__ cos, const float* __restrict__ sin,
     int64_t row_offset, int64_t rope_rows, int max_len, bf16* kc, bf16* vc,
-    const int32_t* __restrict__ lens, float* __restrict__ opart, float* __restrict__ mpart,
-    float* __restrict__ lpart, int Hq, int Hkv, int Smax, int nsplit, int n_rep,
-    float scale_log2, const float* __restrict__ qnw, const float* __restrict__ knw, float eps) {
+    const int32_t* __restrict__ lens, float* __restrict__ opart, float* __restrict__ mlpart,
+    int B, int Hq, int Hkv, int Smax, int n_rep, float scale_log2,
+    const float* __restrict__ qnw, const float* __restrict__ knw, float eps) {
   using namespace mfma;
-  constexpr int KS = D / 16, DT = D / 32, KR = D / 8, HALF = D / 2;
-  constexpr int WKEYS = NCH * KC;      // keys per wavefront
-  constexpr int VI = KC * KR / 64;     // LDS copies per V chunk
-  constexpr int PER_CHUNK = KS + VI;   // vector-memory instructions per chunk
-  static_assert(PER_CHUNK < 64, "vmcnt range");
-  __shared__ __attribute__((aligned(16))) bf16 sV[DEC_WAVES][2][KC * D];
-  __shared__ __attribute__((aligned(16))) bf16 sNew[2][D];
-  __shared__ float sML[DEC_WAVES][2][32];
-  static_assert(sizeof(sV) >= DEC_WAVES * 32 * D * sizeof(float), "merge buffer");
+  constexpr int KT = D / 32;          // 32-dim k-steps of S
+  constexpr int DB = D / 16;          // 16-dim output blocks
+  constexpr int KR = D / 8;           // 16-byte chunks per row
+  constexpr int HALF = D / 2;
+  constexpr int VL = KC * KR / 64;    // 16-byte V loads per lane and chunk
+  static_assert(KC == 32, "two 16-key blocks per chunk");
+  struct WaveLds {
+    bf16 v[KC * D];   // the chunk's V rows, 16-byte chunks swizzled by row
+    float cs[2][64];  // cos, sin row of the pair's new position
+    bf16 nw[D];       // rotated k_new
+  };
+  __shared__ __attribute__((aligned(16))) WaveLds lds_all[DEC_WAVES];
 
-  // which split this workgroup computes: longest first (see decode_job)
-  __shared__ int sJob[3];
-  const int B = gridDim.y / Hkv;
-  if (B <= 64) {
-    if (threadIdx.x < 64)
-      decode_job(lens, B, Hkv, max_len, row_offset, rope_rows,
-                 blockIdx.y * gridDim.x + blockIdx.x, threadIdx.x, sJob);
-  } else if (threadIdx.x == 0) {
-    sJob[0] = blockIdx.x;
-    sJob[1] = blockIdx.y / Hkv;
-    sJob[2] = blockIdx.y % Hkv;
-  }
-  __syncthreads();
-  const int sp_idx = sJob[0];
-  if (sp_idx < 0) return;
-  const int b = sJob[1], g = sJob[2];
-  if (!decode_len_ok(lens[b], max_len, row_offset, rope_rows)) return;
-  const int L = lens[b] + 1;
-  const int newrow = L - 1;  // the token being decoded
-  const int k0 = sp_idx * CH;
-  if (k0 >= L) return;
-  const int k1 = min(k0 + CH, L);
-  const int w = wave_id(), lane = threadIdx.x & 63, hh = lane >> 5, c32 = lane & 31;
-  const int64_t trow = (int64_t)newrow - row_offset;
-  const int kw0 = k0 + w * WKEYS;                                   // first key of the wavefront
-  const int nvc = min(max((k1 - kw0 + KC - 1) / KC, 0), NCH);       // chunks holding keys
-  const bool own_new = newrow >= kw0 && newrow < kw0 + WKEYS;
+  const int w = wave_id(), lane = threadIdx.x & 63, q4 = lane >> 4, c16 = lane & 15;
+  WaveLds& L = lds_all[w];
+  const DecodeSched s{lens, B, Hkv, max_len, row_offset, rope_rows};
+  const int NW = gridDim.x * DEC_WAVES, gw = blockIdx.x * DEC_WAVES + w;
+  const int C = total_chunks(s, lane);
+  const int c_lo = (int)((int64_t)gw * C / NW), c_hi = (int)((int64_t)(gw + 1) * C / NW);
+  if (c_lo >= c_hi) return;
 
-  bf16* kb = kc + ((int64_t)b * Hkv + g) * Smax * D;
-  bf16* vb = vc + ((int64_t)b * Hkv + g) * Smax * D;
-  const float* cr = cos + trow * HALF;
-  const float* sr = sin + trow * HALF;
-
-  // the new token: rotated k and v into the caches and into sNew
-  if (own_new) {
-    const bf16* kn = k_new + ((int64_t)b * Hkv + g) * D;
-    const bf16* vn = v_new + ((int64_t)b * Hkv + g) * D;
-    // lanes 0 .. HALF/8-1 hold elements d0..d0+7 and d0+HALF..+7 of the key
-    const bool kl = lane < HALF / 8;
-    const int d0 = kl ? 8 * lane : 0;
-    float x1[8], x2[8];
-    if (kl) {
-      unpack8(*(const u32x4*)(kn + d0), x1);
-      unpack8(*(const u32x4*)(kn + d0 + HALF), x2);
+  // the chunk's rows, loaded one step ahead: each set is reloaded for the next
+  // chunk as soon as this chunk's products have read it, so one register set
+  // per operand keeps a chunk in flight
+  u32x4 kreg[2][KT];  // key 16 kb + c16 of the chunk, dims 32 ks + 8 q4 .. + 7
+  u32x4 vreg[VL];     // V row (64 j + lane) / KR, chunk (64 j + lane) % KR
+  struct Stash {
+    u32x4 q[KT];     // q row of head c16 (0 for c16 >= n_rep), dims 32 ks + 8 q4 .. + 7
+    float cs[2];     // cos / sin of the new position, dim lane (< HALF)
+    uint32_t kv[2];  // k_new / v_new, dims 2 lane, 2 lane + 1 (lane < D / 2)
+  };
+  auto load_k = [&](const Cursor& cur) {
+    const int last = cur.len;  // keys 0 .. len
+    const int64_t base = ((int64_t)cur.b * Hkv + cur.g) * Smax * D;
+    const int r0 = cur.lc * KC;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      const int key = min(r0 + 16 * kb + c16, last);
+#pragma unroll
+      for (int ks = 0; ks < KT; ++ks)
+        kreg[kb][ks] = *(const u32x4*)(kc + base + (int64_t)key * D + 32 * ks + 8 * q4);
     }
-    if constexpr (QKN) {
-      float ss = 0.f;
-      if (kl)
+  };
+  auto load_v = [&](const Cursor& cur) {
+    const int last = cur.len;
+    const int64_t base = ((int64_t)cur.b * Hkv + cur.g) * Smax * D;
+    const int r0 = cur.lc * KC;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) ss += x1[j] * x1[j] + x2[j] * x2[j];
-#pragma unroll
-      for (int o = 1; o < HALF / 8; o <<= 1) ss += __shfl_xor(ss, o, 64);
-      if (kl)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          x1[j] = rms_scale<bf16>(x1[j], ss, D, eps, knw[d0 + j]);
-          x2[j] = rms_scale<bf16>(x2[j], ss, D, eps, knw[d0 + HALF + j]);
-        }
+    for (int j = 0; j < VL; ++j) {
+      const int li = 64 * j + lane, row = li / KR, pc = li % KR;
+      const int key = min(r0 + row, last);
+      vreg[j] = *(const u32x4*)(vc + base + (int64_t)key * D + 8 * pc);
     }
-    if (kl) {
-      float r1[8], r2[8];
+  };
+  auto load_stash = [&](const Cursor& cur, Stash& st, bool pair_start, bool new_tok) {
+    if (pair_start) {
+      const int h = c16 < n_rep ? c16 : 0;
+      const bf16* qr = q_new + ((int64_t)cur.b * Hq + (int64_t)cur.g * n_rep + h) * D;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) rope_pair<bf16>(x1[j], x2[j], cr[d0 + j], sr[d0 + j], r1[j], r2[j]);
-      const u32x4 a1 = pack8(r1), a2 = pack8(r2);
-      *(u32x4*)(sNew[0] + d0) = a1;
-      *(u32x4*)(sNew[0] + d0 + HALF) = a2;
-      *(u32x4*)(kb + (int64_t)newrow * D + d0) = a1;
-      *(u32x4*)(kb + (int64_t)newrow * D + d0 + HALF) = a2;
-    } else if (lane >= 32 && lane < 32 + KR) {
-      const int d0 = 8 * (lane - 32);
-      const u32x4 x = *(const u32x4*)(vn + d0);
-      *(u32x4*)(sNew[1] + d0) = x;
-      *(u32x4*)(vb + (int64_t)newrow * D + d0) = x;
+      for (int ks = 0; ks < KT; ++ks) st.q[ks] = *(const u32x4*)(qr + 32 * ks + 8 * q4);
+      const int64_t trow = (int64_t)cur.len - row_offset;
+      const int e = lane < HALF ? lane : 0;
+      st.cs[0] = cos[trow * HALF + e];
+      st.cs[1] = sin[trow * HALF + e];
     }
-  }
-  // query fragment (B operand): column = head of the group, slots = d
-  u32x4 qf[KS];
-  if constexpr (QKN) {
-    // lanes l and l ^ 32 hold the two halves of one query row: both load,
-    // one exchange completes the row's sum of squares
-    const bool ql = c32 < n_rep;
-    const bf16* qr = q_new + ((int64_t)b * Hq + g * n_rep + (ql ? c32 : 0)) * D;
-    u32x4 ra[KS / 2], rb[KS / 2];
-    float ss = 0.f;
-#pragma unroll
-    for (int ks = 0; ks < KS / 2; ++ks) {
-      const int d0 = 16 * ks + 8 * hh;
-      ra[ks] = *(const u32x4*)(qr + d0);
-      rb[ks] = *(const u32x4*)(qr + d0 + HALF);
-      float x1[8], x2[8];
-      unpack8(ra[ks], x1);
-      unpack8(rb[ks], x2);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) ss += x1[j] * x1[j] + x2[j] * x2[j];
-    }
-    ss = pair_sum32(ss);
-#pragma unroll
-    for (int ks = 0; ks < KS / 2; ++ks) {
-      const int d0 = 16 * ks + 8 * hh;
-      float x1[8], x2[8], r1[8], r2[8];
-      unpack8(ra[ks], x1);
-      unpack8(rb[ks], x2);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        x1[j] = rms_scale<bf16>(x1[j], ss, D, eps, qnw[d0 + j]);
-        x2[j] = rms_scale<bf16>(x2[j], ss, D, eps, qnw[d0 + HALF + j]);
-        rope_pair<bf16>(x1[j], x2[j], cr[d0 + j], sr[d0 + j], r1[j], r2[j]);
-      }
-      const u32x4 z = {0u, 0u, 0u, 0u};
-      qf[ks] = ql ? pack8(r1) : z;
-      qf[ks + KS / 2] = ql ? pack8(r2) : z;
-    }
-  } else if (c32 < n_rep) {
-    const bf16* qr = q_new + ((int64_t)b * Hq + g * n_rep + c32) * D;
-#pragma unroll
-    for (int ks = 0; ks < KS / 2; ++ks) {
-      const int d0 = 16 * ks + 8 * hh;
-      float x1[8], x2[8], r1[8], r2[8];
-      unpack8(*(const u32x4*)(qr + d0), x1);
-      unpack8(*(const u32x4*)(qr + d0 + HALF), x2);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) rope_pair<bf16>(x1[j], x2[j], cr[d0 + j], sr[d0 + j], r1[j], r2[j]);
-      qf[ks] = pack8(r1);
-      qf[ks + KS / 2] = pack8(r2);
-    }
-  } else {
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) qf[ks] = u32x4{0u, 0u, 0u, 0u};
-  }
-  // finish every tracked load's consumer before the first direct-to-LDS load
-  // is issued (see gload16)
-#pragma unroll
-  for (int ks = 0; ks < KS; ++ks) asm volatile("" : "+v"(qf[ks])::"memory");
-
-  // chunk loads: K rows into registers, V rows into this wavefront's LDS buffer
-  u32x4 kreg[2][KS];
-  auto issue = [&](int c, u32x4 (&kr)[KS], bf16* tV) {
-    const int r0 = kw0 + c * KC;
-    const int key = min(r0 + c32, k1 - 1);
-    gload16_row<KS>(kr, (uint32_t)(key * D + 8 * hh) * 2u, kb);
-    const uint32_t tva = lds_addr(tV);
-#pragma unroll
-    for (int j = 0; j < VI; ++j) {
-      const int Lc = j * 64 + lane;
-      const int row = Lc / KR, pc = Lc % KR;
-      const int lc = pc ^ swz<KR>(row);
-      const uint32_t grow = (uint32_t)min(r0 + row, k1 - 1);
-      dma16(tva + j * 1024, (grow * D + (uint32_t)lc * 8u) * 2u, vb);
+    if (new_tok) {
+      const int64_t row = ((int64_t)cur.b * Hkv + cur.g) * D;
+      const int e = lane < D / 2 ? lane : 0;
+      st.kv[0] = ((const uint32_t*)(k_new + row))[e];
+      st.kv[1] = ((const uint32_t*)(v_new + row))[e];
     }
   };
 
-  const TrOffsets<D> tro = tr_offsets<D>(lane);
-  float m = -INFINITY, lsum = 0.f;
-  f32x16 acc[DT];
-#pragma unroll
-  for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-    for (int i = 0; i < 16; ++i) acc[dt][i] = 0.f;
+  // transposed-read byte offsets of this lane in the V tile, per 16-dim block:
+  // address lane a = c16 of group q4 reads row 4 q4 + a / 4, dims 16 blk +
+  // 4 (a % 4) .. + 3 (the second read: row + 16, the same swizzle)
+  // chunk (2 blk + x) of the row lands at (2 blk + x) ^ sw = 2 (blk ^ (sw >> 1)) +
+  // (x ^ (sw & 1)): one xor per block
+  const int tr_row = 4 * q4 + (c16 >> 2), tr_sw = swz<KR>(tr_row);
+  const uint32_t tr_base = (uint32_t)((tr_row * KR + (((c16 & 3) >> 1) ^ (tr_sw & 1))) * 16 +
+                                      (4 * (c16 & 1)) * 2);
+  const int tr_hs = tr_sw >> 1;
 
-  issue(0, kreg[0], sV[w][0]);
-#pragma unroll
-  for (int c = 0; c < NCH; ++c) {
-    if (c + 1 < NCH) issue(c + 1, kreg[(c + 1) & 1], sV[w][(c + 1) & 1]);
-    // K of chunk c has landed once only V(c) and the next chunk are pending;
-    // waited on every path, so the registers stay owned until they land
-    if (c + 1 < NCH)
-      wait_vm<VI + PER_CHUNK, KS>(kreg[c & 1]);
-    else
-      wait_vm<VI, KS>(kreg[c & 1]);
-    if (c < nvc) {
-      const int r0 = kw0 + c * KC;
-      bf16* tV = sV[w][c & 1];
-      const bool has_new = own_new && newrow >= r0 && newrow < r0 + KC;
-      // the new row's lane takes k from sNew (a select, so that no load
-      // target is overwritten under divergence, which would force a full
-      // memory-counter wait)
-      u32x4 nk[KS];
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) nk[ks] = u32x4{0u, 0u, 0u, 0u};
-      if (has_new) {
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) nk[ks] = *(const u32x4*)(sNew[0] + 16 * ks + 8 * hh);
+  Stash st;
+  u32x4 qf[KT];
+  f32x4v acc[DB];
+  float m = -INFINITY, lsum = 0.f;
+  Cursor cc = cursor_at(s, c_lo, lane);  // chunk being computed
+  Cursor ic = cc;                        // chunk being loaded
+  load_stash(ic, st, true, ic.lc == ic.nck - 1);
+  load_k(ic);
+  load_v(ic);
+
+  for (int i = c_lo; i < c_hi; ++i) {
+    const bool seg_start = i == c_lo || cc.lc == 0;
+    const bool has_new = cc.lc == cc.nck - 1;
+    const int newrow = cc.len;
+    const int r0 = cc.lc * KC;
+    const int lim = newrow - r0;  // last valid key of the chunk, local
+    const bf16* kvrow_k = nullptr;
+    if (seg_start) {
+      // the pair's cos / sin row into LDS, then the rotated q operand
+      if (lane < HALF) {
+        L.cs[0][lane] = st.cs[0];
+        L.cs[1][lane] = st.cs[1];
       }
-      const bool is_new = has_new && c32 == newrow - r0;
-      bf16x8 kf[KS];
+      float ss = 0.f;
+      if constexpr (QKN) {
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) kf[ks] = as_bf16x8(is_new ? nk[ks] : kreg[c & 1][ks]);
-      f32x16 sc;
+        for (int ks = 0; ks < KT; ++ks) {
+          float x[8];
+          unpack8(st.q[ks], x);
 #pragma unroll
-      for (int i = 0; i < 16; ++i) sc[i] = 0.f;
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks)
-        sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[ks], as_bf16x8(qf[ks]), sc, 0, 0, 0);
-      const int lim = k1 - 1 - r0;  // last valid key of the chunk, local
-      float tmax = -INFINITY;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int local = 8 * (i >> 2) + 4 * hh + (i & 3);
-        sc[i] = local > lim ? -INFINITY : sc[i] * scale_log2;
-        tmax = fmaxf(tmax, sc[i]);
-      }
-      tmax = pair_max32(tmax);
-      const float mnew = fmaxf(m, tmax);  // finite: key r0 is valid
-      const float alpha = fast_exp2(m - mnew);
-      float psum = 0.f;
-      u32x4 pk[2];
-#pragma unroll
-      for (int i = 0; i < 16; i += 2) {
-        const float p0 = fast_exp2(sc[i] - mnew), p1 = fast_exp2(sc[i + 1] - mnew);
-        psum += p0 + p1;
-        pk[i >> 3][(i & 7) >> 1] = pack2(p0, p1);
-      }
-      lsum = lsum * alpha + psum;
-      m = mnew;
-      // V of chunk c has landed once only the next chunk's loads are pending
-      if (c + 1 < NCH)
-        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(PER_CHUNK) : "memory");
-      else
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-      if (lim < KC - 1) {
-        // rows past the split's end hold clamped copies of a row that may be
-        // stale (the slot being written): zero them so 0 * V stays 0
-        for (int Lc = (lim + 1) * KR + lane; Lc < KC * KR; Lc += 64)
-          *(u32x4*)(tV + Lc * 8) = u32x4{0u, 0u, 0u, 0u};
-      }
-      if (has_new && lane < KR) {
-        const int row = newrow - r0;
-        *(u32x4*)(tV + (row * KR + (lane ^ swz<KR>(row))) * 8) = *(const u32x4*)(sNew[1] + 8 * lane);
-      }
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) acc[dt][i] *= alpha;
-#pragma unroll
-      for (int cc = 0; cc < 2; ++cc)
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
-          const bf16x8 a = lds_frag_t<D>(tV, tro, cc, dt);
-          acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, as_bf16x8(pk[cc]), acc[dt], 0, 0, 0);
+          for (int j = 0; j < 8; ++j) ss += x[j] * x[j];
         }
+        // the four lanes of one head (q4 = 0..3) hold its whole row
+        ss += __shfl_xor(ss, 16, 64);
+        ss += __shfl_xor(ss, 32, 64);
+      }
+#pragma unroll
+      for (int ks = 0; ks < KT / 2; ++ks) {
+        const int d0 = 32 * ks + 8 * q4;  // < HALF; its partner is d0 + HALF (ks + KT / 2)
+        float x1[8], x2[8], r1[8], r2[8];
+        unpack8(st.q[ks], x1);
+        unpack8(st.q[ks + KT / 2], x2);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          if constexpr (QKN) {
+            x1[j] = rms_scale<bf16>(x1[j], ss, D, eps, qnw[d0 + j]);
+            x2[j] = rms_scale<bf16>(x2[j], ss, D, eps, qnw[d0 + HALF + j]);
+          }
+          rope_pair<bf16>(x1[j], x2[j], L.cs[0][d0 + j], L.cs[1][d0 + j], r1[j], r2[j]);
+        }
+        const u32x4 z = {0u, 0u, 0u, 0u};
+        qf[ks] = c16 < n_rep ? pack8(r1) : z;
+        qf[ks + KT / 2] = c16 < n_rep ? pack8(r2) : z;
+      }
+      m = -INFINITY;
+      lsum = 0.f;
+#pragma unroll
+      for (int blk = 0; blk < DB; ++blk) acc[blk] = f32x4v{0.f, 0.f, 0.f, 0.f};
     }
-  }
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  const float ltot = pair_sum32(lsum);
-  // merge the wavefronts: (m, l) per head, then o through LDS (reuses sV)
-  if (hh == 0) {
-    sML[w][0][c32] = m;
-    sML[w][1][c32] = ltot;
-  }
-  __syncthreads();
-  // [wave][D][32 heads], head index XOR-swizzled by d so that both the column
-  // writes below and the row reads after are conflict-free
-  float* so = (float*)&sV[0][0][0];
-  auto so_at = [&](int ww, int d, int h) { return ((ww * D + d) << 5) + (h ^ ((d >> 1) & 31)); };
-  float M = -INFINITY;
+    uint32_t vnew = 0u;
+    if (has_new) {
+      // the new token: lane e < D / 2 holds dims 2e, 2e + 1; the RoPE partner
+      // dims (+ HALF) sit in lane e ^ (HALF / 2)
+      const int e = lane;
+      const bool act = e < D / 2;
+      const bool first = (e & (HALF / 2)) == 0;  // dims < HALF
+      const uint32_t own = st.kv[0];
+      const uint32_t par = (uint32_t)__shfl_xor((int)own, HALF / 2, 64);
+      float x[2] = {__uint_as_float(own << 16), __uint_as_float(own & 0xffff0000u)};
+      float y[2] = {__uint_as_float(par << 16), __uint_as_float(par & 0xffff0000u)};
+      const int dd = (2 * e) % HALF;  // table index of the pair
+      if constexpr (QKN) {
+        float ss = act ? x[0] * x[0] + x[1] * x[1] : 0.f;
+        ss = wave_sum(ss);
 #pragma unroll
-  for (int ww = 0; ww < DEC_WAVES; ++ww) M = fmaxf(M, sML[ww][0][c32]);
-  const float wgt = m == -INFINITY ? 0.f : fast_exp2(m - M);
+        for (int t = 0; t < 2; ++t) {
+          const int d = act ? 2 * e + t : 0;
+          const int dp = d ^ HALF;  // the partner dim
+          x[t] = rms_scale<bf16>(x[t], ss, D, eps, knw[d]);
+          y[t] = rms_scale<bf16>(y[t], ss, D, eps, knw[dp]);
+        }
+      }
+      float r[2];
 #pragma unroll
-  for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int d = 32 * dt + 8 * (i >> 2) + 4 * hh + (i & 3);
-      so[so_at(w, d, c32)] = acc[dt][i] * wgt;
+      for (int t = 0; t < 2; ++t) {
+        float r1, r2;
+        const float c = L.cs[0][dd + t], sn = L.cs[1][dd + t];
+        if (first)
+          rope_pair<bf16>(x[t], y[t], c, sn, r1, r2);
+        else
+          rope_pair<bf16>(y[t], x[t], c, sn, r1, r2);
+        r[t] = first ? r1 : r2;
+      }
+      const uint32_t rk = pack2(r[0], r[1]);
+      const int64_t crow = (((int64_t)cc.b * Hkv + cc.g) * Smax + newrow) * D;
+      if (act) {
+        ((uint32_t*)L.nw)[e] = rk;
+        ((uint32_t*)(kc + crow))[e] = rk;
+        ((uint32_t*)(vc + crow))[e] = st.kv[1];
+      }
+      vnew = st.kv[1];
+      kvrow_k = L.nw;
     }
-  __syncthreads();
-  for (int it = threadIdx.x; it < n_rep * D; it += 256) {
-    const int hr = it / D, d = it % D;
-    float o = 0.f;
-#pragma unroll
-    for (int ww = 0; ww < DEC_WAVES; ++ww) o += so[so_at(ww, d, hr)];
-    const int64_t ph = ((int64_t)b * Hq + g * n_rep + hr) * nsplit + sp_idx;
-    opart[ph * D + d] = o;
-    if (d == 0) {
-      float Mh = -INFINITY;
-#pragma unroll
-      for (int ww = 0; ww < DEC_WAVES; ++ww) Mh = fmaxf(Mh, sML[ww][0][hr]);
-      float lh = 0.f;
-#pragma unroll
-      for (int ww = 0; ww < DEC_WAVES; ++ww)
-        lh += sML[ww][0][hr] == -INFINITY ? 0.f : sML[ww][1][hr] * fast_exp2(sML[ww][0][hr] - Mh);
-      mpart[ph] = Mh;
-      lpart[ph] = lh;
+    // the next chunk (possibly of the next pair): its pair data now, its K
+    // rows once this chunk's S products have read kreg, its V rows once this
+    // chunk's V rows are in LDS
+    const bool more = i + 1 < c_hi;
+    if (more) {
+      cursor_next(ic, s);
+      load_stash(ic, st, ic.lc == 0, ic.lc == ic.nck - 1);
     }
+    if (has_new) {
+      // the lane of the new row takes its key from L.nw
+      const int loc = newrow - r0;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        const bool is_new = 16 * kb + c16 == loc;
+#pragma unroll
+        for (int ks = 0; ks < KT; ++ks) {
+          const u32x4 nk = *(const u32x4*)(kvrow_k + 32 * ks + 8 * q4);
+          kreg[kb][ks] = is_new ? nk : kreg[kb][ks];
+        }
+      }
+    }
+    // S^T and the online softmax (per head: lanes c16, c16 + 16, + 32, + 48)
+    f32x4v sc[2];
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      sc[kb] = f32x4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < KT; ++ks)
+        sc[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kreg[kb][ks]),
+                                                         as_bf16x8(qf[ks]), sc[kb], 0, 0, 0);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int local = 16 * kb + 4 * q4 + t;
+        sc[kb][t] = local > lim ? -INFINITY : sc[kb][t] * scale_log2;
+        tmax = fmaxf(tmax, sc[kb][t]);
+      }
+    }
+    if (more) load_k(ic);
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+    const float mnew = fmaxf(m, tmax);  // finite: key r0 is valid
+    const float alpha = fast_exp2(m - mnew);
+    float p[8];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      p[t] = fast_exp2(sc[0][t] - mnew);
+      p[4 + t] = fast_exp2(sc[1][t] - mnew);
+    }
+    float psum = 0.f;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) psum += p[t];
+    lsum = lsum * alpha + psum;
+    m = mnew;
+    const u32x4 pb = {pack2(p[0], p[1]), pack2(p[2], p[3]), pack2(p[4], p[5]), pack2(p[6], p[7])};
+    // V rows into the tile (rows past the last key as zeros, the new row from v_new)
+#pragma unroll
+    for (int j = 0; j < VL; ++j) {
+      const int li = 64 * j + lane, row = li / KR, pc = li % KR;
+      const u32x4 z = {0u, 0u, 0u, 0u};
+      *(u32x4*)(L.v + (row * KR + (pc ^ swz<KR>(row))) * 8) = row > lim ? z : vreg[j];
+    }
+    // the V registers are free: the next chunk's rows (loaded one step ahead,
+    // like its K rows, which were issued at the top of this step)
+    if (more) load_v(ic);
+    if (has_new && lane < D / 2) {
+      const int row = newrow - r0, el = 2 * lane, pc = el >> 3;
+      *(uint32_t*)(L.v + (row * KR + (pc ^ swz<KR>(row))) * 8 + (el & 7)) = vnew;
+    }
+#pragma unroll
+    for (int blk = 0; blk < DB; ++blk) acc[blk] *= alpha;
+#pragma unroll
+    for (int blk = 0; blk < DB; ++blk) {
+      const char* base = (const char*)L.v + tr_base + (uint32_t)((blk ^ tr_hs) * 32);
+      const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)base);
+      const s16x4 hi =
+          __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)(base + 16 * KR * 16));
+      typedef short s16x8 __attribute__((ext_vector_type(8)));
+      const s16x8 vt = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+      acc[blk] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, vt),
+                                                         as_bf16x8(pb), acc[blk], 0, 0, 0);
+    }
+    if (!more || has_new) {
+      // the pair's part of this wavefront ends: partial (o, m, l) to slot gw + p
+      float ltot = lsum + __shfl_xor(lsum, 16, 64);
+      ltot += __shfl_xor(ltot, 32, 64);
+      if (c16 < n_rep) {
+        const int64_t slot = (int64_t)gw + (int64_t)cc.b * Hkv + cc.g;
+        float* orow = opart + (slot * n_rep + c16) * D;
+#pragma unroll
+        for (int blk = 0; blk < DB; ++blk) *(f32x4v*)(orow + 16 * blk + 4 * q4) = acc[blk];
+        if (q4 == 0) *(float2*)(mlpart + (slot * n_rep + c16) * 2) = make_float2(m, ltot);
+      }
+    }
+    cursor_next(cc, s);
   }
 }
 
-// One workgroup of D threads per (b, hq): every thread rescales and sums its
-// output element over the splits (independent loads, unrolled).
+// One workgroup of D threads per (b, hq): the partials of the wavefronts whose
+// ranges met pair (b, g) are rescaled to a common maximum and summed.
 template <typename T>
-__global__ __launch_bounds__(256) void decode_merge_kernel(const float* __restrict__ opart,
-                                                           const float* __restrict__ mpart,
-                                                           const float* __restrict__ lpart,
-                                                           const int32_t* __restrict__ lens,
-                                                           T* __restrict__ out, int Hq, int D,
-                                                           int nsplit, int max_len,
-                                                           int64_t row_offset,
-                                                           int64_t rope_rows) {
-  __shared__ float sw[1024];
+__global__ __launch_bounds__(256) void decode_merge_kernel(
+    const float* __restrict__ opart, const float* __restrict__ mlpart,
+    const int32_t* __restrict__ lens, T* __restrict__ out, int B, int Hq, int Hkv, int D,
+    int NW, int max_len, int64_t row_offset, int64_t rope_rows) {
+  __shared__ float sw[DEC_GRID_MAX * DEC_WAVES];
+  __shared__ int sRange[3];
   __shared__ float sinv;
   const int bh = blockIdx.x;
-  const int b = bh / Hq;
+  const int b = bh / Hq, hq = bh % Hq, n_rep = Hq / Hkv, g = hq / n_rep, h = hq % n_rep;
   const int d = threadIdx.x;
-  if (!decode_len_ok(lens[b], max_len, row_offset, rope_rows)) {
+  const DecodeSched s{lens, B, Hkv, max_len, row_offset, rope_rows};
+  if (threadIdx.x < 64) {
+    const int lane = threadIdx.x;
+    const int C = total_chunks(s, lane);
+    const int n = s.nck(b);
+    // first chunk of pair (b, g): Hkv * (chunks of sequences before b) + g * n
+    int pre = 0;
+    for (int b0 = 0; b0 < b; b0 += 64)
+      pre += wave_sum_int(b0 + lane < b ? s.nck(b0 + lane) : 0);
+    if (lane == 0) {
+      sRange[2] = C;
+      if (n == 0) {
+        sRange[0] = 1;
+        sRange[1] = 0;
+      } else {
+        const int c0 = pre * Hkv + g * n;
+        sRange[0] = chunk_owner(c0, C, NW);
+        sRange[1] = chunk_owner(c0 + n - 1, C, NW);
+      }
+    }
+  }
+  __syncthreads();
+  const int w0 = sRange[0], w1 = sRange[1], C = sRange[2];
+  if (w1 < w0) {  // unusable length: NaN output, no cache write happened
     if (d < D) out[(int64_t)bh * D + d] = from_f32<T>(NAN);
     return;
   }
-  const int ns = min((lens[b] + 1 + CH - 1) / CH, 1024);  // <= nsplit (lens[b] < max_len)
-  const int64_t base = (int64_t)bh * nsplit;
+  const int64_t p = (int64_t)b * Hkv + g;
   if (threadIdx.x < 64) {
     const int lane = threadIdx.x;
+    // wavefronts with an empty range (C < NW) between w0 and w1 wrote nothing
+    auto empty = [&](int w) {
+      return (int64_t)w * C / NW == (int64_t)(w + 1) * C / NW;
+    };
     float M = -INFINITY;
-    for (int s0 = lane; s0 < ns; s0 += 64) M = fmaxf(M, mpart[base + s0]);
+    for (int w = w0 + lane; w <= w1; w += 64)
+      if (!empty(w)) M = fmaxf(M, mlpart[((w + p) * n_rep + h) * 2]);
     M = wave_max(M);
     float lt = 0.f;
-    for (int s0 = lane; s0 < ns; s0 += 64) {
-      const float wgt = fast_exp2(mpart[base + s0] - M);
-      sw[s0] = wgt;
-      lt += lpart[base + s0] * wgt;
+    for (int w = w0 + lane; w <= w1; w += 64) {
+      float wgt = 0.f;
+      if (!empty(w)) {
+        const float2 ml = *(const float2*)(mlpart + ((w + p) * n_rep + h) * 2);
+        wgt = fast_exp2(ml.x - M);
+        lt += ml.y * wgt;
+      }
+      sw[w - w0] = wgt;
     }
     lt = wave_sum(lt);
     if (lane == 0) sinv = 1.f / lt;
   }
   __syncthreads();
   if (d >= D) return;
+  const int n = w1 - w0 + 1;
+  const float* ob = opart + ((w0 + p) * n_rep + h) * D + d;
+  const int64_t stride = (int64_t)n_rep * D;
   float o = 0.f;
-  int s = 0;
-  for (; s + 4 <= ns; s += 4) {
-    const float a0 = opart[(base + s) * D + d], a1 = opart[(base + s + 1) * D + d];
-    const float a2 = opart[(base + s + 2) * D + d], a3 = opart[(base + s + 3) * D + d];
-    o += a0 * sw[s] + a1 * sw[s + 1] + a2 * sw[s + 2] + a3 * sw[s + 3];
+  int j = 0;
+  // an empty wavefront's slot holds stale data: its weight is 0 and it is not read
+  for (; j + 4 <= n; j += 4) {
+    float a[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) a[u] = sw[j + u] != 0.f ? ob[(j + u) * stride] : 0.f;
+    o += a[0] * sw[j] + a[1] * sw[j + 1] + a[2] * sw[j + 2] + a[3] * sw[j + 3];
   }
-  for (; s < ns; ++s) o += opart[(base + s) * D + d] * sw[s];
+  for (; j < n; ++j)
+    if (sw[j] != 0.f) o += ob[j * stride] * sw[j];
   out[(int64_t)bh * D + d] = from_f32<T>(o * sinv);
 }
 
@@ -630,38 +685,45 @@ int launch_append(const T* k_new, const T* v_new, const float* cos, const float*
   return KF_OK;
 }
 
+// Grid of the stream kernel: two workgroups per CU, at most DEC_GRID_MAX.
+int decode_grid() { return std::max(1, std::min(DEC_GRID_MAX, 2 * device_cu_count())); }
+
 template <int D>
-int launch_split(const DecodeArgs& a, float* opart, float* mpart, float* lpart, int nsplit) {
+int launch_stream(const DecodeArgs& a, float* opart, float* mlpart, int grid) {
   const bool qkn = a.q_norm_w != nullptr;
-  KF_LAUNCH("decode_split", (qkn ? decode_split_kernel<D, true> : decode_split_kernel<D, false>),
-            dim3(nsplit, a.B * a.Hkv), dim3(256), 0,
-            a.stream, (const bf16*)a.q_new, (const bf16*)a.k_new, (const bf16*)a.v_new, a.cos,
-            a.sin, a.rope_row_offset, a.rope_rows, a.max_len, (bf16*)a.k_cache, (bf16*)a.v_cache,
-            a.lens, opart, mpart, lpart, a.Hq, a.Hkv, a.Smax, nsplit, a.Hq / a.Hkv,
-            a.scale * kLog2e, a.q_norm_w, a.k_norm_w, a.norm_eps);
+  KF_LAUNCH("decode_stream", (qkn ? decode_stream_kernel<D, true> : decode_stream_kernel<D, false>),
+            dim3(grid), dim3(64 * DEC_WAVES), 0, a.stream, (const bf16*)a.q_new,
+            (const bf16*)a.k_new, (const bf16*)a.v_new, a.cos, a.sin, a.rope_row_offset,
+            a.rope_rows, a.max_len, (bf16*)a.k_cache, (bf16*)a.v_cache, a.lens, opart, mlpart,
+            a.B, a.Hq, a.Hkv, a.Smax, a.Hq / a.Hkv, a.scale * kLog2e, a.q_norm_w, a.k_norm_w,
+            a.norm_eps);
   KF_CHECK_LAUNCH();
   return KF_OK;
 }
+
+// Partial slots of the stream kernel: one per (wavefront, pair it touches),
+// at most the grid's wavefronts plus the pairs.
+size_t decode_slots(int B, int Hkv) { return (size_t)DEC_GRID_MAX * DEC_WAVES + (size_t)B * Hkv; }
 
 template <typename T>
 int decode_typed(const DecodeArgs& a, void* workspace) {
   int rc = KF_OK;
   const int n_rep = a.Hq / a.Hkv;
-  const bool fast = __is_same(T, bf16) && (a.D == 64 || a.D == 128) && n_rep <= 32 &&
-                    (a.max_len + CH - 1) / CH <= 1024 &&
+  const bool fast = __is_same(T, bf16) && (a.D == 64 || a.D == 128) && n_rep <= 16 &&
+                    (int64_t)a.B * a.Hkv * ((a.max_len + KC - 1) / KC) < INT_MAX &&
                     ((uintptr_t)a.q_new | (uintptr_t)a.k_new | (uintptr_t)a.v_new |
                      (uintptr_t)a.k_cache | (uintptr_t)a.v_cache) % 16 == 0;
   if (fast) {
-    const int nsplit = (a.max_len + CH - 1) / CH;
+    const size_t slots = decode_slots(a.B, a.Hkv);
     float* opart = (float*)workspace;
-    float* mpart = opart + (size_t)a.B * a.Hq * nsplit * a.D;
-    float* lpart = mpart + (size_t)a.B * a.Hq * nsplit;
-    rc = a.D == 128 ? launch_split<128>(a, opart, mpart, lpart, nsplit)
-                    : launch_split<64>(a, opart, mpart, lpart, nsplit);
+    float* mlpart = opart + slots * n_rep * a.D;
+    const int grid = decode_grid();
+    rc = a.D == 128 ? launch_stream<128>(a, opart, mlpart, grid)
+                    : launch_stream<64>(a, opart, mlpart, grid);
     if (rc) return rc;
     KF_LAUNCH("decode_merge", decode_merge_kernel<T>, dim3(a.B * a.Hq), dim3(a.D), 0, a.stream,
-              opart, mpart, lpart, a.lens, (T*)a.out, a.Hq, a.D, nsplit, a.max_len,
-              a.rope_row_offset, a.rope_rows);
+              opart, mlpart, a.lens, (T*)a.out, a.B, a.Hq, a.Hkv, a.D, grid * DEC_WAVES,
+              a.max_len, a.rope_row_offset, a.rope_rows);
     KF_CHECK_LAUNCH();
     return KF_OK;
   }
@@ -679,9 +741,10 @@ int decode_typed(const DecodeArgs& a, void* workspace) {
 
 }  // namespace
 
-size_t decode_workspace(int B, int Hq, int D, int max_len) {
-  const size_t nsplit = (size_t)((max_len + CH - 1) / CH);
-  return (size_t)B * Hq * nsplit * (D + 2) * sizeof(float);
+size_t decode_workspace(int B, int Hq, int Hkv, int D, int max_len) {
+  (void)max_len;
+  const size_t n_rep = (size_t)(Hq / Hkv);
+  return decode_slots(B, Hkv) * n_rep * (size_t)(D + 2) * sizeof(float);
 }
 
 int decode(const DecodeArgs& a, void* workspace) {

@@ -93,8 +93,9 @@ struct DecodeArgs {
   float scale;
   hipStream_t stream;
 };
-size_t decode_workspace(int B, int Hq, int D, int max_len);
+size_t decode_workspace(int B, int Hq, int Hkv, int D, int max_len);
 int decode(const DecodeArgs& a, void* workspace);
+
 
 // cache append (kf_decode.hip)
 int cache_append(const void* k_new, const void* v_new, const float* cos, const float* sin,
