@@ -136,7 +136,7 @@ int kf_attn_decode_workspace_size(int B, int Hq, int Hkv, int D, int max_len, in
  *       KVCache.seq_len for the batch; equal entries reproduce it)
  *   rope_cos/sin [rope_rows, D/2]: sequence b uses row lens[b] - rope_row_offset
  *   out  [B, 1, Hq, D]
- *   max_len  an upper bound on lens[b] + 1 (<= Smax); sizes the grid
+ *   max_len  an upper bound on lens[b] + 1 (<= Smax)
  *   q_norm_weight, k_norm_weight  [D] float32 per-head RMSNorm weights, or
  *       both NULL: given, q_new and k_new are normalised first, as the
  *       reference's q_norm / k_norm do before RoPE (kempnerforge/model/
@@ -156,6 +156,27 @@ int kf_attn_decode(const void* q_new, const void* k_new, const void* v_new, void
                    size_t workspace_bytes, int B, int Smax, int Hq, int Hkv, int D, int max_len,
                    const float* q_norm_weight, const float* k_norm_weight, float norm_eps,
                    int dtype, void* stream);
+
+/* kf_attn_decode without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid allocation).  No counterpart in the reference.
+ *
+ * Same arguments and results as kf_attn_decode.  The split-K partial results
+ * live in one static device array of 32 MiB per GPU, held from the library's
+ * load until the process ends; a call whose workspace would not fit
+ * (kf_attn_decode_workspace_size > 32 MiB, e.g. B * Hkv beyond about 6000 at
+ * 8 query heads per KV head and head_dim 128) returns KF_ERR_WORKSPACE.  Each
+ * call writes the partials it reads, so nothing needs clearing between calls.
+ * Every call on one GPU uses the same array: calls that overlap on one GPU
+ * (concurrent streams) race and must be serialised by the caller.  Allocates
+ * nothing, synchronises nothing. */
+int kf_attn_decode_noalloc(const void* q_new, const void* k_new, const void* v_new,
+                           void* k_cache, void* v_cache, const int32_t* lens,
+                           const float* rope_cos, const float* rope_sin,
+                           int64_t rope_row_offset, int64_t rope_rows, void* out, int B,
+                           int Smax, int Hq, int Hkv, int D, int max_len,
+                           const float* q_norm_weight, const float* k_norm_weight,
+                           float norm_eps, int dtype, void* stream);
 
 /* Append Snew tokens to a KV cache at positions start .. start+Snew-1.
  *

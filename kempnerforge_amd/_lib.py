@@ -35,6 +35,8 @@ SIGNATURES = {
     "kf_attn_decode_workspace_size": ([_c_int] * 6 + [_szp], _c_int),
     "kf_attn_decode": ([_vp, _vp, _vp, _vp, _vp, _vp, _fp, _fp, _c_i64, _c_i64, _vp, _vp, _c_sz]
                        + [_c_int] * 6 + [_fp, _fp, ctypes.c_float, _c_int, _vp], _c_int),
+    "kf_attn_decode_noalloc": ([_vp, _vp, _vp, _vp, _vp, _vp, _fp, _fp, _c_i64, _c_i64, _vp]
+                               + [_c_int] * 6 + [_fp, _fp, ctypes.c_float, _c_int, _vp], _c_int),
     "kf_kv_cache_append": ([_vp, _vp, _fp, _fp, _vp, _vp] + [_c_int] * 7 + [_vp], _c_int),
     "kf_attn_capture_workspace_size": ([_c_int] * 7 + [_szp], _c_int),
     "kf_attn_capture": ([_vp, _vp, _vp, _fp, _fp, _fp, _vp, _fp, _vp, _c_sz] + [_c_int] * 6

@@ -253,6 +253,31 @@ int kf_attn_decode(const void* q_new, const void* k_new, const void* v_new, void
   return decode(a, workspace);
 }
 
+int kf_attn_decode_noalloc(const void* q_new, const void* k_new, const void* v_new,
+                           void* k_cache, void* v_cache, const int32_t* lens,
+                           const float* rope_cos, const float* rope_sin,
+                           int64_t rope_row_offset, int64_t rope_rows, void* out, int B,
+                           int Smax, int Hq, int Hkv, int D, int max_len,
+                           const float* q_norm_weight, const float* k_norm_weight,
+                           float norm_eps, int dtype, void* stream) {
+  DecodeArgs a;
+  int rc = decode_args(&a, q_new, k_new, v_new, k_cache, v_cache, lens, rope_cos, rope_sin,
+                       rope_row_offset, rope_rows, out, B, Smax, Hq, Hkv, D, max_len,
+                       q_norm_weight, k_norm_weight, norm_eps, dtype, stream);
+  if (rc) return rc;
+  const size_t need = decode_workspace(B, Hq, Hkv, D, max_len);
+  if (need > DECODE_SCRATCH_BYTES) {
+    set_error("decode needs %zu bytes of partials, more than the %zu-byte static scratch of "
+              "kf_attn_decode_noalloc; use kf_attn_decode with a workspace",
+              need, (size_t)DECODE_SCRATCH_BYTES);
+    return KF_ERR_WORKSPACE;
+  }
+  void* ptr = nullptr;
+  rc = decode_scratch(&ptr);
+  if (rc) return rc;
+  return decode(a, ptr);
+}
+
 int kf_kv_cache_append(const void* k_new, const void* v_new, const float* rope_cos,
                        const float* rope_sin, void* k_cache, void* v_cache, int start, int B,
                        int Snew, int Hkv, int Smax, int D, int dtype, void* stream) {

@@ -22,7 +22,9 @@
 #include "kf_mfma.h"
 
 #include <algorithm>
+#include <atomic>
 #include <climits>
+#include <mutex>
 #include <type_traits>
 
 namespace kf {
@@ -745,6 +747,45 @@ size_t decode_workspace(int B, int Hq, int Hkv, int D, int max_len) {
   (void)max_len;
   const size_t n_rep = (size_t)(Hq / Hkv);
   return decode_slots(B, Hkv) * n_rep * (size_t)(D + 2) * sizeof(float);
+}
+
+// ---- allocation-free decode ---------------------------------------------------
+// The decode's partials for callers that cannot allocate: one array in device
+// memory for the life of the process, a copy per device the library runs on.
+// In host code `scratch` only names the symbol; the device address of the
+// current device's copy comes from hipGetSymbolAddress, looked up once per
+// device and kept.  Nothing in it needs clearing: a call reads only the
+// partial slots it wrote itself.
+static __device__ __align__(256) unsigned char scratch[DECODE_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::atomic<void*> g_scratch_ptr[kMaxDevices];
+std::mutex g_scratch_mu;
+}  // namespace
+
+int decode_scratch(void** ptr) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    set_error("decode scratch: no usable current device (%s)", hipGetErrorString(e));
+    return KF_ERR_HIP;
+  }
+  void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (p == nullptr) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+    if (p == nullptr) {
+      e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      if (e != hipSuccess || p == nullptr) {
+        set_error("decode scratch: hipGetSymbolAddress failed (%s)", hipGetErrorString(e));
+        return KF_ERR_HIP;
+      }
+      g_scratch_ptr[dev].store(p, std::memory_order_release);
+    }
+  }
+  *ptr = p;
+  return KF_OK;
 }
 
 int decode(const DecodeArgs& a, void* workspace) {

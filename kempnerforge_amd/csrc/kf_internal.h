@@ -95,7 +95,10 @@ struct DecodeArgs {
 };
 size_t decode_workspace(int B, int Hq, int Hkv, int D, int max_len);
 int decode(const DecodeArgs& a, void* workspace);
-
+// Allocation-free decode: the current device's copy of a static device array
+// of DECODE_SCRATCH_BYTES stands in for the workspace.
+constexpr size_t DECODE_SCRATCH_BYTES = (size_t)32 << 20;
+int decode_scratch(void** ptr);
 
 // cache append (kf_decode.hip)
 int cache_append(const void* k_new, const void* v_new, const float* cos, const float* sin,
