@@ -163,9 +163,27 @@ __device__ __forceinline__ void locate_chunk(const DecodeSched& s, int c, int la
   }
 }
 
+// floor(x / d) for 0 <= x < 2^53 and 0 < d < 2^31: the double quotient is
+// within one of the exact one (its relative error is below 2^-52 and x / d <
+// 2^53), so one correction step either way makes it exact, in far fewer
+// instructions than a 64-bit integer division.
+__device__ __forceinline__ int64_t floor_div(int64_t x, int64_t d) {
+  int64_t q = (int64_t)((double)x / (double)d);
+  if (q * d > x)
+    --q;
+  else if ((q + 1) * d <= x)
+    ++q;
+  return q;
+}
+
+// First chunk of wavefront w's range, floor(w C / NW).
+__device__ __forceinline__ int range_start(int w, int C, int NW) {
+  return (int)floor_div((int64_t)w * C, NW);
+}
+
 // The wavefront whose range holds chunk c: the largest w with w C / NW <= c.
 __device__ __forceinline__ int chunk_owner(int c, int C, int NW) {
-  return (int)((((int64_t)c + 1) * NW - 1) / C);
+  return (int)floor_div(((int64_t)c + 1) * NW - 1, C);
 }
 
 // Position in the chunk list: pair (b, g), local chunk lc of nck, new-token
@@ -254,7 +272,7 @@ __global__ __launch_bounds__(256, 2) void decode_stream_kernel(
   const DecodeSched s{lens, B, Hkv, max_len, row_offset, rope_rows};
   const int NW = gridDim.x * DEC_WAVES, gw = blockIdx.x * DEC_WAVES + w;
   const int C = total_chunks(s, lane);
-  const int c_lo = (int)((int64_t)gw * C / NW), c_hi = (int)((int64_t)(gw + 1) * C / NW);
+  const int c_lo = range_start(gw, C, NW), c_hi = range_start(gw + 1, C, NW);
   if (c_lo >= c_hi) return;
 
   // the chunk's rows, loaded one step ahead: each set is reloaded for the next
@@ -520,87 +538,88 @@ __global__ __launch_bounds__(256, 2) void decode_stream_kernel(
   }
 }
 
-// One workgroup of D threads per (b, hq): the partials of the wavefronts whose
-// ranges met pair (b, g) are rescaled to a common maximum and summed.
-template <typename T>
+// One wavefront per (b, hq), four per workgroup: the partials of the
+// wavefronts whose ranges met pair (b, g) are rescaled to a common maximum and
+// summed.  The slot range comes from one pass over lens; the partial outputs
+// of the first MERGE_PRE slots are then loaded together with the (m, l)
+// values, so a merge costs two dependent memory round trips.
+constexpr int MERGE_PRE = 16;
+
+template <int D>
 __global__ __launch_bounds__(256) void decode_merge_kernel(
     const float* __restrict__ opart, const float* __restrict__ mlpart,
-    const int32_t* __restrict__ lens, T* __restrict__ out, int B, int Hq, int Hkv, int D,
-    int NW, int max_len, int64_t row_offset, int64_t rope_rows) {
-  __shared__ float sw[DEC_GRID_MAX * DEC_WAVES];
-  __shared__ int sRange[3];
-  __shared__ float sinv;
-  const int bh = blockIdx.x;
+    const int32_t* __restrict__ lens, bf16* __restrict__ out, int B, int Hq, int Hkv, int NW,
+    int max_len, int64_t row_offset, int64_t rope_rows) {
+  constexpr int PER = D / 64;
+  const int lane = threadIdx.x & 63;
+  const int bh = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (bh >= B * Hq) return;
   const int b = bh / Hq, hq = bh % Hq, n_rep = Hq / Hkv, g = hq / n_rep, h = hq % n_rep;
-  const int d = threadIdx.x;
   const DecodeSched s{lens, B, Hkv, max_len, row_offset, rope_rows};
-  if (threadIdx.x < 64) {
-    const int lane = threadIdx.x;
-    const int C = total_chunks(s, lane);
-    const int n = s.nck(b);
-    // first chunk of pair (b, g): Hkv * (chunks of sequences before b) + g * n
-    int pre = 0;
-    for (int b0 = 0; b0 < b; b0 += 64)
-      pre += wave_sum_int(b0 + lane < b ? s.nck(b0 + lane) : 0);
-    if (lane == 0) {
-      sRange[2] = C;
-      if (n == 0) {
-        sRange[0] = 1;
-        sRange[1] = 0;
-      } else {
-        const int c0 = pre * Hkv + g * n;
-        sRange[0] = chunk_owner(c0, C, NW);
-        sRange[1] = chunk_owner(c0 + n - 1, C, NW);
-      }
-    }
+  // C, Hkv * (chunks of the sequences before b) and b's chunks, from one
+  // load of lens per lane
+  int tot = 0, pre = 0, n = 0;
+  for (int b0 = 0; b0 < B; b0 += 64) {
+    const int nb = b0 + lane < B ? s.nck(b0 + lane) : 0;
+    tot += wave_sum_int(nb);
+    pre += wave_sum_int(b0 + lane < b ? nb : 0);
+    if (b >= b0 && b < b0 + 64) n = __shfl(nb, b - b0, 64);
   }
-  __syncthreads();
-  const int w0 = sRange[0], w1 = sRange[1], C = sRange[2];
-  if (w1 < w0) {  // unusable length: NaN output, no cache write happened
-    if (d < D) out[(int64_t)bh * D + d] = from_f32<T>(NAN);
+  const int C = tot * Hkv;
+  bf16* orow = out + (int64_t)bh * D + lane;
+  if (n == 0) {  // unusable length: NaN output, no cache write happened
+#pragma unroll
+    for (int k = 0; k < PER; ++k) orow[64 * k] = (bf16)NAN;
     return;
   }
-  const int64_t p = (int64_t)b * Hkv + g;
-  if (threadIdx.x < 64) {
-    const int lane = threadIdx.x;
-    // wavefronts with an empty range (C < NW) between w0 and w1 wrote nothing
-    auto empty = [&](int w) {
-      return (int64_t)w * C / NW == (int64_t)(w + 1) * C / NW;
-    };
-    float M = -INFINITY;
-    for (int w = w0 + lane; w <= w1; w += 64)
-      if (!empty(w)) M = fmaxf(M, mlpart[((w + p) * n_rep + h) * 2]);
-    M = wave_max(M);
-    float lt = 0.f;
-    for (int w = w0 + lane; w <= w1; w += 64) {
-      float wgt = 0.f;
-      if (!empty(w)) {
-        const float2 ml = *(const float2*)(mlpart + ((w + p) * n_rep + h) * 2);
-        wgt = fast_exp2(ml.x - M);
-        lt += ml.y * wgt;
-      }
-      sw[w - w0] = wgt;
-    }
-    lt = wave_sum(lt);
-    if (lane == 0) sinv = 1.f / lt;
-  }
-  __syncthreads();
-  if (d >= D) return;
-  const int n = w1 - w0 + 1;
-  const float* ob = opart + ((w0 + p) * n_rep + h) * D + d;
-  const int64_t stride = (int64_t)n_rep * D;
-  float o = 0.f;
-  int j = 0;
-  // an empty wavefront's slot holds stale data: its weight is 0 and it is not read
-  for (; j + 4 <= n; j += 4) {
-    float a[4];
+  const int c0 = pre * Hkv + g * n;
+  const int w0 = chunk_owner(c0, C, NW), ns = chunk_owner(c0 + n - 1, C, NW) - w0 + 1;
+  const int64_t first = ((int64_t)w0 + (int64_t)b * Hkv + g) * n_rep + h;  // slot w0 + p's row
+  const float* ob = opart + first * D + lane;
+  const float* mb = mlpart + first * 2;
+  const int64_t ost = (int64_t)n_rep * D, mst = (int64_t)n_rep * 2;  // per slot
+  // wavefronts with an empty range (C < NW) between w0 and w1 wrote nothing:
+  // their slots hold stale data, get weight 0 and are never added
+  auto live = [&](int j) {
+    return j < ns && range_start(w0 + j, C, NW) != range_start(w0 + j + 1, C, NW);
+  };
+  float po[MERGE_PRE][PER];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) a[u] = sw[j + u] != 0.f ? ob[(j + u) * stride] : 0.f;
-    o += a[0] * sw[j] + a[1] * sw[j + 1] + a[2] * sw[j + 2] + a[3] * sw[j + 3];
+  for (int j = 0; j < MERGE_PRE; ++j)
+#pragma unroll
+    for (int k = 0; k < PER; ++k) po[j][k] = j < ns ? ob[j * ost + 64 * k] : 0.f;
+  const bool live0 = live(lane);
+  float2 ml0 = make_float2(-INFINITY, 0.f);
+  if (live0) ml0 = *(const float2*)(mb + lane * mst);
+  float M = ml0.x;
+  for (int j = 64 + lane; j < ns; j += 64)
+    if (live(j)) M = fmaxf(M, mb[j * mst]);
+  M = wave_max(M);
+  const float wgt0 = live0 ? fast_exp2(ml0.x - M) : 0.f;
+  float lt = live0 ? ml0.y * wgt0 : 0.f;
+  for (int j = 64 + lane; j < ns; j += 64)
+    if (live(j)) lt += mb[j * mst + 1] * fast_exp2(mb[j * mst] - M);
+  lt = wave_sum(lt);
+  float o[PER];
+#pragma unroll
+  for (int k = 0; k < PER; ++k) o[k] = 0.f;
+#pragma unroll
+  for (int j = 0; j < MERGE_PRE; ++j) {
+    const float wj = __shfl(wgt0, j, 64);
+    if (wj != 0.f)
+#pragma unroll
+      for (int k = 0; k < PER; ++k) o[k] += po[j][k] * wj;
   }
-  for (; j < n; ++j)
-    if (sw[j] != 0.f) o += ob[j * stride] * sw[j];
-  out[(int64_t)bh * D + d] = from_f32<T>(o * sinv);
+  for (int j = MERGE_PRE; j < ns; ++j) {
+    const float wj = j < 64 ? __shfl(wgt0, j, 64)
+                            : (live(j) ? fast_exp2(mb[j * mst] - M) : 0.f);
+    if (wj != 0.f)
+#pragma unroll
+      for (int k = 0; k < PER; ++k) o[k] += ob[j * ost + 64 * k] * wj;
+  }
+  const float inv = 1.f / lt;
+#pragma unroll
+  for (int k = 0; k < PER; ++k) orow[64 * k] = (bf16)(o[k] * inv);
 }
 
 // One wavefront per (b, hq); keys 0..lens[b] read from the (already appended)
@@ -723,9 +742,10 @@ int decode_typed(const DecodeArgs& a, void* workspace) {
     rc = a.D == 128 ? launch_stream<128>(a, opart, mlpart, grid)
                     : launch_stream<64>(a, opart, mlpart, grid);
     if (rc) return rc;
-    KF_LAUNCH("decode_merge", decode_merge_kernel<T>, dim3(a.B * a.Hq), dim3(a.D), 0, a.stream,
-              opart, mlpart, a.lens, (T*)a.out, a.B, a.Hq, a.Hkv, a.D, grid * DEC_WAVES,
-              a.max_len, a.rope_row_offset, a.rope_rows);
+    KF_LAUNCH("decode_merge", (a.D == 128 ? decode_merge_kernel<128> : decode_merge_kernel<64>),
+              dim3((a.B * a.Hq + 3) / 4), dim3(256), 0, a.stream, opart, mlpart, a.lens,
+              (bf16*)a.out, a.B, a.Hq, a.Hkv, grid * DEC_WAVES, a.max_len, a.rope_row_offset,
+              a.rope_rows);
     KF_CHECK_LAUNCH();
     return KF_OK;
   }
