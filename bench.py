@@ -50,7 +50,7 @@ C5 = dict(B=1, S=16384, Hq=64, Hkv=8, D=128, theta=500000.0, cap_tokens=2048)
 
 # what bounds each kernel (the roofline its "achieved" figure is quoted on)
 BOUND = {"fwd_mfma": "mfma", "bwd_dkdv": "mfma", "bwd_dq": "mfma", "bwd_dq_ds": "hbm",
-         "q_prep_bwd": "hbm", "kv_prep": "hbm", "decode_split": "hbm", "decode_merge": "hbm",
+         "q_prep_bwd": "hbm", "kv_prep": "hbm", "decode_stream": "hbm", "decode_merge": "hbm",
          "capture_probs": "hbm", "capture_lse": "mfma"}
 
 
@@ -385,15 +385,15 @@ def run_full(args, torch, wl):
     n_dec = max(args.steps, 50)
     dec_s = timed(torch, wl.c4_step, args.warmup, n_dec)
     dstats = kernel_stats(torch, wl.c4_step, n_dec)
-    split_us = dstats.get("decode_split", {}).get("avg_us")
+    stream_us = dstats.get("decode_stream", {}).get("avg_us")
     decode = {"config": "C4 B=32 Hq=32 Hkv=8 D=128 L~U[1024,8192] seed 4",
               "bytes": dec_bytes, "us_per_step": round(dec_s * 1e6, 1),
               "GB/s": round(dec_bytes / dec_s / 1e9, 1),
               "frac_of_hbm_peak": round(dec_bytes / dec_s / 1e9 / PEAK_HBM_GBPS, 4),
               "kernels_us": {n: round(s["avg_us"], 1) for n, s in dstats.items()},
-              "split_kernel_GB/s": round(dec_bytes / (split_us * 1e-6) / 1e9, 1)
-              if split_us else None,
-              "split_kernel_traffic": traffic.get("decode_split@C4")}
+              "stream_kernel_GB/s": round(dec_bytes / (stream_us * 1e-6) / 1e9, 1)
+              if stream_us else None,
+              "stream_kernel_traffic": traffic.get("decode_stream@C4")}
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -437,12 +437,18 @@ def run_full(args, torch, wl):
 # --------------------------------------------------------------------------- rocprof summary
 def _short(name: str) -> str:
     """Kernel symbol -> the launcher's name (kf::..._kernel<...> -> ...)."""
-    m = re.search(r"(kv_prep|fwd_mfma|q_prep_bwd|bwd_dkdv|bwd_dq_ds|bwd_dq|decode_split|"
+    m = re.search(r"(kv_prep|fwd_mfma|q_prep_bwd|bwd_dkdv|bwd_dq_ds|bwd_dq|decode_stream|"
                   r"decode_merge|capture_probs_mfma|capture_lse|kv_append|append)_kernel", name)
     if m:
         return {"capture_probs_mfma": "capture_probs", "append": "kv_append"}.get(m.group(1),
                                                                                  m.group(1))
     return "copy" if "copyBuffer" in name else name[:40]
+
+
+def _ours(name: str) -> bool:
+    """A kernel of this library (rocprofv3 reports some names mangled, some
+    demangled)."""
+    return "_ZN2kf" in name or "kf::" in name
 
 
 def _drop_warmup(rows, warmup, steps, key):
@@ -484,19 +490,19 @@ def rocprof_summary(dirs, warmup, steps, traffic_json=None):
         pmc = sorted(glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True))
         if trace:
             with open(trace[0]) as f:
-                rows = [r for r in csv.DictReader(f) if "_ZN2kf" in r["Kernel_Name"]]
+                rows = [r for r in csv.DictReader(f) if _ours(r["Kernel_Name"])]
             rows.sort(key=lambda r: int(r["Start_Timestamp"]))
             by = _drop_warmup(rows, warmup, steps, lambda r: _short(r["Kernel_Name"]))
             lines.append(f"\n{wl}: kernel trace ({trace[0]})\n")
-            lines.append("| kernel | launches | avg us | median us | min us | VGPR | AGPR | LDS B |")
-            lines.append("|---|---|---|---|---|---|---|---|")
+            lines.append("| kernel | launches | avg us | median us | min us | LDS B |")
+            lines.append("|---|---|---|---|---|---|")
             for k, rs in sorted(by.items(), key=lambda kv: -sum(
                     int(r["End_Timestamp"]) - int(r["Start_Timestamp"]) for r in kv[1])):
                 us = [(int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3 for r in rs]
                 r0 = rs[0]
                 lines.append(f"| {k} | {len(us)} | {statistics.mean(us):.1f} | "
-                             f"{statistics.median(us):.1f} | {min(us):.1f} | {r0['VGPR_Count']} |"
-                             f" {r0['Accum_VGPR_Count']} | {r0['LDS_Block_Size']} |")
+                             f"{statistics.median(us):.1f} | {min(us):.1f} | "
+                             f"{r0['LDS_Block_Size']} |")
         for path in pmc:
             with open(path) as f:
                 rows = list(csv.DictReader(f))
@@ -506,7 +512,7 @@ def rocprof_summary(dirs, warmup, steps, traffic_json=None):
                 if "copyBuffer" in r["Kernel_Name"]:
                     calib[r["Counter_Name"]] = max(calib.get(r["Counter_Name"], 0.0),
                                                    float(r["Counter_Value"]))
-            rows = [r for r in rows if "_ZN2kf" in r["Kernel_Name"]]
+            rows = [r for r in rows if _ours(r["Kernel_Name"])]
             disp = {}
             for r in rows:
                 e = disp.setdefault((int(r["Dispatch_Id"]), _short(r["Kernel_Name"])), {})

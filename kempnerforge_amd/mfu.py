@@ -162,7 +162,7 @@ def attention_kernel_flops(pairs: int, head_dim: int, backward: bool = True) -> 
 
 
 # ---------------------------------------------------------------- profiler
-_ATTN_KEYS = ("fwd_mfma", "bwd_dkdv", "bwd_dq", "q_prep_bwd", "kv_prep", "decode_split",
+_ATTN_KEYS = ("fwd_mfma", "bwd_dkdv", "bwd_dq", "q_prep_bwd", "kv_prep", "decode_stream",
               "decode_merge", "decode_generic", "capture_probs", "fwd_generic",
               "bwd_dq_generic", "bwd_dkdv_generic", "cache_append", "append_kernel",
               "kf::attn", "flash", "fmha", "attention")

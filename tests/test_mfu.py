@@ -155,7 +155,7 @@ class TestClassifier:
         ("Memcpy DtoD", "memory"),
         ("fwd_mfma_kernel<128, false>", "attention"),
         ("bwd_dkdv_kernel<128, false>", "attention"),
-        ("decode_split_kernel<128>", "attention"),
+        ("decode_stream_kernel<128, false>", "attention"),
         ("kf::attn_fwd", "attention"),
         ("aten::relu", "other"),
     ])
