@@ -45,6 +45,7 @@
 #include "kf_mfma.h"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace kf {
 
@@ -65,8 +66,9 @@ __host__ __device__ constexpr int pad_len(int S) { return (S + BKV - 1) / BKV * 
 // 4*half + j = row 16c + 8*half + 4*hh + j.  Records are ordered (KV head,
 // query tile, key column, query head of the group); with a causal mask only
 // the key columns k32 <= 2*qt + 1 that the tile's rows can see exist.
-constexpr int DSQ = 64;  // query positions per record (= BQ)
-constexpr int DSK = 32;  // keys per record (one dS wavefront)
+constexpr int DSQ = DS_REC_Q;  // query positions per record (= BQ)
+constexpr int DSK = DS_REC_K;  // keys per record (one dS wavefront)
+static_assert(DSQ == BQ, "one record row block per query tile");
 constexpr int DS_DOC_MAX_TILES = 1024;  // packed documents keep records up to S = 65536
 
 // record pair index of (KV head bh, query tile qt, key column k32); nqtp = P / DSQ
@@ -278,35 +280,43 @@ __device__ __forceinline__ void dkdv_role(
     }
     u32x4 pk[4];
     if (!DSROLE) {
+      // the causal test only on diagonal tiles (a uniform branch, not a
+      // per-element select on every tile)
+      auto make_p = [&](auto masked) {
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt)
+        for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-        for (int gq = 0; gq < 4; ++gq) {
-          const int r0 = 32 * mt + 8 * gq + 4 * hh;
-          const f32x4 l4 = rowv[4 * mt + gq];
-          float v[4];
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            float p = fast_exp2(__builtin_fmaf(x[mt][4 * gq + j], scale_log2, -l4[j]));
-            if (!(KPM && dmask) && diag) p = (rel > r0 + j) ? 0.f : p;
-            v[j] = p;
-          }
-          if (DOC && dmask) {
-            const i32x4 qd = *(const i32x4*)&sQD[buf][r0];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) v[j] = qd[j] != kdoc ? 0.f : v[j];
-          }
-          if (KPM && dmask) {
-            // guarded rows keep every key; the others need it valid and not later
+          for (int gq = 0; gq < 4; ++gq) {
+            const int r0 = 32 * mt + 8 * gq + 4 * hh;
+            const f32x4 l4 = rowv[4 * mt + gq];
+            float v[4];
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-              const bool guarded = q0 + r0 + j < fv;
-              v[j] = (!guarded && (rel > r0 + j || !kdoc)) ? 0.f : v[j];
+              float p = fast_exp2(__builtin_fmaf(x[mt][4 * gq + j], scale_log2, -l4[j]));
+              if (decltype(masked)::value) p = (rel > r0 + j) ? 0.f : p;
+              v[j] = p;
             }
+            if (DOC && dmask) {
+              const i32x4 qd = *(const i32x4*)&sQD[buf][r0];
+#pragma unroll
+              for (int j = 0; j < 4; ++j) v[j] = qd[j] != kdoc ? 0.f : v[j];
+            }
+            if (KPM && dmask) {
+              // guarded rows keep every key; the others need it valid and not later
+#pragma unroll
+              for (int j = 0; j < 4; ++j) {
+                const bool guarded = q0 + r0 + j < fv;
+                v[j] = (!guarded && (rel > r0 + j || !kdoc)) ? 0.f : v[j];
+              }
+            }
+            pk[2 * mt + (gq >> 1)][2 * (gq & 1)] = pack2(v[0], v[1]);
+            pk[2 * mt + (gq >> 1)][2 * (gq & 1) + 1] = pack2(v[2], v[3]);
           }
-          pk[2 * mt + (gq >> 1)][2 * (gq & 1)] = pack2(v[0], v[1]);
-          pk[2 * mt + (gq >> 1)][2 * (gq & 1) + 1] = pack2(v[2], v[3]);
-        }
+      };
+      if (!(KPM && dmask) && diag)
+        make_p(std::true_type{});
+      else
+        make_p(std::false_type{});
 #pragma unroll
       for (int c = 0; c < 4; ++c) myP[c * 64] = pk[c];
     }

@@ -69,6 +69,10 @@ size_t fwd_mfma_workspace(int B, int Sk, int Hkv, int D);
 int fwd_mfma(const FwdArgs& a, void* workspace);
 int capture_probs_mfma(const FwdArgs& a, const float* lse, float* probs, void* workspace);
 
+// dS record tile of the backward (dK/dV kernels write, dQ reads): DS_REC_Q
+// query positions x DS_REC_K keys of one query head, 4 KB of bf16.
+constexpr int DS_REC_Q = 64, DS_REC_K = 32;
+
 bool bwd_mfma_supported(const BwdArgs& a);
 size_t bwd_mfma_workspace(int B, int S, int Hq, int Hkv, int D);
 // Workspace with which bwd_mfma stores the dS tiles once for dQ instead of
