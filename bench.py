@@ -49,7 +49,7 @@ C4 = dict(B=32, Hq=32, Hkv=8, D=128, lo=1024, hi=8192, theta=500000.0)
 C5 = dict(B=1, S=16384, Hq=64, Hkv=8, D=128, theta=500000.0, cap_tokens=2048)
 
 # what bounds each kernel (the roofline its "achieved" figure is quoted on)
-BOUND = {"fwd_mfma": "mfma", "bwd_dkdv": "mfma", "bwd_dkdv_wide": "mfma", "bwd_dq": "mfma", "bwd_dq_ds": "hbm",
+BOUND = {"fwd_mfma": "mfma", "bwd_dkdv": "mfma", "bwd_dq": "mfma", "bwd_dq_ds": "hbm",
          "q_prep_bwd": "hbm", "kv_prep": "hbm", "decode_stream": "hbm", "decode_merge": "hbm",
          "capture_probs": "hbm", "capture_lse": "mfma"}
 
@@ -323,8 +323,7 @@ def run_full(args, torch, wl):
     ms_step = secs * 1e3
     value = flops_step / secs / 1e12
     kstats = kernel_stats(torch, wl.c3_step, args.steps)
-    algo = {"fwd_mfma": 4.0 * D * P, "bwd_dkdv": 8.0 * D * P, "bwd_dkdv_wide": 8.0 * D * P,
-            "bwd_dq": 2.0 * D * P,
+    algo = {"fwd_mfma": 4.0 * D * P, "bwd_dkdv": 8.0 * D * P, "bwd_dq": 2.0 * D * P,
             "bwd_dq_ds": float(ds_record_bytes(B, Hq, S))}
     roof = roofline(kstats, algo, traffic, "C3")
     fwd_us = kstats.get("fwd_mfma", {}).get("avg_us")
@@ -364,8 +363,7 @@ def run_full(args, torch, wl):
     P5 = pairs(C5["B"], C5["Hq"], C5["S"])
     c5_s = timed(torch, wl.c5_step, 2, max(5, args.steps // 2))
     k5 = kernel_stats(torch, wl.c5_step, max(3, args.steps // 4))
-    algo5 = {"fwd_mfma": 4.0 * D * P5, "bwd_dkdv": 8.0 * D * P5, "bwd_dkdv_wide": 8.0 * D * P5,
-             "bwd_dq": 2.0 * D * P5,
+    algo5 = {"fwd_mfma": 4.0 * D * P5, "bwd_dkdv": 8.0 * D * P5, "bwd_dq": 2.0 * D * P5,
              "bwd_dq_ds": float(ds_record_bytes(C5["B"], C5["Hq"], C5["S"]))}
     c5 = {"config": "C5 llama3-70b fwd+bwd B=1 S=16384 Hq=64 Hkv=8 D=128",
           "ms": round(c5_s * 1e3, 3), "TFLOP/s": round(14.0 * D * P5 / c5_s / 1e12, 1),
@@ -439,8 +437,7 @@ def run_full(args, torch, wl):
 # --------------------------------------------------------------------------- rocprof summary
 def _short(name: str) -> str:
     """Kernel symbol -> the launcher's name (kf::..._kernel<...> -> ...)."""
-    m = re.search(r"(kv_prep|fwd_mfma|q_prep_bwd|bwd_dkdv_wide|bwd_dkdv|bwd_dq_ds|bwd_dq|"
-                  r"decode_stream|"
+    m = re.search(r"(kv_prep|fwd_mfma|q_prep_bwd|bwd_dkdv|bwd_dq_ds|bwd_dq|decode_stream|"
                   r"decode_merge|capture_probs_mfma|capture_lse|kv_append|append)_kernel", name)
     if m:
         return {"capture_probs_mfma": "capture_probs", "append": "kv_append"}.get(m.group(1),
