@@ -377,7 +377,7 @@ def run_full(args, torch, wl):
              "us": round(cap_s * 1e6, 1), "bytes": cap_b, "GB/s": round(cap_b / cap_s / 1e9, 1),
              "frac_of_hbm_peak": round(cap_b / cap_s / 1e9 / PEAK_HBM_GBPS, 4),
              "kernels_us": {n: round(s["avg_us"], 1) for n, s in kcap.items()},
-             "capture_kernel_traffic": traffic.get("capture_probs@C5-cap")}
+             "capture_kernel_traffic": traffic.get("capture_probs@C5CAP")}
     wl.c5_free()
 
     # C4 decode
