@@ -240,8 +240,10 @@ __device__ __forceinline__ void dkdv_role(
   __syncthreads();
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) settle(bf[ks]);
-  for (int it = 0; it < total; ++it) {
-    const int buf = it & 1;
+  // the tile loop unrolled by two, so that each copy's LDS buffer is a
+  // compile-time constant: fragment addresses are then loop-invariant per lane
+  auto tile_body = [&](int it, auto bufc) {
+    constexpr int buf = decltype(bufc)::value;
     if (it + 1 < total) stage(it + 1, buf ^ 1);
     const DkdvStage<D>& S_ = st[buf];
     const int e = entry(it);
@@ -395,6 +397,10 @@ __device__ __forceinline__ void dkdv_role(
     }
     lds_copy_wait();
     __syncthreads();
+  };
+  for (int it = 0; it < total; it += 2) {
+    tile_body(it, std::integral_constant<int, 0>{});
+    if (it + 1 < total) tile_body(it + 1, std::integral_constant<int, 1>{});
   }
 
   if (key >= S) return;

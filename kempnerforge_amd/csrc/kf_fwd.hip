@@ -26,6 +26,8 @@
 #include "kf_internal.h"
 #include "kf_mfma.h"
 
+#include <type_traits>
+
 namespace kf {
 
 namespace {
@@ -248,8 +250,11 @@ __global__ __launch_bounds__(256, 2) void fwd_mfma_kernel(
 
   lds_copy_wait();
   __syncthreads();
-  for (int it = 0; it < ntiles; ++it) {
-    const int buf = it & 1;
+  // the tile loop unrolled by two, so that each copy's LDS buffer is a
+  // compile-time constant: fragment addresses are then loop-invariant per lane
+  // (the buffer only changes the instruction's immediate offset)
+  auto tile_body = [&](int it, auto bufc) {
+    constexpr int buf = decltype(bufc)::value;
     const int e = entry(it);
     const int t = tile_of(e);
     if (it + 1 < ntiles) stage(tile_of(entry(it + 1)), buf ^ 1);
@@ -343,6 +348,10 @@ __global__ __launch_bounds__(256, 2) void fwd_mfma_kernel(
     }
     lds_copy_wait();
     __syncthreads();
+  };
+  for (int it = 0; it < ntiles; it += 2) {
+    tile_body(it, std::integral_constant<int, 0>{});
+    if (it + 1 < ntiles) tile_body(it + 1, std::integral_constant<int, 1>{});
   }
 
   const float ltot = pair_sum32(lsum);
