@@ -445,11 +445,13 @@ __global__ __launch_bounds__(256, 2) void capture_probs_mfma_kernel(
 
   // K tiles double-buffered: tile t+1 loads while tile t is computed and stored
   if (ntiles > 0) tile_to_lds<BN, KR>(kbase, D, sK[0], w, lane);
-  for (int t = 0; t < ntiles; ++t) {
+  // unrolled by two: each copy's LDS buffer is a compile-time constant
+  auto tile_body = [&](int t, auto bufc) {
+    constexpr int buf = decltype(bufc)::value;
     lds_copy_wait();
     __syncthreads();
-    if (t + 1 < ntiles) tile_to_lds<BN, KR>(kbase + (int64_t)(t + 1) * BN * D, D, sK[(t + 1) & 1], w, lane);
-    const bf16* tK = sK[t & 1];
+    if (t + 1 < ntiles) tile_to_lds<BN, KR>(kbase + (int64_t)(t + 1) * BN * D, D, sK[buf ^ 1], w, lane);
+    const bf16* tK = sK[buf];
     const bool diag = (causal && t * BN + BN - 1 > ri.p0) || t * BN + BN > Sk;
     f32x16 pv[2];
 #pragma unroll
@@ -486,6 +488,10 @@ __global__ __launch_bounds__(256, 2) void capture_probs_mfma_kernel(
         pbase[(int64_t)roff[i][h2] * Sk + key] = __uint_as_float(sw[h2]);
       }
     }
+  };
+  for (int t = 0; t < ntiles; t += 2) {
+    tile_body(t, std::integral_constant<int, 0>{});
+    if (t + 1 < ntiles) tile_body(t + 1, std::integral_constant<int, 1>{});
   }
   // zero the tiles right of the causal frontier
   if (causal) {
