@@ -2,12 +2,12 @@
 //
 // Four launches, no atomics (bit-deterministic):
 //  kv_prep      (shared with the forward) per KV head: K rotated (eager bf16
-//               RoPE) and V, both [bh][P][D].
+//               RoPE) [bh][P][D], rows past S zero.
 //  q_prep_bwd   per query head: Q rotated [bhq][P][D]; lse*log2(e) and Delta =
 //               rowsum(dO o O) [bhq][P].  P = S rounded up to 128; padded rows
-//               are zero with lse = +inf, so they contribute nothing.  dO is read
-//               in place ([B, S, Hq, D]) by the kernels below, rows past S
-//               repeating row S - 1.
+//               are zero with lse = +inf, so they contribute nothing.  dO and V
+//               are read in place ([B, S, H, D]) by the kernels below, rows past
+//               S repeating row S - 1 (or zero).
 //  Transposed operands (K^T, Q^T, dO^T) are never stored: they are read from
 //  the row-major LDS tiles with ds_read_b64_tr_b16 (lds_frag_t).
 //  dkdv         workgroup = 128 keys of one KV head (4 wavefronts x 32 keys,
@@ -161,7 +161,7 @@ struct DkdvStage {
 // need the key valid and not after them.
 template <int D, bool DSROLE, int MODE, bool STORE>
 __device__ __forceinline__ void dkdv_role(
-    DkdvStage<D>* st, u32x4* sP, const bf16* __restrict__ krot, const bf16* __restrict__ vn,
+    DkdvStage<D>* st, u32x4* sP, const bf16* __restrict__ krot, const bf16* __restrict__ v,
     const bf16* __restrict__ qrot, const bf16* __restrict__ dout,
     const float* __restrict__ lse2, const float* __restrict__ delta,
     const float* __restrict__ cos, const float* __restrict__ sin, bf16* __restrict__ dk,
@@ -208,12 +208,16 @@ __device__ __forceinline__ void dkdv_role(
   // DOC: the first tile was staged by the caller before the list was built
   if (!DOC && total > 0) stage(0, 0);
 
-  // this role's register-resident B operand: K for P waves, V for dS waves
+  // this role's register-resident B operand: K (rotated, workspace rows up to P)
+  // for P waves, V (read in place, [B, S, Hkv, D]; zero past S) for dS waves
   bf16x8 bf[KS];
   {
-    const bf16* src = (DSROLE ? vn : krot) + ((int64_t)bh * P + key) * D + 8 * hh;
+    const bool ok = !DSROLE || key < S;
+    const bf16* src = DSROLE ? v + (((int64_t)b * S + (ok ? key : 0)) * Hkv + g) * D + 8 * hh
+                             : krot + ((int64_t)bh * P + key) * D + 8 * hh;
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) bf[ks] = as_bf16x8(*(const u32x4*)(src + 16 * ks));
+    for (int ks = 0; ks < KS; ++ks)
+      bf[ks] = as_bf16x8(ok ? *(const u32x4*)(src + 16 * ks) : u32x4{0u, 0u, 0u, 0u});
   }
   f32x16 acc[DT];
 #pragma unroll
@@ -454,7 +458,7 @@ __device__ __forceinline__ void dkdv_stage_first(
 
 template <int D, int MODE, bool STORE>
 __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(
-    const bf16* __restrict__ krot, const bf16* __restrict__ vn, const bf16* __restrict__ qrot,
+    const bf16* __restrict__ krot, const bf16* __restrict__ v, const bf16* __restrict__ qrot,
     const bf16* __restrict__ dout, const float* __restrict__ lse2, const float* __restrict__ delta,
     const float* __restrict__ cos, const float* __restrict__ sin, bf16* __restrict__ dk,
     bf16* __restrict__ dv, int S, int P, int Hq, int Hkv, int n_rep, int nkb, int nitems,
@@ -517,12 +521,12 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(
       nlist = __builtin_amdgcn_readfirstlane(sCount);
     }
     if (w >= 4)
-      dkdv_role<D, true, MODE, STORE>(st, sP, krot, vn, qrot, dout, lse2, delta, cos, sin, dk,
+      dkdv_role<D, true, MODE, STORE>(st, sP, krot, v, qrot, dout, lse2, delta, cos, sin, dk,
                                       dv, S, P, Hq, Hkv, n_rep, b, g, bh, k0, w, lane,
                                       scale_log2, scale, causal, drow, sList, nlist, sQD, fv,
                                       dsb, P / DSQ);
     else
-      dkdv_role<D, false, MODE, STORE>(st, sP, krot, vn, qrot, dout, lse2, delta, cos, sin, dk,
+      dkdv_role<D, false, MODE, STORE>(st, sP, krot, v, qrot, dout, lse2, delta, cos, sin, dk,
                                        dv, S, P, Hq, Hkv, n_rep, b, g, bh, k0, w, lane,
                                        scale_log2, scale, causal, drow, sList, nlist, sQD, fv,
                                        dsb, P / DSQ);
@@ -538,7 +542,7 @@ constexpr int DQ_ROWS = 256;
 template <int D, int MODE>
 __global__ __launch_bounds__(512, 1) void bwd_dq_kernel(
     const bf16* __restrict__ qrot, const bf16* __restrict__ dout, const float* __restrict__ lse2,
-    const float* __restrict__ delta, const bf16* __restrict__ krot, const bf16* __restrict__ vn,
+    const float* __restrict__ delta, const bf16* __restrict__ krot, const bf16* __restrict__ v,
     const float* __restrict__ cos, const float* __restrict__ sin, bf16* __restrict__ dq, int S,
     int P, int Hq, int Hkv, int n_rep, int bm_pos, int nqb, int nitems, float scale_log2,
     float scale, int causal, const int32_t* __restrict__ aux, const int2* __restrict__ ranges) {
@@ -568,10 +572,13 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_kernel(
     const int32_t* drow = LIST ? aux + (int64_t)ri.b * S : nullptr;
     const int2* rec = ranges + (int64_t)ri.b * (P / BN);
     const bf16* kbase = krot + (int64_t)bh * P * D;
-    const bf16* vbase = vn + (int64_t)bh * P * D;
+    // V read in place ([B, S, Hkv, D]); rows past S repeat row S - 1 (their K
+    // rows are zero, so they add nothing to dQ)
+    const bf16* vbase = v + ((int64_t)ri.b * S * Hkv + ri.g) * D;
     auto stage = [&](int t, int buf) {
       tile_to_lds<BN, KR, 8>(kbase + (int64_t)t * BN * D, D, st[buf].k, w, lane);
-      tile_to_lds<BN, KR, 8>(vbase + (int64_t)t * BN * D, D, st[buf].v, w, lane);
+      tile_to_lds<BN, KR, 8>(vbase + (int64_t)t * BN * Hkv * D, Hkv * D, st[buf].v, w, lane,
+                             S - t * BN);
       if (LIST && w == 0) dma4(lds_addr(sKD[buf]), (uint32_t)min(t * BN + lane, S - 1) * 4u, drow);
     };
     int di = 0;        // DOC: this row's document
@@ -933,7 +940,7 @@ __global__ __launch_bounds__(64 * HB) void bwd_dq_ds_kernel(
 }
 
 struct Ws {
-  bf16 *krot, *vn, *qrot;
+  bf16 *krot, *qrot;
   float *lse2, *delta;
   int2* ranges;  // [B][P/64] document-id range per tile (packed documents only)
   u32x4* dsb;    // dS records (when kept)
@@ -941,7 +948,7 @@ struct Ws {
 
 size_t base_bytes(int B, int S, int Hq, int Hkv, int D) {
   const size_t P = (size_t)pad_len(S);
-  return (2 * (size_t)B * Hkv + (size_t)B * Hq) * P * D * sizeof(uint16_t) +
+  return ((size_t)B * Hkv + (size_t)B * Hq) * P * D * sizeof(uint16_t) +
          2 * (size_t)B * Hq * P * sizeof(float) + (size_t)B * (P / BN) * sizeof(int2);
 }
 size_t align256(size_t n) { return (n + 255) / 256 * 256; }
@@ -964,7 +971,6 @@ Ws carve(void* base, int B, int S, int Hq, int Hkv, int D) {
   Ws w;
   bf16* p = (bf16*)base;
   w.krot = p; p += kv;
-  w.vn = p; p += kv;
   w.qrot = p; p += qq;
   float* f = (float*)p;
   w.lse2 = f; f += (size_t)B * Hq * P;
@@ -1004,7 +1010,7 @@ int launch_bwd(const BwdArgs& a, void* workspace, bool keep_ds) {
   fa.ksh = fa.vsh = D;
   fa.k_rotated = 0; fa.dtype = BF16; fa.stream = a.stream;
   fa.doc = a.doc; fa.kvalid = a.kvalid; fa.causal = a.causal;
-  int rc = launch_kv_prep(fa, w.krot, w.vn, P, w.ranges);
+  int rc = launch_kv_prep(fa, w.krot, nullptr, P, w.ranges, KV_V_NONE);
   if (rc) return rc;
   KF_LAUNCH("q_prep_bwd", q_prep_bwd_kernel<D>, dim3(P / BN, a.B * a.Hq), dim3(256), 0, a.stream,
             (const bf16*)a.q, (const bf16*)a.out, (const bf16*)a.dout, a.lse, a.cos, a.sin,
@@ -1023,7 +1029,7 @@ int launch_bwd(const BwdArgs& a, void* workspace, bool keep_ds) {
              : mode == MASK_KPM ? bwd_dkdv_kernel<D, MASK_KPM, false>
              : keep_ds          ? bwd_dkdv_kernel<D, MASK_NONE, true>
                                 : bwd_dkdv_kernel<D, MASK_NONE, false>),
-            dim3(std::min(nkb * a.B * a.Hkv, grid_cap)), dim3(512), 0, a.stream, w.krot, w.vn,
+            dim3(std::min(nkb * a.B * a.Hkv, grid_cap)), dim3(512), 0, a.stream, w.krot, (const bf16*)a.v,
             w.qrot, (const bf16*)a.dout, w.lse2, w.delta, a.cos, a.sin, (bf16*)a.dk,
             (bf16*)a.dv, a.S, P, a.Hq, a.Hkv, n_rep, nkb, nkb * a.B * a.Hkv,
             scale_log2, a.scale, a.causal, aux, w.ranges, w.dsb);
@@ -1039,7 +1045,7 @@ int launch_bwd(const BwdArgs& a, void* workspace, bool keep_ds) {
              : mode == MASK_KPM ? bwd_dq_kernel<D, MASK_KPM>
                                 : bwd_dq_kernel<D, MASK_NONE>),
             dim3(std::min(nqb * a.B * a.Hkv, grid_cap)), dim3(512), 0, a.stream, w.qrot,
-            (const bf16*)a.dout, w.lse2, w.delta, w.krot, w.vn, a.cos, a.sin, (bf16*)a.dq, a.S, P,
+            (const bf16*)a.dout, w.lse2, w.delta, w.krot, (const bf16*)a.v, a.cos, a.sin, (bf16*)a.dq, a.S, P,
             a.Hq, a.Hkv, n_rep, bm_pos, nqb, nqb * a.B * a.Hkv, scale_log2, a.scale, a.causal,
             aux, w.ranges);
   KF_CHECK_LAUNCH();

@@ -40,9 +40,9 @@ __global__ __launch_bounds__(256) void kv_prep_kernel(
     const float* __restrict__ sin, bf16* __restrict__ krot, bf16* __restrict__ vn, int Sk,
     int Skp, int Hkv, int64_t ksb, int64_t kss, int64_t ksh, int64_t vsb, int64_t vss,
     int64_t vsh, int k_rotated, const int32_t* __restrict__ doc, const int32_t* __restrict__ kvalid,
-    int2* __restrict__ ranges, int v_transposed) {
+    int2* __restrict__ ranges, int v_mode) {
   constexpr int HALF = D / 2;
-  __shared__ __attribute__((aligned(16))) bf16 sVt[D * BN];  // v_transposed: [d][key slot]
+  __shared__ __attribute__((aligned(16))) bf16 sVt[D * BN];  // KV_V_TRANSPOSED: [d][key slot]
   constexpr int CP = HALF / 8;
   const int s0 = blockIdx.x * BN;
   const int bh = blockIdx.y;
@@ -92,7 +92,8 @@ __global__ __launch_bounds__(256) void kv_prep_kernel(
     *(u32x4*)(dst + 8 * c) = o1;
     *(u32x4*)(dst + 8 * c + HALF) = o2;
   }
-  if (!v_transposed) {
+  if (v_mode == KV_V_NONE) return;
+  if (v_mode == KV_V_ROWS) {
     for (int it = tid; it < BN * (D / 8); it += 256) {
       const int key = it / (D / 8), c = it % (D / 8);
       const int s = s0 + key;
@@ -539,7 +540,7 @@ size_t fwd_mfma_workspace(int B, int Sk, int Hkv, int D) {
 }
 
 int launch_kv_prep(const FwdArgs& a, void* krot_, void* vn_, int Skp, int2* ranges,
-                   int v_transposed) {
+                   int v_mode) {
   bf16* krot = (bf16*)krot_;
   bf16* vn = (bf16*)vn_;
   dim3 grid(Skp / BN, a.B * a.Hkv);
@@ -547,12 +548,12 @@ int launch_kv_prep(const FwdArgs& a, void* krot_, void* vn_, int Skp, int2* rang
     KF_LAUNCH("kv_prep", kv_prep_kernel<128>, grid, dim3(256), 0, a.stream, (const bf16*)a.k,
                        (const bf16*)a.v, a.cos, a.sin, krot, vn, a.Sk, Skp, a.Hkv, a.ksb, a.kss,
                        a.ksh, a.vsb, a.vss, a.vsh, a.k_rotated, a.doc, a.kvalid, ranges,
-                       v_transposed);
+                       v_mode);
   else
     KF_LAUNCH("kv_prep", kv_prep_kernel<64>, grid, dim3(256), 0, a.stream, (const bf16*)a.k,
                        (const bf16*)a.v, a.cos, a.sin, krot, vn, a.Sk, Skp, a.Hkv, a.ksb, a.kss,
                        a.ksh, a.vsb, a.vss, a.vsh, a.k_rotated, a.doc, a.kvalid, ranges,
-                       v_transposed);
+                       v_mode);
   KF_CHECK_LAUNCH();
   return KF_OK;
 }
@@ -621,7 +622,7 @@ void launch_capture_mode(const FwdArgs& a, const FwdWs& w, const float* lse, flo
 int fwd_mfma(const FwdArgs& a, void* workspace) {
   const int Skp = (a.Sk + BN - 1) / BN * BN;
   const FwdWs w = carve_fwd(a, workspace, Skp);
-  int rc = launch_kv_prep(a, w.krot, w.vn, Skp, w.ranges, 1);
+  int rc = launch_kv_prep(a, w.krot, w.vn, Skp, w.ranges, KV_V_TRANSPOSED);
   if (rc) return rc;
   const int n_rep = a.Hq / a.Hkv;
   const int bm_pos = pick_bm_pos(n_rep);

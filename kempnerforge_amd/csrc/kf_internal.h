@@ -56,15 +56,17 @@ int capture_probs_generic(const FwdArgs& a, const float* lse, float* probs);
 
 // bf16 MFMA kernels (kf_fwd.hip, kf_bwd.hip, kf_capture.hip)
 bool fwd_mfma_supported(const FwdArgs& a);
-// Rotated K and zero-padded V, both [B*Hkv][Skp][D] bf16 (Skp a multiple of 64);
-// v_transposed: V^T [B*Hkv][D][Skp] instead, keys of each 16 in the P^T fragment
-// order 0-3, 8-11, 4-7, 12-15 (what the forward kernel reads).  With a.doc also
-// the [min, max] document id of each 64-key tile, [B][Skp/64] (a.kvalid: valid
-// count and first valid key).
+// Rotated K [B*Hkv][Skp][D] bf16 (Skp a multiple of 64, rows past Sk zero) and,
+// by v_mode: KV_V_ROWS zero-padded V [B*Hkv][Skp][D]; KV_V_TRANSPOSED V^T
+// [B*Hkv][D][Skp], keys of each 16 in the P^T fragment order 0-3, 8-11, 4-7,
+// 12-15 (what the forward kernel reads); KV_V_NONE no V (vn unused).  With
+// a.doc also the [min, max] document id of each 64-key tile, [B][Skp/64]
+// (a.kvalid: valid count and first valid key).
+enum { KV_V_ROWS = 0, KV_V_TRANSPOSED = 1, KV_V_NONE = 2 };
 // Compute units of the current device (cached per device), to size persistent grids.
 int device_cu_count();
 int launch_kv_prep(const FwdArgs& a, void* krot, void* vn, int Skp, int2* ranges,
-                   int v_transposed = 0);
+                   int v_mode = KV_V_ROWS);
 size_t fwd_mfma_workspace(int B, int Sk, int Hkv, int D);
 int fwd_mfma(const FwdArgs& a, void* workspace);
 int capture_probs_mfma(const FwdArgs& a, const float* lse, float* probs, void* workspace);

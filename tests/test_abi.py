@@ -58,11 +58,14 @@ def test_host_only_calls():
     assert b"multiple" in lib.kf_last_error()
     assert lib.kf_attn_fwd_workspace_size(1, 8, 8, 4, 4, 63, 1, ctypes.byref(n)) == 1
     assert lib.kf_attn_decode_workspace_size(32, 32, 8, 128, 8193, 1, ctypes.byref(n)) == 0
-    assert n.value == 32 * 32 * 9 * 130 * 4  # ceil(8193 / 1024) splits of (o[D], m, l)
-    # backward: rotated K, V (per KV head) and Q (per query head) bf16 [P][D], then
-    # lse and Delta float32 [P] per query head, then the int2 tile records
+    # (o[D], m, l) per query head of a KV group for each partial slot: one per
+    # wavefront of the stream kernel (at most 2048) plus one per (sequence, KV head)
+    assert n.value == (2048 + 32 * 8) * 4 * (128 + 2) * 4
+    # backward: rotated K (per KV head) and Q (per query head) bf16 [P][D], then
+    # lse and Delta float32 [P] per query head, then the int2 tile records (V and
+    # dO are read in place)
     B, S, Hq, Hkv, D, P = 4, 4096, 32, 8, 128, 4096
-    base = (2 * B * Hkv + B * Hq) * P * D * 2 + 2 * B * Hq * P * 4 + B * (P // 64) * 8
+    base = (B * Hkv + B * Hq) * P * D * 2 + 2 * B * Hq * P * 4 + B * (P // 64) * 8
     assert lib.kf_attn_bwd_workspace_size(B, S, Hq, Hkv, D, 1, ctypes.byref(n)) == 0
     assert n.value == base
     # kept dS tiles: bf16 over the causal 64-row x 32-key blocks, P * (P + 64) bytes per
