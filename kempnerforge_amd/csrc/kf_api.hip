@@ -316,9 +316,7 @@ int kf_attn_capture(const void* q, const void* k, const void* v, const float* ro
       set_error("workspace too small: need %zu bytes, got %zu", need, workspace_bytes);
       return KF_ERR_WORKSPACE;
     }
-    rc = fwd_mfma(a, workspace);
-    if (rc) return rc;
-    return capture_probs_mfma(a, lse, probs, workspace);
+    return capture_probs_mfma(a, probs, workspace);
   }
   rc = fwd_generic(a);
   if (rc) return rc;

@@ -374,143 +374,284 @@ __global__ __launch_bounds__(256, 2) void fwd_mfma_kernel(
   }
 }
 
-// Capture probabilities P = exp(s - lse) as float32 [B, Hq, Sq, Sk].
-// S = Q·K^T with Q the A operand (this lane's rotated Q fragment doubles as the
-// A operand: row = l%32, k = 8h + j) and K^T the B operand read from LDS, so a
-// C register i holds (query row 8*(i/4)+4h+(i%4), key l%32): for a fixed i the
-// 32 lanes of one half write 32 consecutive floats of one row.  Key tiles fully
-// above the diagonal are written as zeros without computing.  MASK_DOC: keys
-// of another document get probability 0 (each lane tests its one key per
-// 32-key half against the document of each of its 16 rows).  MASK_KPM: padded
-// keys get 0, except in guarded rows (before the first valid key), which
-// attend every key; a workgroup holding one computes every tile.
+// Capture: LSE, the probabilities P = exp(s - lse) as float32 [B, Hq, Sq, Sk]
+// and out = P·V in one launch per (query block, KV head).  The workgroup walks
+// its key tiles twice in the forward's S^T = K·Q^T layout (a lane holds one
+// query row's 32 scores of a 64-key tile): the first walk forms each row's
+// running max and sum only (no P·V); the second forms the normalised P,
+// stores it, and accumulates O^T = V^T·P^T from P rounded to bf16, so O needs
+// no final division.  P leaves through an LDS slice per wavefront (see
+// store_p) as whole 128-byte line segments.  The stores of tile t issue at the
+// start of tile t+1, before its tile loads: the end-of-tile wait (vmcnt counts
+// loads and stores together) then finds stores a whole tile old.  Key tiles
+// right of the causal frontier are zero without computing; their rows are
+// spread over the tile iterations.  Stores are non-temporal: nothing reads P
+// back, and cached it would evict the K and V tiles the other workgroups of
+// the KV head re-read.  Query blocks are taken long and short alternately
+// (qb = nqb-1, 0, nqb-2, 1, ...), so a CU's two resident workgroups tend to
+// pair a compute-heavy block with a write-heavy one.  Explicit masks as in the
+// forward (MASK_DOC: other documents get P = 0; MASK_KPM: padded keys get 0,
+// except in guarded rows before the first valid key, which attend every key
+// below Sk, so a workgroup holding one walks every tile); with an explicit
+// mask every tile takes the element test.
 template <int D, int MODE>
 __global__ __launch_bounds__(256, 2) void capture_probs_mfma_kernel(
     const bf16* __restrict__ q, const float* __restrict__ cos, const float* __restrict__ sin,
-    const bf16* __restrict__ krot, const float* __restrict__ lse, float* __restrict__ probs,
-    int Sq, int Sk, int Skp, int Hq, int Hkv, int n_rep, int bm_pos, int nqb, float scale_log2,
-    int causal, const int32_t* __restrict__ aux, const int2* __restrict__ ranges) {
-  constexpr bool DOC = MODE == MASK_DOC, KPM = MODE == MASK_KPM;
-  constexpr int KS = D / 16;
+    const bf16* __restrict__ krot, const bf16* __restrict__ vn, bf16* __restrict__ out,
+    float* __restrict__ lse, float* __restrict__ probs, int Sq, int Sk, int Skp, int Hq, int Hkv,
+    int n_rep, int bm_pos, int nqb, float scale_log2, int causal,
+    const int32_t* __restrict__ aux, const int2* __restrict__ ranges) {
+  constexpr bool DOC = MODE == MASK_DOC, KPM = MODE == MASK_KPM, LIST = DOC || KPM;
+  constexpr int KS = D / 16, DT = D / 32;
   constexpr int KR = D / 8;
   __shared__ __attribute__((aligned(16))) bf16 sK[2][BN * D];
-  __shared__ float sL[ROWS];
-  __shared__ int sRowOff[ROWS];  // row offset of (hq, pos) in units of Sk floats, or -1
+  __shared__ __attribute__((aligned(16))) bf16 sV[2][BN * D];
+  __shared__ __attribute__((aligned(16))) int32_t sKD[2][BN];  // LIST: per-key aux values
+  __shared__ __attribute__((aligned(16))) float sP[4][32 * 32];  // per wave: 32 rows x 32 keys
 
   const int tid = threadIdx.x, w = wave_id(), lane = tid & 63, hh = lane >> 5, c32 = lane & 31;
   const int logical = xcd_logical_id(blockIdx.x, gridDim.x);
-  const RowInfo ri = row_info(logical, nqb, Hkv, n_rep, bm_pos, Sq, w * 32 + c32);
+  // row_info maps logical index bh*nqb + j to query block nqb-1-j; alternate
+  const int zz = logical % nqb, zq = (zz & 1) ? nqb - 1 - (zz >> 1) : (zz >> 1);
+  const RowInfo ri = row_info(logical - zz + zq, nqb, Hkv, n_rep, bm_pos, Sq, w * 32 + c32);
   const int bh = ri.b * Hkv + ri.g;
+  const int32_t* arow = LIST ? aux + (int64_t)ri.b * Sk : nullptr;
+  const int nrows = n_rep * bm_pos;  // rows of the block in use
 
-  if (hh == 0) {
-    const int r = w * 32 + c32;
-    const int64_t ro = ((int64_t)ri.b * Hq + ri.hq) * Sq + ri.pos;
-    sL[r] = ri.q_valid ? lse[ro] * kLog2e : 0.f;
-    sRowOff[r] = ri.q_valid ? (int)(ri.hq - (int64_t)ri.g * n_rep) * Sq + (ri.pos - ri.p0) : -1;
-  }
-  bf16x8 qf[KS];
-  load_q_frag<D>(q, cos, sin, ri, Sq, Hq, hh, qf);
-  __syncthreads();
-
-  // per-lane rows of the C layout (register i -> row 8*(i/4)+4h+(i%4) of the
-  // wave): log2-domain LSE, positions and (DOC/KPM) document or guard flag,
-  // hoisted out of the tile loop.  After the probabilities of both 32-key
-  // halves of a tile are formed, v_permlane32_swap exchanges the upper half of
-  // register i of the first with the lower half of the second, so each register
-  // then holds 64 consecutive keys of one row (row 8*(i/4)+(i%4) in the first,
-  // +4 in the second): one store writes 256 contiguous bytes.  Those rows are
-  // wavefront-uniform, so their P offsets live in scalar registers.
   const int qmax = min(ri.p0 + bm_pos, Sq) - 1;  // largest position in the block
   const int ntiles_all = (Sk + BN - 1) / BN;
   // KPM: first valid key of the batch row; rows before it are guarded
   const int fv = KPM ? kpm_first_valid(ranges + (int64_t)ri.b * (Skp / BN), Skp / BN, lane) : 0;
   const int ntiles = causal && !(KPM && ri.p0 < fv) ? min(ntiles_all, (qmax + BN) / BN)
                                                       : ntiles_all;
+  const int di = DOC ? arow[min(ri.pos, Sq - 1)] : 0;  // DOC: this row's document
+  const bool grd = KPM && ri.pos < fv;                  // KPM: guarded row
   const bf16* kbase = krot + (int64_t)bh * Skp * D;
-  float* pbase = probs + (((int64_t)ri.b * Hq + (int64_t)ri.g * n_rep) * Sq + ri.p0) * Sk;
-  float lrow[16];
-  int posr[16];
-  int drw[16];  // DOC: document of each row; KPM: 1 for a guarded row
-  int roff[16][2];  // P row offset (Sk floats) of the stored rows, -1: no row
-  const int32_t* drow = DOC || KPM ? aux + (int64_t)ri.b * Sk : nullptr;
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const int r = w * 32 + 8 * (i >> 2) + 4 * hh + (i & 3);
-    lrow[i] = sL[r];
-    posr[i] = ri.p0 + (r % bm_pos);
-    drw[i] = DOC ? drow[min(posr[i], Sq - 1)] : KPM ? (int)(posr[i] < fv) : 0;
-#pragma unroll
-    for (int h2 = 0; h2 < 2; ++h2)
-      roff[i][h2] = __builtin_amdgcn_readfirstlane(sRowOff[w * 32 + 8 * (i >> 2) + 4 * h2 + (i & 3)]);
-  }
+  const bf16* vbase = vn + (int64_t)bh * D * Skp;  // V^T, keys in fragment order
+  auto stage_k = [&](int t, int buf) {
+    tile_to_lds<BN, KR>(kbase + (int64_t)t * BN * D, D, sK[buf], w, lane);
+    if (LIST && w == 0) dma4(lds_addr(sKD[buf]), (uint32_t)min(t * BN + lane, Sk - 1) * 4u, arow);
+  };
+  auto stage_v = [&](int t, int buf) {
+    tile_to_lds<D, BN / 8>(vbase + (int64_t)t * BN, Skp, sV[buf], w, lane);
+  };
+  if (ntiles > 0) stage_k(0, 0);
 
-  // K tiles double-buffered: tile t+1 loads while tile t is computed and stored
-  if (ntiles > 0) tile_to_lds<BN, KR>(kbase, D, sK[0], w, lane);
-  // unrolled by two: each copy's LDS buffer is a compile-time constant
-  auto tile_body = [&](int t, auto bufc) {
-    constexpr int buf = decltype(bufc)::value;
-    lds_copy_wait();
-    __syncthreads();
-    if (t + 1 < ntiles) tile_to_lds<BN, KR>(kbase + (int64_t)(t + 1) * BN * D, D, sK[buf ^ 1], w, lane);
-    const bf16* tK = sK[buf];
-    const bool diag = (causal && t * BN + BN - 1 > ri.p0) || t * BN + BN > Sk;
-    f32x16 pv[2];
+  bf16x8 qf[KS];
+  load_q_frag<D>(q, cos, sin, ri, Sq, Hq, hh, qf);
+
+  // S^T of tile t with masked scores set to -inf
+  auto scores = [&](int t, const bf16* tK, const int32_t* kdl, f32x16 (&s)[2]) {
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-      f32x16 sv;
+    for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) sv[i] = 0.f;
+      for (int i = 0; i < 16; ++i) s[mt][i] = 0.f;
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        const bf16x8 bk = lds_frag<KR>(tK, 32 * nt + c32, 2 * ks + hh);
-        sv = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qf[ks], bk, sv, 0, 0, 0);
-      }
-      const int key = t * BN + 32 * nt + c32;
-      const int kd = DOC || KPM ? drow[min(key, Sk - 1)] : 0;
+    for (int ks = 0; ks < KS; ++ks) {
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        float p = fast_exp2(sv[i] * scale_log2 - lrow[i]);
-        const bool guarded = KPM && drw[i];
-        if (diag && causal && key > posr[i] && !guarded) p = 0.f;
-        if (DOC && kd != drw[i]) p = 0.f;
-        if (KPM && !guarded && kd == 0) p = 0.f;
-        pv[nt][i] = p;
+      for (int mt = 0; mt < 2; ++mt) {
+        const bf16x8 a = lds_frag<KR>(tK, 32 * mt + c32, 2 * ks + hh);
+        s[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[ks], s[mt], 0, 0, 0);
       }
     }
-    const int key = t * BN + lane;  // this lane's key after the swap
+    const int k0 = t * BN;
+    if constexpr (LIST) {
+      // explicit masks come with causal self-attention
+      const int lim = (grd ? Sk - 1 : min(ri.pos, Sk - 1)) - k0;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(pv[0][i]),
-                                                       __float_as_uint(pv[1][i]), false, false);
+      for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-      for (int h2 = 0; h2 < 2; ++h2) {
-        if (roff[i][h2] < 0) continue;
-        if (diag && key >= Sk) continue;
-        pbase[(int64_t)roff[i][h2] * Sk + key] = __uint_as_float(sw[h2]);
-      }
+        for (int g4 = 0; g4 < 4; ++g4) {
+          const i32x4 kd = *(const i32x4*)&kdl[32 * mt + 8 * g4 + 4 * hh];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int local = 32 * mt + 8 * g4 + 4 * hh + j;
+            const bool other = DOC ? kd[j] != di : (!grd && kd[j] == 0);
+            s[mt][4 * g4 + j] = (local > lim || other) ? -INFINITY : s[mt][4 * g4 + j];
+          }
+        }
+    } else if ((causal && k0 + BN - 1 > ri.p0) || k0 + BN > Sk) {
+      const int lim = (causal ? min(ri.pos, Sk - 1) : Sk - 1) - k0;
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int local = 32 * mt + 8 * (i >> 2) + 4 * hh + (i & 3);
+          s[mt][i] = local > lim ? -INFINITY : s[mt][i];
+        }
     }
   };
-  for (int t = 0; t < ntiles; t += 2) {
-    tile_body(t, std::integral_constant<int, 0>{});
-    if (t + 1 < ntiles) tile_body(t + 1, std::integral_constant<int, 1>{});
-  }
-  // zero the tiles right of the causal frontier
-  if (causal) {
-    const int zstart = ntiles * BN;
-    if (zstart < Sk) {
-      for (int r = 0; r < ROWS; ++r) {
-        const int off = sRowOff[r];
-        if (off < 0) continue;
-        float* prow = pbase + (int64_t)off * Sk;
-        for (int key = zstart + tid * 4; key < Sk; key += 256 * 4) {
-          if (key + 3 < Sk && (Sk & 3) == 0) {
-            *(f32x4*)(prow + key) = f32x4{0.f, 0.f, 0.f, 0.f};
-          } else {
-            for (int e = key; e < min(key + 4, Sk); ++e) prow[e] = 0.f;
-          }
+
+  // Key tiles right of the causal frontier are zero.  Their rows are written
+  // in 2*ntiles pieces, one at the start of each tile iteration of the two
+  // walks (ahead of that iteration's tile loads), so the zeros stream out
+  // while the block computes instead of after it.
+  const bool vec4 = (Sk & 3) == 0;  // 16-byte aligned rows
+  const int zstart = ntiles * BN;
+  const int zper = causal && zstart < Sk ? (nrows + 2 * ntiles - 1) / (2 * ntiles) : 0;
+  auto zero_rows = [&](int z) {
+    const int r1 = min(z * zper + zper, nrows);
+    for (int r = z * zper; r < r1; ++r) {
+      const int pos = ri.p0 + r % bm_pos;
+      if (pos >= Sq) continue;
+      float* zrow = probs + (((int64_t)ri.b * Hq + (int64_t)ri.g * n_rep + r / bm_pos) * Sq + pos) * Sk;
+      for (int key = zstart + tid * 4; key < Sk; key += 256 * 4) {
+        if (vec4) {
+          __builtin_nontemporal_store(f32x4{0.f, 0.f, 0.f, 0.f}, (f32x4*)(zrow + key));
+        } else {
+          for (int e = key; e < min(key + 4, Sk); ++e) zrow[e] = 0.f;
         }
       }
     }
+  };
+
+  lds_copy_wait();
+  __syncthreads();
+  // Walk 1: running max m and sum (log2 domain).  Starting m at -1e30 keeps
+  // exp2(m - mnew) finite for a row that sees no key in a tile.  Its last
+  // iteration stages tile 0 of walk 2 (K and V).  Both walks are unrolled by
+  // two so that each copy's LDS buffer is a compile-time constant.
+  float m = -1e30f, lsum = 0.f;
+  auto body1 = [&](int it, auto bufc) {
+    constexpr int buf = decltype(bufc)::value;
+    zero_rows(it);
+    if (it + 1 < ntiles) {
+      stage_k(it + 1, buf ^ 1);
+    } else {
+      stage_k(0, buf ^ 1);
+      stage_v(0, buf ^ 1);
+    }
+    f32x16 s[2];
+    scores(it, sK[buf], sKD[buf], s);
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) tmax = fmaxf(tmax, s[mt][i]);
+    const float mnew = fmaxf(m, pair_max32(tmax) * scale_log2);
+    float psum = 0.f;
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) psum += fast_exp2(__builtin_fmaf(s[mt][i], scale_log2, -mnew));
+    lsum = lsum * fast_exp2(m - mnew) + psum;
+    m = mnew;
+    lds_copy_wait();
+    __syncthreads();
+  };
+  for (int it = 0; it < ntiles; it += 2) {
+    body1(it, std::integral_constant<int, 0>{});
+    if (it + 1 < ntiles) body1(it + 1, std::integral_constant<int, 1>{});
+  }
+  const float L = m + log2f(pair_sum32(lsum));  // log2-domain LSE of this row
+  if (ri.q_valid && hh == 0) lse[((int64_t)ri.b * Hq + ri.hq) * Sq + ri.pos] = L * kLn2;
+
+  // Walk 2: P, its stores, and O^T += V^T P^T
+  f32x16 acc[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[dt][i] = 0.f;
+  // P leaves through the wave's LDS slice, 32 rows x 32 keys at a time: the C
+  // layout is written as 16-byte chunks (chunk c of row r at c ^ (r & 7), so
+  // neither the writes nor the reads conflict) and read back so that 8 lanes
+  // cover a row's 128 bytes: every store instruction writes 8 whole 128-byte
+  // line segments.  Lane l stores rows 8j + l/8 (j = 0..3) of the wave.
+  float* prs[4];
+  int pvalid = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int r = w * 32 + 8 * j + (lane >> 3);
+    const int pos = ri.p0 + r % bm_pos;
+    const bool ok = r < nrows && pos < Sq;
+    pvalid |= (int)ok << j;
+    prs[j] = probs + (((int64_t)ri.b * Hq + (int64_t)ri.g * n_rep + (ok ? r / bm_pos : 0)) * Sq +
+                      (ok ? pos : 0)) * Sk;
+  }
+  float* stg = sP[w];
+  f32x16 held[2];  // P of the previous tile, stored by the next
+  auto store_p = [&](int t) {
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4)
+        *(f32x4*)&stg[c32 * 32 + (((2 * g4 + hh) ^ (c32 & 7)) * 4)] =
+            f32x4{held[mt][4 * g4], held[mt][4 * g4 + 1], held[mt][4 * g4 + 2],
+                  held[mt][4 * g4 + 3]};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int rr = 8 * j + (lane >> 3), cl = lane & 7;
+        const f32x4 v4 = *(const f32x4*)&stg[rr * 32 + ((cl ^ (rr & 7)) * 4)];
+        const int key = t * BN + 32 * mt + 4 * cl;
+        if (!((pvalid >> j) & 1)) continue;
+        if (vec4) {
+          if (key < Sk) __builtin_nontemporal_store(v4, (f32x4*)(prs[j] + key));
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (key + e < Sk) prs[j][key + e] = v4[e];
+        }
+      }
+    }
+  };
+  auto body2 = [&](int it, auto bufc) {
+    constexpr int buf = decltype(bufc)::value;
+    if (it > 0) store_p(it - 1);
+    zero_rows(ntiles + it);
+    if (it + 1 < ntiles) {
+      stage_k(it + 1, buf ^ 1);
+      stage_v(it + 1, buf ^ 1);
+    }
+    f32x16 s[2];
+    scores(it, sK[buf], sKD[buf], s);
+    u32x4 pk[4];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int i = 0; i < 16; i += 2) {
+        const float p0 = fast_exp2(__builtin_fmaf(s[mt][i], scale_log2, -L));
+        const float p1 = fast_exp2(__builtin_fmaf(s[mt][i + 1], scale_log2, -L));
+        held[mt][i] = p0;
+        held[mt][i + 1] = p1;
+        pk[2 * mt + (i >> 3)][(i & 7) >> 1] = pack2(p0, p1);
+      }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const bf16x8 pb = as_bf16x8(pk[c]);
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        const bf16x8 a = lds_frag<BN / 8>(sV[buf], 32 * dt + c32, 2 * c + hh);
+        acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb, acc[dt], 0, 0, 0);
+      }
+    }
+    lds_copy_wait();
+    __syncthreads();
+  };
+  // walk 2 starts in the buffer walk 1's last iteration filled: buffer 1 when
+  // ntiles is odd (that first tile is peeled), else 0
+  int it2 = 0;
+  if (ntiles & 1) {
+    body2(0, std::integral_constant<int, 1>{});
+    it2 = 1;
+  }
+  for (; it2 < ntiles; it2 += 2) {
+    body2(it2, std::integral_constant<int, 0>{});
+    if (it2 + 1 < ntiles) body2(it2 + 1, std::integral_constant<int, 1>{});
+  }
+  if (ntiles > 0) store_p(ntiles - 1);
+
+  if (ri.q_valid) {
+    bf16* orow = out + (((int64_t)ri.b * Sq + ri.pos) * Hq + ri.hq) * D;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int gi = 0; gi < 4; ++gi) {
+        const int d = 32 * dt + 8 * gi + 4 * hh;
+        u32x2 pk2;
+        pk2[0] = pack2(acc[dt][4 * gi], acc[dt][4 * gi + 1]);
+        pk2[1] = pack2(acc[dt][4 * gi + 2], acc[dt][4 * gi + 3]);
+        *(u32x2*)(orow + d) = pk2;
+      }
   }
 }
 
@@ -595,25 +736,25 @@ void launch_fwd_mode(const FwdArgs& a, const FwdWs& w, int Skp, int n_rep, int b
 }
 
 template <int D, int MODE>
-void launch_capture_kernel(const FwdArgs& a, const FwdWs& w, const float* lse, float* probs,
-                           int Skp, int n_rep, int bm_pos, int nqb, unsigned nblk) {
+void launch_capture_kernel(const FwdArgs& a, const FwdWs& w, float* probs, int Skp, int n_rep,
+                           int bm_pos, int nqb, unsigned nblk) {
   KF_LAUNCH("capture_probs_mfma", (capture_probs_mfma_kernel<D, MODE>), dim3(nblk), dim3(256), 0,
-            a.stream, (const bf16*)a.q, a.cos, a.sin, w.krot, lse, probs, a.Sq, a.Sk, Skp, a.Hq,
-            a.Hkv, n_rep, bm_pos, nqb, a.scale * kLog2e, a.causal, a.doc ? a.doc : a.kvalid,
-            w.ranges);
+            a.stream, (const bf16*)a.q, a.cos, a.sin, w.krot, w.vn, (bf16*)a.out, a.lse, probs,
+            a.Sq, a.Sk, Skp, a.Hq, a.Hkv, n_rep, bm_pos, nqb, a.scale * kLog2e, a.causal,
+            a.doc ? a.doc : a.kvalid, w.ranges);
 }
 
 template <int D>
-void launch_capture_mode(const FwdArgs& a, const FwdWs& w, const float* lse, float* probs,
-                         int Skp, int n_rep, int bm_pos, int nqb, unsigned nblk) {
+void launch_capture_mode(const FwdArgs& a, const FwdWs& w, float* probs, int Skp, int n_rep,
+                         int bm_pos, int nqb, unsigned nblk) {
   switch (mask_mode(a)) {
     case MASK_DOC:
-      launch_capture_kernel<D, MASK_DOC>(a, w, lse, probs, Skp, n_rep, bm_pos, nqb, nblk);
+      launch_capture_kernel<D, MASK_DOC>(a, w, probs, Skp, n_rep, bm_pos, nqb, nblk);
       break;
     case MASK_KPM:
-      launch_capture_kernel<D, MASK_KPM>(a, w, lse, probs, Skp, n_rep, bm_pos, nqb, nblk);
+      launch_capture_kernel<D, MASK_KPM>(a, w, probs, Skp, n_rep, bm_pos, nqb, nblk);
       break;
-    default: launch_capture_kernel<D, MASK_NONE>(a, w, lse, probs, Skp, n_rep, bm_pos, nqb, nblk);
+    default: launch_capture_kernel<D, MASK_NONE>(a, w, probs, Skp, n_rep, bm_pos, nqb, nblk);
   }
 }
 
@@ -635,16 +776,18 @@ int fwd_mfma(const FwdArgs& a, void* workspace) {
   return KF_OK;
 }
 
-// Requires fwd_mfma to have run with the same workspace (krot is reused).
-int capture_probs_mfma(const FwdArgs& a, const float* lse, float* probs, void* workspace) {
+int capture_probs_mfma(const FwdArgs& a, float* probs, void* workspace) {
   const int Skp = (a.Sk + BN - 1) / BN * BN;
   const FwdWs w = carve_fwd(a, workspace, Skp);
+  int rc = launch_kv_prep(a, w.krot, w.vn, Skp, w.ranges, KV_V_TRANSPOSED);
+  if (rc) return rc;
   const int n_rep = a.Hq / a.Hkv;
   const int bm_pos = pick_bm_pos(n_rep);
   const int nqb = (a.Sq + bm_pos - 1) / bm_pos;
-  const unsigned nblk = (unsigned)((int64_t)nqb * a.B * a.Hkv);
-  if (a.D == 128) launch_capture_mode<128>(a, w, lse, probs, Skp, n_rep, bm_pos, nqb, nblk);
-  else launch_capture_mode<64>(a, w, lse, probs, Skp, n_rep, bm_pos, nqb, nblk);
+  const int64_t nblk = (int64_t)nqb * a.B * a.Hkv;
+  KF_CHECK_ARG(nblk < (1LL << 31), "grid too large");
+  if (a.D == 128) launch_capture_mode<128>(a, w, probs, Skp, n_rep, bm_pos, nqb, (unsigned)nblk);
+  else launch_capture_mode<64>(a, w, probs, Skp, n_rep, bm_pos, nqb, (unsigned)nblk);
   KF_CHECK_LAUNCH();
   return KF_OK;
 }

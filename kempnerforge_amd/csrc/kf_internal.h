@@ -69,7 +69,9 @@ int launch_kv_prep(const FwdArgs& a, void* krot, void* vn, int Skp, int2* ranges
                    int v_mode = KV_V_ROWS);
 size_t fwd_mfma_workspace(int B, int Sk, int Hkv, int D);
 int fwd_mfma(const FwdArgs& a, void* workspace);
-int capture_probs_mfma(const FwdArgs& a, const float* lse, float* probs, void* workspace);
+// LSE (a.lse), probabilities and out (a.out) of the capture path in one launch
+// after kv_prep; the workspace is fwd_mfma's.
+int capture_probs_mfma(const FwdArgs& a, float* probs, void* workspace);
 
 // dS record tile of the backward (dK/dV kernels write, dQ reads): DS_REC_Q
 // query positions x DS_REC_K keys of one query head, 4 KB of bf16.
