@@ -43,6 +43,7 @@ if ROOT not in sys.path:
 METRIC = "causal GQA attn TFLOP/s fwd+bwd (8B shape) + decode HBM GB/s, 1 MI355X"
 PEAK_BF16_TFLOPS = 2516.6  # 256 CU x 2.4 GHz x 4096 flop/clk, dense
 PEAK_HBM_GBPS = 8000.0
+SHORT_WARM, SHORT_STEPS = 50, 200  # minimum warm-up / timed calls of the sub-ms lines
 
 C3 = dict(B=4, S=4096, Hq=32, Hkv=8, D=128, theta=500000.0)
 C4 = dict(B=32, Hq=32, Hkv=8, D=128, lo=1024, hi=8192, theta=500000.0)
@@ -51,7 +52,7 @@ C5 = dict(B=1, S=16384, Hq=64, Hkv=8, D=128, theta=500000.0, cap_tokens=2048)
 # what bounds each kernel (the roofline its "achieved" figure is quoted on)
 BOUND = {"fwd_mfma": "mfma", "bwd_dkdv": "mfma", "bwd_dq": "mfma", "bwd_dq_ds": "hbm",
          "q_prep_bwd": "hbm", "kv_prep": "hbm", "decode_stream": "hbm", "decode_merge": "hbm",
-         "capture_probs": "hbm", "capture_lse": "mfma"}
+         "capture_probs": "hbm"}
 
 
 def pairs(B, Hq, S):
@@ -370,7 +371,10 @@ def run_full(args, torch, wl):
           "frac_of_peak": round(14.0 * D * P5 / c5_s / 1e12 / PEAK_BF16_TFLOPS, 4),
           "kernels_us": {n: round(s["avg_us"], 1) for n, s in k5.items()},
           "roofline": roofline(k5, algo5, traffic, "C5")}
-    cap_s = timed(torch, wl.c5cap_step, 2, args.steps)
+    # The capture and decode lines time at least SHORT_STEPS calls after
+    # SHORT_WARM untimed ones: a capture call is ~0.3 ms, and its first few
+    # dozen calls on a fresh buffer run ~13% slower than the steady state.
+    cap_s = timed(torch, wl.c5cap_step, max(args.warmup, SHORT_WARM), max(args.steps, SHORT_STEPS))
     kcap = kernel_stats(torch, wl.c5cap_step, args.steps)
     cap_b = capture_bytes()
     c5cap = {"config": "C5-cap first 2048 tokens of C5, P [1,64,2048,2048] fp32",
@@ -382,8 +386,8 @@ def run_full(args, torch, wl):
 
     # C4 decode
     dec_bytes = wl.c4_inputs()[-1]
-    n_dec = max(args.steps, 50)
-    dec_s = timed(torch, wl.c4_step, args.warmup, n_dec)
+    n_dec = max(args.steps, SHORT_STEPS)
+    dec_s = timed(torch, wl.c4_step, max(args.warmup, SHORT_WARM), n_dec)
     dstats = kernel_stats(torch, wl.c4_step, n_dec)
     stream_us = dstats.get("decode_stream", {}).get("avg_us")
     decode = {"config": "C4 B=32 Hq=32 Hkv=8 D=128 L~U[1024,8192] seed 4",
@@ -438,7 +442,7 @@ def run_full(args, torch, wl):
 def _short(name: str) -> str:
     """Kernel symbol -> the launcher's name (kf::..._kernel<...> -> ...)."""
     m = re.search(r"(kv_prep|fwd_mfma|q_prep_bwd|bwd_dkdv|bwd_dq_ds|bwd_dq|decode_stream|"
-                  r"decode_merge|capture_probs_mfma|capture_lse|kv_append|append)_kernel", name)
+                  r"decode_merge|capture_probs_mfma|kv_append|append)_kernel", name)
     if m:
         return {"capture_probs_mfma": "capture_probs", "append": "kv_append"}.get(m.group(1),
                                                                                  m.group(1))
