@@ -285,6 +285,8 @@ __global__ __launch_bounds__(256, 2) void decode_stream_kernel(
     float cs[2];     // cos / sin of the new position, dim lane (< HALF)
     uint32_t kv[2];  // k_new / v_new, dims 2 lane, 2 lane + 1 (lane < D / 2)
   };
+  // The cache is streamed once per step and at serving sizes does not fit the
+  // MALL: non-temporal loads (~15% more HBM read rate than cached ones).
   auto load_k = [&](const Cursor& cur) {
     const int last = cur.len;  // keys 0 .. len
     const int64_t base = ((int64_t)cur.b * Hkv + cur.g) * Smax * D;
@@ -294,7 +296,7 @@ __global__ __launch_bounds__(256, 2) void decode_stream_kernel(
       const int key = min(r0 + 16 * kb + c16, last);
 #pragma unroll
       for (int ks = 0; ks < KT; ++ks)
-        kreg[kb][ks] = *(const u32x4*)(kc + base + (int64_t)key * D + 32 * ks + 8 * q4);
+        kreg[kb][ks] = __builtin_nontemporal_load((const u32x4*)(kc + base + (int64_t)key * D + 32 * ks + 8 * q4));
     }
   };
   auto load_v = [&](const Cursor& cur) {
@@ -305,7 +307,7 @@ __global__ __launch_bounds__(256, 2) void decode_stream_kernel(
     for (int j = 0; j < VL; ++j) {
       const int li = 64 * j + lane, row = li / KR, pc = li % KR;
       const int key = min(r0 + row, last);
-      vreg[j] = *(const u32x4*)(vc + base + (int64_t)key * D + 8 * pc);
+      vreg[j] = __builtin_nontemporal_load((const u32x4*)(vc + base + (int64_t)key * D + 8 * pc));
     }
   };
   auto load_stash = [&](const Cursor& cur, Stash& st, bool pair_start, bool new_tok) {
