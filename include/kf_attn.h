@@ -118,6 +118,47 @@ int kf_attn_bwd(const void* q, const void* k, const void* v, const float* rope_c
                 int S, int Hq, int Hkv, int D, int causal, const int32_t* doc_ids,
                 const int32_t* key_valid, int dtype, void* stream);
 
+/* Rotated operands kept from the forward for the backward ("rot"): q and k
+ * after RoPE as the backward's kernels read them, K [B*Hkv][P][D] then Q
+ * [B*Hq][P][D] in bf16, P = S rounded up to 128, rows past S zero.  The pair
+ * below replaces kf_attn_fwd / kf_attn_bwd for self-attention (k_rotated = 0,
+ * contiguous BSHD k and v): the forward writes rot next to out and lse, and
+ * the backward reads it instead of q and k, skipping their rotation (one fewer
+ * pass over q and k).  A caller that keeps rot for the backward need not keep
+ * q and k, which is what the reference's autograd saves for SDPA's backward
+ * (kempnerforge/model/attention.py:165-166,231).  Results are bit-identical
+ * to kf_attn_fwd / kf_attn_bwd.  No counterpart in the reference's interface.
+ *
+ * kf_attn_rot_size: bytes of rot, or KF_ERR_UNSUPPORTED when the pair does
+ * not take these sizes, dtype (bf16 only) or mask kinds (has_doc,
+ * has_key_valid: whether doc_ids / key_valid will be passed). */
+int kf_attn_rot_size(int B, int S, int Hq, int Hkv, int D, int dtype, int has_doc,
+                     int has_key_valid, size_t* bytes);
+
+/* kf_attn_fwd (same arguments; Sq == Sk == S, contiguous BSHD k and v) that
+ * also fills rot.  Workspace: kf_attn_fwd_workspace_size.  KF_ERR_UNSUPPORTED
+ * when kf_attn_rot_size rejects the sizes or a pointer is not 16-byte aligned;
+ * then call kf_attn_fwd / kf_attn_bwd instead. */
+int kf_attn_fwd_rot(const void* q, const void* k, const void* v, const float* rope_cos,
+                    const float* rope_sin, void* out, float* lse, void* rot, void* workspace,
+                    size_t workspace_bytes, int B, int S, int Hq, int Hkv, int D, int causal,
+                    const int32_t* doc_ids, const int32_t* key_valid, int dtype, void* stream);
+
+/* Workspace bytes of kf_attn_bwd_rot: with_ds = 0 the minimum, 1 with the dS
+ * records kept (as kf_attn_bwd_workspace_size_ds: unmasked or doc_ids
+ * launches; equal to the minimum where records do not apply).  Smaller than
+ * kf_attn_bwd's by the size of rot. */
+int kf_attn_bwd_rot_workspace_size(int B, int S, int Hq, int Hkv, int D, int dtype, int causal,
+                                   int with_ds, size_t* bytes);
+
+/* kf_attn_bwd reading the rotated q and k from rot (kf_attn_fwd_rot of the
+ * same q, k, cos, sin and masks) instead of q and k. */
+int kf_attn_bwd_rot(const void* rot, const void* v, const float* rope_cos, const float* rope_sin,
+                    const void* out, const float* lse, const void* dout, void* dq, void* dk,
+                    void* dv, void* workspace, size_t workspace_bytes, int B, int S, int Hq,
+                    int Hkv, int D, int causal, const int32_t* doc_ids, const int32_t* key_valid,
+                    int dtype, void* stream);
+
 /* Workspace bytes kf_attn_decode needs; max_len bounds lens[b] + 1. */
 int kf_attn_decode_workspace_size(int B, int Hq, int Hkv, int D, int max_len, int dtype,
                                   size_t* bytes);

@@ -32,6 +32,12 @@ SIGNATURES = {
     "kf_attn_bwd_workspace_size_ds": ([_c_int] * 7 + [_szp], _c_int),
     "kf_attn_bwd": ([_vp, _vp, _vp, _fp, _fp, _vp, _fp, _vp, _vp, _vp, _vp, _vp, _c_sz]
                     + [_c_int] * 6 + [_vp, _vp, _c_int, _vp], _c_int),
+    "kf_attn_rot_size": ([_c_int] * 8 + [_szp], _c_int),
+    "kf_attn_fwd_rot": ([_vp, _vp, _vp, _fp, _fp, _vp, _fp, _vp, _vp, _c_sz] + [_c_int] * 6
+                        + [_vp, _vp, _c_int, _vp], _c_int),
+    "kf_attn_bwd_rot_workspace_size": ([_c_int] * 8 + [_szp], _c_int),
+    "kf_attn_bwd_rot": ([_vp, _vp, _fp, _fp, _vp, _fp, _vp, _vp, _vp, _vp, _vp, _c_sz]
+                        + [_c_int] * 6 + [_vp, _vp, _c_int, _vp], _c_int),
     "kf_attn_decode_workspace_size": ([_c_int] * 6 + [_szp], _c_int),
     "kf_attn_decode": ([_vp, _vp, _vp, _vp, _vp, _vp, _fp, _fp, _c_i64, _c_i64, _vp, _vp, _c_sz]
                        + [_c_int] * 6 + [_fp, _fp, ctypes.c_float, _c_int, _vp], _c_int),

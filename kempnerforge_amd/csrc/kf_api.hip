@@ -191,6 +191,110 @@ int kf_attn_bwd(const void* q, const void* k, const void* v, const float* rope_c
   return bwd_generic(a, workspace);
 }
 
+// Whether the rotated-operand pair (kf_attn_fwd_rot / kf_attn_bwd_rot) takes
+// these sizes, dtype and mask kinds: both MFMA paths, pointer alignment aside.
+static bool rot_supported(int B, int S, int Hq, int Hkv, int D, int dtype, int has_doc,
+                          int has_key_valid) {
+  FwdArgs f = make_fwd((void*)16, (void*)16, (void*)16, (float*)16, (float*)16, (void*)16,
+                       (float*)16, B, S, S, Hq, Hkv, D, (int64_t)S * Hkv * D, (int64_t)Hkv * D,
+                       D, (int64_t)S * Hkv * D, (int64_t)Hkv * D, D, 0, 1,
+                       has_doc ? (const int32_t*)16 : nullptr,
+                       has_key_valid ? (const int32_t*)16 : nullptr, dtype, nullptr);
+  BwdArgs b = sizing_args(B, S, Hq, Hkv, D, dtype, 1);
+  b.doc = f.doc;
+  b.kvalid = f.kvalid;
+  return fwd_mfma_supported(f) && bwd_mfma_supported(b);
+}
+
+int kf_attn_rot_size(int B, int S, int Hq, int Hkv, int D, int dtype, int has_doc,
+                     int has_key_valid, size_t* bytes) {
+  int rc = check_common(B, S, S, Hq, Hkv, D, dtype);
+  if (rc) return rc;
+  KF_CHECK_ARG(bytes != nullptr, "bytes is null");
+  if (!rot_supported(B, S, Hq, Hkv, D, dtype, has_doc, has_key_valid)) {
+    set_error("the rotated-operand path needs bf16, head_dim 64 or 128 and one mask kind at most");
+    return KF_ERR_UNSUPPORTED;
+  }
+  *bytes = rot_bytes(B, S, Hq, Hkv, D);
+  return KF_OK;
+}
+
+int kf_attn_fwd_rot(const void* q, const void* k, const void* v, const float* rope_cos,
+                    const float* rope_sin, void* out, float* lse, void* rot, void* workspace,
+                    size_t workspace_bytes, int B, int S, int Hq, int Hkv, int D, int causal,
+                    const int32_t* doc_ids, const int32_t* key_valid, int dtype, void* stream) {
+  int rc = check_common(B, S, S, Hq, Hkv, D, dtype);
+  if (rc) return rc;
+  KF_CHECK_ARG(q && k && v && rope_cos && rope_sin && out && lse && rot, "null tensor pointer");
+  rc = check_masks(doc_ids, key_valid, causal, S, S, 0);
+  if (rc) return rc;
+  FwdArgs a = make_fwd(q, k, v, rope_cos, rope_sin, out, lse, B, S, S, Hq, Hkv, D,
+                       (int64_t)S * Hkv * D, (int64_t)Hkv * D, D, (int64_t)S * Hkv * D,
+                       (int64_t)Hkv * D, D, 0, causal, doc_ids, key_valid, dtype, stream);
+  if (!rot_supported(B, S, Hq, Hkv, D, dtype, doc_ids != nullptr, key_valid != nullptr) ||
+      !fwd_mfma_supported(a) || ((uintptr_t)rot & 15) != 0) {
+    set_error("kf_attn_fwd_rot needs the bf16 MFMA path (sizes as kf_attn_rot_size accepts, "
+              "16-byte aligned pointers)");
+    return KF_ERR_UNSUPPORTED;
+  }
+  a.rot = rot;
+  const size_t need = fwd_mfma_workspace(B, S, Hkv, D);
+  if (workspace_bytes < need || !workspace) {
+    set_error("workspace too small: need %zu bytes, got %zu", need, workspace_bytes);
+    return KF_ERR_WORKSPACE;
+  }
+  return fwd_mfma(a, workspace);
+}
+
+int kf_attn_bwd_rot_workspace_size(int B, int S, int Hq, int Hkv, int D, int dtype, int causal,
+                                   int with_ds, size_t* bytes) {
+  int rc = check_common(B, S, S, Hq, Hkv, D, dtype);
+  if (rc) return rc;
+  KF_CHECK_ARG(bytes != nullptr, "bytes is null");
+  if (!rot_supported(B, S, Hq, Hkv, D, dtype, 0, 0)) {
+    set_error("the rotated-operand path needs bf16 and head_dim 64 or 128");
+    return KF_ERR_UNSUPPORTED;
+  }
+  BwdArgs a = sizing_args(B, S, Hq, Hkv, D, dtype, causal);
+  a.rot = (const void*)16;
+  *bytes = with_ds ? bwd_mfma_workspace_ds(a) : bwd_mfma_workspace(B, S, Hq, Hkv, D, true);
+  return KF_OK;
+}
+
+int kf_attn_bwd_rot(const void* rot, const void* v, const float* rope_cos, const float* rope_sin,
+                    const void* out, const float* lse, const void* dout, void* dq, void* dk,
+                    void* dv, void* workspace, size_t workspace_bytes, int B, int S, int Hq,
+                    int Hkv, int D, int causal, const int32_t* doc_ids, const int32_t* key_valid,
+                    int dtype, void* stream) {
+  int rc = check_common(B, S, S, Hq, Hkv, D, dtype);
+  if (rc) return rc;
+  KF_CHECK_ARG(rot && v && rope_cos && rope_sin && out && lse && dout && dq && dk && dv,
+               "null tensor pointer");
+  rc = check_masks(doc_ids, key_valid, causal, S, S, 0);
+  if (rc) return rc;
+  BwdArgs a;
+  a.q = nullptr; a.k = nullptr; a.rot = rot;
+  a.v = v; a.cos = rope_cos; a.sin = rope_sin; a.out = out; a.lse = lse;
+  a.dout = dout; a.dq = dq; a.dk = dk; a.dv = dv;
+  a.B = B; a.S = S; a.Hq = Hq; a.Hkv = Hkv; a.D = D; a.causal = causal; a.dtype = dtype;
+  a.doc = doc_ids;
+  a.kvalid = key_valid;
+  a.scale = 1.0f / sqrtf((float)D);
+  a.stream = (hipStream_t)stream;
+  if (!rot_supported(B, S, Hq, Hkv, D, dtype, doc_ids != nullptr, key_valid != nullptr) ||
+      !bwd_mfma_supported(a) || ((uintptr_t)rot & 15) != 0) {
+    set_error("kf_attn_bwd_rot needs the bf16 MFMA path (sizes as kf_attn_rot_size accepts, "
+              "16-byte aligned pointers)");
+    return KF_ERR_UNSUPPORTED;
+  }
+  const size_t need = bwd_mfma_workspace(B, S, Hq, Hkv, D, true);
+  if (workspace_bytes < need || !workspace) {
+    set_error("workspace too small: need %zu bytes, got %zu", need, workspace_bytes);
+    return KF_ERR_WORKSPACE;
+  }
+  return bwd_mfma(a, workspace, workspace_bytes);
+}
+
 int kf_attn_decode_workspace_size(int B, int Hq, int Hkv, int D, int max_len, int dtype,
                                   size_t* bytes) {
   int rc = check_common(B, 1, max_len, Hq, Hkv, D, dtype);

@@ -86,7 +86,8 @@ __global__ __launch_bounds__(256) void q_prep_bwd_kernel(
   constexpr int HALF = D / 2, CP = HALF / 8, TPR = D / 8;
   const int s0 = blockIdx.x * BN, bhq = blockIdx.y, b = bhq / Hq, h = bhq % Hq;
   const int tid = threadIdx.x;
-  for (int it = tid; it < BN * CP; it += 256) {
+  // q null: the rotated rows are already in qrot (written by the forward)
+  for (int it = tid; q != nullptr && it < BN * CP; it += 256) {
     const int row = it / CP, c = it % CP, s = s0 + row;
     u32x4 o1 = {0u, 0u, 0u, 0u}, o2 = {0u, 0u, 0u, 0u};
     if (s < S) {
@@ -948,9 +949,10 @@ struct Ws {
   u32x4* dsb;    // dS records (when kept)
 };
 
-size_t base_bytes(int B, int S, int Hq, int Hkv, int D) {
+// krot and qrot (unless the caller's rot holds them), lse2, delta, tile records
+size_t base_bytes(int B, int S, int Hq, int Hkv, int D, bool rot) {
   const size_t P = (size_t)pad_len(S);
-  return ((size_t)B * Hkv + (size_t)B * Hq) * P * D * sizeof(uint16_t) +
+  return (rot ? 0 : ((size_t)B * Hkv + (size_t)B * Hq) * P * D * sizeof(uint16_t)) +
          2 * (size_t)B * Hq * P * sizeof(float) + (size_t)B * (P / BN) * sizeof(int2);
 }
 size_t align256(size_t n) { return (n + 255) / 256 * 256; }
@@ -967,18 +969,18 @@ size_t ds_bytes(const BwdArgs& a) {
   return bytes <= DS_STORE_MAX ? bytes : 0;
 }
 
-Ws carve(void* base, int B, int S, int Hq, int Hkv, int D) {
+Ws carve(void* base, int B, int S, int Hq, int Hkv, int D, const void* rot) {
   const size_t P = (size_t)pad_len(S);
   const size_t kv = (size_t)B * Hkv * P * D, qq = (size_t)B * Hq * P * D;
   Ws w;
-  bf16* p = (bf16*)base;
+  bf16* p = rot ? (bf16*)rot : (bf16*)base;
   w.krot = p; p += kv;
   w.qrot = p; p += qq;
-  float* f = (float*)p;
+  float* f = rot ? (float*)base : (float*)p;
   w.lse2 = f; f += (size_t)B * Hq * P;
   w.delta = f; f += (size_t)B * Hq * P;
   w.ranges = (int2*)f;
-  w.dsb = (u32x4*)((char*)base + align256(base_bytes(B, S, Hq, Hkv, D)));
+  w.dsb = (u32x4*)((char*)base + align256(base_bytes(B, S, Hq, Hkv, D, rot != nullptr)));
   return w;
 }
 
@@ -1001,7 +1003,7 @@ int launch_dq_ds(const BwdArgs& a, const Ws& w) {
 template <int D>
 int launch_bwd(const BwdArgs& a, void* workspace, bool keep_ds) {
   const int P = pad_len(a.S);
-  const Ws w = carve(workspace, a.B, a.S, a.Hq, a.Hkv, D);
+  const Ws w = carve(workspace, a.B, a.S, a.Hq, a.Hkv, D, a.rot);
   const int n_rep = a.Hq / a.Hkv;
   const float scale_log2 = a.scale * kLog2e;
   FwdArgs fa{};
@@ -1012,10 +1014,14 @@ int launch_bwd(const BwdArgs& a, void* workspace, bool keep_ds) {
   fa.ksh = fa.vsh = D;
   fa.k_rotated = 0; fa.dtype = BF16; fa.stream = a.stream;
   fa.doc = a.doc; fa.kvalid = a.kvalid; fa.causal = a.causal;
-  int rc = launch_kv_prep(fa, w.krot, nullptr, P, w.ranges, KV_V_NONE);
-  if (rc) return rc;
+  // with a.rot the rotated K and Q are the forward's: only the tile records of
+  // an explicit mask are left to prepare
+  if (!a.rot || a.doc || a.kvalid) {
+    const int rc = launch_kv_prep(fa, a.rot ? nullptr : w.krot, P, nullptr, P, w.ranges, KV_V_NONE);
+    if (rc) return rc;
+  }
   KF_LAUNCH("q_prep_bwd", q_prep_bwd_kernel<D>, dim3(P / BN, a.B * a.Hq), dim3(256), 0, a.stream,
-            (const bf16*)a.q, (const bf16*)a.out, (const bf16*)a.dout, a.lse, a.cos, a.sin,
+            a.rot ? nullptr : (const bf16*)a.q, (const bf16*)a.out, (const bf16*)a.dout, a.lse, a.cos, a.sin,
             w.qrot, w.lse2, w.delta, a.S, P, a.Hq);
   KF_CHECK_LAUNCH();
   const int nkb = P / BKV;
@@ -1067,12 +1073,12 @@ bool bwd_mfma_supported(const BwdArgs& a) {
          al16(a.dk) && al16(a.dv) && al16(a.cos) && al16(a.sin);
 }
 
-size_t bwd_mfma_workspace(int B, int S, int Hq, int Hkv, int D) {
-  return base_bytes(B, S, Hq, Hkv, D);
+size_t bwd_mfma_workspace(int B, int S, int Hq, int Hkv, int D, bool rot) {
+  return base_bytes(B, S, Hq, Hkv, D, rot);
 }
 
 size_t bwd_mfma_workspace_ds(const BwdArgs& a) {
-  const size_t base = base_bytes(a.B, a.S, a.Hq, a.Hkv, a.D), ds = ds_bytes(a);
+  const size_t base = base_bytes(a.B, a.S, a.Hq, a.Hkv, a.D, a.rot != nullptr), ds = ds_bytes(a);
   return ds ? align256(base) + ds : base;
 }
 

@@ -37,10 +37,10 @@ using namespace mfma;
 template <int D>
 __global__ __launch_bounds__(256) void kv_prep_kernel(
     const bf16* __restrict__ k, const bf16* __restrict__ v, const float* __restrict__ cos,
-    const float* __restrict__ sin, bf16* __restrict__ krot, bf16* __restrict__ vn, int Sk,
-    int Skp, int Hkv, int64_t ksb, int64_t kss, int64_t ksh, int64_t vsb, int64_t vss,
+    const float* __restrict__ sin, bf16* __restrict__ krot, int krows, bf16* __restrict__ vn,
+    int Sk, int Skp, int Hkv, int64_t ksb, int64_t kss, int64_t ksh, int64_t vsb, int64_t vss,
     int64_t vsh, int k_rotated, const int32_t* __restrict__ doc, const int32_t* __restrict__ kvalid,
-    int2* __restrict__ ranges, int v_mode) {
+    int2* __restrict__ ranges, int v_mode, bf16* __restrict__ qpad, int Hq) {
   constexpr int HALF = D / 2;
   __shared__ __attribute__((aligned(16))) bf16 sVt[D * BN];  // KV_V_TRANSPOSED: [d][key slot]
   constexpr int CP = HALF / 8;
@@ -48,24 +48,27 @@ __global__ __launch_bounds__(256) void kv_prep_kernel(
   const int bh = blockIdx.y;
   const int b = bh / Hkv, g = bh % Hkv;
   const int tid = threadIdx.x;
+  // tiles below Skp carry V and the tile records; the ones up to krows only K rows
+  const int nvb = Skp / BN;
+  const bool vtile = (int)blockIdx.x < nvb;
 
-  if (doc != nullptr && g == 0 && tid < 64) {
+  if (vtile && doc != nullptr && g == 0 && tid < 64) {
     // document-id range of this tile (empty: min > max, when all keys >= Sk)
     const int s = s0 + tid;
     const int d = s < Sk ? doc[(int64_t)b * Sk + s] : 0;
     const int lo = wave_min_i(s < Sk ? d : INT_MAX), hi = wave_max_i(s < Sk ? d : INT_MIN);
-    if (tid == 0) ranges[(int64_t)b * gridDim.x + blockIdx.x] = make_int2(lo, hi);
-  } else if (kvalid != nullptr && g == 0 && tid < 64) {
+    if (tid == 0) ranges[(int64_t)b * nvb + blockIdx.x] = make_int2(lo, hi);
+  } else if (vtile && kvalid != nullptr && g == 0 && tid < 64) {
     // number of valid keys in this tile and the first one's position
     const int s = s0 + tid;
     const bool ok = s < Sk && kvalid[(int64_t)b * Sk + s] != 0;
     const uint64_t m = __builtin_amdgcn_ballot_w64(ok);
     if (tid == 0)
-      ranges[(int64_t)b * gridDim.x + blockIdx.x] =
+      ranges[(int64_t)b * nvb + blockIdx.x] =
           make_int2(__builtin_popcountll(m), m ? s0 + __builtin_ctzll(m) : INT_MAX);
   }
 
-  for (int it = tid; it < BN * CP; it += 256) {
+  for (int it = tid; krot != nullptr && it < BN * CP; it += 256) {
     const int key = it / CP, c = it % CP;
     const int s = s0 + key;
     u32x4 o1 = {0u, 0u, 0u, 0u}, o2 = {0u, 0u, 0u, 0u};
@@ -88,11 +91,22 @@ __global__ __launch_bounds__(256) void kv_prep_kernel(
         o2 = pack8(r2);
       }
     }
-    bf16* dst = krot + ((int64_t)bh * Skp + s) * D;
+    bf16* dst = krot + ((int64_t)bh * krows + s) * D;
     *(u32x4*)(dst + 8 * c) = o1;
     *(u32x4*)(dst + 8 * c + HALF) = o2;
   }
-  if (v_mode == KV_V_NONE) return;
+  if (qpad != nullptr && s0 + BN > Sk) {
+    // rotated-Q rows past the sequence, for the group's query heads
+    const int n_rep = Hq / Hkv;
+    for (int it = tid; it < n_rep * BN * (D / 8); it += 256) {
+      const int hl = it / (BN * (D / 8)), r = (it / (D / 8)) % BN, c = it % (D / 8);
+      const int s = s0 + r;
+      if (s >= Sk && s < krows)
+        *(u32x4*)(qpad + (((int64_t)b * Hq + g * n_rep + hl) * krows + s) * D + 8 * c) =
+            u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+  if (!vtile || v_mode == KV_V_NONE) return;
   if (v_mode == KV_V_ROWS) {
     for (int it = tid; it < BN * (D / 8); it += 256) {
       const int key = it / (D / 8), c = it % (D / 8);
@@ -169,9 +183,9 @@ template <int D, int MODE>
 __global__ __launch_bounds__(256, 2) void fwd_mfma_kernel(
     const bf16* __restrict__ q, const float* __restrict__ cos, const float* __restrict__ sin,
     const bf16* __restrict__ krot, const bf16* __restrict__ vn, bf16* __restrict__ out,
-    float* __restrict__ lse, int Sq, int Sk, int Skp, int Hq, int Hkv, int n_rep, int bm_pos,
-    int nqb, float scale_log2, int causal, const int32_t* __restrict__ aux,
-    const int2* __restrict__ ranges) {
+    float* __restrict__ lse, int Sq, int Sk, int Skp, int krows, int Hq, int Hkv, int n_rep,
+    int bm_pos, int nqb, float scale_log2, int causal, const int32_t* __restrict__ aux,
+    const int2* __restrict__ ranges, bf16* __restrict__ qrot) {
   constexpr bool DOC = MODE == MASK_DOC, KPM = MODE == MASK_KPM, LIST = DOC || KPM;
   constexpr int KS = D / 16, DT = D / 32;
   constexpr int KR = D / 8;  // 16-byte chunks per K / V row
@@ -190,7 +204,7 @@ __global__ __launch_bounds__(256, 2) void fwd_mfma_kernel(
   int ntiles = (kend + BN - 1) / BN;
   const int32_t* arow = LIST ? aux + (int64_t)ri.b * Sk : nullptr;
   const int2* rec = ranges + (int64_t)ri.b * (Skp / BN);
-  const bf16* kbase = krot + (int64_t)bh * Skp * D;
+  const bf16* kbase = krot + (int64_t)bh * krows * D;
   const bf16* vbase = vn + (int64_t)bh * D * Skp;  // V^T, keys in fragment order
   auto stage = [&](int t, int buf) {
     tile_to_lds<BN, KR>(kbase + (int64_t)t * BN * D, D, sK[buf], w, lane);
@@ -241,6 +255,14 @@ __global__ __launch_bounds__(256, 2) void fwd_mfma_kernel(
 
   bf16x8 qf[KS];
   load_q_frag<D>(q, cos, sin, ri, Sq, Hq, hh, qf);
+  if (qrot != nullptr && ri.q_valid) {
+    // the rotated q row for the backward (read there long after: streaming stores)
+    bf16* dst = qrot + (((int64_t)ri.b * Hq + ri.hq) * krows + ri.pos) * D + 8 * hh;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+      __builtin_nontemporal_store(__builtin_bit_cast(u32x4, qf[ks]),
+                                  (u32x4*)(dst + (ks < KS / 2 ? 16 * ks : D / 2 + 16 * (ks - KS / 2))));
+  }
 
   float m = LIST ? -1e30f : -INFINITY, lsum = 0.f;
   f32x16 acc[DT];
@@ -680,23 +702,29 @@ size_t fwd_mfma_workspace(int B, int Sk, int Hkv, int D) {
   return 2 * (size_t)B * Hkv * Skp * D * sizeof(uint16_t) + (size_t)B * (Skp / BN) * sizeof(int2);
 }
 
-int launch_kv_prep(const FwdArgs& a, void* krot_, void* vn_, int Skp, int2* ranges,
-                   int v_mode) {
+int launch_kv_prep(const FwdArgs& a, void* krot_, int krows, void* vn_, int Skp, int2* ranges,
+                   int v_mode, void* qpad_) {
   bf16* krot = (bf16*)krot_;
   bf16* vn = (bf16*)vn_;
-  dim3 grid(Skp / BN, a.B * a.Hkv);
+  bf16* qpad = (bf16*)qpad_;
+  dim3 grid((krot ? krows : Skp) / BN, a.B * a.Hkv);
   if (a.D == 128)
     KF_LAUNCH("kv_prep", kv_prep_kernel<128>, grid, dim3(256), 0, a.stream, (const bf16*)a.k,
-                       (const bf16*)a.v, a.cos, a.sin, krot, vn, a.Sk, Skp, a.Hkv, a.ksb, a.kss,
-                       a.ksh, a.vsb, a.vss, a.vsh, a.k_rotated, a.doc, a.kvalid, ranges,
-                       v_mode);
+              (const bf16*)a.v, a.cos, a.sin, krot, krows, vn, a.Sk, Skp, a.Hkv, a.ksb, a.kss,
+              a.ksh, a.vsb, a.vss, a.vsh, a.k_rotated, a.doc, a.kvalid, ranges, v_mode, qpad,
+              a.Hq);
   else
     KF_LAUNCH("kv_prep", kv_prep_kernel<64>, grid, dim3(256), 0, a.stream, (const bf16*)a.k,
-                       (const bf16*)a.v, a.cos, a.sin, krot, vn, a.Sk, Skp, a.Hkv, a.ksb, a.kss,
-                       a.ksh, a.vsb, a.vss, a.vsh, a.k_rotated, a.doc, a.kvalid, ranges,
-                       v_mode);
+              (const bf16*)a.v, a.cos, a.sin, krot, krows, vn, a.Sk, Skp, a.Hkv, a.ksb, a.kss,
+              a.ksh, a.vsb, a.vss, a.vsh, a.k_rotated, a.doc, a.kvalid, ranges, v_mode, qpad,
+              a.Hq);
   KF_CHECK_LAUNCH();
   return KF_OK;
+}
+
+size_t rot_bytes(int B, int S, int Hq, int Hkv, int D) {
+  return ((size_t)B * Hkv + (size_t)B * Hq) * (size_t)((S + 127) / 128 * 128) * D *
+         sizeof(uint16_t);
 }
 
 namespace {
@@ -704,13 +732,25 @@ namespace {
 struct FwdWs {
   bf16 *krot, *vn;
   int2* ranges;
+  int krows;   // rows of krot per KV head
+  bf16* qrot;  // a.rot's rotated Q, or null
 };
 
+// With a.rot the rotated K goes there (P rows per KV head, as the backward
+// reads it) instead of the workspace's krot region, and the forward also
+// writes the rotated Q after it.
 FwdWs carve_fwd(const FwdArgs& a, void* workspace, int Skp) {
   FwdWs w;
   w.krot = (bf16*)workspace;
   w.vn = w.krot + (size_t)a.B * a.Hkv * Skp * a.D;
   w.ranges = (int2*)(w.vn + (size_t)a.B * a.Hkv * Skp * a.D);
+  w.krows = Skp;
+  w.qrot = nullptr;
+  if (a.rot != nullptr) {
+    w.krows = (a.Sk + 127) / 128 * 128;
+    w.krot = (bf16*)a.rot;
+    w.qrot = w.krot + (size_t)a.B * a.Hkv * w.krows * a.D;
+  }
   return w;
 }
 
@@ -721,8 +761,8 @@ void launch_fwd_kernel(const FwdArgs& a, const FwdWs& w, int Skp, int n_rep, int
                        unsigned nblk) {
   KF_LAUNCH("fwd_mfma", (fwd_mfma_kernel<D, MODE>), dim3(nblk), dim3(256), 0, a.stream,
             (const bf16*)a.q, a.cos, a.sin, w.krot, w.vn, (bf16*)a.out, a.lse, a.Sq, a.Sk, Skp,
-            a.Hq, a.Hkv, n_rep, bm_pos, nqb, a.scale * kLog2e, a.causal,
-            a.doc ? a.doc : a.kvalid, w.ranges);
+            w.krows, a.Hq, a.Hkv, n_rep, bm_pos, nqb, a.scale * kLog2e, a.causal,
+            a.doc ? a.doc : a.kvalid, w.ranges, w.qrot);
 }
 
 template <int D>
@@ -763,7 +803,7 @@ void launch_capture_mode(const FwdArgs& a, const FwdWs& w, float* probs, int Skp
 int fwd_mfma(const FwdArgs& a, void* workspace) {
   const int Skp = (a.Sk + BN - 1) / BN * BN;
   const FwdWs w = carve_fwd(a, workspace, Skp);
-  int rc = launch_kv_prep(a, w.krot, w.vn, Skp, w.ranges, KV_V_TRANSPOSED);
+  int rc = launch_kv_prep(a, w.krot, w.krows, w.vn, Skp, w.ranges, KV_V_TRANSPOSED, w.qrot);
   if (rc) return rc;
   const int n_rep = a.Hq / a.Hkv;
   const int bm_pos = pick_bm_pos(n_rep);
@@ -779,7 +819,7 @@ int fwd_mfma(const FwdArgs& a, void* workspace) {
 int capture_probs_mfma(const FwdArgs& a, float* probs, void* workspace) {
   const int Skp = (a.Sk + BN - 1) / BN * BN;
   const FwdWs w = carve_fwd(a, workspace, Skp);
-  int rc = launch_kv_prep(a, w.krot, w.vn, Skp, w.ranges, KV_V_TRANSPOSED);
+  int rc = launch_kv_prep(a, w.krot, Skp, w.vn, Skp, w.ranges, KV_V_TRANSPOSED);
   if (rc) return rc;
   const int n_rep = a.Hq / a.Hkv;
   const int bm_pos = pick_bm_pos(n_rep);

@@ -30,6 +30,9 @@ struct FwdArgs {
   int dtype;
   float scale;        // softmax scale, D^-1/2
   hipStream_t stream;
+  void* rot = nullptr;  // null, or the backward's rotated operands written by fwd_mfma (self-
+                        // attention): K [B*Hkv][P][D] then Q [B*Hq][P][D] bf16 after
+                        // RoPE, P = S rounded up to 128, rows past S zero
 };
 
 struct BwdArgs {
@@ -45,6 +48,7 @@ struct BwdArgs {
   const int32_t* kvalid;  // [B, S] key validity or null (see FwdArgs::kvalid)
   float scale;
   hipStream_t stream;
+  const void* rot = nullptr;  // FwdArgs::rot of the forward call; q and k are then unused
 };
 
 // generic kernels (kf_generic.hip)
@@ -65,8 +69,12 @@ bool fwd_mfma_supported(const FwdArgs& a);
 enum { KV_V_ROWS = 0, KV_V_TRANSPOSED = 1, KV_V_NONE = 2 };
 // Compute units of the current device (cached per device), to size persistent grids.
 int device_cu_count();
-int launch_kv_prep(const FwdArgs& a, void* krot, void* vn, int Skp, int2* ranges,
-                   int v_mode = KV_V_ROWS);
+// krot holds krows >= Skp rows per KV head (null: only the tile records); qpad,
+// if set, is the rotated-Q buffer of FwdArgs::rot, whose rows past Sq it zeroes.
+int launch_kv_prep(const FwdArgs& a, void* krot, int krows, void* vn, int Skp, int2* ranges,
+                   int v_mode, void* qpad = nullptr);
+// bytes of FwdArgs::rot
+size_t rot_bytes(int B, int S, int Hq, int Hkv, int D);
 size_t fwd_mfma_workspace(int B, int Sk, int Hkv, int D);
 int fwd_mfma(const FwdArgs& a, void* workspace);
 // LSE (a.lse), probabilities and out (a.out) of the capture path in one launch
@@ -78,7 +86,7 @@ int capture_probs_mfma(const FwdArgs& a, float* probs, void* workspace);
 constexpr int DS_REC_Q = 64, DS_REC_K = 32;
 
 bool bwd_mfma_supported(const BwdArgs& a);
-size_t bwd_mfma_workspace(int B, int S, int Hq, int Hkv, int D);
+size_t bwd_mfma_workspace(int B, int S, int Hq, int Hkv, int D, bool rot = false);
 // Workspace with which bwd_mfma stores the dS tiles once for dQ instead of
 // recomputing S and dP (unmasked launches up to a size cap); otherwise
 // bwd_mfma_workspace.  bwd_mfma takes that path when workspace_bytes allows.

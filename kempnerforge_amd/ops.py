@@ -226,6 +226,102 @@ def bwd_raw(q, k, v, cos, sin, out, lse, dout, *, causal: bool, doc_ids=None,
     return dq, dk, dv
 
 
+_KF_ERR_UNSUPPORTED = 2
+
+
+def rot_size(B: int, S: int, Hq: int, Hkv: int, D: int, dtype: torch.dtype, has_doc: bool,
+             has_key_padding: bool) -> int:
+    """Bytes of the rotated-operand buffer of :func:`fwd_rot_raw`, or 0 when that
+    path does not take these sizes, dtype or mask kinds (``kf_attn_rot_size``)."""
+    lib = _lib.load()
+    if dtype not in _DTYPES or not hasattr(lib, "kf_attn_rot_size"):  # (a KF_ATTN_LIB build
+        return 0                                                        # predating the pair)
+    n = _lib.size_out()
+    rc = lib.kf_attn_rot_size(B, S, Hq, Hkv, D, _DTYPES[dtype], int(has_doc),
+                                      int(has_key_padding), ctypes.byref(n))
+    if rc == _KF_ERR_UNSUPPORTED:
+        return 0
+    _lib.check(rc, "kf_attn_rot_size")
+    return n.value
+
+
+def fwd_rot_raw(q, k, v, cos, sin, *, causal: bool, doc_ids=None, key_padding_mask=None):
+    """out, lse, rot for self-attention (``kf_attn_fwd_rot``): :func:`fwd_raw` with
+    un-rotated BSHD k that also returns ``rot``, q and k after RoPE as the
+    backward reads them, so that :func:`bwd_rot_raw` needs neither q nor k.
+    None when that path does not apply (dtype, head_dim, alignment): then use
+    :func:`fwd_raw` and :func:`bwd_raw`."""
+    _require_gpu(q, k, v)
+    lib = _lib.load()
+    q, k, v = (t.contiguous() for t in (q, k, v))
+    B, S, Hq, D = q.shape
+    Hkv = k.shape[2]
+    if (tuple(k.shape) != (B, S, Hkv, D) or tuple(v.shape) != tuple(k.shape)
+            or k.dtype != q.dtype or v.dtype != q.dtype):
+        return None
+    cos = _rope_table(cos, S, D // 2, "rope_cos")
+    sin = _rope_table(sin, S, D // 2, "rope_sin")
+    doc = _doc_ids(doc_ids, B, S, q.device)
+    kv = _key_valid(key_padding_mask, B, S, q.device)
+    nrot = rot_size(B, S, Hq, Hkv, D, q.dtype, doc is not None, kv is not None)
+    if nrot == 0:
+        return None
+    dt = _dtype_code(q)
+    out = torch.empty_like(q)
+    lse = torch.empty(B, Hq, S, dtype=torch.float32, device=q.device)
+    rot = torch.empty(nrot // q.element_size(), dtype=q.dtype, device=q.device)
+    nbytes = _lib.size_out()
+    _lib.check(lib.kf_attn_fwd_workspace_size(B, S, S, Hq, Hkv, D, dt, ctypes.byref(nbytes)),
+               "kf_attn_fwd_workspace_size")
+    ws = _workspace(nbytes.value, q.device)
+    rc = lib.kf_attn_fwd_rot(_ptr(q), _ptr(k), _ptr(v), _ptr(cos), _ptr(sin), _ptr(out),
+                             _ptr(lse), _ptr(rot), _ptr(ws), ws.numel(), B, S, Hq, Hkv, D,
+                             int(causal), _ptr(doc), _ptr(kv), dt, _stream(q))
+    if rc == _KF_ERR_UNSUPPORTED:
+        return None
+    _lib.check(rc, "kf_attn_fwd_rot")
+    return out, lse, rot
+
+
+def bwd_rot_raw(rot, v, cos, sin, out, lse, dout, *, causal: bool, doc_ids=None,
+                key_padding_mask=None, low_memory: bool | None = None):
+    """dq, dk, dv for :func:`fwd_rot_raw` from its ``rot`` (``kf_attn_bwd_rot``);
+    workspace policy as in :func:`bwd_raw`.  The results equal :func:`bwd_raw`'s
+    bit for bit."""
+    _require_gpu(rot, v, out, lse, dout)
+    lib = _lib.load()
+    v, out, dout, lse = (t.contiguous() for t in (v, out, dout, lse))
+    if dout.data_ptr() % 16:
+        dout = dout.clone()
+    B, S, Hq, D = out.shape
+    Hkv = v.shape[2]
+    cos = _rope_table(cos, S, D // 2, "rope_cos")
+    sin = _rope_table(sin, S, D // 2, "rope_sin")
+    doc = _doc_ids(doc_ids, B, S, out.device)
+    kv = _key_valid(key_padding_mask, B, S, out.device)
+    dt = _dtype_code(out)
+    dq, dk, dv = torch.empty_like(out), torch.empty_like(v), torch.empty_like(v)
+    nbytes = _lib.size_out()
+    _lib.check(lib.kf_attn_bwd_rot_workspace_size(B, S, Hq, Hkv, D, dt, int(causal), 0,
+                                                  ctypes.byref(nbytes)),
+               "kf_attn_bwd_rot_workspace_size")
+    low_memory = _BWD_LOW_MEMORY if low_memory is None else low_memory
+    if not low_memory and kv is None:  # key padding never keeps dS
+        with_ds = _lib.size_out()
+        _lib.check(lib.kf_attn_bwd_rot_workspace_size(B, S, Hq, Hkv, D, dt, int(causal), 1,
+                                                      ctypes.byref(with_ds)),
+                   "kf_attn_bwd_rot_workspace_size")
+        if keep_ds_tiles(with_ds.value - nbytes.value, available_bytes(out.device)):
+            nbytes = with_ds
+    ws = _workspace(nbytes.value, out.device)
+    _lib.check(lib.kf_attn_bwd_rot(_ptr(rot), _ptr(v), _ptr(cos), _ptr(sin), _ptr(out),
+                                   _ptr(lse), _ptr(dout), _ptr(dq), _ptr(dk), _ptr(dv),
+                                   _ptr(ws), ws.numel(), B, S, Hq, Hkv, D, int(causal),
+                                   _ptr(doc), _ptr(kv), dt, _stream(out)),
+               "kf_attn_bwd_rot")
+    return dq, dk, dv
+
+
 def decode_raw(q_new, k_new, v_new, k_cache, v_cache, lens, cos, sin, *, rope_row_offset: int,
                max_len: int, q_norm_weight=None, k_norm_weight=None, norm_eps: float = 1e-5):
     """One decode step (``kf_attn_decode``); writes the rotated new k and v into
@@ -346,15 +442,25 @@ def capture_raw(q, k, v, cos, sin, *, causal: bool, k_rotated: bool, k_layout: s
 def attn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos: torch.Tensor,
              sin: torch.Tensor, causal: bool, doc_ids: Optional[torch.Tensor] = None,
              key_padding_mask: Optional[torch.Tensor] = None
-             ) -> tuple[torch.Tensor, torch.Tensor]:
-    return fwd_raw(q, k, v, cos, sin, causal=causal, k_rotated=False, doc_ids=doc_ids,
-                   key_padding_mask=key_padding_mask)
+             ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """out, lse and rot (empty when the rotated-operand path does not apply)."""
+    res = fwd_rot_raw(q, k, v, cos, sin, causal=causal, doc_ids=doc_ids,
+                      key_padding_mask=key_padding_mask)
+    if res is not None:
+        return res
+    out, lse = fwd_raw(q, k, v, cos, sin, causal=causal, k_rotated=False, doc_ids=doc_ids,
+                       key_padding_mask=key_padding_mask)
+    return out, lse, q.new_empty(0)
 
 
 @attn_fwd.register_fake
 def _(q, k, v, cos, sin, causal, doc_ids=None, key_padding_mask=None):
-    B, S, Hq, _ = q.shape
-    return torch.empty_like(q), q.new_empty(B, Hq, S, dtype=torch.float32)
+    # rot's size assumes 16-byte aligned inputs (as allocator tensors are)
+    B, S, Hq, D = q.shape
+    nrot = rot_size(B, S, Hq, k.shape[2], D, q.dtype, doc_ids is not None,
+                    key_padding_mask is not None) if k.shape[1] == S else 0
+    return (torch.empty_like(q), q.new_empty(B, Hq, S, dtype=torch.float32),
+            q.new_empty(nrot // q.element_size()))
 
 
 @torch.library.custom_op("kf::attn_bwd", mutates_args=(), device_types="cuda")
@@ -372,17 +478,45 @@ def _(q, k, v, cos, sin, out, lse, dout, causal, doc_ids=None, key_padding_mask=
     return torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
 
 
+@torch.library.custom_op("kf::attn_bwd_rot", mutates_args=(), device_types="cuda")
+def attn_bwd_rot(rot: torch.Tensor, v: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+                 out: torch.Tensor, lse: torch.Tensor, dout: torch.Tensor, causal: bool,
+                 doc_ids: Optional[torch.Tensor] = None,
+                 key_padding_mask: Optional[torch.Tensor] = None
+                 ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    return bwd_rot_raw(rot, v, cos, sin, out, lse, dout, causal=causal, doc_ids=doc_ids,
+                       key_padding_mask=key_padding_mask)
+
+
+@attn_bwd_rot.register_fake
+def _(rot, v, cos, sin, out, lse, dout, causal, doc_ids=None, key_padding_mask=None):
+    return torch.empty_like(out), torch.empty_like(v), torch.empty_like(v)
+
+
 def _setup_context(ctx, inputs, output):
     q, k, v, cos, sin, causal, doc_ids, key_padding_mask = inputs
-    out, lse = output
-    ctx.save_for_backward(q, k, v, cos, sin, out, lse, doc_ids, key_padding_mask)
+    out, lse, rot = output
+    # only out carries a gradient: no zero-filled gradients for lse and rot
+    ctx.mark_non_differentiable(lse, rot)
+    ctx.set_materialize_grads(False)
+    # with rot the backward needs neither q nor k: keep rot in their place
+    ctx.use_rot = rot.numel() > 0
+    if ctx.use_rot:
+        ctx.save_for_backward(rot, v, cos, sin, out, lse, doc_ids, key_padding_mask)
+    else:
+        ctx.save_for_backward(q, k, v, cos, sin, out, lse, doc_ids, key_padding_mask)
     ctx.causal = causal
 
 
-def _backward(ctx, dout, dlse):
-    q, k, v, cos, sin, out, lse, doc_ids, key_padding_mask = ctx.saved_tensors
-    dq, dk, dv = attn_bwd(q, k, v, cos, sin, out, lse, dout.contiguous(), ctx.causal, doc_ids,
-                          key_padding_mask)
+def _backward(ctx, dout, dlse, drot):
+    if ctx.use_rot:
+        rot, v, cos, sin, out, lse, doc_ids, key_padding_mask = ctx.saved_tensors
+        dq, dk, dv = attn_bwd_rot(rot, v, cos, sin, out, lse, dout.contiguous(), ctx.causal,
+                                  doc_ids, key_padding_mask)
+    else:
+        q, k, v, cos, sin, out, lse, doc_ids, key_padding_mask = ctx.saved_tensors
+        dq, dk, dv = attn_bwd(q, k, v, cos, sin, out, lse, dout.contiguous(), ctx.causal,
+                              doc_ids, key_padding_mask)
     return dq, dk, dv, None, None, None, None, None
 
 
@@ -402,5 +536,5 @@ def attention(q, k, v, rope_cos, rope_sin, *, causal: bool = True, doc_ids=None,
     ``key_padding_mask [B,S]`` (True = attend) its padded-key branch
     (``:214-225``, ``kempnerforge/model/mot.py:188-198``), NaN guard included.
     """
-    out, _ = attn_fwd(q, k, v, rope_cos, rope_sin, causal, doc_ids, key_padding_mask)
+    out, _, _ = attn_fwd(q, k, v, rope_cos, rope_sin, causal, doc_ids, key_padding_mask)
     return out

@@ -30,7 +30,8 @@ def test_header_declares_the_entry_points():
         "kf_version", "kf_last_error", "kf_attn_fwd", "kf_attn_bwd", "kf_attn_decode",
         "kf_kv_cache_append", "kf_attn_capture", "kf_attn_fwd_workspace_size",
         "kf_attn_bwd_workspace_size", "kf_attn_decode_workspace_size",
-        "kf_attn_capture_workspace_size",
+        "kf_attn_capture_workspace_size", "kf_attn_rot_size", "kf_attn_fwd_rot",
+        "kf_attn_bwd_rot_workspace_size", "kf_attn_bwd_rot",
     }
 
 
@@ -80,6 +81,22 @@ def test_host_only_calls():
         assert lib.kf_attn_bwd_workspace_size(*args[:6], ctypes.byref(small)) == 0
         assert lib.kf_attn_bwd_workspace_size_ds(*args, ctypes.byref(big)) == 0
         assert big.value == small.value
+    # rotated operands kept from the forward: K per KV head then Q per query head,
+    # bf16 [P][D]; the backward reading them needs that much less workspace
+    assert lib.kf_attn_rot_size(B, S, Hq, Hkv, D, 1, 0, 0, ctypes.byref(n)) == 0
+    rot = (B * Hkv + B * Hq) * P * D * 2
+    assert n.value == rot
+    assert lib.kf_attn_rot_size(B, 4000, Hq, Hkv, D, 1, 1, 0, ctypes.byref(n)) == 0
+    assert n.value == rot  # P = 4096 for S = 4000
+    assert lib.kf_attn_bwd_rot_workspace_size(B, S, Hq, Hkv, D, 1, 1, 0, ctypes.byref(n)) == 0
+    assert n.value == base - rot
+    assert lib.kf_attn_bwd_rot_workspace_size(B, S, Hq, Hkv, D, 1, 1, 1, ctypes.byref(n)) == 0
+    assert n.value == (base - rot + 255) // 256 * 256 + B * Hq * P * (P + 64)
+    # only the bf16 MFMA kernels take that path (fp32, head_dim 96, both masks)
+    for args in ((B, S, Hq, Hkv, D, 0, 0, 0), (B, S, Hq, Hkv, 96, 1, 0, 0),
+                 (B, S, Hq, Hkv, D, 1, 1, 1)):
+        assert lib.kf_attn_rot_size(*args, ctypes.byref(n)) == 2
+    assert lib.kf_attn_bwd_rot_workspace_size(B, S, Hq, Hkv, 96, 1, 1, 0, ctypes.byref(n)) == 2
     # kv-cache overflow is rejected on the host (reference generate.py:92-96 guard)
     rc = lib.kf_kv_cache_append(ctypes.c_void_p(16), ctypes.c_void_p(16), ctypes.c_void_p(16),
                                 ctypes.c_void_p(16), ctypes.c_void_p(16), ctypes.c_void_p(16),
