@@ -442,7 +442,8 @@ def run_full(args, torch, wl):
 def _short(name: str) -> str:
     """Kernel symbol -> the launcher's name (kf::..._kernel<...> -> ...)."""
     m = re.search(r"(kv_prep|fwd_mfma|q_prep_bwd|bwd_dkdv|bwd_dq_ds|bwd_dq|decode_stream|"
-                  r"decode_merge|capture_probs_mfma|kv_append|append)_kernel", name)
+                  r"decode_merge|capture_probs_mfma|kv_append|append|doc_block_tiles|"
+                  r"order_by_count)_kernel", name)
     if m:
         return {"capture_probs_mfma": "capture_probs", "append": "kv_append"}.get(m.group(1),
                                                                                  m.group(1))

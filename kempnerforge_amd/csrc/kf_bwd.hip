@@ -467,7 +467,7 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(
     bf16* __restrict__ dv, int S, int P, int Hq, int Hkv, int n_rep, int nkb, int nitems,
     float scale_log2,
     float scale, int causal, const int32_t* __restrict__ aux, const int2* __restrict__ ranges,
-    u32x4* __restrict__ dsb) {
+    u32x4* __restrict__ dsb, const int* __restrict__ order) {
   constexpr bool DOC = MODE == MASK_DOC, KPM = MODE == MASK_KPM;
   __shared__ __attribute__((aligned(16))) DkdvStage<D> st[2];
   __shared__ __attribute__((aligned(16))) u32x4 sP[4 * 4 * 64];  // [key group][chunk][lane]
@@ -478,8 +478,15 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(
   // persistent: one (key block, KV head) item per round
   const XcdItems xi = xcd_items(nitems);
   for (int rnd = 0;; ++rnd) {
-    const int logical = xcd_item(xi, rnd);
+    int logical = xcd_item(xi, rnd);
     if (logical < 0) break;
+    if (order != nullptr) {
+      // items by descending work (the (batch row, key block) order, heads
+      // adjacent), dealt round-robin over the XCDs
+      const int rank = (logical - xi.lo) * 8 + (int)(blockIdx.x % 8);
+      const int bk = order[rank / Hkv];
+      logical = ((bk / nkb) * Hkv + rank % Hkv) * nkb + bk % nkb;
+    }
     const int bh = logical / nkb;
     const int kb = logical % nkb;  // ascending: the longest causal key tiles first
     const int b = bh / Hkv, g = bh % Hkv;
@@ -942,18 +949,78 @@ __global__ __launch_bounds__(64 * HB) void bwd_dq_ds_kernel(
   }
 }
 
+// MASK_DOC: how many query tiles each (batch row, 128-key block) lists, i.e.
+// the dK/dV kernel's work per item; one wavefront per block.
+__global__ __launch_bounds__(256) void doc_block_tiles_kernel(const int32_t* __restrict__ doc,
+                                                              const int2* __restrict__ ranges,
+                                                              int S, int P, int nkb, int nblocks,
+                                                              int* __restrict__ counts) {
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int i = blockIdx.x * 4 + w;
+  if (i >= nblocks) return;
+  const int b = i / nkb, k0 = (i % nkb) * BKV;
+  const int n = doc_tile_list(doc + (int64_t)b * S, k0, min(k0 + BKV, S),
+                              ranges + (int64_t)b * (P / BN), k0 / BQ, (S + BQ - 1) / BQ,
+                              nullptr, lane);
+  if (lane == 0) counts[i] = n;
+}
+
+// The blocks by descending count (a counting sort in one workgroup): the dK/dV
+// workgroup of rank r takes the r-th, so the hardware's in-order dispatch
+// deals the longest items first and each XCD (every 8th rank) an equal share.
+// Ties land in any order; no result depends on which workgroup computes an item.
+__global__ __launch_bounds__(1024) void order_by_count_kernel(const int* __restrict__ counts,
+                                                              int n, int* __restrict__ order) {
+  __shared__ int hist[DOC_MAX_TILES + 1];
+  const int t = threadIdx.x;
+  for (int c = t; c <= DOC_MAX_TILES; c += 1024) hist[c] = 0;
+  __syncthreads();
+  for (int i = t; i < n; i += 1024) atomicAdd(&hist[min(counts[i], DOC_MAX_TILES)], 1);
+  __syncthreads();
+  if (t < 64) {
+    // start of each count's run in descending order: lane t sums PER bins from
+    // the top, then an exclusive prefix of the lane sums
+    constexpr int PER = (DOC_MAX_TILES + 1 + 63) / 64;
+    int local[PER], sum = 0;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const int c = DOC_MAX_TILES - (PER * t + j);
+      local[j] = c >= 0 ? hist[c] : 0;
+      sum += local[j];
+    }
+    int incl = sum;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int v = __shfl_up(incl, o, 64);
+      if (t >= o) incl += v;
+    }
+    int run = incl - sum;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const int c = DOC_MAX_TILES - (PER * t + j);
+      if (c >= 0) hist[c] = run;
+      run += local[j];
+    }
+  }
+  __syncthreads();
+  for (int i = t; i < n; i += 1024) order[atomicAdd(&hist[min(counts[i], DOC_MAX_TILES)], 1)] = i;
+}
+
 struct Ws {
   bf16 *krot, *qrot;
   float *lse2, *delta;
   int2* ranges;  // [B][P/64] document-id range per tile (packed documents only)
+  int *counts, *order;  // [B][P/128] each: dK/dV item work and order (packed documents)
   u32x4* dsb;    // dS records (when kept)
 };
 
-// krot and qrot (unless the caller's rot holds them), lse2, delta, tile records
+// krot and qrot (unless the caller's rot holds them), lse2, delta, tile
+// records, item counts and order
 size_t base_bytes(int B, int S, int Hq, int Hkv, int D, bool rot) {
   const size_t P = (size_t)pad_len(S);
   return (rot ? 0 : ((size_t)B * Hkv + (size_t)B * Hq) * P * D * sizeof(uint16_t)) +
-         2 * (size_t)B * Hq * P * sizeof(float) + (size_t)B * (P / BN) * sizeof(int2);
+         2 * (size_t)B * Hq * P * sizeof(float) + (size_t)B * (P / BN) * sizeof(int2) +
+         2 * (size_t)B * (P / BKV) * sizeof(int);
 }
 size_t align256(size_t n) { return (n + 255) / 256 * 256; }
 
@@ -980,6 +1047,8 @@ Ws carve(void* base, int B, int S, int Hq, int Hkv, int D, const void* rot) {
   w.lse2 = f; f += (size_t)B * Hq * P;
   w.delta = f; f += (size_t)B * Hq * P;
   w.ranges = (int2*)f;
+  w.counts = (int*)(w.ranges + (size_t)B * (P / BN));
+  w.order = w.counts + (size_t)B * (P / BKV);
   w.dsb = (u32x4*)((char*)base + align256(base_bytes(B, S, Hq, Hkv, D, rot != nullptr)));
   return w;
 }
@@ -1025,6 +1094,16 @@ int launch_bwd(const BwdArgs& a, void* workspace, bool keep_ds) {
             w.qrot, w.lse2, w.delta, a.S, P, a.Hq);
   KF_CHECK_LAUNCH();
   const int nkb = P / BKV;
+  // packed documents: the dK/dV items by their listed query tiles, most first
+  const int* order = nullptr;
+  if (a.doc) {
+    const int nblk = a.B * nkb;
+    KF_LAUNCH("doc_block_tiles", doc_block_tiles_kernel, dim3((nblk + 3) / 4), dim3(256), 0,
+              a.stream, a.doc, w.ranges, a.S, P, nkb, nblk, w.counts);
+    KF_LAUNCH("order_by_count", order_by_count_kernel, dim3(1), dim3(1024), 0, a.stream,
+              w.counts, nblk, w.order);
+    order = w.order;
+  }
   // persistent grids: one workgroup per CU (a multiple of 8, one share per XCD).
   // With an explicit mask the items' lengths no longer fall in launch order, so
   // the zigzag shares would not balance: one workgroup per item there.
@@ -1040,7 +1119,7 @@ int launch_bwd(const BwdArgs& a, void* workspace, bool keep_ds) {
             dim3(std::min(nkb * a.B * a.Hkv, grid_cap)), dim3(512), 0, a.stream, w.krot, (const bf16*)a.v,
             w.qrot, (const bf16*)a.dout, w.lse2, w.delta, a.cos, a.sin, (bf16*)a.dk,
             (bf16*)a.dv, a.S, P, a.Hq, a.Hkv, n_rep, nkb, nkb * a.B * a.Hkv,
-            scale_log2, a.scale, a.causal, aux, w.ranges, w.dsb);
+            scale_log2, a.scale, a.causal, aux, w.ranges, w.dsb, order);
   KF_CHECK_LAUNCH();
   if (keep_ds)
     return n_rep % 4 == 0   ? launch_dq_ds<D, 4>(a, w)

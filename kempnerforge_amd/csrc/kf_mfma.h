@@ -260,6 +260,7 @@ __device__ __forceinline__ int wave_max_i(int v) {
 // list[] gets t | DOC_MASK_FLAG, or plain t when the tile and the rows are one
 // and the same document.  Returns the count.  Called by one wavefront; the
 // caller publishes the count and synchronises before others read the list.
+// With list null it only counts.
 // The rows' ids and the first 64 tile ranges are loaded together, so the list
 // costs one memory round trip for up to 64 tiles.
 __device__ __forceinline__ int doc_tile_list(const int32_t* __restrict__ drow, int p_begin,
@@ -288,7 +289,7 @@ __device__ __forceinline__ int doc_tile_list(const int32_t* __restrict__ drow, i
     const uint64_t m = __builtin_amdgcn_ballot_w64(vis);
     const int below = __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
                                                 __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0));
-    if (vis && n + below < DOC_MAX_TILES)
+    if (list != nullptr && vis && n + below < DOC_MAX_TILES)
       list[n + below] = (uint16_t)(t | (whole ? 0 : DOC_MASK_FLAG));
     n += __builtin_popcountll(m);
   }

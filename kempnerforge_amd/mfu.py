@@ -165,6 +165,7 @@ def attention_kernel_flops(pairs: int, head_dim: int, backward: bool = True) -> 
 _ATTN_KEYS = ("fwd_mfma", "bwd_dkdv", "bwd_dq", "q_prep_bwd", "kv_prep", "decode_stream",
               "decode_merge", "decode_generic", "capture_probs", "fwd_generic",
               "bwd_dq_generic", "bwd_dkdv_generic", "cache_append", "append_kernel",
+              "doc_block_tiles", "order_by_count",
               "kf::attn", "flash", "fmha", "attention")
 _MATMUL_KEYS = ("gemm", "mm", "matmul", "dot", "bmm", "cublas", "nvjet", "cutlass",
                 "cijk_", "hipblaslt", "rocblas", "ck_tile", "wvsplitk")

@@ -63,10 +63,11 @@ def test_host_only_calls():
     # wavefront of the stream kernel (at most 2048) plus one per (sequence, KV head)
     assert n.value == (2048 + 32 * 8) * 4 * (128 + 2) * 4
     # backward: rotated K (per KV head) and Q (per query head) bf16 [P][D], then
-    # lse and Delta float32 [P] per query head, then the int2 tile records (V and
-    # dO are read in place)
+    # lse and Delta float32 [P] per query head, then the int2 tile records and
+    # the int32 count and order of the 128-key blocks (V and dO are read in place)
     B, S, Hq, Hkv, D, P = 4, 4096, 32, 8, 128, 4096
-    base = (B * Hkv + B * Hq) * P * D * 2 + 2 * B * Hq * P * 4 + B * (P // 64) * 8
+    base = (B * Hkv + B * Hq) * P * D * 2 + 2 * B * Hq * P * 4 + B * (P // 64) * 8 \
+        + 2 * B * (P // 128) * 4  # + the dK/dV item counts and order
     assert lib.kf_attn_bwd_workspace_size(B, S, Hq, Hkv, D, 1, ctypes.byref(n)) == 0
     assert n.value == base
     # kept dS tiles: bf16 over the causal 64-row x 32-key blocks, P * (P + 64) bytes per
