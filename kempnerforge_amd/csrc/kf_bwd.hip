@@ -949,23 +949,26 @@ __global__ __launch_bounds__(64 * HB) void bwd_dq_ds_kernel(
   }
 }
 
-// MASK_DOC: how many query tiles each (batch row, 128-key block) lists, i.e.
-// the dK/dV kernel's work per item; one wavefront per block.
-__global__ __launch_bounds__(256) void doc_block_tiles_kernel(const int32_t* __restrict__ doc,
-                                                              const int2* __restrict__ ranges,
-                                                              int S, int P, int nkb, int nblocks,
-                                                              int* __restrict__ counts) {
+// MASK_DOC: how many tiles each block of a workgroup's rows lists, i.e. the
+// work of the item it takes; one wavefront per block.  Key side (rows = keys):
+// the query tiles from the block's diagonal tile to the end; query side: the
+// key tiles from 0 to the last one the block's rows can see (causal).  ranges
+// is [B][rstride] per 64-position tile; counts[b * nblk + i] for block i.
+__global__ __launch_bounds__(256) void doc_block_tiles_kernel(
+    const int32_t* __restrict__ doc, const int2* __restrict__ ranges, int S, int rstride,
+    int rows, int nblk, int nitems, int key_side, int* __restrict__ counts) {
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int i = blockIdx.x * 4 + w;
-  if (i >= nblocks) return;
-  const int b = i / nkb, k0 = (i % nkb) * BKV;
-  const int n = doc_tile_list(doc + (int64_t)b * S, k0, min(k0 + BKV, S),
-                              ranges + (int64_t)b * (P / BN), k0 / BQ, (S + BQ - 1) / BQ,
+  if (i >= nitems) return;
+  const int b = i / nblk, p0 = (i % nblk) * rows, p1 = min(p0 + rows, S);
+  const int t0 = key_side ? p0 / BN : 0;
+  const int t1 = key_side ? (S + BN - 1) / BN : (p1 + BN - 1) / BN;
+  const int n = doc_tile_list(doc + (int64_t)b * S, p0, p1, ranges + (int64_t)b * rstride, t0, t1,
                               nullptr, lane);
   if (lane == 0) counts[i] = n;
 }
 
-// The blocks by descending count (a counting sort in one workgroup): the dK/dV
+// The blocks by descending count (a counting sort in one workgroup): the
 // workgroup of rank r takes the r-th, so the hardware's in-order dispatch
 // deals the longest items first and each XCD (every 8th rank) an equal share.
 // Ties land in any order; no result depends on which workgroup computes an item.
@@ -1005,6 +1008,21 @@ __global__ __launch_bounds__(1024) void order_by_count_kernel(const int* __restr
   __syncthreads();
   for (int i = t; i < n; i += 1024) order[atomicAdd(&hist[min(counts[i], DOC_MAX_TILES)], 1)] = i;
 }
+
+}  // namespace
+
+int launch_doc_order(const int32_t* doc, const int2* ranges, int S, int rstride, int rows, int B,
+                     int nblk, int key_side, int* counts, int* order, hipStream_t stream) {
+  const int nitems = B * nblk;
+  KF_LAUNCH("doc_block_tiles", doc_block_tiles_kernel, dim3((nitems + 3) / 4), dim3(256), 0,
+            stream, doc, ranges, S, rstride, rows, nblk, nitems, key_side, counts);
+  KF_LAUNCH("order_by_count", order_by_count_kernel, dim3(1), dim3(1024), 0, stream, counts,
+            nitems, order);
+  KF_CHECK_LAUNCH();
+  return KF_OK;
+}
+
+namespace {
 
 struct Ws {
   bf16 *krot, *qrot;
@@ -1097,11 +1115,9 @@ int launch_bwd(const BwdArgs& a, void* workspace, bool keep_ds) {
   // packed documents: the dK/dV items by their listed query tiles, most first
   const int* order = nullptr;
   if (a.doc) {
-    const int nblk = a.B * nkb;
-    KF_LAUNCH("doc_block_tiles", doc_block_tiles_kernel, dim3((nblk + 3) / 4), dim3(256), 0,
-              a.stream, a.doc, w.ranges, a.S, P, nkb, nblk, w.counts);
-    KF_LAUNCH("order_by_count", order_by_count_kernel, dim3(1), dim3(1024), 0, a.stream,
-              w.counts, nblk, w.order);
+    const int rc = launch_doc_order(a.doc, w.ranges, a.S, P / BN, BKV, a.B, nkb, 1, w.counts,
+                                    w.order, a.stream);
+    if (rc) return rc;
     order = w.order;
   }
   // persistent grids: one workgroup per CU (a multiple of 8, one share per XCD).

@@ -185,7 +185,7 @@ __global__ __launch_bounds__(256, 2) void fwd_mfma_kernel(
     const bf16* __restrict__ krot, const bf16* __restrict__ vn, bf16* __restrict__ out,
     float* __restrict__ lse, int Sq, int Sk, int Skp, int krows, int Hq, int Hkv, int n_rep,
     int bm_pos, int nqb, float scale_log2, int causal, const int32_t* __restrict__ aux,
-    const int2* __restrict__ ranges, bf16* __restrict__ qrot) {
+    const int2* __restrict__ ranges, bf16* __restrict__ qrot, const int* __restrict__ order) {
   constexpr bool DOC = MODE == MASK_DOC, KPM = MODE == MASK_KPM, LIST = DOC || KPM;
   constexpr int KS = D / 16, DT = D / 32;
   constexpr int KR = D / 8;  // 16-byte chunks per K / V row
@@ -196,7 +196,14 @@ __global__ __launch_bounds__(256, 2) void fwd_mfma_kernel(
   __shared__ int sCount, sFirst;
 
   const int tid = threadIdx.x, w = wave_id(), lane = tid & 63, hh = lane >> 5, c32 = lane & 31;
-  const int logical = xcd_logical_id(blockIdx.x, gridDim.x);
+  int logical = xcd_logical_id(blockIdx.x, gridDim.x);
+  if (order != nullptr) {
+    // DOC: the workgroup of rank r takes the (batch row, query block) of the
+    // r-th most listed key tiles, its KV heads adjacent (longest first, each
+    // XCD every 8th)
+    const int bq = order[blockIdx.x / Hkv];
+    logical = ((bq / nqb) * Hkv + (int)blockIdx.x % Hkv) * nqb + (nqb - 1 - bq % nqb);
+  }
   const RowInfo ri = row_info(logical, nqb, Hkv, n_rep, bm_pos, Sq, w * 32 + c32);
   const int bh = ri.b * Hkv + ri.g;
 
@@ -696,10 +703,13 @@ bool fwd_mfma_supported(const FwdArgs& a) {
 }
 
 // krot ([B*Hkv][Skp][D] bf16) and V^T ([B*Hkv][D][Skp] bf16), then the per-tile
-// records ([B][Skp/64] int2, written only with an explicit mask).
+// records ([B][Skp/64] int2, written only with an explicit mask), then the
+// query blocks' listed-tile counts and order (packed documents; at most Sk
+// blocks of one position per batch row).
 size_t fwd_mfma_workspace(int B, int Sk, int Hkv, int D) {
   const size_t Skp = (size_t)((Sk + BN - 1) / BN) * BN;
-  return 2 * (size_t)B * Hkv * Skp * D * sizeof(uint16_t) + (size_t)B * (Skp / BN) * sizeof(int2);
+  return 2 * (size_t)B * Hkv * Skp * D * sizeof(uint16_t) + (size_t)B * (Skp / BN) * sizeof(int2) +
+         2 * (size_t)B * Skp * sizeof(int);
 }
 
 int launch_kv_prep(const FwdArgs& a, void* krot_, int krows, void* vn_, int Skp, int2* ranges,
@@ -732,6 +742,7 @@ namespace {
 struct FwdWs {
   bf16 *krot, *vn;
   int2* ranges;
+  int *counts, *order;  // [B][Skp] each (packed documents)
   int krows;   // rows of krot per KV head
   bf16* qrot;  // a.rot's rotated Q, or null
 };
@@ -744,6 +755,8 @@ FwdWs carve_fwd(const FwdArgs& a, void* workspace, int Skp) {
   w.krot = (bf16*)workspace;
   w.vn = w.krot + (size_t)a.B * a.Hkv * Skp * a.D;
   w.ranges = (int2*)(w.vn + (size_t)a.B * a.Hkv * Skp * a.D);
+  w.counts = (int*)(w.ranges + (size_t)a.B * (Skp / BN));
+  w.order = w.counts + (size_t)a.B * Skp;
   w.krows = Skp;
   w.qrot = nullptr;
   if (a.rot != nullptr) {
@@ -758,20 +771,24 @@ int mask_mode(const FwdArgs& a) { return a.doc ? MASK_DOC : a.kvalid ? MASK_KPM 
 
 template <int D, int MODE>
 void launch_fwd_kernel(const FwdArgs& a, const FwdWs& w, int Skp, int n_rep, int bm_pos, int nqb,
-                       unsigned nblk) {
+                       unsigned nblk, const int* order) {
   KF_LAUNCH("fwd_mfma", (fwd_mfma_kernel<D, MODE>), dim3(nblk), dim3(256), 0, a.stream,
             (const bf16*)a.q, a.cos, a.sin, w.krot, w.vn, (bf16*)a.out, a.lse, a.Sq, a.Sk, Skp,
             w.krows, a.Hq, a.Hkv, n_rep, bm_pos, nqb, a.scale * kLog2e, a.causal,
-            a.doc ? a.doc : a.kvalid, w.ranges, w.qrot);
+            a.doc ? a.doc : a.kvalid, w.ranges, w.qrot, order);
 }
 
 template <int D>
 void launch_fwd_mode(const FwdArgs& a, const FwdWs& w, int Skp, int n_rep, int bm_pos, int nqb,
                      unsigned nblk) {
   switch (mask_mode(a)) {
-    case MASK_DOC: launch_fwd_kernel<D, MASK_DOC>(a, w, Skp, n_rep, bm_pos, nqb, nblk); break;
-    case MASK_KPM: launch_fwd_kernel<D, MASK_KPM>(a, w, Skp, n_rep, bm_pos, nqb, nblk); break;
-    default: launch_fwd_kernel<D, MASK_NONE>(a, w, Skp, n_rep, bm_pos, nqb, nblk);
+    case MASK_DOC:
+      launch_fwd_kernel<D, MASK_DOC>(a, w, Skp, n_rep, bm_pos, nqb, nblk, w.order);
+      break;
+    case MASK_KPM:
+      launch_fwd_kernel<D, MASK_KPM>(a, w, Skp, n_rep, bm_pos, nqb, nblk, nullptr);
+      break;
+    default: launch_fwd_kernel<D, MASK_NONE>(a, w, Skp, n_rep, bm_pos, nqb, nblk, nullptr);
   }
 }
 
@@ -810,6 +827,12 @@ int fwd_mfma(const FwdArgs& a, void* workspace) {
   const int nqb = (a.Sq + bm_pos - 1) / bm_pos;
   const int64_t nblk = (int64_t)nqb * a.B * a.Hkv;
   KF_CHECK_ARG(nblk < (1LL << 31), "grid too large");
+  if (a.doc) {
+    // the query blocks by their listed key tiles, most first
+    rc = launch_doc_order(a.doc, w.ranges, a.Sq, Skp / BN, bm_pos, a.B, nqb, 0, w.counts,
+                          w.order, a.stream);
+    if (rc) return rc;
+  }
   if (a.D == 128) launch_fwd_mode<128>(a, w, Skp, n_rep, bm_pos, nqb, (unsigned)nblk);
   else launch_fwd_mode<64>(a, w, Skp, n_rep, bm_pos, nqb, (unsigned)nblk);
   KF_CHECK_LAUNCH();

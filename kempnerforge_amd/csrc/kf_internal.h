@@ -73,6 +73,12 @@ int device_cu_count();
 // if set, is the rotated-Q buffer of FwdArgs::rot, whose rows past Sq it zeroes.
 int launch_kv_prep(const FwdArgs& a, void* krot, int krows, void* vn, int Skp, int2* ranges,
                    int v_mode, void* qpad = nullptr);
+// Packed documents: B*nblk blocks of `rows` positions ordered by how many
+// 64-position tiles each lists, most first (order[r] = block index; counts is
+// scratch of the same size).  key_side: key blocks listing query tiles from
+// their diagonal on; else query blocks listing key tiles up to theirs.
+int launch_doc_order(const int32_t* doc, const int2* ranges, int S, int rstride, int rows, int B,
+                     int nblk, int key_side, int* counts, int* order, hipStream_t stream);
 // bytes of FwdArgs::rot
 size_t rot_bytes(int B, int S, int Hq, int Hkv, int D);
 size_t fwd_mfma_workspace(int B, int Sk, int Hkv, int D);

@@ -53,8 +53,9 @@ def test_host_only_calls():
     assert lib.kf_version() >= 100
     n = _lib.size_out()
     assert lib.kf_attn_fwd_workspace_size(4, 4096, 4096, 32, 8, 128, 1, ctypes.byref(n)) == 0
-    # rotated K and V (bf16), then one int2 document range per batch row and 64-key tile
-    assert n.value == 2 * 4 * 8 * 4096 * 128 * 2 + 4 * 64 * 8
+    # rotated K and V (bf16), then one int2 document range per batch row and 64-key tile,
+    # then int32 counts and order of up to one query block per position
+    assert n.value == 2 * 4 * 8 * 4096 * 128 * 2 + 4 * 64 * 8 + 2 * 4 * 4096 * 4
     assert lib.kf_attn_fwd_workspace_size(1, 8, 8, 6, 4, 64, 1, ctypes.byref(n)) == 1
     assert b"multiple" in lib.kf_last_error()
     assert lib.kf_attn_fwd_workspace_size(1, 8, 8, 4, 4, 63, 1, ctypes.byref(n)) == 1
@@ -64,10 +65,10 @@ def test_host_only_calls():
     assert n.value == (2048 + 32 * 8) * 4 * (128 + 2) * 4
     # backward: rotated K (per KV head) and Q (per query head) bf16 [P][D], then
     # lse and Delta float32 [P] per query head, then the int2 tile records and
-    # the int32 count and order of the 128-key blocks (V and dO are read in place)
+    # the int32 counts and order of the dK/dV items (V and dO are read in place)
     B, S, Hq, Hkv, D, P = 4, 4096, 32, 8, 128, 4096
     base = (B * Hkv + B * Hq) * P * D * 2 + 2 * B * Hq * P * 4 + B * (P // 64) * 8 \
-        + 2 * B * (P // 128) * 4  # + the dK/dV item counts and order
+        + 2 * B * (P // 128) * 4  # + the dK/dV items' counts and order (packed documents)
     assert lib.kf_attn_bwd_workspace_size(B, S, Hq, Hkv, D, 1, ctypes.byref(n)) == 0
     assert n.value == base
     # kept dS tiles: bf16 over the causal 64-row x 32-key blocks, P * (P + 64) bytes per
