@@ -94,15 +94,11 @@ __global__ __launch_bounds__(256) void q_prep_bwd_kernel(
       // q and O are read once here: non-temporal loads (streaming, ~15% faster
       // from HBM than cached ones); dO stays cached for the kernels after
       const bf16* src = q + (((int64_t)b * S + s) * Hq + h) * D;
-      float x1[8], x2[8], r1[8], r2[8];
+      float x1[8], x2[8];
       unpack8(__builtin_nontemporal_load((const u32x4*)(src + 8 * c)), x1);
       unpack8(__builtin_nontemporal_load((const u32x4*)(src + 8 * c + HALF)), x2);
-      const float* cr = cos + (int64_t)s * HALF + 8 * c;
-      const float* sr = sin + (int64_t)s * HALF + 8 * c;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) rope_pair<bf16>(x1[j], x2[j], cr[j], sr[j], r1[j], r2[j]);
-      o1 = pack8(r1);
-      o2 = pack8(r2);
+      rope8_bf16(x1, x2, cos + (int64_t)s * HALF + 8 * c, sin + (int64_t)s * HALF + 8 * c, o1,
+                 o2);
     }
     bf16* dst = qrot + ((int64_t)bhq * P + s) * D;
     *(u32x4*)(dst + 8 * c) = o1;

@@ -103,6 +103,36 @@ __device__ __forceinline__ u32x4 pack8(const float* f) {
   return u;
 }
 
+// Round two floats to bf16 (round to nearest even) with one conversion, back
+// to fp32: the same bits as two round_to<bf16>.
+__device__ __forceinline__ void round2_bf16(float& x, float& y) {
+  const uint32_t p = pack2(x, y);
+  x = __uint_as_float(p << 16);
+  y = __uint_as_float(p & 0xffff0000u);
+}
+
+// rope_pair<bf16> on 8 pairs, outputs packed as bf16x8 (r1 -> o1, r2 -> o2).
+// The same bits as rope_pair<bf16> then pack8, with two roundings per
+// conversion instruction and the last rounding done by the pack itself.
+__device__ __forceinline__ void rope8_bf16(const float* x1, const float* x2, const float* cf,
+                                           const float* sf, u32x4& o1, u32x4& o2) {
+#pragma clang fp contract(off)
+  float r1[8], r2[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    float c = cf[j], s = sf[j];
+    round2_bf16(c, s);
+    float a = x1[j] * c, e = x2[j] * c;
+    round2_bf16(a, e);
+    float b = x2[j] * s, f = x1[j] * s;
+    round2_bf16(b, f);
+    r1[j] = a - b;
+    r2[j] = e + f;
+  }
+  o1 = pack8(r1);
+  o2 = pack8(r2);
+}
+
 }  // namespace kf
 
 // ---------------------------------------------------------------- host side

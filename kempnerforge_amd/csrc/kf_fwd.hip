@@ -80,15 +80,11 @@ __global__ __launch_bounds__(256) void kv_prep_kernel(
         o1 = a;
         o2 = bb;
       } else {
-        float x1[8], x2[8], r1[8], r2[8];
+        float x1[8], x2[8];
         unpack8(a, x1);
         unpack8(bb, x2);
-        const float* cr = cos + (int64_t)s * HALF + 8 * c;
-        const float* sr = sin + (int64_t)s * HALF + 8 * c;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) rope_pair<bf16>(x1[j], x2[j], cr[j], sr[j], r1[j], r2[j]);
-        o1 = pack8(r1);
-        o2 = pack8(r2);
+        rope8_bf16(x1, x2, cos + (int64_t)s * HALF + 8 * c, sin + (int64_t)s * HALF + 8 * c, o1,
+                   o2);
       }
     }
     bf16* dst = krot + ((int64_t)bh * krows + s) * D;
@@ -157,13 +153,13 @@ __device__ __forceinline__ void load_q_frag(const bf16* __restrict__ q,
 #pragma unroll
   for (int ks = 0; ks < KS / 2; ++ks) {
     const int d0 = 16 * ks + 8 * hh;
-    float x1[8], x2[8], r1[8], r2[8];
+    float x1[8], x2[8];
     unpack8(*(const u32x4*)(qrow + d0), x1);
     unpack8(*(const u32x4*)(qrow + d0 + HALF), x2);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) rope_pair<bf16>(x1[j], x2[j], cr[d0 + j], sr[d0 + j], r1[j], r2[j]);
-    qf[ks] = as_bf16x8(pack8(r1));
-    qf[ks + KS / 2] = as_bf16x8(pack8(r2));
+    u32x4 o1, o2;
+    rope8_bf16(x1, x2, cr + d0, sr + d0, o1, o2);
+    qf[ks] = as_bf16x8(o1);
+    qf[ks + KS / 2] = as_bf16x8(o2);
   }
 }
 
