@@ -34,6 +34,10 @@ namespace {
 
 using namespace mfma;
 
+// how far (log2 units) a row's max may outgrow the forward's exponent base
+// before the running output is rescaled
+constexpr float RESCALE_SLACK = 8.f;
+
 template <int D>
 __global__ __launch_bounds__(256) void kv_prep_kernel(
     const bf16* __restrict__ k, const bf16* __restrict__ v, const float* __restrict__ cos,
@@ -337,11 +341,13 @@ __global__ __launch_bounds__(256, 2) void fwd_mfma_kernel(
 #pragma unroll
       for (int i = 0; i < 16; ++i) tmax = fmaxf(tmax, s[mt][i]);
     tmax = pair_max32(tmax) * scale_log2;
-    // Rescale the running output only when some row's max grew: the exponent
-    // base m may lag the true max (exp2 arguments stay <= 0 either way, since
-    // m >= every score seen so far), and rows whose max did not move keep
+    // Rescale the running output only when some row's max grew by more than
+    // RESCALE_SLACK (log2 units): until then the exponent base m lags the
+    // row's max by at most that much, so p <= 2^RESCALE_SLACK, well inside
+    // bf16 and fp32 range with their precision unchanged (O / l and the LSE
+    // m + log2(l) are exact for any base).  Rows whose max did not move keep
     // alpha = 1.  The branch is wavefront-uniform.
-    if (__builtin_amdgcn_ballot_w64(tmax > m) != 0) {
+    if (__builtin_amdgcn_ballot_w64(tmax > m + RESCALE_SLACK) != 0) {
       const float mnew = fmaxf(m, tmax);
       const float alpha = fast_exp2(m - mnew);
       lsum *= alpha;
