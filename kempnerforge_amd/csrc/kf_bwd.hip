@@ -854,24 +854,27 @@ __global__ __launch_bounds__(64 * HB) void bwd_dq_ds_kernel(
       dma16(lds_addr(st[buf].k + j * 512), off, kbase);
     }
     // this wavefront's record (read once: streaming loads), 4 x 1 KB of 64
-    // 16-byte B-operand pieces; lane i of an LDS copy takes piece i ^ 4*(i >> 5),
-    // so that the two 32-lane halves a transposed read combines sit in
-    // different bank halves
+    // 16-byte B-operand pieces; lane i of LDS copy j takes piece
+    // (i ^ 8 (j & 1)) ^ 4 (i >> 5): the 4 (i >> 5) term puts the two 16-lane
+    // groups of a transposed read's pass that share a copy in different halves
+    // of a 256-byte bank window, the 8 (j & 1) term (128 bytes) does the same
+    // for the two groups that read copies j and j + 1
     const u32x4* src = rec0 + ((int64_t)t * n_rep + w) * 256;
 #pragma unroll
     for (int j = 0; j < 4; ++j)
       dma16_nt(lds_addr(st[buf].ds + w * 256 + j * 64),
-               (uint32_t)((j * 64 + (lane ^ ((lane >> 5) << 2))) * 16), src);
+               (uint32_t)((j * 64 + ((lane ^ (8 * (j & 1))) ^ ((lane >> 5) << 2))) * 16), src);
   };
 
   // transposed-read address of this lane inside its record (row block mh adds
-  // 2048 bytes, key chunk c 256, the second read of a chunk 128): address-lane
-  // 4e + k of group G fetches rows 16(G&1) + 4k .. +3 of key 4(G>>1) + e
+  // 2048 bytes, key chunk c 256, the second read of a chunk 128, which the odd
+  // copies hold 128 bytes lower): address-lane 4e + k of group G fetches rows
+  // 16(G&1) + 4k .. +3 of key 4(G>>1) + e
   uint32_t ds_off;
   {
     const int G = lane >> 4, a = lane & 15, e = a >> 2, k = a & 3;
     const int piece = 32 * (k & 1) + 4 * ((G >> 1) ^ (k & 1)) + e;
-    ds_off = (uint32_t)(w * 4096 + (G & 1) * 1024 + piece * 16 + 8 * (k >> 1));
+    ds_off = (uint32_t)(w * 4096 + (G & 1) * (1024 + 128) + piece * 16 + 8 * (k >> 1));
   }
   const TrOffsets<D> tro = tr_offsets<D>(lane);
   f32x16 acc[2][DT];
@@ -898,14 +901,15 @@ __global__ __launch_bounds__(64 * HB) void bwd_dq_ds_kernel(
     if (t + NBUF - 1 < nk) stage(t + NBUF - 1, (t + NBUF - 1) % NBUF);
     const Stage& S_ = st[t % NBUF];
     const char* dsl = (const char*)S_.ds + ds_off;
+    const char* dsh = (const char*)S_.ds + (ds_off ^ 128u);
 #pragma unroll
     for (int c = 0; c < DSK / 16; ++c) {
       bf16x8 bds[2];
 #pragma unroll
       for (int mh = 0; mh < 2; ++mh) {
-        const char* p = dsl + 2048 * mh + 256 * c;
-        const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)p);
-        const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)(p + 128));
+        const int o = 2048 * mh + 256 * c;
+        const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)(dsl + o));
+        const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)(dsh + o));
         bds[mh] = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5,
                                                                      6, 7));
       }

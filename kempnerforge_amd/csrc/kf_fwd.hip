@@ -122,20 +122,44 @@ __global__ __launch_bounds__(256) void kv_prep_kernel(
   // key order of a P^T fragment built from the 32x32 C layout (lane half h holds
   // keys 4h..4h+3 and 8+4h..8+4h+3 of each 16), so one 16-byte read of a V^T row
   // is a complete A fragment of O^T += V^T P^T.
-  for (int it = tid; it < BN * (D / 8); it += 256) {
-    const int key = it / (D / 8), c = it % (D / 8);
-    const int s = s0 + key;
-    u32x4 a = {0u, 0u, 0u, 0u};
-    if (s < Sk) a = *(const u32x4*)(v + b * vsb + (int64_t)s * vss + g * vsh + 8 * c);
-    const int slot = (key & ~12) | ((key & 4) << 1) | ((key & 8) >> 1);
-    const bf16* e = (const bf16*)&a;
+  //
+  // The transpose goes through LDS as [d][key slot] rows of 128 bytes.  A lane
+  // takes two adjacent keys (adjacent slots) of one 16-byte d chunk c and
+  // writes 8 packed dwords, rows 8c..8c+7; a wavefront covers 16 key pairs x
+  // 4 chunks.  Odd chunks walk their rows in pair-swapped order (row 8c + (jj ^
+  // 1) at step jj), so each store has both row parities in flight (the two
+  // 128-byte halves of a 256-byte bank window), and rows 16..31 of every 32
+  // hold their 16-byte slot chunks at index ^ 4: the 64 lanes of a store meet
+  // 64 distinct banks.  The 16-byte reads undo the chunk swizzle.
+  constexpr int CH = D / 32;  // 4-chunk groups of a key row
+  for (int it = tid; it < (BN / 2) * (D / 8); it += 256) {
+    const int rest = it >> 6;
+    const int c = 4 * (rest % CH) + (it & 3);
+    const int kp = 16 * (rest / CH) + ((it >> 2) & 15);
+    const int s = s0 + 2 * kp;
+    const bf16* src = v + b * vsb + (int64_t)s * vss + g * vsh + 8 * c;
+    u32x4 a = {0u, 0u, 0u, 0u}, a2 = {0u, 0u, 0u, 0u};
+    if (s < Sk) a = *(const u32x4*)src;
+    if (s + 1 < Sk) a2 = *(const u32x4*)(src + vss);
+    uint32_t wd[8];  // (key 2kp, key 2kp + 1) of d = 8c + j
 #pragma unroll
-    for (int j = 0; j < 8; ++j) sVt[(8 * c + j) * BN + slot] = e[j];
+    for (int i = 0; i < 4; ++i) {
+      wd[2 * i] = (a[i] & 0xffffu) | (a2[i] << 16);
+      wd[2 * i + 1] = (a[i] >> 16) | (a2[i] & 0xffff0000u);
+    }
+    const int key = 2 * kp;
+    const int slot = (key & ~12) | ((key & 4) << 1) | ((key & 8) >> 1);
+    const int col = slot ^ (32 * ((c >> 1) & 1));
+    const int flip = c & 1;
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj)
+      *(uint32_t*)&sVt[(8 * c + (jj ^ flip)) * BN + col] = flip ? wd[jj ^ 1] : wd[jj];
   }
   __syncthreads();
   for (int it = tid; it < D * (BN / 8); it += 256) {
     const int d = it / (BN / 8), c = it % (BN / 8);
-    *(u32x4*)(vn + ((int64_t)bh * D + d) * Skp + s0 + 8 * c) = *(const u32x4*)&sVt[d * BN + 8 * c];
+    const int pc = c ^ (4 * ((d >> 4) & 1));
+    *(u32x4*)(vn + ((int64_t)bh * D + d) * Skp + s0 + 8 * c) = *(const u32x4*)&sVt[d * BN + 8 * pc];
   }
 }
 

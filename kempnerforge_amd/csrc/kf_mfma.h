@@ -66,15 +66,27 @@ __device__ __forceinline__ RowInfo row_info(int logical, int nqb, int Hkv, int n
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
 // LDS tiles are stored unpadded, [rows][R] 16-byte chunks (R = 8 or 16), with
-// chunk c of row r at position c ^ swz<R>(r).  swz spreads the rows of a
-// fragment read over distinct 16-byte bank groups for both access patterns the
-// kernels use: ds_read_b128 with one row per lane (measured at the LDS peak of
-// ~128 B/clk/CU on MI355X) and ds_read_b64_tr_b16 with 4 rows x 32 bytes per
-// 16-lane group (~100 B/clk/CU; the plain c ^ (r % R) swizzle reaches only ~58
-// there).
+// chunk c of row r at position c ^ swz<R>(r).  gfx950's LDS has 64 banks of 4
+// bytes; ds_read_b128 serves a wavefront in 4 passes of 16 lanes and the 8-byte
+// reads (ds_read_b64, ds_read_b64_tr_b16) in 2 passes of 32 lanes, each pass
+// 256 bytes wide, and two lanes of a pass that touch different words of one
+// bank cost a cycle more.  swz makes every pass of the three read patterns the
+// kernels use touch 256 distinct bytes modulo 256:
+//  - ds_read_b128, one row per lane, 16 consecutive rows per pass, same chunk:
+//    the positions (r % 2, c ^ swz) (R = 8) or c ^ swz (R = 16) must differ;
+//  - ds_read_b64_tr_b16 of the backward (lds_frag_t): rows 4k..4k+3 per pass,
+//    4 chunks 4j..4j+3 each, so swz >> 2 (R = 16) or bit 2 of swz between rows
+//    of one parity (R = 8) must differ;
+//  - the decode's transposed V read: rows 8k..8k+7 per pass, chunk pairs
+//    2j, 2j+1, so swz >> 1 must differ over the rows (of one parity for R = 8).
+// Both forms are bit permutations of row % 16 that satisfy all three
+// (measured: 0 bank-conflict cycles per instruction for each pattern, where
+// the previous (r % 8, r / 8) interleave cost 4 per ds_read_b128 on 128-byte
+// rows and 2 per transposed read on 256-byte rows).
 template <int R>
 __device__ __forceinline__ int swz(int row) {
-  return R == 16 ? (((row & 7) << 1) | ((row >> 3) & 1)) : (((row & 3) << 1) | ((row >> 2) & 1));
+  return R == 16 ? (((row & 3) << 2) | ((row >> 1) & 2) | ((row >> 3) & 1))
+                 : (((row << 1) & 4) | ((row >> 1) & 2) | ((row >> 3) & 1));
 }
 
 template <int R>
