@@ -104,8 +104,9 @@ __global__ __launch_bounds__(256) void q_prep_bwd_kernel(
     *(u32x4*)(dst + 8 * c) = o1;
     *(u32x4*)(dst + 8 * c + HALF) = o2;
   }
-  // Delta (TPR consecutive lanes own one row); dO itself is read in place by
-  // the dK/dV and dQ kernels
+  // -Delta (TPR consecutive lanes own one row; stored negated so that the dK/dV
+  // kernel can start its dP accumulation from it); dO itself is read in place
+  // by the dK/dV and dQ kernels
   // all of a thread's dO and O loads are issued before the first reduction
   constexpr int NIT = BN * TPR / 256;
   u32x4 ad[NIT], ao[NIT];
@@ -132,7 +133,7 @@ __global__ __launch_bounds__(256) void q_prep_bwd_kernel(
 #pragma unroll
     for (int o = 1; o < TPR; o <<= 1) part += __shfl_xor(part, o, 64);
     if (c == 0) {
-      delta[(int64_t)bhq * P + s] = part;
+      delta[(int64_t)bhq * P + s] = -part;
       lse2[(int64_t)bhq * P + s] = s < S ? lse[(int64_t)bhq * S + s] * kLog2e : INFINITY;
     }
   }
@@ -148,7 +149,7 @@ __global__ __launch_bounds__(256) void q_prep_bwd_kernel(
 template <int D>
 struct DkdvStage {
   bf16 q[BQ * D], o[BQ * D];
-  float l[BQ], dl[BQ];
+  float l[BQ], dl[BQ];  // lse · log2(e) and -Delta of the tile's rows
 };
 
 // MASK_DOC: qlist[0, nlist) holds the listed query tiles (DOC_MASK_FLAG: needs
@@ -255,22 +256,34 @@ __device__ __forceinline__ void dkdv_role(
     const bool diag = causal && q0 < k0 + BKV;
     const bool dmask = LIST && (e & DOC_MASK_FLAG);
 
-    // this lane's 32 rows' log-sum-exp (P waves) or Delta (dS waves), read
+    // this lane's 32 rows' log-sum-exp (P waves) or -Delta (dS waves), read
     // before the phase-1 products so the reads complete under them: read at
-    // the point of use they queue behind the fragment reads of the other role
-    f32x4 rowv[8];
+    // the point of use they queue behind the fragment reads of the other role.
+    // Element 4 gq + j of half mt is row 32 mt + 8 gq + 4 hh + j, the row of
+    // the C-layout element x[mt][4 gq + j].
+    f32x16 rowv[2];
     {
       const float* src = DSROLE ? S_.dl : S_.l;
 #pragma unroll
-      for (int r = 0; r < 8; ++r) rowv[r] = *(const f32x4*)(&src[8 * r + 4 * hh]);
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int gq = 0; gq < 4; ++gq) {
+          const f32x4 r4 = *(const f32x4*)(&src[32 * mt + 8 * gq + 4 * hh]);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) rowv[mt][4 * gq + j] = r4[j];
+        }
     }
 
-    // phase 1: S (P waves) or dP (dS waves) for both 32-row halves
+    // phase 1: S (P waves) or dP - Delta (dS waves: the accumulation starts
+    // from -Delta) for both 32-row halves
     f32x16 x[2];
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) {
+      if (DSROLE)
+        x[mt] = rowv[mt];
+      else
 #pragma unroll
-      for (int i = 0; i < 16; ++i) x[mt][i] = 0.f;
+        for (int i = 0; i < 16; ++i) x[mt][i] = 0.f;
       const bf16* tA = first_tile(S_);
       bf16x8 fa[KS];
 #pragma unroll
@@ -293,11 +306,10 @@ __device__ __forceinline__ void dkdv_role(
 #pragma unroll
           for (int gq = 0; gq < 4; ++gq) {
             const int r0 = 32 * mt + 8 * gq + 4 * hh;
-            const f32x4 l4 = rowv[4 * mt + gq];
             float v[4];
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-              float p = fast_exp2(__builtin_fmaf(x[mt][4 * gq + j], scale_log2, -l4[j]));
+              float p = fast_exp2(__builtin_fmaf(x[mt][4 * gq + j], scale_log2, -rowv[mt][4 * gq + j]));
               if (decltype(masked)::value) p = (rel > r0 + j) ? 0.f : p;
               v[j] = p;
             }
@@ -336,14 +348,8 @@ __device__ __forceinline__ void dkdv_role(
       asm volatile("" : "+s"(rec));
     }
     if (DSROLE) {
-      // dP - Delta and the first dK fragments while P is still on its way:
-      // only the product with P is left between the barrier and the dK products
-#pragma unroll
-      for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-        for (int gq = 0; gq < 4; ++gq)
-#pragma unroll
-          for (int j = 0; j < 4; ++j) x[mt][4 * gq + j] -= rowv[4 * mt + gq][j];
+      // the first dK fragments while P is still on its way: only the product
+      // with P is left between the barrier and the dK products
       asm volatile("" : "+v"(x[0]), "+v"(x[1]));
 #pragma unroll
       for (int n = 0; n < PF; ++n) fpre[n] = lds_frag_t<D>(second_tile(S_), tro, n / DT, n % DT);
@@ -628,7 +634,7 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_kernel(
     if (KPM && ntiles > 0) stage(tile_of(entry(0)), 0);
 
     bf16x8 qf[KS], df[KS];
-    float l2 = INFINITY, dl = 0.f;
+    float l2 = INFINITY, ndl = 0.f;  // ndl: -Delta of this lane's row
     if (ri.q_valid) {
       const bf16* qr = qrot + (bhq * P + ri.pos) * D + 8 * hh;
       const bf16* dr = dout + (((int64_t)ri.b * S + ri.pos) * Hq + ri.hq) * D + 8 * hh;
@@ -638,7 +644,7 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_kernel(
         df[ks] = as_bf16x8(*(const u32x4*)(dr + 16 * ks));
       }
       l2 = lse2[bhq * P + ri.pos];
-      dl = delta[bhq * P + ri.pos];
+      ndl = delta[bhq * P + ri.pos];
     } else {
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
@@ -662,7 +668,7 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_kernel(
       settle(df[ks]);
     }
     settle(l2);
-    settle(dl);
+    settle(ndl);
     for (int it = 0; it < ntiles; ++it) {
       const int buf = it & 1;
       const int e = entry(it);
@@ -723,7 +729,7 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_kernel(
               if (DOC && dmask) p = kd[j] != di ? 0.f : p;
               if (KPM && dmask && !grd) p = kd[j] == 0 ? 0.f : p;
             }
-            dsv[j] = p * (dp[i + j] - dl);
+            dsv[j] = p * (dp[i + j] + ndl);
           }
           dsk[i >> 3][(i & 7) >> 1] = pack2(dsv[0], dsv[1]);
         }
@@ -1026,7 +1032,7 @@ namespace {
 
 struct Ws {
   bf16 *krot, *qrot;
-  float *lse2, *delta;
+  float *lse2, *delta;  // delta holds -Delta (q_prep_bwd)
   int2* ranges;  // [B][P/64] document-id range per tile (packed documents only)
   int *counts, *order;  // [B][P/128] each: dK/dV item work and order (packed documents)
   u32x4* dsb;    // dS records (when kept)
