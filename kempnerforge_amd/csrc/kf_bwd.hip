@@ -82,7 +82,7 @@ __global__ __launch_bounds__(256) void q_prep_bwd_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ out, const bf16* __restrict__ dout,
     const float* __restrict__ lse, const float* __restrict__ cos, const float* __restrict__ sin,
     bf16* __restrict__ qrot, float* __restrict__ lse2, float* __restrict__ delta, int S, int P,
-    int Hq) {
+    int Hq, float inv_scale) {
   constexpr int HALF = D / 2, CP = HALF / 8, TPR = D / 8;
   const int s0 = blockIdx.x * BN, bhq = blockIdx.y, b = bhq / Hq, h = bhq % Hq;
   const int tid = threadIdx.x;
@@ -134,7 +134,9 @@ __global__ __launch_bounds__(256) void q_prep_bwd_kernel(
     for (int o = 1; o < TPR; o <<= 1) part += __shfl_xor(part, o, 64);
     if (c == 0) {
       delta[(int64_t)bhq * P + s] = -part;
-      lse2[(int64_t)bhq * P + s] = s < S ? lse[(int64_t)bhq * S + s] * kLog2e : INFINITY;
+      // -lse / scale: the dK/dV kernel starts its S accumulation from it, so
+      // that P = exp2(scale log2(e) x) (rows past S: -inf, P = 0)
+      lse2[(int64_t)bhq * P + s] = s < S ? -lse[(int64_t)bhq * S + s] * inv_scale : -INFINITY;
     }
   }
 }
@@ -149,7 +151,7 @@ __global__ __launch_bounds__(256) void q_prep_bwd_kernel(
 template <int D>
 struct DkdvStage {
   bf16 q[BQ * D], o[BQ * D];
-  float l[BQ], dl[BQ];  // lse · log2(e) and -Delta of the tile's rows
+  float l[BQ], dl[BQ];  // -lse / scale and -Delta of the tile's rows
 };
 
 // MASK_DOC: qlist[0, nlist) holds the listed query tiles (DOC_MASK_FLAG: needs
@@ -256,11 +258,11 @@ __device__ __forceinline__ void dkdv_role(
     const bool diag = causal && q0 < k0 + BKV;
     const bool dmask = LIST && (e & DOC_MASK_FLAG);
 
-    // this lane's 32 rows' log-sum-exp (P waves) or -Delta (dS waves), read
-    // before the phase-1 products so the reads complete under them: read at
-    // the point of use they queue behind the fragment reads of the other role.
-    // Element 4 gq + j of half mt is row 32 mt + 8 gq + 4 hh + j, the row of
-    // the C-layout element x[mt][4 gq + j].
+    // this lane's 32 rows' -lse / scale (P waves) or -Delta (dS waves), the
+    // start of the phase-1 accumulation (the first MFMA's C operand, so the
+    // registers are free for the rest of the tile).  Element 4 gq + j of half
+    // mt is row 32 mt + 8 gq + 4 hh + j, the row of the C-layout element
+    // x[mt][4 gq + j].
     f32x16 rowv[2];
     {
       const float* src = DSROLE ? S_.dl : S_.l;
@@ -274,16 +276,12 @@ __device__ __forceinline__ void dkdv_role(
         }
     }
 
-    // phase 1: S (P waves) or dP - Delta (dS waves: the accumulation starts
-    // from -Delta) for both 32-row halves
+    // phase 1: S - lse / scale (P waves) or dP - Delta (dS waves) for both
+    // 32-row halves
     f32x16 x[2];
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) {
-      if (DSROLE)
-        x[mt] = rowv[mt];
-      else
-#pragma unroll
-        for (int i = 0; i < 16; ++i) x[mt][i] = 0.f;
+      x[mt] = rowv[mt];
       const bf16* tA = first_tile(S_);
       bf16x8 fa[KS];
 #pragma unroll
@@ -309,7 +307,7 @@ __device__ __forceinline__ void dkdv_role(
             float v[4];
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-              float p = fast_exp2(__builtin_fmaf(x[mt][4 * gq + j], scale_log2, -rowv[mt][4 * gq + j]));
+              float p = fast_exp2(x[mt][4 * gq + j] * scale_log2);
               if (decltype(masked)::value) p = (rel > r0 + j) ? 0.f : p;
               v[j] = p;
             }
@@ -643,7 +641,7 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_kernel(
         qf[ks] = as_bf16x8(*(const u32x4*)(qr + 16 * ks));
         df[ks] = as_bf16x8(*(const u32x4*)(dr + 16 * ks));
       }
-      l2 = lse2[bhq * P + ri.pos];
+      l2 = -lse2[bhq * P + ri.pos] * scale_log2;  // lse log2(e) from -lse / scale
       ndl = delta[bhq * P + ri.pos];
     } else {
 #pragma unroll
@@ -1032,7 +1030,7 @@ namespace {
 
 struct Ws {
   bf16 *krot, *qrot;
-  float *lse2, *delta;  // delta holds -Delta (q_prep_bwd)
+  float *lse2, *delta;  // -lse / scale and -Delta (q_prep_bwd)
   int2* ranges;  // [B][P/64] document-id range per tile (packed documents only)
   int *counts, *order;  // [B][P/128] each: dK/dV item work and order (packed documents)
   u32x4* dsb;    // dS records (when kept)
@@ -1115,7 +1113,7 @@ int launch_bwd(const BwdArgs& a, void* workspace, bool keep_ds) {
   }
   KF_LAUNCH("q_prep_bwd", q_prep_bwd_kernel<D>, dim3(P / BN, a.B * a.Hq), dim3(256), 0, a.stream,
             a.rot ? nullptr : (const bf16*)a.q, (const bf16*)a.out, (const bf16*)a.dout, a.lse, a.cos, a.sin,
-            w.qrot, w.lse2, w.delta, a.S, P, a.Hq);
+            w.qrot, w.lse2, w.delta, a.S, P, a.Hq, 1.f / a.scale);
   KF_CHECK_LAUNCH();
   const int nkb = P / BKV;
   // packed documents: the dK/dV items by their listed query tiles, most first
