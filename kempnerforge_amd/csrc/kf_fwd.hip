@@ -448,6 +448,162 @@ __global__ __launch_bounds__(256, 2) void fwd_mfma_kernel(
   }
 }
 
+// Forward without an explicit mask on 32-key tiles: half the LDS (32 KB per
+// workgroup, K and V^T double-buffered) and half the score registers of
+// fwd_mfma_kernel, so that three workgroups share a CU (three wavefronts per
+// SIMD to hide each one's MFMA -> softmax -> MFMA dependencies; measured on
+// the loop's skeleton: 1779 against 1444 TFLOP/s for two workgroups of
+// 64-key tiles).  Same rows per workgroup and the same per-key arithmetic as
+// fwd_mfma_kernel; the running max is taken per 32-key tile, so the points
+// where the output is rescaled (and with them the last bits) can differ.
+constexpr int FBN = 32;  // keys per tile of fwd32_kernel
+template <int D>
+__global__ __launch_bounds__(256, 3) void fwd32_kernel(
+    const bf16* __restrict__ q, const float* __restrict__ cos, const float* __restrict__ sin,
+    const bf16* __restrict__ krot, const bf16* __restrict__ vn, bf16* __restrict__ out,
+    float* __restrict__ lse, int Sq, int Sk, int Skp, int krows, int Hq, int Hkv, int n_rep,
+    int bm_pos, int nqb, float scale_log2, int causal, bf16* __restrict__ qrot) {
+  constexpr int KS = D / 16, DT = D / 32;
+  constexpr int KR = D / 8;  // 16-byte chunks per K row
+  __shared__ __attribute__((aligned(16))) bf16 sK[2][FBN * D];
+  __shared__ __attribute__((aligned(16))) bf16 sV[2][D * FBN];
+
+  const int tid = threadIdx.x, w = wave_id(), lane = tid & 63, hh = lane >> 5, c32 = lane & 31;
+  const int logical = xcd_logical_id(blockIdx.x, gridDim.x);
+  const RowInfo ri = row_info(logical, nqb, Hkv, n_rep, bm_pos, Sq, w * 32 + c32);
+  const int bh = ri.b * Hkv + ri.g;
+  const int kend = causal ? min(Sk, min(ri.p0 + bm_pos, Sq)) : Sk;
+  const int ntiles = (kend + FBN - 1) / FBN;
+  const bf16* kbase = krot + (int64_t)bh * krows * D;
+  const bf16* vbase = vn + (int64_t)bh * D * Skp;  // V^T, keys in fragment order
+  auto stage = [&](int t, int buf) {
+    tile_to_lds<FBN, KR>(kbase + (int64_t)t * FBN * D, D, sK[buf], w, lane);
+    tile_to_lds<D, FBN / 8>(vbase + (int64_t)t * FBN, Skp, sV[buf], w, lane);
+  };
+  if (ntiles > 0) stage(0, 0);
+
+  bf16x8 qf[KS];
+  load_q_frag<D>(q, cos, sin, ri, Sq, Hq, hh, qf);
+  if (qrot != nullptr && ri.q_valid) {
+    // the rotated q row for the backward (read there long after: streaming stores)
+    bf16* dst = qrot + (((int64_t)ri.b * Hq + ri.hq) * krows + ri.pos) * D + 8 * hh;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+      __builtin_nontemporal_store(__builtin_bit_cast(u32x4, qf[ks]),
+                                  (u32x4*)(dst + (ks < KS / 2 ? 16 * ks : D / 2 + 16 * (ks - KS / 2))));
+  }
+
+  float m = -INFINITY, lsum = 0.f;
+  f32x16 acc[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[dt][i] = 0.f;
+
+  lds_copy_wait();
+  __syncthreads();
+  auto tile_body = [&](int it, auto bufc) {
+    constexpr int buf = decltype(bufc)::value;
+    if (it + 1 < ntiles) stage(it + 1, buf ^ 1);
+    const bf16* tK = sK[buf];
+    const bf16* tV = sV[buf];
+
+    // S^T of the tile's 32 keys x this wavefront's 32 rows
+    f32x16 s;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) s[i] = 0.f;
+    {
+      auto kfrag = [&](int j) { return lds_frag<KR>(tK, c32, 2 * j + hh); };
+      bf16x8 fa[KS];
+#pragma unroll
+      for (int j = 0; j < FWD_PF; ++j) fa[j] = kfrag(j);
+#pragma unroll
+      for (int j = 0; j < KS; ++j) {
+        __builtin_amdgcn_sched_barrier(0);
+        if (j + FWD_PF < KS) fa[j + FWD_PF] = kfrag(j + FWD_PF);
+        s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[j], qf[j], s, 0, 0, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+
+    const int k0 = it * FBN;
+    if ((causal && k0 + FBN - 1 > ri.p0) || (k0 + FBN > Sk)) {
+      // last visible key of this lane's row, relative to k0 (branch-free select)
+      const int lim = (causal ? min(ri.pos, Sk - 1) : Sk - 1) - k0;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int local = 8 * (i >> 2) + 4 * hh + (i & 3);
+        s[i] = local > lim ? -INFINITY : s[i];
+      }
+    }
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) tmax = fmaxf(tmax, s[i]);
+    tmax = pair_max32(tmax) * scale_log2;
+    if (__builtin_amdgcn_ballot_w64(tmax > m + RESCALE_SLACK) != 0) {
+      const float mnew = fmaxf(m, tmax);
+      const float alpha = fast_exp2(m - mnew);
+      lsum *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[dt][i] *= alpha;
+      m = mnew;
+    }
+    float psum = 0.f;
+    u32x4 pk[2];
+#pragma unroll
+    for (int i = 0; i < 16; i += 2) {
+      const float p0 = fast_exp2(__builtin_fmaf(s[i], scale_log2, -m));
+      const float p1 = fast_exp2(__builtin_fmaf(s[i + 1], scale_log2, -m));
+      psum += p0 + p1;
+      pk[i >> 3][(i & 7) >> 1] = pack2(p0, p1);
+    }
+    lsum += psum;
+    {
+      constexpr int NV = 2 * DT;
+      auto vfrag = [&](int j) {
+        return lds_frag<FBN / 8>(tV, 32 * (j % DT) + c32, 2 * (j / DT) + hh);
+      };
+      bf16x8 fb[NV];
+#pragma unroll
+      for (int j = 0; j < FWD_PF; ++j) fb[j] = vfrag(j);
+#pragma unroll
+      for (int j = 0; j < NV; ++j) {
+        __builtin_amdgcn_sched_barrier(0);
+        if (j + FWD_PF < NV) fb[j + FWD_PF] = vfrag(j + FWD_PF);
+        acc[j % DT] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[j], as_bf16x8(pk[j / DT]),
+                                                             acc[j % DT], 0, 0, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    lds_copy_wait();
+    __syncthreads();
+  };
+  for (int it = 0; it < ntiles; it += 2) {
+    tile_body(it, std::integral_constant<int, 0>{});
+    if (it + 1 < ntiles) tile_body(it + 1, std::integral_constant<int, 1>{});
+  }
+
+  const float ltot = pair_sum32(lsum);
+  const float inv = 1.f / ltot;
+  if (ri.q_valid) {
+    bf16* orow = out + (((int64_t)ri.b * Sq + ri.pos) * Hq + ri.hq) * D;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int gi = 0; gi < 4; ++gi) {
+        const int d = 32 * dt + 8 * gi + 4 * hh;
+        u32x2 pk2;
+        pk2[0] = pack2(acc[dt][4 * gi] * inv, acc[dt][4 * gi + 1] * inv);
+        pk2[1] = pack2(acc[dt][4 * gi + 2] * inv, acc[dt][4 * gi + 3] * inv);
+        *(u32x2*)(orow + d) = pk2;
+      }
+    if (lse != nullptr && hh == 0)
+      lse[((int64_t)ri.b * Hq + ri.hq) * Sq + ri.pos] = (m + log2f(ltot)) * kLn2;
+  }
+}
+
 // Capture: LSE, the probabilities P = exp(s - lse) as float32 [B, Hq, Sq, Sk]
 // and out = P·V in one launch per (query block, KV head).  The workgroup walks
 // its key tiles twice in the forward's S^T = K·Q^T layout (a lane holds one
@@ -833,7 +989,10 @@ void launch_fwd_mode(const FwdArgs& a, const FwdWs& w, int Skp, int n_rep, int b
     case MASK_KPM:
       launch_fwd_kernel<D, MASK_KPM>(a, w, Skp, n_rep, bm_pos, nqb, nblk, nullptr);
       break;
-    default: launch_fwd_kernel<D, MASK_NONE>(a, w, Skp, n_rep, bm_pos, nqb, nblk, nullptr);
+    default:
+      KF_LAUNCH("fwd_mfma", fwd32_kernel<D>, dim3(nblk), dim3(256), 0, a.stream, (const bf16*)a.q,
+                a.cos, a.sin, w.krot, w.vn, (bf16*)a.out, a.lse, a.Sq, a.Sk, Skp, w.krows, a.Hq,
+                a.Hkv, n_rep, bm_pos, nqb, a.scale * kLog2e, a.causal, w.qrot);
   }
 }
 

@@ -83,10 +83,14 @@ typedef __attribute__((address_space(3))) void* lds_ptr_t;
 // (measured: 0 bank-conflict cycles per instruction for each pattern, where
 // the previous (r % 8, r / 8) interleave cost 4 per ds_read_b128 on 128-byte
 // rows and 2 per transposed read on 256-byte rows).
+// R = 4 (64-byte rows, only read one row per lane with ds_read_b128): the row's
+// 4-row group index, so 16 consecutive rows of one chunk meet 16 distinct
+// 16-byte slots of a 256-byte window.
 template <int R>
 __device__ __forceinline__ int swz(int row) {
-  return R == 16 ? (((row & 3) << 2) | ((row >> 1) & 2) | ((row >> 3) & 1))
-                 : (((row << 1) & 4) | ((row >> 1) & 2) | ((row >> 3) & 1));
+  return R == 16  ? (((row & 3) << 2) | ((row >> 1) & 2) | ((row >> 3) & 1))
+         : R == 8 ? (((row << 1) & 4) | ((row >> 1) & 2) | ((row >> 3) & 1))
+                  : ((row >> 2) & 3);
 }
 
 template <int R>
