@@ -441,12 +441,13 @@ def run_full(args, torch, wl):
 # --------------------------------------------------------------------------- rocprof summary
 def _short(name: str) -> str:
     """Kernel symbol -> the launcher's name (kf::..._kernel<...> -> ...)."""
-    m = re.search(r"(kv_prep|fwd_mfma|q_prep_bwd|bwd_dkdv|bwd_dq_ds|bwd_dq|decode_stream|"
+    m = re.search(r"(kv_prep|fwd_mfma|fwd32|q_prep_bwd|bwd_dkdv|bwd_dq_ds|bwd_dq|decode_stream|"
                   r"decode_merge|capture_probs_mfma|kv_append|append|doc_block_tiles|"
                   r"order_by_count)_kernel", name)
     if m:
-        return {"capture_probs_mfma": "capture_probs", "append": "kv_append"}.get(m.group(1),
-                                                                                 m.group(1))
+        # fwd32_kernel is the unmasked forward's kernel, launched as fwd_mfma
+        return {"capture_probs_mfma": "capture_probs", "append": "kv_append",
+                "fwd32": "fwd_mfma"}.get(m.group(1), m.group(1))
     return "copy" if "copyBuffer" in name else name[:40]
 
 
