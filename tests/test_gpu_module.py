@@ -149,6 +149,45 @@ def test_generate_style_decode_matches_full_forward():
         attn(x[:, :1], cos[:1], sin[:1], kv_cache=cache)
 
 
+def test_chunked_prefill_masks_top_left():
+    """A second multi-token chunk into a filled cache: the reference calls SDPA
+    with is_causal=True on the [Sq, Sk] scores (attention.py:228-231), whose
+    causal mask is top-left aligned (query row i sees keys 0..i).  Checked
+    against a float32 CPU restatement of that call on the module's own bf16
+    projections; 32 queries against 72 keys leave a ragged last 32-key tile."""
+    announce("module chunked prefill (Sq 32, Sk 72)")
+    torch.manual_seed(0)
+    dim, H, Hkv, D = 512, 8, 2, 64
+    attn = Attention(dim, H, Hkv).to(DEV).to(torch.bfloat16).eval()
+    P, T = 40, 72
+    cos, sin = precompute_rope_frequencies(D, 128, 5e5)
+    cos, sin = cos.to(DEV), sin.to(DEV)
+    x = torch.randn(2, T, dim, device=DEV, dtype=torch.bfloat16)
+    with torch.no_grad():
+        cache = KVCache(2, T, Hkv, D, torch.bfloat16, DEV)
+        attn(x[:, :P], cos[:P], sin[:P], kv_cache=cache)
+        got = attn(x[:, P:], cos[P:T], sin[P:T], kv_cache=cache).float().cpu()
+        q = attn.q_proj(x[:, P:]).float().cpu().view(2, T - P, H, D).transpose(1, 2)
+        k = attn.k_proj(x).float().cpu().view(2, T, Hkv, D).transpose(1, 2)
+        v = attn.v_proj(x).float().cpu().view(2, T, Hkv, D).transpose(1, 2)
+        wo = attn.o_proj.weight.float().cpu()
+    c, s = cos.cpu(), sin.cpu()
+
+    def rope(t, cc, ss):
+        t1, t2 = t[..., :D // 2], t[..., D // 2:]
+        return torch.cat([t1 * cc - t2 * ss, t2 * cc + t1 * ss], -1)
+
+    q, k = rope(q, c[P:T], s[P:T]), rope(k, c[:T], s[:T])
+    k, v = k.repeat_interleave(H // Hkv, 1), v.repeat_interleave(H // Hkv, 1)
+    scores = (q @ k.transpose(-1, -2)) / D ** 0.5
+    top_left = torch.ones(T - P, T, dtype=torch.bool).tril()
+    p = scores.masked_fill(~top_left, float("-inf")).softmax(-1)
+    want = (p @ v).transpose(1, 2).reshape(2, T - P, H * D) @ wo.t()
+    err = (got - want).abs().max().item()
+    print(f"chunked prefill max-abs err {err:.3e}")
+    assert cache.seq_len == T and err <= 1.5e-2
+
+
 def test_one_document_equals_causal():
     # packed-document path (reference :190-227) with one document equals plain
     # causal (reference tests/unit/test_packing.py:269-277); an all-True
