@@ -587,21 +587,32 @@ __global__ __launch_bounds__(256, 3) void fwd32_kernel(
 
   const float ltot = pair_sum32(lsum);
   const float inv = 1.f / ltot;
-  if (ri.q_valid) {
-    bf16* orow = out + (((int64_t)ri.b * Sq + ri.pos) * Hq + ri.hq) * D;
+  // The output leaves through LDS (the tile buffers are free after the loop's
+  // last barrier): each wavefront writes its 32 rows into its own 32 x D slice,
+  // 16-byte chunks XOR-swizzled by row, then stores whole 16-byte chunks, each
+  // row by KR consecutive lanes, so a store instruction covers 64 / KR whole
+  // rows instead of 16 bytes of each of 32 rows.
+  bf16* slice = w < 2 ? sK[w] : sV[w - 2];  // FBN x D bf16 = 32 rows x D
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
+  for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-      for (int gi = 0; gi < 4; ++gi) {
-        const int d = 32 * dt + 8 * gi + 4 * hh;
-        u32x2 pk2;
-        pk2[0] = pack2(acc[dt][4 * gi] * inv, acc[dt][4 * gi + 1] * inv);
-        pk2[1] = pack2(acc[dt][4 * gi + 2] * inv, acc[dt][4 * gi + 3] * inv);
-        *(u32x2*)(orow + d) = pk2;
-      }
-    if (lse != nullptr && hh == 0)
-      lse[((int64_t)ri.b * Hq + ri.hq) * Sq + ri.pos] = (m + log2f(ltot)) * kLn2;
+    for (int gi = 0; gi < 4; ++gi) {
+      const int ch = 4 * dt + gi;  // 16-byte chunk of columns 32 dt + 8 gi ..
+      u32x2 pk2;
+      pk2[0] = pack2(acc[dt][4 * gi] * inv, acc[dt][4 * gi + 1] * inv);
+      pk2[1] = pack2(acc[dt][4 * gi + 2] * inv, acc[dt][4 * gi + 3] * inv);
+      *(u32x2*)(slice + (c32 * KR + (ch ^ (c32 & (KR - 1)))) * 8 + 4 * hh) = pk2;
+    }
+  __syncthreads();
+#pragma unroll
+  for (int i2 = 0; i2 < 32 * KR / 64; ++i2) {
+    const int L = 64 * i2 + lane, row = L / KR, ch = L % KR;
+    const u32x4 v = *(const u32x4*)(slice + (row * KR + (ch ^ (row & (KR - 1)))) * 8);
+    const RowInfo rj = row_info(logical, nqb, Hkv, n_rep, bm_pos, Sq, w * 32 + row);
+    if (rj.q_valid) *(u32x4*)(out + (((int64_t)rj.b * Sq + rj.pos) * Hq + rj.hq) * D + 8 * ch) = v;
   }
+  if (ri.q_valid && lse != nullptr && hh == 0)
+    lse[((int64_t)ri.b * Hq + ri.hq) * Sq + ri.pos] = (m + log2f(ltot)) * kLn2;
 }
 
 // Capture: LSE, the probabilities P = exp(s - lse) as float32 [B, Hq, Sq, Sk]
