@@ -484,14 +484,6 @@ __global__ __launch_bounds__(256, 3) void fwd32_kernel(
 
   bf16x8 qf[KS];
   load_q_frag<D>(q, cos, sin, ri, Sq, Hq, hh, qf);
-  if (qrot != nullptr && ri.q_valid) {
-    // the rotated q row for the backward (read there long after: streaming stores)
-    bf16* dst = qrot + (((int64_t)ri.b * Hq + ri.hq) * krows + ri.pos) * D + 8 * hh;
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks)
-      __builtin_nontemporal_store(__builtin_bit_cast(u32x4, qf[ks]),
-                                  (u32x4*)(dst + (ks < KS / 2 ? 16 * ks : D / 2 + 16 * (ks - KS / 2))));
-  }
 
   float m = -INFINITY, lsum = 0.f;
   f32x16 acc[DT];
@@ -610,6 +602,25 @@ __global__ __launch_bounds__(256, 3) void fwd32_kernel(
     const u32x4 v = *(const u32x4*)(slice + (row * KR + (ch ^ (row & (KR - 1)))) * 8);
     const RowInfo rj = row_info(logical, nqb, Hkv, n_rep, bm_pos, Sq, w * 32 + row);
     if (rj.q_valid) *(u32x4*)(out + (((int64_t)rj.b * Sq + rj.pos) * Hq + rj.hq) * D + 8 * ch) = v;
+  }
+  if (qrot != nullptr) {
+    // the rotated q rows for the backward, the same way (read there long after:
+    // streaming stores); fragment ks holds the row's 16-byte chunk c below
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const int c = ks < KS / 2 ? 2 * ks + hh : KR / 2 + 2 * (ks - KS / 2) + hh;
+      *(u32x4*)(slice + (c32 * KR + (c ^ (c32 & (KR - 1)))) * 8) = __builtin_bit_cast(u32x4, qf[ks]);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i2 = 0; i2 < 32 * KR / 64; ++i2) {
+      const int L = 64 * i2 + lane, row = L / KR, ch = L % KR;
+      const u32x4 v = *(const u32x4*)(slice + (row * KR + (ch ^ (row & (KR - 1)))) * 8);
+      const RowInfo rj = row_info(logical, nqb, Hkv, n_rep, bm_pos, Sq, w * 32 + row);
+      if (rj.q_valid)
+        __builtin_nontemporal_store(
+            v, (u32x4*)(qrot + (((int64_t)rj.b * Hq + rj.hq) * krows + rj.pos) * D + 8 * ch));
+    }
   }
   if (ri.q_valid && lse != nullptr && hh == 0)
     lse[((int64_t)ri.b * Hq + ri.hq) * Sq + ri.pos] = (m + log2f(ltot)) * kLn2;
