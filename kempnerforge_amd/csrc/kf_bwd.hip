@@ -929,11 +929,17 @@ __global__ __launch_bounds__(64 * HB) void bwd_dq_ds_kernel(
   }
 
   const int hq = g * n_rep + hg * HB + w;
+  // dQ leaves through LDS (the ring is free once every wavefront is past its
+  // last products): each wavefront writes its 64 rows into its own 64 x D
+  // slice, 16-byte chunks XOR-swizzled by row, then stores whole chunks, KR
+  // consecutive lanes per row, instead of 8 bytes of each of 32 rows.
+  static_assert(HB * 64 * D * 2 <= NBUF * (int)sizeof(Stage), "dQ slices exceed the ring");
+  __syncthreads();
+  bf16* slice = (bf16*)st + w * 64 * D;
 #pragma unroll
   for (int mh = 0; mh < 2; ++mh) {
-    const int pos = qt * DSQ + 32 * mh + c32;
-    if (pos >= S) break;
-    bf16* dqr = dq + (((int64_t)b * S + pos) * Hq + hq) * D;
+    const int r = 32 * mh + c32;
+    const int pos = min(qt * DSQ + r, S - 1);  // rows past S are formed, not stored
     const float* cr = cos + (int64_t)pos * HALF;
     const float* sr = sin + (int64_t)pos * HALF;
 #pragma unroll
@@ -947,9 +953,20 @@ __global__ __launch_bounds__(64 * HB) void bwd_dq_ds_kernel(
           rope_pair_bwd<bf16>(acc[mh][dt][4 * gi + e] * scale,
                               acc[mh][dt + DT / 2][4 * gi + e] * scale, cr[d + e], sr[d + e],
                               lo[e], hi[e]);
-        *(u32x2*)(dqr + d) = u32x2{pack2(lo[0], lo[1]), pack2(lo[2], lo[3])};
-        *(u32x2*)(dqr + d + HALF) = u32x2{pack2(hi[0], hi[1]), pack2(hi[2], hi[3])};
+        const int cl = 4 * dt + gi, chh = KR / 2 + 4 * dt + gi;  // chunks of d and d + HALF
+        *(u32x2*)(slice + (r * KR + (cl ^ (r & (KR - 1)))) * 8 + 4 * hh) =
+            u32x2{pack2(lo[0], lo[1]), pack2(lo[2], lo[3])};
+        *(u32x2*)(slice + (r * KR + (chh ^ (r & (KR - 1)))) * 8 + 4 * hh) =
+            u32x2{pack2(hi[0], hi[1]), pack2(hi[2], hi[3])};
       }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i2 = 0; i2 < KR; ++i2) {
+    const int L = 64 * i2 + lane, r = L / KR, ch = L % KR;
+    const int pos = qt * DSQ + r;
+    const u32x4 v = *(const u32x4*)(slice + (r * KR + (ch ^ (r & (KR - 1)))) * 8);
+    if (pos < S) *(u32x4*)(dq + (((int64_t)b * S + pos) * Hq + hq) * D + 8 * ch) = v;
   }
 }
 
