@@ -289,14 +289,6 @@ __global__ __launch_bounds__(256, 2) void fwd_mfma_kernel(
 
   bf16x8 qf[KS];
   load_q_frag<D>(q, cos, sin, ri, Sq, Hq, hh, qf);
-  if (qrot != nullptr && ri.q_valid) {
-    // the rotated q row for the backward (read there long after: streaming stores)
-    bf16* dst = qrot + (((int64_t)ri.b * Hq + ri.hq) * krows + ri.pos) * D + 8 * hh;
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks)
-      __builtin_nontemporal_store(__builtin_bit_cast(u32x4, qf[ks]),
-                                  (u32x4*)(dst + (ks < KS / 2 ? 16 * ks : D / 2 + 16 * (ks - KS / 2))));
-  }
 
   float m = LIST ? -1e30f : -INFINITY, lsum = 0.f;
   f32x16 acc[DT];
@@ -431,21 +423,51 @@ __global__ __launch_bounds__(256, 2) void fwd_mfma_kernel(
 
   const float ltot = pair_sum32(lsum);
   const float inv = 1.f / ltot;
-  if (ri.q_valid) {
-    bf16* orow = out + (((int64_t)ri.b * Sq + ri.pos) * Hq + ri.hq) * D;
+  // The output leaves through LDS (the tile buffers are free after the loop's
+  // last barrier): each wavefront writes its 32 rows into its own 32 x D slice,
+  // 16-byte chunks XOR-swizzled by row, then stores whole 16-byte chunks, each
+  // row by KR consecutive lanes, so a store instruction covers 64 / KR whole
+  // rows instead of 16 bytes of each of 32 rows.
+  bf16* slice = &sK[0][0] + w * 32 * D;  // 32 rows x D (sK holds 2 x 64 rows)
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
+  for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-      for (int gi = 0; gi < 4; ++gi) {
-        const int d = 32 * dt + 8 * gi + 4 * hh;
-        u32x2 pk2;
-        pk2[0] = pack2(acc[dt][4 * gi] * inv, acc[dt][4 * gi + 1] * inv);
-        pk2[1] = pack2(acc[dt][4 * gi + 2] * inv, acc[dt][4 * gi + 3] * inv);
-        *(u32x2*)(orow + d) = pk2;
-      }
-    if (lse != nullptr && hh == 0)
-      lse[((int64_t)ri.b * Hq + ri.hq) * Sq + ri.pos] = (m + log2f(ltot)) * kLn2;
+    for (int gi = 0; gi < 4; ++gi) {
+      const int ch = 4 * dt + gi;  // 16-byte chunk of columns 32 dt + 8 gi ..
+      u32x2 pk2;
+      pk2[0] = pack2(acc[dt][4 * gi] * inv, acc[dt][4 * gi + 1] * inv);
+      pk2[1] = pack2(acc[dt][4 * gi + 2] * inv, acc[dt][4 * gi + 3] * inv);
+      *(u32x2*)(slice + (c32 * KR + (ch ^ (c32 & (KR - 1)))) * 8 + 4 * hh) = pk2;
+    }
+  __syncthreads();
+#pragma unroll
+  for (int i2 = 0; i2 < 32 * KR / 64; ++i2) {
+    const int L = 64 * i2 + lane, row = L / KR, ch = L % KR;
+    const u32x4 v = *(const u32x4*)(slice + (row * KR + (ch ^ (row & (KR - 1)))) * 8);
+    const RowInfo rj = row_info(logical, nqb, Hkv, n_rep, bm_pos, Sq, w * 32 + row);
+    if (rj.q_valid) *(u32x4*)(out + (((int64_t)rj.b * Sq + rj.pos) * Hq + rj.hq) * D + 8 * ch) = v;
   }
+  if (qrot != nullptr) {
+    // the rotated q rows for the backward, the same way (read there long after:
+    // streaming stores); fragment ks holds the row's 16-byte chunk c below
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const int c = ks < KS / 2 ? 2 * ks + hh : KR / 2 + 2 * (ks - KS / 2) + hh;
+      *(u32x4*)(slice + (c32 * KR + (c ^ (c32 & (KR - 1)))) * 8) = __builtin_bit_cast(u32x4, qf[ks]);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i2 = 0; i2 < 32 * KR / 64; ++i2) {
+      const int L = 64 * i2 + lane, row = L / KR, ch = L % KR;
+      const u32x4 v = *(const u32x4*)(slice + (row * KR + (ch ^ (row & (KR - 1)))) * 8);
+      const RowInfo rj = row_info(logical, nqb, Hkv, n_rep, bm_pos, Sq, w * 32 + row);
+      if (rj.q_valid)
+        __builtin_nontemporal_store(
+            v, (u32x4*)(qrot + (((int64_t)rj.b * Hq + rj.hq) * krows + rj.pos) * D + 8 * ch));
+    }
+  }
+  if (ri.q_valid && lse != nullptr && hh == 0)
+    lse[((int64_t)ri.b * Hq + ri.hq) * Sq + ri.pos] = (m + log2f(ltot)) * kLn2;
 }
 
 // Forward without an explicit mask on 32-key tiles: half the LDS (32 KB per
