@@ -188,8 +188,13 @@ class Workloads:
             qn = seeded((B, 1, Hq, D), 0, self.bf16, self.dev)
             kn = seeded((B, 1, Hkv, D), 1, self.bf16, self.dev)
             vn = seeded((B, 1, Hkv, D), 2, self.bf16, self.dev)
-            kc = torch.randn(B, Hkv, Smax, D, device=self.dev, dtype=self.bf16)
-            vc = torch.randn(B, Hkv, Smax, D, device=self.dev, dtype=self.bf16)
+            # the caches from the same seeded CPU generator as everything else
+            # (drawn one sequence at a time, to bound host memory)
+            kc = torch.empty(B, Hkv, Smax, D, device=self.dev, dtype=self.bf16)
+            vc = torch.empty_like(kc)
+            for b in range(B):
+                kc[b].copy_(torch.randn(Hkv, Smax, D, generator=g, dtype=self.bf16))
+                vc[b].copy_(torch.randn(Hkv, Smax, D, generator=g, dtype=self.bf16))
             cos, sin = self.rope(D, Smax, C4["theta"])
             nbytes = sum(4 * (int(L) + 1) * Hkv * D for L in lens) + 4 * B * Hq * D \
                 + 4 * B * Hkv * D

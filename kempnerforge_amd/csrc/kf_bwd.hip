@@ -175,7 +175,9 @@ __device__ __forceinline__ void dkdv_role(
   static_assert(!(STORE && KPM), "dS records are not kept with key padding");
   constexpr int KS = D / 16, DT = D / 32, HALF = D / 2;
   constexpr int KR = D / 8;
-  constexpr int PF = 3;  // fragment reads run PF MFMAs ahead
+  // fragment reads run PF MFMAs ahead (2 in the masked modes, whose lists and
+  // masks take the registers of a third)
+  constexpr int PF = LIST ? 2 : 3;
   const int hh = lane >> 5, c32 = lane & 31;
   const int kw = w & 3;
   const int key = k0 + 32 * kw + c32;
@@ -197,11 +199,13 @@ __device__ __forceinline__ void dkdv_role(
     const int64_t bhq = (int64_t)b * Hq + hq;
     const int q0 = qtile * BQ;
     DkdvStage<D>& S_ = st[buf];
-    tile_to_lds<BQ, KR, 8>(qrot + (bhq * P + q0) * D, D, S_.q, w, lane);
+    // (the masked modes recompute the per-lane offsets per tile: their lists
+    // and masks leave no registers to keep them in)
+    tile_to_lds<BQ, KR, 8, LIST>(qrot + (bhq * P + q0) * D, D, S_.q, w, lane);
     // dO in place ([B, S, Hq, D]): rows past S repeat row S - 1 (their lse is
     // +inf, so they contribute nothing)
-    tile_to_lds<BQ, KR, 8>(dout + (((int64_t)b * S + q0) * Hq + hq) * D, Hq * D, S_.o, w, lane,
-                           S - q0);
+    tile_to_lds<BQ, KR, 8, LIST>(dout + (((int64_t)b * S + q0) * Hq + hq) * D, Hq * D, S_.o, w,
+                                 lane, S - q0);
     if (w == 0) row_to_lds(lse2 + bhq * P + q0, S_.l, lane);
     if (w == 1) row_to_lds(delta + bhq * P + q0, S_.dl, lane);
     if (DOC && w == 2) dma4(lds_addr(sQD[buf]), (uint32_t)min(q0 + lane, S - 1) * 4u, drow);
@@ -411,15 +415,16 @@ __device__ __forceinline__ void dkdv_role(
   }
 
   if (key >= S) return;
+  const int key_e = key, hoff = 4 * hh;
   if (DSROLE) {
-    bf16* dkr = dk + (((int64_t)b * S + key) * Hkv + g) * D;
-    const float* cr = cos + (int64_t)key * HALF;
-    const float* sr = sin + (int64_t)key * HALF;
+    bf16* dkr = dk + (((int64_t)b * S + key_e) * Hkv + g) * D + hoff;
+    const float* cr = cos + (int64_t)key_e * HALF + hoff;
+    const float* sr = sin + (int64_t)key_e * HALF + hoff;
 #pragma unroll
     for (int dt = 0; dt < DT / 2; ++dt)
 #pragma unroll
       for (int gi = 0; gi < 4; ++gi) {
-        const int d = 32 * dt + 8 * gi + 4 * hh;
+        const int d = 32 * dt + 8 * gi;
         float lo[4], hi[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e)
@@ -429,12 +434,12 @@ __device__ __forceinline__ void dkdv_role(
         *(u32x2*)(dkr + d + HALF) = u32x2{pack2(hi[0], hi[1]), pack2(hi[2], hi[3])};
       }
   } else {
-    bf16* dvr = dv + (((int64_t)b * S + key) * Hkv + g) * D;
+    bf16* dvr = dv + (((int64_t)b * S + key_e) * Hkv + g) * D + hoff;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
       for (int gi = 0; gi < 4; ++gi) {
-        const int d = 32 * dt + 8 * gi + 4 * hh;
+        const int d = 32 * dt + 8 * gi;
         *(u32x2*)(dvr + d) = u32x2{pack2(acc[dt][4 * gi], acc[dt][4 * gi + 1]),
                                    pack2(acc[dt][4 * gi + 2], acc[dt][4 * gi + 3])};
       }
@@ -573,7 +578,12 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_kernel(
   for (int rnd = 0;; ++rnd) {
     const int logical = xcd_item(xi, rnd);
     if (logical < 0) break;
-    const RowInfo ri = row_info(logical, nqb, Hkv, n_rep, bm_pos, S, w * 32 + c32);
+    // per-lane values laundered per item: hoisted out of the persistent loop,
+    // the row split and the per-lane 64-bit bases derived from them would be
+    // kept in scratch across the item
+    int r_l = w * 32 + c32, lane_l = lane;
+    asm volatile("" : "+v"(r_l), "+v"(lane_l));
+    const RowInfo ri = row_info(logical, nqb, Hkv, n_rep, bm_pos, S, r_l);
     const int bh = ri.b * Hkv + ri.g;
     const int64_t bhq = (int64_t)ri.b * Hq + ri.hq;
 
@@ -586,9 +596,9 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_kernel(
     // rows are zero, so they add nothing to dQ)
     const bf16* vbase = v + ((int64_t)ri.b * S * Hkv + ri.g) * D;
     auto stage = [&](int t, int buf) {
-      tile_to_lds<BN, KR, 8>(kbase + (int64_t)t * BN * D, D, st[buf].k, w, lane);
-      tile_to_lds<BN, KR, 8>(vbase + (int64_t)t * BN * Hkv * D, Hkv * D, st[buf].v, w, lane,
-                             S - t * BN);
+      tile_to_lds<BN, KR, 8, true>(kbase + (int64_t)t * BN * D, D, st[buf].k, w, lane);
+      tile_to_lds<BN, KR, 8, true>(vbase + (int64_t)t * BN * Hkv * D, Hkv * D, st[buf].v, w, lane,
+                                   S - t * BN);
       if (LIST && w == 0) dma4(lds_addr(sKD[buf]), (uint32_t)min(t * BN + lane, S - 1) * 4u, drow);
     };
     int di = 0;        // DOC: this row's document
@@ -600,7 +610,7 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_kernel(
       di = drow[min(ri.pos, S - 1)];
       if (w == 0) {
         const int n = doc_tile_list(drow, ri.p0, min(ri.p0 + bm_pos, S), rec, 0, ntiles, sList,
-                                    lane);
+                                    lane_l);
         if (lane == 0) sCount = n;
       }
       __syncthreads();
@@ -612,7 +622,7 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_kernel(
         const bool guard_block = ri.p0 < f;  // a guarded row needs every key tile
         const int n = kpm_tile_list(rec, 0, guard_block ? nall : ntiles,
                                     [&](int, int2 r) { return guard_block ? 2 : r.x == 0 ? 0 : r.x < BN ? 2 : 1; },
-                                    sList, lane);
+                                    sList, lane_l);
         if (lane == 0) {
           sCount = n;
           sFirst = f;
@@ -634,8 +644,9 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_kernel(
     bf16x8 qf[KS], df[KS];
     float l2 = INFINITY, ndl = 0.f;  // ndl: -Delta of this lane's row
     if (ri.q_valid) {
-      const bf16* qr = qrot + (bhq * P + ri.pos) * D + 8 * hh;
-      const bf16* dr = dout + (((int64_t)ri.b * S + ri.pos) * Hq + ri.hq) * D + 8 * hh;
+      const int hoff = 8 * (lane_l >> 5);
+      const bf16* qr = qrot + (bhq * P + ri.pos) * D + hoff;
+      const bf16* dr = dout + (((int64_t)ri.b * S + ri.pos) * Hq + ri.hq) * D + hoff;
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
         qf[ks] = as_bf16x8(*(const u32x4*)(qr + 16 * ks));
@@ -754,20 +765,21 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_kernel(
 
     if (ri.q_valid) {
       bf16* dqr = dq + (((int64_t)ri.b * S + ri.pos) * Hq + ri.hq) * D;
-      const float* cr = cos + (int64_t)ri.pos * HALF;
-      const float* sr = sin + (int64_t)ri.pos * HALF;
+      const int hoff = 4 * (lane_l >> 5);
+      const float* cr = cos + (int64_t)ri.pos * HALF + hoff;
+      const float* sr = sin + (int64_t)ri.pos * HALF + hoff;
 #pragma unroll
       for (int dt = 0; dt < DT / 2; ++dt)
 #pragma unroll
         for (int gi = 0; gi < 4; ++gi) {
-          const int d = 32 * dt + 8 * gi + 4 * hh;
+          const int d = 32 * dt + 8 * gi;
           float lo[4], hi[4];
 #pragma unroll
           for (int e = 0; e < 4; ++e)
             rope_pair_bwd<bf16>(acc[dt][4 * gi + e] * scale, acc[dt + DT / 2][4 * gi + e] * scale,
                                 cr[d + e], sr[d + e], lo[e], hi[e]);
-          *(u32x2*)(dqr + d) = u32x2{pack2(lo[0], lo[1]), pack2(lo[2], lo[3])};
-          *(u32x2*)(dqr + d + HALF) = u32x2{pack2(hi[0], hi[1]), pack2(hi[2], hi[3])};
+          *(u32x2*)(dqr + d + hoff) = u32x2{pack2(lo[0], lo[1]), pack2(lo[2], lo[3])};
+          *(u32x2*)(dqr + d + hoff + HALF) = u32x2{pack2(hi[0], hi[1]), pack2(hi[2], hi[3])};
         }
     }
     __syncthreads();  // LDS of this item is free for the next

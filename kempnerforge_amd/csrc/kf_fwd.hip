@@ -644,8 +644,13 @@ __global__ __launch_bounds__(256, 3) void fwd32_kernel(
             v, (u32x4*)(qrot + (((int64_t)rj.b * Hq + rj.hq) * krows + rj.pos) * D + 8 * ch));
     }
   }
-  if (ri.q_valid && lse != nullptr && hh == 0)
-    lse[((int64_t)ri.b * Hq + ri.hq) * Sq + ri.pos] = (m + log2f(ltot)) * kLn2;
+  // this row's LSE: its index recomputed here from a laundered row number, so
+  // the prologue's 64-bit value is not kept live (in scratch) across the loop
+  int r_l = w * 32 + c32;
+  asm volatile("" : "+v"(r_l));
+  const RowInfo rl = row_info(logical, nqb, Hkv, n_rep, bm_pos, Sq, r_l);
+  if (rl.q_valid && lse != nullptr && hh == 0)
+    lse[((int64_t)rl.b * Hq + rl.hq) * Sq + rl.pos] = (m + log2f(ltot)) * kLn2;
 }
 
 // Capture: LSE, the probabilities P = exp(s - lse) as float32 [B, Hq, Sq, Sk]

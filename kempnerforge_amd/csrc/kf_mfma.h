@@ -139,12 +139,16 @@ __device__ __forceinline__ void dma4(uint32_t lds, uint32_t voff, const void* ba
 // by vmcnt: wait with lds_copy_wait() and a barrier before reading the tile.
 // Rows at or beyond `rows` (when given) repeat global row rows - 1: a tile
 // that runs past the end of an unpadded tensor stays in bounds.
-template <int ROWS_T, int R, int NW = 4>
+// FRESH: the per-lane offsets are recomputed at every call (a few VALU
+// instructions) instead of being kept live across the caller's loop, for
+// kernels whose registers are otherwise spent.
+template <int ROWS_T, int R, int NW = 4, bool FRESH = false>
 __device__ __forceinline__ void tile_to_lds(const bf16* __restrict__ g, uint32_t ld, bf16* lds,
                                             int w, int lane, int rows = ROWS_T) {
   constexpr int TOTAL = ROWS_T * R / 64;
   static_assert(TOTAL % NW == 0, "tile must split evenly over the wavefronts");
   constexpr int PER = TOTAL / NW;
+  if (FRESH) asm volatile("" : "+v"(lane));
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
     const int L = (w * PER + j) * 64 + lane;

@@ -50,6 +50,12 @@ def _ptr(t: torch.Tensor | None) -> ctypes.c_void_p:
     return ctypes.c_void_p(0 if t is None else t.data_ptr())
 
 
+def _aligned(t: torch.Tensor) -> torch.Tensor:
+    """t itself when its data starts on a 16-byte boundary (the MFMA kernels'
+    vector loads need it), else a fresh copy (the allocator aligns those)."""
+    return t if t.data_ptr() % 16 == 0 else t.clone()
+
+
 def _workspace(nbytes: int, device) -> torch.Tensor:
     return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
 
@@ -136,7 +142,7 @@ def fwd_raw(q, k, v, cos, sin, *, causal: bool, k_rotated: bool, k_layout: str =
 _BWD_LOW_MEMORY = False
 # Largest share of the memory available to the caching allocator (free device
 # memory plus what it holds unused) that the kept dS tiles may take.
-_DS_BUDGET_FRACTION = 0.5
+_DS_BUDGET_FRACTION: float | None = 0.5
 
 
 def set_backward_low_memory(enabled: bool) -> None:
@@ -145,16 +151,22 @@ def set_backward_low_memory(enabled: bool) -> None:
     tiles (about B*Hq*S*S bytes), trading ~5-11% of backward time for memory."""
     global _BWD_LOW_MEMORY
     _BWD_LOW_MEMORY = bool(enabled)
+    _DS_DECISIONS.clear()
 
 
-def set_backward_ds_budget(fraction: float) -> None:
+def set_backward_ds_budget(fraction: float | None) -> None:
     """Share (0..1] of the memory the allocator can still hand out that the
     backward's kept dS tiles may take (default 0.5); above it the backward
-    falls back to recomputing S and dP for dQ."""
+    falls back to recomputing S and dP for dQ.  None keeps them whenever the
+    library offers them, whatever the free memory (a policy that does not
+    depend on the allocator's state at all).  The decision is made once per
+    backward shape and then reused, so that dQ's last bits do not change from
+    step to step; setting the budget starts over."""
     global _DS_BUDGET_FRACTION
-    if not 0.0 < fraction <= 1.0:
-        raise ValueError(f"fraction must lie in (0, 1] (got {fraction})")
-    _DS_BUDGET_FRACTION = float(fraction)
+    if fraction is not None and not 0.0 < fraction <= 1.0:
+        raise ValueError(f"fraction must lie in (0, 1] or be None (got {fraction})")
+    _DS_BUDGET_FRACTION = None if fraction is None else float(fraction)
+    _DS_DECISIONS.clear()
 
 
 def available_bytes(device) -> int | None:
@@ -169,6 +181,25 @@ def available_bytes(device) -> int | None:
     return int(free) + max(int(idle), 0)
 
 
+# The keep-dS decision per backward shape, made once (the first backward of
+# that shape) and reused: the kept-tile and recompute dQ paths differ in the
+# last bits, so deciding again from the allocator's state at every call could
+# switch paths from one step to the next.  Cleared by set_backward_ds_budget
+# and set_backward_low_memory.
+_DS_DECISIONS: dict[tuple, bool] = {}
+
+
+def _keep_ds_for(key: tuple, extra_bytes: int, device) -> bool:
+    hit = _DS_DECISIONS.get(key)
+    if hit is None:
+        if _DS_BUDGET_FRACTION is None:
+            hit = extra_bytes > 0
+        else:
+            hit = keep_ds_tiles(extra_bytes, available_bytes(device))
+        _DS_DECISIONS[key] = hit
+    return hit
+
+
 def keep_ds_tiles(extra_bytes: int, available: int | None, fraction: float | None = None) -> bool:
     """Whether the backward keeps its dS tiles: their ``extra_bytes`` must fit in
     ``fraction`` of the ``available`` bytes (the memory-aware default; the
@@ -178,6 +209,8 @@ def keep_ds_tiles(extra_bytes: int, available: int | None, fraction: float | Non
     fraction = _DS_BUDGET_FRACTION if fraction is None else fraction
     if extra_bytes <= 0:
         return False
+    if fraction is None:
+        return True
     return available is None or extra_bytes <= fraction * available
 
 
@@ -215,7 +248,8 @@ def bwd_raw(q, k, v, cos, sin, out, lse, dout, *, causal: bool, doc_ids=None,
         _lib.check(lib.kf_attn_bwd_workspace_size_ds(B, S, Hq, Hkv, D, dt, int(causal),
                                                      ctypes.byref(with_ds)),
                    "kf_attn_bwd_workspace_size_ds")
-        if keep_ds_tiles(with_ds.value - nbytes.value, available_bytes(q.device)):
+        key = ("bwd", q.device, B, S, Hq, Hkv, D, q.dtype, bool(causal), doc is not None)
+        if _keep_ds_for(key, with_ds.value - nbytes.value, q.device):
             nbytes = with_ds
     ws = _workspace(nbytes.value, q.device)
     _lib.check(lib.kf_attn_bwd(_ptr(q), _ptr(k), _ptr(v), _ptr(cos), _ptr(sin), _ptr(out),
@@ -245,6 +279,16 @@ def rot_size(B: int, S: int, Hq: int, Hkv: int, D: int, dtype: torch.dtype, has_
     return n.value
 
 
+def _rot_shapes_ok(q, k, v) -> bool:
+    """Self-attention shapes and one dtype: what the rotated-operand pair takes
+    before kf_attn_rot_size's own size / dtype / mask checks."""
+    if q.dim() != 4 or k.dim() != 4:
+        return False
+    B, S, Hq, D = q.shape
+    return (k.shape[0] == B and k.shape[1] == S and k.shape[3] == D
+            and tuple(v.shape) == tuple(k.shape) and k.dtype == q.dtype and v.dtype == q.dtype)
+
+
 def fwd_rot_raw(q, k, v, cos, sin, *, causal: bool, doc_ids=None, key_padding_mask=None):
     """out, lse, rot for self-attention (``kf_attn_fwd_rot``): :func:`fwd_raw` with
     un-rotated BSHD k that also returns ``rot``, q and k after RoPE as the
@@ -253,14 +297,15 @@ def fwd_rot_raw(q, k, v, cos, sin, *, causal: bool, doc_ids=None, key_padding_ma
     :func:`fwd_raw` and :func:`bwd_raw`."""
     _require_gpu(q, k, v)
     lib = _lib.load()
-    q, k, v = (t.contiguous() for t in (q, k, v))
+    if not _rot_shapes_ok(q, k, v):
+        return None
+    # misaligned views are copied, so that whenever rot_size() is non-zero the
+    # call below takes the rotated-operand path (the fake kernel relies on it)
+    q, k, v = (_aligned(t.contiguous()) for t in (q, k, v))
     B, S, Hq, D = q.shape
     Hkv = k.shape[2]
-    if (tuple(k.shape) != (B, S, Hkv, D) or tuple(v.shape) != tuple(k.shape)
-            or k.dtype != q.dtype or v.dtype != q.dtype):
-        return None
-    cos = _rope_table(cos, S, D // 2, "rope_cos")
-    sin = _rope_table(sin, S, D // 2, "rope_sin")
+    cos = _aligned(_rope_table(cos, S, D // 2, "rope_cos"))
+    sin = _aligned(_rope_table(sin, S, D // 2, "rope_sin"))
     doc = _doc_ids(doc_ids, B, S, q.device)
     kv = _key_valid(key_padding_mask, B, S, q.device)
     nrot = rot_size(B, S, Hq, Hkv, D, q.dtype, doc is not None, kv is not None)
@@ -291,14 +336,22 @@ def bwd_rot_raw(rot, v, cos, sin, out, lse, dout, *, causal: bool, doc_ids=None,
     _require_gpu(rot, v, out, lse, dout)
     lib = _lib.load()
     v, out, dout, lse = (t.contiguous() for t in (v, out, dout, lse))
-    if dout.data_ptr() % 16:
-        dout = dout.clone()
+    dout = _aligned(dout)
     B, S, Hq, D = out.shape
     Hkv = v.shape[2]
     cos = _rope_table(cos, S, D // 2, "rope_cos")
     sin = _rope_table(sin, S, D // 2, "rope_sin")
     doc = _doc_ids(doc_ids, B, S, out.device)
     kv = _key_valid(key_padding_mask, B, S, out.device)
+    # the C ABI takes rot without a length: check it here, before any launch,
+    # so a rot from another shape or mask kind cannot send the kernels out of bounds
+    want = rot_size(B, S, Hq, Hkv, D, out.dtype, doc is not None, kv is not None)
+    if (rot.dtype != out.dtype or not rot.is_contiguous() or rot.device != out.device
+            or rot.data_ptr() % 16 or want == 0 or rot.numel() * rot.element_size() != want):
+        raise ValueError(
+            f"rot must be the contiguous, 16-byte aligned {out.dtype} buffer fwd_rot_raw "
+            f"returns for these shapes and masks ({want} bytes on {out.device}); got "
+            f"{rot.numel() * rot.element_size()} bytes of {rot.dtype} on {rot.device}")
     dt = _dtype_code(out)
     dq, dk, dv = torch.empty_like(out), torch.empty_like(v), torch.empty_like(v)
     nbytes = _lib.size_out()
@@ -311,7 +364,8 @@ def bwd_rot_raw(rot, v, cos, sin, out, lse, dout, *, causal: bool, doc_ids=None,
         _lib.check(lib.kf_attn_bwd_rot_workspace_size(B, S, Hq, Hkv, D, dt, int(causal), 1,
                                                       ctypes.byref(with_ds)),
                    "kf_attn_bwd_rot_workspace_size")
-        if keep_ds_tiles(with_ds.value - nbytes.value, available_bytes(out.device)):
+        key = ("bwd_rot", out.device, B, S, Hq, Hkv, D, out.dtype, bool(causal), doc is not None)
+        if _keep_ds_for(key, with_ds.value - nbytes.value, out.device):
             nbytes = with_ds
     ws = _workspace(nbytes.value, out.device)
     _lib.check(lib.kf_attn_bwd_rot(_ptr(rot), _ptr(v), _ptr(cos), _ptr(sin), _ptr(out),
@@ -441,24 +495,29 @@ def capture_raw(q, k, v, cos, sin, *, causal: bool, k_rotated: bool, k_layout: s
 @torch.library.custom_op("kf::attn_fwd", mutates_args=(), device_types="cuda")
 def attn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos: torch.Tensor,
              sin: torch.Tensor, causal: bool, doc_ids: Optional[torch.Tensor] = None,
-             key_padding_mask: Optional[torch.Tensor] = None
+             key_padding_mask: Optional[torch.Tensor] = None, keep_rot: bool = True
              ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
-    """out, lse and rot (empty when the rotated-operand path does not apply)."""
-    res = fwd_rot_raw(q, k, v, cos, sin, causal=causal, doc_ids=doc_ids,
-                      key_padding_mask=key_padding_mask)
-    if res is not None:
-        return res
+    """out, lse and rot: the rotated q and k for the backward, written only
+    when ``keep_rot`` (a backward will run) and the rotated-operand path takes
+    these inputs; empty otherwise."""
+    if keep_rot:
+        res = fwd_rot_raw(q, k, v, cos, sin, causal=causal, doc_ids=doc_ids,
+                          key_padding_mask=key_padding_mask)
+        if res is not None:
+            return res
     out, lse = fwd_raw(q, k, v, cos, sin, causal=causal, k_rotated=False, doc_ids=doc_ids,
                        key_padding_mask=key_padding_mask)
     return out, lse, q.new_empty(0)
 
 
 @attn_fwd.register_fake
-def _(q, k, v, cos, sin, causal, doc_ids=None, key_padding_mask=None):
-    # rot's size assumes 16-byte aligned inputs (as allocator tensors are)
+def _(q, k, v, cos, sin, causal, doc_ids=None, key_padding_mask=None, keep_rot=True):
+    # the same decision as the real kernel: rot exactly when keep_rot, the
+    # shapes and dtypes fit and kf_attn_rot_size accepts the sizes (the real
+    # op copies misaligned inputs, so alignment never changes it)
     B, S, Hq, D = q.shape
     nrot = rot_size(B, S, Hq, k.shape[2], D, q.dtype, doc_ids is not None,
-                    key_padding_mask is not None) if k.shape[1] == S else 0
+                    key_padding_mask is not None) if keep_rot and _rot_shapes_ok(q, k, v) else 0
     return (torch.empty_like(q), q.new_empty(B, Hq, S, dtype=torch.float32),
             q.new_empty(nrot // q.element_size()))
 
@@ -494,7 +553,7 @@ def _(rot, v, cos, sin, out, lse, dout, causal, doc_ids=None, key_padding_mask=N
 
 
 def _setup_context(ctx, inputs, output):
-    q, k, v, cos, sin, causal, doc_ids, key_padding_mask = inputs
+    q, k, v, cos, sin, causal, doc_ids, key_padding_mask, _keep_rot = inputs
     out, lse, rot = output
     # only out carries a gradient: no zero-filled gradients for lse and rot
     ctx.mark_non_differentiable(lse, rot)
@@ -517,7 +576,7 @@ def _backward(ctx, dout, dlse, drot):
         q, k, v, cos, sin, out, lse, doc_ids, key_padding_mask = ctx.saved_tensors
         dq, dk, dv = attn_bwd(q, k, v, cos, sin, out, lse, dout.contiguous(), ctx.causal,
                               doc_ids, key_padding_mask)
-    return dq, dk, dv, None, None, None, None, None
+    return dq, dk, dv, None, None, None, None, None, None
 
 
 attn_fwd.register_autograd(_backward, setup_context=_setup_context)
@@ -536,5 +595,10 @@ def attention(q, k, v, rope_cos, rope_sin, *, causal: bool = True, doc_ids=None,
     ``key_padding_mask [B,S]`` (True = attend) its padded-key branch
     (``:214-225``, ``kempnerforge/model/mot.py:188-198``), NaN guard included.
     """
-    out, _, _ = attn_fwd(q, k, v, rope_cos, rope_sin, causal, doc_ids, key_padding_mask)
+    # rot only when a backward can run: under no_grad / inference it would be
+    # written (q and k rotated, (B*Hkv + B*Hq)*S*D elements) and never read
+    keep_rot = torch.is_grad_enabled() and (q.requires_grad or k.requires_grad
+                                            or v.requires_grad)
+    out, _, _ = attn_fwd(q, k, v, rope_cos, rope_sin, causal, doc_ids, key_padding_mask,
+                         keep_rot)
     return out

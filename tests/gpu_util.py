@@ -53,14 +53,19 @@ def grad_bound(want: torch.Tensor, dtype, group: int = 1) -> torch.Tensor:
 
     ``group``: the number of query heads a dK / dV element sums (n_rep).  Each
     head's contribution carries the rounding of its bf16 P and dS tiles (the
-    MFMA operands), and the contributions share the same key rows, so their
-    errors can add up: the 2e-2 is stated for the benchmark shapes (groups of
-    4 and 8) and grows in proportion to the group above that (a group of 32,
-    multi-query attention: 8e-2).
+    MFMA operands); the roundings of different heads are independent, so their
+    sum's error grows like the square root of the number of heads.  The 2e-2 is
+    stated for the benchmark shapes (groups of 4 and 8); above 8 the bound is
+    1.25 * sqrt(group / 8) times it (2.5x at a group of 32, multi-query
+    attention).  Measured at group 32 (the factor on 2e-2 the worst element
+    needs, printed by check_grad): 1.23-1.33 with causal or packed-document
+    masks, 2.11 with random key padding on 200 positions, whose rows attend few
+    keys (P near 1, so the bf16 rounding of P and dS is largest against dK).
     """
     if dtype == torch.float32:
         return torch.full_like(want.double(), TOL[torch.float32])
-    return TOL[dtype] * max(1.0, group / 8.0) + half_ulp(want, dtype)
+    factor = 1.0 if group <= 8 else 1.25 * (group / 8.0) ** 0.5
+    return TOL[dtype] * factor + half_ulp(want, dtype)
 
 
 def check_grad(got, want, dtype, name: str, group: int = 1) -> float:
@@ -69,8 +74,12 @@ def check_grad(got, want, dtype, name: str, group: int = 1) -> float:
     w = want.detach().double().cpu()
     err = (got.detach().float().cpu().double() - w).abs()
     ratio = (err / grad_bound(w, dtype, group)).max().item()
+    # the factor on the base tolerance this result needs: max (err - half ulp) / tol
+    need = ((err - half_ulp(w, dtype)) / TOL[dtype]).max().item() if dtype != torch.float32 \
+        else (err / TOL[dtype]).max().item()
     print(f"[{name}] max-abs err {err.max().item():.3e} (max |ref| {w.abs().max().item():.3g}); "
-          f"worst err/bound {ratio:.3f}", flush=True)
+          f"worst err/bound {ratio:.3f}; group {group} needs {need:.2f}x the base tolerance",
+          flush=True)
     assert ratio <= 1.0, f"{name}: error {err.max().item():.3e} exceeds the per-element bound"
     return ratio
 

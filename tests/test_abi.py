@@ -165,3 +165,22 @@ def test_kept_ds_budget_decision():
     assert ops.keep_ds_tiles(1, None)          # availability unknown: keep
     with pytest.raises(ValueError):
         ops.set_backward_ds_budget(0.0)
+
+
+def test_noalloc_rejects_oversized_partials():
+    """kf_attn_decode_noalloc refuses partials beyond its 32 MiB static array on
+    the host, before it looks up the array or launches anything: the pointers
+    here are never dereferenced (no device is touched)."""
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.skip("library not built")
+    lib = _lib.load()
+    nbytes = _lib.size_out()
+    B, Hq, Hkv, D = 4096, 64, 8, 128
+    assert lib.kf_attn_decode_workspace_size(B, Hq, Hkv, D, 1024, _lib.DTYPE_BF16,
+                                             ctypes.byref(nbytes)) == 0
+    assert nbytes.value > 32 << 20
+    p = ctypes.c_void_p(1 << 20)  # non-null, never dereferenced
+    rc = lib.kf_attn_decode_noalloc(p, p, p, p, p, p, p, p, 0, 1, p, B, 1024, Hq, Hkv, D, 1024,
+                                    None, None, ctypes.c_float(1e-5), _lib.DTYPE_BF16,
+                                    ctypes.c_void_p(0))
+    assert rc == 4 and b"static scratch" in lib.kf_last_error()

@@ -57,19 +57,3 @@ def test_noalloc_equals_workspace_decode(first, second):
         torch.cuda.synchronize()
         assert torch.equal(got, want)
         assert torch.equal(kc, kc1) and torch.equal(vc, vc1)
-
-
-def test_noalloc_rejects_oversized_partials():
-    """Partials beyond the 32 MiB array are refused before any launch."""
-    lib = _lib.load()
-    nbytes = _lib.size_out()
-    B, Hq, Hkv, D = 4096, 64, 8, 128
-    _lib.check(lib.kf_attn_decode_workspace_size(B, Hq, Hkv, D, 1024, _lib.DTYPE_BF16,
-                                                 ctypes.byref(nbytes)), "size")
-    assert nbytes.value > 32 << 20
-    t = torch.zeros(16, dtype=torch.bfloat16, device=DEV)
-    p = ctypes.c_void_p(t.data_ptr())
-    rc = lib.kf_attn_decode_noalloc(p, p, p, p, p, p, p, p, 0, 1, p, B, 1024, Hq, Hkv, D, 1024,
-                                    None, None, ctypes.c_float(1e-5), _lib.DTYPE_BF16,
-                                    ctypes.c_void_p(0))
-    assert rc == 4 and b"static scratch" in lib.kf_last_error()
