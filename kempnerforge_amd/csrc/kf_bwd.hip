@@ -194,6 +194,7 @@ __device__ __forceinline__ void dkdv_role(
   // DOC: this lane's key's document; KPM: 1 if this lane's key is valid
   const int kdoc = DOC ? drow[min(key, S - 1)] : KPM ? (key < S && drow[min(key, S - 1)] != 0) : 0;
 
+  const uint32_t st_lds = lds_addr(st);
   auto stage_tile = [&](int hl, int qtile, int buf) {
     const int hq = g * n_rep + hl;
     const int64_t bhq = (int64_t)b * Hq + hq;
@@ -206,8 +207,17 @@ __device__ __forceinline__ void dkdv_role(
     // +inf, so they contribute nothing)
     tile_to_lds<BQ, KR, 8, LIST>(dout + (((int64_t)b * S + q0) * Hq + hq) * D, Hq * D, S_.o, w,
                                  lane, S - q0);
-    if (w == 0) row_to_lds(lse2 + bhq * P + q0, S_.l, lane);
-    if (w == 1) row_to_lds(delta + bhq * P + q0, S_.dl, lane);
+    if (LIST) {
+      // the row statistics' LDS addresses from the stage array's base plus
+      // constant offsets: with the pointer into the stage member, the masked
+      // kernels fail to compile ("Operand has incorrect register class")
+      const uint32_t sb = st_lds + (uint32_t)(buf * sizeof(DkdvStage<D>));
+      if (w == 0) dma4(sb + offsetof(DkdvStage<D>, l), (uint32_t)lane * 4u, lse2 + bhq * P + q0);
+      if (w == 1) dma4(sb + offsetof(DkdvStage<D>, dl), (uint32_t)lane * 4u, delta + bhq * P + q0);
+    } else {
+      if (w == 0) row_to_lds(lse2 + bhq * P + q0, S_.l, lane);
+      if (w == 1) row_to_lds(delta + bhq * P + q0, S_.dl, lane);
+    }
     if (DOC && w == 2) dma4(lds_addr(sQD[buf]), (uint32_t)min(q0 + lane, S - 1) * 4u, drow);
   };
   auto stage = [&](int it, int buf) { stage_tile(it / per_head, tile_of(entry(it)), buf); };
@@ -218,9 +228,15 @@ __device__ __forceinline__ void dkdv_role(
   // for P waves, V (read in place, [B, S, Hkv, D]; zero past S) for dS waves
   bf16x8 bf[KS];
   {
-    const bool ok = !DSROLE || key < S;
-    const bf16* src = DSROLE ? v + (((int64_t)b * S + (ok ? key : 0)) * Hkv + g) * D + 8 * hh
-                             : krot + ((int64_t)bh * P + key) * D + 8 * hh;
+    // (masked modes: key and half laundered, so that the 64-bit row address
+    // is formed here per item rather than hoisted out of the persistent loop
+    // and kept in scratch)
+    const int key_l = key;
+    int hh_l = hh;
+    if (LIST) asm volatile("" : "+v"(hh_l));
+    const bool ok = !DSROLE || key_l < S;
+    const bf16* src = DSROLE ? v + (((int64_t)b * S + (ok ? key_l : 0)) * Hkv + g) * D + 8 * hh_l
+                             : krot + ((int64_t)bh * P + key_l) * D + 8 * hh_l;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks)
       bf[ks] = as_bf16x8(ok ? *(const u32x4*)(src + 16 * ks) : u32x4{0u, 0u, 0u, 0u});
@@ -415,7 +431,9 @@ __device__ __forceinline__ void dkdv_role(
   }
 
   if (key >= S) return;
-  const int key_e = key, hoff = 4 * hh;
+  const int key_e = key;
+  int hoff = 4 * hh;
+  if (LIST) asm volatile("" : "+v"(hoff));
   if (DSROLE) {
     bf16* dkr = dk + (((int64_t)b * S + key_e) * Hkv + g) * D + hoff;
     const float* cr = cos + (int64_t)key_e * HALF + hoff;
