@@ -10,13 +10,13 @@ with P = B*Hq*S*(S+1)/2 causal (query, key) pairs (forward 4*D*P, backward
 Also reported: per-kernel HIP-event timings (the library brackets each launch
 on its own stream), the roofline of the dominant kernel, the forward alone
 (C2), the C3 step on packed documents (C3-doc; flops of same-document pairs
-only), the Llama-3-70B shape fwd+bwd (C5: B=1, S=16384, 64 query heads) and its
+only) and with an all-True key_padding_mask (C3-kpm), the Llama-3-70B shape fwd+bwd (C5: B=1, S=16384, 64 query heads) and its
 2048-token probability capture (C5-cap), the KV-cache decode configuration C4
 in GB/s, and the reference's PyTorch paths timed on the host CPU (C3 sample,
 C4 decode, C5-cap capture) next to them.
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline]
-    python bench.py --only c3|c2|c3doc|c5|c5cap|c4 [--steps K] [--warmup W]
+    python bench.py --only c3|c2|c3doc|c3kpm|c5|c5cap|c4 [--steps K] [--warmup W]
         one workload: W untimed steps, K timed steps, then K steps with the
         per-kernel event timing (the shape profiling runs use)
     python bench.py --rocprof-summary DIR [DIR ...] --warmup W --steps K
@@ -96,7 +96,7 @@ class Workloads:
         self.torch, self.ops, self.dev = torch, ops, dev
         self.rope = precompute_rope_frequencies
         self.bf16 = torch.bfloat16
-        self._c3 = self._c5 = self._c4 = self._doc = None
+        self._c3 = self._c5 = self._c4 = self._doc = self._ones = None
 
     # C3 / C2 / C3-doc share the 8B-shape tensors
     def c3_inputs(self):
@@ -150,6 +150,16 @@ class Workloads:
         q, k, v, do, cos, sin = self.c3_inputs()
         doc = self.doc_inputs()[0]
         out = self.ops.attention(q, k, v, cos, sin, causal=True, doc_ids=doc)
+        self.torch.autograd.grad(out, (q, k, v), do)
+
+    def c3kpm_step(self):
+        # the image-prefix VLM arches pass a key_padding_mask on every step,
+        # all-True when nothing is padded
+        q, k, v, do, cos, sin = self.c3_inputs()
+        if self._ones is None:
+            self._ones = self.torch.ones(q.shape[0], q.shape[1], dtype=self.torch.bool,
+                                         device=self.dev)
+        out = self.ops.attention(q, k, v, cos, sin, causal=True, key_padding_mask=self._ones)
         self.torch.autograd.grad(out, (q, k, v), do)
 
     def c5_inputs(self):
@@ -306,7 +316,8 @@ def capture_bytes():
 # --------------------------------------------------------------------------- modes
 def run_only(args, torch, wl):
     """One workload: W untimed steps, K timed steps, K event-timed steps."""
-    steps = {"c3": wl.c3_step, "c2": wl.c2_step, "c3doc": wl.c3doc_step, "c5": wl.c5_step,
+    steps = {"c3": wl.c3_step, "c2": wl.c2_step, "c3doc": wl.c3doc_step,
+             "c3kpm": wl.c3kpm_step, "c5": wl.c5_step,
              "c5cap": wl.c5cap_step, "c4": wl.c4_step}
     fn = steps[args.only]
     secs = timed(torch, fn, args.warmup, args.steps)
@@ -364,6 +375,15 @@ def run_full(args, torch, wl):
              "ms": round(doc_s * 1e3, 4), "TFLOP/s": round(14.0 * D * vis / doc_s / 1e12, 1),
              "visible_pair_frac": round(vis / P, 4),
              "speedup_vs_dense_causal": round(ms_step / (doc_s * 1e3), 2)}
+
+    # C3-kpm: the C3 step with an all-True key_padding_mask (what the VLM arches
+    # pass when nothing is padded): the explicit-mask kernels, dS records kept
+    kpm_s = timed(torch, wl.c3kpm_step, args.warmup, args.steps)
+    kk = kernel_stats(torch, wl.c3kpm_step, args.steps)
+    c3kpm = {"config": "C3-kpm C3 with an all-True key_padding_mask",
+             "ms": round(kpm_s * 1e3, 4), "TFLOP/s": round(flops_step / kpm_s / 1e12, 1),
+             "vs_unmasked_step": round(kpm_s * 1e3 / ms_step, 3),
+             "kernels_us": {n: round(s["avg_us"], 1) for n, s in kk.items()}}
 
     # C5 and C5-cap
     P5 = pairs(C5["B"], C5["Hq"], C5["S"])
@@ -435,6 +455,7 @@ def run_full(args, torch, wl):
         "c2_fwd": c2,
         "c3_graph": c3_graph,
         "c3_doc": c3doc,
+        "c3_kpm": c3kpm,
         "c5": c5,
         "c5_cap": c5cap,
         "decode": decode,
@@ -571,7 +592,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--only", choices=("c3", "c2", "c3doc", "c5", "c5cap", "c4"))
+    ap.add_argument("--only", choices=("c3", "c2", "c3doc", "c3kpm", "c5", "c5cap", "c4"))
     ap.add_argument("--rocprof-summary", nargs="+", metavar="DIR")
     ap.add_argument("--traffic-json", metavar="PATH",
                     help="with --rocprof-summary: write HBM bytes per launch per kernel")

@@ -90,10 +90,12 @@ int kf_attn_bwd_workspace_size(int B, int S, int Hq, int Hkv, int D, int dtype, 
 /* Workspace bytes with which kf_attn_bwd keeps the bf16 dS tiles of the dK/dV
  * pass for dQ instead of recomputing S and dP (one fewer pass over the
  * attention matrix; B*Hq*P*(P+64) bytes extra for causal, 2*B*Hq*P*P for full
- * attention, P = S rounded up to 128).  Applies to the bf16 kernels without
- * key_valid, up to 32 GiB of tiles (and S <= 65536 with doc_ids, whose tiles
- * are then written only where documents meet); otherwise this equals
- * kf_attn_bwd_workspace_size.  kf_attn_bwd takes the faster path whenever
+ * attention, P = S rounded up to 128).  Applies to the bf16 kernels up to
+ * 32 GiB of tiles (and S <= 65536 with doc_ids or key_valid; with doc_ids the
+ * tiles are written only where documents meet; with key_valid only causal
+ * launches keep them, and only for the batch rows whose key 0 is valid, which
+ * have no rows attending past the diagonal: the others recompute, decided on
+ * the device); otherwise this equals kf_attn_bwd_workspace_size.  kf_attn_bwd takes the faster path whenever
  * workspace_bytes reaches this size.  No counterpart in the reference (its
  * SDPA backward manages its own memory). */
 int kf_attn_bwd_workspace_size_ds(int B, int S, int Hq, int Hkv, int D, int dtype, int causal,
@@ -145,8 +147,8 @@ int kf_attn_fwd_rot(const void* q, const void* k, const void* v, const float* ro
                     const int32_t* doc_ids, const int32_t* key_valid, int dtype, void* stream);
 
 /* Workspace bytes of kf_attn_bwd_rot: with_ds = 0 the minimum, 1 with the dS
- * records kept (as kf_attn_bwd_workspace_size_ds: unmasked or doc_ids
- * launches; equal to the minimum where records do not apply).  Smaller than
+ * records kept (as kf_attn_bwd_workspace_size_ds; equal to the minimum where
+ * records do not apply).  Smaller than
  * kf_attn_bwd's by the size of rot. */
 int kf_attn_bwd_rot_workspace_size(int B, int S, int Hq, int Hkv, int D, int dtype, int causal,
                                    int with_ds, size_t* bytes);

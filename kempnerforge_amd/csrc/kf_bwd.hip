@@ -17,11 +17,14 @@
 //               accumulators.  S = Q K^T and dP = dO V^T land in the 32x32 C
 //               layout with one key per lane; P and dS then feed dV^T += dO^T P
 //               and dK^T += Q^T dS as B operands directly.  RoPE backward and the
-//               softmax scale are applied at the dK store.  Without an explicit
-//               mask, and when the caller's workspace holds them, it also writes
-//               every dS tile (bf16) to a record for dQ.
+//               softmax scale are applied at the dK store.  When the caller's
+//               workspace holds them it also writes every dS tile (bf16) to a
+//               record for dQ (with key padding: for the batch rows whose first
+//               key is valid).
 //  dq_ds        (dS records kept) dQ^T += K^T dS^T from the records: one
 //               product per element and one read of the dS bytes, HBM-bound.
+//               With key padding it serves the batch rows whose first key is
+//               valid and dq the others.
 //  dq           (otherwise) forward-shaped: 256 (head, position) rows per
 //               workgroup sharing each K/V tile; recomputes S^T = K Q^T and
 //               dP^T = V dO^T, then dQ^T += K^T dS^T.
@@ -58,8 +61,10 @@ constexpr int BQ = 64;    // queries per dK/dV tile
 
 __host__ __device__ constexpr int pad_len(int S) { return (S + BKV - 1) / BKV * BKV; }
 
-// dS records.  Without an explicit mask the dK/dV kernel writes every dS tile
-// it computes, bf16, for the dQ kernel to read instead of recomputing S and dP.
+// dS records.  The dK/dV kernel writes every dS tile it computes, bf16, for
+// the dQ kernel to read instead of recomputing S and dP (with key padding only
+// for batch rows without guarded rows, i.e. whose key 0 is valid: a guarded
+// row sees keys past the diagonal, outside this layout).
 // A record is one dS wavefront's tile: DSQ query positions x DSK keys of one
 // query head, 4 KB, stored as that wavefront's four MFMA B operands exactly as
 // they sit in registers: [chunk c][lane][8 bf16], lane = 32*hh + key, slot
@@ -69,7 +74,7 @@ __host__ __device__ constexpr int pad_len(int S) { return (S + BKV - 1) / BKV * 
 constexpr int DSQ = DS_REC_Q;  // query positions per record (= BQ)
 constexpr int DSK = DS_REC_K;  // keys per record (one dS wavefront)
 static_assert(DSQ == BQ, "one record row block per query tile");
-constexpr int DS_DOC_MAX_TILES = 1024;  // packed documents keep records up to S = 65536
+constexpr int DS_DOC_MAX_TILES = 1024;  // explicit masks keep records up to S = 65536
 
 // record pair index of (KV head bh, query tile qt, key column k32); nqtp = P / DSQ
 __host__ __device__ inline int64_t ds_pair(int bh, int qt, int k32, int nqtp, int causal) {
@@ -172,7 +177,9 @@ __device__ __forceinline__ void dkdv_role(
     const uint16_t* qlist, int nlist, int32_t (*sQD)[BQ], int fv, u32x4* __restrict__ dsb,
     int nqtp) {
   constexpr bool DOC = MODE == MASK_DOC, KPM = MODE == MASK_KPM, LIST = DOC || KPM;
-  static_assert(!(STORE && KPM), "dS records are not kept with key padding");
+  // key padding keeps records only for a batch row whose first key is valid:
+  // it has no guarded rows, so every dS tile lies in the causal record layout
+  const bool keep = STORE && (!KPM || fv == 0);
   constexpr int KS = D / 16, DT = D / 32, HALF = D / 2;
   constexpr int KR = D / 8;
   // fragment reads run PF MFMAs ahead (2 in the masked modes, whose lists and
@@ -358,7 +365,7 @@ __device__ __forceinline__ void dkdv_role(
     bf16x8 fpre[PF];  // dS waves: first phase-2 fragments, read before the barrier
     // record of this tile (-1: above the causal diagonal, nothing to keep)
     int64_t rec = -1;
-    if (STORE && DSROLE) {
+    if (STORE && DSROLE && keep) {
       const int qt = q0 / DSQ;
       if (!causal || k32 <= 2 * qt + 1)
         rec = ((rec_bh + (causal ? (int64_t)qt * (qt + 1) : (int64_t)qt * nqtp2) + k32) * n_rep +
@@ -578,7 +585,8 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_kernel(
     const float* __restrict__ delta, const bf16* __restrict__ krot, const bf16* __restrict__ v,
     const float* __restrict__ cos, const float* __restrict__ sin, bf16* __restrict__ dq, int S,
     int P, int Hq, int Hkv, int n_rep, int bm_pos, int nqb, int nitems, float scale_log2,
-    float scale, int causal, const int32_t* __restrict__ aux, const int2* __restrict__ ranges) {
+    float scale, int causal, const int32_t* __restrict__ aux, const int2* __restrict__ ranges,
+    int kpm_skip_clean) {
   constexpr bool DOC = MODE == MASK_DOC, KPM = MODE == MASK_KPM, LIST = DOC || KPM;
   constexpr int KS = D / 16, DT = D / 32, HALF = D / 2;
   constexpr int KR = D / 8;
@@ -596,6 +604,11 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_kernel(
   for (int rnd = 0;; ++rnd) {
     const int logical = xcd_item(xi, rnd);
     if (logical < 0) break;
+    // kpm_skip_clean: the batch rows whose key 0 is valid have their dQ from
+    // the dS records (bwd_dq_ds); this launch serves the others
+    if (KPM && kpm_skip_clean &&
+        __builtin_amdgcn_readfirstlane(ranges[(int64_t)(logical / nqb / Hkv) * (P / BN)].y) == 0)
+      continue;
     // per-lane values laundered per item: hoisted out of the persistent loop,
     // the row split and the per-lane 64-bit bases derived from them would be
     // kept in scratch across the item
@@ -828,13 +841,16 @@ __device__ __forceinline__ void vm_wait() {
 // instruction, which turns a record's one-key-per-lane layout into one row per
 // lane.  The kernel moves the dS bytes once and does one product per element;
 // it is bound by HBM.  With packed documents (DOC) the steps walk only the key
-// tiles listed for the query tile, two record columns per 64-key tile.
-template <int D, int HB, bool DOC, int NBUF>
+// tiles listed for the query tile, two record columns per 64-key tile; with key
+// padding (KPM) the causal tiles holding a valid key, in batch rows whose key 0
+// is valid (the others are left to the recompute kernel).
+template <int D, int HB, int MODE, int NBUF>
 __global__ __launch_bounds__(64 * HB) void bwd_dq_ds_kernel(
     const u32x4* __restrict__ dsb, const bf16* __restrict__ krot, const float* __restrict__ cos,
     const float* __restrict__ sin, bf16* __restrict__ dq, int S, int P, int Hq, int Hkv,
     int n_rep, int nqt, int causal, float scale, const int32_t* __restrict__ doc,
     const int2* __restrict__ ranges) {
+  constexpr bool DOC = MODE == MASK_DOC, KPM = MODE == MASK_KPM, LIST = DOC || KPM;
   constexpr int NW = HB, KR = D / 8, DT = D / 32, HALF = D / 2;
   static_assert(NBUF == 3 || NBUF == 4, "ring depth");
   constexpr int KI = DSK * KR / 64;  // 1 KB load instructions per K step
@@ -859,8 +875,21 @@ __global__ __launch_bounds__(64 * HB) void bwd_dq_ds_kernel(
   // DOC: the 64-key tiles whose document range meets this tile's rows (the
   // dK/dV pass listed this query tile for their key blocks, so their records
   // exist); each listed tile is two steps.  Causal: tiles 0 .. qt.
-  __shared__ uint16_t sList[DOC ? DS_DOC_MAX_TILES : 1];
+  // KPM: the tiles 0 .. qt with a valid key (the dK/dV pass listed this query
+  // tile for every key block holding one), when the batch row's key 0 is valid
+  __shared__ uint16_t sList[LIST ? DS_DOC_MAX_TILES : 1];
   __shared__ int sCount;
+  if constexpr (KPM) {
+    const int2* rec = ranges + (int64_t)b * (P / BN);
+    if (__builtin_amdgcn_readfirstlane(rec[0].y) != 0) return;  // guarded rows: dq's
+    if (w == 0) {
+      const int n = kpm_tile_list(rec, 0, qt + 1, [](int, int2 r) { return r.x > 0 ? 1 : 0; },
+                                  sList, lane);
+      if (lane == 0) sCount = n;
+    }
+    __syncthreads();
+    nk = 2 * __builtin_amdgcn_readfirstlane(sCount);
+  }
   if constexpr (DOC) {
     if (w == 0) {
       const int n = doc_tile_list(doc + (int64_t)b * S, qt * DSQ, min(qt * DSQ + DSQ, S),
@@ -872,8 +901,8 @@ __global__ __launch_bounds__(64 * HB) void bwd_dq_ds_kernel(
   }
   // record column (32 keys) of step t
   auto col = [&](int t) -> int {
-    return DOC ? 2 * (__builtin_amdgcn_readfirstlane((int)sList[t >> 1]) & ~DOC_MASK_FLAG) + (t & 1)
-               : t;
+    return LIST ? 2 * (__builtin_amdgcn_readfirstlane((int)sList[t >> 1]) & ~DOC_MASK_FLAG) + (t & 1)
+                : t;
   };
   const u32x4* rec0 = dsb + (ds_pair(bh, qt, 0, nqtp, causal) * n_rep + hg * HB) * 256;
   const bf16* kbase = krot + (int64_t)bh * P * D;
@@ -1098,7 +1127,9 @@ constexpr size_t DS_STORE_MAX = (size_t)32 << 30;
 
 // bytes of the dS records of this launch, or 0 when they are not kept
 size_t ds_bytes(const BwdArgs& a) {
-  if (a.kvalid || (a.doc && pad_len(a.S) / DSQ > DS_DOC_MAX_TILES)) return 0;
+  // key padding: the causal layout only (its batch rows without guarded rows)
+  if ((a.kvalid && !a.causal) || ((a.doc || a.kvalid) && pad_len(a.S) / DSQ > DS_DOC_MAX_TILES))
+    return 0;
   const size_t nqtp = (size_t)pad_len(a.S) / DSQ;
   const size_t pairs = a.causal ? nqtp * (nqtp + 1) : 2 * nqtp * nqtp;
   const size_t bytes = (size_t)a.B * a.Hq * pairs * 4096;
@@ -1129,8 +1160,12 @@ int launch_dq_ds(const BwdArgs& a, const Ws& w) {
   // buffers 485 against 517 us at S = 4096, 3115 against 2967 at S = 16384)
   const bool deep = HB == 4 && a.S <= 8192;
   KF_LAUNCH("bwd_dq_ds",
-            (a.doc ? (deep ? bwd_dq_ds_kernel<D, HB, true, 4> : bwd_dq_ds_kernel<D, HB, true, 3>)
-                   : (deep ? bwd_dq_ds_kernel<D, HB, false, 4> : bwd_dq_ds_kernel<D, HB, false, 3>)),
+            (a.doc      ? (deep ? bwd_dq_ds_kernel<D, HB, MASK_DOC, 4>
+                                : bwd_dq_ds_kernel<D, HB, MASK_DOC, 3>)
+             : a.kvalid ? (deep ? bwd_dq_ds_kernel<D, HB, MASK_KPM, 4>
+                                : bwd_dq_ds_kernel<D, HB, MASK_KPM, 3>)
+                        : (deep ? bwd_dq_ds_kernel<D, HB, MASK_NONE, 4>
+                                : bwd_dq_ds_kernel<D, HB, MASK_NONE, 3>)),
             dim3(a.B * a.Hkv * (n_rep / HB) * nqt), dim3(64 * HB), 0, a.stream, w.dsb, w.krot,
             a.cos, a.sin, (bf16*)a.dq, a.S, P, a.Hq, a.Hkv, n_rep, nqt, a.causal, a.scale,
             a.doc, w.ranges);
@@ -1180,7 +1215,8 @@ int launch_bwd(const BwdArgs& a, void* workspace, bool keep_ds) {
   KF_LAUNCH("bwd_dkdv",
             (mode == MASK_DOC   ? (keep_ds ? bwd_dkdv_kernel<D, MASK_DOC, true>
                                            : bwd_dkdv_kernel<D, MASK_DOC, false>)
-             : mode == MASK_KPM ? bwd_dkdv_kernel<D, MASK_KPM, false>
+             : mode == MASK_KPM ? (keep_ds ? bwd_dkdv_kernel<D, MASK_KPM, true>
+                                           : bwd_dkdv_kernel<D, MASK_KPM, false>)
              : keep_ds          ? bwd_dkdv_kernel<D, MASK_NONE, true>
                                 : bwd_dkdv_kernel<D, MASK_NONE, false>),
             dim3(std::min(nkb * a.B * a.Hkv, grid_cap)), dim3(512), 0, a.stream, w.krot, (const bf16*)a.v,
@@ -1188,10 +1224,14 @@ int launch_bwd(const BwdArgs& a, void* workspace, bool keep_ds) {
             (bf16*)a.dv, a.S, P, a.Hq, a.Hkv, n_rep, nkb, nkb * a.B * a.Hkv,
             scale_log2, a.scale, a.causal, aux, w.ranges, w.dsb, order);
   KF_CHECK_LAUNCH();
-  if (keep_ds)
-    return n_rep % 4 == 0   ? launch_dq_ds<D, 4>(a, w)
-           : n_rep % 2 == 0 ? launch_dq_ds<D, 2>(a, w)
-                            : launch_dq_ds<D, 1>(a, w);
+  if (keep_ds) {
+    const int rc = n_rep % 4 == 0   ? launch_dq_ds<D, 4>(a, w)
+                   : n_rep % 2 == 0 ? launch_dq_ds<D, 2>(a, w)
+                                    : launch_dq_ds<D, 1>(a, w);
+    // key padding: the batch rows with guarded rows still recompute their dQ
+    // (the records launch skipped them; this one skips the rest)
+    if (rc || mode != MASK_KPM) return rc;
+  }
   const int bm_pos = DQ_ROWS / n_rep;
   const int nqb = (a.S + bm_pos - 1) / bm_pos;
   KF_LAUNCH("bwd_dq",
@@ -1201,7 +1241,7 @@ int launch_bwd(const BwdArgs& a, void* workspace, bool keep_ds) {
             dim3(std::min(nqb * a.B * a.Hkv, grid_cap)), dim3(512), 0, a.stream, w.qrot,
             (const bf16*)a.dout, w.lse2, w.delta, w.krot, (const bf16*)a.v, a.cos, a.sin, (bf16*)a.dq, a.S, P,
             a.Hq, a.Hkv, n_rep, bm_pos, nqb, nqb * a.B * a.Hkv, scale_log2, a.scale, a.causal,
-            aux, w.ranges);
+            aux, w.ranges, (int)keep_ds);
   KF_CHECK_LAUNCH();
   return KF_OK;
 }

@@ -243,12 +243,15 @@ def bwd_raw(q, k, v, cos, sin, out, lse, dout, *, causal: bool, doc_ids=None,
     _lib.check(lib.kf_attn_bwd_workspace_size(B, S, Hq, Hkv, D, dt, ctypes.byref(nbytes)),
                "kf_attn_bwd_workspace_size")
     low_memory = _BWD_LOW_MEMORY if low_memory is None else low_memory
-    if not low_memory and kv is None:  # key padding never keeps dS
+    # key padding keeps dS only causally, and only for the batch rows whose key
+    # 0 is valid (decided on the device; the others recompute)
+    if not low_memory and (kv is None or causal):
         with_ds = _lib.size_out()
         _lib.check(lib.kf_attn_bwd_workspace_size_ds(B, S, Hq, Hkv, D, dt, int(causal),
                                                      ctypes.byref(with_ds)),
                    "kf_attn_bwd_workspace_size_ds")
-        key = ("bwd", q.device, B, S, Hq, Hkv, D, q.dtype, bool(causal), doc is not None)
+        key = ("bwd", q.device, B, S, Hq, Hkv, D, q.dtype, bool(causal), doc is not None,
+               kv is not None)
         if _keep_ds_for(key, with_ds.value - nbytes.value, q.device):
             nbytes = with_ds
     ws = _workspace(nbytes.value, q.device)
@@ -359,12 +362,13 @@ def bwd_rot_raw(rot, v, cos, sin, out, lse, dout, *, causal: bool, doc_ids=None,
                                                   ctypes.byref(nbytes)),
                "kf_attn_bwd_rot_workspace_size")
     low_memory = _BWD_LOW_MEMORY if low_memory is None else low_memory
-    if not low_memory and kv is None:  # key padding never keeps dS
+    if not low_memory and (kv is None or causal):  # as in bwd_raw
         with_ds = _lib.size_out()
         _lib.check(lib.kf_attn_bwd_rot_workspace_size(B, S, Hq, Hkv, D, dt, int(causal), 1,
                                                       ctypes.byref(with_ds)),
                    "kf_attn_bwd_rot_workspace_size")
-        key = ("bwd_rot", out.device, B, S, Hq, Hkv, D, out.dtype, bool(causal), doc is not None)
+        key = ("bwd_rot", out.device, B, S, Hq, Hkv, D, out.dtype, bool(causal), doc is not None,
+               kv is not None)
         if _keep_ds_for(key, with_ds.value - nbytes.value, out.device):
             nbytes = with_ds
     ws = _workspace(nbytes.value, out.device)

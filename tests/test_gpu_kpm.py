@@ -195,3 +195,52 @@ def test_module_key_padding_mask(dtype):
     assert p.shape == (2, 8, S, S)
     assert p[0, :, 70:, :70].abs().max().item() == 0.0  # padded keys get nothing
     assert p[0, :, :70, :].float().sum(-1).sub(1).abs().max().item() < 2e-2  # guarded rows
+
+
+@pytest.mark.parametrize("cfg", [(3, 300, 8, 2, 128), (2, 200, 4, 4, 64), (2, 260, 6, 3, 128)],
+                         ids=lambda c: "-".join(map(str, c)))
+def test_backward_records_path(cfg):
+    """Batch rows whose key 0 is valid keep the dS records (dQ from them), rows
+    with guarded rows recompute dQ, in one launch: dK/dV are the same bits as
+    with low_memory=True (no records), dQ of the guarded batch row too, and
+    every gradient is within tolerance of the oracle."""
+    B, S, Hq, Hkv, D = cfg
+    announce(f"kpm records {cfg}")
+    dtype = torch.bfloat16
+    q, k, v, do, cos, sin = _inputs(dtype, B, S, Hq, Hkv, D, seed=11)
+    kpm = torch.ones(B, S, dtype=torch.bool)
+    kpm[0, S // 3: S // 3 + 40] = False           # key 0 valid: records
+    kpm[1, : 45] = False                          # leading padding: guarded rows, recompute
+    if B > 2:
+        kpm[2, 130:200] = False                   # whole tiles and ragged edges, records
+    args = [t.to(DEV) for t in (q, k, v, cos, sin)]
+    out, lse = ops.fwd_raw(*args, causal=True, k_rotated=False, key_padding_mask=kpm.to(DEV))
+    kept = ops.bwd_raw(*args, out, lse, do.to(DEV), causal=True, key_padding_mask=kpm.to(DEV))
+    recomputed = ops.bwd_raw(*args, out, lse, do.to(DEV), causal=True,
+                             key_padding_mask=kpm.to(DEV), low_memory=True)
+    torch.cuda.synchronize()
+    assert torch.equal(kept[1], recomputed[1]) and torch.equal(kept[2], recomputed[2])
+    assert torch.equal(kept[0][1], recomputed[0][1])  # the guarded batch row's dQ
+    # the records path is the one taken for the other rows: a different
+    # accumulation than the recompute kernel's, so not the same bits
+    assert not torch.equal(kept[0][0], recomputed[0][0])
+    dq, dk, dv = ref.attention_bwd(q, k, v, cos, sin, do, key_padding_mask=kpm)
+    for got, want, name in ((kept[0], dq, "dq"), (kept[1], dk, "dk"), (kept[2], dv, "dv")):
+        check_grad(got, want, dtype, name, group=Hq // Hkv if name != "dq" else 1)
+
+
+def test_all_valid_mask_equals_unmasked_backward():
+    """An all-True key_padding_mask (what the VLM arches pass when nothing is
+    padded) takes the masked kernels with the dS records kept; every tile is
+    listed without an element test, so dQ, dK and dV equal the unmasked
+    backward's bit for bit (same out and LSE in)."""
+    B, S, Hq, Hkv, D = 2, 1100, 32, 8, 128
+    announce("kpm all-valid == unmasked backward")
+    q, k, v, do, cos, sin = (t.to(DEV) for t in _inputs(torch.bfloat16, B, S, Hq, Hkv, D, seed=5))
+    ones = torch.ones(B, S, dtype=torch.bool, device=DEV)
+    out, lse = ops.fwd_raw(q, k, v, cos, sin, causal=True, k_rotated=False)
+    g_mask = ops.bwd_raw(q, k, v, cos, sin, out, lse, do, causal=True, key_padding_mask=ones)
+    g_none = ops.bwd_raw(q, k, v, cos, sin, out, lse, do, causal=True)
+    torch.cuda.synchronize()
+    for a, b_, name in zip(g_mask, g_none, ("dq", "dk", "dv")):
+        assert torch.equal(a, b_), f"{name}: max diff {(a.float() - b_.float()).abs().max().item()}"
