@@ -175,7 +175,7 @@ __device__ __forceinline__ void dkdv_role(
     bf16* __restrict__ dv, int S, int P, int Hq, int Hkv, int n_rep, int b, int g, int bh, int k0,
     int w, int lane, float scale_log2, float scale, int causal, const int32_t* __restrict__ drow,
     const uint16_t* qlist, int nlist, int32_t (*sQD)[BQ], int fv, u32x4* __restrict__ dsb,
-    int nqtp) {
+    int nqtp, bool live) {
   constexpr bool DOC = MODE == MASK_DOC, KPM = MODE == MASK_KPM, LIST = DOC || KPM;
   // key padding keeps records only for a batch row whose first key is valid:
   // it has no guarded rows, so every dS tile lies in the causal record layout
@@ -192,7 +192,9 @@ __device__ __forceinline__ void dkdv_role(
   const int nqt = (S + BQ - 1) / BQ;
   const int qt0 = causal ? k0 / BQ : 0;
   const int per_head = LIST ? nlist : nqt - qt0;
-  const int total = per_head > 0 ? per_head * n_rep : 0;
+  // (live false: no query tile, dK / dV stored as zeros; a later launch
+  // writes this item's results)
+  const int total = per_head > 0 && live ? per_head * n_rep : 0;
   // iteration -> query tile entry (tile | DOC_MASK_FLAG when listed), head-major
   auto entry = [&](int it) -> int {
     return LIST ? __builtin_amdgcn_readfirstlane((int)qlist[it % per_head]) : qt0 + it % per_head;
@@ -489,7 +491,12 @@ __device__ __forceinline__ void dkdv_stage_first(
   if (w == 2) dma4(lds_addr(sqd), (uint32_t)min(q0 + lane, S - 1) * 4u, drow);
 }
 
-template <int D, int MODE, bool STORE>
+// kpm_flags (causal key padding; per batch row, 1 = every key valid): rows
+// without padding run the unmasked kernel (SPLIT), the others the KPM one,
+// which runs after it and skips the rows without padding; the unmasked launch
+// walks no query tile for the padded rows' items (their dK / dV are written
+// as zeros, then overwritten by the KPM launch).
+template <int D, int MODE, bool STORE, bool SPLIT = false>
 __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(
     const bf16* __restrict__ krot, const bf16* __restrict__ v, const bf16* __restrict__ qrot,
     const bf16* __restrict__ dout, const float* __restrict__ lse2, const float* __restrict__ delta,
@@ -497,7 +504,7 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(
     bf16* __restrict__ dv, int S, int P, int Hq, int Hkv, int n_rep, int nkb, int nitems,
     float scale_log2,
     float scale, int causal, const int32_t* __restrict__ aux, const int2* __restrict__ ranges,
-    u32x4* __restrict__ dsb, const int* __restrict__ order) {
+    u32x4* __restrict__ dsb, const int* __restrict__ order, const int* __restrict__ kpm_flags) {
   constexpr bool DOC = MODE == MASK_DOC, KPM = MODE == MASK_KPM;
   __shared__ __attribute__((aligned(16))) DkdvStage<D> st[2];
   __shared__ __attribute__((aligned(16))) u32x4 sP[4 * 4 * 64];  // [key group][chunk][lane]
@@ -523,6 +530,8 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(
     const int k0 = kb * BKV;
     const int32_t* drow = DOC || KPM ? aux + (int64_t)b * S : nullptr;
     const int2* rec = ranges + (int64_t)b * (P / BN);
+    if (KPM && kpm_flags != nullptr && kpm_flags[b] != 0) continue;
+    const bool live = !SPLIT || kpm_flags[b] != 0;
     int nlist = 0, fv = 0;
     if constexpr (KPM) {
       if (w == 0) {
@@ -564,12 +573,12 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(
       dkdv_role<D, true, MODE, STORE>(st, sP, krot, v, qrot, dout, lse2, delta, cos, sin, dk,
                                       dv, S, P, Hq, Hkv, n_rep, b, g, bh, k0, w, lane,
                                       scale_log2, scale, causal, drow, sList, nlist, sQD, fv,
-                                      dsb, P / DSQ);
+                                      dsb, P / DSQ, live);
     else
       dkdv_role<D, false, MODE, STORE>(st, sP, krot, v, qrot, dout, lse2, delta, cos, sin, dk,
                                        dv, S, P, Hq, Hkv, n_rep, b, g, bh, k0, w, lane,
                                        scale_log2, scale, causal, drow, sList, nlist, sQD, fv,
-                                       dsb, P / DSQ);
+                                       dsb, P / DSQ, live);
     __syncthreads();  // LDS of this item is free for the next
   }
 }
@@ -1212,6 +1221,21 @@ int launch_bwd(const BwdArgs& a, void* workspace, bool keep_ds) {
   const int grid_cap = a.doc || a.kvalid ? INT_MAX : device_cu_count() / 8 * 8;
   const int mode = a.doc ? MASK_DOC : a.kvalid ? MASK_KPM : MASK_NONE;
   const int32_t* aux = a.doc ? a.doc : a.kvalid;
+  // causal key padding: the batch rows whose keys are all valid go to the
+  // unmasked (persistent) kernel first, the rest to the KPM one
+  const int* kpm_flags = mode == MASK_KPM && a.causal ? w.counts : nullptr;
+  if (kpm_flags) {
+    const int rc = launch_kpm_row_flags(w.ranges, P / BN, a.S, a.B, w.counts, a.stream);
+    if (rc) return rc;
+    KF_LAUNCH("bwd_dkdv",
+              (keep_ds ? bwd_dkdv_kernel<D, MASK_NONE, true, true>
+                       : bwd_dkdv_kernel<D, MASK_NONE, false, true>),
+              dim3(std::min(nkb * a.B * a.Hkv, device_cu_count() / 8 * 8)), dim3(512), 0, a.stream,
+              w.krot, (const bf16*)a.v, w.qrot, (const bf16*)a.dout, w.lse2, w.delta, a.cos,
+              a.sin, (bf16*)a.dk, (bf16*)a.dv, a.S, P, a.Hq, a.Hkv, n_rep, nkb,
+              nkb * a.B * a.Hkv, scale_log2, a.scale, a.causal, nullptr, w.ranges, w.dsb,
+              nullptr, kpm_flags);
+  }
   KF_LAUNCH("bwd_dkdv",
             (mode == MASK_DOC   ? (keep_ds ? bwd_dkdv_kernel<D, MASK_DOC, true>
                                            : bwd_dkdv_kernel<D, MASK_DOC, false>)
@@ -1222,7 +1246,7 @@ int launch_bwd(const BwdArgs& a, void* workspace, bool keep_ds) {
             dim3(std::min(nkb * a.B * a.Hkv, grid_cap)), dim3(512), 0, a.stream, w.krot, (const bf16*)a.v,
             w.qrot, (const bf16*)a.dout, w.lse2, w.delta, a.cos, a.sin, (bf16*)a.dk,
             (bf16*)a.dv, a.S, P, a.Hq, a.Hkv, n_rep, nkb, nkb * a.B * a.Hkv,
-            scale_log2, a.scale, a.causal, aux, w.ranges, w.dsb, order);
+            scale_log2, a.scale, a.causal, aux, w.ranges, w.dsb, order, kpm_flags);
   KF_CHECK_LAUNCH();
   if (keep_ds) {
     const int rc = n_rep % 4 == 0   ? launch_dq_ds<D, 4>(a, w)

@@ -212,7 +212,8 @@ __global__ __launch_bounds__(256, 2) void fwd_mfma_kernel(
     const bf16* __restrict__ krot, const bf16* __restrict__ vn, bf16* __restrict__ out,
     float* __restrict__ lse, int Sq, int Sk, int Skp, int krows, int Hq, int Hkv, int n_rep,
     int bm_pos, int nqb, float scale_log2, int causal, const int32_t* __restrict__ aux,
-    const int2* __restrict__ ranges, bf16* __restrict__ qrot, const int* __restrict__ order) {
+    const int2* __restrict__ ranges, bf16* __restrict__ qrot, const int* __restrict__ order,
+    const int* __restrict__ kpm_flags) {
   constexpr bool DOC = MODE == MASK_DOC, KPM = MODE == MASK_KPM, LIST = DOC || KPM;
   constexpr int KS = D / 16, DT = D / 32;
   constexpr int KR = D / 8;  // 16-byte chunks per K / V row
@@ -238,6 +239,8 @@ __global__ __launch_bounds__(256, 2) void fwd_mfma_kernel(
   int ntiles = (kend + BN - 1) / BN;
   const int32_t* arow = LIST ? aux + (int64_t)ri.b * Sk : nullptr;
   const int2* rec = ranges + (int64_t)ri.b * (Skp / BN);
+  // kpm_flags (per batch row, 1 = every key valid): those rows are fwd32_kernel's
+  if (KPM && kpm_flags != nullptr && kpm_flags[ri.b] != 0) return;
   const bf16* kbase = krot + (int64_t)bh * krows * D;
   const bf16* vbase = vn + (int64_t)bh * D * Skp;  // V^T, keys in fragment order
   auto stage = [&](int t, int buf) {
@@ -484,7 +487,8 @@ __global__ __launch_bounds__(256, 3) void fwd32_kernel(
     const bf16* __restrict__ q, const float* __restrict__ cos, const float* __restrict__ sin,
     const bf16* __restrict__ krot, const bf16* __restrict__ vn, bf16* __restrict__ out,
     float* __restrict__ lse, int Sq, int Sk, int Skp, int krows, int Hq, int Hkv, int n_rep,
-    int bm_pos, int nqb, float scale_log2, int causal, bf16* __restrict__ qrot) {
+    int bm_pos, int nqb, float scale_log2, int causal, bf16* __restrict__ qrot,
+    const int* __restrict__ kpm_flags) {
   constexpr int KS = D / 16, DT = D / 32;
   constexpr int KR = D / 8;  // 16-byte chunks per K row
   __shared__ __attribute__((aligned(16))) bf16 sK[2][FBN * D];
@@ -493,6 +497,9 @@ __global__ __launch_bounds__(256, 3) void fwd32_kernel(
   const int tid = threadIdx.x, w = wave_id(), lane = tid & 63, hh = lane >> 5, c32 = lane & 31;
   const int logical = xcd_logical_id(blockIdx.x, gridDim.x);
   const RowInfo ri = row_info(logical, nqb, Hkv, n_rep, bm_pos, Sq, w * 32 + c32);
+  // key padding (kpm_flags per batch row, 1 = every key valid): only the rows
+  // without padding (plain causal attention); fwd_mfma_kernel takes the others
+  if (kpm_flags != nullptr && kpm_flags[ri.b] == 0) return;
   const int bh = ri.b * Hkv + ri.g;
   const int kend = causal ? min(Sk, min(ri.p0 + bm_pos, Sq)) : Sk;
   const int ntiles = (kend + FBN - 1) / FBN;
@@ -982,6 +989,25 @@ int launch_kv_prep(const FwdArgs& a, void* krot_, int krows, void* vn_, int Skp,
   return KF_OK;
 }
 
+namespace {
+// flags[b] = 1 when every key of batch row b is valid (from its tile records),
+// else 0: one wavefront per batch row
+__global__ __launch_bounds__(64) void kpm_row_flags_kernel(const int2* __restrict__ ranges,
+                                                           int rstride, int S,
+                                                           int* __restrict__ flags) {
+  const bool all = kpm_all_valid(ranges + (int64_t)blockIdx.x * rstride, S, threadIdx.x);
+  if (threadIdx.x == 0) flags[blockIdx.x] = all ? 1 : 0;
+}
+}  // namespace
+
+int launch_kpm_row_flags(const int2* ranges, int rstride, int S, int B, int* flags,
+                         hipStream_t stream) {
+  KF_LAUNCH("kpm_row_flags", kpm_row_flags_kernel, dim3(B), dim3(64), 0, stream, ranges, rstride,
+            S, flags);
+  KF_CHECK_LAUNCH();
+  return KF_OK;
+}
+
 size_t rot_bytes(int B, int S, int Hq, int Hkv, int D) {
   return ((size_t)B * Hkv + (size_t)B * Hq) * (size_t)((S + 127) / 128 * 128) * D *
          sizeof(uint16_t);
@@ -1021,11 +1047,19 @@ int mask_mode(const FwdArgs& a) { return a.doc ? MASK_DOC : a.kvalid ? MASK_KPM 
 
 template <int D, int MODE>
 void launch_fwd_kernel(const FwdArgs& a, const FwdWs& w, int Skp, int n_rep, int bm_pos, int nqb,
-                       unsigned nblk, const int* order) {
+                       unsigned nblk, const int* order, const int* kpm_flags = nullptr) {
   KF_LAUNCH("fwd_mfma", (fwd_mfma_kernel<D, MODE>), dim3(nblk), dim3(256), 0, a.stream,
             (const bf16*)a.q, a.cos, a.sin, w.krot, w.vn, (bf16*)a.out, a.lse, a.Sq, a.Sk, Skp,
             w.krows, a.Hq, a.Hkv, n_rep, bm_pos, nqb, a.scale * kLog2e, a.causal,
-            a.doc ? a.doc : a.kvalid, w.ranges, w.qrot, order);
+            a.doc ? a.doc : a.kvalid, w.ranges, w.qrot, order, kpm_flags);
+}
+
+template <int D>
+void launch_fwd32(const FwdArgs& a, const FwdWs& w, int Skp, int n_rep, int bm_pos, int nqb,
+                  unsigned nblk, const int* kpm_flags) {
+  KF_LAUNCH("fwd_mfma", fwd32_kernel<D>, dim3(nblk), dim3(256), 0, a.stream, (const bf16*)a.q,
+            a.cos, a.sin, w.krot, w.vn, (bf16*)a.out, a.lse, a.Sq, a.Sk, Skp, w.krows, a.Hq,
+            a.Hkv, n_rep, bm_pos, nqb, a.scale * kLog2e, a.causal, w.qrot, kpm_flags);
 }
 
 template <int D>
@@ -1036,12 +1070,16 @@ void launch_fwd_mode(const FwdArgs& a, const FwdWs& w, int Skp, int n_rep, int b
       launch_fwd_kernel<D, MASK_DOC>(a, w, Skp, n_rep, bm_pos, nqb, nblk, w.order);
       break;
     case MASK_KPM:
-      launch_fwd_kernel<D, MASK_KPM>(a, w, Skp, n_rep, bm_pos, nqb, nblk, nullptr);
+      // causal self-attention: batch rows without padding run the unmasked
+      // kernel, the others the masked one (each launch skips the other's rows)
+    {
+      // (w.counts holds the per-row flags: launch_kpm_row_flags in fwd_mfma)
+      const int* flags = a.causal && a.Sq == a.Sk ? w.counts : nullptr;
+      if (flags) launch_fwd32<D>(a, w, Skp, n_rep, bm_pos, nqb, nblk, flags);
+      launch_fwd_kernel<D, MASK_KPM>(a, w, Skp, n_rep, bm_pos, nqb, nblk, nullptr, flags);
       break;
-    default:
-      KF_LAUNCH("fwd_mfma", fwd32_kernel<D>, dim3(nblk), dim3(256), 0, a.stream, (const bf16*)a.q,
-                a.cos, a.sin, w.krot, w.vn, (bf16*)a.out, a.lse, a.Sq, a.Sk, Skp, w.krows, a.Hq,
-                a.Hkv, n_rep, bm_pos, nqb, a.scale * kLog2e, a.causal, w.qrot);
+    }
+    default: launch_fwd32<D>(a, w, Skp, n_rep, bm_pos, nqb, nblk, nullptr);
   }
 }
 
@@ -1084,6 +1122,10 @@ int fwd_mfma(const FwdArgs& a, void* workspace) {
     // the query blocks by their listed key tiles, most first
     rc = launch_doc_order(a.doc, w.ranges, a.Sq, Skp / BN, bm_pos, a.B, nqb, 0, w.counts,
                           w.order, a.stream);
+    if (rc) return rc;
+  }
+  if (a.kvalid && a.causal && a.Sq == a.Sk) {
+    rc = launch_kpm_row_flags(w.ranges, Skp / BN, a.Sk, a.B, w.counts, a.stream);
     if (rc) return rc;
   }
   if (a.D == 128) launch_fwd_mode<128>(a, w, Skp, n_rep, bm_pos, nqb, (unsigned)nblk);

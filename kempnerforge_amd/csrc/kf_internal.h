@@ -79,6 +79,10 @@ int launch_kv_prep(const FwdArgs& a, void* krot, int krows, void* vn, int Skp, i
 // their diagonal on; else query blocks listing key tiles up to theirs.
 int launch_doc_order(const int32_t* doc, const int2* ranges, int S, int rstride, int rows, int B,
                      int nblk, int key_side, int* counts, int* order, hipStream_t stream);
+// Key padding: flags[b] = 1 when every key of batch row b is valid (ranges:
+// kv_prep's tile records, rstride per batch row), else 0.
+int launch_kpm_row_flags(const int2* ranges, int rstride, int S, int B, int* flags,
+                         hipStream_t stream);
 // bytes of FwdArgs::rot
 size_t rot_bytes(int B, int S, int Hq, int Hkv, int D);
 size_t fwd_mfma_workspace(int B, int Sk, int Hkv, int D);

@@ -336,6 +336,20 @@ __device__ __forceinline__ int kpm_first_valid(const int2* __restrict__ rec, int
   return INT_MAX;
 }
 
+// True when every key of the batch row is valid (tile t holds min(64, S - 64 t)
+// valid keys), from the row's tile records; wavefront-uniform.  Such a row is
+// plain causal attention: the launches with key padding hand its rows to the
+// unmasked kernels.
+__device__ __forceinline__ bool kpm_all_valid(const int2* __restrict__ rec, int S, int lane) {
+  const int ntiles = (S + BN - 1) / BN;
+  bool short_tile = false;
+  for (int base = 0; base < ntiles; base += 64) {
+    const int t = base + lane;
+    if (t < ntiles) short_tile |= rec[t].x != min(BN, S - BN * t);
+  }
+  return __builtin_amdgcn_ballot_w64(short_tile) == 0;
+}
+
 // Lists, in ascending order, tiles t in [t0, t1) for which pick(t, rec[t])
 // returns nonzero (2: with DOC_MASK_FLAG).  Same contract as doc_tile_list.
 template <typename Pick>
