@@ -383,7 +383,8 @@ def run_full(args, torch, wl):
     c3kpm = {"config": "C3-kpm C3 with an all-True key_padding_mask",
              "ms": round(kpm_s * 1e3, 4), "TFLOP/s": round(flops_step / kpm_s / 1e12, 1),
              "vs_unmasked_step": round(kpm_s * 1e3 / ms_step, 3),
-             "kernels_us": {n: round(s["avg_us"], 1) for n, s in kk.items()}}
+             "kernels_us": {n: round(s["avg_us"], 1) for n, s in kk.items()},
+             "launches_per_step": {n: s["launches"] // args.steps for n, s in kk.items()}}
 
     # C5 and C5-cap
     P5 = pairs(C5["B"], C5["Hq"], C5["S"])
@@ -469,7 +470,7 @@ def _short(name: str) -> str:
     """Kernel symbol -> the launcher's name (kf::..._kernel<...> -> ...)."""
     m = re.search(r"(kv_prep|fwd_mfma|fwd32|q_prep_bwd|bwd_dkdv|bwd_dq_ds|bwd_dq|decode_stream|"
                   r"decode_merge|capture_probs_mfma|kv_append|append|doc_block_tiles|"
-                  r"order_by_count)_kernel", name)
+                  r"order_by_count|kpm_row_flags)_kernel", name)
     if m:
         # fwd32_kernel is the unmasked forward's kernel, launched as fwd_mfma
         return {"capture_probs_mfma": "capture_probs", "append": "kv_append",

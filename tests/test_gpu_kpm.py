@@ -244,3 +244,34 @@ def test_all_valid_mask_equals_unmasked_backward():
     torch.cuda.synchronize()
     for a, b_, name in zip(g_mask, g_none, ("dq", "dk", "dv")):
         assert torch.equal(a, b_), f"{name}: max diff {(a.float() - b_.float()).abs().max().item()}"
+
+
+def test_mixed_batch_split_paths():
+    """A batch mixing a row without padding (unmasked forward and dK/dV kernels,
+    dS records), a row with padding in the middle (masked kernels, records) and
+    a row with leading padding (masked kernels, recomputed dQ): every output
+    and gradient within tolerance of the oracle, and the unpadded row equal to
+    the same row run without any mask, bit for bit."""
+    B, S, Hq, Hkv, D = 3, 520, 8, 2, 128
+    announce("kpm mixed batch")
+    dtype = torch.bfloat16
+    q, k, v, do, cos, sin = _inputs(dtype, B, S, Hq, Hkv, D, seed=21)
+    kpm = torch.ones(B, S, dtype=torch.bool)
+    kpm[1, 200:290] = False
+    kpm[2, :77] = False
+    qd, kd, vd = (t.to(DEV).requires_grad_(True) for t in (q, k, v))
+    out = ops.attention(qd, kd, vd, cos.to(DEV), sin.to(DEV), key_padding_mask=kpm.to(DEV))
+    out.backward(do.to(DEV))
+    # row 0 alone, no mask
+    q0, k0, v0 = (t[:1].to(DEV).requires_grad_(True) for t in (q, k, v))
+    out0 = ops.attention(q0, k0, v0, cos.to(DEV), sin.to(DEV))
+    out0.backward(do[:1].to(DEV))
+    torch.cuda.synchronize()
+    assert torch.equal(out[:1], out0)
+    for a, b_ in ((qd.grad, q0.grad), (kd.grad, k0.grad), (vd.grad, v0.grad)):
+        assert torch.equal(a[:1], b_)
+    o_ref, _ = ref.attention_fwd(q, k, v, cos, sin, key_padding_mask=kpm)
+    assert max_abs(out, o_ref) <= TOL[dtype]
+    dq, dk, dv = ref.attention_bwd(q, k, v, cos, sin, do, key_padding_mask=kpm)
+    for got, want, name in ((qd.grad, dq, "dq"), (kd.grad, dk, "dk"), (vd.grad, dv, "dv")):
+        check_grad(got, want, dtype, name, group=Hq // Hkv if name != "dq" else 1)
