@@ -1038,6 +1038,156 @@ __global__ __launch_bounds__(64 * HB) void bwd_dq_ds_kernel(
   }
 }
 
+// dQ from the dS records, two query tiles per workgroup (unmasked causal
+// launches, head_dim 128, 4 query heads per workgroup): 8 wavefronts, one per
+// (tile, head); the tiles are adjacent (2p, 2p + 1), so they share the staged
+// K rows of every step but the later tile's last two.  Per step the stage
+// holds the K rows (8 KB, one load per wavefront) and the 8 records (4 KB
+// each); a ring of three stages, two steps in flight.  Against one tile per
+// workgroup: half the K-row traffic and half the workgroups (their start-up
+// and epilogue), and two wavefronts per SIMD.  A wavefront whose tile has no
+// record at a step (the earlier tile at the later tile's last two steps)
+// loads its last record again (the load counts stay equal across wavefronts)
+// and skips the products.
+template <int D, int NBUF>
+__global__ __launch_bounds__(512) void bwd_dq_ds2_kernel(
+    const u32x4* __restrict__ dsb, const bf16* __restrict__ krot, const float* __restrict__ cos,
+    const float* __restrict__ sin, bf16* __restrict__ dq, int S, int P, int Hq, int Hkv,
+    int n_rep, int nqt, float scale) {
+  constexpr int HB = 4, NW = 8, KR = D / 8, DT = D / 32, HALF = D / 2;
+  constexpr int KI = DSK * KR / 64;  // 1 KB load instructions per K step
+  static_assert(KI % NW == 0, "K rows must split evenly over the wavefronts");
+  constexpr int NLOAD = KI / NW + 4;
+  struct Stage {
+    bf16 k[DSK * D];
+    u32x4 ds[NW * 256];
+  };
+  constexpr int RING_B = NBUF * (int)sizeof(Stage), OUT_B = NW * 64 * D * 2;
+  __shared__ __attribute__((aligned(16))) char smem[RING_B > OUT_B ? RING_B : OUT_B];
+  Stage* st = (Stage*)smem;
+  const int w = wave_id(), lane = threadIdx.x & 63, hh = lane >> 5, c32 = lane & 31;
+  const int hw = w % HB, tw = w / HB;
+  const int npair = (nqt + 1) / 2, ngrp = n_rep / HB;
+  const int logical = xcd_logical_id(blockIdx.x, gridDim.x);
+  const int pp = npair - 1 - logical % npair;  // longest causal rows first
+  const int hg = (logical / npair) % ngrp, bh = logical / npair / ngrp;
+  const int b = bh / Hkv, g = bh % Hkv;
+  const int nqtp = P / DSQ;
+  const int qt = 2 * pp + tw;
+  const bool live = qt < nqt;  // (the second tile of an odd last pair does not exist)
+  const int qt_last = min(2 * pp + 1, nqt - 1);
+  const int nkeys = (S + DSK - 1) / DSK;
+  const int nk = min(2 * qt_last + 2, nkeys);            // steps of the workgroup
+  const int nk_w = live ? min(2 * qt + 2, nkeys) : 0;   // steps with a record of this wave
+  const u32x4* rec0 = dsb + (ds_pair(bh, live ? qt : qt_last, 0, nqtp, 1) * n_rep + hg * HB + hw) * 256;
+  const bf16* kbase = krot + (int64_t)bh * P * D;
+  auto stage = [&](int t, int buf) {
+    const int L = w * 64 + lane, row = L / KR, pc = L % KR;  // KI / NW == 1
+    const uint32_t off = ((uint32_t)(t * DSK + row) * D + (uint32_t)(pc ^ swz<KR>(row)) * 8u) * 2u;
+    dma16(lds_addr(st[buf].k + w * 512), off, kbase);
+    // this wavefront's record of column t (its last one again past its steps);
+    // the piece permutation of bwd_dq_ds_kernel
+    const int tr = min(t, max(nk_w, 1) - 1);
+    const u32x4* src = rec0 + (int64_t)tr * n_rep * 256;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      dma16_nt(lds_addr(st[buf].ds + w * 256 + j * 64),
+               (uint32_t)((j * 64 + ((lane ^ (8 * (j & 1))) ^ ((lane >> 5) << 2))) * 16), src);
+  };
+  uint32_t ds_off;
+  {
+    const int G = lane >> 4, a = lane & 15, e = a >> 2, k = a & 3;
+    const int piece = 32 * (k & 1) + 4 * ((G >> 1) ^ (k & 1)) + e;
+    ds_off = (uint32_t)(w * 4096 + (G & 1) * (1024 + 128) + piece * 16 + 8 * (k >> 1));
+  }
+  const TrOffsets<D> tro = tr_offsets<D>(lane);
+  f32x16 acc[2][DT];
+#pragma unroll
+  for (int mh = 0; mh < 2; ++mh)
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc[mh][dt][i] = 0.f;
+
+#pragma unroll
+  for (int t = 0; t < NBUF - 1; ++t)
+    if (t < nk) stage(t, t);
+  for (int t = 0; t < nk; ++t) {
+    const int ahead = min(NBUF - 2, nk - 1 - t);
+    if (ahead >= 2)
+      vm_wait<2 * NLOAD>();
+    else if (ahead == 1)
+      vm_wait<NLOAD>();
+    else
+      vm_wait<0>();
+    __syncthreads();
+    if (t + NBUF - 1 < nk) stage(t + NBUF - 1, (t + NBUF - 1) % NBUF);
+    if (t < nk_w) {
+      const Stage& S_ = st[t % NBUF];
+      const char* dsl = (const char*)S_.ds + ds_off;
+      const char* dsh = (const char*)S_.ds + (ds_off ^ 128u);
+#pragma unroll
+      for (int c = 0; c < DSK / 16; ++c) {
+        bf16x8 bds[2];
+#pragma unroll
+        for (int mh = 0; mh < 2; ++mh) {
+          const int o = 2048 * mh + 256 * c;
+          const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)(dsl + o));
+          const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)(dsh + o));
+          bds[mh] = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5,
+                                                                       6, 7));
+        }
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+          const bf16x8 ak = lds_frag_t<D>(S_.k, tro, c, dt);
+#pragma unroll
+          for (int mh = 0; mh < 2; ++mh)
+            acc[mh][dt] =
+                __builtin_amdgcn_mfma_f32_32x32x16_bf16(ak, bds[mh], acc[mh][dt], 0, 0, 0);
+        }
+      }
+    }
+  }
+
+  // dQ through LDS, every wavefront's 64 rows in its own slice of the ring
+  const int hq = g * n_rep + hg * HB + hw;
+  __syncthreads();
+  bf16* slice = (bf16*)smem + w * 64 * D;
+#pragma unroll
+  for (int mh = 0; mh < 2; ++mh) {
+    const int r = 32 * mh + c32;
+    const int pos = min(qt * DSQ + r, S - 1);  // rows past S are formed, not stored
+    const float* cr = cos + (int64_t)pos * HALF;
+    const float* sr = sin + (int64_t)pos * HALF;
+#pragma unroll
+    for (int dt = 0; dt < DT / 2; ++dt)
+#pragma unroll
+      for (int gi = 0; gi < 4; ++gi) {
+        const int d = 32 * dt + 8 * gi + 4 * hh;
+        float lo[4], hi[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          rope_pair_bwd<bf16>(acc[mh][dt][4 * gi + e] * scale,
+                              acc[mh][dt + DT / 2][4 * gi + e] * scale, cr[d + e], sr[d + e],
+                              lo[e], hi[e]);
+        const int cl = 4 * dt + gi, chh = KR / 2 + 4 * dt + gi;
+        *(u32x2*)(slice + (r * KR + (cl ^ (r & (KR - 1)))) * 8 + 4 * hh) =
+            u32x2{pack2(lo[0], lo[1]), pack2(lo[2], lo[3])};
+        *(u32x2*)(slice + (r * KR + (chh ^ (r & (KR - 1)))) * 8 + 4 * hh) =
+            u32x2{pack2(hi[0], hi[1]), pack2(hi[2], hi[3])};
+      }
+  }
+  __syncthreads();
+  if (!live) return;
+#pragma unroll
+  for (int i2 = 0; i2 < KR; ++i2) {
+    const int L = 64 * i2 + lane, r = L / KR, ch = L % KR;
+    const int pos = qt * DSQ + r;
+    const u32x4 v = *(const u32x4*)(slice + (r * KR + (ch ^ (r & (KR - 1)))) * 8);
+    if (pos < S) *(u32x4*)(dq + (((int64_t)b * S + pos) * Hq + hq) * D + 8 * ch) = v;
+  }
+}
+
 // MASK_DOC: how many tiles each block of a workgroup's rows lists, i.e. the
 // work of the item it takes; one wavefront per block.  Key side (rows = keys):
 // the query tiles from the block's diagonal tile to the end; query side: the
@@ -1168,6 +1318,18 @@ int launch_dq_ds(const BwdArgs& a, const Ws& w) {
   // ring depth by sequence length (measured with 4 heads per workgroup: 4
   // buffers 485 against 517 us at S = 4096, 3115 against 2967 at S = 16384)
   const bool deep = HB == 4 && a.S <= 8192;
+  // two query tiles per workgroup for the long sequences (measured: C5 2910 us
+  // against 2959; at S = 4096 one tile with four stages does better, 468
+  // against 491)
+  if constexpr (D == 128 && HB == 4)
+  if (!a.doc && !a.kvalid && a.causal && !deep) {
+    const int npair = (nqt + 1) / 2;
+    KF_LAUNCH("bwd_dq_ds", (bwd_dq_ds2_kernel<D, 3>), dim3(a.B * a.Hkv * (n_rep / HB) * npair),
+              dim3(512), 0, a.stream, w.dsb, w.krot, a.cos, a.sin, (bf16*)a.dq, a.S, P, a.Hq,
+              a.Hkv, n_rep, nqt, a.scale);
+    KF_CHECK_LAUNCH();
+    return KF_OK;
+  }
   KF_LAUNCH("bwd_dq_ds",
             (a.doc      ? (deep ? bwd_dq_ds_kernel<D, HB, MASK_DOC, 4>
                                 : bwd_dq_ds_kernel<D, HB, MASK_DOC, 3>)
