@@ -12,7 +12,7 @@ import pytest
 import torch
 
 import make_fixtures as mf
-from gpu_util import DEV, TOL, announce, check_grad, check_out, load_fixture, seeded
+from gpu_util import DEV, TOL, announce, check_grad, check_out, half_ulp, load_fixture, seeded
 from kempnerforge_amd import ops
 from oracle import attention_ref as ref
 
@@ -204,3 +204,35 @@ def test_llama70b_shape_prefix_and_identities():
     resid = dk_rot.sum(dim=2).abs().max().item()
     scale = dk_rot.pow(2).sum(dim=2).sqrt().max().item()
     assert resid <= 2e-2 * scale
+
+
+def test_two_tile_dq_long_odd_sequence():
+    """S > 8192 takes the two-query-tile dQ-from-records kernel; with an odd
+    number of 64-row tiles its last workgroup holds one tile.  Its dQ rows
+    below 2048 equal a 2048-token run's (the one-tile kernel) bit for bit (a
+    causal row's dQ depends on rows and keys up to it only), the whole dQ
+    agrees with the recomputing path (low_memory) to twice the per-element bf16
+    gradient bound (each path is within it of the exact value), and
+    dK / dV are the same bits on both paths."""
+    B, S, Hq, Hkv, D = 1, 8256, 8, 2, 128  # 129 query tiles
+    announce("bwd two-tile dQ, S=8256")
+    q, k, v, do = (seeded((B, S, h, D), 40 + i, torch.bfloat16).to(DEV)
+                   for i, h in enumerate((Hq, Hkv, Hkv, Hq)))
+    cos, sin = (t.to(DEV) for t in ref.rope_tables(D, S, 5e5))
+    out, lse = ops.fwd_raw(q, k, v, cos, sin, causal=True, k_rotated=False)
+    kept = ops.bwd_raw(q, k, v, cos, sin, out, lse, do, causal=True)
+    rec = ops.bwd_raw(q, k, v, cos, sin, out, lse, do, causal=True, low_memory=True)
+    n = 2048
+    sl = lambda t: t[:, :n].contiguous()  # noqa: E731
+    o2, l2 = ops.fwd_raw(sl(q), sl(k), sl(v), cos[:n], sin[:n], causal=True, k_rotated=False)
+    short = ops.bwd_raw(sl(q), sl(k), sl(v), cos[:n], sin[:n], o2, l2, sl(do), causal=True)
+    torch.cuda.synchronize()
+    assert torch.equal(kept[1], rec[1]) and torch.equal(kept[2], rec[2])
+    assert torch.equal(kept[0][:, :n], short[0])
+    # each path within the per-element gradient bound (2e-2 + half an ulp) of
+    # the exact value, so the two within twice that of each other
+    err = (kept[0].double() - rec[0].double()).abs()
+    bound = 2 * (2e-2 + half_ulp(rec[0].double(), torch.bfloat16))
+    print(f"dq kept vs recomputed max-abs {err.max().item():.3e}, "
+          f"worst/bound {(err / bound).max().item():.3f}")
+    assert bool((err <= bound).all())
