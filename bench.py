@@ -121,10 +121,11 @@ class Workloads:
                          k_rotated=False)
 
     def c3_raw_step(self):
+        # the kernels the autograd step runs: the rotated-operand pair
         q, k, v, do, cos, sin = self.c3_inputs()
         qn, kn, vn = q.detach(), k.detach(), v.detach()
-        o, l = self.ops.fwd_raw(qn, kn, vn, cos, sin, causal=True, k_rotated=False)
-        return self.ops.bwd_raw(qn, kn, vn, cos, sin, o, l, do, causal=True)
+        o, l, rot = self.ops.fwd_rot_raw(qn, kn, vn, cos, sin, causal=True)
+        return self.ops.bwd_rot_raw(rot, vn, cos, sin, o, l, do, causal=True)
 
     def doc_inputs(self):
         """C3 on packed sequences: documents of 64..2048 tokens (seed 7)."""
@@ -350,8 +351,8 @@ def run_full(args, torch, wl):
     c2 = {"config": "C2 llama3-8b fwd B=4 S=4096 Hq=32 Hkv=8 D=128", "ms": round(c2_s * 1e3, 4),
           "TFLOP/s": round(4.0 * D * P / c2_s / 1e12, 1)}
 
-    # C3 replayed from a HIP graph (the raw forward + backward captured once):
-    # the same kernels without per-launch host overhead or autograd
+    # C3 replayed from a HIP graph (the raw rotated-operand forward + backward
+    # captured once): the same kernels without per-launch host overhead or autograd
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):
@@ -363,7 +364,7 @@ def run_full(args, torch, wl):
     with torch.cuda.graph(graph):
         wl.c3_raw_step()
     c3g_s = timed(torch, graph.replay, args.warmup, args.steps)
-    c3_graph = {"config": "C3 step as one HIP graph replay (fwd_raw + bwd_raw)",
+    c3_graph = {"config": "C3 step as one HIP graph replay (fwd_rot_raw + bwd_rot_raw)",
                 "ms": round(c3g_s * 1e3, 4), "TFLOP/s": round(flops_step / c3g_s / 1e12, 1)}
     del graph
 
