@@ -832,13 +832,6 @@ __device__ __forceinline__ void dma16_nt(uint32_t lds, uint32_t voff, const void
                : : "v"(voff), "s"(base), "{m0}"(lds) : "memory");
 }
 
-// s_waitcnt vmcnt(N)
-template <int N>
-__device__ __forceinline__ void vm_wait() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-
 // dQ from the dS records: workgroup = HB query heads of one KV group x DSQ
 // positions, one wavefront per head (its 64 rows as two 32-row blocks, so each
 // K^T fragment feeds two products).  Per DSK-key step it stages the rotated K

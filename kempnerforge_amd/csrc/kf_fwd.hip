@@ -661,21 +661,25 @@ __global__ __launch_bounds__(256, 3) void fwd32_kernel(
 }
 
 // Capture: LSE, the probabilities P = exp(s - lse) as float32 [B, Hq, Sq, Sk]
-// and out = P·V in one launch per (query block, KV head).  The workgroup walks
-// its key tiles twice in the forward's S^T = K·Q^T layout (a lane holds one
-// query row's 32 scores of a 64-key tile): the first walk forms each row's
-// running max and sum only (no P·V); the second forms the normalised P,
-// stores it, and accumulates O^T = V^T·P^T from P rounded to bf16, so O needs
-// no final division.  P leaves through an LDS slice per wavefront (see
-// store_p) as whole 128-byte line segments.  The stores of tile t issue at the
-// start of tile t+1, before its tile loads: the end-of-tile wait (vmcnt counts
-// loads and stores together) then finds stores a whole tile old.  Key tiles
-// right of the causal frontier are zero without computing; their rows are
-// spread over the tile iterations.  Stores are non-temporal: nothing reads P
-// back, and cached it would evict the K and V tiles the other workgroups of
-// the KV head re-read.  Query blocks are taken long and short alternately
-// (qb = nqb-1, 0, nqb-2, 1, ...), so a CU's two resident workgroups tend to
-// pair a compute-heavy block with a write-heavy one.  Explicit masks as in the
+// and out = P·V in one launch; a workgroup takes the query blocks r and
+// nqb-1-r of one KV head, one after the other.  The workgroup walks a block's
+// key tiles twice in the forward's S^T = K·Q^T layout (a lane holds one query
+// row's 32 scores of a 64-key tile): the first walk forms each row's running
+// max and sum only (no P·V), with the four tile buffers as a ring of K tiles
+// staged three ahead; the second forms the normalised P, stores it, and
+// accumulates O^T = V^T·P^T from P rounded to bf16, so O needs no final
+// division.  P leaves through an LDS slice per wavefront (see store_p) as
+// whole 128-byte line segments.  The stores of tile t issue in tile t+1,
+// after its tile loads and zero rows: the end-of-tile wait (vmcnt counts loads
+// and stores together, in issue order) can then leave them in flight through
+// tile t+2.  Key tiles right of the causal frontier are zero without
+// computing; their rows are spread over the tile iterations.  Stores are
+// non-temporal: nothing reads P back, and cached it would evict the K and V
+// tiles the other workgroups of the KV head re-read.  Pairing a long query
+// block with a short one gives every workgroup about the same work, so the
+// grid runs as one even wave; one block per workgroup (long and short blocks
+// alternating) left the CUs of the long blocks busy long after the others had
+// drained.  Explicit masks as in the
 // forward (MASK_DOC: other documents get P = 0; MASK_KPM: padded keys get 0,
 // except in guarded rows before the first valid key, which attend every key
 // below Sk, so a workgroup holding one walks every tile); with an explicit
@@ -692,14 +696,29 @@ __global__ __launch_bounds__(256, 2) void capture_probs_mfma_kernel(
   constexpr int KR = D / 8;
   __shared__ __attribute__((aligned(16))) bf16 sK[2][BN * D];
   __shared__ __attribute__((aligned(16))) bf16 sV[2][BN * D];
-  __shared__ __attribute__((aligned(16))) int32_t sKD[2][BN];  // LIST: per-key aux values
+  __shared__ __attribute__((aligned(16))) int32_t sKD[4][BN];  // LIST: per-key aux values
   __shared__ __attribute__((aligned(16))) float sP[4][32 * 32];  // per wave: 32 rows x 32 keys
 
-  const int tid = threadIdx.x, w = wave_id(), lane = tid & 63, hh = lane >> 5, c32 = lane & 31;
-  const int logical = xcd_logical_id(blockIdx.x, gridDim.x);
-  // row_info maps logical index bh*nqb + j to query block nqb-1-j; alternate
-  const int zz = logical % nqb, zq = (zz & 1) ? nqb - 1 - (zz >> 1) : (zz >> 1);
-  const RowInfo ri = row_info(logical - zz + zq, nqb, Hkv, n_rep, bm_pos, Sq, w * 32 + c32);
+  // workgroup = query blocks r and nqb-1-r of one (batch row, KV head): every
+  // workgroup gets about the same number of key tiles, so the grid runs in one
+  // even wave (one block per workgroup leaves the long blocks' CUs busy long
+  // after the short ones' have drained)
+  const int npair = (nqb + 1) / 2;
+  const int pl = xcd_logical_id(blockIdx.x, gridDim.x);
+  const int bhq = pl / npair, pr = pl % npair;
+  const int nb = 2 * pr + 1 == nqb ? 1 : 2;
+  for (int kb = 0; kb < nb; ++kb) {
+  // length rank of this block (0 = longest): even workgroups take the long
+  // one first, odd ones the short one
+  const int zq = (kb ^ (pl & 1)) == 0 ? pr : nqb - 1 - pr;
+  if (kb > 0) __syncthreads();  // the previous block's LDS reads are done
+  // the lane's values are formed anew per block (laundered): held across
+  // the block loop, the addresses derived from them spill
+  int tid = threadIdx.x;
+  asm volatile("" : "+v"(tid));
+  const int w = wave_id(), lane = tid & 63, hh = lane >> 5, c32 = lane & 31;
+  // row_info maps logical index bh*nqb + j to query block nqb-1-j
+  const RowInfo ri = row_info(bhq * nqb + zq, nqb, Hkv, n_rep, bm_pos, Sq, w * 32 + c32);
   const int bh = ri.b * Hkv + ri.g;
   const int32_t* arow = LIST ? aux + (int64_t)ri.b * Sk : nullptr;
   const int nrows = n_rep * bm_pos;  // rows of the block in use
@@ -721,7 +740,16 @@ __global__ __launch_bounds__(256, 2) void capture_probs_mfma_kernel(
   auto stage_v = [&](int t, int buf) {
     tile_to_lds<D, BN / 8>(vbase + (int64_t)t * BN, Skp, sV[buf], w, lane);
   };
-  if (ntiles > 0) stage_k(0, 0);
+  // Walk 1 reads only K tiles: all four tile buffers form its ring, staged
+  // three tiles ahead (slot s: sK[0], sK[1], sV[0], sV[1]; aux values in sKD[s])
+  bf16* const ring[4] = {sK[0], sK[1], sV[0], sV[1]};
+  auto stage_kr = [&](int t, int slot) {
+    tile_to_lds<BN, KR>(kbase + (int64_t)t * BN * D, D, ring[slot], w, lane);
+    if (LIST && w == 0) dma4(lds_addr(sKD[slot]), (uint32_t)min(t * BN + lane, Sk - 1) * 4u, arow);
+  };
+#pragma unroll
+  for (int t = 0; t < 3; ++t)
+    if (t < ntiles) stage_kr(t, t);
 
   bf16x8 qf[KS];
   load_q_frag<D>(q, cos, sin, ri, Sq, Hq, hh, qf);
@@ -795,20 +823,23 @@ __global__ __launch_bounds__(256, 2) void capture_probs_mfma_kernel(
   __syncthreads();
   // Walk 1: running max m and sum (log2 domain).  Starting m at -1e30 keeps
   // exp2(m - mnew) finite for a row that sees no key in a tile.  Its last
-  // iteration stages tile 0 of walk 2 (K and V).  Both walks are unrolled by
-  // two so that each copy's LDS buffer is a compile-time constant.
+  // iteration stages tile 0 of walk 2 (K and V) into the buffer pair whose
+  // slots it is not reading (pair 1 when ntiles is odd).  Walk 1 is unrolled
+  // by four and walk 2 by two so that each copy's LDS buffer is a
+  // compile-time constant.
   float m = -1e30f, lsum = 0.f;
-  auto body1 = [&](int it, auto bufc) {
-    constexpr int buf = decltype(bufc)::value;
+  constexpr int NK = BN * KR / 64 / 4;  // direct loads per lane of one K tile
+  auto body1 = [&](int it, auto slotc) {
+    constexpr int slot = decltype(slotc)::value;
     zero_rows(it);
-    if (it + 1 < ntiles) {
-      stage_k(it + 1, buf ^ 1);
-    } else {
-      stage_k(0, buf ^ 1);
-      stage_v(0, buf ^ 1);
+    if (it + 3 < ntiles) {
+      stage_kr(it + 3, (slot + 3) & 3);
+    } else if (it + 1 == ntiles) {
+      stage_k(0, (slot & 1) ^ 1);
+      stage_v(0, (slot & 1) ^ 1);
     }
     f32x16 s[2];
-    scores(it, sK[buf], sKD[buf], s);
+    scores(it, ring[slot], sKD[slot], s);
     float tmax = -INFINITY;
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt)
@@ -822,12 +853,21 @@ __global__ __launch_bounds__(256, 2) void capture_probs_mfma_kernel(
       for (int i = 0; i < 16; ++i) psum += fast_exp2(__builtin_fmaf(s[mt][i], scale_log2, -mnew));
     lsum = lsum * fast_exp2(m - mnew) + psum;
     m = mnew;
-    lds_copy_wait();
+    // tile it + 1 in LDS; tiles it + 2 and it + 3 (NK loads per lane each,
+    // issued after it) may stay in flight
+    if (it + 3 < ntiles)
+      vm_wait<2 * NK>();
+    else if (it + 2 < ntiles)
+      vm_wait<NK>();
+    else
+      lds_copy_wait();
     __syncthreads();
   };
-  for (int it = 0; it < ntiles; it += 2) {
+  for (int it = 0; it < ntiles; it += 4) {
     body1(it, std::integral_constant<int, 0>{});
     if (it + 1 < ntiles) body1(it + 1, std::integral_constant<int, 1>{});
+    if (it + 2 < ntiles) body1(it + 2, std::integral_constant<int, 2>{});
+    if (it + 3 < ntiles) body1(it + 3, std::integral_constant<int, 3>{});
   }
   const float L = m + log2f(pair_sum32(lsum));  // log2-domain LSE of this row
   if (ri.q_valid && hh == 0) lse[((int64_t)ri.b * Hq + ri.hq) * Sq + ri.pos] = L * kLn2;
@@ -856,6 +896,9 @@ __global__ __launch_bounds__(256, 2) void capture_probs_mfma_kernel(
   }
   float* stg = sP[w];
   f32x16 held[2];  // P of the previous tile, stored by the next
+  // true when every lane of store_p(t)'s 8 store instructions is active, so
+  // that exactly 8 vector-memory instructions issue
+  auto full_p = [&](int t) { return pvalid == 15 && vec4 && (t + 1) * BN <= Sk; };
   auto store_p = [&](int t) {
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) {
@@ -882,12 +925,16 @@ __global__ __launch_bounds__(256, 2) void capture_probs_mfma_kernel(
   };
   auto body2 = [&](int it, auto bufc) {
     constexpr int buf = decltype(bufc)::value;
-    if (it > 0) store_p(it - 1);
-    zero_rows(ntiles + it);
+    // the tile loads, the zero rows, then P of tile it - 1: the 8 P stores
+    // are the last vector-memory instructions of the tile, so the end-of-tile
+    // wait can leave them in flight through the next tile
     if (it + 1 < ntiles) {
       stage_k(it + 1, buf ^ 1);
       stage_v(it + 1, buf ^ 1);
     }
+    zero_rows(ntiles + it);
+    const bool full = it > 0 && __builtin_amdgcn_ballot_w64(!full_p(it - 1)) == 0;
+    if (it > 0) store_p(it - 1);
     f32x16 s[2];
     scores(it, sK[buf], sKD[buf], s);
     u32x4 pk[4];
@@ -910,7 +957,10 @@ __global__ __launch_bounds__(256, 2) void capture_probs_mfma_kernel(
         acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb, acc[dt], 0, 0, 0);
       }
     }
-    lds_copy_wait();
+    if (full)
+      vm_wait<8>();
+    else
+      lds_copy_wait();
     __syncthreads();
   };
   // walk 2 starts in the buffer walk 1's last iteration filled: buffer 1 when
@@ -938,6 +988,7 @@ __global__ __launch_bounds__(256, 2) void capture_probs_mfma_kernel(
         pk2[1] = pack2(acc[dt][4 * gi + 2], acc[dt][4 * gi + 3]);
         *(u32x2*)(orow + d) = pk2;
       }
+  }
   }
 }
 
@@ -1142,7 +1193,8 @@ int capture_probs_mfma(const FwdArgs& a, float* probs, void* workspace) {
   const int n_rep = a.Hq / a.Hkv;
   const int bm_pos = pick_bm_pos(n_rep);
   const int nqb = (a.Sq + bm_pos - 1) / bm_pos;
-  const int64_t nblk = (int64_t)nqb * a.B * a.Hkv;
+  // one workgroup per pair of query blocks
+  const int64_t nblk = (int64_t)((nqb + 1) / 2) * a.B * a.Hkv;
   KF_CHECK_ARG(nblk < (1LL << 31), "grid too large");
   if (a.D == 128) launch_capture_mode<128>(a, w, probs, Skp, n_rep, bm_pos, nqb, (unsigned)nblk);
   else launch_capture_mode<64>(a, w, probs, Skp, n_rep, bm_pos, nqb, (unsigned)nblk);

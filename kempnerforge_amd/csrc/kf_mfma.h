@@ -221,6 +221,15 @@ __device__ __forceinline__ void row_to_lds(const float* __restrict__ g, float* l
 
 __device__ __forceinline__ void lds_copy_wait() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
+// s_waitcnt vmcnt(N): all but the last N vector-memory instructions issued
+// have completed (gfx950 counts loads, direct-to-LDS loads and stores in one
+// counter, in issue order)
+template <int N>
+__device__ __forceinline__ void vm_wait() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
 // Pin a loaded value at this point: the compiler waits for its load here, not
 // at its first use, which may sit inside a loop that keeps direct-to-LDS
 // loads in flight (a wait there would stall on those every iteration).
