@@ -708,287 +708,289 @@ __global__ __launch_bounds__(256, 2) void capture_probs_mfma_kernel(
   const int bhq = pl / npair, pr = pl % npair;
   const int nb = 2 * pr + 1 == nqb ? 1 : 2;
   for (int kb = 0; kb < nb; ++kb) {
-  // length rank of this block (0 = longest): even workgroups take the long
-  // one first, odd ones the short one
-  const int zq = (kb ^ (pl & 1)) == 0 ? pr : nqb - 1 - pr;
-  if (kb > 0) __syncthreads();  // the previous block's LDS reads are done
-  // the lane's values are formed anew per block (laundered): held across
-  // the block loop, the addresses derived from them spill
-  int tid = threadIdx.x;
-  asm volatile("" : "+v"(tid));
-  const int w = wave_id(), lane = tid & 63, hh = lane >> 5, c32 = lane & 31;
-  // row_info maps logical index bh*nqb + j to query block nqb-1-j
-  const RowInfo ri = row_info(bhq * nqb + zq, nqb, Hkv, n_rep, bm_pos, Sq, w * 32 + c32);
-  const int bh = ri.b * Hkv + ri.g;
-  const int32_t* arow = LIST ? aux + (int64_t)ri.b * Sk : nullptr;
-  const int nrows = n_rep * bm_pos;  // rows of the block in use
+    // length rank of this block (0 = longest): even workgroups take the long
+    // one first, odd ones the short one
+    const int zq = (kb ^ (pl & 1)) == 0 ? pr : nqb - 1 - pr;
+    if (kb > 0) __syncthreads();  // the previous block's LDS reads are done
+    // the lane's values are formed anew per block (laundered): held across
+    // the block loop, the addresses derived from them spill
+    int tid = threadIdx.x;
+    asm volatile("" : "+v"(tid));
+    const int w = wave_id(), lane = tid & 63, hh = lane >> 5, c32 = lane & 31;
+    // row_info maps logical index bh*nqb + j to query block nqb-1-j
+    const RowInfo ri = row_info(bhq * nqb + zq, nqb, Hkv, n_rep, bm_pos, Sq, w * 32 + c32);
+    const int bh = ri.b * Hkv + ri.g;
+    const int32_t* arow = LIST ? aux + (int64_t)ri.b * Sk : nullptr;
+    const int nrows = n_rep * bm_pos;  // rows of the block in use
 
-  const int qmax = min(ri.p0 + bm_pos, Sq) - 1;  // largest position in the block
-  const int ntiles_all = (Sk + BN - 1) / BN;
-  // KPM: first valid key of the batch row; rows before it are guarded
-  const int fv = KPM ? kpm_first_valid(ranges + (int64_t)ri.b * (Skp / BN), Skp / BN, lane) : 0;
-  const int ntiles = causal && !(KPM && ri.p0 < fv) ? min(ntiles_all, (qmax + BN) / BN)
-                                                      : ntiles_all;
-  const int di = DOC ? arow[min(ri.pos, Sq - 1)] : 0;  // DOC: this row's document
-  const bool grd = KPM && ri.pos < fv;                  // KPM: guarded row
-  const bf16* kbase = krot + (int64_t)bh * Skp * D;
-  const bf16* vbase = vn + (int64_t)bh * D * Skp;  // V^T, keys in fragment order
-  auto stage_k = [&](int t, int buf) {
-    tile_to_lds<BN, KR>(kbase + (int64_t)t * BN * D, D, sK[buf], w, lane);
-    if (LIST && w == 0) dma4(lds_addr(sKD[buf]), (uint32_t)min(t * BN + lane, Sk - 1) * 4u, arow);
-  };
-  auto stage_v = [&](int t, int buf) {
-    tile_to_lds<D, BN / 8>(vbase + (int64_t)t * BN, Skp, sV[buf], w, lane);
-  };
-  // Walk 1 reads only K tiles: all four tile buffers form its ring, staged
-  // three tiles ahead (slot s: sK[0], sK[1], sV[0], sV[1]; aux values in sKD[s])
-  bf16* const ring[4] = {sK[0], sK[1], sV[0], sV[1]};
-  auto stage_kr = [&](int t, int slot) {
-    tile_to_lds<BN, KR>(kbase + (int64_t)t * BN * D, D, ring[slot], w, lane);
-    if (LIST && w == 0) dma4(lds_addr(sKD[slot]), (uint32_t)min(t * BN + lane, Sk - 1) * 4u, arow);
-  };
+    const int qmax = min(ri.p0 + bm_pos, Sq) - 1;  // largest position in the block
+    const int ntiles_all = (Sk + BN - 1) / BN;
+    // KPM: first valid key of the batch row; rows before it are guarded
+    const int fv = KPM ? kpm_first_valid(ranges + (int64_t)ri.b * (Skp / BN), Skp / BN, lane) : 0;
+    const int ntiles = causal && !(KPM && ri.p0 < fv) ? min(ntiles_all, (qmax + BN) / BN)
+                                                        : ntiles_all;
+    const int di = DOC ? arow[min(ri.pos, Sq - 1)] : 0;  // DOC: this row's document
+    const bool grd = KPM && ri.pos < fv;                  // KPM: guarded row
+    const bf16* kbase = krot + (int64_t)bh * Skp * D;
+    const bf16* vbase = vn + (int64_t)bh * D * Skp;  // V^T, keys in fragment order
+    auto stage_k = [&](int t, int buf) {
+      tile_to_lds<BN, KR>(kbase + (int64_t)t * BN * D, D, sK[buf], w, lane);
+      if (LIST && w == 0) dma4(lds_addr(sKD[buf]), (uint32_t)min(t * BN + lane, Sk - 1) * 4u, arow);
+    };
+    auto stage_v = [&](int t, int buf) {
+      tile_to_lds<D, BN / 8>(vbase + (int64_t)t * BN, Skp, sV[buf], w, lane);
+    };
+    // Walk 1 reads only K tiles: all four tile buffers form its ring, staged
+    // three tiles ahead (slot s: sK[0], sK[1], sV[0], sV[1]; aux values in sKD[s])
+    bf16* const ring[4] = {sK[0], sK[1], sV[0], sV[1]};
+    auto stage_kr = [&](int t, int slot) {
+      tile_to_lds<BN, KR>(kbase + (int64_t)t * BN * D, D, ring[slot], w, lane);
+      if (LIST && w == 0)
+        dma4(lds_addr(sKD[slot]), (uint32_t)min(t * BN + lane, Sk - 1) * 4u, arow);
+    };
 #pragma unroll
-  for (int t = 0; t < 3; ++t)
-    if (t < ntiles) stage_kr(t, t);
+    for (int t = 0; t < 3; ++t)
+      if (t < ntiles) stage_kr(t, t);
 
-  bf16x8 qf[KS];
-  load_q_frag<D>(q, cos, sin, ri, Sq, Hq, hh, qf);
+    bf16x8 qf[KS];
+    load_q_frag<D>(q, cos, sin, ri, Sq, Hq, hh, qf);
 
-  // S^T of tile t with masked scores set to -inf
-  auto scores = [&](int t, const bf16* tK, const int32_t* kdl, f32x16 (&s)[2]) {
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) s[mt][i] = 0.f;
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-#pragma unroll
-      for (int mt = 0; mt < 2; ++mt) {
-        const bf16x8 a = lds_frag<KR>(tK, 32 * mt + c32, 2 * ks + hh);
-        s[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[ks], s[mt], 0, 0, 0);
-      }
-    }
-    const int k0 = t * BN;
-    if constexpr (LIST) {
-      // explicit masks come with causal self-attention
-      const int lim = (grd ? Sk - 1 : min(ri.pos, Sk - 1)) - k0;
+    // S^T of tile t with masked scores set to -inf
+    auto scores = [&](int t, const bf16* tK, const int32_t* kdl, f32x16 (&s)[2]) {
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-        for (int g4 = 0; g4 < 4; ++g4) {
-          const i32x4 kd = *(const i32x4*)&kdl[32 * mt + 8 * g4 + 4 * hh];
+        for (int i = 0; i < 16; ++i) s[mt][i] = 0.f;
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const int local = 32 * mt + 8 * g4 + 4 * hh + j;
-            const bool other = DOC ? kd[j] != di : (!grd && kd[j] == 0);
-            s[mt][4 * g4 + j] = (local > lim || other) ? -INFINITY : s[mt][4 * g4 + j];
+      for (int ks = 0; ks < KS; ++ks) {
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) {
+          const bf16x8 a = lds_frag<KR>(tK, 32 * mt + c32, 2 * ks + hh);
+          s[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[ks], s[mt], 0, 0, 0);
+        }
+      }
+      const int k0 = t * BN;
+      if constexpr (LIST) {
+        // explicit masks come with causal self-attention
+        const int lim = (grd ? Sk - 1 : min(ri.pos, Sk - 1)) - k0;
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+          for (int g4 = 0; g4 < 4; ++g4) {
+            const i32x4 kd = *(const i32x4*)&kdl[32 * mt + 8 * g4 + 4 * hh];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              const int local = 32 * mt + 8 * g4 + 4 * hh + j;
+              const bool other = DOC ? kd[j] != di : (!grd && kd[j] == 0);
+              s[mt][4 * g4 + j] = (local > lim || other) ? -INFINITY : s[mt][4 * g4 + j];
+            }
+          }
+      } else if ((causal && k0 + BN - 1 > ri.p0) || k0 + BN > Sk) {
+        const int lim = (causal ? min(ri.pos, Sk - 1) : Sk - 1) - k0;
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const int local = 32 * mt + 8 * (i >> 2) + 4 * hh + (i & 3);
+            s[mt][i] = local > lim ? -INFINITY : s[mt][i];
+          }
+      }
+    };
+
+    // Key tiles right of the causal frontier are zero.  Their rows are written
+    // in 2*ntiles pieces, one at the start of each tile iteration of the two
+    // walks (ahead of that iteration's tile loads), so the zeros stream out
+    // while the block computes instead of after it.
+    const bool vec4 = (Sk & 3) == 0;  // 16-byte aligned rows
+    const int zstart = ntiles * BN;
+    const int zper = causal && zstart < Sk ? (nrows + 2 * ntiles - 1) / (2 * ntiles) : 0;
+    auto zero_rows = [&](int z) {
+      const int r1 = min(z * zper + zper, nrows);
+      for (int r = z * zper; r < r1; ++r) {
+        const int pos = ri.p0 + r % bm_pos;
+        if (pos >= Sq) continue;
+        float* zrow =
+            probs + (((int64_t)ri.b * Hq + (int64_t)ri.g * n_rep + r / bm_pos) * Sq + pos) * Sk;
+        for (int key = zstart + tid * 4; key < Sk; key += 256 * 4) {
+          if (vec4) {
+            __builtin_nontemporal_store(f32x4{0.f, 0.f, 0.f, 0.f}, (f32x4*)(zrow + key));
+          } else {
+            for (int e = key; e < min(key + 4, Sk); ++e) zrow[e] = 0.f;
           }
         }
-    } else if ((causal && k0 + BN - 1 > ri.p0) || k0 + BN > Sk) {
-      const int lim = (causal ? min(ri.pos, Sk - 1) : Sk - 1) - k0;
+      }
+    };
+
+    lds_copy_wait();
+    __syncthreads();
+    // Walk 1: running max m and sum (log2 domain).  Starting m at -1e30 keeps
+    // exp2(m - mnew) finite for a row that sees no key in a tile.  Its last
+    // iteration stages tile 0 of walk 2 (K and V) into the buffer pair whose
+    // slots it is not reading (pair 1 when ntiles is odd).  Walk 1 is unrolled
+    // by four and walk 2 by two so that each copy's LDS buffer is a
+    // compile-time constant.
+    float m = -1e30f, lsum = 0.f;
+    constexpr int NK = BN * KR / 64 / 4;  // direct loads per lane of one K tile
+    auto body1 = [&](int it, auto slotc) {
+      constexpr int slot = decltype(slotc)::value;
+      zero_rows(it);
+      if (it + 3 < ntiles) {
+        stage_kr(it + 3, (slot + 3) & 3);
+      } else if (it + 1 == ntiles) {
+        stage_k(0, (slot & 1) ^ 1);
+        stage_v(0, (slot & 1) ^ 1);
+      }
+      f32x16 s[2];
+      scores(it, ring[slot], sKD[slot], s);
+      float tmax = -INFINITY;
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int local = 32 * mt + 8 * (i >> 2) + 4 * hh + (i & 3);
-          s[mt][i] = local > lim ? -INFINITY : s[mt][i];
-        }
+        for (int i = 0; i < 16; ++i) tmax = fmaxf(tmax, s[mt][i]);
+      const float mnew = fmaxf(m, pair_max32(tmax) * scale_log2);
+      float psum = 0.f;
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) psum += fast_exp2(__builtin_fmaf(s[mt][i], scale_log2, -mnew));
+      lsum = lsum * fast_exp2(m - mnew) + psum;
+      m = mnew;
+      // tile it + 1 in LDS; tiles it + 2 and it + 3 (NK loads per lane each,
+      // issued after it) may stay in flight
+      if (it + 3 < ntiles)
+        vm_wait<2 * NK>();
+      else if (it + 2 < ntiles)
+        vm_wait<NK>();
+      else
+        lds_copy_wait();
+      __syncthreads();
+    };
+    for (int it = 0; it < ntiles; it += 4) {
+      body1(it, std::integral_constant<int, 0>{});
+      if (it + 1 < ntiles) body1(it + 1, std::integral_constant<int, 1>{});
+      if (it + 2 < ntiles) body1(it + 2, std::integral_constant<int, 2>{});
+      if (it + 3 < ntiles) body1(it + 3, std::integral_constant<int, 3>{});
     }
-  };
+    const float L = m + log2f(pair_sum32(lsum));  // log2-domain LSE of this row
+    if (ri.q_valid && hh == 0) lse[((int64_t)ri.b * Hq + ri.hq) * Sq + ri.pos] = L * kLn2;
 
-  // Key tiles right of the causal frontier are zero.  Their rows are written
-  // in 2*ntiles pieces, one at the start of each tile iteration of the two
-  // walks (ahead of that iteration's tile loads), so the zeros stream out
-  // while the block computes instead of after it.
-  const bool vec4 = (Sk & 3) == 0;  // 16-byte aligned rows
-  const int zstart = ntiles * BN;
-  const int zper = causal && zstart < Sk ? (nrows + 2 * ntiles - 1) / (2 * ntiles) : 0;
-  auto zero_rows = [&](int z) {
-    const int r1 = min(z * zper + zper, nrows);
-    for (int r = z * zper; r < r1; ++r) {
-      const int pos = ri.p0 + r % bm_pos;
-      if (pos >= Sq) continue;
-      float* zrow = probs + (((int64_t)ri.b * Hq + (int64_t)ri.g * n_rep + r / bm_pos) * Sq + pos) * Sk;
-      for (int key = zstart + tid * 4; key < Sk; key += 256 * 4) {
-        if (vec4) {
-          __builtin_nontemporal_store(f32x4{0.f, 0.f, 0.f, 0.f}, (f32x4*)(zrow + key));
-        } else {
-          for (int e = key; e < min(key + 4, Sk); ++e) zrow[e] = 0.f;
-        }
-      }
-    }
-  };
-
-  lds_copy_wait();
-  __syncthreads();
-  // Walk 1: running max m and sum (log2 domain).  Starting m at -1e30 keeps
-  // exp2(m - mnew) finite for a row that sees no key in a tile.  Its last
-  // iteration stages tile 0 of walk 2 (K and V) into the buffer pair whose
-  // slots it is not reading (pair 1 when ntiles is odd).  Walk 1 is unrolled
-  // by four and walk 2 by two so that each copy's LDS buffer is a
-  // compile-time constant.
-  float m = -1e30f, lsum = 0.f;
-  constexpr int NK = BN * KR / 64 / 4;  // direct loads per lane of one K tile
-  auto body1 = [&](int it, auto slotc) {
-    constexpr int slot = decltype(slotc)::value;
-    zero_rows(it);
-    if (it + 3 < ntiles) {
-      stage_kr(it + 3, (slot + 3) & 3);
-    } else if (it + 1 == ntiles) {
-      stage_k(0, (slot & 1) ^ 1);
-      stage_v(0, (slot & 1) ^ 1);
-    }
-    f32x16 s[2];
-    scores(it, ring[slot], sKD[slot], s);
-    float tmax = -INFINITY;
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) tmax = fmaxf(tmax, s[mt][i]);
-    const float mnew = fmaxf(m, pair_max32(tmax) * scale_log2);
-    float psum = 0.f;
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) psum += fast_exp2(__builtin_fmaf(s[mt][i], scale_log2, -mnew));
-    lsum = lsum * fast_exp2(m - mnew) + psum;
-    m = mnew;
-    // tile it + 1 in LDS; tiles it + 2 and it + 3 (NK loads per lane each,
-    // issued after it) may stay in flight
-    if (it + 3 < ntiles)
-      vm_wait<2 * NK>();
-    else if (it + 2 < ntiles)
-      vm_wait<NK>();
-    else
-      lds_copy_wait();
-    __syncthreads();
-  };
-  for (int it = 0; it < ntiles; it += 4) {
-    body1(it, std::integral_constant<int, 0>{});
-    if (it + 1 < ntiles) body1(it + 1, std::integral_constant<int, 1>{});
-    if (it + 2 < ntiles) body1(it + 2, std::integral_constant<int, 2>{});
-    if (it + 3 < ntiles) body1(it + 3, std::integral_constant<int, 3>{});
-  }
-  const float L = m + log2f(pair_sum32(lsum));  // log2-domain LSE of this row
-  if (ri.q_valid && hh == 0) lse[((int64_t)ri.b * Hq + ri.hq) * Sq + ri.pos] = L * kLn2;
-
-  // Walk 2: P, its stores, and O^T += V^T P^T
-  f32x16 acc[DT];
-#pragma unroll
-  for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-    for (int i = 0; i < 16; ++i) acc[dt][i] = 0.f;
-  // P leaves through the wave's LDS slice, 32 rows x 32 keys at a time: the C
-  // layout is written as 16-byte chunks (chunk c of row r at c ^ (r & 7), so
-  // neither the writes nor the reads conflict) and read back so that 8 lanes
-  // cover a row's 128 bytes: every store instruction writes 8 whole 128-byte
-  // line segments.  Lane l stores rows 8j + l/8 (j = 0..3) of the wave.
-  float* prs[4];
-  int pvalid = 0;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int r = w * 32 + 8 * j + (lane >> 3);
-    const int pos = ri.p0 + r % bm_pos;
-    const bool ok = r < nrows && pos < Sq;
-    pvalid |= (int)ok << j;
-    prs[j] = probs + (((int64_t)ri.b * Hq + (int64_t)ri.g * n_rep + (ok ? r / bm_pos : 0)) * Sq +
-                      (ok ? pos : 0)) * Sk;
-  }
-  float* stg = sP[w];
-  f32x16 held[2];  // P of the previous tile, stored by the next
-  // true when every lane of store_p(t)'s 8 store instructions is active, so
-  // that exactly 8 vector-memory instructions issue
-  auto full_p = [&](int t) { return pvalid == 15 && vec4 && (t + 1) * BN <= Sk; };
-  auto store_p = [&](int t) {
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
-#pragma unroll
-      for (int g4 = 0; g4 < 4; ++g4)
-        *(f32x4*)&stg[c32 * 32 + (((2 * g4 + hh) ^ (c32 & 7)) * 4)] =
-            f32x4{held[mt][4 * g4], held[mt][4 * g4 + 1], held[mt][4 * g4 + 2],
-                  held[mt][4 * g4 + 3]};
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int rr = 8 * j + (lane >> 3), cl = lane & 7;
-        const f32x4 v4 = *(const f32x4*)&stg[rr * 32 + ((cl ^ (rr & 7)) * 4)];
-        const int key = t * BN + 32 * mt + 4 * cl;
-        if (!((pvalid >> j) & 1)) continue;
-        if (vec4) {
-          if (key < Sk) __builtin_nontemporal_store(v4, (f32x4*)(prs[j] + key));
-        } else {
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            if (key + e < Sk) prs[j][key + e] = v4[e];
-        }
-      }
-    }
-  };
-  auto body2 = [&](int it, auto bufc) {
-    constexpr int buf = decltype(bufc)::value;
-    // the tile loads, the zero rows, then P of tile it - 1: the 8 P stores
-    // are the last vector-memory instructions of the tile, so the end-of-tile
-    // wait can leave them in flight through the next tile
-    if (it + 1 < ntiles) {
-      stage_k(it + 1, buf ^ 1);
-      stage_v(it + 1, buf ^ 1);
-    }
-    zero_rows(ntiles + it);
-    const bool full = it > 0 && __builtin_amdgcn_ballot_w64(!full_p(it - 1)) == 0;
-    if (it > 0) store_p(it - 1);
-    f32x16 s[2];
-    scores(it, sK[buf], sKD[buf], s);
-    u32x4 pk[4];
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-      for (int i = 0; i < 16; i += 2) {
-        const float p0 = fast_exp2(__builtin_fmaf(s[mt][i], scale_log2, -L));
-        const float p1 = fast_exp2(__builtin_fmaf(s[mt][i + 1], scale_log2, -L));
-        held[mt][i] = p0;
-        held[mt][i + 1] = p1;
-        pk[2 * mt + (i >> 3)][(i & 7) >> 1] = pack2(p0, p1);
-      }
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const bf16x8 pb = as_bf16x8(pk[c]);
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt) {
-        const bf16x8 a = lds_frag<BN / 8>(sV[buf], 32 * dt + c32, 2 * c + hh);
-        acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb, acc[dt], 0, 0, 0);
-      }
-    }
-    if (full)
-      vm_wait<8>();
-    else
-      lds_copy_wait();
-    __syncthreads();
-  };
-  // walk 2 starts in the buffer walk 1's last iteration filled: buffer 1 when
-  // ntiles is odd (that first tile is peeled), else 0
-  int it2 = 0;
-  if (ntiles & 1) {
-    body2(0, std::integral_constant<int, 1>{});
-    it2 = 1;
-  }
-  for (; it2 < ntiles; it2 += 2) {
-    body2(it2, std::integral_constant<int, 0>{});
-    if (it2 + 1 < ntiles) body2(it2 + 1, std::integral_constant<int, 1>{});
-  }
-  if (ntiles > 0) store_p(ntiles - 1);
-
-  if (ri.q_valid) {
-    bf16* orow = out + (((int64_t)ri.b * Sq + ri.pos) * Hq + ri.hq) * D;
+    // Walk 2: P, its stores, and O^T += V^T P^T
+    f32x16 acc[DT];
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-      for (int gi = 0; gi < 4; ++gi) {
-        const int d = 32 * dt + 8 * gi + 4 * hh;
-        u32x2 pk2;
-        pk2[0] = pack2(acc[dt][4 * gi], acc[dt][4 * gi + 1]);
-        pk2[1] = pack2(acc[dt][4 * gi + 2], acc[dt][4 * gi + 3]);
-        *(u32x2*)(orow + d) = pk2;
+      for (int i = 0; i < 16; ++i) acc[dt][i] = 0.f;
+    // P leaves through the wave's LDS slice, 32 rows x 32 keys at a time: the C
+    // layout is written as 16-byte chunks (chunk c of row r at c ^ (r & 7), so
+    // neither the writes nor the reads conflict) and read back so that 8 lanes
+    // cover a row's 128 bytes: every store instruction writes 8 whole 128-byte
+    // line segments.  Lane l stores rows 8j + l/8 (j = 0..3) of the wave.
+    float* prs[4];
+    int pvalid = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int r = w * 32 + 8 * j + (lane >> 3);
+      const int pos = ri.p0 + r % bm_pos;
+      const bool ok = r < nrows && pos < Sq;
+      pvalid |= (int)ok << j;
+      prs[j] = probs + (((int64_t)ri.b * Hq + (int64_t)ri.g * n_rep + (ok ? r / bm_pos : 0)) * Sq +
+                        (ok ? pos : 0)) * Sk;
+    }
+    float* stg = sP[w];
+    f32x16 held[2];  // P of the previous tile, stored by the next
+    // true when every lane of store_p(t)'s 8 store instructions is active, so
+    // that exactly 8 vector-memory instructions issue
+    auto full_p = [&](int t) { return pvalid == 15 && vec4 && (t + 1) * BN <= Sk; };
+    auto store_p = [&](int t) {
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) {
+#pragma unroll
+        for (int g4 = 0; g4 < 4; ++g4)
+          *(f32x4*)&stg[c32 * 32 + (((2 * g4 + hh) ^ (c32 & 7)) * 4)] =
+              f32x4{held[mt][4 * g4], held[mt][4 * g4 + 1], held[mt][4 * g4 + 2],
+                    held[mt][4 * g4 + 3]};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int rr = 8 * j + (lane >> 3), cl = lane & 7;
+          const f32x4 v4 = *(const f32x4*)&stg[rr * 32 + ((cl ^ (rr & 7)) * 4)];
+          const int key = t * BN + 32 * mt + 4 * cl;
+          if (!((pvalid >> j) & 1)) continue;
+          if (vec4) {
+            if (key < Sk) __builtin_nontemporal_store(v4, (f32x4*)(prs[j] + key));
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              if (key + e < Sk) prs[j][key + e] = v4[e];
+          }
+        }
       }
-  }
+    };
+    auto body2 = [&](int it, auto bufc) {
+      constexpr int buf = decltype(bufc)::value;
+      // the tile loads, the zero rows, then P of tile it - 1: the 8 P stores
+      // are the last vector-memory instructions of the tile, so the end-of-tile
+      // wait can leave them in flight through the next tile
+      if (it + 1 < ntiles) {
+        stage_k(it + 1, buf ^ 1);
+        stage_v(it + 1, buf ^ 1);
+      }
+      zero_rows(ntiles + it);
+      const bool full = it > 0 && __builtin_amdgcn_ballot_w64(!full_p(it - 1)) == 0;
+      if (it > 0) store_p(it - 1);
+      f32x16 s[2];
+      scores(it, sK[buf], sKD[buf], s);
+      u32x4 pk[4];
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int i = 0; i < 16; i += 2) {
+          const float p0 = fast_exp2(__builtin_fmaf(s[mt][i], scale_log2, -L));
+          const float p1 = fast_exp2(__builtin_fmaf(s[mt][i + 1], scale_log2, -L));
+          held[mt][i] = p0;
+          held[mt][i + 1] = p1;
+          pk[2 * mt + (i >> 3)][(i & 7) >> 1] = pack2(p0, p1);
+        }
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const bf16x8 pb = as_bf16x8(pk[c]);
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+          const bf16x8 a = lds_frag<BN / 8>(sV[buf], 32 * dt + c32, 2 * c + hh);
+          acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb, acc[dt], 0, 0, 0);
+        }
+      }
+      if (full)
+        vm_wait<8>();
+      else
+        lds_copy_wait();
+      __syncthreads();
+    };
+    // walk 2 starts in the buffer walk 1's last iteration filled: buffer 1 when
+    // ntiles is odd (that first tile is peeled), else 0
+    int it2 = 0;
+    if (ntiles & 1) {
+      body2(0, std::integral_constant<int, 1>{});
+      it2 = 1;
+    }
+    for (; it2 < ntiles; it2 += 2) {
+      body2(it2, std::integral_constant<int, 0>{});
+      if (it2 + 1 < ntiles) body2(it2 + 1, std::integral_constant<int, 1>{});
+    }
+    if (ntiles > 0) store_p(ntiles - 1);
+
+    if (ri.q_valid) {
+      bf16* orow = out + (((int64_t)ri.b * Sq + ri.pos) * Hq + ri.hq) * D;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int gi = 0; gi < 4; ++gi) {
+          const int d = 32 * dt + 8 * gi + 4 * hh;
+          u32x2 pk2;
+          pk2[0] = pack2(acc[dt][4 * gi], acc[dt][4 * gi + 1]);
+          pk2[1] = pack2(acc[dt][4 * gi + 2], acc[dt][4 * gi + 3]);
+          *(u32x2*)(orow + d) = pk2;
+        }
+    }
   }
 }
 
