@@ -10,13 +10,14 @@ with P = B*Hq*S*(S+1)/2 causal (query, key) pairs (forward 4*D*P, backward
 Also reported: per-kernel HIP-event timings (the library brackets each launch
 on its own stream), the roofline of the dominant kernel, the forward alone
 (C2), the C3 step on packed documents (C3-doc; flops of same-document pairs
-only) and with an all-True key_padding_mask (C3-kpm), the Llama-3-70B shape fwd+bwd (C5: B=1, S=16384, 64 query heads) and its
+only), with an all-True key_padding_mask (C3-kpm) and in float16 (C3-fp16), the
+Llama-3-70B shape fwd+bwd (C5: B=1, S=16384, 64 query heads) and its
 2048-token probability capture (C5-cap), the KV-cache decode configuration C4
 in GB/s, and the reference's PyTorch paths timed on the host CPU (C3 sample,
 C4 decode, C5-cap capture) next to them.
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline]
-    python bench.py --only c3|c2|c3doc|c3kpm|c5|c5cap|c4 [--steps K] [--warmup W]
+    python bench.py --only c3|c2|c3doc|c3kpm|c3fp16|c5|c5cap|c4 [--steps K] [--warmup W]
         one workload: W untimed steps, K timed steps, then K steps with the
         per-kernel event timing (the shape profiling runs use)
     python bench.py --rocprof-summary DIR [DIR ...] --warmup W --steps K
@@ -96,7 +97,7 @@ class Workloads:
         self.torch, self.ops, self.dev = torch, ops, dev
         self.rope = precompute_rope_frequencies
         self.bf16 = torch.bfloat16
-        self._c3 = self._c5 = self._c4 = self._doc = self._ones = None
+        self._c3 = self._c5 = self._c4 = self._doc = self._ones = self._c3h = None
 
     # C3 / C2 / C3-doc share the 8B-shape tensors
     def c3_inputs(self):
@@ -112,6 +113,17 @@ class Workloads:
 
     def c3_step(self):
         q, k, v, do, cos, sin = self.c3_inputs()
+        out = self.ops.attention(q, k, v, cos, sin, causal=True)
+        self.torch.autograd.grad(out, (q, k, v), do)
+
+    def c3fp16_step(self):
+        # the C3 step in float16 (the reference's mixed_precision = "fp16"):
+        # the same seeded values, stored as fp16
+        if self._c3h is None:
+            self._c3h = tuple(t.detach().to(self.torch.float16).requires_grad_(t.requires_grad)
+                              if t.is_floating_point() and t.dtype == self.bf16 else t
+                              for t in self.c3_inputs())
+        q, k, v, do, cos, sin = self._c3h
         out = self.ops.attention(q, k, v, cos, sin, causal=True)
         self.torch.autograd.grad(out, (q, k, v), do)
 
@@ -318,7 +330,7 @@ def capture_bytes():
 def run_only(args, torch, wl):
     """One workload: W untimed steps, K timed steps, K event-timed steps."""
     steps = {"c3": wl.c3_step, "c2": wl.c2_step, "c3doc": wl.c3doc_step,
-             "c3kpm": wl.c3kpm_step, "c5": wl.c5_step,
+             "c3kpm": wl.c3kpm_step, "c3fp16": wl.c3fp16_step, "c5": wl.c5_step,
              "c5cap": wl.c5cap_step, "c4": wl.c4_step}
     fn = steps[args.only]
     secs = timed(torch, fn, args.warmup, args.steps)
@@ -386,6 +398,15 @@ def run_full(args, torch, wl):
              "vs_unmasked_step": round(kpm_s * 1e3 / ms_step, 3),
              "kernels_us": {n: round(s["avg_us"], 1) for n, s in kk.items()},
              "launches_per_step": {n: s["launches"] // args.steps for n, s in kk.items()}}
+
+    # C3-fp16: the C3 step on float16 inputs (mixed_precision = "fp16")
+    h_s = timed(torch, wl.c3fp16_step, args.warmup, args.steps)
+    kh = kernel_stats(torch, wl.c3fp16_step, args.steps)
+    c3fp16 = {"config": "C3-fp16 C3 with float16 q/k/v/dO (the same seeded values)",
+              "ms": round(h_s * 1e3, 4), "TFLOP/s": round(flops_step / h_s / 1e12, 1),
+              "vs_bf16_step": round(h_s * 1e3 / ms_step, 3),
+              "kernels_us": {n: round(s["avg_us"], 1) for n, s in kh.items()}}
+    wl._c3h = None
 
     # C5 and C5-cap
     P5 = pairs(C5["B"], C5["Hq"], C5["S"])
@@ -458,6 +479,7 @@ def run_full(args, torch, wl):
         "c3_graph": c3_graph,
         "c3_doc": c3doc,
         "c3_kpm": c3kpm,
+        "c3_fp16": c3fp16,
         "c5": c5,
         "c5_cap": c5cap,
         "decode": decode,
@@ -594,7 +616,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--only", choices=("c3", "c2", "c3doc", "c3kpm", "c5", "c5cap", "c4"))
+    ap.add_argument("--only", choices=("c3", "c2", "c3doc", "c3kpm", "c3fp16", "c5", "c5cap",
+                                         "c4"))
     ap.add_argument("--rocprof-summary", nargs="+", metavar="DIR")
     ap.add_argument("--traffic-json", metavar="PATH",
                     help="with --rocprof-summary: write HBM bytes per launch per kernel")

@@ -87,10 +87,11 @@ int kf_attn_fwd(const void* q, const void* k, const void* v, const float* rope_c
 /* Workspace bytes kf_attn_bwd needs. */
 int kf_attn_bwd_workspace_size(int B, int S, int Hq, int Hkv, int D, int dtype, size_t* bytes);
 
-/* Workspace bytes with which kf_attn_bwd keeps the bf16 dS tiles of the dK/dV
+/* Workspace bytes with which kf_attn_bwd keeps the dS tiles (bf16 or fp16, the
+ * input's type) of the dK/dV
  * pass for dQ instead of recomputing S and dP (one fewer pass over the
  * attention matrix; B*Hq*P*(P+64) bytes extra for causal, 2*B*Hq*P*P for full
- * attention, P = S rounded up to 128).  Applies to the bf16 kernels up to
+ * attention, P = S rounded up to 128).  Applies to the bf16 / fp16 kernels up to
  * 32 GiB of tiles (and S <= 65536 with doc_ids or key_valid; with doc_ids the
  * tiles are written only where documents meet; with key_valid only causal
  * launches keep them, and only for the batch rows whose key 0 is valid, which
@@ -122,7 +123,7 @@ int kf_attn_bwd(const void* q, const void* k, const void* v, const float* rope_c
 
 /* Rotated operands kept from the forward for the backward ("rot"): q and k
  * after RoPE as the backward's kernels read them, K [B*Hkv][P][D] then Q
- * [B*Hq][P][D] in bf16, P = S rounded up to 128, rows past S zero.  The pair
+ * [B*Hq][P][D] in the input's type, P = S rounded up to 128, rows past S zero.  The pair
  * below replaces kf_attn_fwd / kf_attn_bwd for self-attention (k_rotated = 0,
  * contiguous BSHD k and v): the forward writes rot next to out and lse, and
  * the backward reads it instead of q and k, skipping their rotation (one fewer
@@ -132,7 +133,7 @@ int kf_attn_bwd(const void* q, const void* k, const void* v, const float* rope_c
  * to kf_attn_fwd / kf_attn_bwd.  No counterpart in the reference's interface.
  *
  * kf_attn_rot_size: bytes of rot, or KF_ERR_UNSUPPORTED when the pair does
- * not take these sizes, dtype (bf16 only) or mask kinds (has_doc,
+ * not take these sizes, dtype (bf16 or fp16) or mask kinds (has_doc,
  * has_key_valid: whether doc_ids / key_valid will be passed). */
 int kf_attn_rot_size(int B, int S, int Hq, int Hkv, int D, int dtype, int has_doc,
                      int has_key_valid, size_t* bytes);

@@ -212,7 +212,8 @@ int kf_attn_rot_size(int B, int S, int Hq, int Hkv, int D, int dtype, int has_do
   if (rc) return rc;
   KF_CHECK_ARG(bytes != nullptr, "bytes is null");
   if (!rot_supported(B, S, Hq, Hkv, D, dtype, has_doc, has_key_valid)) {
-    set_error("the rotated-operand path needs bf16, head_dim 64 or 128 and one mask kind at most");
+    set_error(
+        "the rotated-operand path needs bf16 or fp16, head_dim 64 or 128 and one mask kind at most");
     return KF_ERR_UNSUPPORTED;
   }
   *bytes = rot_bytes(B, S, Hq, Hkv, D);
@@ -233,7 +234,7 @@ int kf_attn_fwd_rot(const void* q, const void* k, const void* v, const float* ro
                        (int64_t)Hkv * D, D, 0, causal, doc_ids, key_valid, dtype, stream);
   if (!rot_supported(B, S, Hq, Hkv, D, dtype, doc_ids != nullptr, key_valid != nullptr) ||
       !fwd_mfma_supported(a) || ((uintptr_t)rot & 15) != 0) {
-    set_error("kf_attn_fwd_rot needs the bf16 MFMA path (sizes as kf_attn_rot_size accepts, "
+    set_error("kf_attn_fwd_rot needs the MFMA path (sizes as kf_attn_rot_size accepts, "
               "16-byte aligned pointers)");
     return KF_ERR_UNSUPPORTED;
   }
@@ -252,7 +253,7 @@ int kf_attn_bwd_rot_workspace_size(int B, int S, int Hq, int Hkv, int D, int dty
   if (rc) return rc;
   KF_CHECK_ARG(bytes != nullptr, "bytes is null");
   if (!rot_supported(B, S, Hq, Hkv, D, dtype, 0, 0)) {
-    set_error("the rotated-operand path needs bf16 and head_dim 64 or 128");
+    set_error("the rotated-operand path needs bf16 or fp16 and head_dim 64 or 128");
     return KF_ERR_UNSUPPORTED;
   }
   BwdArgs a = sizing_args(B, S, Hq, Hkv, D, dtype, causal);
@@ -283,7 +284,7 @@ int kf_attn_bwd_rot(const void* rot, const void* v, const float* rope_cos, const
   a.stream = (hipStream_t)stream;
   if (!rot_supported(B, S, Hq, Hkv, D, dtype, doc_ids != nullptr, key_valid != nullptr) ||
       !bwd_mfma_supported(a) || ((uintptr_t)rot & 15) != 0) {
-    set_error("kf_attn_bwd_rot needs the bf16 MFMA path (sizes as kf_attn_rot_size accepts, "
+    set_error("kf_attn_bwd_rot needs the MFMA path (sizes as kf_attn_rot_size accepts, "
               "16-byte aligned pointers)");
     return KF_ERR_UNSUPPORTED;
   }

@@ -1,7 +1,7 @@
-// bf16 MFMA backward attention for gfx950 (head_dim 64 or 128).
+// bf16 / fp16 MFMA backward attention for gfx950 (head_dim 64 or 128).
 //
 // Four launches, no atomics (bit-deterministic):
-//  kv_prep      (shared with the forward) per KV head: K rotated (eager bf16
+//  kv_prep      (shared with the forward) per KV head: K rotated (eager
 //               RoPE) [bh][P][D], rows past S zero.
 //  q_prep_bwd   per query head: Q rotated [bhq][P][D]; lse*log2(e) and Delta =
 //               rowsum(dO o O) [bhq][P].  P = S rounded up to 128; padded rows
@@ -18,7 +18,7 @@
 //               layout with one key per lane; P and dS then feed dV^T += dO^T P
 //               and dK^T += Q^T dS as B operands directly.  RoPE backward and the
 //               softmax scale are applied at the dK store.  When the caller's
-//               workspace holds them it also writes every dS tile (bf16) to a
+//               workspace holds them it also writes every dS tile (16-bit) to a
 //               record for dQ (with key padding: for the batch rows whose first
 //               key is valid).
 //  dq_ds        (dS records kept) dQ^T += K^T dS^T from the records: one
@@ -61,13 +61,14 @@ constexpr int BQ = 64;    // queries per dK/dV tile
 
 __host__ __device__ constexpr int pad_len(int S) { return (S + BKV - 1) / BKV * BKV; }
 
-// dS records.  The dK/dV kernel writes every dS tile it computes, bf16, for
+// dS records.  The dK/dV kernel writes every dS tile it computes, in the
+// input's 16-bit type, for
 // the dQ kernel to read instead of recomputing S and dP (with key padding only
 // for batch rows without guarded rows, i.e. whose key 0 is valid: a guarded
 // row sees keys past the diagonal, outside this layout).
 // A record is one dS wavefront's tile: DSQ query positions x DSK keys of one
 // query head, 4 KB, stored as that wavefront's four MFMA B operands exactly as
-// they sit in registers: [chunk c][lane][8 bf16], lane = 32*hh + key, slot
+// they sit in registers: [chunk c][lane][8 elements], lane = 32*hh + key, slot
 // 4*half + j = row 16c + 8*half + 4*hh + j.  Records are ordered (KV head,
 // query tile, key column, query head of the group); with a causal mask only
 // the key columns k32 <= 2*qt + 1 that the tile's rows can see exist.
@@ -82,11 +83,11 @@ __host__ __device__ inline int64_t ds_pair(int bh, int qt, int k32, int nqtp, in
                 : ((int64_t)bh * nqtp + qt) * (2 * nqtp) + k32;
 }
 
-template <int D>
+template <typename T, int D>
 __global__ __launch_bounds__(256) void q_prep_bwd_kernel(
-    const bf16* __restrict__ q, const bf16* __restrict__ out, const bf16* __restrict__ dout,
+    const T* __restrict__ q, const T* __restrict__ out, const T* __restrict__ dout,
     const float* __restrict__ lse, const float* __restrict__ cos, const float* __restrict__ sin,
-    bf16* __restrict__ qrot, float* __restrict__ lse2, float* __restrict__ delta, int S, int P,
+    T* __restrict__ qrot, float* __restrict__ lse2, float* __restrict__ delta, int S, int P,
     int Hq, float inv_scale) {
   constexpr int HALF = D / 2, CP = HALF / 8, TPR = D / 8;
   const int s0 = blockIdx.x * BN, bhq = blockIdx.y, b = bhq / Hq, h = bhq % Hq;
@@ -98,14 +99,14 @@ __global__ __launch_bounds__(256) void q_prep_bwd_kernel(
     if (s < S) {
       // q and O are read once here: non-temporal loads (streaming, ~15% faster
       // from HBM than cached ones); dO stays cached for the kernels after
-      const bf16* src = q + (((int64_t)b * S + s) * Hq + h) * D;
+      const T* src = q + (((int64_t)b * S + s) * Hq + h) * D;
       float x1[8], x2[8];
-      unpack8(__builtin_nontemporal_load((const u32x4*)(src + 8 * c)), x1);
-      unpack8(__builtin_nontemporal_load((const u32x4*)(src + 8 * c + HALF)), x2);
-      rope8_bf16(x1, x2, cos + (int64_t)s * HALF + 8 * c, sin + (int64_t)s * HALF + 8 * c, o1,
+      unpack8<T>(__builtin_nontemporal_load((const u32x4*)(src + 8 * c)), x1);
+      unpack8<T>(__builtin_nontemporal_load((const u32x4*)(src + 8 * c + HALF)), x2);
+      rope8<T>(x1, x2, cos + (int64_t)s * HALF + 8 * c, sin + (int64_t)s * HALF + 8 * c, o1,
                  o2);
     }
-    bf16* dst = qrot + ((int64_t)bhq * P + s) * D;
+    T* dst = qrot + ((int64_t)bhq * P + s) * D;
     *(u32x4*)(dst + 8 * c) = o1;
     *(u32x4*)(dst + 8 * c + HALF) = o2;
   }
@@ -130,8 +131,8 @@ __global__ __launch_bounds__(256) void q_prep_bwd_kernel(
     float part = 0.f;
     if (s < S) {
       float fd[8], fo[8];
-      unpack8(ad[k], fd);
-      unpack8(ao[k], fo);
+      unpack8<T>(ad[k], fd);
+      unpack8<T>(ao[k], fo);
 #pragma unroll
       for (int j = 0; j < 8; ++j) part += fd[j] * fo[j];
     }
@@ -148,14 +149,14 @@ __global__ __launch_bounds__(256) void q_prep_bwd_kernel(
 
 // dK/dV workgroup: 8 wavefronts on the same 128 keys, two roles that split the
 // four products evenly.  Wavefronts 0-3 ("P waves") compute S = Q K^T, turn it
-// into P (bf16) and accumulate dV^T += dO^T P; they hand P to the wavefront of
+// into P (16-bit) and accumulate dV^T += dO^T P; they hand P to the wavefront of
 // the other role that owns the same 32 keys through LDS.  Wavefronts 4-7
 // ("dS waves") compute dP = dO V^T meanwhile, then dS = P o (dP - Delta) and
 // accumulate dK^T += Q^T dS.  Each role needs only its own B operands and
 // accumulators, so two wavefronts fit per SIMD and overlap each other.
-template <int D>
+template <typename T, int D>
 struct DkdvStage {
-  bf16 q[BQ * D], o[BQ * D];
+  T q[BQ * D], o[BQ * D];
   float l[BQ], dl[BQ];  // -lse / scale and -Delta of the tile's rows
 };
 
@@ -166,13 +167,13 @@ struct DkdvStage {
 // MASK_KPM: qlist as above, drow the key-validity row, fv the first valid
 // key's position: query rows before it (guarded) see every key, other rows
 // need the key valid and not after them.
-template <int D, bool DSROLE, int MODE, bool STORE>
+template <typename T, int D, bool DSROLE, int MODE, bool STORE>
 __device__ __forceinline__ void dkdv_role(
-    DkdvStage<D>* st, u32x4* sP, const bf16* __restrict__ krot, const bf16* __restrict__ v,
-    const bf16* __restrict__ qrot, const bf16* __restrict__ dout,
+    DkdvStage<T, D>* st, u32x4* sP, const T* __restrict__ krot, const T* __restrict__ v,
+    const T* __restrict__ qrot, const T* __restrict__ dout,
     const float* __restrict__ lse2, const float* __restrict__ delta,
-    const float* __restrict__ cos, const float* __restrict__ sin, bf16* __restrict__ dk,
-    bf16* __restrict__ dv, int S, int P, int Hq, int Hkv, int n_rep, int b, int g, int bh, int k0,
+    const float* __restrict__ cos, const float* __restrict__ sin, T* __restrict__ dk,
+    T* __restrict__ dv, int S, int P, int Hq, int Hkv, int n_rep, int b, int g, int bh, int k0,
     int w, int lane, float scale_log2, float scale, int causal, const int32_t* __restrict__ drow,
     const uint16_t* qlist, int nlist, int32_t (*sQD)[BQ], int fv, u32x4* __restrict__ dsb,
     int nqtp, bool live) {
@@ -208,7 +209,7 @@ __device__ __forceinline__ void dkdv_role(
     const int hq = g * n_rep + hl;
     const int64_t bhq = (int64_t)b * Hq + hq;
     const int q0 = qtile * BQ;
-    DkdvStage<D>& S_ = st[buf];
+    DkdvStage<T, D>& S_ = st[buf];
     // (the masked modes recompute the per-lane offsets per tile: their lists
     // and masks leave no registers to keep them in)
     tile_to_lds<BQ, KR, 8, LIST>(qrot + (bhq * P + q0) * D, D, S_.q, w, lane);
@@ -220,9 +221,10 @@ __device__ __forceinline__ void dkdv_role(
       // the row statistics' LDS addresses from the stage array's base plus
       // constant offsets: with the pointer into the stage member, the masked
       // kernels fail to compile ("Operand has incorrect register class")
-      const uint32_t sb = st_lds + (uint32_t)(buf * sizeof(DkdvStage<D>));
-      if (w == 0) dma4(sb + offsetof(DkdvStage<D>, l), (uint32_t)lane * 4u, lse2 + bhq * P + q0);
-      if (w == 1) dma4(sb + offsetof(DkdvStage<D>, dl), (uint32_t)lane * 4u, delta + bhq * P + q0);
+      using Stage = DkdvStage<T, D>;
+      const uint32_t sb = st_lds + (uint32_t)(buf * sizeof(Stage));
+      if (w == 0) dma4(sb + offsetof(Stage, l), (uint32_t)lane * 4u, lse2 + bhq * P + q0);
+      if (w == 1) dma4(sb + offsetof(Stage, dl), (uint32_t)lane * 4u, delta + bhq * P + q0);
     } else {
       if (w == 0) row_to_lds(lse2 + bhq * P + q0, S_.l, lane);
       if (w == 1) row_to_lds(delta + bhq * P + q0, S_.dl, lane);
@@ -244,7 +246,7 @@ __device__ __forceinline__ void dkdv_role(
     int hh_l = hh;
     if (LIST) asm volatile("" : "+v"(hh_l));
     const bool ok = !DSROLE || key_l < S;
-    const bf16* src = DSROLE ? v + (((int64_t)b * S + (ok ? key_l : 0)) * Hkv + g) * D + 8 * hh_l
+    const T* src = DSROLE ? v + (((int64_t)b * S + (ok ? key_l : 0)) * Hkv + g) * D + 8 * hh_l
                              : krot + ((int64_t)bh * P + key_l) * D + 8 * hh_l;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks)
@@ -257,8 +259,8 @@ __device__ __forceinline__ void dkdv_role(
     for (int i = 0; i < 16; ++i) acc[dt][i] = 0.f;
 
   // A-operand tiles of the two products of this role
-  auto first_tile = [](const DkdvStage<D>& S_) -> const bf16* { return DSROLE ? S_.o : S_.q; };
-  auto second_tile = [](const DkdvStage<D>& S_) -> const bf16* { return DSROLE ? S_.q : S_.o; };
+  auto first_tile = [](const DkdvStage<T, D>& S_) -> const T* { return DSROLE ? S_.o : S_.q; };
+  auto second_tile = [](const DkdvStage<T, D>& S_) -> const T* { return DSROLE ? S_.q : S_.o; };
   u32x4* myP = sP + kw * 4 * 64 + lane;  // chunk c at myP[c * 64]
   const TrOffsets<D> tro = tr_offsets<D>(lane);
 
@@ -280,7 +282,7 @@ __device__ __forceinline__ void dkdv_role(
   auto tile_body = [&](int it, auto bufc) {
     constexpr int buf = decltype(bufc)::value;
     if (it + 1 < total) stage(it + 1, buf ^ 1);
-    const DkdvStage<D>& S_ = st[buf];
+    const DkdvStage<T, D>& S_ = st[buf];
     const int e = entry(it);
     const int q0 = tile_of(e) * BQ;
     const int rel = key - q0;  // rows r of this tile see the key when r >= rel
@@ -311,7 +313,7 @@ __device__ __forceinline__ void dkdv_role(
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) {
       x[mt] = rowv[mt];
-      const bf16* tA = first_tile(S_);
+      const T* tA = first_tile(S_);
       bf16x8 fa[KS];
 #pragma unroll
       for (int ks = 0; ks < PF; ++ks) fa[ks] = lds_frag<KR>(tA, 32 * mt + c32, 2 * ks + hh);
@@ -319,7 +321,7 @@ __device__ __forceinline__ void dkdv_role(
       for (int ks = 0; ks < KS; ++ks) {
         __builtin_amdgcn_sched_barrier(0);
         if (ks + PF < KS) fa[ks + PF] = lds_frag<KR>(tA, 32 * mt + c32, 2 * (ks + PF) + hh);
-        x[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[ks], bf[ks], x[mt], 0, 0, 0);
+        x[mt] = mfma32<T>(fa[ks], bf[ks], x[mt]);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -353,8 +355,8 @@ __device__ __forceinline__ void dkdv_role(
                 v[j] = (!guarded && (rel > r0 + j || !kdoc)) ? 0.f : v[j];
               }
             }
-            pk[2 * mt + (gq >> 1)][2 * (gq & 1)] = pack2(v[0], v[1]);
-            pk[2 * mt + (gq >> 1)][2 * (gq & 1) + 1] = pack2(v[2], v[3]);
+            pk[2 * mt + (gq >> 1)][2 * (gq & 1)] = pack2<T>(v[0], v[1]);
+            pk[2 * mt + (gq >> 1)][2 * (gq & 1) + 1] = pack2<T>(v[2], v[3]);
           }
       };
       if (!(KPM && dmask) && diag)
@@ -394,14 +396,12 @@ __device__ __forceinline__ void dkdv_role(
             float v[4];
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
-              const uint32_t word = pp[2 * half + j];
-              v[2 * j] = __uint_as_float(word << 16);
-              v[2 * j + 1] = __uint_as_float(word & 0xffff0000u);
+              unpack2<T>(pp[2 * half + j], v[2 * j], v[2 * j + 1]);
             }
 #pragma unroll
             for (int j = 0; j < 4; ++j) v[j] *= x[mt][4 * gq + j];
-            pk[2 * mt + cc][2 * half] = pack2(v[0], v[1]);
-            pk[2 * mt + cc][2 * half + 1] = pack2(v[2], v[3]);
+            pk[2 * mt + cc][2 * half] = pack2<T>(v[0], v[1]);
+            pk[2 * mt + cc][2 * half + 1] = pack2<T>(v[2], v[3]);
           }
         }
       if (STORE && rec >= 0) {
@@ -412,7 +412,7 @@ __device__ __forceinline__ void dkdv_role(
     // phase 2: dV^T += dO^T P (P waves) or dK^T += Q^T dS (dS waves)
     {
       constexpr int NS = 4 * DT;
-      const bf16* tA = second_tile(S_);
+      const T* tA = second_tile(S_);
       bf16x8 fa[NS];
 #pragma unroll
       for (int n = 0; n < PF; ++n)
@@ -422,8 +422,7 @@ __device__ __forceinline__ void dkdv_role(
         __builtin_amdgcn_sched_barrier(0);
         if (n + PF < NS)
           fa[n + PF] = lds_frag_t<D>(tA, tro, (n + PF) / DT, (n + PF) % DT);
-        acc[n % DT] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[n], as_bf16x8(pk[n / DT]),
-                                                             acc[n % DT], 0, 0, 0);
+        acc[n % DT] = mfma32<T>(fa[n], as_bf16x8(pk[n / DT]), acc[n % DT]);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -444,7 +443,7 @@ __device__ __forceinline__ void dkdv_role(
   int hoff = 4 * hh;
   if (LIST) asm volatile("" : "+v"(hoff));
   if (DSROLE) {
-    bf16* dkr = dk + (((int64_t)b * S + key_e) * Hkv + g) * D + hoff;
+    T* dkr = dk + (((int64_t)b * S + key_e) * Hkv + g) * D + hoff;
     const float* cr = cos + (int64_t)key_e * HALF + hoff;
     const float* sr = sin + (int64_t)key_e * HALF + hoff;
 #pragma unroll
@@ -455,29 +454,29 @@ __device__ __forceinline__ void dkdv_role(
         float lo[4], hi[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          rope_pair_bwd<bf16>(acc[dt][4 * gi + e] * scale, acc[dt + DT / 2][4 * gi + e] * scale,
+          rope_pair_bwd<T>(acc[dt][4 * gi + e] * scale, acc[dt + DT / 2][4 * gi + e] * scale,
                               cr[d + e], sr[d + e], lo[e], hi[e]);
-        *(u32x2*)(dkr + d) = u32x2{pack2(lo[0], lo[1]), pack2(lo[2], lo[3])};
-        *(u32x2*)(dkr + d + HALF) = u32x2{pack2(hi[0], hi[1]), pack2(hi[2], hi[3])};
+        *(u32x2*)(dkr + d) = u32x2{pack2<T>(lo[0], lo[1]), pack2<T>(lo[2], lo[3])};
+        *(u32x2*)(dkr + d + HALF) = u32x2{pack2<T>(hi[0], hi[1]), pack2<T>(hi[2], hi[3])};
       }
   } else {
-    bf16* dvr = dv + (((int64_t)b * S + key_e) * Hkv + g) * D + hoff;
+    T* dvr = dv + (((int64_t)b * S + key_e) * Hkv + g) * D + hoff;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
       for (int gi = 0; gi < 4; ++gi) {
         const int d = 32 * dt + 8 * gi;
-        *(u32x2*)(dvr + d) = u32x2{pack2(acc[dt][4 * gi], acc[dt][4 * gi + 1]),
-                                   pack2(acc[dt][4 * gi + 2], acc[dt][4 * gi + 3])};
+        *(u32x2*)(dvr + d) = u32x2{pack2<T>(acc[dt][4 * gi], acc[dt][4 * gi + 1]),
+                                   pack2<T>(acc[dt][4 * gi + 2], acc[dt][4 * gi + 3])};
       }
   }
 }
 
 // Stage query tile q0 of query head bhq into buffer 0 (what dkdv_role's
 // iteration 0 reads) with its document ids.
-template <int D>
+template <typename T, int D>
 __device__ __forceinline__ void dkdv_stage_first(
-    DkdvStage<D>* st, const bf16* __restrict__ qrot, const bf16* __restrict__ dout,
+    DkdvStage<T, D>* st, const T* __restrict__ qrot, const T* __restrict__ dout,
     const float* __restrict__ lse2, const float* __restrict__ delta,
     const int32_t* __restrict__ drow, int S, int P, int Hq, int b, int hq, int q0, int32_t* sqd,
     int w, int lane) {
@@ -496,17 +495,17 @@ __device__ __forceinline__ void dkdv_stage_first(
 // which runs after it and skips the rows without padding; the unmasked launch
 // walks no query tile for the padded rows' items (their dK / dV are written
 // as zeros, then overwritten by the KPM launch).
-template <int D, int MODE, bool STORE, bool SPLIT = false>
+template <typename T, int D, int MODE, bool STORE, bool SPLIT = false>
 __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(
-    const bf16* __restrict__ krot, const bf16* __restrict__ v, const bf16* __restrict__ qrot,
-    const bf16* __restrict__ dout, const float* __restrict__ lse2, const float* __restrict__ delta,
-    const float* __restrict__ cos, const float* __restrict__ sin, bf16* __restrict__ dk,
-    bf16* __restrict__ dv, int S, int P, int Hq, int Hkv, int n_rep, int nkb, int nitems,
+    const T* __restrict__ krot, const T* __restrict__ v, const T* __restrict__ qrot,
+    const T* __restrict__ dout, const float* __restrict__ lse2, const float* __restrict__ delta,
+    const float* __restrict__ cos, const float* __restrict__ sin, T* __restrict__ dk,
+    T* __restrict__ dv, int S, int P, int Hq, int Hkv, int n_rep, int nkb, int nitems,
     float scale_log2,
     float scale, int causal, const int32_t* __restrict__ aux, const int2* __restrict__ ranges,
     u32x4* __restrict__ dsb, const int* __restrict__ order, const int* __restrict__ kpm_flags) {
   constexpr bool DOC = MODE == MASK_DOC, KPM = MODE == MASK_KPM;
-  __shared__ __attribute__((aligned(16))) DkdvStage<D> st[2];
+  __shared__ __attribute__((aligned(16))) DkdvStage<T, D> st[2];
   __shared__ __attribute__((aligned(16))) u32x4 sP[4 * 4 * 64];  // [key group][chunk][lane]
   __shared__ __attribute__((aligned(16))) int32_t sQD[2][BQ];   // DOC: query document ids
   __shared__ uint16_t sList[DOC_MAX_TILES];                      // listed query tiles
@@ -559,7 +558,7 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(
     }
     if constexpr (DOC) {
       const int qt0 = k0 / BQ;  // the diagonal query tile: always listed, first
-      dkdv_stage_first<D>(st, qrot, dout, lse2, delta, drow, S, P, Hq, b, g * n_rep,
+      dkdv_stage_first<T, D>(st, qrot, dout, lse2, delta, drow, S, P, Hq, b, g * n_rep,
                           qt0 * BQ, sQD[0], w, lane);
       if (w == 0) {
         const int n = doc_tile_list(drow, k0, min(k0 + BKV, S), ranges + (int64_t)b * (P / BN),
@@ -570,12 +569,12 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(
       nlist = __builtin_amdgcn_readfirstlane(sCount);
     }
     if (w >= 4)
-      dkdv_role<D, true, MODE, STORE>(st, sP, krot, v, qrot, dout, lse2, delta, cos, sin, dk,
+      dkdv_role<T, D, true, MODE, STORE>(st, sP, krot, v, qrot, dout, lse2, delta, cos, sin, dk,
                                       dv, S, P, Hq, Hkv, n_rep, b, g, bh, k0, w, lane,
                                       scale_log2, scale, causal, drow, sList, nlist, sQD, fv,
                                       dsb, P / DSQ, live);
     else
-      dkdv_role<D, false, MODE, STORE>(st, sP, krot, v, qrot, dout, lse2, delta, cos, sin, dk,
+      dkdv_role<T, D, false, MODE, STORE>(st, sP, krot, v, qrot, dout, lse2, delta, cos, sin, dk,
                                        dv, S, P, Hq, Hkv, n_rep, b, g, bh, k0, w, lane,
                                        scale_log2, scale, causal, drow, sList, nlist, sQD, fv,
                                        dsb, P / DSQ, live);
@@ -588,11 +587,11 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(
 // DOC walks the listed key tiles last to first, like the forward.
 constexpr int DQ_ROWS = 256;
 
-template <int D, int MODE>
+template <typename T, int D, int MODE>
 __global__ __launch_bounds__(512, 1) void bwd_dq_kernel(
-    const bf16* __restrict__ qrot, const bf16* __restrict__ dout, const float* __restrict__ lse2,
-    const float* __restrict__ delta, const bf16* __restrict__ krot, const bf16* __restrict__ v,
-    const float* __restrict__ cos, const float* __restrict__ sin, bf16* __restrict__ dq, int S,
+    const T* __restrict__ qrot, const T* __restrict__ dout, const float* __restrict__ lse2,
+    const float* __restrict__ delta, const T* __restrict__ krot, const T* __restrict__ v,
+    const float* __restrict__ cos, const float* __restrict__ sin, T* __restrict__ dq, int S,
     int P, int Hq, int Hkv, int n_rep, int bm_pos, int nqb, int nitems, float scale_log2,
     float scale, int causal, const int32_t* __restrict__ aux, const int2* __restrict__ ranges,
     int kpm_skip_clean) {
@@ -600,7 +599,7 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_kernel(
   constexpr int KS = D / 16, DT = D / 32, HALF = D / 2;
   constexpr int KR = D / 8;
   struct Stage {
-    bf16 k[BN * D], v[BN * D];
+    T k[BN * D], v[BN * D];
   };
   __shared__ __attribute__((aligned(16))) Stage st[2];
   __shared__ __attribute__((aligned(16))) int32_t sKD[2][BN];  // LIST: per-key aux values
@@ -631,10 +630,10 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_kernel(
     int ntiles = (kend + BN - 1) / BN;
     const int32_t* drow = LIST ? aux + (int64_t)ri.b * S : nullptr;
     const int2* rec = ranges + (int64_t)ri.b * (P / BN);
-    const bf16* kbase = krot + (int64_t)bh * P * D;
+    const T* kbase = krot + (int64_t)bh * P * D;
     // V read in place ([B, S, Hkv, D]); rows past S repeat row S - 1 (their K
     // rows are zero, so they add nothing to dQ)
-    const bf16* vbase = v + ((int64_t)ri.b * S * Hkv + ri.g) * D;
+    const T* vbase = v + ((int64_t)ri.b * S * Hkv + ri.g) * D;
     auto stage = [&](int t, int buf) {
       tile_to_lds<BN, KR, 8, true>(kbase + (int64_t)t * BN * D, D, st[buf].k, w, lane);
       tile_to_lds<BN, KR, 8, true>(vbase + (int64_t)t * BN * Hkv * D, Hkv * D, st[buf].v, w, lane,
@@ -685,8 +684,8 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_kernel(
     float l2 = INFINITY, ndl = 0.f;  // ndl: -Delta of this lane's row
     if (ri.q_valid) {
       const int hoff = 8 * (lane_l >> 5);
-      const bf16* qr = qrot + (bhq * P + ri.pos) * D + hoff;
-      const bf16* dr = dout + (((int64_t)ri.b * S + ri.pos) * Hq + ri.hq) * D + hoff;
+      const T* qr = qrot + (bhq * P + ri.pos) * D + hoff;
+      const T* dr = dout + (((int64_t)ri.b * S + ri.pos) * Hq + ri.hq) * D + hoff;
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
         qf[ks] = as_bf16x8(*(const u32x4*)(qr + 16 * ks));
@@ -753,8 +752,8 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_kernel(
               fk[ks + PF] = lds_frag<KR>(S_.k, 32 * mt + c32, 2 * (ks + PF) + hh);
               fv[ks + PF] = lds_frag<KR>(S_.v, 32 * mt + c32, 2 * (ks + PF) + hh);
             }
-            s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fk[ks], qf[ks], s, 0, 0, 0);
-            dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fv[ks], df[ks], dp, 0, 0, 0);
+            s = mfma32<T>(fk[ks], qf[ks], s);
+            dp = mfma32<T>(fv[ks], df[ks], dp);
           }
           __builtin_amdgcn_sched_barrier(0);
         }
@@ -780,7 +779,7 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_kernel(
             }
             dsv[j] = p * (dp[i + j] + ndl);
           }
-          dsk[i >> 3][(i & 7) >> 1] = pack2(dsv[0], dsv[1]);
+          dsk[i >> 3][(i & 7) >> 1] = pack2<T>(dsv[0], dsv[1]);
         }
         {
           constexpr int NS = 2 * DT, PF = 1;
@@ -793,8 +792,7 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_kernel(
             __builtin_amdgcn_sched_barrier(0);
             if (n + PF < NS)
               fa[n + PF] = lds_frag_t<D>(S_.k, tro, 2 * mt + (n + PF) / DT, (n + PF) % DT);
-            acc[n % DT] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[n], as_bf16x8(dsk[n / DT]),
-                                                                 acc[n % DT], 0, 0, 0);
+            acc[n % DT] = mfma32<T>(fa[n], as_bf16x8(dsk[n / DT]), acc[n % DT]);
           }
           __builtin_amdgcn_sched_barrier(0);
         }
@@ -804,7 +802,7 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_kernel(
     }
 
     if (ri.q_valid) {
-      bf16* dqr = dq + (((int64_t)ri.b * S + ri.pos) * Hq + ri.hq) * D;
+      T* dqr = dq + (((int64_t)ri.b * S + ri.pos) * Hq + ri.hq) * D;
       const int hoff = 4 * (lane_l >> 5);
       const float* cr = cos + (int64_t)ri.pos * HALF + hoff;
       const float* sr = sin + (int64_t)ri.pos * HALF + hoff;
@@ -816,10 +814,10 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_kernel(
           float lo[4], hi[4];
 #pragma unroll
           for (int e = 0; e < 4; ++e)
-            rope_pair_bwd<bf16>(acc[dt][4 * gi + e] * scale, acc[dt + DT / 2][4 * gi + e] * scale,
+            rope_pair_bwd<T>(acc[dt][4 * gi + e] * scale, acc[dt + DT / 2][4 * gi + e] * scale,
                                 cr[d + e], sr[d + e], lo[e], hi[e]);
-          *(u32x2*)(dqr + d + hoff) = u32x2{pack2(lo[0], lo[1]), pack2(lo[2], lo[3])};
-          *(u32x2*)(dqr + d + hoff + HALF) = u32x2{pack2(hi[0], hi[1]), pack2(hi[2], hi[3])};
+          *(u32x2*)(dqr + d + hoff) = u32x2{pack2<T>(lo[0], lo[1]), pack2<T>(lo[2], lo[3])};
+          *(u32x2*)(dqr + d + hoff + HALF) = u32x2{pack2<T>(hi[0], hi[1]), pack2<T>(hi[2], hi[3])};
         }
     }
     __syncthreads();  // LDS of this item is free for the next
@@ -846,10 +844,10 @@ __device__ __forceinline__ void dma16_nt(uint32_t lds, uint32_t voff, const void
 // tiles listed for the query tile, two record columns per 64-key tile; with key
 // padding (KPM) the causal tiles holding a valid key, in batch rows whose key 0
 // is valid (the others are left to the recompute kernel).
-template <int D, int HB, int MODE, int NBUF>
+template <typename T, int D, int HB, int MODE, int NBUF>
 __global__ __launch_bounds__(64 * HB) void bwd_dq_ds_kernel(
-    const u32x4* __restrict__ dsb, const bf16* __restrict__ krot, const float* __restrict__ cos,
-    const float* __restrict__ sin, bf16* __restrict__ dq, int S, int P, int Hq, int Hkv,
+    const u32x4* __restrict__ dsb, const T* __restrict__ krot, const float* __restrict__ cos,
+    const float* __restrict__ sin, T* __restrict__ dq, int S, int P, int Hq, int Hkv,
     int n_rep, int nqt, int causal, float scale, const int32_t* __restrict__ doc,
     const int2* __restrict__ ranges) {
   constexpr bool DOC = MODE == MASK_DOC, KPM = MODE == MASK_KPM, LIST = DOC || KPM;
@@ -860,7 +858,7 @@ __global__ __launch_bounds__(64 * HB) void bwd_dq_ds_kernel(
   // load instructions per wavefront and step: its share of K, its record's 4 KB
   constexpr int NLOAD = KI / NW + 4;
   struct Stage {
-    bf16 k[DSK * D];
+    T k[DSK * D];
     u32x4 ds[HB * 256];
   };
   __shared__ __attribute__((aligned(16))) Stage st[NBUF];
@@ -907,7 +905,7 @@ __global__ __launch_bounds__(64 * HB) void bwd_dq_ds_kernel(
                 : t;
   };
   const u32x4* rec0 = dsb + (ds_pair(bh, qt, 0, nqtp, causal) * n_rep + hg * HB) * 256;
-  const bf16* kbase = krot + (int64_t)bh * P * D;
+  const T* kbase = krot + (int64_t)bh * P * D;
   auto stage = [&](int t_, int buf) {
     const int t = col(t_);
 #pragma unroll
@@ -984,7 +982,7 @@ __global__ __launch_bounds__(64 * HB) void bwd_dq_ds_kernel(
 #pragma unroll
         for (int mh = 0; mh < 2; ++mh)
           acc[mh][dt] =
-              __builtin_amdgcn_mfma_f32_32x32x16_bf16(ak, bds[mh], acc[mh][dt], 0, 0, 0);
+              mfma32<T>(ak, bds[mh], acc[mh][dt]);
       }
     }
   }
@@ -996,7 +994,7 @@ __global__ __launch_bounds__(64 * HB) void bwd_dq_ds_kernel(
   // consecutive lanes per row, instead of 8 bytes of each of 32 rows.
   static_assert(HB * 64 * D * 2 <= NBUF * (int)sizeof(Stage), "dQ slices exceed the ring");
   __syncthreads();
-  bf16* slice = (bf16*)st + w * 64 * D;
+  T* slice = (T*)st + w * 64 * D;
 #pragma unroll
   for (int mh = 0; mh < 2; ++mh) {
     const int r = 32 * mh + c32;
@@ -1011,14 +1009,14 @@ __global__ __launch_bounds__(64 * HB) void bwd_dq_ds_kernel(
         float lo[4], hi[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          rope_pair_bwd<bf16>(acc[mh][dt][4 * gi + e] * scale,
+          rope_pair_bwd<T>(acc[mh][dt][4 * gi + e] * scale,
                               acc[mh][dt + DT / 2][4 * gi + e] * scale, cr[d + e], sr[d + e],
                               lo[e], hi[e]);
         const int cl = 4 * dt + gi, chh = KR / 2 + 4 * dt + gi;  // chunks of d and d + HALF
         *(u32x2*)(slice + (r * KR + (cl ^ (r & (KR - 1)))) * 8 + 4 * hh) =
-            u32x2{pack2(lo[0], lo[1]), pack2(lo[2], lo[3])};
+            u32x2{pack2<T>(lo[0], lo[1]), pack2<T>(lo[2], lo[3])};
         *(u32x2*)(slice + (r * KR + (chh ^ (r & (KR - 1)))) * 8 + 4 * hh) =
-            u32x2{pack2(hi[0], hi[1]), pack2(hi[2], hi[3])};
+            u32x2{pack2<T>(hi[0], hi[1]), pack2<T>(hi[2], hi[3])};
       }
   }
   __syncthreads();
@@ -1042,17 +1040,17 @@ __global__ __launch_bounds__(64 * HB) void bwd_dq_ds_kernel(
 // record at a step (the earlier tile at the later tile's last two steps)
 // loads its last record again (the load counts stay equal across wavefronts)
 // and skips the products.
-template <int D, int NBUF>
+template <typename T, int D, int NBUF>
 __global__ __launch_bounds__(512) void bwd_dq_ds2_kernel(
-    const u32x4* __restrict__ dsb, const bf16* __restrict__ krot, const float* __restrict__ cos,
-    const float* __restrict__ sin, bf16* __restrict__ dq, int S, int P, int Hq, int Hkv,
+    const u32x4* __restrict__ dsb, const T* __restrict__ krot, const float* __restrict__ cos,
+    const float* __restrict__ sin, T* __restrict__ dq, int S, int P, int Hq, int Hkv,
     int n_rep, int nqt, float scale) {
   constexpr int HB = 4, NW = 8, KR = D / 8, DT = D / 32, HALF = D / 2;
   constexpr int KI = DSK * KR / 64;  // 1 KB load instructions per K step
   static_assert(KI % NW == 0, "K rows must split evenly over the wavefronts");
   constexpr int NLOAD = KI / NW + 4;
   struct Stage {
-    bf16 k[DSK * D];
+    T k[DSK * D];
     u32x4 ds[NW * 256];
   };
   constexpr int RING_B = NBUF * (int)sizeof(Stage), OUT_B = NW * 64 * D * 2;
@@ -1073,7 +1071,7 @@ __global__ __launch_bounds__(512) void bwd_dq_ds2_kernel(
   const int nk = min(2 * qt_last + 2, nkeys);            // steps of the workgroup
   const int nk_w = live ? min(2 * qt + 2, nkeys) : 0;   // steps with a record of this wave
   const u32x4* rec0 = dsb + (ds_pair(bh, live ? qt : qt_last, 0, nqtp, 1) * n_rep + hg * HB + hw) * 256;
-  const bf16* kbase = krot + (int64_t)bh * P * D;
+  const T* kbase = krot + (int64_t)bh * P * D;
   auto stage = [&](int t, int buf) {
     const int L = w * 64 + lane, row = L / KR, pc = L % KR;  // KI / NW == 1
     const uint32_t off = ((uint32_t)(t * DSK + row) * D + (uint32_t)(pc ^ swz<KR>(row)) * 8u) * 2u;
@@ -1136,7 +1134,7 @@ __global__ __launch_bounds__(512) void bwd_dq_ds2_kernel(
 #pragma unroll
           for (int mh = 0; mh < 2; ++mh)
             acc[mh][dt] =
-                __builtin_amdgcn_mfma_f32_32x32x16_bf16(ak, bds[mh], acc[mh][dt], 0, 0, 0);
+                mfma32<T>(ak, bds[mh], acc[mh][dt]);
         }
       }
     }
@@ -1145,7 +1143,7 @@ __global__ __launch_bounds__(512) void bwd_dq_ds2_kernel(
   // dQ through LDS, every wavefront's 64 rows in its own slice of the ring
   const int hq = g * n_rep + hg * HB + hw;
   __syncthreads();
-  bf16* slice = (bf16*)smem + w * 64 * D;
+  T* slice = (T*)smem + w * 64 * D;
 #pragma unroll
   for (int mh = 0; mh < 2; ++mh) {
     const int r = 32 * mh + c32;
@@ -1160,14 +1158,14 @@ __global__ __launch_bounds__(512) void bwd_dq_ds2_kernel(
         float lo[4], hi[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          rope_pair_bwd<bf16>(acc[mh][dt][4 * gi + e] * scale,
+          rope_pair_bwd<T>(acc[mh][dt][4 * gi + e] * scale,
                               acc[mh][dt + DT / 2][4 * gi + e] * scale, cr[d + e], sr[d + e],
                               lo[e], hi[e]);
         const int cl = 4 * dt + gi, chh = KR / 2 + 4 * dt + gi;
         *(u32x2*)(slice + (r * KR + (cl ^ (r & (KR - 1)))) * 8 + 4 * hh) =
-            u32x2{pack2(lo[0], lo[1]), pack2(lo[2], lo[3])};
+            u32x2{pack2<T>(lo[0], lo[1]), pack2<T>(lo[2], lo[3])};
         *(u32x2*)(slice + (r * KR + (chh ^ (r & (KR - 1)))) * 8 + 4 * hh) =
-            u32x2{pack2(hi[0], hi[1]), pack2(hi[2], hi[3])};
+            u32x2{pack2<T>(hi[0], hi[1]), pack2<T>(hi[2], hi[3])};
       }
   }
   __syncthreads();
@@ -1257,7 +1255,7 @@ int launch_doc_order(const int32_t* doc, const int2* ranges, int S, int rstride,
 namespace {
 
 struct Ws {
-  bf16 *krot, *qrot;
+  uint16_t *krot, *qrot;  // 16-bit elements of the call's dtype
   float *lse2, *delta;  // -lse / scale and -Delta (q_prep_bwd)
   int2* ranges;  // [B][P/64] document-id range per tile (packed documents only)
   int *counts, *order;  // [B][P/128] each: dK/dV item work and order (packed documents)
@@ -1292,7 +1290,7 @@ Ws carve(void* base, int B, int S, int Hq, int Hkv, int D, const void* rot) {
   const size_t P = (size_t)pad_len(S);
   const size_t kv = (size_t)B * Hkv * P * D, qq = (size_t)B * Hq * P * D;
   Ws w;
-  bf16* p = rot ? (bf16*)rot : (bf16*)base;
+  uint16_t* p = rot ? (uint16_t*)rot : (uint16_t*)base;
   w.krot = p; p += kv;
   w.qrot = p; p += qq;
   float* f = rot ? (float*)base : (float*)p;
@@ -1305,7 +1303,7 @@ Ws carve(void* base, int B, int S, int Hq, int Hkv, int D, const void* rot) {
   return w;
 }
 
-template <int D, int HB>
+template <typename T, int D, int HB>
 int launch_dq_ds(const BwdArgs& a, const Ws& w) {
   const int P = pad_len(a.S), n_rep = a.Hq / a.Hkv, nqt = (a.S + DSQ - 1) / DSQ;
   // ring depth by sequence length (measured with 4 heads per workgroup: 4
@@ -1317,27 +1315,27 @@ int launch_dq_ds(const BwdArgs& a, const Ws& w) {
   if constexpr (D == 128 && HB == 4)
   if (!a.doc && !a.kvalid && a.causal && !deep) {
     const int npair = (nqt + 1) / 2;
-    KF_LAUNCH("bwd_dq_ds", (bwd_dq_ds2_kernel<D, 3>), dim3(a.B * a.Hkv * (n_rep / HB) * npair),
-              dim3(512), 0, a.stream, w.dsb, w.krot, a.cos, a.sin, (bf16*)a.dq, a.S, P, a.Hq,
-              a.Hkv, n_rep, nqt, a.scale);
+    KF_LAUNCH("bwd_dq_ds", (bwd_dq_ds2_kernel<T, D, 3>), dim3(a.B * a.Hkv * (n_rep / HB) * npair),
+              dim3(512), 0, a.stream, w.dsb, (const T*)w.krot, a.cos, a.sin, (T*)a.dq, a.S, P,
+              a.Hq, a.Hkv, n_rep, nqt, a.scale);
     KF_CHECK_LAUNCH();
     return KF_OK;
   }
   KF_LAUNCH("bwd_dq_ds",
-            (a.doc      ? (deep ? bwd_dq_ds_kernel<D, HB, MASK_DOC, 4>
-                                : bwd_dq_ds_kernel<D, HB, MASK_DOC, 3>)
-             : a.kvalid ? (deep ? bwd_dq_ds_kernel<D, HB, MASK_KPM, 4>
-                                : bwd_dq_ds_kernel<D, HB, MASK_KPM, 3>)
-                        : (deep ? bwd_dq_ds_kernel<D, HB, MASK_NONE, 4>
-                                : bwd_dq_ds_kernel<D, HB, MASK_NONE, 3>)),
-            dim3(a.B * a.Hkv * (n_rep / HB) * nqt), dim3(64 * HB), 0, a.stream, w.dsb, w.krot,
-            a.cos, a.sin, (bf16*)a.dq, a.S, P, a.Hq, a.Hkv, n_rep, nqt, a.causal, a.scale,
-            a.doc, w.ranges);
+            (a.doc      ? (deep ? bwd_dq_ds_kernel<T, D, HB, MASK_DOC, 4>
+                                : bwd_dq_ds_kernel<T, D, HB, MASK_DOC, 3>)
+             : a.kvalid ? (deep ? bwd_dq_ds_kernel<T, D, HB, MASK_KPM, 4>
+                                : bwd_dq_ds_kernel<T, D, HB, MASK_KPM, 3>)
+                        : (deep ? bwd_dq_ds_kernel<T, D, HB, MASK_NONE, 4>
+                                : bwd_dq_ds_kernel<T, D, HB, MASK_NONE, 3>)),
+            dim3(a.B * a.Hkv * (n_rep / HB) * nqt), dim3(64 * HB), 0, a.stream, w.dsb,
+            (const T*)w.krot, a.cos, a.sin, (T*)a.dq, a.S, P, a.Hq, a.Hkv, n_rep, nqt, a.causal,
+            a.scale, a.doc, w.ranges);
   KF_CHECK_LAUNCH();
   return KF_OK;
 }
 
-template <int D>
+template <typename T, int D>
 int launch_bwd(const BwdArgs& a, void* workspace, bool keep_ds) {
   const int P = pad_len(a.S);
   const Ws w = carve(workspace, a.B, a.S, a.Hq, a.Hkv, D, a.rot);
@@ -1349,7 +1347,7 @@ int launch_bwd(const BwdArgs& a, void* workspace, bool keep_ds) {
   fa.ksb = fa.vsb = (int64_t)a.S * a.Hkv * D;
   fa.kss = fa.vss = (int64_t)a.Hkv * D;
   fa.ksh = fa.vsh = D;
-  fa.k_rotated = 0; fa.dtype = BF16; fa.stream = a.stream;
+  fa.k_rotated = 0; fa.dtype = dtype_code<T>(); fa.stream = a.stream;
   fa.doc = a.doc; fa.kvalid = a.kvalid; fa.causal = a.causal;
   // with a.rot the rotated K and Q are the forward's: only the tile records of
   // an explicit mask are left to prepare
@@ -1357,9 +1355,9 @@ int launch_bwd(const BwdArgs& a, void* workspace, bool keep_ds) {
     const int rc = launch_kv_prep(fa, a.rot ? nullptr : w.krot, P, nullptr, P, w.ranges, KV_V_NONE);
     if (rc) return rc;
   }
-  KF_LAUNCH("q_prep_bwd", q_prep_bwd_kernel<D>, dim3(P / BN, a.B * a.Hq), dim3(256), 0, a.stream,
-            a.rot ? nullptr : (const bf16*)a.q, (const bf16*)a.out, (const bf16*)a.dout, a.lse, a.cos, a.sin,
-            w.qrot, w.lse2, w.delta, a.S, P, a.Hq, 1.f / a.scale);
+  KF_LAUNCH("q_prep_bwd", (q_prep_bwd_kernel<T, D>), dim3(P / BN, a.B * a.Hq), dim3(256), 0,
+            a.stream, a.rot ? nullptr : (const T*)a.q, (const T*)a.out, (const T*)a.dout, a.lse,
+            a.cos, a.sin, (T*)w.qrot, w.lse2, w.delta, a.S, P, a.Hq, 1.f / a.scale);
   KF_CHECK_LAUNCH();
   const int nkb = P / BKV;
   // packed documents: the dK/dV items by their listed query tiles, most first
@@ -1383,30 +1381,30 @@ int launch_bwd(const BwdArgs& a, void* workspace, bool keep_ds) {
     const int rc = launch_kpm_row_flags(w.ranges, P / BN, a.S, a.B, w.counts, a.stream);
     if (rc) return rc;
     KF_LAUNCH("bwd_dkdv",
-              (keep_ds ? bwd_dkdv_kernel<D, MASK_NONE, true, true>
-                       : bwd_dkdv_kernel<D, MASK_NONE, false, true>),
+              (keep_ds ? bwd_dkdv_kernel<T, D, MASK_NONE, true, true>
+                       : bwd_dkdv_kernel<T, D, MASK_NONE, false, true>),
               dim3(std::min(nkb * a.B * a.Hkv, device_cu_count() / 8 * 8)), dim3(512), 0, a.stream,
-              w.krot, (const bf16*)a.v, w.qrot, (const bf16*)a.dout, w.lse2, w.delta, a.cos,
-              a.sin, (bf16*)a.dk, (bf16*)a.dv, a.S, P, a.Hq, a.Hkv, n_rep, nkb,
+              (const T*)w.krot, (const T*)a.v, (const T*)w.qrot, (const T*)a.dout, w.lse2, w.delta,
+              a.cos, a.sin, (T*)a.dk, (T*)a.dv, a.S, P, a.Hq, a.Hkv, n_rep, nkb,
               nkb * a.B * a.Hkv, scale_log2, a.scale, a.causal, nullptr, w.ranges, w.dsb,
               nullptr, kpm_flags);
   }
   KF_LAUNCH("bwd_dkdv",
-            (mode == MASK_DOC   ? (keep_ds ? bwd_dkdv_kernel<D, MASK_DOC, true>
-                                           : bwd_dkdv_kernel<D, MASK_DOC, false>)
-             : mode == MASK_KPM ? (keep_ds ? bwd_dkdv_kernel<D, MASK_KPM, true>
-                                           : bwd_dkdv_kernel<D, MASK_KPM, false>)
-             : keep_ds          ? bwd_dkdv_kernel<D, MASK_NONE, true>
-                                : bwd_dkdv_kernel<D, MASK_NONE, false>),
-            dim3(std::min(nkb * a.B * a.Hkv, grid_cap)), dim3(512), 0, a.stream, w.krot, (const bf16*)a.v,
-            w.qrot, (const bf16*)a.dout, w.lse2, w.delta, a.cos, a.sin, (bf16*)a.dk,
-            (bf16*)a.dv, a.S, P, a.Hq, a.Hkv, n_rep, nkb, nkb * a.B * a.Hkv,
+            (mode == MASK_DOC   ? (keep_ds ? bwd_dkdv_kernel<T, D, MASK_DOC, true>
+                                           : bwd_dkdv_kernel<T, D, MASK_DOC, false>)
+             : mode == MASK_KPM ? (keep_ds ? bwd_dkdv_kernel<T, D, MASK_KPM, true>
+                                           : bwd_dkdv_kernel<T, D, MASK_KPM, false>)
+             : keep_ds          ? bwd_dkdv_kernel<T, D, MASK_NONE, true>
+                                : bwd_dkdv_kernel<T, D, MASK_NONE, false>),
+            dim3(std::min(nkb * a.B * a.Hkv, grid_cap)), dim3(512), 0, a.stream, (const T*)w.krot,
+            (const T*)a.v, (const T*)w.qrot, (const T*)a.dout, w.lse2, w.delta, a.cos, a.sin,
+            (T*)a.dk, (T*)a.dv, a.S, P, a.Hq, a.Hkv, n_rep, nkb, nkb * a.B * a.Hkv,
             scale_log2, a.scale, a.causal, aux, w.ranges, w.dsb, order, kpm_flags);
   KF_CHECK_LAUNCH();
   if (keep_ds) {
-    const int rc = n_rep % 4 == 0   ? launch_dq_ds<D, 4>(a, w)
-                   : n_rep % 2 == 0 ? launch_dq_ds<D, 2>(a, w)
-                                    : launch_dq_ds<D, 1>(a, w);
+    const int rc = n_rep % 4 == 0   ? launch_dq_ds<T, D, 4>(a, w)
+                   : n_rep % 2 == 0 ? launch_dq_ds<T, D, 2>(a, w)
+                                    : launch_dq_ds<T, D, 1>(a, w);
     // key padding: the batch rows with guarded rows still recompute their dQ
     // (the records launch skipped them; this one skips the rest)
     if (rc || mode != MASK_KPM) return rc;
@@ -1414,11 +1412,12 @@ int launch_bwd(const BwdArgs& a, void* workspace, bool keep_ds) {
   const int bm_pos = DQ_ROWS / n_rep;
   const int nqb = (a.S + bm_pos - 1) / bm_pos;
   KF_LAUNCH("bwd_dq",
-            (mode == MASK_DOC   ? bwd_dq_kernel<D, MASK_DOC>
-             : mode == MASK_KPM ? bwd_dq_kernel<D, MASK_KPM>
-                                : bwd_dq_kernel<D, MASK_NONE>),
-            dim3(std::min(nqb * a.B * a.Hkv, grid_cap)), dim3(512), 0, a.stream, w.qrot,
-            (const bf16*)a.dout, w.lse2, w.delta, w.krot, (const bf16*)a.v, a.cos, a.sin, (bf16*)a.dq, a.S, P,
+            (mode == MASK_DOC   ? bwd_dq_kernel<T, D, MASK_DOC>
+             : mode == MASK_KPM ? bwd_dq_kernel<T, D, MASK_KPM>
+                                : bwd_dq_kernel<T, D, MASK_NONE>),
+            dim3(std::min(nqb * a.B * a.Hkv, grid_cap)), dim3(512), 0, a.stream, (const T*)w.qrot,
+            (const T*)a.dout, w.lse2, w.delta, (const T*)w.krot, (const T*)a.v, a.cos, a.sin,
+            (T*)a.dq, a.S, P,
             a.Hq, a.Hkv, n_rep, bm_pos, nqb, nqb * a.B * a.Hkv, scale_log2, a.scale, a.causal,
             aux, w.ranges, (int)keep_ds);
   KF_CHECK_LAUNCH();
@@ -1430,7 +1429,7 @@ int launch_bwd(const BwdArgs& a, void* workspace, bool keep_ds) {
 bool bwd_mfma_supported(const BwdArgs& a) {
   if (a.doc && a.kvalid) return false;  // one explicit mask kind at a time
   if ((a.doc || a.kvalid) && pad_len(a.S) / BN > DOC_MAX_TILES) return false;
-  if (a.dtype != BF16 || (a.D != 64 && a.D != 128)) return false;
+  if ((a.dtype != BF16 && a.dtype != F16) || (a.D != 64 && a.D != 128)) return false;
   const int n_rep = a.Hq / a.Hkv;
   if (n_rep < 1 || n_rep > ROWS) return false;  // also bounds DQ_ROWS / n_rep >= 2
   auto al16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
@@ -1450,8 +1449,11 @@ size_t bwd_mfma_workspace_ds(const BwdArgs& a) {
 int bwd_mfma(const BwdArgs& a, void* workspace, size_t workspace_bytes) {
   KF_CHECK_ARG((int64_t)pad_len(a.S) / BN * (int64_t)a.B * a.Hq < (1LL << 31), "grid too large");
   const bool keep_ds = ds_bytes(a) != 0 && workspace_bytes >= bwd_mfma_workspace_ds(a);
-  return a.D == 128 ? launch_bwd<128>(a, workspace, keep_ds)
-                    : launch_bwd<64>(a, workspace, keep_ds);
+  if (a.dtype == F16)
+    return a.D == 128 ? launch_bwd<f16, 128>(a, workspace, keep_ds)
+                      : launch_bwd<f16, 64>(a, workspace, keep_ds);
+  return a.D == 128 ? launch_bwd<bf16, 128>(a, workspace, keep_ds)
+                    : launch_bwd<bf16, 64>(a, workspace, keep_ds);
 }
 
 }  // namespace kf

@@ -11,6 +11,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace kf {
 
 typedef __bf16 bf16;
@@ -81,57 +83,106 @@ __device__ __forceinline__ float wave_sum(float v) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// Unpack 8 bf16 held in a 16-byte vector into floats.
-__device__ __forceinline__ void unpack8(const u32x4& u, float* f) {
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    f[2 * i] = __uint_as_float(u[i] << 16);
-    f[2 * i + 1] = __uint_as_float(u[i] & 0xffff0000u);
-  }
-}
+// ---- 16-bit element types of the MFMA kernels ------------------------------
+// The MFMA kernels move bf16 and fp16 tensors as raw 16-bit words (u32x4
+// chunks, and bf16x8 vectors as the container of an 8-element MFMA operand
+// whatever its type); the element type T (bf16 or f16) decides only how
+// those words are converted to and from float and which MFMA multiplies them.
+typedef _Float16 f16;
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-// Two floats -> two round-to-nearest-even bf16 in one dword (lo in bits 0-15).
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+// Two floats -> two round-to-nearest-even T in one dword (lo in bits 0-15).
+template <typename T>
 __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+  static_assert(std::is_same<T, bf16>::value || std::is_same<T, f16>::value, "16-bit T");
   const f32x2 f = {lo, hi};
-  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2));
+  if constexpr (std::is_same<T, bf16>::value)
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2));
+  else
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, f16x2));
 }
+// The two T of a dword as floats (exact).
+template <typename T>
+__device__ __forceinline__ void unpack2(uint32_t w, float& lo, float& hi) {
+  if constexpr (std::is_same<T, bf16>::value) {
+    lo = __uint_as_float(w << 16);
+    hi = __uint_as_float(w & 0xffff0000u);
+  } else {
+    const f16x2 h = __builtin_bit_cast(f16x2, w);
+    lo = (float)h[0];
+    hi = (float)h[1];
+  }
+}
+// Unpack 8 T held in a 16-byte vector into floats.
+template <typename T>
+__device__ __forceinline__ void unpack8(const u32x4& u, float* f) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) unpack2<T>(u[i], f[2 * i], f[2 * i + 1]);
+}
+template <typename T>
 __device__ __forceinline__ u32x4 pack8(const float* f) {
   u32x4 u;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) u[i] = pack2(f[2 * i], f[2 * i + 1]);
+  for (int i = 0; i < 4; ++i) u[i] = pack2<T>(f[2 * i], f[2 * i + 1]);
   return u;
 }
 
-// Round two floats to bf16 (round to nearest even) with one conversion, back
-// to fp32: the same bits as two round_to<bf16>.
-__device__ __forceinline__ void round2_bf16(float& x, float& y) {
-  const uint32_t p = pack2(x, y);
-  x = __uint_as_float(p << 16);
-  y = __uint_as_float(p & 0xffff0000u);
+// Round two floats to T (round to nearest even) with one conversion, back to
+// fp32: the same bits as two round_to<T>.
+template <typename T>
+__device__ __forceinline__ void round2(float& x, float& y) {
+  unpack2<T>(pack2<T>(x, y), x, y);
 }
 
-// rope_pair<bf16> on 8 pairs, outputs packed as bf16x8 (r1 -> o1, r2 -> o2).
-// The same bits as rope_pair<bf16> then pack8, with two roundings per
-// conversion instruction and the last rounding done by the pack itself.
-__device__ __forceinline__ void rope8_bf16(const float* x1, const float* x2, const float* cf,
-                                           const float* sf, u32x4& o1, u32x4& o2) {
+// rope_pair<T> on 8 pairs, outputs packed as 8 T (r1 -> o1, r2 -> o2).  The
+// same bits as rope_pair<T> then pack8, with two roundings per conversion
+// instruction and the last rounding done by the pack itself.
+template <typename T>
+__device__ __forceinline__ void rope8(const float* x1, const float* x2, const float* cf,
+                                      const float* sf, u32x4& o1, u32x4& o2) {
 #pragma clang fp contract(off)
   float r1[8], r2[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     float c = cf[j], s = sf[j];
-    round2_bf16(c, s);
+    round2<T>(c, s);
     float a = x1[j] * c, e = x2[j] * c;
-    round2_bf16(a, e);
+    round2<T>(a, e);
     float b = x2[j] * s, f = x1[j] * s;
-    round2_bf16(b, f);
+    round2<T>(b, f);
     r1[j] = a - b;
     r2[j] = e + f;
   }
-  o1 = pack8(r1);
-  o2 = pack8(r2);
+  o1 = pack8<T>(r1);
+  o2 = pack8<T>(r2);
 }
+
+// C += A·B on 32x32x16 (resp. 16x16x32) tiles of T, fp32 accumulation; the
+// operands are 8 T each, carried in bf16x8 containers.
+template <typename T>
+__device__ __forceinline__ f32x16 mfma32(const bf16x8& a, const bf16x8& b, const f32x16& c) {
+  if constexpr (std::is_same<T, bf16>::value)
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+template <typename T>
+__device__ __forceinline__ f32x4 mfma16(const bf16x8& a, const bf16x8& b, const f32x4& c) {
+  if constexpr (std::is_same<T, bf16>::value)
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+
+// DType code of a 16-bit element type (the C ABI's dtype argument).
+template <typename T> constexpr int dtype_code();
+template <> constexpr int dtype_code<bf16>() { return BF16; }
+template <> constexpr int dtype_code<f16>() { return F16; }
 
 }  // namespace kf
 

@@ -15,7 +15,7 @@
 // With QK-norm weights the per-head RMSNorm of q_new and k_new (the
 // reference's q_norm / k_norm, applied before RoPE) happens where the rows
 // are loaded, instead of in separate launches.
-// Shapes outside the fast path (dtype other than bf16, D not in {64, 128}, or
+// Shapes outside the fast path (dtype other than bf16 / fp16, D not in {64, 128}, or
 // n_rep > 16) use decode_generic: one wavefront per (b, hq).
 #include "kf_common.h"
 #include "kf_internal.h"
@@ -218,7 +218,7 @@ __device__ __forceinline__ void cursor_next(Cursor& cur, const DecodeSched& s) {
 
 // Streaming split-K decode on MFMA.  Each wavefront walks its chunk range
 // independently (no workgroup barriers).  Per chunk of KC = 32 keys of pair
-// (b, g), with v_mfma_f32_16x16x32_bf16 (operand layout below):
+// (b, g), with v_mfma_f32_16x16x32_bf16 / _f16 (operand layout below):
 //   S^T = K q^T   two 16-key blocks; the pair's n_rep <= 16 query heads are the
 //                 B-operand columns (zero-padded to 16), so one read of the KV
 //                 head serves every head of the group
@@ -245,11 +245,11 @@ __device__ __forceinline__ void cursor_next(Cursor& cur, const DecodeSched& s) {
 // with k slot j <-> key (j < 4 ? 4 q4 + j : 16 + 4 q4 + j - 4).
 typedef float f32x4v __attribute__((ext_vector_type(4)));
 
-template <int D, bool QKN>
+template <typename T, int D, bool QKN>
 __global__ __launch_bounds__(256, 2) void decode_stream_kernel(
-    const bf16* __restrict__ q_new, const bf16* __restrict__ k_new,
-    const bf16* __restrict__ v_new, const float* __restrict__ cos, const float* __restrict__ sin,
-    int64_t row_offset, int64_t rope_rows, int max_len, bf16* kc, bf16* vc,
+    const T* __restrict__ q_new, const T* __restrict__ k_new,
+    const T* __restrict__ v_new, const float* __restrict__ cos, const float* __restrict__ sin,
+    int64_t row_offset, int64_t rope_rows, int max_len, T* kc, T* vc,
     const int32_t* __restrict__ lens, float* __restrict__ opart, float* __restrict__ mlpart,
     int B, int Hq, int Hkv, int Smax, int n_rep, float scale_log2,
     const float* __restrict__ qnw, const float* __restrict__ knw, float eps) {
@@ -261,9 +261,9 @@ __global__ __launch_bounds__(256, 2) void decode_stream_kernel(
   constexpr int VL = KC * KR / 64;    // 16-byte V loads per lane and chunk
   static_assert(KC == 32, "two 16-key blocks per chunk");
   struct WaveLds {
-    bf16 v[KC * D];   // the chunk's V rows, 16-byte chunks swizzled by row
+    T v[KC * D];   // the chunk's V rows, 16-byte chunks swizzled by row
     float cs[2][64];  // cos, sin row of the pair's new position
-    bf16 nw[D];       // rotated k_new
+    T nw[D];       // rotated k_new
   };
   __shared__ __attribute__((aligned(16))) WaveLds lds_all[DEC_WAVES];
 
@@ -313,7 +313,7 @@ __global__ __launch_bounds__(256, 2) void decode_stream_kernel(
   auto load_stash = [&](const Cursor& cur, Stash& st, bool pair_start, bool new_tok) {
     if (pair_start) {
       const int h = c16 < n_rep ? c16 : 0;
-      const bf16* qr = q_new + ((int64_t)cur.b * Hq + (int64_t)cur.g * n_rep + h) * D;
+      const T* qr = q_new + ((int64_t)cur.b * Hq + (int64_t)cur.g * n_rep + h) * D;
 #pragma unroll
       for (int ks = 0; ks < KT; ++ks) st.q[ks] = *(const u32x4*)(qr + 32 * ks + 8 * q4);
       const int64_t trow = (int64_t)cur.len - row_offset;
@@ -355,7 +355,7 @@ __global__ __launch_bounds__(256, 2) void decode_stream_kernel(
     const int newrow = cc.len;
     const int r0 = cc.lc * KC;
     const int lim = newrow - r0;  // last valid key of the chunk, local
-    const bf16* kvrow_k = nullptr;
+    const T* kvrow_k = nullptr;
     if (seg_start) {
       // the pair's cos / sin row into LDS, then the rotated q operand
       if (lane < HALF) {
@@ -367,7 +367,7 @@ __global__ __launch_bounds__(256, 2) void decode_stream_kernel(
 #pragma unroll
         for (int ks = 0; ks < KT; ++ks) {
           float x[8];
-          unpack8(st.q[ks], x);
+          unpack8<T>(st.q[ks], x);
 #pragma unroll
           for (int j = 0; j < 8; ++j) ss += x[j] * x[j];
         }
@@ -379,19 +379,19 @@ __global__ __launch_bounds__(256, 2) void decode_stream_kernel(
       for (int ks = 0; ks < KT / 2; ++ks) {
         const int d0 = 32 * ks + 8 * q4;  // < HALF; its partner is d0 + HALF (ks + KT / 2)
         float x1[8], x2[8], r1[8], r2[8];
-        unpack8(st.q[ks], x1);
-        unpack8(st.q[ks + KT / 2], x2);
+        unpack8<T>(st.q[ks], x1);
+        unpack8<T>(st.q[ks + KT / 2], x2);
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
           if constexpr (QKN) {
-            x1[j] = rms_scale<bf16>(x1[j], ss, D, eps, qnw[d0 + j]);
-            x2[j] = rms_scale<bf16>(x2[j], ss, D, eps, qnw[d0 + HALF + j]);
+            x1[j] = rms_scale<T>(x1[j], ss, D, eps, qnw[d0 + j]);
+            x2[j] = rms_scale<T>(x2[j], ss, D, eps, qnw[d0 + HALF + j]);
           }
-          rope_pair<bf16>(x1[j], x2[j], L.cs[0][d0 + j], L.cs[1][d0 + j], r1[j], r2[j]);
+          rope_pair<T>(x1[j], x2[j], L.cs[0][d0 + j], L.cs[1][d0 + j], r1[j], r2[j]);
         }
         const u32x4 z = {0u, 0u, 0u, 0u};
-        qf[ks] = c16 < n_rep ? pack8(r1) : z;
-        qf[ks + KT / 2] = c16 < n_rep ? pack8(r2) : z;
+        qf[ks] = c16 < n_rep ? pack8<T>(r1) : z;
+        qf[ks + KT / 2] = c16 < n_rep ? pack8<T>(r2) : z;
       }
       m = -INFINITY;
       lsum = 0.f;
@@ -407,8 +407,9 @@ __global__ __launch_bounds__(256, 2) void decode_stream_kernel(
       const bool first = (e & (HALF / 2)) == 0;  // dims < HALF
       const uint32_t own = st.kv[0];
       const uint32_t par = (uint32_t)__shfl_xor((int)own, HALF / 2, 64);
-      float x[2] = {__uint_as_float(own << 16), __uint_as_float(own & 0xffff0000u)};
-      float y[2] = {__uint_as_float(par << 16), __uint_as_float(par & 0xffff0000u)};
+      float x[2], y[2];
+      unpack2<T>(own, x[0], x[1]);
+      unpack2<T>(par, y[0], y[1]);
       const int dd = (2 * e) % HALF;  // table index of the pair
       if constexpr (QKN) {
         float ss = act ? x[0] * x[0] + x[1] * x[1] : 0.f;
@@ -417,8 +418,8 @@ __global__ __launch_bounds__(256, 2) void decode_stream_kernel(
         for (int t = 0; t < 2; ++t) {
           const int d = act ? 2 * e + t : 0;
           const int dp = d ^ HALF;  // the partner dim
-          x[t] = rms_scale<bf16>(x[t], ss, D, eps, knw[d]);
-          y[t] = rms_scale<bf16>(y[t], ss, D, eps, knw[dp]);
+          x[t] = rms_scale<T>(x[t], ss, D, eps, knw[d]);
+          y[t] = rms_scale<T>(y[t], ss, D, eps, knw[dp]);
         }
       }
       float r[2];
@@ -427,12 +428,12 @@ __global__ __launch_bounds__(256, 2) void decode_stream_kernel(
         float r1, r2;
         const float c = L.cs[0][dd + t], sn = L.cs[1][dd + t];
         if (first)
-          rope_pair<bf16>(x[t], y[t], c, sn, r1, r2);
+          rope_pair<T>(x[t], y[t], c, sn, r1, r2);
         else
-          rope_pair<bf16>(y[t], x[t], c, sn, r1, r2);
+          rope_pair<T>(y[t], x[t], c, sn, r1, r2);
         r[t] = first ? r1 : r2;
       }
-      const uint32_t rk = pack2(r[0], r[1]);
+      const uint32_t rk = pack2<T>(r[0], r[1]);
       const int64_t crow = (((int64_t)cc.b * Hkv + cc.g) * Smax + newrow) * D;
       if (act) {
         ((uint32_t*)L.nw)[e] = rk;
@@ -471,8 +472,7 @@ __global__ __launch_bounds__(256, 2) void decode_stream_kernel(
       sc[kb] = f32x4v{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < KT; ++ks)
-        sc[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kreg[kb][ks]),
-                                                         as_bf16x8(qf[ks]), sc[kb], 0, 0, 0);
+        sc[kb] = mfma16<T>(as_bf16x8(kreg[kb][ks]), as_bf16x8(qf[ks]), sc[kb]);
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
         const int local = 16 * kb + 4 * q4 + t;
@@ -496,7 +496,7 @@ __global__ __launch_bounds__(256, 2) void decode_stream_kernel(
     for (int t = 0; t < 8; ++t) psum += p[t];
     lsum = lsum * alpha + psum;
     m = mnew;
-    const u32x4 pb = {pack2(p[0], p[1]), pack2(p[2], p[3]), pack2(p[4], p[5]), pack2(p[6], p[7])};
+    const u32x4 pb = {pack2<T>(p[0], p[1]), pack2<T>(p[2], p[3]), pack2<T>(p[4], p[5]), pack2<T>(p[6], p[7])};
     // V rows into the tile (rows past the last key as zeros, the new row from v_new)
 #pragma unroll
     for (int j = 0; j < VL; ++j) {
@@ -521,8 +521,7 @@ __global__ __launch_bounds__(256, 2) void decode_stream_kernel(
           __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)(base + 16 * KR * 16));
       typedef short s16x8 __attribute__((ext_vector_type(8)));
       const s16x8 vt = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-      acc[blk] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, vt),
-                                                         as_bf16x8(pb), acc[blk], 0, 0, 0);
+      acc[blk] = mfma16<T>(__builtin_bit_cast(bf16x8, vt), as_bf16x8(pb), acc[blk]);
     }
     if (!more || has_new) {
       // the pair's part of this wavefront ends: partial (o, m, l) to slot gw + p
@@ -547,10 +546,10 @@ __global__ __launch_bounds__(256, 2) void decode_stream_kernel(
 // values, so a merge costs two dependent memory round trips.
 constexpr int MERGE_PRE = 16;
 
-template <int D>
+template <typename T, int D>
 __global__ __launch_bounds__(256) void decode_merge_kernel(
     const float* __restrict__ opart, const float* __restrict__ mlpart,
-    const int32_t* __restrict__ lens, bf16* __restrict__ out, int B, int Hq, int Hkv, int NW,
+    const int32_t* __restrict__ lens, T* __restrict__ out, int B, int Hq, int Hkv, int NW,
     int max_len, int64_t row_offset, int64_t rope_rows) {
   constexpr int PER = D / 64;
   const int lane = threadIdx.x & 63;
@@ -568,10 +567,10 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(
     if (b >= b0 && b < b0 + 64) n = __shfl(nb, b - b0, 64);
   }
   const int C = tot * Hkv;
-  bf16* orow = out + (int64_t)bh * D + lane;
+  T* orow = out + (int64_t)bh * D + lane;
   if (n == 0) {  // unusable length: NaN output, no cache write happened
 #pragma unroll
-    for (int k = 0; k < PER; ++k) orow[64 * k] = (bf16)NAN;
+    for (int k = 0; k < PER; ++k) orow[64 * k] = from_f32<T>(NAN);
     return;
   }
   const int c0 = pre * Hkv + g * n;
@@ -621,7 +620,7 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(
   }
   const float inv = 1.f / lt;
 #pragma unroll
-  for (int k = 0; k < PER; ++k) orow[64 * k] = (bf16)(o[k] * inv);
+  for (int k = 0; k < PER; ++k) orow[64 * k] = from_f32<T>(o[k] * inv);
 }
 
 // One wavefront per (b, hq); keys 0..lens[b] read from the (already appended)
@@ -711,13 +710,14 @@ int launch_append(const T* k_new, const T* v_new, const float* cos, const float*
 // Grid of the stream kernel: two workgroups per CU, at most DEC_GRID_MAX.
 int decode_grid() { return std::max(1, std::min(DEC_GRID_MAX, 2 * device_cu_count())); }
 
-template <int D>
+template <typename T, int D>
 int launch_stream(const DecodeArgs& a, float* opart, float* mlpart, int grid) {
   const bool qkn = a.q_norm_w != nullptr;
-  KF_LAUNCH("decode_stream", (qkn ? decode_stream_kernel<D, true> : decode_stream_kernel<D, false>),
-            dim3(grid), dim3(64 * DEC_WAVES), 0, a.stream, (const bf16*)a.q_new,
-            (const bf16*)a.k_new, (const bf16*)a.v_new, a.cos, a.sin, a.rope_row_offset,
-            a.rope_rows, a.max_len, (bf16*)a.k_cache, (bf16*)a.v_cache, a.lens, opart, mlpart,
+  KF_LAUNCH("decode_stream",
+            (qkn ? decode_stream_kernel<T, D, true> : decode_stream_kernel<T, D, false>),
+            dim3(grid), dim3(64 * DEC_WAVES), 0, a.stream, (const T*)a.q_new,
+            (const T*)a.k_new, (const T*)a.v_new, a.cos, a.sin, a.rope_row_offset,
+            a.rope_rows, a.max_len, (T*)a.k_cache, (T*)a.v_cache, a.lens, opart, mlpart,
             a.B, a.Hq, a.Hkv, a.Smax, a.Hq / a.Hkv, a.scale * kLog2e, a.q_norm_w, a.k_norm_w,
             a.norm_eps);
   KF_CHECK_LAUNCH();
@@ -732,7 +732,8 @@ template <typename T>
 int decode_typed(const DecodeArgs& a, void* workspace) {
   int rc = KF_OK;
   const int n_rep = a.Hq / a.Hkv;
-  const bool fast = __is_same(T, bf16) && (a.D == 64 || a.D == 128) && n_rep <= 16 &&
+  const bool fast = (__is_same(T, bf16) || __is_same(T, f16)) && (a.D == 64 || a.D == 128) &&
+                    n_rep <= 16 &&
                     (int64_t)a.B * a.Hkv * ((a.max_len + KC - 1) / KC) < INT_MAX &&
                     ((uintptr_t)a.q_new | (uintptr_t)a.k_new | (uintptr_t)a.v_new |
                      (uintptr_t)a.k_cache | (uintptr_t)a.v_cache) % 16 == 0;
@@ -741,15 +742,18 @@ int decode_typed(const DecodeArgs& a, void* workspace) {
     float* opart = (float*)workspace;
     float* mlpart = opart + slots * n_rep * a.D;
     const int grid = decode_grid();
-    rc = a.D == 128 ? launch_stream<128>(a, opart, mlpart, grid)
-                    : launch_stream<64>(a, opart, mlpart, grid);
-    if (rc) return rc;
-    KF_LAUNCH("decode_merge", (a.D == 128 ? decode_merge_kernel<128> : decode_merge_kernel<64>),
-              dim3((a.B * a.Hq + 3) / 4), dim3(256), 0, a.stream, opart, mlpart, a.lens,
-              (bf16*)a.out, a.B, a.Hq, a.Hkv, grid * DEC_WAVES, a.max_len, a.rope_row_offset,
-              a.rope_rows);
-    KF_CHECK_LAUNCH();
-    return KF_OK;
+    if constexpr (__is_same(T, bf16) || __is_same(T, f16)) {
+      rc = a.D == 128 ? launch_stream<T, 128>(a, opart, mlpart, grid)
+                      : launch_stream<T, 64>(a, opart, mlpart, grid);
+      if (rc) return rc;
+      KF_LAUNCH("decode_merge",
+                (a.D == 128 ? decode_merge_kernel<T, 128> : decode_merge_kernel<T, 64>),
+                dim3((a.B * a.Hq + 3) / 4), dim3(256), 0, a.stream, opart, mlpart, a.lens,
+                (T*)a.out, a.B, a.Hq, a.Hkv, grid * DEC_WAVES, a.max_len, a.rope_row_offset,
+                a.rope_rows);
+      KF_CHECK_LAUNCH();
+      return KF_OK;
+    }
   }
   rc = launch_append<T>((const T*)a.k_new, (const T*)a.v_new, a.cos, a.sin, (T*)a.k_cache,
                         (T*)a.v_cache, a.lens, 0, a.rope_row_offset, a.rope_rows, a.max_len, a.B,

@@ -1,9 +1,10 @@
-// bf16 MFMA forward attention for gfx950 (head_dim 64 or 128).
+// bf16 / fp16 MFMA forward attention for gfx950 (head_dim 64 or 128).
 //
 // Two kernels:
 //  kv_prep   stages one KV head's keys and values in the layout the MFMA loop
-//            reads: K rotated by RoPE (eager bf16 rounding) [bh][Skp][D], and V
-//            either as V^T [bh][D][Skp] in P^T fragment key order (forward) or
+//            reads: K rotated by RoPE (eager rounding in the input dtype)
+//            [bh][Skp][D], and V either as V^T [bh][D][Skp] in P^T fragment
+//            key order (forward) or
 //            row-major [bh][Skp][D] (backward); keys >= Sk zeroed.
 //            With document ids it also records each 64-key tile's id range,
 //            with a key-validity mask its valid-key count and first valid key.
@@ -11,7 +12,7 @@
 //            a row is (query head of the KV group, position): every K/V tile in
 //            LDS is shared by all n_rep query heads of the group.  Each wave
 //            owns 32 rows and computes S^T = K·Q^T with
-//            v_mfma_f32_32x32x16_bf16, so a lane holds one query's 32 scores of
+//            v_mfma_f32_32x32x16_bf16 (_f16), so a lane holds one query's 32 scores of
 //            a 64-key tile: the online-softmax max/sum is lane-local plus one
 //            exchange with lane^32.  O^T = V^T·P^T accumulates in 16 fp32
 //            registers per 32-d tile; its V^T operand is one ds_read_b128 of
@@ -41,15 +42,15 @@ constexpr float RESCALE_SLACK = 8.f;
 // the compiler's order; 5 and 8 measured no better)
 constexpr int FWD_PF = 3;
 
-template <int D>
+template <typename T, int D>
 __global__ __launch_bounds__(256) void kv_prep_kernel(
-    const bf16* __restrict__ k, const bf16* __restrict__ v, const float* __restrict__ cos,
-    const float* __restrict__ sin, bf16* __restrict__ krot, int krows, bf16* __restrict__ vn,
+    const T* __restrict__ k, const T* __restrict__ v, const float* __restrict__ cos,
+    const float* __restrict__ sin, T* __restrict__ krot, int krows, T* __restrict__ vn,
     int Sk, int Skp, int Hkv, int64_t ksb, int64_t kss, int64_t ksh, int64_t vsb, int64_t vss,
     int64_t vsh, int k_rotated, const int32_t* __restrict__ doc, const int32_t* __restrict__ kvalid,
-    int2* __restrict__ ranges, int v_mode, bf16* __restrict__ qpad, int Hq) {
+    int2* __restrict__ ranges, int v_mode, T* __restrict__ qpad, int Hq) {
   constexpr int HALF = D / 2;
-  __shared__ __attribute__((aligned(16))) bf16 sVt[D * BN];  // KV_V_TRANSPOSED: [d][key slot]
+  __shared__ __attribute__((aligned(16))) T sVt[D * BN];  // KV_V_TRANSPOSED: [d][key slot]
   constexpr int CP = HALF / 8;
   const int s0 = blockIdx.x * BN;
   const int bh = blockIdx.y;
@@ -80,7 +81,7 @@ __global__ __launch_bounds__(256) void kv_prep_kernel(
     const int s = s0 + key;
     u32x4 o1 = {0u, 0u, 0u, 0u}, o2 = {0u, 0u, 0u, 0u};
     if (s < Sk) {
-      const bf16* src = k + b * ksb + (int64_t)s * kss + g * ksh;
+      const T* src = k + b * ksb + (int64_t)s * kss + g * ksh;
       const u32x4 a = *(const u32x4*)(src + 8 * c);
       const u32x4 bb = *(const u32x4*)(src + 8 * c + HALF);
       if (k_rotated) {
@@ -88,13 +89,13 @@ __global__ __launch_bounds__(256) void kv_prep_kernel(
         o2 = bb;
       } else {
         float x1[8], x2[8];
-        unpack8(a, x1);
-        unpack8(bb, x2);
-        rope8_bf16(x1, x2, cos + (int64_t)s * HALF + 8 * c, sin + (int64_t)s * HALF + 8 * c, o1,
+        unpack8<T>(a, x1);
+        unpack8<T>(bb, x2);
+        rope8<T>(x1, x2, cos + (int64_t)s * HALF + 8 * c, sin + (int64_t)s * HALF + 8 * c, o1,
                    o2);
       }
     }
-    bf16* dst = krot + ((int64_t)bh * krows + s) * D;
+    T* dst = krot + ((int64_t)bh * krows + s) * D;
     *(u32x4*)(dst + 8 * c) = o1;
     *(u32x4*)(dst + 8 * c + HALF) = o2;
   }
@@ -140,7 +141,7 @@ __global__ __launch_bounds__(256) void kv_prep_kernel(
     const int c = 4 * (rest % CH) + (it & 3);
     const int kp = 16 * (rest / CH) + ((it >> 2) & 15);
     const int s = s0 + 2 * kp;
-    const bf16* src = v + b * vsb + (int64_t)s * vss + g * vsh + 8 * c;
+    const T* src = v + b * vsb + (int64_t)s * vss + g * vsh + 8 * c;
     u32x4 a = {0u, 0u, 0u, 0u}, a2 = {0u, 0u, 0u, 0u};
     if (s < Sk) a = *(const u32x4*)src;
     if (s + 1 < Sk) a2 = *(const u32x4*)(src + vss);
@@ -167,8 +168,8 @@ __global__ __launch_bounds__(256) void kv_prep_kernel(
 }
 
 // Load this lane's rotated Q fragment: slots ks cover d = 16ks + 8h + 0..7.
-template <int D>
-__device__ __forceinline__ void load_q_frag(const bf16* __restrict__ q,
+template <typename T, int D>
+__device__ __forceinline__ void load_q_frag(const T* __restrict__ q,
                                             const float* __restrict__ cos,
                                             const float* __restrict__ sin, const RowInfo& ri,
                                             int Sq, int Hq, int hh, bf16x8* qf) {
@@ -178,17 +179,17 @@ __device__ __forceinline__ void load_q_frag(const bf16* __restrict__ q,
     for (int ks = 0; ks < KS; ++ks) qf[ks] = as_bf16x8(u32x4{0u, 0u, 0u, 0u});
     return;
   }
-  const bf16* qrow = q + (((int64_t)ri.b * Sq + ri.pos) * Hq + ri.hq) * D;
+  const T* qrow = q + (((int64_t)ri.b * Sq + ri.pos) * Hq + ri.hq) * D;
   const float* cr = cos + (int64_t)ri.pos * HALF;
   const float* sr = sin + (int64_t)ri.pos * HALF;
 #pragma unroll
   for (int ks = 0; ks < KS / 2; ++ks) {
     const int d0 = 16 * ks + 8 * hh;
     float x1[8], x2[8];
-    unpack8(*(const u32x4*)(qrow + d0), x1);
-    unpack8(*(const u32x4*)(qrow + d0 + HALF), x2);
+    unpack8<T>(*(const u32x4*)(qrow + d0), x1);
+    unpack8<T>(*(const u32x4*)(qrow + d0 + HALF), x2);
     u32x4 o1, o2;
-    rope8_bf16(x1, x2, cr + d0, sr + d0, o1, o2);
+    rope8<T>(x1, x2, cr + d0, sr + d0, o1, o2);
     qf[ks] = as_bf16x8(o1);
     qf[ks + KS / 2] = as_bf16x8(o2);
   }
@@ -206,19 +207,19 @@ __device__ __forceinline__ void load_q_frag(const bf16* __restrict__ q,
 // The running max starts at -1e30 instead of -inf in both, because a row can
 // see no key at all in a listed tile (exp2 of -inf - -inf would be NaN); every
 // row sees some key in some tile, so the final max is a real score.
-template <int D, int MODE>
+template <typename T, int D, int MODE>
 __global__ __launch_bounds__(256, 2) void fwd_mfma_kernel(
-    const bf16* __restrict__ q, const float* __restrict__ cos, const float* __restrict__ sin,
-    const bf16* __restrict__ krot, const bf16* __restrict__ vn, bf16* __restrict__ out,
+    const T* __restrict__ q, const float* __restrict__ cos, const float* __restrict__ sin,
+    const T* __restrict__ krot, const T* __restrict__ vn, T* __restrict__ out,
     float* __restrict__ lse, int Sq, int Sk, int Skp, int krows, int Hq, int Hkv, int n_rep,
     int bm_pos, int nqb, float scale_log2, int causal, const int32_t* __restrict__ aux,
-    const int2* __restrict__ ranges, bf16* __restrict__ qrot, const int* __restrict__ order,
+    const int2* __restrict__ ranges, T* __restrict__ qrot, const int* __restrict__ order,
     const int* __restrict__ kpm_flags) {
   constexpr bool DOC = MODE == MASK_DOC, KPM = MODE == MASK_KPM, LIST = DOC || KPM;
   constexpr int KS = D / 16, DT = D / 32;
   constexpr int KR = D / 8;  // 16-byte chunks per K / V row
-  __shared__ __attribute__((aligned(16))) bf16 sK[2][BN * D];
-  __shared__ __attribute__((aligned(16))) bf16 sV[2][BN * D];
+  __shared__ __attribute__((aligned(16))) T sK[2][BN * D];
+  __shared__ __attribute__((aligned(16))) T sV[2][BN * D];
   __shared__ __attribute__((aligned(16))) int32_t sKD[2][BN];  // LIST: per-key aux values
   __shared__ uint16_t sList[DOC_MAX_TILES];                     // LIST: listed key tiles
   __shared__ int sCount, sFirst;
@@ -241,8 +242,8 @@ __global__ __launch_bounds__(256, 2) void fwd_mfma_kernel(
   const int2* rec = ranges + (int64_t)ri.b * (Skp / BN);
   // kpm_flags (per batch row, 1 = every key valid): those rows are fwd32_kernel's
   if (KPM && kpm_flags != nullptr && kpm_flags[ri.b] != 0) return;
-  const bf16* kbase = krot + (int64_t)bh * krows * D;
-  const bf16* vbase = vn + (int64_t)bh * D * Skp;  // V^T, keys in fragment order
+  const T* kbase = krot + (int64_t)bh * krows * D;
+  const T* vbase = vn + (int64_t)bh * D * Skp;  // V^T, keys in fragment order
   auto stage = [&](int t, int buf) {
     tile_to_lds<BN, KR>(kbase + (int64_t)t * BN * D, D, sK[buf], w, lane);
     tile_to_lds<D, BN / 8>(vbase + (int64_t)t * BN, Skp, sV[buf], w, lane);
@@ -291,7 +292,7 @@ __global__ __launch_bounds__(256, 2) void fwd_mfma_kernel(
   if (KPM && ntiles > 0) stage(tile_of(entry(0)), 0);
 
   bf16x8 qf[KS];
-  load_q_frag<D>(q, cos, sin, ri, Sq, Hq, hh, qf);
+  load_q_frag<T, D>(q, cos, sin, ri, Sq, Hq, hh, qf);
 
   float m = LIST ? -1e30f : -INFINITY, lsum = 0.f;
   f32x16 acc[DT];
@@ -310,8 +311,8 @@ __global__ __launch_bounds__(256, 2) void fwd_mfma_kernel(
     const int e = entry(it);
     const int t = tile_of(e);
     if (it + 1 < ntiles) stage(tile_of(entry(it + 1)), buf ^ 1);
-    const bf16* tK = sK[buf];
-    const bf16* tV = sV[buf];
+    const T* tK = sK[buf];
+    const T* tV = sV[buf];
 
     f32x16 s[2];
 #pragma unroll
@@ -330,7 +331,7 @@ __global__ __launch_bounds__(256, 2) void fwd_mfma_kernel(
       for (int j = 0; j < NQ; ++j) {
         __builtin_amdgcn_sched_barrier(0);
         if (j + FWD_PF < NQ) fa[j + FWD_PF] = kfrag(j + FWD_PF);
-        s[j & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[j], qf[j >> 1], s[j & 1], 0, 0, 0);
+        s[j & 1] = mfma32<T>(fa[j], qf[j >> 1], s[j & 1]);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -374,7 +375,7 @@ __global__ __launch_bounds__(256, 2) void fwd_mfma_kernel(
     // Rescale the running output only when some row's max grew by more than
     // RESCALE_SLACK (log2 units): until then the exponent base m lags the
     // row's max by at most that much, so p <= 2^RESCALE_SLACK, well inside
-    // bf16 and fp32 range with their precision unchanged (O / l and the LSE
+    // bf16, fp16 and fp32 range with their precision unchanged (O / l and the LSE
     // m + log2(l) are exact for any base).  Rows whose max did not move keep
     // alpha = 1.  The branch is wavefront-uniform.
     if (__builtin_amdgcn_ballot_w64(tmax > m + RESCALE_SLACK) != 0) {
@@ -396,7 +397,7 @@ __global__ __launch_bounds__(256, 2) void fwd_mfma_kernel(
         const float p0 = fast_exp2(__builtin_fmaf(s[mt][i], scale_log2, -m));
         const float p1 = fast_exp2(__builtin_fmaf(s[mt][i + 1], scale_log2, -m));
         psum += p0 + p1;
-        pk[2 * mt + (i >> 3)][(i & 7) >> 1] = pack2(p0, p1);
+        pk[2 * mt + (i >> 3)][(i & 7) >> 1] = pack2<T>(p0, p1);
       }
     lsum += psum;
     {
@@ -411,8 +412,7 @@ __global__ __launch_bounds__(256, 2) void fwd_mfma_kernel(
       for (int j = 0; j < NV; ++j) {
         __builtin_amdgcn_sched_barrier(0);
         if (j + FWD_PF < NV) fb[j + FWD_PF] = vfrag(j + FWD_PF);
-        acc[j % DT] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[j], as_bf16x8(pk[j / DT]),
-                                                             acc[j % DT], 0, 0, 0);
+        acc[j % DT] = mfma32<T>(fb[j], as_bf16x8(pk[j / DT]), acc[j % DT]);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -431,15 +431,15 @@ __global__ __launch_bounds__(256, 2) void fwd_mfma_kernel(
   // 16-byte chunks XOR-swizzled by row, then stores whole 16-byte chunks, each
   // row by KR consecutive lanes, so a store instruction covers 64 / KR whole
   // rows instead of 16 bytes of each of 32 rows.
-  bf16* slice = &sK[0][0] + w * 32 * D;  // 32 rows x D (sK holds 2 x 64 rows)
+  T* slice = &sK[0][0] + w * 32 * D;  // 32 rows x D (sK holds 2 x 64 rows)
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
     for (int gi = 0; gi < 4; ++gi) {
       const int ch = 4 * dt + gi;  // 16-byte chunk of columns 32 dt + 8 gi ..
       u32x2 pk2;
-      pk2[0] = pack2(acc[dt][4 * gi] * inv, acc[dt][4 * gi + 1] * inv);
-      pk2[1] = pack2(acc[dt][4 * gi + 2] * inv, acc[dt][4 * gi + 3] * inv);
+      pk2[0] = pack2<T>(acc[dt][4 * gi] * inv, acc[dt][4 * gi + 1] * inv);
+      pk2[1] = pack2<T>(acc[dt][4 * gi + 2] * inv, acc[dt][4 * gi + 3] * inv);
       *(u32x2*)(slice + (c32 * KR + (ch ^ (c32 & (KR - 1)))) * 8 + 4 * hh) = pk2;
     }
   __syncthreads();
@@ -482,17 +482,17 @@ __global__ __launch_bounds__(256, 2) void fwd_mfma_kernel(
 // fwd_mfma_kernel; the running max is taken per 32-key tile, so the points
 // where the output is rescaled (and with them the last bits) can differ.
 constexpr int FBN = 32;  // keys per tile of fwd32_kernel
-template <int D>
+template <typename T, int D>
 __global__ __launch_bounds__(256, 3) void fwd32_kernel(
-    const bf16* __restrict__ q, const float* __restrict__ cos, const float* __restrict__ sin,
-    const bf16* __restrict__ krot, const bf16* __restrict__ vn, bf16* __restrict__ out,
+    const T* __restrict__ q, const float* __restrict__ cos, const float* __restrict__ sin,
+    const T* __restrict__ krot, const T* __restrict__ vn, T* __restrict__ out,
     float* __restrict__ lse, int Sq, int Sk, int Skp, int krows, int Hq, int Hkv, int n_rep,
-    int bm_pos, int nqb, float scale_log2, int causal, bf16* __restrict__ qrot,
+    int bm_pos, int nqb, float scale_log2, int causal, T* __restrict__ qrot,
     const int* __restrict__ kpm_flags) {
   constexpr int KS = D / 16, DT = D / 32;
   constexpr int KR = D / 8;  // 16-byte chunks per K row
-  __shared__ __attribute__((aligned(16))) bf16 sK[2][FBN * D];
-  __shared__ __attribute__((aligned(16))) bf16 sV[2][D * FBN];
+  __shared__ __attribute__((aligned(16))) T sK[2][FBN * D];
+  __shared__ __attribute__((aligned(16))) T sV[2][D * FBN];
 
   const int tid = threadIdx.x, w = wave_id(), lane = tid & 63, hh = lane >> 5, c32 = lane & 31;
   const int logical = xcd_logical_id(blockIdx.x, gridDim.x);
@@ -503,8 +503,8 @@ __global__ __launch_bounds__(256, 3) void fwd32_kernel(
   const int bh = ri.b * Hkv + ri.g;
   const int kend = causal ? min(Sk, min(ri.p0 + bm_pos, Sq)) : Sk;
   const int ntiles = (kend + FBN - 1) / FBN;
-  const bf16* kbase = krot + (int64_t)bh * krows * D;
-  const bf16* vbase = vn + (int64_t)bh * D * Skp;  // V^T, keys in fragment order
+  const T* kbase = krot + (int64_t)bh * krows * D;
+  const T* vbase = vn + (int64_t)bh * D * Skp;  // V^T, keys in fragment order
   auto stage = [&](int t, int buf) {
     tile_to_lds<FBN, KR>(kbase + (int64_t)t * FBN * D, D, sK[buf], w, lane);
     tile_to_lds<D, FBN / 8>(vbase + (int64_t)t * FBN, Skp, sV[buf], w, lane);
@@ -512,7 +512,7 @@ __global__ __launch_bounds__(256, 3) void fwd32_kernel(
   if (ntiles > 0) stage(0, 0);
 
   bf16x8 qf[KS];
-  load_q_frag<D>(q, cos, sin, ri, Sq, Hq, hh, qf);
+  load_q_frag<T, D>(q, cos, sin, ri, Sq, Hq, hh, qf);
 
   float m = -INFINITY, lsum = 0.f;
   f32x16 acc[DT];
@@ -526,8 +526,8 @@ __global__ __launch_bounds__(256, 3) void fwd32_kernel(
   auto tile_body = [&](int it, auto bufc) {
     constexpr int buf = decltype(bufc)::value;
     if (it + 1 < ntiles) stage(it + 1, buf ^ 1);
-    const bf16* tK = sK[buf];
-    const bf16* tV = sV[buf];
+    const T* tK = sK[buf];
+    const T* tV = sV[buf];
 
     // S^T of the tile's 32 keys x this wavefront's 32 rows
     f32x16 s;
@@ -542,7 +542,7 @@ __global__ __launch_bounds__(256, 3) void fwd32_kernel(
       for (int j = 0; j < KS; ++j) {
         __builtin_amdgcn_sched_barrier(0);
         if (j + FWD_PF < KS) fa[j + FWD_PF] = kfrag(j + FWD_PF);
-        s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[j], qf[j], s, 0, 0, 0);
+        s = mfma32<T>(fa[j], qf[j], s);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -578,7 +578,7 @@ __global__ __launch_bounds__(256, 3) void fwd32_kernel(
       const float p0 = fast_exp2(__builtin_fmaf(s[i], scale_log2, -m));
       const float p1 = fast_exp2(__builtin_fmaf(s[i + 1], scale_log2, -m));
       psum += p0 + p1;
-      pk[i >> 3][(i & 7) >> 1] = pack2(p0, p1);
+      pk[i >> 3][(i & 7) >> 1] = pack2<T>(p0, p1);
     }
     lsum += psum;
     {
@@ -593,8 +593,7 @@ __global__ __launch_bounds__(256, 3) void fwd32_kernel(
       for (int j = 0; j < NV; ++j) {
         __builtin_amdgcn_sched_barrier(0);
         if (j + FWD_PF < NV) fb[j + FWD_PF] = vfrag(j + FWD_PF);
-        acc[j % DT] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[j], as_bf16x8(pk[j / DT]),
-                                                             acc[j % DT], 0, 0, 0);
+        acc[j % DT] = mfma32<T>(fb[j], as_bf16x8(pk[j / DT]), acc[j % DT]);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -613,15 +612,15 @@ __global__ __launch_bounds__(256, 3) void fwd32_kernel(
   // 16-byte chunks XOR-swizzled by row, then stores whole 16-byte chunks, each
   // row by KR consecutive lanes, so a store instruction covers 64 / KR whole
   // rows instead of 16 bytes of each of 32 rows.
-  bf16* slice = w < 2 ? sK[w] : sV[w - 2];  // FBN x D bf16 = 32 rows x D
+  T* slice = w < 2 ? sK[w] : sV[w - 2];  // FBN x D elements = 32 rows x D
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
     for (int gi = 0; gi < 4; ++gi) {
       const int ch = 4 * dt + gi;  // 16-byte chunk of columns 32 dt + 8 gi ..
       u32x2 pk2;
-      pk2[0] = pack2(acc[dt][4 * gi] * inv, acc[dt][4 * gi + 1] * inv);
-      pk2[1] = pack2(acc[dt][4 * gi + 2] * inv, acc[dt][4 * gi + 3] * inv);
+      pk2[0] = pack2<T>(acc[dt][4 * gi] * inv, acc[dt][4 * gi + 1] * inv);
+      pk2[1] = pack2<T>(acc[dt][4 * gi + 2] * inv, acc[dt][4 * gi + 3] * inv);
       *(u32x2*)(slice + (c32 * KR + (ch ^ (c32 & (KR - 1)))) * 8 + 4 * hh) = pk2;
     }
   __syncthreads();
@@ -667,7 +666,7 @@ __global__ __launch_bounds__(256, 3) void fwd32_kernel(
 // row's 32 scores of a 64-key tile): the first walk forms each row's running
 // max and sum only (no P·V), with the four tile buffers as a ring of K tiles
 // staged three ahead; the second forms the normalised P, stores it, and
-// accumulates O^T = V^T·P^T from P rounded to bf16, so O needs no final
+// accumulates O^T = V^T·P^T from P rounded to T, so O needs no final
 // division.  P leaves through an LDS slice per wavefront (see store_p) as
 // whole 128-byte line segments.  The stores of tile t issue in tile t+1,
 // after its tile loads and zero rows: the end-of-tile wait (vmcnt counts loads
@@ -684,18 +683,18 @@ __global__ __launch_bounds__(256, 3) void fwd32_kernel(
 // except in guarded rows before the first valid key, which attend every key
 // below Sk, so a workgroup holding one walks every tile); with an explicit
 // mask every tile takes the element test.
-template <int D, int MODE>
+template <typename T, int D, int MODE>
 __global__ __launch_bounds__(256, 2) void capture_probs_mfma_kernel(
-    const bf16* __restrict__ q, const float* __restrict__ cos, const float* __restrict__ sin,
-    const bf16* __restrict__ krot, const bf16* __restrict__ vn, bf16* __restrict__ out,
+    const T* __restrict__ q, const float* __restrict__ cos, const float* __restrict__ sin,
+    const T* __restrict__ krot, const T* __restrict__ vn, T* __restrict__ out,
     float* __restrict__ lse, float* __restrict__ probs, int Sq, int Sk, int Skp, int Hq, int Hkv,
     int n_rep, int bm_pos, int nqb, float scale_log2, int causal,
     const int32_t* __restrict__ aux, const int2* __restrict__ ranges) {
   constexpr bool DOC = MODE == MASK_DOC, KPM = MODE == MASK_KPM, LIST = DOC || KPM;
   constexpr int KS = D / 16, DT = D / 32;
   constexpr int KR = D / 8;
-  __shared__ __attribute__((aligned(16))) bf16 sK[2][BN * D];
-  __shared__ __attribute__((aligned(16))) bf16 sV[2][BN * D];
+  __shared__ __attribute__((aligned(16))) T sK[2][BN * D];
+  __shared__ __attribute__((aligned(16))) T sV[2][BN * D];
   __shared__ __attribute__((aligned(16))) int32_t sKD[4][BN];  // LIST: per-key aux values
   __shared__ __attribute__((aligned(16))) float sP[4][32 * 32];  // per wave: 32 rows x 32 keys
 
@@ -731,8 +730,8 @@ __global__ __launch_bounds__(256, 2) void capture_probs_mfma_kernel(
                                                         : ntiles_all;
     const int di = DOC ? arow[min(ri.pos, Sq - 1)] : 0;  // DOC: this row's document
     const bool grd = KPM && ri.pos < fv;                  // KPM: guarded row
-    const bf16* kbase = krot + (int64_t)bh * Skp * D;
-    const bf16* vbase = vn + (int64_t)bh * D * Skp;  // V^T, keys in fragment order
+    const T* kbase = krot + (int64_t)bh * Skp * D;
+    const T* vbase = vn + (int64_t)bh * D * Skp;  // V^T, keys in fragment order
     auto stage_k = [&](int t, int buf) {
       tile_to_lds<BN, KR>(kbase + (int64_t)t * BN * D, D, sK[buf], w, lane);
       if (LIST && w == 0) dma4(lds_addr(sKD[buf]), (uint32_t)min(t * BN + lane, Sk - 1) * 4u, arow);
@@ -742,7 +741,7 @@ __global__ __launch_bounds__(256, 2) void capture_probs_mfma_kernel(
     };
     // Walk 1 reads only K tiles: all four tile buffers form its ring, staged
     // three tiles ahead (slot s: sK[0], sK[1], sV[0], sV[1]; aux values in sKD[s])
-    bf16* const ring[4] = {sK[0], sK[1], sV[0], sV[1]};
+    T* const ring[4] = {sK[0], sK[1], sV[0], sV[1]};
     auto stage_kr = [&](int t, int slot) {
       tile_to_lds<BN, KR>(kbase + (int64_t)t * BN * D, D, ring[slot], w, lane);
       if (LIST && w == 0)
@@ -753,10 +752,10 @@ __global__ __launch_bounds__(256, 2) void capture_probs_mfma_kernel(
       if (t < ntiles) stage_kr(t, t);
 
     bf16x8 qf[KS];
-    load_q_frag<D>(q, cos, sin, ri, Sq, Hq, hh, qf);
+    load_q_frag<T, D>(q, cos, sin, ri, Sq, Hq, hh, qf);
 
     // S^T of tile t with masked scores set to -inf
-    auto scores = [&](int t, const bf16* tK, const int32_t* kdl, f32x16 (&s)[2]) {
+    auto scores = [&](int t, const T* tK, const int32_t* kdl, f32x16 (&s)[2]) {
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
@@ -766,7 +765,7 @@ __global__ __launch_bounds__(256, 2) void capture_probs_mfma_kernel(
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt) {
           const bf16x8 a = lds_frag<KR>(tK, 32 * mt + c32, 2 * ks + hh);
-          s[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[ks], s[mt], 0, 0, 0);
+          s[mt] = mfma32<T>(a, qf[ks], s[mt]);
         }
       }
       const int k0 = t * BN;
@@ -948,7 +947,7 @@ __global__ __launch_bounds__(256, 2) void capture_probs_mfma_kernel(
           const float p1 = fast_exp2(__builtin_fmaf(s[mt][i + 1], scale_log2, -L));
           held[mt][i] = p0;
           held[mt][i + 1] = p1;
-          pk[2 * mt + (i >> 3)][(i & 7) >> 1] = pack2(p0, p1);
+          pk[2 * mt + (i >> 3)][(i & 7) >> 1] = pack2<T>(p0, p1);
         }
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
@@ -956,7 +955,7 @@ __global__ __launch_bounds__(256, 2) void capture_probs_mfma_kernel(
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) {
           const bf16x8 a = lds_frag<BN / 8>(sV[buf], 32 * dt + c32, 2 * c + hh);
-          acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb, acc[dt], 0, 0, 0);
+          acc[dt] = mfma32<T>(a, pb, acc[dt]);
         }
       }
       if (full)
@@ -979,15 +978,15 @@ __global__ __launch_bounds__(256, 2) void capture_probs_mfma_kernel(
     if (ntiles > 0) store_p(ntiles - 1);
 
     if (ri.q_valid) {
-      bf16* orow = out + (((int64_t)ri.b * Sq + ri.pos) * Hq + ri.hq) * D;
+      T* orow = out + (((int64_t)ri.b * Sq + ri.pos) * Hq + ri.hq) * D;
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
         for (int gi = 0; gi < 4; ++gi) {
           const int d = 32 * dt + 8 * gi + 4 * hh;
           u32x2 pk2;
-          pk2[0] = pack2(acc[dt][4 * gi], acc[dt][4 * gi + 1]);
-          pk2[1] = pack2(acc[dt][4 * gi + 2], acc[dt][4 * gi + 3]);
+          pk2[0] = pack2<T>(acc[dt][4 * gi], acc[dt][4 * gi + 1]);
+          pk2[1] = pack2<T>(acc[dt][4 * gi + 2], acc[dt][4 * gi + 3]);
           *(u32x2*)(orow + d) = pk2;
         }
     }
@@ -999,7 +998,7 @@ int pick_bm_pos(int n_rep) { return n_rep <= ROWS ? ROWS / n_rep : 0; }
 }  // namespace
 
 bool fwd_mfma_supported(const FwdArgs& a) {
-  if (a.dtype != BF16 || (a.D != 64 && a.D != 128)) return false;
+  if ((a.dtype != BF16 && a.dtype != F16) || (a.D != 64 && a.D != 128)) return false;
   // one explicit mask kind at a time, with a tile list that fits
   if (a.doc && a.kvalid) return false;
   if ((a.doc || a.kvalid) && (a.Sk + BN - 1) / BN > DOC_MAX_TILES) return false;
@@ -1012,7 +1011,7 @@ bool fwd_mfma_supported(const FwdArgs& a) {
   return true;
 }
 
-// krot ([B*Hkv][Skp][D] bf16) and V^T ([B*Hkv][D][Skp] bf16), then the per-tile
+// krot ([B*Hkv][Skp][D]) and V^T ([B*Hkv][D][Skp]), 16-bit elements, then the per-tile
 // records ([B][Skp/64] int2, written only with an explicit mask), then the
 // query blocks' listed-tile counts and order (packed documents; at most Sk
 // blocks of one position per batch row).
@@ -1022,22 +1021,28 @@ size_t fwd_mfma_workspace(int B, int Sk, int Hkv, int D) {
          2 * (size_t)B * Skp * sizeof(int);
 }
 
-int launch_kv_prep(const FwdArgs& a, void* krot_, int krows, void* vn_, int Skp, int2* ranges,
-                   int v_mode, void* qpad_) {
-  bf16* krot = (bf16*)krot_;
-  bf16* vn = (bf16*)vn_;
-  bf16* qpad = (bf16*)qpad_;
+namespace {
+template <typename T, int D>
+void launch_kv_prep_t(const FwdArgs& a, void* krot, int krows, void* vn, int Skp, int2* ranges,
+                      int v_mode, void* qpad) {
   dim3 grid((krot ? krows : Skp) / BN, a.B * a.Hkv);
-  if (a.D == 128)
-    KF_LAUNCH("kv_prep", kv_prep_kernel<128>, grid, dim3(256), 0, a.stream, (const bf16*)a.k,
-              (const bf16*)a.v, a.cos, a.sin, krot, krows, vn, a.Sk, Skp, a.Hkv, a.ksb, a.kss,
-              a.ksh, a.vsb, a.vss, a.vsh, a.k_rotated, a.doc, a.kvalid, ranges, v_mode, qpad,
-              a.Hq);
-  else
-    KF_LAUNCH("kv_prep", kv_prep_kernel<64>, grid, dim3(256), 0, a.stream, (const bf16*)a.k,
-              (const bf16*)a.v, a.cos, a.sin, krot, krows, vn, a.Sk, Skp, a.Hkv, a.ksb, a.kss,
-              a.ksh, a.vsb, a.vss, a.vsh, a.k_rotated, a.doc, a.kvalid, ranges, v_mode, qpad,
-              a.Hq);
+  KF_LAUNCH("kv_prep", (kv_prep_kernel<T, D>), grid, dim3(256), 0, a.stream, (const T*)a.k,
+            (const T*)a.v, a.cos, a.sin, (T*)krot, krows, (T*)vn, a.Sk, Skp, a.Hkv, a.ksb, a.kss,
+            a.ksh, a.vsb, a.vss, a.vsh, a.k_rotated, a.doc, a.kvalid, ranges, v_mode, (T*)qpad,
+            a.Hq);
+}
+}  // namespace
+
+int launch_kv_prep(const FwdArgs& a, void* krot, int krows, void* vn, int Skp, int2* ranges,
+                   int v_mode, void* qpad) {
+  const bool h = a.dtype == F16;
+  if (a.D == 128) {
+    if (h) launch_kv_prep_t<f16, 128>(a, krot, krows, vn, Skp, ranges, v_mode, qpad);
+    else launch_kv_prep_t<bf16, 128>(a, krot, krows, vn, Skp, ranges, v_mode, qpad);
+  } else {
+    if (h) launch_kv_prep_t<f16, 64>(a, krot, krows, vn, Skp, ranges, v_mode, qpad);
+    else launch_kv_prep_t<bf16, 64>(a, krot, krows, vn, Skp, ranges, v_mode, qpad);
+  }
   KF_CHECK_LAUNCH();
   return KF_OK;
 }
@@ -1069,11 +1074,11 @@ size_t rot_bytes(int B, int S, int Hq, int Hkv, int D) {
 namespace {
 
 struct FwdWs {
-  bf16 *krot, *vn;
+  uint16_t *krot, *vn;  // 16-bit elements of the call's dtype
   int2* ranges;
   int *counts, *order;  // [B][Skp] each (packed documents)
-  int krows;   // rows of krot per KV head
-  bf16* qrot;  // a.rot's rotated Q, or null
+  int krows;       // rows of krot per KV head
+  uint16_t* qrot;  // a.rot's rotated Q, or null
 };
 
 // With a.rot the rotated K goes there (P rows per KV head, as the backward
@@ -1081,7 +1086,7 @@ struct FwdWs {
 // writes the rotated Q after it.
 FwdWs carve_fwd(const FwdArgs& a, void* workspace, int Skp) {
   FwdWs w;
-  w.krot = (bf16*)workspace;
+  w.krot = (uint16_t*)workspace;
   w.vn = w.krot + (size_t)a.B * a.Hkv * Skp * a.D;
   w.ranges = (int2*)(w.vn + (size_t)a.B * a.Hkv * Skp * a.D);
   w.counts = (int*)(w.ranges + (size_t)a.B * (Skp / BN));
@@ -1090,7 +1095,7 @@ FwdWs carve_fwd(const FwdArgs& a, void* workspace, int Skp) {
   w.qrot = nullptr;
   if (a.rot != nullptr) {
     w.krows = (a.Sk + 127) / 128 * 128;
-    w.krot = (bf16*)a.rot;
+    w.krot = (uint16_t*)a.rot;
     w.qrot = w.krot + (size_t)a.B * a.Hkv * w.krows * a.D;
   }
   return w;
@@ -1098,29 +1103,30 @@ FwdWs carve_fwd(const FwdArgs& a, void* workspace, int Skp) {
 
 int mask_mode(const FwdArgs& a) { return a.doc ? MASK_DOC : a.kvalid ? MASK_KPM : MASK_NONE; }
 
-template <int D, int MODE>
+template <typename T, int D, int MODE>
 void launch_fwd_kernel(const FwdArgs& a, const FwdWs& w, int Skp, int n_rep, int bm_pos, int nqb,
                        unsigned nblk, const int* order, const int* kpm_flags = nullptr) {
-  KF_LAUNCH("fwd_mfma", (fwd_mfma_kernel<D, MODE>), dim3(nblk), dim3(256), 0, a.stream,
-            (const bf16*)a.q, a.cos, a.sin, w.krot, w.vn, (bf16*)a.out, a.lse, a.Sq, a.Sk, Skp,
-            w.krows, a.Hq, a.Hkv, n_rep, bm_pos, nqb, a.scale * kLog2e, a.causal,
-            a.doc ? a.doc : a.kvalid, w.ranges, w.qrot, order, kpm_flags);
+  KF_LAUNCH("fwd_mfma", (fwd_mfma_kernel<T, D, MODE>), dim3(nblk), dim3(256), 0, a.stream,
+            (const T*)a.q, a.cos, a.sin, (const T*)w.krot, (const T*)w.vn, (T*)a.out, a.lse, a.Sq,
+            a.Sk, Skp, w.krows, a.Hq, a.Hkv, n_rep, bm_pos, nqb, a.scale * kLog2e, a.causal,
+            a.doc ? a.doc : a.kvalid, w.ranges, (T*)w.qrot, order, kpm_flags);
 }
 
-template <int D>
+template <typename T, int D>
 void launch_fwd32(const FwdArgs& a, const FwdWs& w, int Skp, int n_rep, int bm_pos, int nqb,
                   unsigned nblk, const int* kpm_flags) {
-  KF_LAUNCH("fwd_mfma", fwd32_kernel<D>, dim3(nblk), dim3(256), 0, a.stream, (const bf16*)a.q,
-            a.cos, a.sin, w.krot, w.vn, (bf16*)a.out, a.lse, a.Sq, a.Sk, Skp, w.krows, a.Hq,
-            a.Hkv, n_rep, bm_pos, nqb, a.scale * kLog2e, a.causal, w.qrot, kpm_flags);
+  KF_LAUNCH("fwd_mfma", (fwd32_kernel<T, D>), dim3(nblk), dim3(256), 0, a.stream, (const T*)a.q,
+            a.cos, a.sin, (const T*)w.krot, (const T*)w.vn, (T*)a.out, a.lse, a.Sq, a.Sk, Skp,
+            w.krows, a.Hq, a.Hkv, n_rep, bm_pos, nqb, a.scale * kLog2e, a.causal, (T*)w.qrot,
+            kpm_flags);
 }
 
-template <int D>
+template <typename T, int D>
 void launch_fwd_mode(const FwdArgs& a, const FwdWs& w, int Skp, int n_rep, int bm_pos, int nqb,
                      unsigned nblk) {
   switch (mask_mode(a)) {
     case MASK_DOC:
-      launch_fwd_kernel<D, MASK_DOC>(a, w, Skp, n_rep, bm_pos, nqb, nblk, w.order);
+      launch_fwd_kernel<T, D, MASK_DOC>(a, w, Skp, n_rep, bm_pos, nqb, nblk, w.order);
       break;
     case MASK_KPM:
       // causal self-attention: batch rows without padding run the unmasked
@@ -1128,34 +1134,34 @@ void launch_fwd_mode(const FwdArgs& a, const FwdWs& w, int Skp, int n_rep, int b
     {
       // (w.counts holds the per-row flags: launch_kpm_row_flags in fwd_mfma)
       const int* flags = a.causal && a.Sq == a.Sk ? w.counts : nullptr;
-      if (flags) launch_fwd32<D>(a, w, Skp, n_rep, bm_pos, nqb, nblk, flags);
-      launch_fwd_kernel<D, MASK_KPM>(a, w, Skp, n_rep, bm_pos, nqb, nblk, nullptr, flags);
+      if (flags) launch_fwd32<T, D>(a, w, Skp, n_rep, bm_pos, nqb, nblk, flags);
+      launch_fwd_kernel<T, D, MASK_KPM>(a, w, Skp, n_rep, bm_pos, nqb, nblk, nullptr, flags);
       break;
     }
-    default: launch_fwd32<D>(a, w, Skp, n_rep, bm_pos, nqb, nblk, nullptr);
+    default: launch_fwd32<T, D>(a, w, Skp, n_rep, bm_pos, nqb, nblk, nullptr);
   }
 }
 
-template <int D, int MODE>
+template <typename T, int D, int MODE>
 void launch_capture_kernel(const FwdArgs& a, const FwdWs& w, float* probs, int Skp, int n_rep,
                            int bm_pos, int nqb, unsigned nblk) {
-  KF_LAUNCH("capture_probs_mfma", (capture_probs_mfma_kernel<D, MODE>), dim3(nblk), dim3(256), 0,
-            a.stream, (const bf16*)a.q, a.cos, a.sin, w.krot, w.vn, (bf16*)a.out, a.lse, probs,
-            a.Sq, a.Sk, Skp, a.Hq, a.Hkv, n_rep, bm_pos, nqb, a.scale * kLog2e, a.causal,
-            a.doc ? a.doc : a.kvalid, w.ranges);
+  KF_LAUNCH("capture_probs_mfma", (capture_probs_mfma_kernel<T, D, MODE>), dim3(nblk), dim3(256),
+            0, a.stream, (const T*)a.q, a.cos, a.sin, (const T*)w.krot, (const T*)w.vn,
+            (T*)a.out, a.lse, probs, a.Sq, a.Sk, Skp, a.Hq, a.Hkv, n_rep, bm_pos, nqb,
+            a.scale * kLog2e, a.causal, a.doc ? a.doc : a.kvalid, w.ranges);
 }
 
-template <int D>
+template <typename T, int D>
 void launch_capture_mode(const FwdArgs& a, const FwdWs& w, float* probs, int Skp, int n_rep,
                          int bm_pos, int nqb, unsigned nblk) {
   switch (mask_mode(a)) {
     case MASK_DOC:
-      launch_capture_kernel<D, MASK_DOC>(a, w, probs, Skp, n_rep, bm_pos, nqb, nblk);
+      launch_capture_kernel<T, D, MASK_DOC>(a, w, probs, Skp, n_rep, bm_pos, nqb, nblk);
       break;
     case MASK_KPM:
-      launch_capture_kernel<D, MASK_KPM>(a, w, probs, Skp, n_rep, bm_pos, nqb, nblk);
+      launch_capture_kernel<T, D, MASK_KPM>(a, w, probs, Skp, n_rep, bm_pos, nqb, nblk);
       break;
-    default: launch_capture_kernel<D, MASK_NONE>(a, w, probs, Skp, n_rep, bm_pos, nqb, nblk);
+    default: launch_capture_kernel<T, D, MASK_NONE>(a, w, probs, Skp, n_rep, bm_pos, nqb, nblk);
   }
 }
 
@@ -1181,8 +1187,14 @@ int fwd_mfma(const FwdArgs& a, void* workspace) {
     rc = launch_kpm_row_flags(w.ranges, Skp / BN, a.Sk, a.B, w.counts, a.stream);
     if (rc) return rc;
   }
-  if (a.D == 128) launch_fwd_mode<128>(a, w, Skp, n_rep, bm_pos, nqb, (unsigned)nblk);
-  else launch_fwd_mode<64>(a, w, Skp, n_rep, bm_pos, nqb, (unsigned)nblk);
+  const bool h = a.dtype == F16;
+  if (a.D == 128) {
+    if (h) launch_fwd_mode<f16, 128>(a, w, Skp, n_rep, bm_pos, nqb, (unsigned)nblk);
+    else launch_fwd_mode<bf16, 128>(a, w, Skp, n_rep, bm_pos, nqb, (unsigned)nblk);
+  } else {
+    if (h) launch_fwd_mode<f16, 64>(a, w, Skp, n_rep, bm_pos, nqb, (unsigned)nblk);
+    else launch_fwd_mode<bf16, 64>(a, w, Skp, n_rep, bm_pos, nqb, (unsigned)nblk);
+  }
   KF_CHECK_LAUNCH();
   return KF_OK;
 }
@@ -1198,8 +1210,14 @@ int capture_probs_mfma(const FwdArgs& a, float* probs, void* workspace) {
   // one workgroup per pair of query blocks
   const int64_t nblk = (int64_t)((nqb + 1) / 2) * a.B * a.Hkv;
   KF_CHECK_ARG(nblk < (1LL << 31), "grid too large");
-  if (a.D == 128) launch_capture_mode<128>(a, w, probs, Skp, n_rep, bm_pos, nqb, (unsigned)nblk);
-  else launch_capture_mode<64>(a, w, probs, Skp, n_rep, bm_pos, nqb, (unsigned)nblk);
+  const bool h = a.dtype == F16;
+  if (a.D == 128) {
+    if (h) launch_capture_mode<f16, 128>(a, w, probs, Skp, n_rep, bm_pos, nqb, (unsigned)nblk);
+    else launch_capture_mode<bf16, 128>(a, w, probs, Skp, n_rep, bm_pos, nqb, (unsigned)nblk);
+  } else {
+    if (h) launch_capture_mode<f16, 64>(a, w, probs, Skp, n_rep, bm_pos, nqb, (unsigned)nblk);
+    else launch_capture_mode<bf16, 64>(a, w, probs, Skp, n_rep, bm_pos, nqb, (unsigned)nblk);
+  }
   KF_CHECK_LAUNCH();
   return KF_OK;
 }

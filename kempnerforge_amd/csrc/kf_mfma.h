@@ -93,8 +93,10 @@ __device__ __forceinline__ int swz(int row) {
                   : ((row >> 2) & 3);
 }
 
-template <int R>
-__device__ __forceinline__ const bf16x8& lds_frag(const bf16* tile, int row, int chunk) {
+// (E: the tile's 16-bit element type; fragments are bf16x8 containers)
+template <int R, typename E>
+__device__ __forceinline__ const bf16x8& lds_frag(const E* tile, int row, int chunk) {
+  static_assert(sizeof(E) == 2, "16-bit elements");
   return *(const bf16x8*)(tile + (row * R + (chunk ^ swz<R>(row))) * 8);
 }
 
@@ -131,7 +133,7 @@ __device__ __forceinline__ void dma4(uint32_t lds, uint32_t voff, const void* ba
                : : "v"(voff), "s"(base), "{m0}"(lds) : "memory");
 }
 
-// Copy a [ROWS_T][R chunks] bf16 tile whose rows start `ld` elements apart in
+// Copy a [ROWS_T][R chunks] 16-bit tile whose rows start `ld` elements apart in
 // global memory into a swizzled LDS tile with direct global->LDS loads: each
 // instruction moves 64 lanes x 16 bytes into 1 KB of contiguous LDS, so the
 // lane picks the global chunk that belongs at its LDS position.  The 4
@@ -142,9 +144,10 @@ __device__ __forceinline__ void dma4(uint32_t lds, uint32_t voff, const void* ba
 // FRESH: the per-lane offsets are recomputed at every call (a few VALU
 // instructions) instead of being kept live across the caller's loop, for
 // kernels whose registers are otherwise spent.
-template <int ROWS_T, int R, int NW = 4, bool FRESH = false>
-__device__ __forceinline__ void tile_to_lds(const bf16* __restrict__ g, uint32_t ld, bf16* lds,
+template <int ROWS_T, int R, int NW = 4, bool FRESH = false, typename E>
+__device__ __forceinline__ void tile_to_lds(const E* __restrict__ g, uint32_t ld, E* lds,
                                             int w, int lane, int rows = ROWS_T) {
+  static_assert(sizeof(E) == 2, "16-bit elements");
   constexpr int TOTAL = ROWS_T * R / 64;
   static_assert(TOTAL % NW == 0, "tile must split evenly over the wavefronts");
   constexpr int PER = TOTAL / NW;
@@ -203,9 +206,10 @@ __device__ __forceinline__ TrOffsets<D> tr_offsets(int lane) {
 // whose slot (h, j) carries row 16c + (j < 4 ? 4h + j : 8 + 4h + j - 4).  The
 // second read (rows + 8) fills slots 4..7.  That is the slot order of the P^T /
 // dS B operands built from the 32x32 C layout, so the products line up.
-template <int D>
-__device__ __forceinline__ bf16x8 lds_frag_t(const bf16* tile, const TrOffsets<D>& t, int c,
+template <int D, typename E>
+__device__ __forceinline__ bf16x8 lds_frag_t(const E* tile, const TrOffsets<D>& t, int c,
                                              int dt) {
+  static_assert(sizeof(E) == 2, "16-bit elements");
   const char* base = (const char*)tile + c * 16 * D * 2;
   const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)(base + t.o[dt][0]));
   const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)(base + t.o[dt][1]));

@@ -16,9 +16,12 @@ if GOLDEN not in sys.path:
 DEV = torch.device("cuda:0") if torch.cuda.is_available() else None
 
 # max-abs tolerances of the attention outputs (and of gradients before the
-# rounding of a low-precision output, see grad_bound): float32 1e-5,
-# bfloat16 / float16 2e-2, against a float64 oracle on the same inputs
-TOL = {torch.float32: 1e-5, torch.bfloat16: 2e-2, torch.float16: 2e-2}
+# rounding of a low-precision output, see grad_bound), against a float64
+# oracle on the same inputs: float32 1e-5 and bfloat16 2e-2 (the north star's);
+# float16, which the north star does not name, 5e-3: its significand has three
+# more bits than bfloat16's, so the kernels' roundings of P and dS (the MFMA
+# operands) and of the outputs are 8x smaller
+TOL = {torch.float32: 1e-5, torch.bfloat16: 2e-2, torch.float16: 5e-3}
 # significand bits (implicit bit included) of each storage format
 _SIG_BITS = {torch.float32: 24, torch.bfloat16: 8, torch.float16: 11}
 
@@ -42,8 +45,8 @@ def half_ulp(x: torch.Tensor, dtype) -> torch.Tensor:
 def grad_bound(want: torch.Tensor, dtype, group: int = 1) -> torch.Tensor:
     """Per-element bound on |got - want| for a gradient stored in ``dtype``.
 
-    float32: the absolute 1e-5.  bfloat16 / float16: 2e-2 plus half an ulp of
-    the storage format at |want|.  A gradient returned in bf16 is the computed
+    float32: the absolute 1e-5.  bfloat16 / float16: TOL (2e-2 / 5e-3) plus
+    half an ulp of the storage format at |want|.  A gradient returned in bf16 is the computed
     value rounded to bf16, and that rounding alone reaches half an ulp: 0.031
     for |g| in [8, 16), above 2e-2.  A bound of max(2e-2, half ulp) is
     therefore not met by any bf16-output kernel (an element whose rounding

@@ -43,7 +43,8 @@ def test_fixture():
     (torch.bfloat16, 70, 8, 2, 64, 900, 2200, 2300),  # plain split order (B > 64)
     (torch.bfloat16, 2, 8, 1, 128, 0, 3, 8),         # empty cache (len 0) and tiny
     (torch.bfloat16, 2, 6, 2, 128, 10, 90, 100),     # n_rep 3 (padded MFMA columns)
-    (torch.bfloat16, 2, 32, 1, 128, 500, 700, 800),  # n_rep 32, the widest fast case
+    (torch.bfloat16, 2, 16, 1, 128, 500, 700, 800),  # n_rep 16, the widest fast case
+    (torch.bfloat16, 2, 32, 1, 128, 500, 700, 800),  # n_rep 32 -> generic kernel
     (torch.bfloat16, 1, 64, 8, 128, 1000, 1300, 1400),  # 70B heads, n_rep 8
     (torch.bfloat16, 2, 64, 1, 64, 10, 90, 100),     # n_rep 64 -> generic kernel
     (torch.float32, 2, 4, 2, 64, 10, 90, 100),       # fp32 -> generic kernel

@@ -2,7 +2,8 @@
 
 Tolerances (north-star): float32 max-abs 1e-5; bfloat16 max-abs 2e-2 on the
 output and 1e-3 on the LSE, both against the float64 oracle evaluated from the
-same inputs with the reference's RoPE rounding.
+same inputs with the reference's RoPE rounding; float16 (not named by the north
+star) 5e-3 on the output and 1e-3 on the LSE.
 """
 
 from __future__ import annotations
@@ -11,13 +12,11 @@ import pytest
 import torch
 
 import make_fixtures as mf
-from gpu_util import DEV, announce, load_fixture, max_abs, seeded
+from gpu_util import DEV, TOL, announce, load_fixture, max_abs, seeded
 from kempnerforge_amd import ops
 from oracle import attention_ref as ref
 
 pytestmark = pytest.mark.gpu
-
-TOL = {torch.float32: 1e-5, torch.bfloat16: 2e-2, torch.float16: 2e-2}
 
 
 def _run(q, k, v, cos, sin, causal=True):
@@ -45,7 +44,10 @@ SHAPES = [
     (torch.bfloat16, 1, 1, 4, 2, 128, 5e5),      # single token
     (torch.bfloat16, 1, 64, 32, 1, 128, 5e5),    # n_rep 32: 4 positions per block
     (torch.bfloat16, 1, 77, 4, 2, 32, 1e4),      # generic kernel (D=32)
-    (torch.float16, 1, 90, 4, 2, 128, 1e4),      # generic kernel (fp16)
+    (torch.float16, 1, 90, 4, 2, 128, 1e4),      # MFMA kernels in fp16
+    (torch.float16, 2, 200, 4, 4, 64, 1e4),      # fp16, MHA, D=64
+    (torch.float16, 1, 300, 8, 1, 128, 5e5),     # fp16, MQA
+    (torch.float16, 1, 77, 4, 2, 32, 1e4),       # generic kernel (fp16, D=32)
     (torch.float32, 1, 150, 8, 2, 128, 5e5),     # generic kernel (fp32, D=128)
 ]
 

@@ -29,6 +29,10 @@ def _f32(x: float) -> float:
     return float(np.float32(x))
 
 
+def _f16(x: float) -> float:
+    return float(np.float16(np.float32(x)))
+
+
 # --------------------------------------------------------------------------- RoPE tables
 class TestRopeTables:
     # reference tests/unit/test_model.py:67-106
@@ -74,6 +78,24 @@ class TestApplyRope:
                 x1, x2 = float(x[0, 0, s, j]), float(x[0, 0, s, j + d])
                 r1 = _bf16(_f32(_bf16(x1 * c) - _bf16(x2 * sn)))
                 r2 = _bf16(_f32(_bf16(x2 * c) + _bf16(x1 * sn)))
+                assert float(got[0, 0, s, j]) == r1
+                assert float(got[0, 0, s, j + d]) == r2
+
+    def test_scalar_loop_fp16_rounding(self):
+        # the same for float16 (the reference's mixed_precision = "fp16"): the
+        # tables cast to fp16 and every product and sum rounded to fp16
+        g = torch.Generator().manual_seed(14)
+        S, D = 5, 8
+        cos, sin = ref.rope_tables(D, S, 10000.0)
+        x = torch.randn(1, 1, S, D, generator=g).half()
+        got = ref.apply_rope(x, cos, sin).float()
+        d = D // 2
+        for s in range(S):
+            for j in range(d):
+                c, sn = _f16(float(cos[s, j])), _f16(float(sin[s, j]))
+                x1, x2 = float(x[0, 0, s, j]), float(x[0, 0, s, j + d])
+                r1 = _f16(_f32(_f16(x1 * c) - _f16(x2 * sn)))
+                r2 = _f16(_f32(_f16(x2 * c) + _f16(x1 * sn)))
                 assert float(got[0, 0, s, j]) == r1
                 assert float(got[0, 0, s, j + d]) == r2
 
