@@ -244,6 +244,46 @@ def attention_bwd(q, k, v, cos, sin, dout, *, causal: bool = True, compute_dtype
     )
 
 
+def attention_bwd_rounded_operands(q, k, v, cos, sin, dout, *, operand_dtype,
+                                   causal: bool = True, doc_ids=None, key_padding_mask=None):
+    """:func:`attention_bwd` with the products' 16-bit operands rounded: the
+    closed-form flash-attention backward in float64 except that P (the operand of
+    dV = P^T dO) and dS = P (dP - Delta) (the operand of dK and dQ) are rounded
+    to ``operand_dtype``, and Delta = rowsum(dO * O) uses the output O as stored
+    (rounded to the input dtype).  Any backward whose matrix products take bf16
+    (fp16) P and dS operands, the reference's bf16 SDPA backward included, carries
+    at least this rounding against exact arithmetic; the GPU tests use the
+    difference to :func:`attention_bwd` as the error the operand format itself
+    forces.  ``operand_dtype=None`` rounds nothing (and keeps O exact), which
+    equals :func:`attention_bwd` to float64 rounding (``tests/test_oracle.py``).
+    """
+    qr, kr, vt = _rotated_bhsd(q, k, v, cos, sin)
+    n_rep = qr.shape[1] // kr.shape[1]
+    f64 = torch.float64
+    rnd = (lambda x: x) if operand_dtype is None else (lambda x: x.to(operand_dtype).to(f64))
+    qf, kf, vf = qr.to(f64), gqa_expand(kr, n_rep).to(f64), gqa_expand(vt, n_rep).to(f64)
+    do = dout.transpose(1, 2).to(f64)
+    scale = q.shape[-1] ** -0.5
+    s = _scores(qf, kf, causal, doc_ids, key_padding_mask)
+    p = torch.exp(s - torch.logsumexp(s, dim=-1, keepdim=True))
+    o = torch.matmul(p, vf)
+    o_stored = o if operand_dtype is None else o.to(q.dtype).to(f64)
+    pr = rnd(p)
+    dv = torch.matmul(pr.transpose(-2, -1), do)
+    dp = torch.matmul(do, vf.transpose(-2, -1))
+    delta = (do * o_stored).sum(-1, keepdim=True)
+    ds = rnd(pr * (dp - delta))
+    dq = torch.matmul(ds, kf) * scale
+    dk = torch.matmul(ds.transpose(-2, -1), qf) * scale
+    B, Hq, S, D = dk.shape
+    dk = dk.view(B, Hq // n_rep, n_rep, S, D).sum(2)
+    dv = dv.view(B, Hq // n_rep, n_rep, -1, D).sum(2)
+    dq = rotate_half_inverse(dq, cos, sin, q.dtype)
+    dk = rotate_half_inverse(dk, cos, sin, k.dtype)
+    return (dq.transpose(1, 2).contiguous(), dk.transpose(1, 2).contiguous(),
+            dv.transpose(1, 2).contiguous())
+
+
 def decode_step(q_new, k_new, v_new, k_cache, v_cache, lens, cos_table, sin_table,
                 *, compute_dtype=torch.float64):
     """One KV-cache decode step with a per-sequence cache fill level.

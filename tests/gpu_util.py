@@ -42,7 +42,7 @@ def half_ulp(x: torch.Tensor, dtype) -> torch.Tensor:
     return torch.exp2(torch.floor(torch.log2(a)) - _SIG_BITS[dtype])
 
 
-def grad_bound(want: torch.Tensor, dtype, group: int = 1) -> torch.Tensor:
+def grad_bound(want: torch.Tensor, dtype, group: int = 1, operand_err=None) -> torch.Tensor:
     """Per-element bound on |got - want| for a gradient stored in ``dtype``.
 
     float32: the absolute 1e-5.  bfloat16 / float16: TOL (2e-2 / 5e-3) plus
@@ -64,19 +64,37 @@ def grad_bound(want: torch.Tensor, dtype, group: int = 1) -> torch.Tensor:
     needs, printed by check_grad): 1.23-1.33 with causal or packed-document
     masks, 2.11 with random key padding on 200 positions, whose rows attend few
     keys (P near 1, so the bf16 rounding of P and dS is largest against dK).
+
+    ``operand_err``: optionally, per element, |g_r - want| where g_r is the
+    gradient computed exactly except for P and dS rounded to the 16-bit
+    operand type (oracle.attention_bwd_rounded_operands): the error the
+    operand format itself forces on any backward that multiplies bf16 (fp16)
+    P and dS, the reference's bf16 SDPA backward included.  On short rows it
+    can exceed the base tolerance by itself (a 31-position causal case with
+    groups of 8 reaches 1.17x the bound with exact arithmetic otherwise), and
+    is then added to the bound.
     """
     if dtype == torch.float32:
         return torch.full_like(want.double(), TOL[torch.float32])
     factor = 1.0 if group <= 8 else 1.25 * (group / 8.0) ** 0.5
-    return TOL[dtype] * factor + half_ulp(want, dtype)
+    bound = TOL[dtype] * factor + half_ulp(want, dtype)
+    return bound if operand_err is None else bound + operand_err
 
 
-def check_grad(got, want, dtype, name: str, group: int = 1) -> float:
+def check_grad(got, want, dtype, name: str, group: int = 1, operand_ref=None) -> float:
     """Assert |got - want| <= grad_bound(want, dtype, group) for every element;
-    prints the observed max-abs error and the worst ratio of error to bound."""
+    prints the observed max-abs error and the worst ratio of error to bound.
+    With ``operand_ref`` (the rounded-operand gradient, see grad_bound) its
+    distance to ``want`` is added to the bound and printed."""
     w = want.detach().double().cpu()
     err = (got.detach().float().cpu().double() - w).abs()
-    ratio = (err / grad_bound(w, dtype, group)).max().item()
+    op_err = None
+    if operand_ref is not None:
+        op_err = (operand_ref.detach().double().cpu() - w).abs()
+        print(f"[{name}] rounded-operand gradient: max-abs err {op_err.max().item():.3e}; "
+              f"its worst err/bound {(op_err / grad_bound(w, dtype, group)).max().item():.3f}",
+              flush=True)
+    ratio = (err / grad_bound(w, dtype, group, op_err)).max().item()
     # the factor on the base tolerance this result needs: max (err - half ulp) / tol
     need = ((err - half_ulp(w, dtype)) / TOL[dtype]).max().item() if dtype != torch.float32 \
         else (err / TOL[dtype]).max().item()

@@ -306,6 +306,71 @@ class TestBackward:
         assert torch.allclose(dv, vv.grad, atol=1e-10)
 
 
+    @pytest.mark.parametrize("mask", [None, "noncausal", "doc", "kpm"])
+    def test_rounded_operands_without_rounding_equal_autograd(self, mask):
+        # the closed-form restatement (no rounding) against autograd of the
+        # pinned forward, masks and NaN guard included: catches a wrong
+        # Delta, a missing group sum or scale, a transposed dS
+        B, S, Hq, Hkv, D = 2, 23, 6, 2, 16
+        q, k, v, cos, sin = _inputs(B, S, Hq, Hkv, D, torch.bfloat16, seed=31)
+        do = torch.randn(B, S, Hq, D, generator=torch.Generator().manual_seed(32)).bfloat16()
+        kw = {}
+        if mask == "doc":
+            kw["doc_ids"] = torch.tensor([[0] * 9 + [1] * 14, [0] * 3 + [1] * 20])
+        elif mask == "kpm":
+            kpm = torch.ones(B, S, dtype=torch.bool)
+            kpm[0, :5] = False
+            kpm[1, 10:15] = False
+            kw["key_padding_mask"] = kpm
+        causal = mask != "noncausal"
+        want = ref.attention_bwd(q, k, v, cos, sin, do, causal=causal, **kw)
+        got = ref.attention_bwd_rounded_operands(q, k, v, cos, sin, do, operand_dtype=None,
+                                                 causal=causal, **kw)
+        for g, w in zip(got, want):
+            assert torch.allclose(g, w, atol=1e-10, rtol=0)
+
+    def test_rounded_operands_scalar_loop(self):
+        # brute force on one head: P and dS rounded to bf16, O as stored in bf16,
+        # everything else exact (catches rounding at the wrong point, e.g. dS
+        # formed from the unrounded P or rounded before the product)
+        S, D = 4, 2
+        q, k, v, cos, sin = _inputs(1, S, 1, 1, D, torch.bfloat16, seed=33)
+        do = torch.randn(1, S, 1, D, generator=torch.Generator().manual_seed(34)).bfloat16()
+        got = ref.attention_bwd_rounded_operands(q, k, v, cos, sin, do,
+                                                 operand_dtype=torch.bfloat16)
+        qr = ref.apply_rope(q.transpose(1, 2), cos, sin)[0, 0].double().tolist()
+        kr = ref.apply_rope(k.transpose(1, 2), cos, sin)[0, 0].double().tolist()
+        vv = v[0, :, 0].double().tolist()
+        dd = do[0, :, 0].double().tolist()
+        sc = D ** -0.5
+        dqr = [[0.0] * D for _ in range(S)]
+        dkr = [[0.0] * D for _ in range(S)]
+        dv = [[0.0] * D for _ in range(S)]
+        for i in range(S):
+            s = [sum(qr[i][d] * kr[j][d] for d in range(D)) * sc for j in range(i + 1)]
+            m = max(s)
+            z = sum(math.exp(x - m) for x in s)
+            p = [math.exp(x - m) / z for x in s]
+            o = [_bf16(sum(p[j] * vv[j][d] for j in range(i + 1))) for d in range(D)]
+            delta = sum(dd[i][d] * o[d] for d in range(D))
+            for j in range(i + 1):
+                pr = _bf16(p[j])
+                dp = sum(dd[i][d] * vv[j][d] for d in range(D))
+                ds = _bf16(pr * (dp - delta))
+                for d in range(D):
+                    dv[j][d] += pr * dd[i][d]
+                    dqr[i][d] += ds * kr[j][d] * sc
+                    dkr[j][d] += ds * qr[i][d] * sc
+        want_dv = torch.tensor(dv, dtype=torch.float64)
+        assert torch.allclose(got[2][0, :, 0], want_dv, atol=1e-12, rtol=0)
+        dq = ref.rotate_half_inverse(torch.tensor(dqr, dtype=torch.float64).view(1, 1, S, D), cos, sin,
+                                     torch.bfloat16)
+        dk = ref.rotate_half_inverse(torch.tensor(dkr, dtype=torch.float64).view(1, 1, S, D), cos, sin,
+                                     torch.bfloat16)
+        assert torch.allclose(got[0][0, :, 0], dq[0, 0], atol=1e-12, rtol=0)
+        assert torch.allclose(got[1][0, :, 0], dk[0, 0], atol=1e-12, rtol=0)
+
+
 # --------------------------------------------------------------------------- packed documents
 def _packed_doc_ids(B, lengths_per_row):
     """[B, S] int64 document ids, contiguous increasing segments per row (what
