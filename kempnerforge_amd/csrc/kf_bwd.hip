@@ -167,7 +167,7 @@ struct DkdvStage {
 // MASK_KPM: qlist as above, drow the key-validity row, fv the first valid
 // key's position: query rows before it (guarded) see every key, other rows
 // need the key valid and not after them.
-template <typename T, int D, bool DSROLE, int MODE, bool STORE>
+template <typename T, int D, bool DSROLE, int MODE, bool STORE, bool PART>
 __device__ __forceinline__ void dkdv_role(
     DkdvStage<T, D>* st, u32x4* sP, const T* __restrict__ krot, const T* __restrict__ v,
     const T* __restrict__ qrot, const T* __restrict__ dout,
@@ -176,7 +176,7 @@ __device__ __forceinline__ void dkdv_role(
     T* __restrict__ dv, int S, int P, int Hq, int Hkv, int n_rep, int b, int g, int bh, int k0,
     int w, int lane, float scale_log2, float scale, int causal, const int32_t* __restrict__ drow,
     const uint16_t* qlist, int nlist, int32_t (*sQD)[BQ], int fv, u32x4* __restrict__ dsb,
-    int nqtp, bool live) {
+    int nqtp, bool live, int part, int nsplit, float* __restrict__ pout) {
   constexpr bool DOC = MODE == MASK_DOC, KPM = MODE == MASK_KPM, LIST = DOC || KPM;
   // key padding keeps records only for a batch row whose first key is valid:
   // it has no guarded rows, so every dS tile lies in the causal record layout
@@ -195,7 +195,10 @@ __device__ __forceinline__ void dkdv_role(
   const int per_head = LIST ? nlist : nqt - qt0;
   // (live false: no query tile, dK / dV stored as zeros; a later launch
   // writes this item's results)
-  const int total = per_head > 0 && live ? per_head * n_rep : 0;
+  // PART: part `part` of `nsplit` takes the group's query heads
+  // [h_base, h_base + n_rep / nsplit); otherwise all n_rep
+  const int nh = PART ? n_rep / nsplit : n_rep, h_base = PART ? part * nh : 0;
+  const int total = per_head > 0 && live ? per_head * nh : 0;
   // iteration -> query tile entry (tile | DOC_MASK_FLAG when listed), head-major
   auto entry = [&](int it) -> int {
     return LIST ? __builtin_amdgcn_readfirstlane((int)qlist[it % per_head]) : qt0 + it % per_head;
@@ -217,10 +220,12 @@ __device__ __forceinline__ void dkdv_role(
     // +inf, so they contribute nothing)
     tile_to_lds<BQ, KR, 8, LIST>(dout + (((int64_t)b * S + q0) * Hq + hq) * D, Hq * D, S_.o, w,
                                  lane, S - q0);
-    if (LIST) {
+    if (LIST || PART) {
       // the row statistics' LDS addresses from the stage array's base plus
       // constant offsets: with the pointer into the stage member, the masked
-      // kernels fail to compile ("Operand has incorrect register class")
+      // and split kernels fail to compile ("Operand has incorrect register
+      // class": a constant generic-to-LDS address cast lowered with an
+      // illegal null test)
       using Stage = DkdvStage<T, D>;
       const uint32_t sb = st_lds + (uint32_t)(buf * sizeof(Stage));
       if (w == 0) dma4(sb + offsetof(Stage, l), (uint32_t)lane * 4u, lse2 + bhq * P + q0);
@@ -231,7 +236,9 @@ __device__ __forceinline__ void dkdv_role(
     }
     if (DOC && w == 2) dma4(lds_addr(sQD[buf]), (uint32_t)min(q0 + lane, S - 1) * 4u, drow);
   };
-  auto stage = [&](int it, int buf) { stage_tile(it / per_head, tile_of(entry(it)), buf); };
+  auto stage = [&](int it, int buf) {
+    stage_tile(h_base + it / per_head, tile_of(entry(it)), buf);
+  };
   // DOC: the first tile was staged by the caller before the list was built
   if (!DOC && total > 0) stage(0, 0);
 
@@ -271,7 +278,7 @@ __device__ __forceinline__ void dkdv_role(
   const int k32 = k0 / DSK + kw;  // this wavefront's 32-key record column
   const int nqtp2 = 2 * nqtp;
   const int64_t rec_bh = (int64_t)bh * nqtp * (causal ? nqtp + 1 : nqtp2);
-  int rec_head = 0, rec_tile = 0;  // head and tile count of iteration it (no division)
+  int rec_head = h_base, rec_tile = 0;  // head and tile count of iteration it (no division)
 
   lds_copy_wait();
   __syncthreads();
@@ -439,6 +446,19 @@ __device__ __forceinline__ void dkdv_role(
   }
 
   if (key >= S) return;
+  if (PART) {
+    // a part of a split item: this role's float32 sums (dK or dV; the
+    // reduction applies the scale, the RoPE backward and the rounding);
+    // element 4 gi + e of acc[dt] is dim 32 dt + 8 gi + 4 hh + e
+    float* dst = pout + ((int64_t)bh * S + key) * D + 4 * hh;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int gi = 0; gi < 4; ++gi)
+        *(f32x4*)(dst + 32 * dt + 8 * gi) =
+            f32x4{acc[dt][4 * gi], acc[dt][4 * gi + 1], acc[dt][4 * gi + 2], acc[dt][4 * gi + 3]};
+    return;
+  }
   const int key_e = key;
   int hoff = 4 * hh;
   if (LIST) asm volatile("" : "+v"(hoff));
@@ -495,7 +515,7 @@ __device__ __forceinline__ void dkdv_stage_first(
 // which runs after it and skips the rows without padding; the unmasked launch
 // walks no query tile for the padded rows' items (their dK / dV are written
 // as zeros, then overwritten by the KPM launch).
-template <typename T, int D, int MODE, bool STORE, bool SPLIT = false>
+template <typename T, int D, int MODE, bool STORE, bool SPLIT = false, bool PART = false>
 __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(
     const T* __restrict__ krot, const T* __restrict__ v, const T* __restrict__ qrot,
     const T* __restrict__ dout, const float* __restrict__ lse2, const float* __restrict__ delta,
@@ -503,7 +523,8 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(
     T* __restrict__ dv, int S, int P, int Hq, int Hkv, int n_rep, int nkb, int nitems,
     float scale_log2,
     float scale, int causal, const int32_t* __restrict__ aux, const int2* __restrict__ ranges,
-    u32x4* __restrict__ dsb, const int* __restrict__ order, const int* __restrict__ kpm_flags) {
+    u32x4* __restrict__ dsb, const int* __restrict__ order, const int* __restrict__ kpm_flags,
+    int nsplit, float* __restrict__ dkp, float* __restrict__ dvp, int64_t part_stride) {
   constexpr bool DOC = MODE == MASK_DOC, KPM = MODE == MASK_KPM;
   __shared__ __attribute__((aligned(16))) DkdvStage<T, D> st[2];
   __shared__ __attribute__((aligned(16))) u32x4 sP[4 * 4 * 64];  // [key group][chunk][lane]
@@ -511,11 +532,16 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(
   __shared__ uint16_t sList[DOC_MAX_TILES];                      // listed query tiles
   __shared__ int sCount, sFirst;
   const int w = wave_id(), lane = threadIdx.x & 63;
-  // persistent: one (key block, KV head) item per round
+  // persistent: one (key block, KV head) item per round; PART: an item is one
+  // of nsplit parts of a key block, each with n_rep / nsplit of the group's
+  // query heads, the parts adjacent in the order (unmasked launches only)
   const XcdItems xi = xcd_items(nitems);
   for (int rnd = 0;; ++rnd) {
     int logical = xcd_item(xi, rnd);
     if (logical < 0) break;
+    // (wavefront-uniform; readfirstlane keeps the staging bases scalar)
+    const int part = PART ? __builtin_amdgcn_readfirstlane(logical % nsplit) : 0;
+    if (PART) logical = __builtin_amdgcn_readfirstlane(logical / nsplit);
     if (order != nullptr) {
       // items by descending work (the (batch row, key block) order, heads
       // adjacent), dealt round-robin over the XCDs
@@ -569,16 +595,61 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(
       nlist = __builtin_amdgcn_readfirstlane(sCount);
     }
     if (w >= 4)
-      dkdv_role<T, D, true, MODE, STORE>(st, sP, krot, v, qrot, dout, lse2, delta, cos, sin, dk,
+      dkdv_role<T, D, true, MODE, STORE, PART>(st, sP, krot, v, qrot, dout, lse2, delta, cos, sin, dk,
                                       dv, S, P, Hq, Hkv, n_rep, b, g, bh, k0, w, lane,
                                       scale_log2, scale, causal, drow, sList, nlist, sQD, fv,
-                                      dsb, P / DSQ, live);
+                                      dsb, P / DSQ, live, part, nsplit,
+                                      PART ? dkp + part * part_stride : nullptr);
     else
-      dkdv_role<T, D, false, MODE, STORE>(st, sP, krot, v, qrot, dout, lse2, delta, cos, sin, dk,
+      dkdv_role<T, D, false, MODE, STORE, PART>(st, sP, krot, v, qrot, dout, lse2, delta, cos, sin, dk,
                                        dv, S, P, Hq, Hkv, n_rep, b, g, bh, k0, w, lane,
                                        scale_log2, scale, causal, drow, sList, nlist, sQD, fv,
-                                       dsb, P / DSQ, live);
+                                       dsb, P / DSQ, live, part, nsplit,
+                                       PART ? dvp + part * part_stride : nullptr);
     __syncthreads();  // LDS of this item is free for the next
+  }
+}
+
+// dK and dV of split dK/dV items: the nsplit parts' float32 sums added in
+// part order, then what the unsplit kernel does at its store (dV rounded to T;
+// dK scaled, rotated back by the dtype-cast tables, rounded).  Row r = bh * S
+// + key; per row HALF / 4 threads take four dK dims and their RoPE partners,
+// D / 8 threads eight dV dims.
+template <typename T, int D>
+__global__ __launch_bounds__(256) void dkdv_reduce_kernel(
+    const float* __restrict__ dkp, const float* __restrict__ dvp, int nsplit,
+    int64_t part_stride, const float* __restrict__ cos, const float* __restrict__ sin,
+    T* __restrict__ dk, T* __restrict__ dv, int S, int Hkv, float scale, int nrows) {
+  constexpr int HALF = D / 2, TK = HALF / 4, TPR = TK + D / 8;
+  const int t = blockIdx.x * 256 + threadIdx.x;
+  const int row = t / TPR, j = t % TPR;
+  if (row >= nrows) return;
+  const int bh = row / S, key = row % S, b = bh / Hkv, g = bh % Hkv;
+  const int64_t out = (((int64_t)b * S + key) * Hkv + g) * D;
+  const int64_t in = (int64_t)row * D;
+  if (j < TK) {
+    const int d0 = 4 * j;
+    f32x4 lo = {0.f, 0.f, 0.f, 0.f}, hi = lo;
+    for (int p = 0; p < nsplit; ++p) {
+      lo += *(const f32x4*)(dkp + p * part_stride + in + d0);
+      hi += *(const f32x4*)(dkp + p * part_stride + in + d0 + HALF);
+    }
+    float r1[4], r2[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      rope_pair_bwd<T>(lo[e] * scale, hi[e] * scale, cos[(int64_t)key * HALF + d0 + e],
+                       sin[(int64_t)key * HALF + d0 + e], r1[e], r2[e]);
+    *(u32x2*)(dk + out + d0) = u32x2{pack2<T>(r1[0], r1[1]), pack2<T>(r1[2], r1[3])};
+    *(u32x2*)(dk + out + d0 + HALF) = u32x2{pack2<T>(r2[0], r2[1]), pack2<T>(r2[2], r2[3])};
+  } else {
+    const int d0 = 8 * (j - TK);
+    f32x4 a = {0.f, 0.f, 0.f, 0.f}, c = a;
+    for (int p = 0; p < nsplit; ++p) {
+      a += *(const f32x4*)(dvp + p * part_stride + in + d0);
+      c += *(const f32x4*)(dvp + p * part_stride + in + d0 + 4);
+    }
+    *(u32x4*)(dv + out + d0) = u32x4{pack2<T>(a[0], a[1]), pack2<T>(a[2], a[3]),
+                                     pack2<T>(c[0], c[1]), pack2<T>(c[2], c[3])};
   }
 }
 
@@ -1257,20 +1328,55 @@ namespace {
 struct Ws {
   uint16_t *krot, *qrot;  // 16-bit elements of the call's dtype
   float *lse2, *delta;  // -lse / scale and -Delta (q_prep_bwd)
+  float* dkvp;  // split dK/dV items: nsplit dK parts, then nsplit dV parts, [B*Hkv][S][D] each
   int2* ranges;  // [B][P/64] document-id range per tile (packed documents only)
   int *counts, *order;  // [B][P/128] each: dK/dV item work and order (packed documents)
   u32x4* dsb;    // dS records (when kept)
 };
 
+// Parts each unmasked dK/dV item is split into.  The persistent grid has one
+// workgroup per CU and its zigzag shares pair long items with short ones, so
+// it needs at least two items per workgroup; a launch with fewer (few batch
+// rows and KV heads: a tensor-parallel rank's share, long single sequences)
+// gives each part of an item an equal share of the KV group's query heads
+// (the smallest divisor of n_rep up to 8 that reaches two items per
+// workgroup, else the largest), and dkdv_reduce_kernel adds the parts'
+// float32 sums.  Measured without the split on the reference's TP = 4
+// shares, the dK/dV kernel took 2.9x (70B) and 5.4x (29B) its C3 time per
+// causal pair.  The masked kernels are not persistent and are not split (key
+// padding's unpadded batch rows run the unmasked kernel, split the same way).
+int dkdv_splits(int B, int S, int Hq, int Hkv) {
+  const int n_rep = Hq / Hkv;
+  const int64_t items = (int64_t)(pad_len(S) / BKV) * B * Hkv;
+  const int64_t want = 2 * (int64_t)(device_cu_count() / 8 * 8);
+  if (items >= want) return 1;
+  int n = 1;
+  for (int d = 2; d <= 8 && d <= n_rep; ++d) {
+    if (n_rep % d) continue;
+    n = d;
+    if (items * d >= want) break;
+  }
+  return n;
+}
+
+size_t align256(size_t n) { return (n + 255) / 256 * 256; }
+
+// the split items' float32 dK and dV parts (none when unsplit)
+size_t split_bytes(int B, int S, int Hq, int Hkv, int D) {
+  const int n = dkdv_splits(B, S, Hq, Hkv);
+  return n > 1 ? 2 * (size_t)n * B * Hkv * S * D * sizeof(float) : 0;
+}
+
 // krot and qrot (unless the caller's rot holds them), lse2, delta, tile
-// records, item counts and order
+// records, item counts and order, then (256-byte aligned) the split dK/dV parts
 size_t base_bytes(int B, int S, int Hq, int Hkv, int D, bool rot) {
   const size_t P = (size_t)pad_len(S);
-  return (rot ? 0 : ((size_t)B * Hkv + (size_t)B * Hq) * P * D * sizeof(uint16_t)) +
-         2 * (size_t)B * Hq * P * sizeof(float) + (size_t)B * (P / BN) * sizeof(int2) +
-         2 * (size_t)B * (P / BKV) * sizeof(int);
+  const size_t head = (rot ? 0 : ((size_t)B * Hkv + (size_t)B * Hq) * P * D * sizeof(uint16_t)) +
+                      2 * (size_t)B * Hq * P * sizeof(float) +
+                      (size_t)B * (P / BN) * sizeof(int2) + 2 * (size_t)B * (P / BKV) * sizeof(int);
+  const size_t parts = split_bytes(B, S, Hq, Hkv, D);
+  return parts ? align256(head) + parts : head;
 }
-size_t align256(size_t n) { return (n + 255) / 256 * 256; }
 
 // Largest dS record store the backward uses; past it dQ recomputes S and dP.
 constexpr size_t DS_STORE_MAX = (size_t)32 << 30;
@@ -1299,6 +1405,8 @@ Ws carve(void* base, int B, int S, int Hq, int Hkv, int D, const void* rot) {
   w.ranges = (int2*)f;
   w.counts = (int*)(w.ranges + (size_t)B * (P / BN));
   w.order = w.counts + (size_t)B * (P / BKV);
+  w.dkvp = (float*)((char*)base + align256((size_t)((char*)(w.order + (size_t)B * (P / BKV)) -
+                                                    (char*)base)));
   w.dsb = (u32x4*)((char*)base + align256(base_bytes(B, S, Hq, Hkv, D, rot != nullptr)));
   return w;
 }
@@ -1377,29 +1485,56 @@ int launch_bwd(const BwdArgs& a, void* workspace, bool keep_ds) {
   // causal key padding: the batch rows whose keys are all valid go to the
   // unmasked (persistent) kernel first, the rest to the KPM one
   const int* kpm_flags = mode == MASK_KPM && a.causal ? w.counts : nullptr;
+  // The unmasked (persistent) launches with few items split each item into
+  // nsplit parts and add them in dkdv_reduce (the same split for the key
+  // padding rows without padding as for an unmasked launch, so an all-True
+  // mask gives the unmasked result bit for bit)
+  const int64_t part_stride = (int64_t)a.B * a.Hkv * a.S * D;
+  auto reduce_parts = [&](int nsplit, float* dkp, float* dvp) {
+    constexpr int TPR = D / 8 + D / 8;  // threads per row of dkdv_reduce_kernel
+    const int64_t nrows = (int64_t)a.B * a.Hkv * a.S;
+    KF_LAUNCH("dkdv_reduce", (dkdv_reduce_kernel<T, D>),
+              dim3((unsigned)((nrows * TPR + 255) / 256)), dim3(256), 0, a.stream, dkp, dvp,
+              nsplit, part_stride, a.cos, a.sin, (T*)a.dk, (T*)a.dv, a.S, a.Hkv, a.scale,
+              (int)nrows);
+  };
   if (kpm_flags) {
     const int rc = launch_kpm_row_flags(w.ranges, P / BN, a.S, a.B, w.counts, a.stream);
     if (rc) return rc;
+    const int ns = dkdv_splits(a.B, a.S, a.Hq, a.Hkv);
+    float* dkp = ns > 1 ? w.dkvp : nullptr;
+    float* dvp = ns > 1 ? w.dkvp + ns * part_stride : nullptr;
+    const int ni = nkb * a.B * a.Hkv * ns;
     KF_LAUNCH("bwd_dkdv",
-              (keep_ds ? bwd_dkdv_kernel<T, D, MASK_NONE, true, true>
-                       : bwd_dkdv_kernel<T, D, MASK_NONE, false, true>),
-              dim3(std::min(nkb * a.B * a.Hkv, device_cu_count() / 8 * 8)), dim3(512), 0, a.stream,
+              (ns > 1 ? (keep_ds ? bwd_dkdv_kernel<T, D, MASK_NONE, true, true, true>
+                                 : bwd_dkdv_kernel<T, D, MASK_NONE, false, true, true>)
+                      : (keep_ds ? bwd_dkdv_kernel<T, D, MASK_NONE, true, true>
+                                 : bwd_dkdv_kernel<T, D, MASK_NONE, false, true>)),
+              dim3(std::min(ni, device_cu_count() / 8 * 8)), dim3(512), 0, a.stream,
               (const T*)w.krot, (const T*)a.v, (const T*)w.qrot, (const T*)a.dout, w.lse2, w.delta,
-              a.cos, a.sin, (T*)a.dk, (T*)a.dv, a.S, P, a.Hq, a.Hkv, n_rep, nkb,
-              nkb * a.B * a.Hkv, scale_log2, a.scale, a.causal, nullptr, w.ranges, w.dsb,
-              nullptr, kpm_flags);
+              a.cos, a.sin, (T*)a.dk, (T*)a.dv, a.S, P, a.Hq, a.Hkv, n_rep, nkb, ni, scale_log2,
+              a.scale, a.causal, nullptr, w.ranges, w.dsb, nullptr, kpm_flags, ns, dkp, dvp,
+              part_stride);
+    if (ns > 1) reduce_parts(ns, dkp, dvp);
   }
+  const int nsplit = mode == MASK_NONE ? dkdv_splits(a.B, a.S, a.Hq, a.Hkv) : 1;
+  float* dkp = nsplit > 1 ? w.dkvp : nullptr;
+  float* dvp = nsplit > 1 ? w.dkvp + nsplit * part_stride : nullptr;
+  const int nitems = nkb * a.B * a.Hkv * nsplit;
   KF_LAUNCH("bwd_dkdv",
             (mode == MASK_DOC   ? (keep_ds ? bwd_dkdv_kernel<T, D, MASK_DOC, true>
                                            : bwd_dkdv_kernel<T, D, MASK_DOC, false>)
              : mode == MASK_KPM ? (keep_ds ? bwd_dkdv_kernel<T, D, MASK_KPM, true>
                                            : bwd_dkdv_kernel<T, D, MASK_KPM, false>)
+             : nsplit > 1       ? (keep_ds ? bwd_dkdv_kernel<T, D, MASK_NONE, true, false, true>
+                                           : bwd_dkdv_kernel<T, D, MASK_NONE, false, false, true>)
              : keep_ds          ? bwd_dkdv_kernel<T, D, MASK_NONE, true>
                                 : bwd_dkdv_kernel<T, D, MASK_NONE, false>),
-            dim3(std::min(nkb * a.B * a.Hkv, grid_cap)), dim3(512), 0, a.stream, (const T*)w.krot,
+            dim3(std::min(nitems, grid_cap)), dim3(512), 0, a.stream, (const T*)w.krot,
             (const T*)a.v, (const T*)w.qrot, (const T*)a.dout, w.lse2, w.delta, a.cos, a.sin,
-            (T*)a.dk, (T*)a.dv, a.S, P, a.Hq, a.Hkv, n_rep, nkb, nkb * a.B * a.Hkv,
-            scale_log2, a.scale, a.causal, aux, w.ranges, w.dsb, order, kpm_flags);
+            (T*)a.dk, (T*)a.dv, a.S, P, a.Hq, a.Hkv, n_rep, nkb, nitems, scale_log2, a.scale,
+            a.causal, aux, w.ranges, w.dsb, order, kpm_flags, nsplit, dkp, dvp, part_stride);
+  if (nsplit > 1) reduce_parts(nsplit, dkp, dvp);
   KF_CHECK_LAUNCH();
   if (keep_ds) {
     const int rc = n_rep % 4 == 0   ? launch_dq_ds<T, D, 4>(a, w)

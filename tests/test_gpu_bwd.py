@@ -13,7 +13,7 @@ import torch
 
 import make_fixtures as mf
 from gpu_util import DEV, TOL, announce, check_grad, check_out, half_ulp, load_fixture, seeded
-from kempnerforge_amd import ops
+from kempnerforge_amd import _lib, ops
 from oracle import attention_ref as ref
 
 pytestmark = pytest.mark.gpu
@@ -138,7 +138,10 @@ def test_llama8b_shape_one_group():
     v = seeded((B, S, Hkv, D), 2, torch.bfloat16)
     do = seeded((B, S, Hq, D), 3, torch.bfloat16)
     cos, sin = ref.rope_tables(D, S, 5e5)
-    _, dq, dk, dv = _grads(q, k, v, do, cos, sin)
+    with _lib.KernelTimer() as kt:
+        _, dq, dk, dv = _grads(q, k, v, do, cos, sin)
+    # 1024 dK/dV items: the persistent grid needs no split of them
+    assert "dkdv_reduce" not in kt.stats, kt.stats
     _, dq2, dk2, dv2 = _grads(q, k, v, do, cos, sin)
     assert torch.equal(dq, dq2) and torch.equal(dk, dk2) and torch.equal(dv, dv2)
     b, g = 1, 6
@@ -148,6 +151,40 @@ def test_llama8b_shape_one_group():
     check_grad(dq[b:b + 1, :, hs], dq_r, torch.bfloat16, "C3 dq")
     check_grad(dk[b:b + 1, :, g:g + 1], dk_r, torch.bfloat16, "C3 dk")
     check_grad(dv[b:b + 1, :, g:g + 1], dv_r, torch.bfloat16, "C3 dv")
+
+
+# The reference's tensor-parallel rank shares (TP = 4, configs/train/*_tp4*.toml:
+# 70B B=2 Hq=16 Hkv=2, 29B B=1 Hq=12 Hkv=2, 13B B=4 Hq=10 Hkv=2) at shorter
+# lengths, and a one-KV-head case: too few dK/dV items for the persistent grid,
+# so each is split over the KV group's query heads (8, 6, 5 and 4 parts) and
+# dkdv_reduce adds the parts
+SPLIT_SHAPES = [
+    (2, 1024, 16, 2, 128),
+    (1, 1024, 12, 2, 128),
+    (4, 512, 10, 2, 128),
+    (1, 700, 4, 1, 64),
+]
+
+
+@pytest.mark.parametrize("cfg", SPLIT_SHAPES, ids=lambda c: "-".join(map(str, c)))
+def test_split_dkdv_items(cfg):
+    B, S, Hq, Hkv, D = cfg
+    announce(f"bwd split dK/dV items {cfg}")
+    q = seeded((B, S, Hq, D), 50, torch.bfloat16)
+    k = seeded((B, S, Hkv, D), 51, torch.bfloat16)
+    v = seeded((B, S, Hkv, D), 52, torch.bfloat16)
+    do = seeded((B, S, Hq, D), 53, torch.bfloat16)
+    cos, sin = ref.rope_tables(D, S, 5e5)
+    with _lib.KernelTimer() as kt:
+        _, dq, dk, dv = _grads(q, k, v, do, cos, sin)
+    assert "dkdv_reduce" in kt.stats, kt.stats
+    dq_r, dk_r, dv_r = ref.attention_bwd(q, k, v, cos, sin, do)
+    check_grad(dq, dq_r, torch.bfloat16, "dq")
+    check_grad(dk, dk_r, torch.bfloat16, "dk", group=Hq // Hkv)
+    check_grad(dv, dv_r, torch.bfloat16, "dv", group=Hq // Hkv)
+    # a second backward is bit-identical (the parts are added in a fixed order)
+    _, dq2, dk2, dv2 = _grads(q, k, v, do, cos, sin)
+    assert torch.equal(dq, dq2) and torch.equal(dk, dk2) and torch.equal(dv, dv2)
 
 
 def test_llama70b_shape_prefix_and_identities():
