@@ -534,14 +534,23 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(
   const int w = wave_id(), lane = threadIdx.x & 63;
   // persistent: one (key block, KV head) item per round; PART: an item is one
   // of nsplit parts of a key block, each with n_rep / nsplit of the group's
-  // query heads, the parts adjacent in the order (unmasked launches only)
+  // query heads (unmasked kernels only)
   const XcdItems xi = xcd_items(nitems);
   for (int rnd = 0;; ++rnd) {
+    // PART (the small-grid variant): the shares dealt longest first over all
+    // (KV head, part) groups of nkb key blocks
     int logical = xcd_item(xi, rnd);
     if (logical < 0) break;
-    // (wavefront-uniform; readfirstlane keeps the staging bases scalar)
-    const int part = PART ? __builtin_amdgcn_readfirstlane(logical % nsplit) : 0;
-    if (PART) logical = __builtin_amdgcn_readfirstlane(logical / nsplit);
+    if (PART) logical = dealt_order(logical, nitems, nkb);
+    // PART items are numbered (KV head, part, key block), key blocks fastest,
+    // so an XCD's contiguous share holds whole longest-first sweeps of key
+    // blocks (wavefront-uniform; readfirstlane keeps the staging bases scalar)
+    int part = 0;
+    if (PART) {
+      const int kbl = logical % nkb, t = logical / nkb;
+      part = __builtin_amdgcn_readfirstlane(t % nsplit);
+      logical = __builtin_amdgcn_readfirstlane((t / nsplit) * nkb + kbl);
+    }
     if (order != nullptr) {
       // items by descending work (the (batch row, key block) order, heads
       // adjacent), dealt round-robin over the XCDs
@@ -934,10 +943,10 @@ __global__ __launch_bounds__(64 * HB) void bwd_dq_ds_kernel(
   };
   __shared__ __attribute__((aligned(16))) Stage st[NBUF];
   const int w = wave_id(), lane = threadIdx.x & 63, hh = lane >> 5, c32 = lane & 31;
-  // item (KV head, head group, query tile): one XCD runs a contiguous range, a
-  // KV head's tiles longest-causal-row first
+  // item (KV head, head group, query tile), a KV head's tiles numbered
+  // longest-causal-row first, dealt to the XCDs by xcd_logical_id
   const int ngrp = n_rep / HB;
-  const int logical = xcd_logical_id(blockIdx.x, gridDim.x);
+  const int logical = xcd_logical_id(blockIdx.x, gridDim.x, nqt);
   const int qt = nqt - 1 - logical % nqt;
   const int hg = (logical / nqt) % ngrp, bh = logical / nqt / ngrp;
   const int b = bh / Hkv, g = bh % Hkv;
@@ -1130,7 +1139,7 @@ __global__ __launch_bounds__(512) void bwd_dq_ds2_kernel(
   const int w = wave_id(), lane = threadIdx.x & 63, hh = lane >> 5, c32 = lane & 31;
   const int hw = w % HB, tw = w / HB;
   const int npair = (nqt + 1) / 2, ngrp = n_rep / HB;
-  const int logical = xcd_logical_id(blockIdx.x, gridDim.x);
+  const int logical = xcd_logical_id(blockIdx.x, gridDim.x, npair);
   const int pp = npair - 1 - logical % npair;  // longest causal rows first
   const int hg = (logical / npair) % ngrp, bh = logical / npair / ngrp;
   const int b = bh / Hkv, g = bh % Hkv;
@@ -1361,10 +1370,18 @@ int dkdv_splits(int B, int S, int Hq, int Hkv) {
 
 size_t align256(size_t n) { return (n + 255) / 256 * 256; }
 
-// the split items' float32 dK and dV parts (none when unsplit)
+// Whether the unmasked dK/dV launch takes the small-grid variant (PART):
+// split items, or KV heads that do not fill the 8 XCDs in whole groups (its
+// shares are then dealt by lane_order).  It writes float32 parts that
+// dkdv_reduce_kernel adds (one part when unsplit).
+bool dkdv_small_grid(int B, int S, int Hq, int Hkv) {
+  return dkdv_splits(B, S, Hq, Hkv) > 1 || (B * Hkv) % 8 != 0;
+}
+
+// the small-grid variant's float32 dK and dV parts (none otherwise)
 size_t split_bytes(int B, int S, int Hq, int Hkv, int D) {
-  const int n = dkdv_splits(B, S, Hq, Hkv);
-  return n > 1 ? 2 * (size_t)n * B * Hkv * S * D * sizeof(float) : 0;
+  if (!dkdv_small_grid(B, S, Hq, Hkv)) return 0;
+  return 2 * (size_t)dkdv_splits(B, S, Hq, Hkv) * B * Hkv * S * D * sizeof(float);
 }
 
 // krot and qrot (unless the caller's rot holds them), lse2, delta, tile
@@ -1485,11 +1502,12 @@ int launch_bwd(const BwdArgs& a, void* workspace, bool keep_ds) {
   // causal key padding: the batch rows whose keys are all valid go to the
   // unmasked (persistent) kernel first, the rest to the KPM one
   const int* kpm_flags = mode == MASK_KPM && a.causal ? w.counts : nullptr;
-  // The unmasked (persistent) launches with few items split each item into
-  // nsplit parts and add them in dkdv_reduce (the same split for the key
-  // padding rows without padding as for an unmasked launch, so an all-True
-  // mask gives the unmasked result bit for bit)
+  // Small grids (dkdv_small_grid) take the unmasked kernel's PART variant,
+  // whose float32 parts dkdv_reduce adds; key padding's rows without padding
+  // take the same variant as an unmasked launch, so an all-True mask gives the
+  // unmasked result bit for bit
   const int64_t part_stride = (int64_t)a.B * a.Hkv * a.S * D;
+  const bool small = dkdv_small_grid(a.B, a.S, a.Hq, a.Hkv);
   auto reduce_parts = [&](int nsplit, float* dkp, float* dvp) {
     constexpr int TPR = D / 8 + D / 8;  // threads per row of dkdv_reduce_kernel
     const int64_t nrows = (int64_t)a.B * a.Hkv * a.S;
@@ -1502,11 +1520,11 @@ int launch_bwd(const BwdArgs& a, void* workspace, bool keep_ds) {
     const int rc = launch_kpm_row_flags(w.ranges, P / BN, a.S, a.B, w.counts, a.stream);
     if (rc) return rc;
     const int ns = dkdv_splits(a.B, a.S, a.Hq, a.Hkv);
-    float* dkp = ns > 1 ? w.dkvp : nullptr;
-    float* dvp = ns > 1 ? w.dkvp + ns * part_stride : nullptr;
+    float* dkp = small ? w.dkvp : nullptr;
+    float* dvp = small ? w.dkvp + ns * part_stride : nullptr;
     const int ni = nkb * a.B * a.Hkv * ns;
     KF_LAUNCH("bwd_dkdv",
-              (ns > 1 ? (keep_ds ? bwd_dkdv_kernel<T, D, MASK_NONE, true, true, true>
+              (small ? (keep_ds ? bwd_dkdv_kernel<T, D, MASK_NONE, true, true, true>
                                  : bwd_dkdv_kernel<T, D, MASK_NONE, false, true, true>)
                       : (keep_ds ? bwd_dkdv_kernel<T, D, MASK_NONE, true, true>
                                  : bwd_dkdv_kernel<T, D, MASK_NONE, false, true>)),
@@ -1515,18 +1533,19 @@ int launch_bwd(const BwdArgs& a, void* workspace, bool keep_ds) {
               a.cos, a.sin, (T*)a.dk, (T*)a.dv, a.S, P, a.Hq, a.Hkv, n_rep, nkb, ni, scale_log2,
               a.scale, a.causal, nullptr, w.ranges, w.dsb, nullptr, kpm_flags, ns, dkp, dvp,
               part_stride);
-    if (ns > 1) reduce_parts(ns, dkp, dvp);
+    if (small) reduce_parts(ns, dkp, dvp);
   }
   const int nsplit = mode == MASK_NONE ? dkdv_splits(a.B, a.S, a.Hq, a.Hkv) : 1;
-  float* dkp = nsplit > 1 ? w.dkvp : nullptr;
-  float* dvp = nsplit > 1 ? w.dkvp + nsplit * part_stride : nullptr;
+  const bool part = mode == MASK_NONE && small;
+  float* dkp = part ? w.dkvp : nullptr;
+  float* dvp = part ? w.dkvp + nsplit * part_stride : nullptr;
   const int nitems = nkb * a.B * a.Hkv * nsplit;
   KF_LAUNCH("bwd_dkdv",
             (mode == MASK_DOC   ? (keep_ds ? bwd_dkdv_kernel<T, D, MASK_DOC, true>
                                            : bwd_dkdv_kernel<T, D, MASK_DOC, false>)
              : mode == MASK_KPM ? (keep_ds ? bwd_dkdv_kernel<T, D, MASK_KPM, true>
                                            : bwd_dkdv_kernel<T, D, MASK_KPM, false>)
-             : nsplit > 1       ? (keep_ds ? bwd_dkdv_kernel<T, D, MASK_NONE, true, false, true>
+             : part             ? (keep_ds ? bwd_dkdv_kernel<T, D, MASK_NONE, true, false, true>
                                            : bwd_dkdv_kernel<T, D, MASK_NONE, false, false, true>)
              : keep_ds          ? bwd_dkdv_kernel<T, D, MASK_NONE, true>
                                 : bwd_dkdv_kernel<T, D, MASK_NONE, false>),
@@ -1534,7 +1553,7 @@ int launch_bwd(const BwdArgs& a, void* workspace, bool keep_ds) {
             (const T*)a.v, (const T*)w.qrot, (const T*)a.dout, w.lse2, w.delta, a.cos, a.sin,
             (T*)a.dk, (T*)a.dv, a.S, P, a.Hq, a.Hkv, n_rep, nkb, nitems, scale_log2, a.scale,
             a.causal, aux, w.ranges, w.dsb, order, kpm_flags, nsplit, dkp, dvp, part_stride);
-  if (nsplit > 1) reduce_parts(nsplit, dkp, dvp);
+  if (part) reduce_parts(nsplit, dkp, dvp);
   KF_CHECK_LAUNCH();
   if (keep_ds) {
     const int rc = n_rep % 4 == 0   ? launch_dq_ds<T, D, 4>(a, w)

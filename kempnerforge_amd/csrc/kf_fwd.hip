@@ -225,7 +225,7 @@ __global__ __launch_bounds__(256, 2) void fwd_mfma_kernel(
   __shared__ int sCount, sFirst;
 
   const int tid = threadIdx.x, w = wave_id(), lane = tid & 63, hh = lane >> 5, c32 = lane & 31;
-  int logical = xcd_logical_id(blockIdx.x, gridDim.x);
+  int logical = xcd_logical_id(blockIdx.x, gridDim.x, nqb);
   if (order != nullptr) {
     // DOC: the workgroup of rank r takes the (batch row, query block) of the
     // r-th most listed key tiles, its KV heads adjacent (longest first, each
@@ -495,7 +495,7 @@ __global__ __launch_bounds__(256, 3) void fwd32_kernel(
   __shared__ __attribute__((aligned(16))) T sV[2][D * FBN];
 
   const int tid = threadIdx.x, w = wave_id(), lane = tid & 63, hh = lane >> 5, c32 = lane & 31;
-  const int logical = xcd_logical_id(blockIdx.x, gridDim.x);
+  const int logical = xcd_logical_id(blockIdx.x, gridDim.x, nqb);
   const RowInfo ri = row_info(logical, nqb, Hkv, n_rep, bm_pos, Sq, w * 32 + c32);
   // key padding (kpm_flags per batch row, 1 = every key valid): only the rows
   // without padding (plain causal attention); fwd_mfma_kernel takes the others
@@ -703,7 +703,7 @@ __global__ __launch_bounds__(256, 2) void capture_probs_mfma_kernel(
   // even wave (one block per workgroup leaves the long blocks' CUs busy long
   // after the short ones' have drained)
   const int npair = (nqb + 1) / 2;
-  const int pl = xcd_logical_id(blockIdx.x, gridDim.x);
+  const int pl = xcd_logical_id(blockIdx.x, gridDim.x, npair);
   const int bhq = pl / npair, pr = pl % npair;
   const int nb = 2 * pr + 1 == nqb ? 1 : 2;
   for (int kb = 0; kb < nb; ++kb) {

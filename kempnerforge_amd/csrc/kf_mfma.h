@@ -13,17 +13,45 @@ constexpr int ROWS = 128;  // (query head, position) rows per workgroup
 
 __device__ __forceinline__ bf16x8 as_bf16x8(const u32x4& u) { return __builtin_bit_cast(bf16x8, u); }
 
-// Block-id remap so that the workgroups one XCD runs are a contiguous range of
-// logical ids (the dispatcher deals ids round-robin over the 8 XCDs): blocks of
-// one KV head then share that XCD's L2.
-__device__ __forceinline__ int xcd_logical_id(int L, int nblk) {
+// Block-id remap for grids of nblk = nb * G blocks, G per group (the blocks of
+// one KV head, numbered longest causal rows first).  The dispatcher deals
+// block ids round-robin over the 8 XCDs, each XCD running its share in id
+// order.  With nb a multiple of 8, XCD x takes a contiguous range of logical
+// ids, whole groups, so the blocks of one KV head share that XCD's L2.  With
+// fewer groups a contiguous range would be a group's longest (or shortest)
+// blocks, and the XCDs' shares would differ up to threefold: then each group
+// is dealt to s = 8 / gcd(nb, 8) XCDs, XCD j of them taking the group's
+// blocks j, j + s, j + 2s, ... (still longest first), so the shares balance
+// and an XCD still touches few groups.
+//
+// lane_order(c, n, G) is that deal for a position c of the contiguous
+// per-XCD order (used as is by the persistent kernels' shares, xcd_items).
+__host__ __device__ __forceinline__ int lane_order(int c, int nblk, int G) {
+  const int nb = nblk / G;
+  const int s = 8 >> min(__builtin_ctz((unsigned)nb | 8u), 3);  // 8 / gcd(nb, 8)
+  if (s == 1) return c;
+  // c runs over the groups' lanes in order: lane j of group b holds its blocks
+  // j, j + s, ... (q or q + 1 of them, the first m lanes one more)
+  const int b = c / G, r = c % G, q = G / s, m = G % s;
+  int j, t;
+  if (r < m * (q + 1)) {
+    j = r / (q + 1);
+    t = r % (q + 1);
+  } else {
+    j = m + (r - m * (q + 1)) / q;
+    t = (r - m * (q + 1)) % q;
+  }
+  return b * G + j + t * s;
+}
+__host__ __device__ __forceinline__ int xcd_logical_id(int L, int nblk, int G) {
   const int per = nblk / 8, rem = nblk % 8;
   const int xcd = L % 8, idx = L / 8;
-  return xcd * per + min(xcd, rem) + idx;
+  return lane_order(xcd * per + min(xcd, rem) + idx, nblk, G);  // contiguous per XCD, dealt
 }
 
-// Persistent schedule over nitems work items, numbered as xcd_logical_id numbers
-// workgroups (XCD x owns a contiguous range of them).  With G workgroups per
+// Persistent schedule over nitems work items: XCD x owns a contiguous range
+// of positions (the unmasked kernels pass them through lane_order, as
+// xcd_logical_id does for one-item-per-workgroup grids).  With G workgroups per
 // XCD (grid = 8G, or grid = nitems for one item each), round r gives the
 // workgroup of in-XCD index wi the item r*G + wi of its XCD's range in even
 // rounds and r*G + G-1-wi in odd ones: with items ordered longest first, each
@@ -40,6 +68,19 @@ __device__ __forceinline__ XcdItems xcd_items(int nitems) {
 __device__ __forceinline__ int xcd_item(const XcdItems& x, int r) {
   const int j = r * x.G + ((r & 1) ? x.G - 1 - x.wi : x.wi);
   return j < x.cnt ? x.lo + j : -1;
+}
+// Position c of the contiguous per-XCD order (xcd_item) to an item numbered
+// group * L + rank (n / L groups of L items, rank 0 the longest), dealt
+// longest first over all groups: position j of XCD x is entry 8 j + x of the
+// list ordered by (rank, group), so every XCD's share is sorted longest first
+// and holds every rank of every group about equally (for grids whose groups
+// do not fill the XCDs evenly; the plain contiguous shares keep a group's
+// items on one XCD's L2).
+__host__ __device__ __forceinline__ int dealt_order(int c, int n, int L) {
+  const int per = n / 8, rem = n % 8;
+  const int x = c < rem * (per + 1) ? c / (per + 1) : rem + (c - rem * (per + 1)) / per;
+  const int i = 8 * (c - x * per - min(x, rem)) + x, ng = n / L;
+  return (i % ng) * L + i / ng;
 }
 
 struct RowInfo {
