@@ -10,7 +10,8 @@ with P = B*Hq*S*(S+1)/2 causal (query, key) pairs (forward 4*D*P, backward
 Also reported: per-kernel HIP-event timings (the library brackets each launch
 on its own stream), the roofline of the dominant kernel, the forward alone
 (C2), the C3 step on packed documents (C3-doc; flops of same-document pairs
-only), with an all-True key_padding_mask (C3-kpm) and in float16 (C3-fp16), the
+only), with an all-True key_padding_mask (C3-kpm) and in float16 (C3-fp16), one
+rank's share of the reference's TP = 4 training configs at S = 4096, the
 Llama-3-70B shape fwd+bwd (C5: B=1, S=16384, 64 query heads) and its
 2048-token probability capture (C5-cap), the KV-cache decode configuration C4
 in GB/s, and the reference's PyTorch paths timed on the host CPU (C3 sample,
@@ -49,6 +50,11 @@ SHORT_WARM, SHORT_STEPS = 50, 200  # minimum warm-up / timed calls of the sub-ms
 C3 = dict(B=4, S=4096, Hq=32, Hkv=8, D=128, theta=500000.0)
 C4 = dict(B=32, Hq=32, Hkv=8, D=128, lo=1024, hi=8192, theta=500000.0)
 C5 = dict(B=1, S=16384, Hq=64, Hkv=8, D=128, theta=500000.0, cap_tokens=2048)
+# one rank's share of the reference's tensor-parallel training configs (TP = 4:
+# query and KV heads divided by 4; configs/train/70b_32gpu_tp4.toml,
+# 29b_32gpu_tp4_pp2.toml, 13b_32gpu_tp4_pp2.toml, 7b_12gpu_tp4.toml)
+TP4_SHARES = {"70b": dict(B=2, Hq=16, Hkv=2), "29b": dict(B=1, Hq=12, Hkv=2),
+              "13b": dict(B=4, Hq=10, Hkv=2), "7b": dict(B=4, Hq=8, Hkv=2)}
 
 # what bounds each kernel (the roofline its "achieved" figure is quoted on)
 BOUND = {"fwd_mfma": "mfma", "bwd_dkdv": "mfma", "bwd_dq": "mfma", "bwd_dq_ds": "hbm",
@@ -124,6 +130,22 @@ class Workloads:
                               if t.is_floating_point() and t.dtype == self.bf16 else t
                               for t in self.c3_inputs())
         q, k, v, do, cos, sin = self._c3h
+        out = self.ops.attention(q, k, v, cos, sin, causal=True)
+        self.torch.autograd.grad(out, (q, k, v), do)
+
+    def tp4_step(self, name):
+        # C3's length and head_dim on one rank's share of a TP = 4 config
+        if getattr(self, "_tp", (None,))[0] != name:
+            self._tp = None
+            sh, S, D = TP4_SHARES[name], C3["S"], C3["D"]
+            B, Hq, Hkv = sh["B"], sh["Hq"], sh["Hkv"]
+            q = seeded((B, S, Hq, D), 0, self.bf16, self.dev).requires_grad_(True)
+            k = seeded((B, S, Hkv, D), 1, self.bf16, self.dev).requires_grad_(True)
+            v = seeded((B, S, Hkv, D), 2, self.bf16, self.dev).requires_grad_(True)
+            do = seeded((B, S, Hq, D), 3, self.bf16, self.dev)
+            cos, sin = self.rope(D, S, C3["theta"])
+            self._tp = (name, q, k, v, do, cos.to(self.dev), sin.to(self.dev))
+        _, q, k, v, do, cos, sin = self._tp
         out = self.ops.attention(q, k, v, cos, sin, causal=True)
         self.torch.autograd.grad(out, (q, k, v), do)
 
@@ -408,6 +430,21 @@ def run_full(args, torch, wl):
               "kernels_us": {n: round(s["avg_us"], 1) for n, s in kh.items()}}
     wl._c3h = None
 
+    # one rank's share of the reference's TP = 4 training configs at S = 4096
+    tp4 = {}
+    for name, sh in TP4_SHARES.items():
+        step = lambda name=name: wl.tp4_step(name)  # noqa: E731
+        t_s = timed(torch, step, args.warmup, args.steps)
+        Pn = pairs(sh["B"], sh["Hq"], S)
+        tp4[name] = {"B": sh["B"], "Hq": sh["Hq"], "Hkv": sh["Hkv"], "ms": round(t_s * 1e3, 4),
+                     "TFLOP/s": round(14.0 * D * Pn / t_s / 1e12, 1)}
+        if name == "70b":
+            tp4[name]["kernels_us"] = {n: round(s_["avg_us"], 1)
+                                       for n, s_ in kernel_stats(torch, step, args.steps).items()}
+    wl._tp = None
+    tp4 = {"config": "fwd+bwd at S=4096, D=128 on one rank's heads of the reference's TP=4 "
+                     "training configs", **tp4}
+
     # C5 and C5-cap
     P5 = pairs(C5["B"], C5["Hq"], C5["S"])
     c5_s = timed(torch, wl.c5_step, 2, max(5, args.steps // 2))
@@ -480,6 +517,7 @@ def run_full(args, torch, wl):
         "c3_doc": c3doc,
         "c3_kpm": c3kpm,
         "c3_fp16": c3fp16,
+        "tp4_shares": tp4,
         "c5": c5,
         "c5_cap": c5cap,
         "decode": decode,
