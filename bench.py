@@ -18,7 +18,8 @@ in GB/s, and the reference's PyTorch paths timed on the host CPU (C3 sample,
 C4 decode, C5-cap capture) next to them.
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline]
-    python bench.py --only c3|c2|c3doc|c3kpm|c3fp16|c5|c5cap|c4 [--steps K] [--warmup W]
+    python bench.py --only c3|c2|c3doc|c3kpm|c3fp16|c5|c5cap|c4|tp4_70b|tp4_29b|tp4_13b|tp4_7b
+                    [--steps K] [--warmup W]
         one workload: W untimed steps, K timed steps, then K steps with the
         per-kernel event timing (the shape profiling runs use)
     python bench.py --rocprof-summary DIR [DIR ...] --warmup W --steps K
@@ -353,6 +354,7 @@ def run_only(args, torch, wl):
     """One workload: W untimed steps, K timed steps, K event-timed steps."""
     steps = {"c3": wl.c3_step, "c2": wl.c2_step, "c3doc": wl.c3doc_step,
              "c3kpm": wl.c3kpm_step, "c3fp16": wl.c3fp16_step, "c5": wl.c5_step,
+             **{f"tp4_{n}": (lambda n=n: wl.tp4_step(n)) for n in TP4_SHARES},
              "c5cap": wl.c5cap_step, "c4": wl.c4_step}
     fn = steps[args.only]
     secs = timed(torch, fn, args.warmup, args.steps)
@@ -531,7 +533,7 @@ def _short(name: str) -> str:
     """Kernel symbol -> the launcher's name (kf::..._kernel<...> -> ...)."""
     m = re.search(r"(kv_prep|fwd_mfma|fwd32|q_prep_bwd|bwd_dkdv|bwd_dq_ds|bwd_dq|decode_stream|"
                   r"decode_merge|capture_probs_mfma|kv_append|append|doc_block_tiles|"
-                  r"order_by_count|kpm_row_flags)_kernel", name)
+                  r"order_by_count|kpm_row_flags|dkdv_reduce)_kernel", name)
     if m:
         # fwd32_kernel is the unmasked forward's kernel, launched as fwd_mfma
         return {"capture_probs_mfma": "capture_probs", "append": "kv_append",
@@ -655,7 +657,7 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--only", choices=("c3", "c2", "c3doc", "c3kpm", "c3fp16", "c5", "c5cap",
-                                         "c4"))
+                                         "c4", *(f"tp4_{n}" for n in TP4_SHARES)))
     ap.add_argument("--rocprof-summary", nargs="+", metavar="DIR")
     ap.add_argument("--traffic-json", metavar="PATH",
                     help="with --rocprof-summary: write HBM bytes per launch per kernel")
