@@ -18,7 +18,7 @@ in GB/s, and the reference's PyTorch paths timed on the host CPU (C3 sample,
 C4 decode, C5-cap capture) next to them.
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline]
-    python bench.py --only c3|c2|c3doc|c3kpm|c3fp16|c5|c5cap|c4|tp4_70b|tp4_29b|tp4_13b|tp4_7b
+    python bench.py --only c3|c2|c3doc|c3kpm|c3fp16|c3fp32|c5|c5cap|c4|tp4_70b|tp4_29b|tp4_13b|tp4_7b
                     [--steps K] [--warmup W]
         one workload: W untimed steps, K timed steps, then K steps with the
         per-kernel event timing (the shape profiling runs use)
@@ -105,6 +105,7 @@ class Workloads:
         self.rope = precompute_rope_frequencies
         self.bf16 = torch.bfloat16
         self._c3 = self._c5 = self._c4 = self._doc = self._ones = self._c3h = None
+        self._c3f = None
 
     # C3 / C2 / C3-doc share the 8B-shape tensors
     def c3_inputs(self):
@@ -131,6 +132,17 @@ class Workloads:
                               if t.is_floating_point() and t.dtype == self.bf16 else t
                               for t in self.c3_inputs())
         q, k, v, do, cos, sin = self._c3h
+        out = self.ops.attention(q, k, v, cos, sin, causal=True)
+        self.torch.autograd.grad(out, (q, k, v), do)
+
+    def c3fp32_step(self):
+        # the C3 step in float32 (the reference's mixed_precision = "fp32"): the
+        # same seeded values, on the fp32 matrix-core kernels
+        if self._c3f is None:
+            self._c3f = tuple(t.detach().float().requires_grad_(t.requires_grad)
+                              if t.is_floating_point() and t.dtype == self.bf16 else t
+                              for t in self.c3_inputs())
+        q, k, v, do, cos, sin = self._c3f
         out = self.ops.attention(q, k, v, cos, sin, causal=True)
         self.torch.autograd.grad(out, (q, k, v), do)
 
@@ -353,7 +365,8 @@ def capture_bytes():
 def run_only(args, torch, wl):
     """One workload: W untimed steps, K timed steps, K event-timed steps."""
     steps = {"c3": wl.c3_step, "c2": wl.c2_step, "c3doc": wl.c3doc_step,
-             "c3kpm": wl.c3kpm_step, "c3fp16": wl.c3fp16_step, "c5": wl.c5_step,
+             "c3kpm": wl.c3kpm_step, "c3fp16": wl.c3fp16_step, "c3fp32": wl.c3fp32_step,
+             "c5": wl.c5_step,
              **{f"tp4_{n}": (lambda n=n: wl.tp4_step(n)) for n in TP4_SHARES},
              "c5cap": wl.c5cap_step, "c4": wl.c4_step}
     fn = steps[args.only]
@@ -431,6 +444,16 @@ def run_full(args, torch, wl):
               "vs_bf16_step": round(h_s * 1e3 / ms_step, 3),
               "kernels_us": {n: round(s["avg_us"], 1) for n, s in kh.items()}}
     wl._c3h = None
+
+    # C3-fp32: the C3 step on float32 inputs (mixed_precision = "fp32"), whose
+    # matrix-core peak is 157.3 TFLOP/s (dense fp32)
+    f_s = timed(torch, wl.c3fp32_step, 2, max(2, args.steps // 4))
+    kf = kernel_stats(torch, wl.c3fp32_step, max(2, args.steps // 4))
+    c3fp32 = {"config": "C3-fp32 C3 with float32 q/k/v/dO (the same seeded values)",
+              "ms": round(f_s * 1e3, 3), "TFLOP/s": round(flops_step / f_s / 1e12, 1),
+              "frac_of_fp32_peak": round(flops_step / f_s / 157.3e12, 3),
+              "kernels_us": {n: round(s["avg_us"], 1) for n, s in kf.items()}}
+    wl._c3f = None
 
     # one rank's share of the reference's TP = 4 training configs at S = 4096
     tp4 = {}
@@ -519,6 +542,7 @@ def run_full(args, torch, wl):
         "c3_doc": c3doc,
         "c3_kpm": c3kpm,
         "c3_fp16": c3fp16,
+        "c3_fp32": c3fp32,
         "tp4_shares": tp4,
         "c5": c5,
         "c5_cap": c5cap,
@@ -656,8 +680,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--only", choices=("c3", "c2", "c3doc", "c3kpm", "c3fp16", "c5", "c5cap",
-                                         "c4", *(f"tp4_{n}" for n in TP4_SHARES)))
+    ap.add_argument("--only", choices=("c3", "c2", "c3doc", "c3kpm", "c3fp16", "c3fp32", "c5",
+                                         "c5cap", "c4", *(f"tp4_{n}" for n in TP4_SHARES)))
     ap.add_argument("--rocprof-summary", nargs="+", metavar="DIR")
     ap.add_argument("--traffic-json", metavar="PATH",
                     help="with --rocprof-summary: write HBM bytes per launch per kernel")

@@ -71,7 +71,15 @@ static int check_masks(const int32_t* doc, const int32_t* kvalid, int causal, in
 }
 
 static size_t fwd_ws(const FwdArgs& a) {
-  return fwd_mfma_supported(a) ? fwd_mfma_workspace(a.B, a.Sk, a.Hkv, a.D) : 0;
+  if (fwd_mfma_supported(a)) return fwd_mfma_workspace(a.B, a.Sk, a.Hkv, a.D);
+  if (fwd_f32_supported(a)) return a.k_rotated ? 0 : fwd_f32_workspace(a.B, a.Sk, a.Hkv, a.D);
+  return 0;
+}
+
+static size_t bwd_ws(const BwdArgs& a) {
+  if (bwd_mfma_supported(a)) return bwd_mfma_workspace(a.B, a.S, a.Hq, a.Hkv, a.D);
+  if (bwd_f32_supported(a)) return bwd_f32_workspace(a.B, a.S, a.Hq, a.Hkv, a.D);
+  return bwd_generic_workspace(a.B, a.S, a.Hq);
 }
 
 }  // namespace kf
@@ -121,6 +129,14 @@ int kf_attn_fwd(const void* q, const void* k, const void* v, const float* rope_c
     }
     return fwd_mfma(a, workspace);
   }
+  if (fwd_f32_supported(a)) {
+    const size_t need = fwd_ws(a);
+    if (workspace_bytes < need || (need && !workspace)) {
+      set_error("workspace too small: need %zu bytes, got %zu", need, workspace_bytes);
+      return KF_ERR_WORKSPACE;
+    }
+    return fwd_f32(a, workspace);
+  }
   return fwd_generic(a);
 }
 
@@ -141,8 +157,7 @@ int kf_attn_bwd_workspace_size(int B, int S, int Hq, int Hkv, int D, int dtype, 
   if (rc) return rc;
   KF_CHECK_ARG(bytes != nullptr, "bytes is null");
   const BwdArgs a = sizing_args(B, S, Hq, Hkv, D, dtype, 1);
-  *bytes = bwd_mfma_supported(a) ? bwd_mfma_workspace(B, S, Hq, Hkv, D)
-                                 : bwd_generic_workspace(B, S, Hq);
+  *bytes = bwd_ws(a);
   return KF_OK;
 }
 
@@ -152,7 +167,7 @@ int kf_attn_bwd_workspace_size_ds(int B, int S, int Hq, int Hkv, int D, int dtyp
   if (rc) return rc;
   KF_CHECK_ARG(bytes != nullptr, "bytes is null");
   const BwdArgs a = sizing_args(B, S, Hq, Hkv, D, dtype, causal);
-  *bytes = bwd_mfma_supported(a) ? bwd_mfma_workspace_ds(a) : bwd_generic_workspace(B, S, Hq);
+  *bytes = bwd_mfma_supported(a) ? bwd_mfma_workspace_ds(a) : bwd_ws(a);
   return KF_OK;
 }
 
@@ -183,11 +198,12 @@ int kf_attn_bwd(const void* q, const void* k, const void* v, const float* rope_c
     }
     return bwd_mfma(a, workspace, workspace_bytes);
   }
-  const size_t need = bwd_generic_workspace(B, S, Hq);
+  const size_t need = bwd_ws(a);
   if (workspace_bytes < need || !workspace) {
     set_error("workspace too small: need %zu bytes, got %zu", need, workspace_bytes);
     return KF_ERR_WORKSPACE;
   }
+  if (bwd_f32_supported(a)) return bwd_f32(a, workspace);
   return bwd_generic(a, workspace);
 }
 

@@ -1,0 +1,707 @@
+// float32 attention on the fp32 matrix cores (v_mfma_f32_16x16x4_f32): the
+// forward, dQ and dK/dV of the reference's mixed_precision = "fp32"
+// (kempnerforge/config/training.py:31; attention at kempnerforge/model/
+// attention.py:228-231 then runs SDPA in float32), causal or full attention
+// without explicit masks, head_dim 64 or 128.  Nothing is rounded below
+// float32: the products are exact and the sums accumulate in float32, as the
+// reference's float32 SDPA does (the explicit masks and other head sizes stay
+// on the generic kernels).
+//
+// One MFMA multiplies a 16x4 A by a 4x16 B into a 16x16 C: lane l holds
+// A[l % 16][l / 16], B[l / 16][l % 16] and C[4 (l / 16) + r][l % 16] in its
+// register r = 0..3.  Each kernel orients its score tiles so that l % 16 runs
+// over the rows the kernel owns (query rows in the forward and dQ, key rows in
+// dK/dV): row statistics and accumulators stay in the lane, and a score tile's
+// C registers are the B operand of the next product as they are — MFMA kk of
+// that product contracts, in lane group g = l / 16, over row
+// 16 (kk / 4) + 4 g + kk % 4 of the C tile, which lane (g, l % 16) holds in
+// register kk % 4 of block kk / 4.
+//
+// The head dimension of a contraction over D is split over the four lane
+// groups so that a lane holds both halves of each RoPE pair: group g holds the
+// 16-byte chunks (D/32) g + j of the first half and the same chunks of the
+// second half (chunk_of), so the rows a lane loads itself rotate in registers.
+//
+// LDS tiles are [32 rows][D] floats with 16-byte chunk c of row r at position
+// c ^ (r % 16): the chunk reads (16 consecutive rows, one chunk per pass) and
+// the element reads (rows 4 apart, 16 consecutive floats each) both meet 64
+// distinct banks.  Tiles reach LDS by direct global->LDS loads one tile ahead,
+// into the other of two buffers, one barrier per tile; the tiles that need
+// RoPE (K, and Q in dK/dV) come from a prepass that writes the rotated rows.
+#include "kf_internal.h"
+#include "kf_mfma.h"
+
+namespace kf {
+
+namespace {
+
+using mfma::row_info;
+using mfma::RowInfo;
+using mfma::wave_id;
+using mfma::xcd_logical_id;
+
+constexpr int F_ROWS = 64;  // query rows per workgroup (forward, dQ): 4 wavefronts x 16
+constexpr int F_BN = 32;    // keys per tile (forward, dQ), query positions per tile (dK/dV)
+constexpr int F_BK = 64;    // keys per workgroup (dK/dV): 4 wavefronts x 16
+
+__device__ __forceinline__ f32x4 mma(float a, float b, const f32x4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// j-th 16-byte chunk (j < D/16) of lane group g's share of a D-float row
+template <int D>
+__device__ __forceinline__ int chunk_of(int j, int g) {
+  constexpr int H = D / 32;
+  return j < H ? H * g + j : D / 8 + H * g + (j - H);
+}
+// float index of chunk c of row r of an LDS tile
+template <int D>
+__device__ __forceinline__ int tix(int r, int c) {
+  return (r * (D / 4) + (c ^ (r & 15))) * 4;
+}
+// element (r, d) of an LDS tile
+template <int D>
+__device__ __forceinline__ float tel(const float* t, int r, int d) {
+  return t[tix<D>(r, d >> 2) + (d & 3)];
+}
+
+// over the four lanes l % 16 + 16 g of one row
+__device__ __forceinline__ float quad_max(float x) {
+  x = fmaxf(x, __shfl_xor(x, 16, 64));
+  return fmaxf(x, __shfl_xor(x, 32, 64));
+}
+__device__ __forceinline__ float quad_sum(float x) {
+  x += __shfl_xor(x, 16, 64);
+  return x + __shfl_xor(x, 32, 64);
+}
+
+__device__ __forceinline__ void rope4(f32x4& x1, f32x4& x2, const f32x4& c, const f32x4& s) {
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    float r1, r2;
+    rope_pair<float>(x1[e], x2[e], c[e], s[e], r1, r2);
+    x1[e] = r1;
+    x2[e] = r2;
+  }
+}
+
+__device__ __forceinline__ f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
+
+typedef double f64x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ f64x4 to_f64(const f32x4& x) {
+  return f64x4{(double)x[0], (double)x[1], (double)x[2], (double)x[3]};
+}
+__device__ __forceinline__ f32x4 to_f32x4(const f64x4& x) {
+  return f32x4{(float)x[0], (float)x[1], (float)x[2], (float)x[3]};
+}
+
+// [32 rows][D] floats, rows `ld` floats apart from the wavefront-uniform base
+// g, into a swizzled LDS tile by direct global->LDS loads: each instruction
+// moves 64 lanes x 16 bytes into 1 KB of contiguous LDS, so a lane loads the
+// chunk that belongs at its LDS position; the 4 wavefronts split the
+// instructions.  Rows at or past rows_valid repeat row rows_valid - 1 (finite
+// values, which the callers' masks multiply by zero).  Completion: the
+// caller's lds_copy_wait and barrier.
+template <int D>
+__device__ __forceinline__ void tile_dma(const float* g, uint32_t ld, float* lds, int w, int lane,
+                                         int rows_valid) {
+  constexpr int R = D / 4, PER = F_BN * R / 64 / 4;
+  asm volatile("" : "+v"(lane));  // offsets recomputed per call, not kept live across the loop
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const int L = (w * PER + j) * 64 + lane, row = L / R, pc = L % R;
+    const uint32_t off =
+        ((uint32_t)min(row, rows_valid - 1) * ld + (uint32_t)(pc ^ (row & 15)) * 4u) * 4u;
+    mfma::dma16(mfma::lds_addr(lds + (w * PER + j) * 256), off, g);
+  }
+}
+
+// A row's D/16 chunks of lane group g (chunk_of order), RoPE'd at table row
+// `pos` when rot; zero when !valid.
+template <int D>
+__device__ __forceinline__ void load_row_share(const float* __restrict__ row,
+                                               const float* __restrict__ cos,
+                                               const float* __restrict__ sin, int pos, int g,
+                                               bool valid, bool rot, f32x4* x) {
+  constexpr int NJ = D / 16;
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) x[j] = valid ? *(const f32x4*)(row + 4 * chunk_of<D>(j, g)) : zero4();
+  if (valid && rot) {
+#pragma unroll
+    for (int j = 0; j < NJ / 2; ++j) {
+      const int64_t o = (int64_t)pos * (D / 2) + 4 * chunk_of<D>(j, g);
+      rope4(x[j], x[j + NJ / 2], *(const f32x4*)(cos + o), *(const f32x4*)(sin + o));
+    }
+  }
+}
+
+// C[16 x 16] (+)= tile rows r0..r0+15 (A, chunk reads) times the lane's row
+// share x (B): the transposed score tile of one 16-row block.
+template <int D>
+__device__ __forceinline__ void scores2(const float* tile, const f32x4* x, int c16, int g,
+                                        f32x4& s0, f32x4& s1) {
+  constexpr int NJ = D / 16;
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const int c = chunk_of<D>(j, g);
+    const f32x4 a0 = *(const f32x4*)(tile + tix<D>(c16, c));
+    const f32x4 a1 = *(const f32x4*)(tile + tix<D>(16 + c16, c));
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      s0 = mma(a0[e], x[j][e], s0);
+      s1 = mma(a1[e], x[j][e], s1);
+    }
+  }
+}
+
+// acc[db] = alpha acc[db] + tile^T p: the [D x 16] product of a tile's
+// columns with a 32 x 16 score tile held as p0 (rows 0-15) and p1 (rows
+// 16-31), in the C tile's contraction order.  Each 16-column block's 8
+// products go into a fresh accumulator that is added once, so a running sum
+// is rounded once per tile rather than once per MFMA (its float32 error over
+// thousands of positions stays at the reference's own order); two blocks
+// interleave so that consecutive MFMAs are independent.
+template <int D>
+__device__ __forceinline__ void accum_t(const float* tile, const f32x4& p0, const f32x4& p1,
+                                        int c16, int g, f32x4* acc, float alpha = 1.f) {
+  constexpr int NB = D / 16;
+#pragma unroll
+  for (int db = 0; db < NB; db += 2) {
+    f32x4 f0 = zero4(), f1 = zero4();
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) {
+      const int row = 16 * (kk >> 2) + 4 * g + (kk & 3);
+      const float b = kk < 4 ? p0[kk & 3] : p1[kk & 3];
+      f0 = mma(tel<D>(tile, row, 16 * db + c16), b, f0);
+      f1 = mma(tel<D>(tile, row, 16 * (db + 1) + c16), b, f1);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      acc[db][r] = __builtin_fmaf(acc[db][r], alpha, f0[r]);
+      acc[db + 1][r] = __builtin_fmaf(acc[db + 1][r], alpha, f1[r]);
+    }
+  }
+}
+
+// accum_t of two products at once, ta^T pa into a and tb^T pb into b (the
+// dK/dV kernel's dV and dK), their chains interleaved.
+template <int D>
+__device__ __forceinline__ void accum_t2(const float* ta, const f32x4& pa0, const f32x4& pa1,
+                                         f32x4* a, const float* tb, const f32x4& pb0,
+                                         const f32x4& pb1, f32x4* b, int c16, int g) {
+  constexpr int NB = D / 16;
+#pragma unroll
+  for (int db = 0; db < NB; ++db) {
+    f32x4 fa = zero4(), fb = zero4();
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) {
+      const int row = 16 * (kk >> 2) + 4 * g + (kk & 3);
+      fa = mma(tel<D>(ta, row, 16 * db + c16), kk < 4 ? pa0[kk & 3] : pa1[kk & 3], fa);
+      fb = mma(tel<D>(tb, row, 16 * db + c16), kk < 4 ? pb0[kk & 3] : pb1[kk & 3], fb);
+    }
+    a[db] += fa;
+    b[db] += fb;
+    __builtin_amdgcn_sched_barrier(0);  // the next block's reads stay behind this block's products
+  }
+}
+
+// ------------------------------------------------------------------ prepass
+// dst[(b H + h) Sp + s][D] = src[b, s, h, :] after RoPE at table row s (rot)
+// or as is; rows s in [S, Sp) zero.  One thread per chunk pair.
+template <int D>
+__global__ __launch_bounds__(256) void rows_f32_kernel(const float* __restrict__ src, int64_t sb,
+                                                       int64_t ss, int64_t sh,
+                                                       const float* __restrict__ cos,
+                                                       const float* __restrict__ sin,
+                                                       float* __restrict__ dst, int S, int Sp,
+                                                       int H, int rot, int64_t pairs) {
+  const int64_t p = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (p >= pairs) return;
+  const int c = (int)(p % (D / 8));
+  const int64_t rowi = p / (D / 8);
+  const int s = (int)(rowi % Sp);
+  const int64_t bh = rowi / Sp;
+  const int h = (int)(bh % H);
+  const int64_t b = bh / H;
+  f32x4 x1 = zero4(), x2 = zero4();
+  if (s < S) {
+    const float* row = src + b * sb + (int64_t)s * ss + (int64_t)h * sh;
+    x1 = *(const f32x4*)(row + 4 * c);
+    x2 = *(const f32x4*)(row + D / 2 + 4 * c);
+    if (rot) {
+      const int64_t o = (int64_t)s * (D / 2) + 4 * c;
+      rope4(x1, x2, *(const f32x4*)(cos + o), *(const f32x4*)(sin + o));
+    }
+  }
+  *(f32x4*)(dst + rowi * D + 4 * c) = x1;
+  *(f32x4*)(dst + rowi * D + D / 2 + 4 * c) = x2;
+}
+
+// Per query row (b, h, i), i < Sp: -lse log2(e) and Delta = sum_d dO O, in
+// 64-float groups per 32 positions ([B Hq][Sp/32][nl x 32, Delta x 32]);
+// rows past S get -inf and 0 (probability zero).  16 lanes per row.
+template <int D>
+__global__ __launch_bounds__(256) void stats_f32_kernel(const float* __restrict__ o,
+                                                        const float* __restrict__ dout,
+                                                        const float* __restrict__ lse,
+                                                        float* __restrict__ stats, int S, int Sp,
+                                                        int Hq, int64_t rows) {
+  const int64_t row = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);  // (b Hq + h) Sp + i
+  const int l = threadIdx.x & 15;
+  const int i = (int)(row % Sp);
+  const int64_t bh = row / Sp;
+  const bool valid = row < rows && i < S;
+  float s = 0.f;
+  if (valid) {
+    const int64_t off = ((bh / Hq * S + i) * Hq + bh % Hq) * D;
+#pragma unroll
+    for (int c = l; c < D / 4; c += 16) {
+      const f32x4 a = *(const f32x4*)(o + off + 4 * c);
+      const f32x4 b = *(const f32x4*)(dout + off + 4 * c);
+      s += a[0] * b[0] + a[1] * b[1] + a[2] * b[2] + a[3] * b[3];
+    }
+  }
+#pragma unroll
+  for (int x = 8; x >= 1; x >>= 1) s += __shfl_xor(s, x, 16);
+  if (row < rows && l == 0) {
+    float* grp = stats + (bh * (Sp / F_BN) + i / F_BN) * (2 * F_BN) + i % F_BN;
+    grp[0] = valid ? -lse[bh * S + i] * kLog2e : -INFINITY;
+    grp[F_BN] = valid ? s : 0.f;
+  }
+}
+
+// ------------------------------------------------------------------ forward
+// Workgroup: 4 wavefronts x 16 (head, position) rows of one KV group (the
+// rows of all its query heads share each K/V tile); S^T = K·Q^T per 32-key
+// tile, online softmax in the lane, O^T += V^T·P^T.  K comes rotated: element
+// (b, g, key, d) at kt + b kb_b + g kb_h + key kld + d (the prepass's rows or
+// a rotated cache).
+template <int D>
+__global__ __launch_bounds__(256, 2) void fwd_f32_kernel(
+    const float* __restrict__ q, const float* __restrict__ cos, const float* __restrict__ sin,
+    const float* kt, int64_t kb_b, int64_t kb_h, int kld, const float* v, int64_t vsb,
+    int64_t vsh, int vss, float* __restrict__ out, float* __restrict__ lse, int Sq, int Sk,
+    int Hq, int Hkv, int n_rep, int bm_pos, int nqb, int causal, float scale_log2) {
+  constexpr int NJ = D / 16, NB = D / 16;
+  __shared__ __attribute__((aligned(16))) float sK[2][F_BN * D];
+  __shared__ __attribute__((aligned(16))) float sV[2][F_BN * D];
+
+  const int lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15, w = wave_id();
+  const int logical = xcd_logical_id(blockIdx.x, gridDim.x, nqb);
+  const RowInfo ri = row_info(logical, nqb, Hkv, n_rep, bm_pos, Sq, w * 16 + c16);
+  const int kend = causal ? min(Sk, min(ri.p0 + bm_pos, Sq)) : Sk;
+  const int ntiles = (kend + F_BN - 1) / F_BN;
+  const float* kb = kt + (int64_t)ri.b * kb_b + (int64_t)ri.g * kb_h;
+  const float* vb = v + (int64_t)ri.b * vsb + (int64_t)ri.g * vsh;
+  auto stage = [&](int t, int buf) {
+    const int k0 = t * F_BN;
+    tile_dma<D>(kb + (int64_t)k0 * kld, (uint32_t)kld, sK[buf], w, lane, Sk - k0);
+    tile_dma<D>(vb + (int64_t)k0 * vss, (uint32_t)vss, sV[buf], w, lane, Sk - k0);
+  };
+  if (ntiles > 0) stage(0, 0);
+
+  f32x4 qr[NJ];
+  load_row_share<D>(q + (((int64_t)ri.b * Sq + ri.pos) * Hq + ri.hq) * D, cos, sin, ri.pos, g,
+                    ri.q_valid, true, qr);
+
+  float m = -INFINITY, l = 0.f;
+  f32x4 o[NB];
+#pragma unroll
+  for (int db = 0; db < NB; ++db) o[db] = zero4();
+  mfma::lds_copy_wait();
+  __syncthreads();
+
+  for (int t = 0; t < ntiles; ++t) {
+    const int buf = t & 1;
+    if (t + 1 < ntiles) stage(t + 1, buf ^ 1);
+    const float* tK = sK[buf];
+    const float* tV = sV[buf];
+    f32x4 s0 = zero4(), s1 = zero4();
+    scores2<D>(tK, qr, c16, g, s0, s1);
+
+    const int k0 = t * F_BN;
+    if ((causal && k0 + F_BN - 1 > ri.p0) || k0 + F_BN > Sk) {
+      const int lim = (causal ? min(ri.pos, Sk - 1) : Sk - 1) - k0;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        s0[r] = 4 * g + r > lim ? -INFINITY : s0[r];
+        s1[r] = 16 + 4 * g + r > lim ? -INFINITY : s1[r];
+      }
+    }
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) tmax = fmaxf(tmax, fmaxf(s0[r], s1[r]));
+    tmax = quad_max(tmax) * scale_log2;
+    const float mnew = fmaxf(m, tmax);
+    const float alpha = fast_exp2(m - mnew);
+    m = mnew;
+    l *= alpha;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      s0[r] = fast_exp2(__builtin_fmaf(s0[r], scale_log2, -m));
+      s1[r] = fast_exp2(__builtin_fmaf(s1[r], scale_log2, -m));
+      l += s0[r] + s1[r];
+    }
+    accum_t<D>(tV, s0, s1, c16, g, o, alpha);
+    mfma::lds_copy_wait();
+    __syncthreads();
+  }
+
+  const float lt = quad_sum(l);
+  if (ri.q_valid) {
+    const float inv = 1.f / lt;
+    float* orow = out + (((int64_t)ri.b * Sq + ri.pos) * Hq + ri.hq) * D;
+#pragma unroll
+    for (int db = 0; db < NB; ++db) *(f32x4*)(orow + 16 * db + 4 * g) = o[db] * inv;
+    if (lse != nullptr && g == 0)
+      lse[((int64_t)ri.b * Hq + ri.hq) * Sq + ri.pos] = (m + log2f(lt)) * kLn2;
+  }
+}
+
+// ------------------------------------------------------------------ backward
+// Store a lane's share (d = 16 db + 4 g + r) of scale * G^T after the RoPE
+// backward at table row pos (the pair of d < D/2 is d + D/2, in block db + NB/2).
+template <int D>
+__device__ __forceinline__ void store_grad_rope(float* __restrict__ row, const f32x4* acc,
+                                                const float* __restrict__ cos,
+                                                const float* __restrict__ sin, int pos, int g,
+                                                float scale) {
+  constexpr int NB = D / 16;
+#pragma unroll
+  for (int db = 0; db < NB / 2; ++db) {
+    const int d = 16 * db + 4 * g;
+    const f32x4 c = *(const f32x4*)(cos + (int64_t)pos * (D / 2) + d);
+    const f32x4 s = *(const f32x4*)(sin + (int64_t)pos * (D / 2) + d);
+    f32x4 lo, hi;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float d1, d2;
+      rope_pair_bwd<float>(acc[db][r] * scale, acc[db + NB / 2][r] * scale, c[r], s[r], d1, d2);
+      lo[r] = d1;
+      hi[r] = d2;
+    }
+    *(f32x4*)(row + d) = lo;
+    *(f32x4*)(row + D / 2 + d) = hi;
+  }
+}
+
+// dQ: the forward's rows and tiles; per 32-key tile S^T = K·Q^T and
+// dP^T = V·dO^T, dS^T = P^T (dP^T - Delta), dQ^T += K^T·dS^T.  qr / kr: the
+// prepass's rotated rows, Sp per head.
+template <int D>
+__global__ __launch_bounds__(256, 2) void bwd_dq_f32_kernel(
+    const float* __restrict__ qr_rows, const float* kr_rows, const float* v,
+    const float* __restrict__ cos, const float* __restrict__ sin, const float* __restrict__ dout,
+    const float* __restrict__ stats, float* __restrict__ dq, int S, int Sp, int Hq, int Hkv,
+    int n_rep, int bm_pos, int nqb, int causal, float scale, float scale_log2) {
+  constexpr int NJ = D / 16, NB = D / 16;
+  __shared__ __attribute__((aligned(16))) float sK[2][F_BN * D];
+  __shared__ __attribute__((aligned(16))) float sV[2][F_BN * D];
+
+  const int lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15, w = wave_id();
+  const int logical = xcd_logical_id(blockIdx.x, gridDim.x, nqb);
+  const RowInfo ri = row_info(logical, nqb, Hkv, n_rep, bm_pos, S, w * 16 + c16);
+  const int kend = causal ? min(S, ri.p0 + bm_pos) : S;
+  const int ntiles = (kend + F_BN - 1) / F_BN;
+  const float* kb = kr_rows + ((int64_t)ri.b * Hkv + ri.g) * Sp * D;
+  const float* vb = v + ((int64_t)ri.b * S * Hkv + ri.g) * D;
+  const int vss = Hkv * D;
+  auto stage = [&](int t, int buf) {
+    const int k0 = t * F_BN;
+    tile_dma<D>(kb + (int64_t)k0 * D, (uint32_t)D, sK[buf], w, lane, S - k0);
+    tile_dma<D>(vb + (int64_t)k0 * vss, (uint32_t)vss, sV[buf], w, lane, S - k0);
+  };
+  if (ntiles > 0) stage(0, 0);
+
+  const int64_t hrow = (int64_t)ri.b * Hq + ri.hq;
+  const int64_t roff = ((int64_t)ri.b * S + ri.pos) * Hq + ri.hq;
+  f32x4 qr[NJ], dr[NJ];
+  load_row_share<D>(qr_rows + (hrow * Sp + ri.pos) * D, cos, sin, ri.pos, g, ri.q_valid, false, qr);
+  load_row_share<D>(dout + roff * D, cos, sin, ri.pos, g, ri.q_valid, false, dr);
+  const float* st = stats + (hrow * (Sp / F_BN) + ri.pos / F_BN) * (2 * F_BN) + ri.pos % F_BN;
+  const float nl = ri.q_valid ? st[0] : 0.f;
+  const float dl = ri.q_valid ? st[F_BN] : 0.f;
+
+  f32x4 acc[NB];
+#pragma unroll
+  for (int db = 0; db < NB; ++db) acc[db] = zero4();
+  mfma::lds_copy_wait();
+  __syncthreads();
+
+  for (int t = 0; t < ntiles; ++t) {
+    const int buf = t & 1;
+    if (t + 1 < ntiles) stage(t + 1, buf ^ 1);
+    const float* tK = sK[buf];
+    const float* tV = sV[buf];
+    f32x4 s0 = zero4(), s1 = zero4(), d0 = zero4(), d1 = zero4();
+    scores2<D>(tK, qr, c16, g, s0, s1);
+    scores2<D>(tV, dr, c16, g, d0, d1);
+    const int k0 = t * F_BN;
+    const bool edge = (causal && k0 + F_BN - 1 > ri.p0) || k0 + F_BN > S;
+    const int lim = (causal ? min(ri.pos, S - 1) : S - 1) - k0;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float p0 = fast_exp2(__builtin_fmaf(s0[r], scale_log2, nl));
+      float p1 = fast_exp2(__builtin_fmaf(s1[r], scale_log2, nl));
+      if (edge) {
+        p0 = 4 * g + r > lim ? 0.f : p0;
+        p1 = 16 + 4 * g + r > lim ? 0.f : p1;
+      }
+      s0[r] = p0 * (d0[r] - dl);
+      s1[r] = p1 * (d1[r] - dl);
+    }
+    accum_t<D>(tK, s0, s1, c16, g, acc);
+    mfma::lds_copy_wait();
+    __syncthreads();
+  }
+  if (ri.q_valid) store_grad_rope<D>(dq + roff * D, acc, cos, sin, ri.pos, g, scale);
+}
+
+// dK/dV: a workgroup owns 64 keys of one KV head (16 per wavefront, one per
+// lane column), their rotated K and V rows in registers, and walks every
+// query head of the group over the query tiles from the keys' diagonal on:
+// S = Q·K^T and dP = dO·V^T per 32-position tile, then dV^T += dO^T·P and
+// dK^T += Q^T·dS.  Key blocks are numbered longest first.
+template <int D>
+__global__ __launch_bounds__(256, 2) void bwd_dkdv_f32_kernel(
+    const float* qr_rows, const float* __restrict__ kr_rows, const float* __restrict__ v,
+    const float* __restrict__ cos, const float* __restrict__ sin, const float* dout,
+    const float* stats, double* __restrict__ sum64, float* __restrict__ dk,
+    float* __restrict__ dv, int S, int Sp, int Hq, int Hkv, int n_rep, int causal, float scale,
+    float scale_log2) {
+  constexpr int NJ = D / 16, NB = D / 16;
+  __shared__ __attribute__((aligned(16))) float sQ[2][F_BN * D];
+  __shared__ __attribute__((aligned(16))) float sO[2][F_BN * D];
+  __shared__ __attribute__((aligned(16))) float sS[2][2 * F_BN];  // -lse log2(e), Delta
+
+  const int lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15, w = wave_id();
+  const int BH = gridDim.x / ((S + F_BK - 1) / F_BK);
+  const int kblk = blockIdx.x / BH, bh = blockIdx.x % BH;
+  const int b = bh / Hkv, hk = bh % Hkv;
+  const int k0 = kblk * F_BK;
+  const int key = k0 + 16 * w + c16;
+  const bool kvalid = key < S;
+
+  const int nt = (S + F_BN - 1) / F_BN, t0 = causal ? k0 / F_BN : 0;
+  const int per = nt - t0, total = per * n_rep;
+  const int oss = Hq * D;
+  auto stage = [&](int it, int buf) {
+    const int hq = hk * n_rep + it / per, q0 = (t0 + it % per) * F_BN;
+    const int64_t hrow = (int64_t)b * Hq + hq;
+    tile_dma<D>(qr_rows + (hrow * Sp + q0) * D, (uint32_t)D, sQ[buf], w, lane, F_BN);
+    tile_dma<D>(dout + (((int64_t)b * S + q0) * Hq + hq) * D, (uint32_t)oss, sO[buf], w, lane,
+                S - q0);
+    if (w == 0) mfma::row_to_lds(stats + (hrow * (Sp / F_BN) + q0 / F_BN) * (2 * F_BN), sS[buf], lane);
+  };
+  if (total > 0) stage(0, 0);
+
+  const int64_t koff = ((int64_t)b * S + key) * Hkv + hk;
+  f32x4 kr[NJ], vr[NJ];
+  load_row_share<D>(kr_rows + (((int64_t)b * Hkv + hk) * Sp + key) * D, cos, sin, key, g, kvalid,
+                    false, kr);
+  load_row_share<D>(v + koff * D, cos, sin, key, g, kvalid, false, vr);
+
+  f32x4 adk[NB], adv[NB];
+#pragma unroll
+  for (int db = 0; db < NB; ++db) adk[db] = adv[db] = zero4();
+  mfma::lds_copy_wait();
+  __syncthreads();
+
+  for (int it = 0; it < total; ++it) {
+    const int buf = it & 1;
+    if (it + 1 < total) stage(it + 1, buf ^ 1);
+    const float* tQ = sQ[buf];
+    const float* tO = sO[buf];
+    f32x4 s0 = zero4(), s1 = zero4(), d0 = zero4(), d1 = zero4();
+    scores2<D>(tQ, kr, c16, g, s0, s1);
+    scores2<D>(tO, vr, c16, g, d0, d1);
+    const int q0 = (t0 + it % per) * F_BN;
+    const bool edge = causal && q0 < k0 + F_BK - 1;
+    const int lim = key - q0;  // position offsets below lim are masked
+    {
+      const f32x4 nl0 = *(const f32x4*)(sS[buf] + 4 * g);
+      const f32x4 nl1 = *(const f32x4*)(sS[buf] + 16 + 4 * g);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float p0 = fast_exp2(__builtin_fmaf(s0[r], scale_log2, nl0[r]));
+        const float p1 = fast_exp2(__builtin_fmaf(s1[r], scale_log2, nl1[r]));
+        s0[r] = edge && 4 * g + r < lim ? 0.f : p0;
+        s1[r] = edge && 16 + 4 * g + r < lim ? 0.f : p1;
+      }
+    }
+    {
+      const f32x4 dl0 = *(const f32x4*)(sS[buf] + F_BN + 4 * g);
+      const f32x4 dl1 = *(const f32x4*)(sS[buf] + F_BN + 16 + 4 * g);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        d0[r] = s0[r] * (d0[r] - dl0[r]);
+        d1[r] = s1[r] * (d1[r] - dl1[r]);
+      }
+    }
+    accum_t2<D>(tO, s0, s1, adv, tQ, d0, d1, adk, c16, g);
+    if (it % per == per - 1 && it + 1 < total) {
+      // a query head done: its sums (unscaled, before the RoPE backward) join
+      // the group's in float64, in this lane's own elements of sum64 (per key
+      // row, D dK then D dV values), so the group sum adds no float32
+      // rounding per head: the float32 error stays that of one head's sum
+      const int h = it / per;
+      if (kvalid) {
+        // (the row offset recomputed from a laundered key: not kept live across the loop)
+        int kl = key;
+        asm volatile("" : "+v"(kl));
+        const int64_t ro = 2 * ((((int64_t)b * S + kl) * Hkv + hk) * D) + 4 * g;
+#pragma unroll
+        for (int db = 0; db < NB; ++db) {
+          f64x4* pk = (f64x4*)(sum64 + ro + 16 * db);
+          f64x4* pv = (f64x4*)(sum64 + ro + D + 16 * db);
+          const f64x4 ak = to_f64(adk[db]), av = to_f64(adv[db]);
+          *pk = h == 0 ? ak : *pk + ak;
+          *pv = h == 0 ? av : *pv + av;
+          __builtin_amdgcn_sched_barrier(0);  // one block's loads in flight at a time
+        }
+      }
+#pragma unroll
+      for (int db = 0; db < NB; ++db) adk[db] = adv[db] = zero4();
+    }
+    mfma::lds_copy_wait();
+    __syncthreads();
+  }
+  if (kvalid) {
+    int kl = key;
+    asm volatile("" : "+v"(kl));
+    const int64_t ko = (((int64_t)b * S + kl) * Hkv + hk) * D;
+    if (n_rep > 1) {
+#pragma unroll
+      for (int db = 0; db < NB; ++db) {
+        const double* pk = sum64 + 2 * ko + 16 * db + 4 * g;
+        adk[db] = to_f32x4(*(const f64x4*)pk + to_f64(adk[db]));
+        adv[db] = to_f32x4(*(const f64x4*)(pk + D) + to_f64(adv[db]));
+      }
+    }
+    store_grad_rope<D>(dk + ko, adk, cos, sin, kl, g, scale);
+    float* vrow = dv + ko;
+#pragma unroll
+    for (int db = 0; db < NB; ++db) *(f32x4*)(vrow + 16 * db + 4 * g) = adv[db];
+  }
+}
+
+template <int D>
+int launch_rows(const float* src, int64_t sb, int64_t ss, int64_t sh, const float* cos,
+                const float* sin, float* dst, int B, int S, int Sp, int H, int rot,
+                hipStream_t stream) {
+  const int64_t pairs = (int64_t)B * H * Sp * (D / 8);
+  KF_CHECK_ARG((pairs + 255) / 256 < (1LL << 31), "grid too large");
+  KF_LAUNCH("rows_f32", (rows_f32_kernel<D>), dim3((unsigned)((pairs + 255) / 256)), dim3(256),
+            0, stream, src, sb, ss, sh, cos, sin, dst, S, Sp, H, rot, pairs);
+  KF_CHECK_LAUNCH();
+  return KF_OK;
+}
+
+template <int D>
+int fwd_f32_t(const FwdArgs& a, void* workspace) {
+  const int n_rep = a.Hq / a.Hkv, bm_pos = F_ROWS / n_rep;
+  const int nqb = (a.Sq + bm_pos - 1) / bm_pos;
+  const int64_t nblk = (int64_t)nqb * a.B * a.Hkv;
+  KF_CHECK_ARG(nblk < (1LL << 31), "grid too large");
+  const float* kt = (const float*)a.k;
+  int64_t kb_b = a.ksb, kb_h = a.ksh, kld = a.kss;
+  if (!a.k_rotated) {
+    const int Skp = (a.Sk + F_BK - 1) / F_BK * F_BK;
+    float* krot = (float*)workspace;
+    const int rc = launch_rows<D>((const float*)a.k, a.ksb, a.kss, a.ksh, a.cos, a.sin, krot, a.B,
+                                  a.Sk, Skp, a.Hkv, 1, a.stream);
+    if (rc) return rc;
+    kt = krot;
+    kb_h = (int64_t)Skp * D;
+    kb_b = a.Hkv * kb_h;
+    kld = D;
+  }
+  KF_LAUNCH("fwd_f32", (fwd_f32_kernel<D>), dim3((unsigned)nblk), dim3(256), 0, a.stream,
+            (const float*)a.q, a.cos, a.sin, kt, kb_b, kb_h, (int)kld, (const float*)a.v, a.vsb,
+            a.vsh, (int)a.vss, (float*)a.out, a.lse, a.Sq, a.Sk, a.Hq, a.Hkv, n_rep, bm_pos, nqb,
+            a.causal, a.scale * kLog2e);
+  KF_CHECK_LAUNCH();
+  return KF_OK;
+}
+
+template <int D>
+int bwd_f32_t(const BwdArgs& a, void* workspace) {
+  const int n_rep = a.Hq / a.Hkv, bm_pos = F_ROWS / n_rep;
+  const int nqb = (a.S + bm_pos - 1) / bm_pos;
+  const int Sp = (a.S + F_BK - 1) / F_BK * F_BK;
+  const int64_t nqblk = (int64_t)nqb * a.B * a.Hkv;
+  const int64_t nkblk = (int64_t)(Sp / F_BK) * a.B * a.Hkv;
+  KF_CHECK_ARG(nqblk < (1LL << 31) && nkblk < (1LL << 31), "grid too large");
+  float* qrot = (float*)workspace;
+  float* krot = qrot + (size_t)a.B * a.Hq * Sp * D;
+  float* stats = krot + (size_t)a.B * a.Hkv * Sp * D;
+  double* sum64 = (double*)(stats + (size_t)a.B * a.Hq * Sp * 2);
+  const int64_t qss = (int64_t)a.Hq * D, kss = (int64_t)a.Hkv * D;
+  int rc = launch_rows<D>((const float*)a.q, a.S * qss, qss, D, a.cos, a.sin, qrot, a.B, a.S, Sp,
+                          a.Hq, 1, a.stream);
+  if (rc) return rc;
+  rc = launch_rows<D>((const float*)a.k, a.S * kss, kss, D, a.cos, a.sin, krot, a.B, a.S, Sp,
+                      a.Hkv, 1, a.stream);
+  if (rc) return rc;
+  const int64_t rows = (int64_t)a.B * a.Hq * Sp;
+  KF_LAUNCH("stats_f32", (stats_f32_kernel<D>), dim3((unsigned)((rows + 15) / 16)), dim3(256), 0,
+            a.stream, (const float*)a.out, (const float*)a.dout, a.lse, stats, a.S, Sp, a.Hq,
+            rows);
+  KF_LAUNCH("bwd_dq_f32", (bwd_dq_f32_kernel<D>), dim3((unsigned)nqblk), dim3(256), 0, a.stream,
+            qrot, krot, (const float*)a.v, a.cos, a.sin, (const float*)a.dout, stats,
+            (float*)a.dq, a.S, Sp, a.Hq, a.Hkv, n_rep, bm_pos, nqb, a.causal, a.scale,
+            a.scale * kLog2e);
+  KF_LAUNCH("bwd_dkdv_f32", (bwd_dkdv_f32_kernel<D>), dim3((unsigned)nkblk), dim3(256), 0,
+            a.stream, qrot, krot, (const float*)a.v, a.cos, a.sin, (const float*)a.dout, stats,
+            sum64, (float*)a.dk, (float*)a.dv, a.S, Sp, a.Hq, a.Hkv, n_rep, a.causal, a.scale,
+            a.scale * kLog2e);
+  KF_CHECK_LAUNCH();
+  return KF_OK;
+}
+
+bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+}  // namespace
+
+bool fwd_f32_supported(const FwdArgs& a) {
+  if (a.dtype != F32 || (a.D != 64 && a.D != 128)) return false;
+  if (a.doc || a.kvalid || a.rot) return false;
+  if (a.Sq < 1 || a.Sk < 1 || a.Hkv < 1 || a.Hq % a.Hkv) return false;
+  if (a.Hq / a.Hkv > F_ROWS) return false;
+  if (!al16(a.q) || !al16(a.k) || !al16(a.v) || !al16(a.out) || !al16(a.cos) || !al16(a.sin))
+    return false;
+  if ((a.ksb | a.kss | a.ksh | a.vsb | a.vss | a.vsh) & 3) return false;
+  // row strides of the direct tile loads (32-bit offsets)
+  if (a.kss > (1 << 24) || a.vss > (1 << 24)) return false;
+  return true;
+}
+
+size_t fwd_f32_workspace(int B, int Sk, int Hkv, int D) {
+  return (size_t)B * Hkv * ((Sk + F_BK - 1) / F_BK * F_BK) * D * sizeof(float);
+}
+
+int fwd_f32(const FwdArgs& a, void* workspace) {
+  return a.D == 128 ? fwd_f32_t<128>(a, workspace) : fwd_f32_t<64>(a, workspace);
+}
+
+bool bwd_f32_supported(const BwdArgs& a) {
+  if (a.dtype != F32 || (a.D != 64 && a.D != 128)) return false;
+  if (a.doc || a.kvalid || a.rot) return false;
+  if (a.S < 1 || a.Hkv < 1 || a.Hq % a.Hkv) return false;
+  if (a.Hq / a.Hkv > F_ROWS || (int64_t)a.Hq * a.D > (1 << 24)) return false;
+  return al16(a.q) && al16(a.k) && al16(a.v) && al16(a.cos) && al16(a.sin) && al16(a.out) &&
+         al16(a.dout) && al16(a.dq) && al16(a.dk) && al16(a.dv);
+}
+
+size_t bwd_f32_workspace(int B, int S, int Hq, int Hkv, int D) {
+  const size_t Sp = (size_t)(S + F_BK - 1) / F_BK * F_BK;
+  return ((size_t)B * Hq * Sp * D + (size_t)B * Hkv * Sp * D + (size_t)B * Hq * Sp * 2) *
+             sizeof(float) +
+         (Hq > Hkv ? (size_t)B * S * Hkv * D * 2 * sizeof(double) : 0);
+}
+
+int bwd_f32(const BwdArgs& a, void* workspace) {
+  return a.D == 128 ? bwd_f32_t<128>(a, workspace) : bwd_f32_t<64>(a, workspace);
+}
+
+}  // namespace kf

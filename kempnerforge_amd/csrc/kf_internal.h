@@ -58,6 +58,16 @@ size_t bwd_generic_workspace(int B, int S, int Hq);
 int bwd_generic(const BwdArgs& a, void* workspace);
 int capture_probs_generic(const FwdArgs& a, const float* lse, float* probs);
 
+// float32 MFMA kernels (kf_f32.hip): no explicit masks, head_dim 64 or 128.
+// Workspaces: the forward's rotated K (unused when a.k_rotated); the
+// backward's rotated Q and K and per-row softmax statistics.
+bool fwd_f32_supported(const FwdArgs& a);
+size_t fwd_f32_workspace(int B, int Sk, int Hkv, int D);
+int fwd_f32(const FwdArgs& a, void* workspace);
+bool bwd_f32_supported(const BwdArgs& a);
+size_t bwd_f32_workspace(int B, int S, int Hq, int Hkv, int D);
+int bwd_f32(const BwdArgs& a, void* workspace);
+
 // bf16 MFMA kernels (kf_fwd.hip, kf_bwd.hip, kf_capture.hip)
 bool fwd_mfma_supported(const FwdArgs& a);
 // Rotated K [B*Hkv][Skp][D] bf16 (Skp a multiple of 64, rows past Sk zero) and,

@@ -42,7 +42,8 @@ SHAPES = [
     (torch.bfloat16, 1, 300, 8, 1, 128),
     (torch.bfloat16, 1, 130, 6, 2, 128),
     (torch.bfloat16, 1, 64, 4, 2, 32),
-    (torch.float32, 1, 100, 8, 2, 128),
+    (torch.float32, 1, 100, 8, 2, 128),      # fp32 matrix-core kernels
+    (torch.float32, 1, 64, 4, 2, 32),        # generic kernels (fp32, D=32)
 ]
 
 

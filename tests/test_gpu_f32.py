@@ -1,0 +1,134 @@
+"""float32 on the fp32 matrix-core kernels (kf_f32.hip).
+
+The reference trains in float32 when ``mixed_precision = "fp32"``
+(kempnerforge/config/training.py:31); q, k and v then reach SDPA
+(kempnerforge/model/attention.py:231) in float32 and nothing in the path
+rounds below it.  Checked here against the float64 oracle on the same inputs
+with the north star's float32 bound, max-abs 1e-5 on the output, the LSE and
+every gradient element; the launches named by the library's kernel timer are
+the fp32 MFMA ones, not the generic kernels (which keep float32 with explicit
+masks and other head sizes, tested in the other files).
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from gpu_util import DEV, announce, check_grad, check_out, seeded
+from kempnerforge_amd import _lib, ops
+from oracle import attention_ref as ref
+
+pytestmark = pytest.mark.gpu
+
+F32 = torch.float32
+TOL = 1e-5
+GENERIC = {"fwd_generic", "bwd_dkdv_generic", "bwd_dq_generic", "bwd_delta_generic"}
+FWD = {"fwd_f32"}
+BWD = {"stats_f32", "bwd_dq_f32", "bwd_dkdv_f32"}
+
+
+def _inputs(B, S, Hq, Hkv, D, seed=0, theta=5e5):
+    q = seeded((B, S, Hq, D), seed, F32)
+    k = seeded((B, S, Hkv, D), seed + 1, F32)
+    v = seeded((B, S, Hkv, D), seed + 2, F32)
+    do = seeded((B, S, Hq, D), seed + 3, F32)
+    cos, sin = ref.rope_tables(D, S, theta)
+    return q, k, v, do, cos, sin
+
+
+CASES = [
+    # B, S, Hq, Hkv, D, causal        (what it exercises)
+    (2, 256, 4, 2, 64, True),      # the debug configuration's shape (C1)
+    (1, 300, 8, 1, 128, True),     # MQA, ragged last tile and key block
+    (2, 130, 4, 4, 64, False),     # MHA, full attention
+    (1, 257, 8, 2, 128, False),
+    (1, 100, 12, 4, 128, True),    # n_rep 3: 63 of 64 workgroup rows used
+    (1, 96, 64, 1, 128, True),     # n_rep 64: one position per workgroup
+    (1, 1, 4, 2, 128, True),       # single token
+    (2, 33, 6, 2, 64, True),
+    (1, 1000, 8, 2, 128, True),
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=lambda c: "-".join(map(str, c)))
+def test_forward_backward(case):
+    B, S, Hq, Hkv, D, causal = case
+    announce(f"fp32 fwd+bwd {case}")
+    q, k, v, do, cos, sin = _inputs(B, S, Hq, Hkv, D)
+    args = [t.to(DEV) for t in (q, k, v, cos, sin)]
+    with _lib.KernelTimer() as t:
+        out, lse = ops.fwd_raw(*args, causal=causal, k_rotated=False)
+        dq, dk, dv = ops.bwd_raw(*args, out, lse, do.to(DEV), causal=causal)
+        torch.cuda.synchronize()
+    ran = set(t.stats)
+    assert FWD | BWD <= ran and not ran & GENERIC, ran
+    o_ref, l_ref = ref.attention_fwd(q, k, v, cos, sin, causal=causal)
+    check_out(out, o_ref, TOL, "out")
+    check_out(lse, l_ref, TOL, "lse")
+    dq_r, dk_r, dv_r = ref.attention_bwd(q, k, v, cos, sin, do, causal=causal)
+    check_grad(dq, dq_r, F32, "dq")
+    check_grad(dk, dk_r, F32, "dk", group=Hq // Hkv)
+    check_grad(dv, dv_r, F32, "dv", group=Hq // Hkv)
+
+
+def test_autograd_and_determinism():
+    """ops.attention's autograd takes the same kernels; a recompute (activation
+    checkpointing) gives the same bits."""
+    B, S, Hq, Hkv, D = 2, 384, 8, 2, 128
+    announce("fp32 autograd + determinism")
+    q, k, v, do, cos, sin = _inputs(B, S, Hq, Hkv, D, seed=20)
+    grads = []
+    for _ in range(2):
+        qd, kd, vd = (x.to(DEV).requires_grad_(True) for x in (q, k, v))
+        out = ops.attention(qd, kd, vd, cos.to(DEV), sin.to(DEV), causal=True)
+        out.backward(do.to(DEV))
+        torch.cuda.synchronize()
+        grads.append((out.detach(), qd.grad, kd.grad, vd.grad))
+    for a, b in zip(*grads):
+        assert torch.equal(a, b)
+    dq_r, dk_r, dv_r = ref.attention_bwd(q, k, v, cos, sin, do, causal=True)
+    check_grad(grads[0][1], dq_r, F32, "dq")
+    check_grad(grads[0][2], dk_r, F32, "dk", group=Hq // Hkv)
+    check_grad(grads[0][3], dv_r, F32, "dv", group=Hq // Hkv)
+
+
+@pytest.mark.parametrize("Sq,Sk", [(1, 300), (64, 333), (200, 200)])
+def test_rotated_cache_forward(Sq, Sk):
+    """Multi-token forward over a rotated KV cache ([B, Hkv, Smax, D] views,
+    Sq <= Sk, top-left causal): the fp32 forward reads the cache rows
+    directly (no rotation prepass)."""
+    B, Hq, Hkv, D, Smax = 2, 8, 2, 128, 400
+    announce(f"fp32 cache forward Sq={Sq} Sk={Sk}")
+    q = seeded((B, Sq, Hq, D), 30, F32)
+    kc = seeded((B, Hkv, Smax, D), 31, F32)
+    vc = seeded((B, Hkv, Smax, D), 32, F32)
+    cos, sin = ref.rope_tables(D, Sq, 1e4)
+    kd, vd = kc.to(DEV), vc.to(DEV)
+    with _lib.KernelTimer() as t:
+        out, lse = ops.fwd_raw(q.to(DEV), kd[:, :, :Sk], vd[:, :, :Sk], cos.to(DEV), sin.to(DEV),
+                               causal=True, k_rotated=True, k_layout="bhsd")
+        torch.cuda.synchronize()
+    assert FWD <= set(t.stats) and not set(t.stats) & GENERIC, t.stats
+    o_ref, l_ref = ref.attention_fwd_rotated(q, kc[:, :, :Sk], vc[:, :, :Sk], cos, sin)
+    check_out(out, o_ref, TOL, "out")
+    check_out(lse, l_ref, TOL, "lse")
+
+
+def test_longer_rows():
+    """2048 positions, groups of 4: gradients summed over thousands of float32
+    terms still within 1e-5 of the float64 oracle."""
+    B, S, Hq, Hkv, D = 1, 2048, 8, 2, 128
+    announce("fp32 S=2048")
+    q, k, v, do, cos, sin = _inputs(B, S, Hq, Hkv, D, seed=40)
+    args = [t.to(DEV) for t in (q, k, v, cos, sin)]
+    out, lse = ops.fwd_raw(*args, causal=True, k_rotated=False)
+    dq, dk, dv = ops.bwd_raw(*args, out, lse, do.to(DEV), causal=True)
+    torch.cuda.synchronize()
+    o_ref, l_ref = ref.attention_fwd(q, k, v, cos, sin)
+    check_out(out, o_ref, TOL, "out")
+    check_out(lse, l_ref, TOL, "lse")
+    dq_r, dk_r, dv_r = ref.attention_bwd(q, k, v, cos, sin, do)
+    check_grad(dq, dq_r, F32, "dq")
+    check_grad(dk, dk_r, F32, "dk", group=Hq // Hkv)
+    check_grad(dv, dv_r, F32, "dv", group=Hq // Hkv)

@@ -48,7 +48,8 @@ SHAPES = [
     (torch.float16, 2, 200, 4, 4, 64, 1e4),      # fp16, MHA, D=64
     (torch.float16, 1, 300, 8, 1, 128, 5e5),     # fp16, MQA
     (torch.float16, 1, 77, 4, 2, 32, 1e4),       # generic kernel (fp16, D=32)
-    (torch.float32, 1, 150, 8, 2, 128, 5e5),     # generic kernel (fp32, D=128)
+    (torch.float32, 1, 150, 8, 2, 128, 5e5),     # fp32 matrix-core kernel (D=128)
+    (torch.float32, 1, 77, 4, 2, 32, 1e4),       # generic kernel (fp32, D=32)
 ]
 
 
