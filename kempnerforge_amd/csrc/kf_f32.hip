@@ -270,27 +270,156 @@ __global__ __launch_bounds__(256) void stats_f32_kernel(const float* __restrict_
   }
 }
 
+// ------------------------------------------------------------------ masks
+// Explicit masks, one kind at a time, on causal self-attention (Sq == Sk):
+// MASK_DOC, a query sees only keys of its own document, and the walks skip
+// the 32-position tiles whose [min, max] document id misses the workgroup's
+// (exact for any id pattern); MASK_KPM, a query sees only valid keys, and the
+// rows before the batch row's first valid key, which would see none, attend
+// every key instead (the reference's NaN guard, mask | ~mask.any(-1)).
+using mfma::MASK_DOC;
+using mfma::MASK_KPM;
+using mfma::MASK_NONE;
+constexpr int F_MAX_TILES = 4096;  // 32-position tiles of a batch row (S <= 131072)
+
+// Per batch row: MASK_DOC the [min, max] id of each 32-position tile;
+// MASK_KPM the first valid key (INT_MAX when none).  One workgroup per row.
+__global__ __launch_bounds__(256) void mask_prep_f32_kernel(const int32_t* __restrict__ mask,
+                                                            int mode, int S, int nt,
+                                                            int2* __restrict__ ranges,
+                                                            int* __restrict__ first_valid) {
+  __shared__ int sf;
+  const int32_t* mrow = mask + (int64_t)blockIdx.x * S;
+  if (mode == MASK_DOC) {
+    for (int t = threadIdx.x; t < nt; t += 256) {
+      int lo = INT_MAX, hi = INT_MIN;
+      for (int j = t * F_BN; j < min(S, t * F_BN + F_BN); ++j) {
+        lo = min(lo, mrow[j]);
+        hi = max(hi, mrow[j]);
+      }
+      ranges[(int64_t)blockIdx.x * nt + t] = make_int2(lo, hi);
+    }
+  } else {
+    if (threadIdx.x == 0) sf = INT_MAX;
+    __syncthreads();
+    int f = INT_MAX;
+    for (int j = threadIdx.x; j < S; j += 256)
+      if (mrow[j] != 0) {
+        f = j;
+        break;
+      }
+    atomicMin(&sf, f);
+    __syncthreads();
+    if (threadIdx.x == 0) first_valid[blockIdx.x] = sf;
+  }
+}
+
+// [min, max] document id of positions [p_begin, p_end), at most 64 of them;
+// wavefront-uniform.
+__device__ __forceinline__ int2 doc_range64(const int32_t* __restrict__ mrow, int p_begin,
+                                            int p_end, int lane) {
+  const int p = p_begin + lane;
+  const int d = p < p_end ? mrow[p] : 0;
+  const int lo = mfma::wave_min_i(p < p_end ? d : INT_MAX);
+  const int hi = mfma::wave_max_i(p < p_end ? d : INT_MIN);
+  return make_int2(__builtin_amdgcn_readfirstlane(lo), __builtin_amdgcn_readfirstlane(hi));
+}
+
+// Lists, ascending, the tiles t in [t_begin, t_end) whose document range meets
+// [lo, hi]; returns the count.  One wavefront; the caller publishes the count
+// and synchronises before the list is read.
+__device__ __forceinline__ int list_doc_tiles(const int2* __restrict__ rng, int t_begin, int t_end,
+                                              int lo, int hi, uint16_t* list, int lane) {
+  int n = 0;
+  for (int base = t_begin; base < t_end; base += 64) {
+    const int t = base + lane;
+    bool vis = false;
+    if (t < t_end) {
+      const int2 r = rng[t];
+      vis = r.x <= hi && r.y >= lo;
+    }
+    const uint64_t m = __builtin_amdgcn_ballot_w64(vis);
+    const int below = __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                                __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0));
+    if (vis) list[n + below] = (uint16_t)t;
+    n += __builtin_popcountll(m);
+  }
+  return n;
+}
+
+// The key tiles a query-row workgroup (forward, dQ) walks: the causal range up
+// to its last row (every key when one of its rows is a guarded one), under
+// MASK_DOC only the listed tiles.  Returns the count; tiles: tile_at.
+template <int MODE>
+struct KeyWalk {
+  const int32_t* mrow;  // the batch row's mask (doc ids or key validity)
+  int n, fv, di;        // tiles; first valid key (MASK_KPM); this lane's row's document
+  bool guarded;         // this lane's row attends every key (MASK_KPM)
+};
+template <int MODE>
+__device__ __forceinline__ KeyWalk<MODE> key_walk(const RowInfo& ri, int kend_causal, int S,
+                                                  int bm_pos, const int32_t* mask,
+                                                  const int2* ranges, const int* first_valid,
+                                                  int nt32, uint16_t* list, int* count, int w,
+                                                  int lane) {
+  KeyWalk<MODE> k{nullptr, (kend_causal + F_BN - 1) / F_BN, 0, 0, false};
+  if (MODE == MASK_NONE) return k;
+  k.mrow = mask + (int64_t)ri.b * S;
+  if (MODE == MASK_KPM) {
+    k.fv = first_valid[ri.b];
+    k.guarded = ri.pos < k.fv;
+    if (ri.p0 < k.fv) k.n = (S + F_BN - 1) / F_BN;
+  } else {
+    k.di = ri.q_valid ? k.mrow[ri.pos] : 0;
+    const int2 dr = doc_range64(k.mrow, ri.p0, min(ri.p0 + bm_pos, S), lane);
+    if (w == 0) {
+      const int n = list_doc_tiles(ranges + (int64_t)ri.b * nt32, 0, k.n, dr.x, dr.y, list, lane);
+      if (lane == 0) *count = n;
+    }
+    __syncthreads();
+    k.n = __builtin_amdgcn_readfirstlane(*count);
+  }
+  return k;
+}
+
+// Whether this lane's row (query position pos, causal limit lim = pos - k0)
+// sees key k0 + j.
+template <int MODE>
+__device__ __forceinline__ bool row_sees(const KeyWalk<MODE>& k, int k0, int j, int lim, int S) {
+  const int key = k0 + j;
+  if (MODE == MASK_DOC) return j <= lim && k.mrow[min(key, S - 1)] == k.di;
+  return k.guarded ? key < S : j <= lim && k.mrow[min(key, S - 1)] != 0;
+}
+
 // ------------------------------------------------------------------ forward
 // Workgroup: 4 wavefronts x 16 (head, position) rows of one KV group (the
 // rows of all its query heads share each K/V tile); S^T = K·Q^T per 32-key
 // tile, online softmax in the lane, O^T += V^T·P^T.  K comes rotated: element
 // (b, g, key, d) at kt + b kb_b + g kb_h + key kld + d (the prepass's rows or
 // a rotated cache).
-template <int D>
+template <int D, int MODE>
 __global__ __launch_bounds__(256, 2) void fwd_f32_kernel(
     const float* __restrict__ q, const float* __restrict__ cos, const float* __restrict__ sin,
     const float* kt, int64_t kb_b, int64_t kb_h, int kld, const float* v, int64_t vsb,
     int64_t vsh, int vss, float* __restrict__ out, float* __restrict__ lse, int Sq, int Sk,
-    int Hq, int Hkv, int n_rep, int bm_pos, int nqb, int causal, float scale_log2) {
+    int Hq, int Hkv, int n_rep, int bm_pos, int nqb, int causal, float scale_log2,
+    const int32_t* __restrict__ mask, const int2* __restrict__ ranges,
+    const int* __restrict__ first_valid, int nt32) {
   constexpr int NJ = D / 16, NB = D / 16;
   __shared__ __attribute__((aligned(16))) float sK[2][F_BN * D];
   __shared__ __attribute__((aligned(16))) float sV[2][F_BN * D];
+  __shared__ uint16_t sList[MODE == MASK_DOC ? F_MAX_TILES : 1];
+  __shared__ int sCount;
 
   const int lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15, w = wave_id();
   const int logical = xcd_logical_id(blockIdx.x, gridDim.x, nqb);
   const RowInfo ri = row_info(logical, nqb, Hkv, n_rep, bm_pos, Sq, w * 16 + c16);
-  const int kend = causal ? min(Sk, min(ri.p0 + bm_pos, Sq)) : Sk;
-  const int ntiles = (kend + F_BN - 1) / F_BN;
+  const KeyWalk<MODE> kw =
+      key_walk<MODE>(ri, causal ? min(Sk, min(ri.p0 + bm_pos, Sq)) : Sk, Sk, bm_pos, mask,
+                     ranges, first_valid, nt32, sList, &sCount, w, lane);
+  auto tile_at = [&](int i) {
+    return MODE == MASK_DOC ? __builtin_amdgcn_readfirstlane((int)sList[i]) : i;
+  };
   const float* kb = kt + (int64_t)ri.b * kb_b + (int64_t)ri.g * kb_h;
   const float* vb = v + (int64_t)ri.b * vsb + (int64_t)ri.g * vsh;
   auto stage = [&](int t, int buf) {
@@ -298,7 +427,7 @@ __global__ __launch_bounds__(256, 2) void fwd_f32_kernel(
     tile_dma<D>(kb + (int64_t)k0 * kld, (uint32_t)kld, sK[buf], w, lane, Sk - k0);
     tile_dma<D>(vb + (int64_t)k0 * vss, (uint32_t)vss, sV[buf], w, lane, Sk - k0);
   };
-  if (ntiles > 0) stage(0, 0);
+  if (kw.n > 0) stage(tile_at(0), 0);
 
   f32x4 qr[NJ];
   load_row_share<D>(q + (((int64_t)ri.b * Sq + ri.pos) * Hq + ri.hq) * D, cos, sin, ri.pos, g,
@@ -311,21 +440,30 @@ __global__ __launch_bounds__(256, 2) void fwd_f32_kernel(
   mfma::lds_copy_wait();
   __syncthreads();
 
-  for (int t = 0; t < ntiles; ++t) {
-    const int buf = t & 1;
-    if (t + 1 < ntiles) stage(t + 1, buf ^ 1);
+  for (int i = 0; i < kw.n; ++i) {
+    const int buf = i & 1, t = tile_at(i);
+    if (i + 1 < kw.n) stage(tile_at(i + 1), buf ^ 1);
     const float* tK = sK[buf];
     const float* tV = sV[buf];
     f32x4 s0 = zero4(), s1 = zero4();
     scores2<D>(tK, qr, c16, g, s0, s1);
 
     const int k0 = t * F_BN;
-    if ((causal && k0 + F_BN - 1 > ri.p0) || k0 + F_BN > Sk) {
-      const int lim = (causal ? min(ri.pos, Sk - 1) : Sk - 1) - k0;
+    if (MODE == MASK_NONE) {
+      if ((causal && k0 + F_BN - 1 > ri.p0) || k0 + F_BN > Sk) {
+        const int lim = (causal ? min(ri.pos, Sk - 1) : Sk - 1) - k0;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          s0[r] = 4 * g + r > lim ? -INFINITY : s0[r];
+          s1[r] = 16 + 4 * g + r > lim ? -INFINITY : s1[r];
+        }
+      }
+    } else {
+      const int lim = min(ri.pos, Sk - 1) - k0;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        s0[r] = 4 * g + r > lim ? -INFINITY : s0[r];
-        s1[r] = 16 + 4 * g + r > lim ? -INFINITY : s1[r];
+        s0[r] = row_sees<MODE>(kw, k0, 4 * g + r, lim, Sk) ? s0[r] : -INFINITY;
+        s1[r] = row_sees<MODE>(kw, k0, 16 + 4 * g + r, lim, Sk) ? s1[r] : -INFINITY;
       }
     }
     float tmax = -INFINITY;
@@ -333,13 +471,15 @@ __global__ __launch_bounds__(256, 2) void fwd_f32_kernel(
     for (int r = 0; r < 4; ++r) tmax = fmaxf(tmax, fmaxf(s0[r], s1[r]));
     tmax = quad_max(tmax) * scale_log2;
     const float mnew = fmaxf(m, tmax);
-    const float alpha = fast_exp2(m - mnew);
+    // with an explicit mask a row may have seen no key yet (max still -inf)
+    const float mref = MODE == MASK_NONE || mnew != -INFINITY ? mnew : 0.f;
+    const float alpha = fast_exp2(m - mref);
     m = mnew;
     l *= alpha;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      s0[r] = fast_exp2(__builtin_fmaf(s0[r], scale_log2, -m));
-      s1[r] = fast_exp2(__builtin_fmaf(s1[r], scale_log2, -m));
+      s0[r] = fast_exp2(__builtin_fmaf(s0[r], scale_log2, -mref));
+      s1[r] = fast_exp2(__builtin_fmaf(s1[r], scale_log2, -mref));
       l += s0[r] + s1[r];
     }
     accum_t<D>(tV, s0, s1, c16, g, o, alpha);
@@ -388,21 +528,29 @@ __device__ __forceinline__ void store_grad_rope(float* __restrict__ row, const f
 // dQ: the forward's rows and tiles; per 32-key tile S^T = K·Q^T and
 // dP^T = V·dO^T, dS^T = P^T (dP^T - Delta), dQ^T += K^T·dS^T.  qr / kr: the
 // prepass's rotated rows, Sp per head.
-template <int D>
+template <int D, int MODE>
 __global__ __launch_bounds__(256, 2) void bwd_dq_f32_kernel(
     const float* __restrict__ qr_rows, const float* kr_rows, const float* v,
     const float* __restrict__ cos, const float* __restrict__ sin, const float* __restrict__ dout,
     const float* __restrict__ stats, float* __restrict__ dq, int S, int Sp, int Hq, int Hkv,
-    int n_rep, int bm_pos, int nqb, int causal, float scale, float scale_log2) {
+    int n_rep, int bm_pos, int nqb, int causal, float scale, float scale_log2,
+    const int32_t* __restrict__ mask, const int2* __restrict__ ranges,
+    const int* __restrict__ first_valid, int nt32) {
   constexpr int NJ = D / 16, NB = D / 16;
   __shared__ __attribute__((aligned(16))) float sK[2][F_BN * D];
   __shared__ __attribute__((aligned(16))) float sV[2][F_BN * D];
+  __shared__ uint16_t sList[MODE == MASK_DOC ? F_MAX_TILES : 1];
+  __shared__ int sCount;
 
   const int lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15, w = wave_id();
   const int logical = xcd_logical_id(blockIdx.x, gridDim.x, nqb);
   const RowInfo ri = row_info(logical, nqb, Hkv, n_rep, bm_pos, S, w * 16 + c16);
-  const int kend = causal ? min(S, ri.p0 + bm_pos) : S;
-  const int ntiles = (kend + F_BN - 1) / F_BN;
+  const KeyWalk<MODE> kw = key_walk<MODE>(ri, causal ? min(S, ri.p0 + bm_pos) : S, S, bm_pos,
+                                          mask, ranges, first_valid, nt32, sList, &sCount, w,
+                                          lane);
+  auto tile_at = [&](int i) {
+    return MODE == MASK_DOC ? __builtin_amdgcn_readfirstlane((int)sList[i]) : i;
+  };
   const float* kb = kr_rows + ((int64_t)ri.b * Hkv + ri.g) * Sp * D;
   const float* vb = v + ((int64_t)ri.b * S * Hkv + ri.g) * D;
   const int vss = Hkv * D;
@@ -411,7 +559,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_f32_kernel(
     tile_dma<D>(kb + (int64_t)k0 * D, (uint32_t)D, sK[buf], w, lane, S - k0);
     tile_dma<D>(vb + (int64_t)k0 * vss, (uint32_t)vss, sV[buf], w, lane, S - k0);
   };
-  if (ntiles > 0) stage(0, 0);
+  if (kw.n > 0) stage(tile_at(0), 0);
 
   const int64_t hrow = (int64_t)ri.b * Hq + ri.hq;
   const int64_t roff = ((int64_t)ri.b * S + ri.pos) * Hq + ri.hq;
@@ -428,24 +576,29 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_f32_kernel(
   mfma::lds_copy_wait();
   __syncthreads();
 
-  for (int t = 0; t < ntiles; ++t) {
-    const int buf = t & 1;
-    if (t + 1 < ntiles) stage(t + 1, buf ^ 1);
+  for (int i = 0; i < kw.n; ++i) {
+    const int buf = i & 1, t = tile_at(i);
+    if (i + 1 < kw.n) stage(tile_at(i + 1), buf ^ 1);
     const float* tK = sK[buf];
     const float* tV = sV[buf];
     f32x4 s0 = zero4(), s1 = zero4(), d0 = zero4(), d1 = zero4();
     scores2<D>(tK, qr, c16, g, s0, s1);
     scores2<D>(tV, dr, c16, g, d0, d1);
     const int k0 = t * F_BN;
-    const bool edge = (causal && k0 + F_BN - 1 > ri.p0) || k0 + F_BN > S;
+    const bool edge = MODE != MASK_NONE || (causal && k0 + F_BN - 1 > ri.p0) || k0 + F_BN > S;
     const int lim = (causal ? min(ri.pos, S - 1) : S - 1) - k0;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       float p0 = fast_exp2(__builtin_fmaf(s0[r], scale_log2, nl));
       float p1 = fast_exp2(__builtin_fmaf(s1[r], scale_log2, nl));
       if (edge) {
-        p0 = 4 * g + r > lim ? 0.f : p0;
-        p1 = 16 + 4 * g + r > lim ? 0.f : p1;
+        if (MODE == MASK_NONE) {
+          p0 = 4 * g + r > lim ? 0.f : p0;
+          p1 = 16 + 4 * g + r > lim ? 0.f : p1;
+        } else {
+          p0 = row_sees<MODE>(kw, k0, 4 * g + r, lim, S) ? p0 : 0.f;
+          p1 = row_sees<MODE>(kw, k0, 16 + 4 * g + r, lim, S) ? p1 : 0.f;
+        }
       }
       s0[r] = p0 * (d0[r] - dl);
       s1[r] = p1 * (d1[r] - dl);
@@ -459,20 +612,25 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_f32_kernel(
 
 // dK/dV: a workgroup owns 64 keys of one KV head (16 per wavefront, one per
 // lane column), their rotated K and V rows in registers, and walks every
-// query head of the group over the query tiles from the keys' diagonal on:
-// S = Q·K^T and dP = dO·V^T per 32-position tile, then dV^T += dO^T·P and
-// dK^T += Q^T·dS.  Key blocks are numbered longest first.
-template <int D>
+// query head of the group over the query tiles from the keys' diagonal on
+// (under MASK_DOC only the listed ones; under MASK_KPM also the guarded rows'
+// tiles below it): S = Q·K^T and dP = dO·V^T per 32-position tile, then
+// dV^T += dO^T·P and dK^T += Q^T·dS.  Key blocks are numbered longest first.
+template <int D, int MODE>
 __global__ __launch_bounds__(256, 2) void bwd_dkdv_f32_kernel(
     const float* qr_rows, const float* __restrict__ kr_rows, const float* __restrict__ v,
     const float* __restrict__ cos, const float* __restrict__ sin, const float* dout,
     const float* stats, double* __restrict__ sum64, float* __restrict__ dk,
     float* __restrict__ dv, int S, int Sp, int Hq, int Hkv, int n_rep, int causal, float scale,
-    float scale_log2) {
+    float scale_log2, const int32_t* __restrict__ mask, const int2* __restrict__ ranges,
+    const int* __restrict__ first_valid, int nt32) {
   constexpr int NJ = D / 16, NB = D / 16;
   __shared__ __attribute__((aligned(16))) float sQ[2][F_BN * D];
   __shared__ __attribute__((aligned(16))) float sO[2][F_BN * D];
   __shared__ __attribute__((aligned(16))) float sS[2][2 * F_BN];  // -lse log2(e), Delta
+  __shared__ uint16_t sList[MODE == MASK_DOC ? F_MAX_TILES : 1];
+  __shared__ __attribute__((aligned(16))) int32_t sDoc[MODE == MASK_DOC ? 2 : 1][64];
+  __shared__ int sCount;
 
   const int lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15, w = wave_id();
   const int BH = gridDim.x / ((S + F_BK - 1) / F_BK);
@@ -483,15 +641,43 @@ __global__ __launch_bounds__(256, 2) void bwd_dkdv_f32_kernel(
   const bool kvalid = key < S;
 
   const int nt = (S + F_BN - 1) / F_BN, t0 = causal ? k0 / F_BN : 0;
-  const int per = nt - t0, total = per * n_rep;
+  // the query tiles walked per head: tile_of(0 .. per-1)
+  const int32_t* mrow = MODE != MASK_NONE ? mask + (int64_t)b * S : nullptr;
+  int per = nt - t0, ng = 0, kdoc = 0;
+  // MASK_KPM: query rows below fvk (the guarded ones, for a key inside the
+  // sequence) see this key, and so do rows from kkey on (INT_MAX: padding key)
+  int fvk = 0, kkey = INT_MAX;
+  if (MODE == MASK_KPM) {
+    const int fv = first_valid[b];
+    ng = fv >= S ? t0 : min((fv + F_BN - 1) / F_BN, t0);  // guarded rows' tiles below t0
+    per += ng;
+    fvk = kvalid ? fv : 0;
+    kkey = kvalid && mrow[key] != 0 ? key : INT_MAX;
+  } else if (MODE == MASK_DOC) {
+    kdoc = kvalid ? mrow[key] : 0;
+    const int2 dr = doc_range64(mrow, k0, min(k0 + F_BK, S), lane);
+    if (w == 0) {
+      const int n = list_doc_tiles(ranges + (int64_t)b * nt32, t0, nt, dr.x, dr.y, sList, lane);
+      if (lane == 0) sCount = n;
+    }
+    __syncthreads();
+    per = __builtin_amdgcn_readfirstlane(sCount);
+  }
+  auto tile_of = [&](int u) {
+    return MODE == MASK_DOC ? __builtin_amdgcn_readfirstlane((int)sList[u])
+                            : MODE == MASK_KPM && u < ng ? u : t0 + u - ng;
+  };
+  const int total = per * n_rep;
   const int oss = Hq * D;
   auto stage = [&](int it, int buf) {
-    const int hq = hk * n_rep + it / per, q0 = (t0 + it % per) * F_BN;
+    const int hq = hk * n_rep + it / per, q0 = tile_of(it % per) * F_BN;
     const int64_t hrow = (int64_t)b * Hq + hq;
     tile_dma<D>(qr_rows + (hrow * Sp + q0) * D, (uint32_t)D, sQ[buf], w, lane, F_BN);
     tile_dma<D>(dout + (((int64_t)b * S + q0) * Hq + hq) * D, (uint32_t)oss, sO[buf], w, lane,
                 S - q0);
     if (w == 0) mfma::row_to_lds(stats + (hrow * (Sp / F_BN) + q0 / F_BN) * (2 * F_BN), sS[buf], lane);
+    if (MODE == MASK_DOC && w == 1)  // the tile's document ids (positions past S repeat S - 1)
+      mfma::dma4(mfma::lds_addr(sDoc[buf]), 4u * (uint32_t)min(lane, S - 1 - q0), mrow + q0);
   };
   if (total > 0) stage(0, 0);
 
@@ -512,21 +698,49 @@ __global__ __launch_bounds__(256, 2) void bwd_dkdv_f32_kernel(
     if (it + 1 < total) stage(it + 1, buf ^ 1);
     const float* tQ = sQ[buf];
     const float* tO = sO[buf];
+    // MASK_DOC: bit r (4 + r) set when query offset 4g + r (16 + 4g + r) is in
+    // this key's document (formed before the products, whose registers it
+    // would otherwise share)
+    int same = 0;
+    if (MODE == MASK_DOC) {
+      const mfma::i32x4 dq0 = *(const mfma::i32x4*)(sDoc[buf] + 4 * g);
+      const mfma::i32x4 dq1 = *(const mfma::i32x4*)(sDoc[buf] + 16 + 4 * g);
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        same |= (dq0[r] == kdoc ? 1 : 0) << r | (dq1[r] == kdoc ? 16 : 0) << r;
+      asm volatile("" : "+v"(same));
+    }
     f32x4 s0 = zero4(), s1 = zero4(), d0 = zero4(), d1 = zero4();
     scores2<D>(tQ, kr, c16, g, s0, s1);
     scores2<D>(tO, vr, c16, g, d0, d1);
-    const int q0 = (t0 + it % per) * F_BN;
-    const bool edge = causal && q0 < k0 + F_BK - 1;
-    const int lim = key - q0;  // position offsets below lim are masked
+    const int q0 = tile_of(it % per) * F_BN;
+    const bool edge = MODE != MASK_NONE || (causal && q0 < k0 + F_BK - 1);
+    const int lim = key - q0;  // position offsets below lim are masked (causal)
+    const int klim = kkey - q0;  // MASK_KPM: offsets from klim on see this (valid) key
     {
       const f32x4 nl0 = *(const f32x4*)(sS[buf] + 4 * g);
       const f32x4 nl1 = *(const f32x4*)(sS[buf] + 16 + 4 * g);
+
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const float p0 = fast_exp2(__builtin_fmaf(s0[r], scale_log2, nl0[r]));
         const float p1 = fast_exp2(__builtin_fmaf(s1[r], scale_log2, nl1[r]));
-        s0[r] = edge && 4 * g + r < lim ? 0.f : p0;
-        s1[r] = edge && 16 + 4 * g + r < lim ? 0.f : p1;
+        bool v0 = true, v1 = true;
+        if (edge) {
+          const int o0 = 4 * g + r, o1 = 16 + 4 * g + r;
+          if (MODE == MASK_NONE) {
+            v0 = o0 >= lim;
+            v1 = o1 >= lim;
+          } else if (MODE == MASK_DOC) {
+            v0 = o0 >= lim && ((same >> r) & 1);
+            v1 = o1 >= lim && ((same >> (4 + r)) & 1);
+          } else {  // guarded rows (below fvk) see every key, the others valid keys up to theirs
+            v0 = q0 + o0 < fvk || o0 >= klim;
+            v1 = q0 + o1 < fvk || o1 >= klim;
+          }
+        }
+        s0[r] = v0 ? p0 : 0.f;
+        s1[r] = v1 ? p1 : 0.f;
       }
     }
     {
@@ -570,7 +784,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dkdv_f32_kernel(
     int kl = key;
     asm volatile("" : "+v"(kl));
     const int64_t ko = (((int64_t)b * S + kl) * Hkv + hk) * D;
-    if (n_rep > 1) {
+    if (n_rep > 1 && per > 0) {
 #pragma unroll
       for (int db = 0; db < NB; ++db) {
         const double* pk = sum64 + 2 * ko + 16 * db + 4 * g;
@@ -597,6 +811,50 @@ int launch_rows(const float* src, int64_t sb, int64_t ss, int64_t sh, const floa
   return KF_OK;
 }
 
+size_t al256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+int mask_mode_of(const int32_t* doc, const int32_t* kvalid) {
+  return doc ? MASK_DOC : kvalid ? MASK_KPM : MASK_NONE;
+}
+
+// the mask records (mask_prep_f32) at the end of a workspace of `base` bytes
+struct MaskRec {
+  int2* ranges;
+  int* first_valid;
+  int nt32;
+};
+MaskRec mask_rec(void* workspace, size_t base, int B, int S) {
+  MaskRec m;
+  m.nt32 = (S + F_BN - 1) / F_BN;
+  m.ranges = (int2*)((char*)workspace + al256(base));
+  m.first_valid = (int*)(m.ranges + (size_t)B * m.nt32);
+  return m;
+}
+size_t mask_rec_bytes(int B, int S) {
+  return (size_t)B * ((S + F_BN - 1) / F_BN) * sizeof(int2) + (size_t)B * sizeof(int);
+}
+int launch_mask_prep(const int32_t* mask, int mode, int B, int S, const MaskRec& m,
+                     hipStream_t stream) {
+  KF_LAUNCH("mask_prep_f32", mask_prep_f32_kernel, dim3(B), dim3(256), 0, stream, mask, mode, S,
+            m.nt32, m.ranges, m.first_valid);
+  KF_CHECK_LAUNCH();
+  return KF_OK;
+}
+
+size_t fwd_krot_bytes(int B, int Sk, int Hkv, int D) {
+  return (size_t)B * Hkv * ((Sk + F_BK - 1) / F_BK * F_BK) * D * sizeof(float);
+}
+
+template <int D, int MODE>
+void launch_fwd_f32(const FwdArgs& a, const float* kt, int64_t kb_b, int64_t kb_h, int kld,
+                    int n_rep, int bm_pos, int nqb, unsigned nblk, const MaskRec& mr) {
+  KF_LAUNCH("fwd_f32", (fwd_f32_kernel<D, MODE>), dim3(nblk), dim3(256), 0, a.stream,
+            (const float*)a.q, a.cos, a.sin, kt, kb_b, kb_h, kld, (const float*)a.v, a.vsb, a.vsh,
+            (int)a.vss, (float*)a.out, a.lse, a.Sq, a.Sk, a.Hq, a.Hkv, n_rep, bm_pos, nqb,
+            a.causal, a.scale * kLog2e, a.doc ? a.doc : a.kvalid, mr.ranges, mr.first_valid,
+            mr.nt32);
+}
+
 template <int D>
 int fwd_f32_t(const FwdArgs& a, void* workspace) {
   const int n_rep = a.Hq / a.Hkv, bm_pos = F_ROWS / n_rep;
@@ -616,12 +874,47 @@ int fwd_f32_t(const FwdArgs& a, void* workspace) {
     kb_b = a.Hkv * kb_h;
     kld = D;
   }
-  KF_LAUNCH("fwd_f32", (fwd_f32_kernel<D>), dim3((unsigned)nblk), dim3(256), 0, a.stream,
-            (const float*)a.q, a.cos, a.sin, kt, kb_b, kb_h, (int)kld, (const float*)a.v, a.vsb,
-            a.vsh, (int)a.vss, (float*)a.out, a.lse, a.Sq, a.Sk, a.Hq, a.Hkv, n_rep, bm_pos, nqb,
-            a.causal, a.scale * kLog2e);
+  const int mode = mask_mode_of(a.doc, a.kvalid);
+  MaskRec mr{nullptr, nullptr, 0};
+  if (mode != MASK_NONE) {
+    mr = mask_rec(workspace, fwd_krot_bytes(a.B, a.Sk, a.Hkv, D), a.B, a.Sk);
+    const int rc = launch_mask_prep(a.doc ? a.doc : a.kvalid, mode, a.B, a.Sk, mr, a.stream);
+    if (rc) return rc;
+  }
+  if (mode == MASK_DOC)
+    launch_fwd_f32<D, MASK_DOC>(a, kt, kb_b, kb_h, (int)kld, n_rep, bm_pos, nqb, (unsigned)nblk, mr);
+  else if (mode == MASK_KPM)
+    launch_fwd_f32<D, MASK_KPM>(a, kt, kb_b, kb_h, (int)kld, n_rep, bm_pos, nqb, (unsigned)nblk, mr);
+  else
+    launch_fwd_f32<D, MASK_NONE>(a, kt, kb_b, kb_h, (int)kld, n_rep, bm_pos, nqb, (unsigned)nblk,
+                                 mr);
   KF_CHECK_LAUNCH();
   return KF_OK;
+}
+
+// backward workspace: rotated Q, rotated K, row statistics, then (n_rep > 1)
+// the float64 group sums, then the mask records
+size_t bwd_base_bytes(int B, int S, int Hq, int Hkv, int D, size_t* sum_off) {
+  const size_t Sp = (size_t)(S + F_BK - 1) / F_BK * F_BK;
+  const size_t f = ((size_t)B * Hq * Sp * D + (size_t)B * Hkv * Sp * D + (size_t)B * Hq * Sp * 2) *
+                   sizeof(float);
+  *sum_off = al256(f);
+  return *sum_off + (Hq > Hkv ? (size_t)B * S * Hkv * D * 2 * sizeof(double) : 0);
+}
+
+template <int D, int MODE>
+void launch_bwd_kernels(const BwdArgs& a, float* qrot, float* krot, float* stats, double* sum64,
+                        int Sp, int n_rep, int bm_pos, int nqb, unsigned nqblk, unsigned nkblk,
+                        const MaskRec& mr) {
+  const int32_t* mask = a.doc ? a.doc : a.kvalid;
+  KF_LAUNCH("bwd_dq_f32", (bwd_dq_f32_kernel<D, MODE>), dim3(nqblk), dim3(256), 0, a.stream,
+            qrot, krot, (const float*)a.v, a.cos, a.sin, (const float*)a.dout, stats,
+            (float*)a.dq, a.S, Sp, a.Hq, a.Hkv, n_rep, bm_pos, nqb, a.causal, a.scale,
+            a.scale * kLog2e, mask, mr.ranges, mr.first_valid, mr.nt32);
+  KF_LAUNCH("bwd_dkdv_f32", (bwd_dkdv_f32_kernel<D, MODE>), dim3(nkblk), dim3(256), 0, a.stream,
+            qrot, krot, (const float*)a.v, a.cos, a.sin, (const float*)a.dout, stats, sum64,
+            (float*)a.dk, (float*)a.dv, a.S, Sp, a.Hq, a.Hkv, n_rep, a.causal, a.scale,
+            a.scale * kLog2e, mask, mr.ranges, mr.first_valid, mr.nt32);
 }
 
 template <int D>
@@ -632,10 +925,12 @@ int bwd_f32_t(const BwdArgs& a, void* workspace) {
   const int64_t nqblk = (int64_t)nqb * a.B * a.Hkv;
   const int64_t nkblk = (int64_t)(Sp / F_BK) * a.B * a.Hkv;
   KF_CHECK_ARG(nqblk < (1LL << 31) && nkblk < (1LL << 31), "grid too large");
+  size_t sum_off = 0;
+  const size_t base = bwd_base_bytes(a.B, a.S, a.Hq, a.Hkv, D, &sum_off);
   float* qrot = (float*)workspace;
   float* krot = qrot + (size_t)a.B * a.Hq * Sp * D;
   float* stats = krot + (size_t)a.B * a.Hkv * Sp * D;
-  double* sum64 = (double*)(stats + (size_t)a.B * a.Hq * Sp * 2);
+  double* sum64 = (double*)((char*)workspace + sum_off);
   const int64_t qss = (int64_t)a.Hq * D, kss = (int64_t)a.Hkv * D;
   int rc = launch_rows<D>((const float*)a.q, a.S * qss, qss, D, a.cos, a.sin, qrot, a.B, a.S, Sp,
                           a.Hq, 1, a.stream);
@@ -647,14 +942,22 @@ int bwd_f32_t(const BwdArgs& a, void* workspace) {
   KF_LAUNCH("stats_f32", (stats_f32_kernel<D>), dim3((unsigned)((rows + 15) / 16)), dim3(256), 0,
             a.stream, (const float*)a.out, (const float*)a.dout, a.lse, stats, a.S, Sp, a.Hq,
             rows);
-  KF_LAUNCH("bwd_dq_f32", (bwd_dq_f32_kernel<D>), dim3((unsigned)nqblk), dim3(256), 0, a.stream,
-            qrot, krot, (const float*)a.v, a.cos, a.sin, (const float*)a.dout, stats,
-            (float*)a.dq, a.S, Sp, a.Hq, a.Hkv, n_rep, bm_pos, nqb, a.causal, a.scale,
-            a.scale * kLog2e);
-  KF_LAUNCH("bwd_dkdv_f32", (bwd_dkdv_f32_kernel<D>), dim3((unsigned)nkblk), dim3(256), 0,
-            a.stream, qrot, krot, (const float*)a.v, a.cos, a.sin, (const float*)a.dout, stats,
-            sum64, (float*)a.dk, (float*)a.dv, a.S, Sp, a.Hq, a.Hkv, n_rep, a.causal, a.scale,
-            a.scale * kLog2e);
+  const int mode = mask_mode_of(a.doc, a.kvalid);
+  MaskRec mr{nullptr, nullptr, 0};
+  if (mode != MASK_NONE) {
+    mr = mask_rec(workspace, base, a.B, a.S);
+    rc = launch_mask_prep(a.doc ? a.doc : a.kvalid, mode, a.B, a.S, mr, a.stream);
+    if (rc) return rc;
+  }
+  if (mode == MASK_DOC)
+    launch_bwd_kernels<D, MASK_DOC>(a, qrot, krot, stats, sum64, Sp, n_rep, bm_pos, nqb,
+                                    (unsigned)nqblk, (unsigned)nkblk, mr);
+  else if (mode == MASK_KPM)
+    launch_bwd_kernels<D, MASK_KPM>(a, qrot, krot, stats, sum64, Sp, n_rep, bm_pos, nqb,
+                                    (unsigned)nqblk, (unsigned)nkblk, mr);
+  else
+    launch_bwd_kernels<D, MASK_NONE>(a, qrot, krot, stats, sum64, Sp, n_rep, bm_pos, nqb,
+                                     (unsigned)nqblk, (unsigned)nkblk, mr);
   KF_CHECK_LAUNCH();
   return KF_OK;
 }
@@ -665,9 +968,13 @@ bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 bool fwd_f32_supported(const FwdArgs& a) {
   if (a.dtype != F32 || (a.D != 64 && a.D != 128)) return false;
-  if (a.doc || a.kvalid || a.rot) return false;
+  if (a.rot || (a.doc && a.kvalid)) return false;
   if (a.Sq < 1 || a.Sk < 1 || a.Hkv < 1 || a.Hq % a.Hkv) return false;
   if (a.Hq / a.Hkv > F_ROWS) return false;
+  // an explicit mask: causal self-attention (as the C ABI checks), within the tile list
+  if ((a.doc || a.kvalid) &&
+      (!a.causal || a.Sq != a.Sk || a.k_rotated || (a.Sk + F_BN - 1) / F_BN > F_MAX_TILES))
+    return false;
   if (!al16(a.q) || !al16(a.k) || !al16(a.v) || !al16(a.out) || !al16(a.cos) || !al16(a.sin))
     return false;
   if ((a.ksb | a.kss | a.ksh | a.vsb | a.vss | a.vsh) & 3) return false;
@@ -677,7 +984,7 @@ bool fwd_f32_supported(const FwdArgs& a) {
 }
 
 size_t fwd_f32_workspace(int B, int Sk, int Hkv, int D) {
-  return (size_t)B * Hkv * ((Sk + F_BK - 1) / F_BK * F_BK) * D * sizeof(float);
+  return al256(fwd_krot_bytes(B, Sk, Hkv, D)) + mask_rec_bytes(B, Sk);
 }
 
 int fwd_f32(const FwdArgs& a, void* workspace) {
@@ -686,18 +993,17 @@ int fwd_f32(const FwdArgs& a, void* workspace) {
 
 bool bwd_f32_supported(const BwdArgs& a) {
   if (a.dtype != F32 || (a.D != 64 && a.D != 128)) return false;
-  if (a.doc || a.kvalid || a.rot) return false;
+  if (a.rot || (a.doc && a.kvalid)) return false;
   if (a.S < 1 || a.Hkv < 1 || a.Hq % a.Hkv) return false;
   if (a.Hq / a.Hkv > F_ROWS || (int64_t)a.Hq * a.D > (1 << 24)) return false;
+  if ((a.doc || a.kvalid) && (!a.causal || (a.S + F_BN - 1) / F_BN > F_MAX_TILES)) return false;
   return al16(a.q) && al16(a.k) && al16(a.v) && al16(a.cos) && al16(a.sin) && al16(a.out) &&
          al16(a.dout) && al16(a.dq) && al16(a.dk) && al16(a.dv);
 }
 
 size_t bwd_f32_workspace(int B, int S, int Hq, int Hkv, int D) {
-  const size_t Sp = (size_t)(S + F_BK - 1) / F_BK * F_BK;
-  return ((size_t)B * Hq * Sp * D + (size_t)B * Hkv * Sp * D + (size_t)B * Hq * Sp * 2) *
-             sizeof(float) +
-         (Hq > Hkv ? (size_t)B * S * Hkv * D * 2 * sizeof(double) : 0);
+  size_t sum_off = 0;
+  return al256(bwd_base_bytes(B, S, Hq, Hkv, D, &sum_off)) + mask_rec_bytes(B, S);
 }
 
 int bwd_f32(const BwdArgs& a, void* workspace) {

@@ -6,8 +6,8 @@ The reference trains in float32 when ``mixed_precision = "fp32"``
 rounds below it.  Checked here against the float64 oracle on the same inputs
 with the north star's float32 bound, max-abs 1e-5 on the output, the LSE and
 every gradient element; the launches named by the library's kernel timer are
-the fp32 MFMA ones, not the generic kernels (which keep float32 with explicit
-masks and other head sizes, tested in the other files).
+the fp32 MFMA ones, not the generic kernels (which keep float32 for other
+head sizes and both explicit masks at once, tested in the other files).
 """
 
 from __future__ import annotations
@@ -129,6 +129,68 @@ def test_longer_rows():
     check_out(out, o_ref, TOL, "out")
     check_out(lse, l_ref, TOL, "lse")
     dq_r, dk_r, dv_r = ref.attention_bwd(q, k, v, cos, sin, do)
+    check_grad(dq, dq_r, F32, "dq")
+    check_grad(dk, dk_r, F32, "dk", group=Hq // Hkv)
+    check_grad(dv, dv_r, F32, "dv", group=Hq // Hkv)
+
+
+def _doc_ids(B, S, seed):
+    g = torch.Generator().manual_seed(seed)
+    cuts = torch.sort(torch.randint(1, S, (B, 5), generator=g), dim=1).values
+    pos = torch.arange(S).expand(B, S)
+    return (pos[:, :, None] >= cuts[:, None, :]).sum(-1).to(torch.int32)
+
+
+def _key_padding(B, S, layout, seed=0):
+    m = torch.ones(B, S, dtype=torch.bool)
+    g = torch.Generator().manual_seed(seed)
+    for b in range(B):
+        if layout == "leading":       # rows before the first valid key are guarded
+            m[b, : 45 + 29 * b] = False
+        elif layout == "random":
+            m[b] = torch.rand(S, generator=g) > 0.3
+        elif layout == "none_valid":  # an all-padded row: every row guarded
+            m[b] = b % 2 == 1
+        elif layout == "trailing":
+            m[b, S - 50 - 7 * b:] = False
+    return m
+
+
+# B, S, Hq, Hkv, D, mask
+MASKED = [
+    (2, 300, 8, 2, 128, "doc"),
+    (1, 333, 4, 4, 64, "doc"),
+    (1, 200, 32, 1, 128, "doc"),
+    (2, 300, 8, 2, 128, "leading"),
+    (2, 257, 6, 2, 64, "random"),
+    (2, 160, 4, 2, 128, "none_valid"),
+    (2, 190, 8, 1, 128, "trailing"),
+]
+
+
+@pytest.mark.parametrize("case", MASKED, ids=lambda c: "-".join(map(str, c)))
+def test_explicit_masks(case):
+    """Packed documents and key padding (guarded rows included) on the fp32
+    kernels: out, LSE and gradients against the oracle with the explicit mask."""
+    B, S, Hq, Hkv, D, kind = case
+    announce(f"fp32 masked {case}")
+    q, k, v, do, cos, sin = _inputs(B, S, Hq, Hkv, D, seed=50)
+    if kind == "doc":
+        masks = {"doc_ids": _doc_ids(B, S, 51)}
+    else:
+        masks = {"key_padding_mask": _key_padding(B, S, kind, 52)}
+    dev_masks = {n: t.to(DEV) for n, t in masks.items()}
+    args = [t.to(DEV) for t in (q, k, v, cos, sin)]
+    with _lib.KernelTimer() as t:
+        out, lse = ops.fwd_raw(*args, causal=True, k_rotated=False, **dev_masks)
+        dq, dk, dv = ops.bwd_raw(*args, out, lse, do.to(DEV), causal=True, **dev_masks)
+        torch.cuda.synchronize()
+    ran = set(t.stats)
+    assert FWD | BWD <= ran and not ran & GENERIC, ran
+    o_ref, l_ref = ref.attention_fwd(q, k, v, cos, sin, causal=True, **masks)
+    check_out(out, o_ref, TOL, "out")
+    check_out(lse, l_ref, TOL, "lse")
+    dq_r, dk_r, dv_r = ref.attention_bwd(q, k, v, cos, sin, do, causal=True, **masks)
     check_grad(dq, dq_r, F32, "dq")
     check_grad(dk, dk_r, F32, "dk", group=Hq // Hkv)
     check_grad(dv, dv_r, F32, "dv", group=Hq // Hkv)
