@@ -283,7 +283,9 @@ using mfma::MASK_NONE;
 constexpr int F_MAX_TILES = 4096;  // 32-position tiles of a batch row (S <= 131072)
 
 // Per batch row: MASK_DOC the [min, max] id of each 32-position tile;
-// MASK_KPM the first valid key (INT_MAX when none).  One workgroup per row.
+// MASK_KPM the first valid key (INT_MAX when none; -1 when every key is valid,
+// which the kernels then treat as plain causal attention).  One workgroup per
+// row.
 __global__ __launch_bounds__(256) void mask_prep_f32_kernel(const int32_t* __restrict__ mask,
                                                             int mode, int S, int nt,
                                                             int2* __restrict__ ranges,
@@ -300,17 +302,22 @@ __global__ __launch_bounds__(256) void mask_prep_f32_kernel(const int32_t* __res
       ranges[(int64_t)blockIdx.x * nt + t] = make_int2(lo, hi);
     }
   } else {
-    if (threadIdx.x == 0) sf = INT_MAX;
+    __shared__ int sn;
+    if (threadIdx.x == 0) {
+      sf = INT_MAX;
+      sn = 0;
+    }
     __syncthreads();
-    int f = INT_MAX;
+    int f = INT_MAX, n = 0;
     for (int j = threadIdx.x; j < S; j += 256)
       if (mrow[j] != 0) {
-        f = j;
-        break;
+        f = min(f, j);
+        ++n;
       }
     atomicMin(&sf, f);
+    atomicAdd(&sn, n);
     __syncthreads();
-    if (threadIdx.x == 0) first_valid[blockIdx.x] = sf;
+    if (threadIdx.x == 0) first_valid[blockIdx.x] = sn == S ? -1 : sf;
   }
 }
 
@@ -355,6 +362,7 @@ struct KeyWalk {
   const int32_t* mrow;  // the batch row's mask (doc ids or key validity)
   int n, fv, di;        // tiles; first valid key (MASK_KPM); this lane's row's document
   bool guarded;         // this lane's row attends every key (MASK_KPM)
+  bool plain;           // MASK_KPM with every key valid: plain causal attention
 };
 template <int MODE>
 __device__ __forceinline__ KeyWalk<MODE> key_walk(const RowInfo& ri, int kend_causal, int S,
@@ -362,11 +370,13 @@ __device__ __forceinline__ KeyWalk<MODE> key_walk(const RowInfo& ri, int kend_ca
                                                   const int2* ranges, const int* first_valid,
                                                   int nt32, uint16_t* list, int* count, int w,
                                                   int lane) {
-  KeyWalk<MODE> k{nullptr, (kend_causal + F_BN - 1) / F_BN, 0, 0, false};
+  KeyWalk<MODE> k{nullptr, (kend_causal + F_BN - 1) / F_BN, 0, 0, false, MODE == MASK_NONE};
   if (MODE == MASK_NONE) return k;
   k.mrow = mask + (int64_t)ri.b * S;
   if (MODE == MASK_KPM) {
-    k.fv = first_valid[ri.b];
+    const int fv = first_valid[ri.b];
+    k.plain = fv < 0;
+    k.fv = max(fv, 0);
     k.guarded = ri.pos < k.fv;
     if (ri.p0 < k.fv) k.n = (S + F_BN - 1) / F_BN;
   } else {
@@ -449,7 +459,7 @@ __global__ __launch_bounds__(256, 2) void fwd_f32_kernel(
     scores2<D>(tK, qr, c16, g, s0, s1);
 
     const int k0 = t * F_BN;
-    if (MODE == MASK_NONE) {
+    if (kw.plain) {
       if ((causal && k0 + F_BN - 1 > ri.p0) || k0 + F_BN > Sk) {
         const int lim = (causal ? min(ri.pos, Sk - 1) : Sk - 1) - k0;
 #pragma unroll
@@ -585,14 +595,14 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_f32_kernel(
     scores2<D>(tK, qr, c16, g, s0, s1);
     scores2<D>(tV, dr, c16, g, d0, d1);
     const int k0 = t * F_BN;
-    const bool edge = MODE != MASK_NONE || (causal && k0 + F_BN - 1 > ri.p0) || k0 + F_BN > S;
+    const bool edge = !kw.plain || (causal && k0 + F_BN - 1 > ri.p0) || k0 + F_BN > S;
     const int lim = (causal ? min(ri.pos, S - 1) : S - 1) - k0;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       float p0 = fast_exp2(__builtin_fmaf(s0[r], scale_log2, nl));
       float p1 = fast_exp2(__builtin_fmaf(s1[r], scale_log2, nl));
       if (edge) {
-        if (MODE == MASK_NONE) {
+        if (kw.plain) {
           p0 = 4 * g + r > lim ? 0.f : p0;
           p1 = 16 + 4 * g + r > lim ? 0.f : p1;
         } else {
@@ -648,7 +658,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dkdv_f32_kernel(
   // sequence) see this key, and so do rows from kkey on (INT_MAX: padding key)
   int fvk = 0, kkey = INT_MAX;
   if (MODE == MASK_KPM) {
-    const int fv = first_valid[b];
+    const int fv = max(first_valid[b], 0);  // (-1: every key valid)
     ng = fv >= S ? t0 : min((fv + F_BN - 1) / F_BN, t0);  // guarded rows' tiles below t0
     per += ng;
     fvk = kvalid ? fv : 0;

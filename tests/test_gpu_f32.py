@@ -153,6 +153,8 @@ def _key_padding(B, S, layout, seed=0):
             m[b] = b % 2 == 1
         elif layout == "trailing":
             m[b, S - 50 - 7 * b:] = False
+        elif layout == "row1_only":   # batch row 0 all valid (plain causal), row 1 padded
+            m[b, 100:] = b == 0
     return m
 
 
@@ -165,6 +167,7 @@ MASKED = [
     (2, 257, 6, 2, 64, "random"),
     (2, 160, 4, 2, 128, "none_valid"),
     (2, 190, 8, 1, 128, "trailing"),
+    (2, 230, 8, 2, 128, "row1_only"),
 ]
 
 
