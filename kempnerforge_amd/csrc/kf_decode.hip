@@ -15,8 +15,9 @@
 // With QK-norm weights the per-head RMSNorm of q_new and k_new (the
 // reference's q_norm / k_norm, applied before RoPE) happens where the rows
 // are loaded, instead of in separate launches.
-// Shapes outside the fast path (dtype other than bf16 / fp16, D not in {64, 128}, or
-// n_rep > 16) use decode_generic: one wavefront per (b, hq).
+// float32 with D in {64, 128} and n_rep <= 16 appends here and decodes on the
+// fp32 matrix cores (decode_f32, kf_f32.hip); other shapes (D not in {64, 128},
+// or n_rep > 16) use decode_generic: one wavefront per (b, hq).
 #include "kf_common.h"
 #include "kf_internal.h"
 #include "kf_mfma.h"
@@ -759,6 +760,8 @@ int decode_typed(const DecodeArgs& a, void* workspace) {
                         (T*)a.v_cache, a.lens, 0, a.rope_row_offset, a.rope_rows, a.max_len, a.B,
                         1, a.Hkv, a.Smax, a.D, a.stream, a.k_norm_w, a.norm_eps);
   if (rc) return rc;
+  if (__is_same(T, float) && decode_f32_supported(a))
+    return decode_f32(a, workspace, decode_slots(a.B, a.Hkv));
   KF_LAUNCH("decode_generic", decode_generic_kernel<T>, dim3((a.B * a.Hq + 3) / 4), dim3(256), 0,
                      a.stream, (const T*)a.q_new, a.cos, a.sin, a.rope_row_offset, a.rope_rows,
                      a.max_len, (const T*)a.k_cache, (const T*)a.v_cache, a.lens, (T*)a.out, a.B,

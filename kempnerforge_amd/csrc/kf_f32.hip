@@ -102,10 +102,10 @@ __device__ __forceinline__ f32x4 to_f32x4(const f64x4& x) {
 // instructions.  Rows at or past rows_valid repeat row rows_valid - 1 (finite
 // values, which the callers' masks multiply by zero).  Completion: the
 // caller's lds_copy_wait and barrier.
-template <int D>
+template <int D, int ROWS = F_BN>
 __device__ __forceinline__ void tile_dma(const float* g, uint32_t ld, float* lds, int w, int lane,
                                          int rows_valid) {
-  constexpr int R = D / 4, PER = F_BN * R / 64 / 4;
+  constexpr int R = D / 4, PER = ROWS * R / 64 / 4;
   asm volatile("" : "+v"(lane));  // offsets recomputed per call, not kept live across the loop
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
@@ -809,6 +809,225 @@ __global__ __launch_bounds__(256, 2) void bwd_dkdv_f32_kernel(
   }
 }
 
+// QK-norm of one element: x / rms(row) * w, the row's sum of squares ss
+// (RMSNorm in float32, kempnerforge/model/norm.py)
+__device__ __forceinline__ float rms_scale_f32(float x, float ss, int D, float eps, float w) {
+  const float r = rsqrtf(ss / (float)D + eps);
+  return (x * r) * w;
+}
+
+// ------------------------------------------------------------------ decode
+// One new token per sequence against the KV cache (after kv_append has
+// written the rotated new key and value at position lens[b]): split-K over
+// the cache rows.  Workgroup = one (sequence, KV head, split) item, the
+// group's n_rep <= 16 query heads as the 16 columns of S^T = K·q^T; per step
+// 64 keys, 16 per wavefront: the lane's K row chunks straight from HBM (one
+// step ahead, in registers) as the A operand, V rows by direct loads into LDS
+// (double-buffered) for O^T += V^T·P^T.  The wavefronts' states combine
+// through LDS into one partial (unnormalised o, max, sum) per item;
+// decode_merge_f32 combines an item's splits.
+constexpr int DEC_KEYS = 64;  // keys per step (4 wavefronts x 16)
+
+template <int D, bool QKN>
+__global__ __launch_bounds__(256, 2) void decode_f32_kernel(
+    const float* __restrict__ q_new, const float* __restrict__ cos, const float* __restrict__ sin,
+    int64_t row_offset, int64_t rope_rows, int max_len, const float* kc, const float* vc,
+    const int32_t* __restrict__ lens, float* __restrict__ opart, float* __restrict__ mlpart,
+    int Hq, int Hkv, int Smax, int n_rep, int nsplit, float scale_log2,
+    const float* __restrict__ qnw, float eps) {
+  constexpr int NJ = D / 16, NB = D / 16;
+  __shared__ __attribute__((aligned(16))) float sV[2][DEC_KEYS * D];
+  __shared__ float sM[4][16], sL[4][16];
+
+  const int lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15, w = wave_id();
+  const int item = blockIdx.x, pair = item / nsplit, split = item % nsplit;
+  const int b = pair / Hkv, hk = pair % Hkv;
+  const int len = lens[b];
+  const int64_t trow = (int64_t)len - row_offset;
+  const bool ok = len >= 0 && len < max_len && trow >= 0 && trow < rope_rows;
+  const int L = ok ? len + 1 : 0;
+  const int per = (L + nsplit - 1) / nsplit;
+  const int chunk = (per + DEC_KEYS - 1) / DEC_KEYS * DEC_KEYS;
+  const int lo = split * chunk, hi = min(L, lo + chunk);
+  float* op = opart + (int64_t)item * n_rep * D;
+  float* mp = mlpart + (int64_t)item * n_rep * 2;
+  if (lo >= hi) {  // nothing in this split: an empty partial
+    if (threadIdx.x < n_rep) {
+      mp[2 * threadIdx.x] = -INFINITY;
+      mp[2 * threadIdx.x + 1] = 0.f;
+    }
+    return;
+  }
+  const int nsteps = (hi - lo + DEC_KEYS - 1) / DEC_KEYS;
+  const float* kb = kc + ((int64_t)b * Hkv + hk) * Smax * D;
+  const float* vb = vc + ((int64_t)b * Hkv + hk) * Smax * D;
+  auto stage_v = [&](int i, int buf) {
+    const int k0 = lo + i * DEC_KEYS;
+    tile_dma<D, DEC_KEYS>(vb + (int64_t)k0 * D, (uint32_t)D, sV[buf], w, lane, hi - k0);
+  };
+  // this lane's K row chunks for step i (rows past hi repeat hi - 1)
+  auto load_k = [&](int i, f32x4* x) {
+    const int key = min(lo + i * DEC_KEYS + 16 * w + c16, hi - 1);
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) x[j] = *(const f32x4*)(kb + (int64_t)key * D + 4 * chunk_of<D>(j, g));
+  };
+  stage_v(0, 0);
+  f32x4 kx[NJ];
+  load_k(0, kx);
+
+  // the query column c16 (head hk n_rep + c16): QK-norm, then RoPE at trow
+  f32x4 qx[NJ];
+  {
+    const bool hv = c16 < n_rep;
+    load_row_share<D>(q_new + ((int64_t)b * Hq + hk * n_rep + min(c16, n_rep - 1)) * D, cos, sin,
+                      0, g, hv, false, qx);
+    if (QKN) {
+      float ss = 0.f;
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) ss += qx[j][e] * qx[j][e];
+      ss = quad_sum(ss);
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          qx[j][e] = rms_scale_f32(qx[j][e], ss, D, eps, qnw[4 * chunk_of<D>(j, g) + e]);
+    }
+    if (hv) {
+#pragma unroll
+      for (int j = 0; j < NJ / 2; ++j) {
+        const int64_t o = trow * (D / 2) + 4 * chunk_of<D>(j, g);
+        rope4(qx[j], qx[j + NJ / 2], *(const f32x4*)(cos + o), *(const f32x4*)(sin + o));
+      }
+    }
+  }
+
+  float m = -INFINITY, l = 0.f;
+  f32x4 o[NB];
+#pragma unroll
+  for (int db = 0; db < NB; ++db) o[db] = zero4();
+  mfma::lds_copy_wait();
+  __syncthreads();
+
+  for (int i = 0; i < nsteps; ++i) {
+    const int buf = i & 1;
+    f32x4 kn[NJ];
+    if (i + 1 < nsteps) {
+      stage_v(i + 1, buf ^ 1);
+      load_k(i + 1, kn);
+    }
+    // S^T for this wavefront's 16 keys: C[key 4g + r][head c16]
+    f32x4 s = zero4();
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) s = mma(kx[j][e], qx[j][e], s);
+    // (the A operand is K[key c16][d]: the lane's own row chunks)
+    const int kbase = lo + i * DEC_KEYS + 16 * w;
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      s[r] = kbase + 4 * g + r < hi ? s[r] : -INFINITY;
+      tmax = fmaxf(tmax, s[r]);
+    }
+    tmax = quad_max(tmax) * scale_log2;
+    const float mnew = fmaxf(m, tmax);
+    const float mref = mnew == -INFINITY ? 0.f : mnew;  // a wavefront's keys may all lie past hi
+    const float alpha = fast_exp2(m - mref);
+    m = mnew;
+    l *= alpha;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      s[r] = fast_exp2(__builtin_fmaf(s[r], scale_log2, -mref));
+      l += s[r];
+    }
+    // O^T += V^T P^T over the 16 keys: MFMA kk contracts key 16w + 4g + kk
+    const float* tV = sV[buf];
+#pragma unroll
+    for (int db = 0; db < NB; ++db) {
+      f32x4 f = zero4();
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk)
+        f = mma(tel<D>(tV, 16 * w + 4 * g + kk, 16 * db + c16), s[kk], f);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) o[db][r] = __builtin_fmaf(o[db][r], alpha, f[r]);
+    }
+    if (i + 1 < nsteps) {
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) kx[j] = kn[j];
+    }
+    mfma::lds_copy_wait();
+    __syncthreads();
+  }
+
+  // combine the 4 wavefronts: O^T slices through the (now free) V buffers
+  l = quad_sum(l);
+  float* sO = sV[0];  // [4][D][16]
+#pragma unroll
+  for (int db = 0; db < NB; ++db)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) sO[(w * D + 16 * db + 4 * g + r) * 16 + c16] = o[db][r];
+  if (g == 0) {
+    sM[w][c16] = m;
+    sL[w][c16] = l;
+  }
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < n_rep * D; idx += 256) {
+    const int h = idx / D, d = idx % D;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) mx = fmaxf(mx, sM[v][h]);
+    float acc = 0.f, lt = 0.f;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const float wgt = sM[v][h] == -INFINITY ? 0.f : fast_exp2(sM[v][h] - mx);
+      acc += wgt * sO[(v * D + d) * 16 + h];
+      lt += wgt * sL[v][h];
+    }
+    op[h * D + d] = acc;
+    if (d == 0) {
+      mp[2 * h] = mx;
+      mp[2 * h + 1] = lt;
+    }
+  }
+}
+
+// out[b, hq] = the splits' partials combined (max and sums in log2 units);
+// NaN for a sequence whose length fails the checks.  One wavefront per row.
+template <int D>
+__global__ __launch_bounds__(256) void decode_merge_f32_kernel(
+    const float* __restrict__ opart, const float* __restrict__ mlpart,
+    const int32_t* __restrict__ lens, float* __restrict__ out, int B, int Hq, int Hkv,
+    int nsplit, int max_len, int64_t row_offset, int64_t rope_rows) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (row >= B * Hq) return;
+  const int b = row / Hq, hq = row % Hq, n_rep = Hq / Hkv, hk = hq / n_rep, h = hq % n_rep;
+  const int len = lens[b];
+  const int64_t trow = (int64_t)len - row_offset;
+  float* orow = out + (int64_t)row * D;
+  if (!(len >= 0 && len < max_len && trow >= 0 && trow < rope_rows)) {
+    for (int d = lane; d < D; d += 64) orow[d] = NAN;
+    return;
+  }
+  const int64_t item0 = ((int64_t)b * Hkv + hk) * nsplit;
+  float mx = -INFINITY;
+  for (int s = 0; s < nsplit; ++s) mx = fmaxf(mx, mlpart[((item0 + s) * n_rep + h) * 2]);
+  float acc[D / 64] = {}, lt = 0.f;
+  for (int s = 0; s < nsplit; ++s) {
+    const float* ml = mlpart + ((item0 + s) * n_rep + h) * 2;
+    if (ml[1] == 0.f) continue;
+    const float wgt = fast_exp2(ml[0] - mx);
+    lt += wgt * ml[1];
+    const float* o = opart + ((item0 + s) * n_rep + h) * D;
+#pragma unroll
+    for (int k = 0; k < D / 64; ++k) acc[k] += wgt * o[64 * k + lane];
+  }
+  const float inv = 1.f / lt;
+#pragma unroll
+  for (int k = 0; k < D / 64; ++k) orow[64 * k + lane] = acc[k] * inv;
+}
+
 template <int D>
 int launch_rows(const float* src, int64_t sb, int64_t ss, int64_t sh, const float* cos,
                 const float* sin, float* dst, int B, int S, int Sp, int H, int rot,
@@ -1018,6 +1237,45 @@ size_t bwd_f32_workspace(int B, int S, int Hq, int Hkv, int D) {
 
 int bwd_f32(const BwdArgs& a, void* workspace) {
   return a.D == 128 ? bwd_f32_t<128>(a, workspace) : bwd_f32_t<64>(a, workspace);
+}
+
+
+bool decode_f32_supported(const DecodeArgs& a) {
+  if (a.dtype != F32 || (a.D != 64 && a.D != 128) || a.Hkv < 1 || a.Hq % a.Hkv) return false;
+  if (a.Hq / a.Hkv > 16) return false;
+  return al16(a.q_new) && al16(a.k_cache) && al16(a.v_cache) && al16(a.cos) && al16(a.sin) &&
+         al16(a.out);
+}
+
+int decode_f32(const DecodeArgs& a, void* workspace, size_t slots) {
+  const int n_rep = a.Hq / a.Hkv;
+  const int64_t pairs = (int64_t)a.B * a.Hkv;
+  const int nsplit = (int)(1 + (int64_t)(slots - pairs) / pairs);  // items fit the slots
+  const int64_t items = pairs * nsplit;
+  KF_CHECK_ARG(items < (1LL << 31) && (size_t)items <= slots, "decode grid too large");
+  float* opart = (float*)workspace;
+  float* mlpart = opart + slots * n_rep * a.D;
+  const bool qkn = a.q_norm_w != nullptr;
+  const float sl = a.scale * kLog2e;
+#define KF_DEC_F32(DD, Q)                                                                      \
+  KF_LAUNCH("decode_f32", (decode_f32_kernel<DD, Q>), dim3((unsigned)items), dim3(256), 0,    \
+            a.stream, (const float*)a.q_new, a.cos, a.sin, a.rope_row_offset, a.rope_rows,     \
+            a.max_len, (const float*)a.k_cache, (const float*)a.v_cache, a.lens, opart, mlpart, \
+            a.Hq, a.Hkv, a.Smax, n_rep, nsplit, sl, a.q_norm_w, a.norm_eps)
+  if (a.D == 128) {
+    if (qkn) KF_DEC_F32(128, true);
+    else KF_DEC_F32(128, false);
+  } else {
+    if (qkn) KF_DEC_F32(64, true);
+    else KF_DEC_F32(64, false);
+  }
+#undef KF_DEC_F32
+  KF_LAUNCH("decode_merge_f32",
+            (a.D == 128 ? decode_merge_f32_kernel<128> : decode_merge_f32_kernel<64>),
+            dim3((a.B * a.Hq + 3) / 4), dim3(256), 0, a.stream, opart, mlpart, a.lens,
+            (float*)a.out, a.B, a.Hq, a.Hkv, nsplit, a.max_len, a.rope_row_offset, a.rope_rows);
+  KF_CHECK_LAUNCH();
+  return KF_OK;
 }
 
 }  // namespace kf

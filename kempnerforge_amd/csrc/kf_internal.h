@@ -130,6 +130,11 @@ struct DecodeArgs {
   hipStream_t stream;
 };
 size_t decode_workspace(int B, int Hq, int Hkv, int D, int max_len);
+// float32 decode on the fp32 matrix cores (kf_f32.hip), after the caller's
+// append of the new token: split-K over at most `slots` partials of the
+// decode workspace's layout
+bool decode_f32_supported(const DecodeArgs& a);
+int decode_f32(const DecodeArgs& a, void* workspace, size_t slots);
 int decode(const DecodeArgs& a, void* workspace);
 // Allocation-free decode: the current device's copy of a static device array
 // of DECODE_SCRATCH_BYTES stands in for the workspace.

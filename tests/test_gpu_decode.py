@@ -47,7 +47,8 @@ def test_fixture():
     (torch.bfloat16, 2, 32, 1, 128, 500, 700, 800),  # n_rep 32 -> generic kernel
     (torch.bfloat16, 1, 64, 8, 128, 1000, 1300, 1400),  # 70B heads, n_rep 8
     (torch.bfloat16, 2, 64, 1, 64, 10, 90, 100),     # n_rep 64 -> generic kernel
-    (torch.float32, 2, 4, 2, 64, 10, 90, 100),       # fp32 -> generic kernel
+    (torch.float32, 2, 4, 2, 64, 10, 90, 100),       # fp32 matrix-core decode
+    (torch.float32, 2, 4, 2, 32, 10, 90, 100),       # fp32, D=32 -> generic kernel
     (torch.bfloat16, 2, 4, 2, 32, 10, 90, 100),      # D=32 -> generic kernel
 ], ids=lambda c: "-".join(map(str, c)))
 def test_shapes(cfg):

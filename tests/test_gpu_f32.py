@@ -197,3 +197,86 @@ def test_explicit_masks(case):
     check_grad(dq, dq_r, F32, "dq")
     check_grad(dk, dk_r, F32, "dk", group=Hq // Hkv)
     check_grad(dv, dv_r, F32, "dv", group=Hq // Hkv)
+
+
+# decode: B, Hq, Hkv, D, lo, hi, Smax
+DECODE = [
+    (3, 8, 8, 64, 1, 300, 400),        # MHA, D=64
+    (6, 16, 2, 128, 1022, 1025, 1100),
+    (40, 8, 2, 64, 900, 3100, 3200),   # many sequences: few splits each
+    (2, 8, 1, 128, 0, 3, 8),           # empty cache (len 0) and tiny
+    (2, 6, 2, 128, 10, 90, 100),       # n_rep 3: padded MFMA columns
+    (2, 16, 1, 128, 500, 700, 800),    # n_rep 16, the widest
+    (1, 64, 8, 128, 1000, 1300, 1400),
+]
+
+
+@pytest.mark.parametrize("cfg", DECODE, ids=lambda c: "-".join(map(str, c)))
+def test_decode(cfg):
+    """One decode step in float32 on the fp32 matrix cores (split-K over the
+    cache, then the merge): out within 1e-5 of the oracle, the new row written
+    to the cache bit for bit."""
+    B, Hq, Hkv, D, lo, hi, Smax = cfg
+    announce(f"fp32 decode {cfg}")
+    g = torch.Generator().manual_seed(4)
+    lens = torch.randint(lo, hi + 1, (B,), generator=g, dtype=torch.int32)
+    q = seeded((B, 1, Hq, D), 0, F32)
+    kn = seeded((B, 1, Hkv, D), 1, F32)
+    vn = seeded((B, 1, Hkv, D), 2, F32)
+    kc = seeded((B, Hkv, Smax, D), 5, F32)
+    vc = seeded((B, Hkv, Smax, D), 6, F32)
+    cos, sin = ref.rope_tables(D, Smax, 5e5)
+    kcd, vcd = kc.to(DEV), vc.to(DEV)
+    with _lib.KernelTimer() as t:
+        out = ops.decode_raw(q.to(DEV), kn.to(DEV), vn.to(DEV), kcd, vcd, lens.to(DEV),
+                             cos.to(DEV), sin.to(DEV), rope_row_offset=0,
+                             max_len=int(lens.max()) + 1)
+        torch.cuda.synchronize()
+    assert {"decode_f32", "decode_merge_f32"} <= set(t.stats) and "decode_generic" not in t.stats
+    o_ref, kc_ref, vc_ref = ref.decode_step(q, kn, vn, kc, vc, lens, cos, sin)
+    check_out(out, o_ref, TOL, "out")
+    assert torch.equal(kcd.cpu(), kc_ref) and torch.equal(vcd.cpu(), vc_ref)
+
+
+def test_decode_qk_norm_and_bad_length():
+    """The fused QK-norm decode in float32 against RMSNorm (the reference
+    module, float32) followed by the oracle's decode; then a sequence with an
+    out-of-range length: NaN output, caches untouched."""
+    from kempnerforge_amd.norm import RMSNorm
+
+    B, Hq, Hkv, D, Smax = 3, 8, 2, 128, 700
+    announce("fp32 decode qk-norm")
+    lens = torch.tensor([5, 333, 698], dtype=torch.int32)
+    qn = seeded((B, 1, Hq, D), 0, F32) * 3
+    kn = seeded((B, 1, Hkv, D), 1, F32) * 3
+    vn = seeded((B, 1, Hkv, D), 2, F32)
+    kc = seeded((B, Hkv, Smax, D), 3, F32)
+    vc = seeded((B, Hkv, Smax, D), 4, F32)
+    cos, sin = ref.rope_tables(D, Smax, 5e5)
+    qnorm, knorm = RMSNorm(D), RMSNorm(D)
+    with torch.no_grad():
+        g = torch.Generator().manual_seed(9)
+        qnorm.weight.copy_(1 + 0.1 * torch.randn(D, generator=g))
+        knorm.weight.copy_(1 + 0.1 * torch.randn(D, generator=g))
+    kcd, vcd = kc.to(DEV), vc.to(DEV)
+    out = ops.decode_raw(qn.to(DEV), kn.to(DEV), vn.to(DEV), kcd, vcd, lens.to(DEV),
+                         cos.to(DEV), sin.to(DEV), rope_row_offset=0, max_len=Smax,
+                         q_norm_weight=qnorm.weight.to(DEV), k_norm_weight=knorm.weight.to(DEV),
+                         norm_eps=qnorm.eps)
+    torch.cuda.synchronize()
+    with torch.no_grad():
+        qq, kk = qnorm(qn), knorm(kn)
+    o_ref, kc_ref, _ = ref.decode_step(qq, kk, vn, kc, vc, lens, cos, sin)
+    check_out(out, o_ref, TOL, "out")
+    for b in range(B):
+        L = int(lens[b])
+        check_out(kcd[b, :, L], kc_ref[b, :, L], TOL, "k written")
+    # lens[1] + 1 > max_len: NaN for that sequence and no cache write
+    lens = torch.tensor([10, 700, 20], dtype=torch.int32)
+    before = kcd.clone()
+    out = ops.decode_raw(qn.to(DEV), kn.to(DEV), vn.to(DEV), kcd, vcd, lens.to(DEV),
+                         cos.to(DEV), sin.to(DEV), rope_row_offset=0, max_len=Smax)
+    torch.cuda.synchronize()
+    assert torch.isnan(out[1]).all()
+    assert torch.isfinite(out[0]).all() and torch.isfinite(out[2]).all()
+    assert torch.equal(kcd[1], before[1])
