@@ -439,6 +439,14 @@ int kf_attn_capture(const void* q, const void* k, const void* v, const float* ro
     }
     return capture_probs_mfma(a, probs, workspace);
   }
+  if (fwd_f32_supported(a)) {
+    const size_t need = fwd_ws(a);
+    if (workspace_bytes < need || (need && !workspace)) {
+      set_error("workspace too small: need %zu bytes, got %zu", need, workspace_bytes);
+      return KF_ERR_WORKSPACE;
+    }
+    return capture_f32(a, probs, workspace);
+  }
   rc = fwd_generic(a);
   if (rc) return rc;
   return capture_probs_generic(a, lse, probs);

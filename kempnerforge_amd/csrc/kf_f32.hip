@@ -508,6 +508,102 @@ __global__ __launch_bounds__(256, 2) void fwd_f32_kernel(
   }
 }
 
+// ------------------------------------------------------------------ capture
+// The probabilities P = exp(s - lse) as float32 [B, Hq, Sq, Sk] after the
+// forward has written out and lse: the forward's rows and key walk recompute
+// S^T = K·Q^T per 32-key tile (K tiles only) and store each lane's row
+// segment; every tile the walk skips (right of the causal frontier, or whose
+// documents miss the rows') is written as zeros.
+template <int D, int MODE>
+__global__ __launch_bounds__(256, 2) void capture_f32_kernel(
+    const float* __restrict__ q, const float* __restrict__ cos, const float* __restrict__ sin,
+    const float* kt, int64_t kb_b, int64_t kb_h, int kld, const float* __restrict__ lse,
+    float* __restrict__ probs, int Sq, int Sk, int Hq, int Hkv, int n_rep, int bm_pos, int nqb,
+    int causal, float scale_log2, const int32_t* __restrict__ mask,
+    const int2* __restrict__ ranges, const int* __restrict__ first_valid, int nt32) {
+  constexpr int NJ = D / 16;
+  __shared__ __attribute__((aligned(16))) float sK[2][F_BN * D];
+  __shared__ uint16_t sList[MODE == MASK_DOC ? F_MAX_TILES : 1];
+  __shared__ int sCount;
+
+  const int lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15, w = wave_id();
+  const int logical = xcd_logical_id(blockIdx.x, gridDim.x, nqb);
+  const RowInfo ri = row_info(logical, nqb, Hkv, n_rep, bm_pos, Sq, w * 16 + c16);
+  const KeyWalk<MODE> kw =
+      key_walk<MODE>(ri, causal ? min(Sk, min(ri.p0 + bm_pos, Sq)) : Sk, Sk, bm_pos, mask,
+                     ranges, first_valid, nt32, sList, &sCount, w, lane);
+  auto tile_at = [&](int i) {
+    return MODE == MASK_DOC ? __builtin_amdgcn_readfirstlane((int)sList[i]) : i;
+  };
+  const float* kb = kt + (int64_t)ri.b * kb_b + (int64_t)ri.g * kb_h;
+  auto stage = [&](int t, int buf) {
+    const int k0 = t * F_BN;
+    tile_dma<D>(kb + (int64_t)k0 * kld, (uint32_t)kld, sK[buf], w, lane, Sk - k0);
+  };
+  if (kw.n > 0) stage(tile_at(0), 0);
+
+  f32x4 qr[NJ];
+  load_row_share<D>(q + (((int64_t)ri.b * Sq + ri.pos) * Hq + ri.hq) * D, cos, sin, ri.pos, g,
+                    ri.q_valid, true, qr);
+  const float nl = ri.q_valid ? -lse[((int64_t)ri.b * Hq + ri.hq) * Sq + ri.pos] * kLog2e : 0.f;
+  float* prow = probs + (((int64_t)ri.b * Hq + ri.hq) * Sq + ri.pos) * Sk;
+  const bool vec = (Sk & 3) == 0 && ((uintptr_t)probs & 15) == 0;  // rows 16-byte aligned
+  // four probabilities (or zeros) at keys key0.. of this lane's row
+  auto put4 = [&](int key0, const f32x4& x) {
+    if (!ri.q_valid) return;
+    if (vec && key0 + 3 < Sk) {
+      __builtin_nontemporal_store(x, (f32x4*)(prow + key0));
+    } else {
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        if (key0 + r < Sk) prow[key0 + r] = x[r];
+    }
+  };
+  mfma::lds_copy_wait();
+  __syncthreads();
+
+  for (int i = 0; i < kw.n; ++i) {
+    const int buf = i & 1, t = tile_at(i);
+    if (i + 1 < kw.n) stage(tile_at(i + 1), buf ^ 1);
+    f32x4 s0 = zero4(), s1 = zero4();
+    scores2<D>(sK[buf], qr, c16, g, s0, s1);
+    const int k0 = t * F_BN;
+    const int lim = (causal ? min(ri.pos, Sk - 1) : Sk - 1) - k0;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      bool v0, v1;
+      if (kw.plain) {
+        v0 = 4 * g + r <= lim;
+        v1 = 16 + 4 * g + r <= lim;
+      } else {
+        v0 = row_sees<MODE>(kw, k0, 4 * g + r, lim, Sk);
+        v1 = row_sees<MODE>(kw, k0, 16 + 4 * g + r, lim, Sk);
+      }
+      s0[r] = v0 ? fast_exp2(__builtin_fmaf(s0[r], scale_log2, nl)) : 0.f;
+      s1[r] = v1 ? fast_exp2(__builtin_fmaf(s1[r], scale_log2, nl)) : 0.f;
+    }
+    put4(k0 + 4 * g, s0);
+    put4(k0 + 16 + 4 * g, s1);
+    mfma::lds_copy_wait();
+    __syncthreads();
+  }
+  // zeros in the tiles the walk left out (the list is ascending)
+  const int ntot = (Sk + F_BN - 1) / F_BN;
+  int li = 0;
+  for (int t = 0; t < ntot; ++t) {
+    if (MODE == MASK_DOC) {
+      if (li < kw.n && tile_at(li) == t) {
+        ++li;
+        continue;
+      }
+    } else if (t < kw.n) {
+      continue;
+    }
+    put4(t * F_BN + 8 * g, zero4());
+    put4(t * F_BN + 8 * g + 4, zero4());
+  }
+}
+
 // ------------------------------------------------------------------ backward
 // Store a lane's share (d = 16 db + 4 g + r) of scale * G^T after the RoPE
 // backward at table row pos (the pair of d < D/2 is d + D/2, in block db + NB/2).
@@ -1218,6 +1314,40 @@ size_t fwd_f32_workspace(int B, int Sk, int Hkv, int D) {
 
 int fwd_f32(const FwdArgs& a, void* workspace) {
   return a.D == 128 ? fwd_f32_t<128>(a, workspace) : fwd_f32_t<64>(a, workspace);
+}
+
+int capture_f32(const FwdArgs& a, float* probs, void* workspace) {
+  int rc = fwd_f32(a, workspace);  // out, lse, and the rotated K / mask records it leaves
+  if (rc) return rc;
+  const int n_rep = a.Hq / a.Hkv, bm_pos = F_ROWS / n_rep;
+  const int nqb = (a.Sq + bm_pos - 1) / bm_pos;
+  const unsigned nblk = (unsigned)((int64_t)nqb * a.B * a.Hkv);
+  const float* kt = (const float*)a.k;
+  int64_t kb_b = a.ksb, kb_h = a.ksh, kld = a.kss;
+  if (!a.k_rotated) {
+    const int Skp = (a.Sk + F_BK - 1) / F_BK * F_BK;
+    kt = (const float*)workspace;
+    kb_h = (int64_t)Skp * a.D;
+    kb_b = a.Hkv * kb_h;
+    kld = a.D;
+  }
+  const int mode = mask_mode_of(a.doc, a.kvalid);
+  MaskRec mr{nullptr, nullptr, 0};
+  if (mode != MASK_NONE) mr = mask_rec(workspace, fwd_krot_bytes(a.B, a.Sk, a.Hkv, a.D), a.B, a.Sk);
+  const int32_t* mask = a.doc ? a.doc : a.kvalid;
+#define KF_CAP_F32(DD, M)                                                                        KF_LAUNCH("capture_f32", (capture_f32_kernel<DD, M>), dim3(nblk), dim3(256), 0, a.stream,                (const float*)a.q, a.cos, a.sin, kt, kb_b, kb_h, (int)kld, a.lse, probs, a.Sq,                  a.Sk, a.Hq, a.Hkv, n_rep, bm_pos, nqb, a.causal, a.scale * kLog2e, mask,                       mr.ranges, mr.first_valid, mr.nt32)
+  if (a.D == 128) {
+    if (mode == MASK_DOC) KF_CAP_F32(128, MASK_DOC);
+    else if (mode == MASK_KPM) KF_CAP_F32(128, MASK_KPM);
+    else KF_CAP_F32(128, MASK_NONE);
+  } else {
+    if (mode == MASK_DOC) KF_CAP_F32(64, MASK_DOC);
+    else if (mode == MASK_KPM) KF_CAP_F32(64, MASK_KPM);
+    else KF_CAP_F32(64, MASK_NONE);
+  }
+#undef KF_CAP_F32
+  KF_CHECK_LAUNCH();
+  return KF_OK;
 }
 
 bool bwd_f32_supported(const BwdArgs& a) {

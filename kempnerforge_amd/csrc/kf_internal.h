@@ -64,6 +64,9 @@ int capture_probs_generic(const FwdArgs& a, const float* lse, float* probs);
 bool fwd_f32_supported(const FwdArgs& a);
 size_t fwd_f32_workspace(int B, int Sk, int Hkv, int D);
 int fwd_f32(const FwdArgs& a, void* workspace);
+// out, lse (a.lse must be set) and the probabilities, float32 [B, Hq, Sq, Sk];
+// the workspace is fwd_f32's
+int capture_f32(const FwdArgs& a, float* probs, void* workspace);
 bool bwd_f32_supported(const BwdArgs& a);
 size_t bwd_f32_workspace(int B, int S, int Hq, int Hkv, int D);
 int bwd_f32(const BwdArgs& a, void* workspace);

@@ -280,3 +280,38 @@ def test_decode_qk_norm_and_bad_length():
     assert torch.isnan(out[1]).all()
     assert torch.isfinite(out[0]).all() and torch.isfinite(out[2]).all()
     assert torch.equal(kcd[1], before[1])
+
+
+# capture: B, S, Hq, Hkv, D, causal, mask
+CAPTURE = [
+    (1, 200, 8, 2, 128, True, None),
+    (2, 130, 4, 4, 64, False, None),
+    (1, 33, 6, 2, 128, True, None),      # Sk % 4 != 0: element stores
+    (1, 300, 8, 2, 128, True, "doc"),
+    (2, 160, 4, 2, 64, True, "leading"),
+]
+
+
+@pytest.mark.parametrize("case", CAPTURE, ids=lambda c: "-".join(map(str, c)))
+def test_capture(case):
+    """The probability capture in float32 (forward, then the probabilities
+    recomputed per tile): P within 1e-5 of the oracle, zeros where masked,
+    out within 1e-5."""
+    B, S, Hq, Hkv, D, causal, kind = case
+    announce(f"fp32 capture {case}")
+    q, k, v, _, cos, sin = _inputs(B, S, Hq, Hkv, D, seed=60)
+    masks = {}
+    if kind == "doc":
+        masks = {"doc_ids": _doc_ids(B, S, 61)}
+    elif kind is not None:
+        masks = {"key_padding_mask": _key_padding(B, S, kind, 62)}
+    dev_masks = {n: t.to(DEV) for n, t in masks.items()}
+    with _lib.KernelTimer() as t:
+        out, p, lse = ops.capture_raw(q.to(DEV), k.to(DEV), v.to(DEV), cos.to(DEV), sin.to(DEV),
+                                      causal=causal, k_rotated=False, **dev_masks)
+        torch.cuda.synchronize()
+    assert {"fwd_f32", "capture_f32"} <= set(t.stats) and not set(t.stats) & GENERIC, t.stats
+    o_ref, p_ref = ref.capture(q, k, v, cos, sin, causal=causal, **masks)
+    check_out(p, p_ref, TOL, "probs")
+    check_out(out, o_ref, TOL, "out")
+    assert (p.cpu()[p_ref == 0] == 0).all()  # masked entries exactly zero
