@@ -10,7 +10,8 @@ with P = B*Hq*S*(S+1)/2 causal (query, key) pairs (forward 4*D*P, backward
 Also reported: per-kernel HIP-event timings (the library brackets each launch
 on its own stream), the roofline of the dominant kernel, the forward alone
 (C2), the C3 step on packed documents (C3-doc; flops of same-document pairs
-only), with an all-True key_padding_mask (C3-kpm) and in float16 (C3-fp16), one
+only), with an all-True key_padding_mask (C3-kpm), in float16 (C3-fp16) and in
+float32 (C3-fp32; the decode and capture lines also carry float32 runs), one
 rank's share of the reference's TP = 4 training configs at S = 4096, the
 Llama-3-70B shape fwd+bwd (C5: B=1, S=16384, 64 query heads) and its
 2048-token probability capture (C5-cap), the KV-cache decode configuration C4
@@ -492,6 +493,18 @@ def run_full(args, torch, wl):
              "frac_of_hbm_peak": round(cap_b / cap_s / 1e9 / PEAK_HBM_GBPS, 4),
              "kernels_us": {n: round(s["avg_us"], 1) for n, s in kcap.items()},
              "capture_kernel_traffic": traffic.get("capture_probs@C5CAP")}
+    # the same capture on float32 inputs (the fp32 kernels: forward, then P)
+    cap32 = [t.float() for t in wl.c5_inputs()[6]]
+    Sc = C5["cap_tokens"]
+    cos5, sin5 = wl.c5_inputs()[4][:Sc], wl.c5_inputs()[5][:Sc]
+    cap32_step = lambda: wl.ops.capture_raw(*cap32, cos5, sin5, causal=True,  # noqa: E731
+                                            k_rotated=False)
+    cap32_s = timed(torch, cap32_step, 3, 10)
+    c5cap["fp32"] = {"config": "C5-cap with float32 q/k/v (the same seeded values)",
+                     "us": round(cap32_s * 1e6, 1),
+                     "kernels_us": {n: round(s["avg_us"], 1)
+                                    for n, s in kernel_stats(torch, cap32_step, 10).items()}}
+    del cap32
     wl.c5_free()
 
     # C4 decode
@@ -508,6 +521,18 @@ def run_full(args, torch, wl):
               "stream_kernel_GB/s": round(dec_bytes / (stream_us * 1e-6) / 1e9, 1)
               if stream_us else None,
               "stream_kernel_traffic": traffic.get("decode_stream@C4")}
+    # the same decode on float32 inputs and caches (twice the bytes)
+    qn4, kn4, vn4, kc4, vc4, _, lens4, cos4, sin4, Smax4, _ = wl.c4_inputs()
+    dec32 = [t.float() for t in (qn4, kn4, vn4, kc4, vc4)]
+    dec32_step = lambda: wl.ops.decode_raw(*dec32, lens4, cos4, sin4,  # noqa: E731
+                                           rope_row_offset=0, max_len=Smax4)
+    d32_s = timed(torch, dec32_step, SHORT_WARM, SHORT_STEPS)
+    decode["fp32"] = {"config": "C4 with float32 q/k/v and caches", "bytes": 2 * dec_bytes,
+                      "us_per_step": round(d32_s * 1e6, 1),
+                      "GB/s": round(2 * dec_bytes / d32_s / 1e9, 1),
+                      "kernels_us": {n: round(s["avg_us"], 1) for n, s in
+                                     kernel_stats(torch, dec32_step, SHORT_STEPS).items()}}
+    del dec32
 
     cpu = None
     if not args.no_cpu_baseline:
