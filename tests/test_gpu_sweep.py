@@ -4,7 +4,7 @@ The fixed-shape tests pin the cases each kernel was written around; this
 sweep draws shapes the kernels' tiling does not favour: lengths 1..700 (off the
 32-, 64- and 128-position tiles), n_rep 1..16 (odd groups included), head_dim
 64 and 128, several batch rows, causal and full attention, packed documents
-and key padding with random boundaries, bf16 and fp16.  Each case checks the
+and key padding with random boundaries, bf16, fp16 and fp32.  Each case checks the
 output and LSE, every gradient element (gpu_util.grad_bound, with the error
 that rounding P and dS to the operand type forces added to the bound: on these
 short rows it can exceed 2e-2 with otherwise exact arithmetic) and that dK / dV
@@ -132,6 +132,81 @@ def test_decode_sweep(case):
     vn = seeded((B, 1, Hkv, D), 900 + i, dtype)
     kc = seeded((B, Hkv, Smax, D), 1000 + i, dtype)
     vc = seeded((B, Hkv, Smax, D), 1100 + i, dtype)
+    cos, sin = ref.rope_tables(D, Smax, 5e5)
+    kcd, vcd = kc.to(DEV), vc.to(DEV)
+    out = ops.decode_raw(q.to(DEV), kn.to(DEV), vn.to(DEV), kcd, vcd, lens.to(DEV), cos.to(DEV),
+                         sin.to(DEV), rope_row_offset=0, max_len=Smax)
+    torch.cuda.synchronize()
+    o_ref, kc_ref, vc_ref = ref.decode_step(q, kn, vn, kc, vc, lens, cos, sin)
+    check_out(out, o_ref, TOL[dtype], "decode out")
+    assert torch.equal(kcd.cpu(), kc_ref) and torch.equal(vcd.cpu(), vc_ref)
+
+
+def _draw_f32_cases(n, seed=4242):
+    rng = random.Random(seed)
+    cases = []
+    for i in range(n):
+        D = rng.choice([64, 128])
+        Hkv = rng.choice([1, 2, 4])
+        n_rep = rng.choice([1, 2, 3, 4, 5, 8, 16, 32])
+        B = rng.choice([1, 2, 3])
+        S = rng.choice([1, 2, 31, 33, 63, 65, 127, 129, 191, 255, 257, 300, 383, 448, 511,
+                        513, 640, 700])
+        mask = rng.choice([None, None, "doc", "kpm"])
+        causal = True if mask else rng.random() < 0.75
+        cases.append((i, "fp32", B, S, Hkv * n_rep, Hkv, D, causal, mask))
+    return cases
+
+
+@pytest.mark.parametrize("case", _draw_f32_cases(24), ids=lambda c: "-".join(map(str, c)))
+def test_fp32_sweep(case):
+    """float32 on the fp32 matrix-core kernels: out, LSE and every gradient
+    element within 1e-5 of the float64 oracle (nothing below float32 is
+    rounded, so no operand allowance), the autograd and the raw backward the
+    same bits."""
+    i, _, B, S, Hq, Hkv, D, causal, mask = case
+    dtype = torch.float32
+    announce(f"fp32 sweep {case}")
+    q = seeded((B, S, Hq, D), 1300 + i, dtype)
+    k = seeded((B, S, Hkv, D), 1400 + i, dtype)
+    v = seeded((B, S, Hkv, D), 1500 + i, dtype)
+    do = seeded((B, S, Hq, D), 1600 + i, dtype)
+    cos, sin = ref.rope_tables(D, S, 5e5)
+    m = _mask_tensors(case, 1700 + i)
+    md = {n: t.to(DEV) for n, t in m.items()}
+    qd, kd, vd = (t.to(DEV).requires_grad_(True) for t in (q, k, v))
+    out = ops.attention(qd, kd, vd, cos.to(DEV), sin.to(DEV), causal=causal, **md)
+    out.backward(do.to(DEV))
+    _, lse = ops.fwd_raw(q.to(DEV), k.to(DEV), v.to(DEV), cos.to(DEV), sin.to(DEV),
+                         causal=causal, k_rotated=False, **md)
+    raw = ops.bwd_raw(q.to(DEV), k.to(DEV), v.to(DEV), cos.to(DEV), sin.to(DEV), out.detach(),
+                      lse, do.to(DEV), causal=causal, **md)
+    torch.cuda.synchronize()
+    o_ref, l_ref = ref.attention_fwd(q, k, v, cos, sin, causal=causal, **m)
+    check_out(out, o_ref, TOL[dtype], "out")
+    check_out(lse, l_ref, TOL[dtype], "lse")
+    grads = ref.attention_bwd(q, k, v, cos, sin, do, causal=causal, **m)
+    for got, want, name in zip((qd.grad, kd.grad, vd.grad), grads, ("dq", "dk", "dv")):
+        check_grad(got, want, dtype, name, group=Hq // Hkv if name != "dq" else 1)
+    for a, b in zip(raw, (qd.grad, kd.grad, vd.grad)):
+        assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("case", [(i, "fp32", *c[2:]) for i, c in
+                                  enumerate(_draw_decode_cases(8, seed=91))],
+                         ids=lambda c: "-".join(map(str, c)))
+def test_fp32_decode_sweep(case):
+    i, _, B, Hq, Hkv, D, hi = case
+    dtype = torch.float32
+    announce(f"fp32 decode sweep {case}")
+    g = torch.Generator().manual_seed(1800 + i)
+    lens = torch.randint(0, hi + 1, (B,), generator=g, dtype=torch.int32)
+    Smax = hi + 3
+    q = seeded((B, 1, Hq, D), 1900 + i, dtype)
+    kn = seeded((B, 1, Hkv, D), 2000 + i, dtype)
+    vn = seeded((B, 1, Hkv, D), 2100 + i, dtype)
+    kc = seeded((B, Hkv, Smax, D), 2200 + i, dtype)
+    vc = seeded((B, Hkv, Smax, D), 2300 + i, dtype)
     cos, sin = ref.rope_tables(D, Smax, 5e5)
     kcd, vcd = kc.to(DEV), vc.to(DEV)
     out = ops.decode_raw(q.to(DEV), kn.to(DEV), vn.to(DEV), kcd, vcd, lens.to(DEV), cos.to(DEV),
