@@ -96,7 +96,10 @@ int kf_attn_bwd_workspace_size(int B, int S, int Hq, int Hkv, int D, int dtype, 
  * tiles are written only where documents meet; with key_valid only causal
  * launches keep them, and only for the batch rows whose key 0 is valid, which
  * have no rows attending past the diagonal: the others recompute, decided on
- * the device); otherwise this equals kf_attn_bwd_workspace_size.  kf_attn_bwd takes the faster path whenever
+ * the device).  float32 (head_dim 64 or 128, no doc_ids or key_valid) keeps
+ * float32 [32][64] dS blocks, (t/2 + 1) per 32-position tile t when causal,
+ * S/32 * ceil(S/64) for full attention, per query head, up to 32 GiB.
+ * Otherwise this equals kf_attn_bwd_workspace_size.  kf_attn_bwd takes the faster path whenever
  * workspace_bytes reaches this size.  No counterpart in the reference (its
  * SDPA backward manages its own memory). */
 int kf_attn_bwd_workspace_size_ds(int B, int S, int Hq, int Hkv, int D, int dtype, int causal,

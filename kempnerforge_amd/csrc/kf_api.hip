@@ -167,7 +167,9 @@ int kf_attn_bwd_workspace_size_ds(int B, int S, int Hq, int Hkv, int D, int dtyp
   if (rc) return rc;
   KF_CHECK_ARG(bytes != nullptr, "bytes is null");
   const BwdArgs a = sizing_args(B, S, Hq, Hkv, D, dtype, causal);
-  *bytes = bwd_mfma_supported(a) ? bwd_mfma_workspace_ds(a) : bwd_ws(a);
+  *bytes = bwd_mfma_supported(a)  ? bwd_mfma_workspace_ds(a)
+           : bwd_f32_supported(a) ? bwd_f32_workspace_ds(B, S, Hq, Hkv, D, causal)
+                                  : bwd_ws(a);
   return KF_OK;
 }
 
@@ -203,7 +205,7 @@ int kf_attn_bwd(const void* q, const void* k, const void* v, const float* rope_c
     set_error("workspace too small: need %zu bytes, got %zu", need, workspace_bytes);
     return KF_ERR_WORKSPACE;
   }
-  if (bwd_f32_supported(a)) return bwd_f32(a, workspace);
+  if (bwd_f32_supported(a)) return bwd_f32(a, workspace, workspace_bytes);
   return bwd_generic(a, workspace);
 }
 

@@ -604,6 +604,24 @@ __global__ __launch_bounds__(256, 2) void capture_f32_kernel(
   }
 }
 
+// ---- dS records (float32 backward without an explicit mask) --------------
+// The dK/dV pass stores each tile's dS as a record block [32 positions][64
+// keys] per (query head, 32-position tile t, 64-key block kb); the dQ pass
+// multiplies them by K instead of recomputing S and dP.  Causal: the blocks
+// kb <= t / 2 only, numbered tile by tile (rec_off); full attention: nkb
+// blocks per tile.
+__host__ __device__ __forceinline__ int nkb_of(int S) { return (S + F_BK - 1) / F_BK; }
+__host__ __device__ __forceinline__ int64_t rec_off(int t, int kb, int causal, int nkb) {
+  if (!causal) return (int64_t)t * nkb + kb;
+  const int64_t h = t / 2;
+  return ((t & 1) ? (h + 1) * (h + 1) : h * (h + 1)) + kb;  // sum over t' < t of t'/2 + 1
+}
+// record blocks per query head
+__host__ __device__ __forceinline__ int64_t rec_blocks(int S, int causal) {
+  const int nt = (S + F_BN - 1) / F_BN;
+  return rec_off(nt, 0, causal, nkb_of(S));
+}
+
 // ------------------------------------------------------------------ backward
 // Store a lane's share (d = 16 db + 4 g + r) of scale * G^T after the RoPE
 // backward at table row pos (the pair of d < D/2 is d + D/2, in block db + NB/2).
@@ -716,20 +734,70 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_f32_kernel(
   if (ri.q_valid) store_grad_rope<D>(dq + roff * D, acc, cos, sin, ri.pos, g, scale);
 }
 
+// dQ from the dS records: the forward's rows and key tiles, dQ^T += K^T·dS^T
+// with each lane's record row segments as the B operand (two 16-byte loads
+// per tile); blocks right of a row's causal record range contribute zero.
+template <int D>
+__global__ __launch_bounds__(256, 2) void bwd_dq_rec_f32_kernel(
+    const float* kr_rows, const float* __restrict__ rec, const float* __restrict__ cos,
+    const float* __restrict__ sin, float* __restrict__ dq, int S, int Sp, int Hq, int Hkv,
+    int n_rep, int bm_pos, int nqb, int causal, float scale, int64_t rec_nt) {
+  constexpr int NB = D / 16;
+  __shared__ __attribute__((aligned(16))) float sK[2][F_BN * D];
+
+  const int lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15, w = wave_id();
+  const int logical = xcd_logical_id(blockIdx.x, gridDim.x, nqb);
+  const RowInfo ri = row_info(logical, nqb, Hkv, n_rep, bm_pos, S, w * 16 + c16);
+  const int kend = causal ? min(S, ri.p0 + bm_pos) : S;
+  const int ntiles = (kend + F_BN - 1) / F_BN;
+  const float* kb = kr_rows + ((int64_t)ri.b * Hkv + ri.g) * Sp * D;
+  auto stage = [&](int t, int buf) {
+    const int k0 = t * F_BN;
+    tile_dma<D>(kb + (int64_t)k0 * D, (uint32_t)D, sK[buf], w, lane, S - k0);
+  };
+  if (ntiles > 0) stage(0, 0);
+  const int tq = ri.pos / F_BN;  // this row's query tile
+  const float* rrow = rec + (((int64_t)ri.b * Hq + ri.hq) * rec_nt + rec_off(tq, 0, causal, nkb_of(S))) *
+                                (F_BN * F_BK) + (ri.pos % F_BN) * F_BK;
+  f32x4 acc[NB];
+#pragma unroll
+  for (int db = 0; db < NB; ++db) acc[db] = zero4();
+  mfma::lds_copy_wait();
+  __syncthreads();
+
+  for (int t = 0; t < ntiles; ++t) {
+    const int buf = t & 1;
+    if (t + 1 < ntiles) stage(t + 1, buf ^ 1);
+    const int kbk = t / 2;
+    f32x4 r0 = zero4(), r1 = zero4();
+    if (ri.q_valid && (!causal || kbk <= tq / 2)) {
+      const float* p = rrow + (int64_t)kbk * (F_BN * F_BK) + F_BN * (t & 1) + 4 * g;
+      r0 = __builtin_nontemporal_load((const f32x4*)p);
+      r1 = __builtin_nontemporal_load((const f32x4*)(p + 16));
+    }
+    accum_t<D>(sK[buf], r0, r1, c16, g, acc);
+    mfma::lds_copy_wait();
+    __syncthreads();
+  }
+  if (ri.q_valid)
+    store_grad_rope<D>(dq + (((int64_t)ri.b * S + ri.pos) * Hq + ri.hq) * D, acc, cos, sin,
+                       ri.pos, g, scale);
+}
+
 // dK/dV: a workgroup owns 64 keys of one KV head (16 per wavefront, one per
 // lane column), their rotated K and V rows in registers, and walks every
 // query head of the group over the query tiles from the keys' diagonal on
 // (under MASK_DOC only the listed ones; under MASK_KPM also the guarded rows'
 // tiles below it): S = Q·K^T and dP = dO·V^T per 32-position tile, then
 // dV^T += dO^T·P and dK^T += Q^T·dS.  Key blocks are numbered longest first.
-template <int D, int MODE>
+template <int D, int MODE, bool REC = false>
 __global__ __launch_bounds__(256, 2) void bwd_dkdv_f32_kernel(
     const float* qr_rows, const float* __restrict__ kr_rows, const float* __restrict__ v,
     const float* __restrict__ cos, const float* __restrict__ sin, const float* dout,
     const float* stats, double* __restrict__ sum64, float* __restrict__ dk,
     float* __restrict__ dv, int S, int Sp, int Hq, int Hkv, int n_rep, int causal, float scale,
     float scale_log2, const int32_t* __restrict__ mask, const int2* __restrict__ ranges,
-    const int* __restrict__ first_valid, int nt32) {
+    const int* __restrict__ first_valid, int nt32, float* __restrict__ rec, int64_t rec_nt) {
   constexpr int NJ = D / 16, NB = D / 16;
   __shared__ __attribute__((aligned(16))) float sQ[2][F_BN * D];
   __shared__ __attribute__((aligned(16))) float sO[2][F_BN * D];
@@ -856,6 +924,18 @@ __global__ __launch_bounds__(256, 2) void bwd_dkdv_f32_kernel(
       for (int r = 0; r < 4; ++r) {
         d0[r] = s0[r] * (d0[r] - dl0[r]);
         d1[r] = s1[r] * (d1[r] - dl1[r]);
+      }
+    }
+    if (REC) {
+      // this tile's dS (unscaled; zero for keys past S) into its record block
+      // [32 positions][64 keys] for the dQ pass
+      const int t = q0 / F_BN, hq = hk * n_rep + it / per;
+      float* blk = rec + (((int64_t)b * Hq + hq) * rec_nt + rec_off(t, kblk, causal, nkb_of(S))) *
+                             (F_BN * F_BK) + 16 * w + c16;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        __builtin_nontemporal_store(kvalid ? d0[r] : 0.f, blk + (4 * g + r) * F_BK);
+        __builtin_nontemporal_store(kvalid ? d1[r] : 0.f, blk + (16 + 4 * g + r) * F_BK);
       }
     }
     accum_t2<D>(tO, s0, s1, adv, tQ, d0, d1, adk, c16, g);
@@ -1230,8 +1310,22 @@ size_t bwd_base_bytes(int B, int S, int Hq, int Hkv, int D, size_t* sum_off) {
 template <int D, int MODE>
 void launch_bwd_kernels(const BwdArgs& a, float* qrot, float* krot, float* stats, double* sum64,
                         int Sp, int n_rep, int bm_pos, int nqb, unsigned nqblk, unsigned nkblk,
-                        const MaskRec& mr) {
+                        const MaskRec& mr, float* rec) {
   const int32_t* mask = a.doc ? a.doc : a.kvalid;
+  if constexpr (MODE == MASK_NONE) {
+   if (rec != nullptr) {
+    // dK/dV first, keeping dS; then dQ from the records
+    const int64_t rnt = rec_blocks(a.S, a.causal);
+    KF_LAUNCH("bwd_dkdv_f32", (bwd_dkdv_f32_kernel<D, MODE, true>), dim3(nkblk), dim3(256), 0,
+              a.stream, qrot, krot, (const float*)a.v, a.cos, a.sin, (const float*)a.dout,
+              stats, sum64, (float*)a.dk, (float*)a.dv, a.S, Sp, a.Hq, a.Hkv, n_rep, a.causal,
+              a.scale, a.scale * kLog2e, mask, mr.ranges, mr.first_valid, mr.nt32, rec, rnt);
+    KF_LAUNCH("bwd_dq_rec_f32", (bwd_dq_rec_f32_kernel<D>), dim3(nqblk), dim3(256), 0, a.stream,
+              krot, rec, a.cos, a.sin, (float*)a.dq, a.S, Sp, a.Hq, a.Hkv, n_rep, bm_pos, nqb,
+              a.causal, a.scale, rnt);
+    return;
+   }
+  }
   KF_LAUNCH("bwd_dq_f32", (bwd_dq_f32_kernel<D, MODE>), dim3(nqblk), dim3(256), 0, a.stream,
             qrot, krot, (const float*)a.v, a.cos, a.sin, (const float*)a.dout, stats,
             (float*)a.dq, a.S, Sp, a.Hq, a.Hkv, n_rep, bm_pos, nqb, a.causal, a.scale,
@@ -1239,11 +1333,18 @@ void launch_bwd_kernels(const BwdArgs& a, float* qrot, float* krot, float* stats
   KF_LAUNCH("bwd_dkdv_f32", (bwd_dkdv_f32_kernel<D, MODE>), dim3(nkblk), dim3(256), 0, a.stream,
             qrot, krot, (const float*)a.v, a.cos, a.sin, (const float*)a.dout, stats, sum64,
             (float*)a.dk, (float*)a.dv, a.S, Sp, a.Hq, a.Hkv, n_rep, a.causal, a.scale,
-            a.scale * kLog2e, mask, mr.ranges, mr.first_valid, mr.nt32);
+            a.scale * kLog2e, mask, mr.ranges, mr.first_valid, mr.nt32, nullptr, 0);
+}
+
+// bytes of the dS records, or 0 past the cap (dQ then recomputes S and dP)
+constexpr size_t F_REC_MAX = (size_t)32 << 30;
+size_t rec_bytes(int B, int S, int Hq, int causal) {
+  const size_t n = (size_t)B * Hq * (size_t)rec_blocks(S, causal) * (F_BN * F_BK) * sizeof(float);
+  return n <= F_REC_MAX ? n : 0;
 }
 
 template <int D>
-int bwd_f32_t(const BwdArgs& a, void* workspace) {
+int bwd_f32_t(const BwdArgs& a, void* workspace, float* rec) {
   const int n_rep = a.Hq / a.Hkv, bm_pos = F_ROWS / n_rep;
   const int nqb = (a.S + bm_pos - 1) / bm_pos;
   const int Sp = (a.S + F_BK - 1) / F_BK * F_BK;
@@ -1276,13 +1377,13 @@ int bwd_f32_t(const BwdArgs& a, void* workspace) {
   }
   if (mode == MASK_DOC)
     launch_bwd_kernels<D, MASK_DOC>(a, qrot, krot, stats, sum64, Sp, n_rep, bm_pos, nqb,
-                                    (unsigned)nqblk, (unsigned)nkblk, mr);
+                                    (unsigned)nqblk, (unsigned)nkblk, mr, rec);
   else if (mode == MASK_KPM)
     launch_bwd_kernels<D, MASK_KPM>(a, qrot, krot, stats, sum64, Sp, n_rep, bm_pos, nqb,
-                                    (unsigned)nqblk, (unsigned)nkblk, mr);
+                                    (unsigned)nqblk, (unsigned)nkblk, mr, rec);
   else
     launch_bwd_kernels<D, MASK_NONE>(a, qrot, krot, stats, sum64, Sp, n_rep, bm_pos, nqb,
-                                     (unsigned)nqblk, (unsigned)nkblk, mr);
+                                     (unsigned)nqblk, (unsigned)nkblk, mr, rec);
   KF_CHECK_LAUNCH();
   return KF_OK;
 }
@@ -1365,8 +1466,18 @@ size_t bwd_f32_workspace(int B, int S, int Hq, int Hkv, int D) {
   return al256(bwd_base_bytes(B, S, Hq, Hkv, D, &sum_off)) + mask_rec_bytes(B, S);
 }
 
-int bwd_f32(const BwdArgs& a, void* workspace) {
-  return a.D == 128 ? bwd_f32_t<128>(a, workspace) : bwd_f32_t<64>(a, workspace);
+size_t bwd_f32_workspace_ds(int B, int S, int Hq, int Hkv, int D, int causal) {
+  const size_t rb = rec_bytes(B, S, Hq, causal);
+  return rb ? al256(bwd_f32_workspace(B, S, Hq, Hkv, D)) + rb : bwd_f32_workspace(B, S, Hq, Hkv, D);
+}
+
+int bwd_f32(const BwdArgs& a, void* workspace, size_t workspace_bytes) {
+  // the dS records when there is no explicit mask and the workspace holds them
+  float* rec = nullptr;
+  if (!a.doc && !a.kvalid && rec_bytes(a.B, a.S, a.Hq, a.causal) != 0 &&
+      workspace_bytes >= bwd_f32_workspace_ds(a.B, a.S, a.Hq, a.Hkv, a.D, a.causal))
+    rec = (float*)((char*)workspace + al256(bwd_f32_workspace(a.B, a.S, a.Hq, a.Hkv, a.D)));
+  return a.D == 128 ? bwd_f32_t<128>(a, workspace, rec) : bwd_f32_t<64>(a, workspace, rec);
 }
 
 

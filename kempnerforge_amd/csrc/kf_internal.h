@@ -69,7 +69,10 @@ int fwd_f32(const FwdArgs& a, void* workspace);
 int capture_f32(const FwdArgs& a, float* probs, void* workspace);
 bool bwd_f32_supported(const BwdArgs& a);
 size_t bwd_f32_workspace(int B, int S, int Hq, int Hkv, int D);
-int bwd_f32(const BwdArgs& a, void* workspace);
+// with the dS records (used without an explicit mask when workspace_bytes
+// reaches it: dQ then multiplies them by K instead of recomputing S and dP)
+size_t bwd_f32_workspace_ds(int B, int S, int Hq, int Hkv, int D, int causal);
+int bwd_f32(const BwdArgs& a, void* workspace, size_t workspace_bytes);
 
 // bf16 MFMA kernels (kf_fwd.hip, kf_bwd.hip, kf_capture.hip)
 bool fwd_mfma_supported(const FwdArgs& a);

@@ -77,12 +77,24 @@ def test_host_only_calls():
     assert n.value == (base + 255) // 256 * 256 + B * Hq * P * (P + 64)
     assert lib.kf_attn_bwd_workspace_size_ds(B, 4000, Hq, Hkv, D, 1, 0, ctypes.byref(n)) == 0
     assert n.value == (base + 255) // 256 * 256 + B * Hq * 2 * P * P  # P = 4096 for S = 4000
-    # fp32 runs the generic kernels (no tiles kept); past 32 GiB of tiles dQ recomputes
-    for args in ((B, S, Hq, Hkv, D, 0, 1), (1, 65536, 32, 8, 128, 1, 1)):
+    # past 32 GiB of tiles dQ recomputes (bf16 at 65536 positions, fp32 at C5's 16384)
+    for args in ((1, 65536, 32, 8, 128, 1, 1), (1, 16384, 64, 8, 128, 0, 1)):
         small, big = _lib.size_out(), _lib.size_out()
         assert lib.kf_attn_bwd_workspace_size(*args[:6], ctypes.byref(small)) == 0
         assert lib.kf_attn_bwd_workspace_size_ds(*args, ctypes.byref(big)) == 0
         assert big.value == small.value
+    # fp32: rotated Q and K float32 [Sp][D] (Sp = S rounded up to 64), two floats of
+    # row statistics per query row, float64 group sums of dK and dV per key row,
+    # then the mask records (an int2 per batch row and 32-position tile, an int32
+    # per batch row); kept dS: float32 [32][64] blocks, tile t holding t // 2 + 1
+    al = lambda x: (x + 255) // 256 * 256  # noqa: E731
+    f32 = al(al((B * Hq * P * D + B * Hkv * P * D + B * Hq * P * 2) * 4)
+             + B * S * Hkv * D * 2 * 8) + B * (S // 32) * 8 + B * 4
+    assert lib.kf_attn_bwd_workspace_size(B, S, Hq, Hkv, D, 0, ctypes.byref(n)) == 0
+    assert n.value == f32
+    assert lib.kf_attn_bwd_workspace_size_ds(B, S, Hq, Hkv, D, 0, 1, ctypes.byref(n)) == 0
+    blocks = sum(t // 2 + 1 for t in range(S // 32))
+    assert n.value == al(f32) + B * Hq * blocks * 32 * 64 * 4
     # rotated operands kept from the forward: K per KV head then Q per query head,
     # bf16 [P][D]; the backward reading them needs that much less workspace
     assert lib.kf_attn_rot_size(B, S, Hq, Hkv, D, 1, 0, 0, ctypes.byref(n)) == 0

@@ -25,7 +25,7 @@ F32 = torch.float32
 TOL = 1e-5
 GENERIC = {"fwd_generic", "bwd_dkdv_generic", "bwd_dq_generic", "bwd_delta_generic"}
 FWD = {"fwd_f32"}
-BWD = {"stats_f32", "bwd_dq_f32", "bwd_dkdv_f32"}
+BWD = {"stats_f32", "bwd_dkdv_f32"}  # and bwd_dq_f32 or, from the dS records, bwd_dq_rec_f32
 
 
 def _inputs(B, S, Hq, Hkv, D, seed=0, theta=5e5):
@@ -315,3 +315,31 @@ def test_capture(case):
     check_out(p, p_ref, TOL, "probs")
     check_out(out, o_ref, TOL, "out")
     assert (p.cpu()[p_ref == 0] == 0).all()  # masked entries exactly zero
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("shape", [(2, 300, 8, 2, 128), (1, 257, 6, 3, 64), (1, 64, 4, 4, 128)],
+                         ids=lambda c: "-".join(map(str, c)))
+def test_ds_records_and_recompute(shape, causal):
+    """The two float32 dQ paths: from the dS records the dK/dV pass keeps
+    (default workspace) and recomputing S and dP (low_memory).  dK and dV are
+    the same bits either way; both dQ within 1e-5 of the oracle."""
+    B, S, Hq, Hkv, D = shape
+    announce(f"fp32 dS records {shape} causal={causal}")
+    q, k, v, do, cos, sin = _inputs(B, S, Hq, Hkv, D, seed=70)
+    args = [t.to(DEV) for t in (q, k, v, cos, sin)]
+    out, lse = ops.fwd_raw(*args, causal=causal, k_rotated=False)
+    with _lib.KernelTimer() as t1:
+        kept = ops.bwd_raw(*args, out, lse, do.to(DEV), causal=causal)
+        torch.cuda.synchronize()
+    with _lib.KernelTimer() as t2:
+        rec = ops.bwd_raw(*args, out, lse, do.to(DEV), causal=causal, low_memory=True)
+        torch.cuda.synchronize()
+    assert "bwd_dq_rec_f32" in t1.stats and "bwd_dq_f32" not in t1.stats, t1.stats
+    assert "bwd_dq_f32" in t2.stats and "bwd_dq_rec_f32" not in t2.stats, t2.stats
+    assert torch.equal(kept[1], rec[1]) and torch.equal(kept[2], rec[2])
+    dq_r, dk_r, dv_r = ref.attention_bwd(q, k, v, cos, sin, do, causal=causal)
+    check_grad(kept[0], dq_r, F32, "dq (records)")
+    check_grad(rec[0], dq_r, F32, "dq (recomputed)")
+    check_grad(kept[1], dk_r, F32, "dk", group=Hq // Hkv)
+    check_grad(kept[2], dv_r, F32, "dv", group=Hq // Hkv)
