@@ -580,7 +580,8 @@ def run_full(args, torch, wl):
 # --------------------------------------------------------------------------- rocprof summary
 def _short(name: str) -> str:
     """Kernel symbol -> the launcher's name (kf::..._kernel<...> -> ...)."""
-    m = re.search(r"(fwd_f32|bwd_dq_f32|bwd_dkdv_f32|rows_f32|stats_f32|"
+    m = re.search(r"(fwd_f32|bwd_dq_rec_f32|bwd_dq_f32|bwd_dkdv_f32|rows_f32|stats_f32|"
+                  r"mask_prep_f32|capture_f32|decode_merge_f32|decode_f32|"
                   r"kv_prep|fwd_mfma|fwd32|q_prep_bwd|bwd_dkdv|bwd_dq_ds|bwd_dq|decode_stream|"
                   r"decode_merge|capture_probs_mfma|kv_append|append|doc_block_tiles|"
                   r"order_by_count|kpm_row_flags|dkdv_reduce)_kernel", name)
