@@ -1,10 +1,11 @@
 // float32 attention on the fp32 matrix cores (v_mfma_f32_16x16x4_f32): the
-// forward, dQ and dK/dV of the reference's mixed_precision = "fp32"
-// (kempnerforge/config/training.py:31; attention at kempnerforge/model/
-// attention.py:228-231 then runs SDPA in float32), causal or full attention
-// without explicit masks, head_dim 64 or 128.  Nothing is rounded below
-// float32: the products are exact and the sums accumulate in float32, as the
-// reference's float32 SDPA does (the explicit masks and other head sizes stay
+// forward, dQ and dK/dV, the KV-cache decode and the probability capture of
+// the reference's mixed_precision = "fp32" (kempnerforge/config/training.py:31;
+// attention at kempnerforge/model/attention.py:228-231 then runs SDPA in
+// float32), causal or full attention, with packed documents or key padding
+// (one kind at a time), head_dim 64 or 128.  Nothing is rounded below float32:
+// the products are exact and the sums accumulate in float32, as the
+// reference's float32 SDPA does (other head sizes and both masks at once stay
 // on the generic kernels).
 //
 // One MFMA multiplies a 16x4 A by a 4x16 B into a 16x16 C: lane l holds
