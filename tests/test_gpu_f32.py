@@ -168,6 +168,8 @@ MASKED = [
     (2, 160, 4, 2, 128, "none_valid"),
     (2, 190, 8, 1, 128, "trailing"),
     (2, 230, 8, 2, 128, "row1_only"),
+    (1, 333, 8, 2, 64, "doc_repeating"),
+    (1, 1, 4, 2, 128, "leading"),        # a single guarded position
 ]
 
 
@@ -180,6 +182,8 @@ def test_explicit_masks(case):
     q, k, v, do, cos, sin = _inputs(B, S, Hq, Hkv, D, seed=50)
     if kind == "doc":
         masks = {"doc_ids": _doc_ids(B, S, 51)}
+    elif kind == "doc_repeating":  # ids recur (0, 1, 2, 0, 1, ...): same-id runs apart see each other
+        masks = {"doc_ids": ((torch.arange(S) // 37) % 3).to(torch.int32).expand(B, S).contiguous()}
     else:
         masks = {"key_padding_mask": _key_padding(B, S, kind, 52)}
     dev_masks = {n: t.to(DEV) for n, t in masks.items()}
