@@ -140,6 +140,8 @@ int kf_attn_fwd(const void* q, const void* k, const void* v, const float* rope_c
   return fwd_generic(a);
 }
 
+}  // extern "C"
+
 namespace {
 // Sizing stand-in for a backward call: aligned non-null pointers, no masks.
 kf::BwdArgs sizing_args(int B, int S, int Hq, int Hkv, int D, int dtype, int causal) {
@@ -151,6 +153,8 @@ kf::BwdArgs sizing_args(int B, int S, int Hq, int Hkv, int D, int dtype, int cau
   return a;
 }
 }  // namespace
+
+extern "C" {
 
 int kf_attn_bwd_workspace_size(int B, int S, int Hq, int Hkv, int D, int dtype, size_t* bytes) {
   int rc = check_common(B, S, S, Hq, Hkv, D, dtype);
