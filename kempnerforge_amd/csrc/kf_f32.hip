@@ -514,7 +514,10 @@ __global__ __launch_bounds__(256, 2) void fwd_f32_kernel(
 // forward has written out and lse: the forward's rows and key walk recompute
 // S^T = K·Q^T per 32-key tile (K tiles only) and store each lane's row
 // segment; every tile the walk skips (right of the causal frontier, or whose
-// documents miss the rows') is written as zeros.
+// documents miss the rows') is written as zeros.  The stores are write-back:
+// the two 64-byte halves of a row's 128-byte segment come from two store
+// instructions, and L2 joins them into whole lines (non-temporal stores ran
+// the C5-cap slice about 20% slower).
 template <int D, int MODE>
 __global__ __launch_bounds__(256, 2) void capture_f32_kernel(
     const float* __restrict__ q, const float* __restrict__ cos, const float* __restrict__ sin,
@@ -553,7 +556,7 @@ __global__ __launch_bounds__(256, 2) void capture_f32_kernel(
   auto put4 = [&](int key0, const f32x4& x) {
     if (!ri.q_valid) return;
     if (vec && key0 + 3 < Sk) {
-      __builtin_nontemporal_store(x, (f32x4*)(prow + key0));
+      *(f32x4*)(prow + key0) = x;
     } else {
 #pragma unroll
       for (int r = 0; r < 4; ++r)
