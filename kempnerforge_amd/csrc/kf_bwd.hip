@@ -186,6 +186,9 @@ __device__ __forceinline__ void dkdv_role(
   // fragment reads run PF MFMAs ahead (2 in the masked modes, whose lists and
   // masks take the registers of a third)
   constexpr int PF = LIST ? 2 : 3;
+  // the dS waves' phase 2 when they keep records: 2 ahead (its four dS
+  // registers stay live to the end of the tile, for the deferred store)
+  constexpr int PF2 = DSROLE && STORE ? 2 : PF;
   const int hh = lane >> 5, c32 = lane & 31;
   const int kw = w & 3;
   const int key = k0 + 32 * kw + c32;
@@ -271,7 +274,7 @@ __device__ __forceinline__ void dkdv_role(
   u32x4* myP = sP + kw * 4 * 64 + lane;  // chunk c at myP[c * 64]
   const TrOffsets<D> tro = tr_offsets<D>(lane);
 
-  // STORE (dS waves): each dS tile goes to its record right after it is formed
+  // STORE (dS waves): each dS tile goes to its record after the tile's end
   // (non-temporal: the records are read once, by the dQ kernel).  The record's
   // index is scalar work done before the mid-tile barrier, where the dS waves
   // wait for P anyway, not between dS and the dK products.
@@ -373,7 +376,7 @@ __device__ __forceinline__ void dkdv_role(
 #pragma unroll
       for (int c = 0; c < 4; ++c) myP[c * 64] = pk[c];
     }
-    bf16x8 fpre[PF];  // dS waves: first phase-2 fragments, read before the barrier
+    bf16x8 fpre[PF2];  // dS waves: first phase-2 fragments, read before the barrier
     // record of this tile (-1: above the causal diagonal, nothing to keep)
     int64_t rec = -1;
     if (STORE && DSROLE && keep) {
@@ -388,7 +391,7 @@ __device__ __forceinline__ void dkdv_role(
       // with P is left between the barrier and the dK products
       asm volatile("" : "+v"(x[0]), "+v"(x[1]));
 #pragma unroll
-      for (int n = 0; n < PF; ++n) fpre[n] = lds_frag_t<D>(second_tile(S_), tro, n / DT, n % DT);
+      for (int n = 0; n < PF2; ++n) fpre[n] = lds_frag_t<D>(second_tile(S_), tro, n / DT, n % DT);
     }
     __syncthreads();  // P of this tile is in LDS
     if (DSROLE) {
@@ -411,10 +414,6 @@ __device__ __forceinline__ void dkdv_role(
             pk[2 * mt + cc][2 * half + 1] = pack2<T>(v[2], v[3]);
           }
         }
-      if (STORE && rec >= 0) {
-#pragma unroll
-        for (int c = 0; c < 4; ++c) __builtin_nontemporal_store(pk[c], dsb + rec + c * 64 + lane);
-      }
     }
     // phase 2: dV^T += dO^T P (P waves) or dK^T += Q^T dS (dS waves)
     {
@@ -422,13 +421,13 @@ __device__ __forceinline__ void dkdv_role(
       const T* tA = second_tile(S_);
       bf16x8 fa[NS];
 #pragma unroll
-      for (int n = 0; n < PF; ++n)
+      for (int n = 0; n < PF2; ++n)
         fa[n] = DSROLE ? fpre[n] : lds_frag_t<D>(tA, tro, n / DT, n % DT);
 #pragma unroll
       for (int n = 0; n < NS; ++n) {
         __builtin_amdgcn_sched_barrier(0);
-        if (n + PF < NS)
-          fa[n + PF] = lds_frag_t<D>(tA, tro, (n + PF) / DT, (n + PF) % DT);
+        if (n + PF2 < NS)
+          fa[n + PF2] = lds_frag_t<D>(tA, tro, (n + PF2) / DT, (n + PF2) % DT);
         acc[n % DT] = mfma32<T>(fa[n], as_bf16x8(pk[n / DT]), acc[n % DT]);
       }
       __builtin_amdgcn_sched_barrier(0);
@@ -439,6 +438,14 @@ __device__ __forceinline__ void dkdv_role(
     }
     lds_copy_wait();
     __syncthreads();
+    // the dS record leaves after the end-of-tile wait: vmcnt counts stores
+    // with the staging loads, so a store issued inside the tile holds every
+    // wavefront at that wait until it is written; issued here it has the
+    // next tile's duration to complete
+    if (DSROLE && STORE && rec >= 0) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) __builtin_nontemporal_store(pk[c], dsb + rec + c * 64 + lane);
+    }
   };
   for (int it = 0; it < total; it += 2) {
     tile_body(it, std::integral_constant<int, 0>{});
