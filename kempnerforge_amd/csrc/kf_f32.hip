@@ -930,18 +930,6 @@ __global__ __launch_bounds__(256, 2) void bwd_dkdv_f32_kernel(
         d1[r] = s1[r] * (d1[r] - dl1[r]);
       }
     }
-    if (REC) {
-      // this tile's dS (unscaled; zero for keys past S) into its record block
-      // [32 positions][64 keys] for the dQ pass
-      const int t = q0 / F_BN, hq = hk * n_rep + it / per;
-      float* blk = rec + (((int64_t)b * Hq + hq) * rec_nt + rec_off(t, kblk, causal, nkb_of(S))) *
-                             (F_BN * F_BK) + 16 * w + c16;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        __builtin_nontemporal_store(kvalid ? d0[r] : 0.f, blk + (4 * g + r) * F_BK);
-        __builtin_nontemporal_store(kvalid ? d1[r] : 0.f, blk + (16 + 4 * g + r) * F_BK);
-      }
-    }
     accum_t2<D>(tO, s0, s1, adv, tQ, d0, d1, adk, c16, g);
     if (it % per == per - 1 && it + 1 < total) {
       // a query head done: its sums (unscaled, before the RoPE backward) join
@@ -969,6 +957,20 @@ __global__ __launch_bounds__(256, 2) void bwd_dkdv_f32_kernel(
     }
     mfma::lds_copy_wait();
     __syncthreads();
+    if (REC) {
+      // this tile's dS (unscaled; zero for keys past S) into its record block
+      // [32 positions][64 keys] for the dQ pass, after the end-of-tile wait
+      // (vmcnt counts stores with the staging loads: a store issued inside
+      // the tile would hold that wait until it is written)
+      const int t = q0 / F_BN, hq = hk * n_rep + it / per;
+      float* blk = rec + (((int64_t)b * Hq + hq) * rec_nt + rec_off(t, kblk, causal, nkb_of(S))) *
+                             (F_BN * F_BK) + 16 * w + c16;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        __builtin_nontemporal_store(kvalid ? d0[r] : 0.f, blk + (4 * g + r) * F_BK);
+        __builtin_nontemporal_store(kvalid ? d1[r] : 0.f, blk + (16 + 4 * g + r) * F_BK);
+      }
+    }
   }
   if (kvalid) {
     int kl = key;
