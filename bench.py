@@ -582,13 +582,14 @@ def _short(name: str) -> str:
     """Kernel symbol -> the launcher's name (kf::..._kernel<...> -> ...)."""
     m = re.search(r"(fwd_f32|bwd_dq_rec_f32|bwd_dq_f32|bwd_dkdv_f32|rows_f32|stats_f32|"
                   r"mask_prep_f32|capture_f32|decode_merge_f32|decode_f32|"
-                  r"kv_prep|fwd_mfma|fwd32|q_prep_bwd|bwd_dkdv|bwd_dq_ds|bwd_dq|decode_stream|"
+                  r"kv_prep|fwd_mfma|fwd32|q_prep_bwd|bwd_dkdv|bwd_dq_ds2|bwd_dq_ds|bwd_dq|decode_stream|"
                   r"decode_merge|capture_probs_mfma|kv_append|append|doc_block_tiles|"
                   r"order_by_count|kpm_row_flags|dkdv_reduce)_kernel", name)
     if m:
-        # fwd32_kernel is the unmasked forward's kernel, launched as fwd_mfma
+        # fwd32_kernel is the unmasked forward's kernel, launched as fwd_mfma;
+        # bwd_dq_ds2_kernel (two query tiles per workgroup) as bwd_dq_ds
         return {"capture_probs_mfma": "capture_probs", "append": "kv_append",
-                "fwd32": "fwd_mfma"}.get(m.group(1), m.group(1))
+                "fwd32": "fwd_mfma", "bwd_dq_ds2": "bwd_dq_ds"}.get(m.group(1), m.group(1))
     return "copy" if "copyBuffer" in name else name[:40]
 
 
